@@ -1,0 +1,1007 @@
+// api.hip — the C ABI of libfllm_hip.so (include/fllm.h): device context, model weights in
+// GGUF block layout, per-request sequences (device KV cache + scratch + stream), the decode
+// step (eager or replayed from a captured HIP graph) and the verification/microbenchmark
+// entry points. No C++ exception crosses the ABI.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+
+using namespace fllm;
+
+// =====================================================================================
+// errors
+// =====================================================================================
+static thread_local std::string g_err;
+
+static int32_t fail(int32_t code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                          \
+    do {                                                                                       \
+        hipError_t _e = (expr);                                                                \
+        if (_e != hipSuccess) return fail(FLLM_E_DEVICE, "%s: %s", #expr, hipGetErrorString(_e)); \
+    } while (0)
+
+#define NOT_NULL(p)                                                  \
+    do {                                                             \
+        if (!(p)) return fail(FLLM_E_NULL, "%s must not be null", #p); \
+    } while (0)
+
+extern "C" const char* fllm_last_error(void) { return g_err.c_str(); }
+extern "C" int32_t fllm_version(void) { return 100; }
+
+// =====================================================================================
+// objects
+// =====================================================================================
+struct fllm_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int n_cu = 0;
+    int64_t hbm = 0;
+    // scratch for fllm_gemv's activation quantization
+    uint4* xq_parts = nullptr;
+    float4* xq_stats = nullptr;
+    int64_t xq_groups = 0;
+};
+
+struct fllm_buf {
+    fllm_ctx* ctx = nullptr;
+    uint8_t* ptr = nullptr;
+    uint64_t n = 0;
+};
+
+static const uint64_t kPad = 256;  // slack after every weight allocation for aligned over-reads
+
+struct Tensor {
+    uint8_t* ptr = nullptr;
+    int type = -1;
+    int64_t rows = 0, cols = 0;
+    uint64_t bytes = 0;
+    bool present() const { return ptr != nullptr; }
+    WMat mat() const { return WMat{ptr, type, rows, cols}; }
+};
+
+struct Layer {
+    Tensor q, k, v, o, gate, up, down;
+    float *attn_norm = nullptr, *ffn_norm = nullptr, *post_attn = nullptr, *post_ffn = nullptr;
+    float *bq = nullptr, *bk = nullptr, *bv = nullptr;
+};
+
+struct fllm_model {
+    fllm_ctx* ctx = nullptr;
+    fllm_model_desc d{};
+    int qdim = 0, kvdim = 0;
+    Tensor tok_embd, output;
+    bool output_tied = false;
+    float* out_norm = nullptr;
+    std::vector<Layer> layers;
+    std::vector<float> inv_freq;
+    bool finalized = false;
+    uint64_t layer_bytes = 0, head_bytes = 0;
+};
+
+struct ProfAgg {
+    int64_t launches = 0;
+    double ms = 0, bytes = 0;
+};
+
+struct fllm_seq {
+    fllm_model* m = nullptr;
+    hipStream_t st = nullptr;
+    int max_seq = 0;
+    int cur_len = 0;
+    int nsplit = 1;
+    float *kc = nullptr, *vc = nullptr;
+    float2* rope = nullptr;
+    StepParams* params = nullptr;
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
+    float *g = nullptr, *u = nullptr, *h = nullptr, *tmp = nullptr, *logits = nullptr;
+    XQ xq_hidden{}, xq_att{}, xq_h{};
+    float *part_o = nullptr, *part_ml = nullptr;
+    int *topk_ids = nullptr, *topk_count = nullptr;
+    float* topk_vals = nullptr;
+    int topk_cap = 0;
+    float* hidden_dbg = nullptr;
+    bool debug = false;
+    bool use_graph = true;
+    bool graph_valid = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    // profiling
+    bool profile = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<std::pair<std::string, double>> pending;  // name, bytes per pending launch
+    std::map<std::string, ProfAgg> agg;
+    std::vector<std::string> agg_order;
+    std::vector<void*> allocs;
+};
+
+// =====================================================================================
+// context
+// =====================================================================================
+extern "C" int32_t fllm_ctx_create(int32_t device, fllm_ctx** out) {
+    NOT_NULL(out);
+    *out = nullptr;
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(FLLM_E_ARG_RANGE, "device %d outside [0,%d)", device, n);
+    HIP_TRY(hipSetDevice(device));
+    fllm_ctx* c = new fllm_ctx();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) { delete c; return fail(FLLM_E_DEVICE, "hipStreamCreate: %s", hipGetErrorString(e)); }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+        c->n_cu = prop.multiProcessorCount;
+        c->hbm = (int64_t)prop.totalGlobalMem;
+    }
+    *out = c;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_ctx_destroy(fllm_ctx* ctx) {
+    if (!ctx) return FLLM_OK;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->xq_parts) hipFree(ctx->xq_parts);
+    if (ctx->xq_stats) hipFree(ctx->xq_stats);
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_ctx_sync(fllm_ctx* ctx) {
+    NOT_NULL(ctx);
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_ctx_device_info(fllm_ctx* ctx, int32_t* n_cu, int64_t* hbm_bytes) {
+    NOT_NULL(ctx);
+    if (n_cu) *n_cu = ctx->n_cu;
+    if (hbm_bytes) *hbm_bytes = ctx->hbm;
+    return FLLM_OK;
+}
+
+// =====================================================================================
+// element counts and dequantization (Dequantizer.cs:466-504)
+// =====================================================================================
+extern "C" int32_t fllm_element_count(int32_t type, int64_t nbytes, int64_t* out) {
+    NOT_NULL(out);
+    if (!type_supported(type)) return fail(FLLM_E_NOT_SUPPORTED, "Tensor type %d is not supported for dequantization.", type);
+    TypeInfo ti = type_info(type);
+    *out = nbytes / ti.block_bytes * ti.block_elems;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_dequantize(fllm_ctx* ctx, int32_t type, const void* src, uint64_t nbytes, float* dst, int64_t n) {
+    NOT_NULL(ctx);
+    if (!type_supported(type)) return fail(FLLM_E_NOT_SUPPORTED, "Tensor type %d is not supported for dequantization.", type);
+    TypeInfo ti = type_info(type);
+    if (nbytes % (uint64_t)ti.block_bytes != 0)
+        return fail(FLLM_E_ARG, "Source length must be a multiple of %d for type %d.", ti.block_bytes, type);
+    int64_t elems = (int64_t)(nbytes / ti.block_bytes) * ti.block_elems;
+    if (n < elems) return fail(FLLM_E_ARG, "Destination must hold at least %lld floats.", (long long)elems);
+    if (elems == 0) return FLLM_OK;
+    NOT_NULL(src);
+    NOT_NULL(dst);
+    HIP_TRY(hipSetDevice(ctx->device));
+    uint8_t* dsrc = nullptr;
+    float* ddst = nullptr;
+    HIP_TRY(hipMalloc(&dsrc, nbytes + kPad));
+    hipError_t e = hipMalloc(&ddst, sizeof(float) * (size_t)elems);
+    if (e != hipSuccess) { hipFree(dsrc); return fail(FLLM_E_OOM, "hipMalloc: %s", hipGetErrorString(e)); }
+    e = hipMemcpyAsync(dsrc, src, nbytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = launch_dequant(type, dsrc, elems, ddst, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, ddst, sizeof(float) * (size_t)elems, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    hipFree(dsrc);
+    hipFree(ddst);
+    if (e != hipSuccess) return fail(FLLM_E_DEVICE, "dequantize: %s", hipGetErrorString(e));
+    return FLLM_OK;
+}
+
+// =====================================================================================
+// buffers and the standalone GEMV
+// =====================================================================================
+extern "C" int32_t fllm_buf_create(fllm_ctx* ctx, uint64_t nbytes, fllm_buf** out) {
+    NOT_NULL(ctx);
+    NOT_NULL(out);
+    *out = nullptr;
+    HIP_TRY(hipSetDevice(ctx->device));
+    uint8_t* p = nullptr;
+    hipError_t e = hipMalloc(&p, nbytes + kPad);
+    if (e != hipSuccess) return fail(FLLM_E_OOM, "hipMalloc(%llu): %s", (unsigned long long)nbytes, hipGetErrorString(e));
+    e = hipMemsetAsync(p + nbytes, 0, kPad, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) { hipFree(p); return fail(FLLM_E_DEVICE, "hipMemset: %s", hipGetErrorString(e)); }
+    fllm_buf* b = new fllm_buf();
+    b->ctx = ctx;
+    b->ptr = p;
+    b->n = nbytes;
+    *out = b;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_buf_destroy(fllm_buf* b) {
+    if (!b) return FLLM_OK;
+    hipSetDevice(b->ctx->device);
+    hipStreamSynchronize(b->ctx->stream);
+    hipFree(b->ptr);
+    delete b;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_buf_write(fllm_buf* b, uint64_t offset, const void* src, uint64_t n) {
+    NOT_NULL(b);
+    if (offset > b->n || n > b->n - offset) return fail(FLLM_E_ARG, "write [%llu,+%llu) outside buffer of %llu bytes",
+                                                        (unsigned long long)offset, (unsigned long long)n, (unsigned long long)b->n);
+    if (n == 0) return FLLM_OK;
+    NOT_NULL(src);
+    HIP_TRY(hipSetDevice(b->ctx->device));
+    HIP_TRY(hipMemcpyAsync(b->ptr + offset, src, n, hipMemcpyHostToDevice, b->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(b->ctx->stream));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_buf_read(fllm_buf* b, uint64_t offset, void* dst, uint64_t n) {
+    NOT_NULL(b);
+    if (offset > b->n || n > b->n - offset) return fail(FLLM_E_ARG, "read [%llu,+%llu) outside buffer of %llu bytes",
+                                                        (unsigned long long)offset, (unsigned long long)n, (unsigned long long)b->n);
+    if (n == 0) return FLLM_OK;
+    NOT_NULL(dst);
+    HIP_TRY(hipSetDevice(b->ctx->device));
+    HIP_TRY(hipMemcpyAsync(dst, b->ptr + offset, n, hipMemcpyDeviceToHost, b->ctx->stream));
+    HIP_TRY(hipStreamSynchronize(b->ctx->stream));
+    return FLLM_OK;
+}
+
+static bool qpath_type(int t) {
+    return t == FLLM_TYPE_Q4_K || t == FLLM_TYPE_Q5_K || t == FLLM_TYPE_Q6_K || t == FLLM_TYPE_Q8_0 || t == FLLM_TYPE_Q4_0;
+}
+
+static int32_t check_gemv_args(int32_t type, fllm_buf* w, uint64_t w_offset, int64_t rows, int64_t cols, fllm_buf* x,
+                               fllm_buf* y) {
+    NOT_NULL(w);
+    NOT_NULL(x);
+    NOT_NULL(y);
+    if (!type_supported(type)) return fail(FLLM_E_NOT_SUPPORTED, "Tensor type %d is not supported.", type);
+    if (rows <= 0 || cols <= 0) return fail(FLLM_E_ARG, "rows and cols must be positive");
+    TypeInfo ti = type_info(type);
+    if ((rows * cols) % ti.block_elems != 0) return fail(FLLM_E_ARG, "rows*cols must be a whole number of blocks");
+    if (w_offset % 16 != 0) return fail(FLLM_E_ARG, "weight offset must be 16-byte aligned");
+    uint64_t wb = type_bytes(type, rows * cols);
+    if (w_offset > w->n || wb > w->n - w_offset) return fail(FLLM_E_ARG, "weight buffer too small");
+    if ((uint64_t)cols * 4 > x->n) return fail(FLLM_E_ARG, "x buffer too small");
+    if ((uint64_t)rows * 4 > y->n) return fail(FLLM_E_ARG, "y buffer too small");
+    return FLLM_OK;
+}
+
+static int32_t ctx_xq(fllm_ctx* ctx, int64_t groups, XQ* out) {
+    if (groups > ctx->xq_groups) {
+        if (ctx->xq_parts) hipFree(ctx->xq_parts);
+        if (ctx->xq_stats) hipFree(ctx->xq_stats);
+        ctx->xq_parts = nullptr;
+        ctx->xq_stats = nullptr;
+        HIP_TRY(hipMalloc(&ctx->xq_parts, sizeof(uint4) * 6 * (size_t)groups));
+        HIP_TRY(hipMalloc(&ctx->xq_stats, sizeof(float4) * (size_t)groups));
+        ctx->xq_groups = groups;
+    }
+    out->parts = ctx->xq_parts;
+    out->stats = ctx->xq_stats;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_gemv(fllm_ctx* ctx, int32_t type, fllm_buf* w, uint64_t w_offset, int64_t rows, int64_t cols,
+                             fllm_buf* x, fllm_buf* y) {
+    NOT_NULL(ctx);
+    int32_t rc = check_gemv_args(type, w, w_offset, rows, cols, x, y);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(ctx->device));
+    XQ xq{nullptr, nullptr};
+    if (qpath_type(type) && cols % 32 == 0) {
+        rc = ctx_xq(ctx, cols / 32, &xq);
+        if (rc) return rc;
+        HIP_TRY(launch_quantize((const float*)x->ptr, cols, xq, ctx->stream));
+    }
+    WMat m{w->ptr + w_offset, type, rows, cols};
+    HIP_TRY(launch_gemv(m, (const float*)x->ptr, xq, (float*)y->ptr, nullptr, ctx->stream));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_gemv_time(fllm_ctx* ctx, int32_t type, fllm_buf* const* w, int32_t n_w, int64_t rows,
+                                  int64_t cols, fllm_buf* x, fllm_buf* y, int32_t iters, double* avg_us) {
+    NOT_NULL(ctx);
+    NOT_NULL(w);
+    NOT_NULL(avg_us);
+    if (n_w <= 0 || iters <= 0) return fail(FLLM_E_ARG, "n_w and iters must be positive");
+    for (int i = 0; i < n_w; i++) {
+        int32_t rc = check_gemv_args(type, w[i], 0, rows, cols, x, y);
+        if (rc) return rc;
+    }
+    HIP_TRY(hipSetDevice(ctx->device));
+    XQ xq{nullptr, nullptr};
+    if (qpath_type(type) && cols % 32 == 0) {
+        int32_t rc = ctx_xq(ctx, cols / 32, &xq);
+        if (rc) return rc;
+        HIP_TRY(launch_quantize((const float*)x->ptr, cols, xq, ctx->stream));
+    }
+    std::vector<hipEvent_t> ev(2 * (size_t)iters);
+    for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
+    hipError_t err = hipSuccess;
+    for (int i = 0; i < iters && err == hipSuccess; i++) {
+        WMat m{w[i % n_w]->ptr, type, rows, cols};
+        err = hipEventRecord(ev[2 * i], ctx->stream);
+        if (err == hipSuccess) err = launch_gemv(m, (const float*)x->ptr, xq, (float*)y->ptr, nullptr, ctx->stream);
+        if (err == hipSuccess) err = hipEventRecord(ev[2 * i + 1], ctx->stream);
+    }
+    if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
+    double tot = 0;
+    for (int i = 0; i < iters && err == hipSuccess; i++) {
+        float ms = 0;
+        err = hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
+        tot += ms;
+    }
+    for (auto& e : ev) hipEventDestroy(e);
+    if (err != hipSuccess) return fail(FLLM_E_DEVICE, "gemv_time: %s", hipGetErrorString(err));
+    *avg_us = tot * 1000.0 / iters;
+    return FLLM_OK;
+}
+
+// =====================================================================================
+// model
+// =====================================================================================
+extern "C" int32_t fllm_model_create(fllm_ctx* ctx, const fllm_model_desc* desc, fllm_model** out) {
+    NOT_NULL(ctx);
+    NOT_NULL(desc);
+    NOT_NULL(out);
+    *out = nullptr;
+    const fllm_model_desc& d = *desc;
+    if (d.arch < FLLM_ARCH_LLAMA || d.arch > FLLM_ARCH_GEMMA2)
+        return fail(FLLM_E_NOT_SUPPORTED, "Architecture %d is not supported.", d.arch);
+    // LlamaForwardPass.cs:48-52 head configuration check
+    if (d.n_kv_heads <= 0 || d.n_heads <= 0 || d.n_kv_heads > d.n_heads || d.n_heads % d.n_kv_heads != 0)
+        return fail(FLLM_E_ARG_RANGE, "Invalid attention head configuration: NumHeads=%d, NumKvHeads=%d.", d.n_heads, d.n_kv_heads);
+    if (d.n_layers <= 0 || d.hidden <= 0 || d.ffn <= 0 || d.vocab <= 0 || d.head_dim <= 0 || d.max_ctx <= 0)
+        return fail(FLLM_E_ARG, "model dimensions must be positive");
+    if (d.head_dim % 2 != 0) return fail(FLLM_E_ARG, "headDim must be even.");
+    if (d.head_dim % 4 != 0 || d.head_dim > 256) return fail(FLLM_E_NOT_SUPPORTED, "head_dim %d not supported (multiple of 4, <= 256)", d.head_dim);
+    fllm_model* m = new fllm_model();
+    m->ctx = ctx;
+    m->d = d;
+    m->qdim = d.n_heads * d.head_dim;
+    m->kvdim = d.n_kv_heads * d.head_dim;
+    m->layers.resize((size_t)d.n_layers);
+    *out = m;
+    return FLLM_OK;
+}
+
+static void free_tensor(Tensor& t) {
+    if (t.ptr) hipFree(t.ptr);
+    t = Tensor();
+}
+
+extern "C" int32_t fllm_model_destroy(fllm_model* m) {
+    if (!m) return FLLM_OK;
+    hipSetDevice(m->ctx->device);
+    hipDeviceSynchronize();
+    free_tensor(m->tok_embd);
+    if (!m->output_tied) free_tensor(m->output);
+    if (m->out_norm) hipFree(m->out_norm);
+    for (auto& L : m->layers) {
+        free_tensor(L.q); free_tensor(L.k); free_tensor(L.v); free_tensor(L.o);
+        free_tensor(L.gate); free_tensor(L.up); free_tensor(L.down);
+        float* vecs[] = {L.attn_norm, L.ffn_norm, L.post_attn, L.post_ffn, L.bq, L.bk, L.bv};
+        for (float* p : vecs)
+            if (p) hipFree(p);
+    }
+    delete m;
+    return FLLM_OK;
+}
+
+// Expected (rows, cols) of a slot, as LoadTensor's expectedElements (GgufModelLoader.cs:326-354).
+static bool slot_shape(const fllm_model* m, int slot, int64_t& rows, int64_t& cols, bool& vec) {
+    const fllm_model_desc& d = m->d;
+    vec = false;
+    switch (slot) {
+        case FLLM_SLOT_TOKEN_EMBD: case FLLM_SLOT_OUTPUT: rows = d.vocab; cols = d.hidden; return true;
+        case FLLM_SLOT_ATTN_Q: rows = m->qdim; cols = d.hidden; return true;
+        case FLLM_SLOT_ATTN_K: case FLLM_SLOT_ATTN_V: rows = m->kvdim; cols = d.hidden; return true;
+        case FLLM_SLOT_ATTN_OUTPUT: rows = d.hidden; cols = m->qdim; return true;
+        case FLLM_SLOT_FFN_GATE: case FLLM_SLOT_FFN_UP: rows = d.ffn; cols = d.hidden; return true;
+        case FLLM_SLOT_FFN_DOWN: rows = d.hidden; cols = d.ffn; return true;
+        case FLLM_SLOT_OUTPUT_NORM: case FLLM_SLOT_ATTN_NORM: case FLLM_SLOT_POST_ATTN_NORM:
+        case FLLM_SLOT_FFN_NORM: case FLLM_SLOT_POST_FFN_NORM:
+            rows = 1; cols = d.hidden; vec = true; return true;
+        case FLLM_SLOT_ATTN_Q_BIAS: rows = 1; cols = m->qdim; vec = true; return true;
+        case FLLM_SLOT_ATTN_K_BIAS: case FLLM_SLOT_ATTN_V_BIAS: rows = 1; cols = m->kvdim; vec = true; return true;
+        default: return false;
+    }
+}
+
+extern "C" int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer, int32_t type, const void* bytes,
+                                     uint64_t nbytes) {
+    NOT_NULL(m);
+    if (m->finalized) return fail(FLLM_E_INVALID_OP, "model already finalized");
+    int64_t rows, cols;
+    bool vec;
+    if (!slot_shape(m, slot, rows, cols, vec)) return fail(FLLM_E_ARG_RANGE, "unknown tensor slot %d", slot);
+    bool per_layer = slot >= 10;
+    if (per_layer && (layer < 0 || layer >= m->d.n_layers))
+        return fail(FLLM_E_ARG_RANGE, "Layer index must be in [0, %d].", m->d.n_layers - 1);
+    if (!type_supported(type)) return fail(FLLM_E_NOT_SUPPORTED, "Tensor type %d is not supported for dequantization.", type);
+    TypeInfo ti = type_info(type);
+    int64_t n = rows * cols;
+    if (n % ti.block_elems != 0) return fail(FLLM_E_ARG, "tensor of %lld elements is not a whole number of type-%d blocks", (long long)n, type);
+    uint64_t want = type_bytes(type, n);
+    if (nbytes != want)
+        return fail(FLLM_E_ARG, "tensor slot %d: %llu bytes given, %llu expected for %lld elements of type %d", slot,
+                    (unsigned long long)nbytes, (unsigned long long)want, (long long)n, type);
+    NOT_NULL(bytes);
+    hipStream_t st = m->ctx->stream;
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    uint8_t* dev = nullptr;
+    hipError_t e = hipMalloc(&dev, nbytes + kPad);
+    if (e != hipSuccess) return fail(FLLM_E_OOM, "hipMalloc(%llu): %s", (unsigned long long)nbytes, hipGetErrorString(e));
+    e = hipMemcpyAsync(dev, bytes, nbytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipMemsetAsync(dev + nbytes, 0, kPad, st);
+    if (e != hipSuccess) { hipFree(dev); return fail(FLLM_E_DEVICE, "upload: %s", hipGetErrorString(e)); }
+    if (vec) {
+        // norms and biases: dequantize once to F32 on the device
+        float* f = nullptr;
+        e = hipMalloc(&f, sizeof(float) * (size_t)n);
+        if (e == hipSuccess) e = launch_dequant(type, dev, n, f, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        hipFree(dev);
+        if (e != hipSuccess) { if (f) hipFree(f); return fail(FLLM_E_DEVICE, "upload: %s", hipGetErrorString(e)); }
+        float** where = nullptr;
+        if (slot == FLLM_SLOT_OUTPUT_NORM) where = &m->out_norm;
+        else {
+            Layer& L = m->layers[(size_t)layer];
+            switch (slot) {
+                case FLLM_SLOT_ATTN_NORM: where = &L.attn_norm; break;
+                case FLLM_SLOT_FFN_NORM: where = &L.ffn_norm; break;
+                case FLLM_SLOT_POST_ATTN_NORM: where = &L.post_attn; break;
+                case FLLM_SLOT_POST_FFN_NORM: where = &L.post_ffn; break;
+                case FLLM_SLOT_ATTN_Q_BIAS: where = &L.bq; break;
+                case FLLM_SLOT_ATTN_K_BIAS: where = &L.bk; break;
+                default: where = &L.bv; break;
+            }
+        }
+        if (*where) hipFree(*where);
+        *where = f;
+        return FLLM_OK;
+    }
+    e = hipStreamSynchronize(st);
+    if (e != hipSuccess) { hipFree(dev); return fail(FLLM_E_DEVICE, "upload: %s", hipGetErrorString(e)); }
+    Tensor t;
+    t.ptr = dev; t.type = type; t.rows = rows; t.cols = cols; t.bytes = nbytes;
+    Tensor* where = nullptr;
+    if (slot == FLLM_SLOT_TOKEN_EMBD) where = &m->tok_embd;
+    else if (slot == FLLM_SLOT_OUTPUT) where = &m->output;
+    else {
+        Layer& L = m->layers[(size_t)layer];
+        switch (slot) {
+            case FLLM_SLOT_ATTN_Q: where = &L.q; break;
+            case FLLM_SLOT_ATTN_K: where = &L.k; break;
+            case FLLM_SLOT_ATTN_V: where = &L.v; break;
+            case FLLM_SLOT_ATTN_OUTPUT: where = &L.o; break;
+            case FLLM_SLOT_FFN_GATE: where = &L.gate; break;
+            case FLLM_SLOT_FFN_UP: where = &L.up; break;
+            default: where = &L.down; break;
+        }
+    }
+    free_tensor(*where);
+    *where = t;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_model_finalize(fllm_model* m) {
+    NOT_NULL(m);
+    if (m->finalized) return FLLM_OK;
+    const fllm_model_desc& d = m->d;
+    if (!m->tok_embd.present()) return fail(FLLM_E_INVALID_OP, "Required tensor 'token_embd.weight' not found in GGUF file.");
+    if (!m->out_norm) return fail(FLLM_E_INVALID_OP, "Required tensor 'output_norm.weight' not found in GGUF file.");
+    for (int l = 0; l < d.n_layers; l++) {
+        Layer& L = m->layers[(size_t)l];
+        struct { bool ok; const char* name; } req[] = {
+            {L.attn_norm != nullptr, "attn_norm.weight"}, {L.q.present(), "attn_q.weight"},
+            {L.k.present(), "attn_k.weight"}, {L.v.present(), "attn_v.weight"},
+            {L.o.present(), "attn_output.weight"}, {L.ffn_norm != nullptr, "ffn_norm.weight"},
+            {L.gate.present(), "ffn_gate.weight"}, {L.up.present(), "ffn_up.weight"},
+            {L.down.present(), "ffn_down.weight"},
+            {d.arch != FLLM_ARCH_QWEN2 || L.bq, "attn_q.bias"}, {d.arch != FLLM_ARCH_QWEN2 || L.bk, "attn_k.bias"},
+            {d.arch != FLLM_ARCH_QWEN2 || L.bv, "attn_v.bias"},
+            {d.arch != FLLM_ARCH_GEMMA2 || L.post_attn, "post_attn_norm.weight"},
+            {d.arch != FLLM_ARCH_GEMMA2 || L.post_ffn, "post_ffn_norm.weight"},
+        };
+        for (auto& r : req)
+            if (!r.ok) return fail(FLLM_E_INVALID_OP, "Required tensor 'blk.%d.%s' not found in GGUF file.", l, r.name);
+    }
+    if (!m->output.present()) {  // GgufModelLoader.cs:353-354: tied LM head
+        m->output = m->tok_embd;
+        m->output_tied = true;
+    }
+    // RoPE inverse frequencies (LlamaForwardPass.cs:64-70), computed on the host with powf.
+    int half = d.head_dim / 2;
+    m->inv_freq.resize((size_t)half);
+    for (int i = 0; i < half; i++) {
+        float e = (2.0f * (float)i) / (float)d.head_dim;
+        m->inv_freq[(size_t)i] = 1.0f / powf(d.rope_base, e);
+    }
+    uint64_t lb = 0;
+    for (auto& L : m->layers) lb += L.q.bytes + L.k.bytes + L.v.bytes + L.o.bytes + L.gate.bytes + L.up.bytes + L.down.bytes;
+    m->layer_bytes = lb;
+    m->head_bytes = m->output.bytes;
+    m->finalized = true;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_model_get_desc(fllm_model* m, fllm_model_desc* out) {
+    NOT_NULL(m);
+    NOT_NULL(out);
+    *out = m->d;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_model_weight_bytes(fllm_model* m, uint64_t* layer_bytes, uint64_t* head_bytes) {
+    NOT_NULL(m);
+    if (!m->finalized) return fail(FLLM_E_INVALID_OP, "model not finalized");
+    if (layer_bytes) *layer_bytes = m->layer_bytes;
+    if (head_bytes) *head_bytes = m->head_bytes;
+    return FLLM_OK;
+}
+
+// =====================================================================================
+// sequence
+// =====================================================================================
+template <typename T>
+static hipError_t seq_alloc(fllm_seq* s, T** p, size_t count) {
+    void* v = nullptr;
+    hipError_t e = hipMalloc(&v, sizeof(T) * (count ? count : 1));
+    if (e == hipSuccess) {
+        s->allocs.push_back(v);
+        *p = (T*)v;
+    }
+    return e;
+}
+
+static void seq_free(fllm_seq* s) {
+    if (s->gexec) hipGraphExecDestroy(s->gexec);
+    if (s->graph) hipGraphDestroy(s->graph);
+    for (void* p : s->allocs) hipFree(p);
+    for (auto e : s->ev) hipEventDestroy(e);
+    if (s->st) hipStreamDestroy(s->st);
+    delete s;
+}
+
+extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** out) {
+    NOT_NULL(m);
+    NOT_NULL(out);
+    *out = nullptr;
+    if (!m->finalized) return fail(FLLM_E_INVALID_OP, "model not finalized");
+    if (max_seq < 0) return fail(FLLM_E_ARG_RANGE, "max_seq must be >= 0");
+    const fllm_model_desc& d = m->d;
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    fllm_seq* s = new fllm_seq();
+    s->m = m;
+    s->max_seq = max_seq > 0 ? max_seq : d.max_ctx;
+    s->nsplit = (s->max_seq + 255) / 256;
+    hipError_t e = hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking);
+    if (e != hipSuccess) { s->st = nullptr; seq_free(s); return fail(FLLM_E_DEVICE, "hipStreamCreate: %s", hipGetErrorString(e)); }
+    size_t L = (size_t)d.n_layers, kv = (size_t)m->kvdim, H = (size_t)d.hidden, F = (size_t)d.ffn;
+    size_t kvsz = L * (size_t)s->max_seq * kv;
+    int half = d.head_dim / 2;
+    s->topk_cap = d.vocab;
+#define ALLOC(ptr, n) \
+    if (e == hipSuccess) e = seq_alloc(s, &(ptr), (n))
+    ALLOC(s->kc, kvsz);
+    ALLOC(s->vc, kvsz);
+    ALLOC(s->rope, (size_t)s->max_seq * half);
+    ALLOC(s->params, 1);
+    ALLOC(s->x, H);
+    ALLOC(s->xn, H);
+    ALLOC(s->q, (size_t)m->qdim);
+    ALLOC(s->k, kv);
+    ALLOC(s->v, kv);
+    ALLOC(s->att, (size_t)m->qdim);
+    ALLOC(s->g, F);
+    ALLOC(s->u, F);
+    ALLOC(s->h, F);
+    ALLOC(s->tmp, H);
+    ALLOC(s->logits, (size_t)d.vocab);
+    ALLOC(s->xq_hidden.parts, 6 * (H / 32 + 1));
+    ALLOC(s->xq_hidden.stats, H / 32 + 1);
+    ALLOC(s->xq_att.parts, 6 * ((size_t)m->qdim / 32 + 1));
+    ALLOC(s->xq_att.stats, (size_t)m->qdim / 32 + 1);
+    ALLOC(s->xq_h.parts, 6 * (F / 32 + 1));
+    ALLOC(s->xq_h.stats, F / 32 + 1);
+    ALLOC(s->part_o, (size_t)d.n_heads * s->nsplit * d.head_dim);
+    ALLOC(s->part_ml, (size_t)d.n_heads * s->nsplit * 2);
+    ALLOC(s->topk_ids, (size_t)d.vocab);
+    ALLOC(s->topk_vals, (size_t)d.vocab);
+    ALLOC(s->topk_count, 1);
+    ALLOC(s->hidden_dbg, (L + 1) * H);
+#undef ALLOC
+    if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_OOM, "sequence allocation: %s", hipGetErrorString(e)); }
+    // RoPE table: theta = scaledPos * inv[i] (LlamaForwardPass.cs:137-147), cos/sin on the host.
+    std::vector<float2> tab((size_t)s->max_seq * half);
+    for (int p = 0; p < s->max_seq; p++) {
+        float sp = (d.rope_scaled && d.rope_scale > 0.0f) ? (float)p / d.rope_scale : (float)p;
+        for (int i = 0; i < half; i++) {
+            float th = sp * m->inv_freq[(size_t)i];
+            tab[(size_t)p * half + i] = make_float2(cosf(th), sinf(th));
+        }
+    }
+    e = hipMemcpyAsync(s->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice, s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->kc, 0, sizeof(float) * kvsz, s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, sizeof(float) * kvsz, s->st);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->st);
+    if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_DEVICE, "sequence init: %s", hipGetErrorString(e)); }
+    *out = s;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_destroy(fllm_seq* s) {
+    if (!s) return FLLM_OK;
+    hipSetDevice(s->m->ctx->device);
+    hipStreamSynchronize(s->st);
+    seq_free(s);
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_reset(fllm_seq* s) {
+    NOT_NULL(s);
+    HIP_TRY(hipStreamSynchronize(s->st));
+    s->cur_len = 0;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_length(fllm_seq* s, int32_t* len) {
+    NOT_NULL(s);
+    NOT_NULL(len);
+    *len = s->cur_len;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_capacity(fllm_seq* s, int32_t* cap) {
+    NOT_NULL(s);
+    NOT_NULL(cap);
+    *cap = s->max_seq;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_get_model(fllm_seq* s, fllm_model** out) {
+    NOT_NULL(s);
+    NOT_NULL(out);
+    *out = s->m;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_set_graph(fllm_seq* s, int32_t enable) {
+    NOT_NULL(s);
+    s->use_graph = enable != 0;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable) {
+    NOT_NULL(s);
+    if (s->debug != (enable != 0)) s->graph_valid = false;
+    s->debug = enable != 0;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_sync(fllm_seq* s) {
+    NOT_NULL(s);
+    HIP_TRY(hipStreamSynchronize(s->st));
+    return FLLM_OK;
+}
+
+// ---- profiling helpers ------------------------------------------------------------
+static hipError_t prof_begin(fllm_seq* s, const char* name, double bytes) {
+    if (!s->profile) return hipSuccess;
+    size_t i = s->pending.size();
+    while (s->ev.size() < 2 * (i + 1)) {
+        hipEvent_t e;
+        hipError_t r = hipEventCreate(&e);
+        if (r != hipSuccess) return r;
+        s->ev.push_back(e);
+    }
+    s->pending.emplace_back(name, bytes);
+    return hipEventRecord(s->ev[2 * i], s->st);
+}
+
+static hipError_t prof_end(fllm_seq* s) {
+    if (!s->profile) return hipSuccess;
+    size_t i = s->pending.size() - 1;
+    return hipEventRecord(s->ev[2 * i + 1], s->st);
+}
+
+static hipError_t prof_collect(fllm_seq* s) {
+    if (!s->profile || s->pending.empty()) return hipSuccess;
+    hipError_t e = hipStreamSynchronize(s->st);
+    if (e != hipSuccess) return e;
+    for (size_t i = 0; i < s->pending.size(); i++) {
+        float ms = 0;
+        e = hipEventElapsedTime(&ms, s->ev[2 * i], s->ev[2 * i + 1]);
+        if (e != hipSuccess) return e;
+        auto it = s->agg.find(s->pending[i].first);
+        if (it == s->agg.end()) {
+            s->agg_order.push_back(s->pending[i].first);
+            it = s->agg.emplace(s->pending[i].first, ProfAgg()).first;
+        }
+        it->second.launches++;
+        it->second.ms += ms;
+        it->second.bytes += s->pending[i].second;
+    }
+    s->pending.clear();
+    return hipSuccess;
+}
+
+static const char* gemv_name(int type) {
+    switch (type) {
+        case FLLM_TYPE_Q4_K: return "gemv_q4_k";
+        case FLLM_TYPE_Q5_K: return "gemv_q5_k";
+        case FLLM_TYPE_Q6_K: return "gemv_q6_k";
+        case FLLM_TYPE_Q8_0: return "gemv_q8_0";
+        case FLLM_TYPE_Q4_0: return "gemv_q4_0";
+        case FLLM_TYPE_F32: return "gemv_f32";
+        case FLLM_TYPE_F16: return "gemv_f16";
+        case FLLM_TYPE_BF16: return "gemv_bf16";
+        default: return "gemv_generic";
+    }
+}
+
+#define STEP(name, bytes, call)                          \
+    do {                                                 \
+        hipError_t _e = prof_begin(s, (name), (bytes));  \
+        if (_e == hipSuccess) _e = (call);               \
+        if (_e == hipSuccess) _e = prof_end(s);          \
+        if (_e != hipSuccess) return _e;                 \
+    } while (0)
+
+static hipError_t gemv_step(fllm_seq* s, const Tensor& t, const float* xf, const XQ& xq, float* y, const float* res) {
+    double bytes = (double)t.bytes + 4.0 * (double)(t.cols + t.rows);
+    STEP(gemv_name(t.type), bytes, launch_gemv(t.mat(), xf, xq, y, res, s->st));
+    return hipSuccess;
+}
+
+// The decode step body (everything after the step-parameter write), launched eagerly or captured.
+static hipError_t enqueue_body(fllm_seq* s) {
+    fllm_model* m = s->m;
+    const fllm_model_desc& d = m->d;
+    bool gemma = d.arch == FLLM_ARCH_GEMMA2;
+    int H = d.hidden, kvdim = m->kvdim;
+    float eps = gemma ? 1e-6f : d.norm_eps;
+    int nk = gemma ? 1 : 0;
+    size_t layer_kv = (size_t)s->max_seq * kvdim;
+    STEP("embed", 4.0 * H, launch_embed(m->tok_embd.ptr, m->tok_embd.type, H, s->params, s->x, s->st));
+    for (int l = 0; l < d.n_layers; l++) {
+        const Layer& L = m->layers[(size_t)l];
+        STEP("rmsnorm", 12.0 * H, launch_rmsnorm_q(s->x, L.attn_norm, H, eps, nk, s->xn, s->xq_hidden, s->st));
+        hipError_t e;
+        if ((e = gemv_step(s, L.q, s->xn, s->xq_hidden, s->q, nullptr)) != hipSuccess) return e;
+        if ((e = gemv_step(s, L.k, s->xn, s->xq_hidden, s->k, nullptr)) != hipSuccess) return e;
+        if ((e = gemv_step(s, L.v, s->xn, s->xq_hidden, s->v, nullptr)) != hipSuccess) return e;
+        float* kc = s->kc + (size_t)l * layer_kv;
+        float* vc = s->vc + (size_t)l * layer_kv;
+        STEP("qkv_rope_kvstore", 8.0 * (m->qdim + 2 * kvdim),
+             launch_qkv_post(s->q, s->k, s->v, L.bq, L.bk, L.bv, s->rope, d.n_heads, d.n_kv_heads, d.head_dim, kc, vc,
+                             s->params, s->st));
+        int window = 0x7FFFFFFF;
+        if (d.arch == FLLM_ARCH_MISTRAL) window = d.sliding_window;
+        if (gemma && (l % 2) == 0) window = d.sliding_window;
+        STEP("attention", 0.0,
+             launch_attention(s->q, kc, vc, d.n_heads, d.n_kv_heads, d.head_dim, window, d.attn_scale,
+                              gemma ? d.attn_softcap : 0.0f, s->nsplit, s->part_o, s->part_ml, s->att, s->xq_att,
+                              s->params, s->st));
+        if (gemma) {
+            if ((e = gemv_step(s, L.o, s->att, s->xq_att, s->tmp, nullptr)) != hipSuccess) return e;
+            STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));
+        } else {
+            if ((e = gemv_step(s, L.o, s->att, s->xq_att, s->x, s->x)) != hipSuccess) return e;
+        }
+        STEP("rmsnorm", 12.0 * H, launch_rmsnorm_q(s->x, L.ffn_norm, H, eps, nk, s->xn, s->xq_hidden, s->st));
+        if ((e = gemv_step(s, L.gate, s->xn, s->xq_hidden, s->g, nullptr)) != hipSuccess) return e;
+        if ((e = gemv_step(s, L.up, s->xn, s->xq_hidden, s->u, nullptr)) != hipSuccess) return e;
+        STEP("ffn_act", 12.0 * d.ffn, launch_act(s->g, s->u, d.ffn, gemma ? 1 : 0, s->h, s->xq_h, s->st));
+        if (gemma) {
+            if ((e = gemv_step(s, L.down, s->h, s->xq_h, s->tmp, nullptr)) != hipSuccess) return e;
+            STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, s->x, s->st));
+        } else {
+            if ((e = gemv_step(s, L.down, s->h, s->xq_h, s->x, s->x)) != hipSuccess) return e;
+        }
+        if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(s->x, H, s->hidden_dbg + (size_t)l * H, s->st));
+    }
+    STEP("rmsnorm", 12.0 * H, launch_rmsnorm_q(s->x, m->out_norm, H, eps, nk, s->xn, s->xq_hidden, s->st));
+    if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(s->xn, H, s->hidden_dbg + (size_t)d.n_layers * H, s->st));
+    hipError_t e = gemv_step(s, m->output, s->xn, s->xq_hidden, s->logits, nullptr);
+    if (e != hipSuccess) return e;
+    if (gemma && d.final_softcap > 0.0f) STEP("softcap", 8.0 * d.vocab, launch_softcap(s->logits, d.vocab, d.final_softcap, s->st));
+    return hipSuccess;
+}
+
+static int32_t enqueue_step(fllm_seq* s, int token, int pos) {
+    HIP_TRY(launch_set_params(s->params, token, pos, s->cur_len, s->st));
+    bool graph = s->use_graph && !s->profile;
+    if (!graph) {
+        hipError_t e = enqueue_body(s);
+        if (e != hipSuccess) return fail(FLLM_E_DEVICE, "decode step: %s", hipGetErrorString(e));
+        e = prof_collect(s);
+        if (e != hipSuccess) return fail(FLLM_E_DEVICE, "profile: %s", hipGetErrorString(e));
+        return FLLM_OK;
+    }
+    if (!s->graph_valid) {
+        if (s->gexec) { hipGraphExecDestroy(s->gexec); s->gexec = nullptr; }
+        if (s->graph) { hipGraphDestroy(s->graph); s->graph = nullptr; }
+        HIP_TRY(hipStreamBeginCapture(s->st, hipStreamCaptureModeThreadLocal));
+        hipError_t e = enqueue_body(s);
+        hipGraph_t g = nullptr;
+        hipError_t e2 = hipStreamEndCapture(s->st, &g);
+        if (e != hipSuccess) { if (g) hipGraphDestroy(g); return fail(FLLM_E_DEVICE, "capture: %s", hipGetErrorString(e)); }
+        if (e2 != hipSuccess) return fail(FLLM_E_DEVICE, "hipStreamEndCapture: %s", hipGetErrorString(e2));
+        s->graph = g;
+        HIP_TRY(hipGraphInstantiate(&s->gexec, s->graph, nullptr, nullptr, 0));
+        s->graph_valid = true;
+    }
+    HIP_TRY(hipGraphLaunch(s->gexec, s->st));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position) {
+    NOT_NULL(s);
+    const fllm_model_desc& d = s->m->d;
+    if (token < 0 || token >= d.vocab)
+        return fail(FLLM_E_ARG_RANGE, "Token id %d is outside the valid vocabulary range [0, %d].", token, d.vocab - 1);
+    if (position < 0 || position > s->cur_len)
+        return fail(FLLM_E_ARG_RANGE, "position %d outside the cached range [0, %d]", position, s->cur_len);
+    if (s->cur_len >= s->max_seq)
+        return fail(FLLM_E_ARG_RANGE, "KV cache full (%d positions)", s->max_seq);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    int32_t rc = enqueue_step(s, token, position);
+    if (rc) return rc;
+    s->cur_len++;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, int32_t pos0) {
+    NOT_NULL(s);
+    if (n < 0) return fail(FLLM_E_ARG_RANGE, "n must be >= 0");
+    if (n > 0) NOT_NULL(tokens);
+    for (int i = 0; i < n; i++) {
+        int32_t rc = fllm_forward(s, tokens[i], pos0 + i);
+        if (rc) return rc;
+    }
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_logits_copy(fllm_seq* s, float* dst, int64_t n) {
+    NOT_NULL(s);
+    NOT_NULL(dst);
+    int V = s->m->d.vocab;
+    if (n < V) return fail(FLLM_E_ARG, "destination must hold %d floats", V);
+    HIP_TRY(hipMemcpyAsync(dst, s->logits, sizeof(float) * (size_t)V, hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_logits_write(fllm_seq* s, const float* src, int64_t n) {
+    NOT_NULL(s);
+    NOT_NULL(src);
+    int V = s->m->d.vocab;
+    if (n != V) return fail(FLLM_E_ARG, "source must hold exactly %d floats", V);
+    HIP_TRY(hipMemcpyAsync(s->logits, src, sizeof(float) * (size_t)V, hipMemcpyHostToDevice, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token) {
+    NOT_NULL(s);
+    NOT_NULL(out_token);
+    HIP_TRY(launch_argmax(s->logits, s->m->d.vocab, s->params, s->st));
+    StepParams hp;
+    HIP_TRY(hipMemcpyAsync(&hp, s->params, sizeof(hp), hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    *out_token = hp.argmax;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int32_t* ids, float* vals, int32_t cap,
+                                    int32_t* n_out) {
+    NOT_NULL(s);
+    NOT_NULL(n_out);
+    if (k < 1) return fail(FLLM_E_ARG_RANGE, "k must be at least 1.");
+    if (cap > 0) { NOT_NULL(ids); NOT_NULL(vals); }
+    int V = s->m->d.vocab;
+    int dcap = cap < s->topk_cap ? cap : s->topk_cap;
+    HIP_TRY(launch_topk(s->logits, V, inv_temp, k, dcap, s->topk_ids, s->topk_vals, s->topk_count, s->st));
+    int cnt = 0;
+    HIP_TRY(hipMemcpyAsync(&cnt, s->topk_count, sizeof(int), hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    *n_out = cnt;
+    if (cnt > cap) return fail(FLLM_E_ARG, "%d candidates survive top-%d, capacity %d", cnt, k, cap);
+    if (cnt > 0) {
+        HIP_TRY(hipMemcpyAsync(ids, s->topk_ids, sizeof(int) * (size_t)cnt, hipMemcpyDeviceToHost, s->st));
+        HIP_TRY(hipMemcpyAsync(vals, s->topk_vals, sizeof(float) * (size_t)cnt, hipMemcpyDeviceToHost, s->st));
+        HIP_TRY(hipStreamSynchronize(s->st));
+    }
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_debug_hidden(fllm_seq* s, int32_t layer, float* dst, int64_t n) {
+    NOT_NULL(s);
+    NOT_NULL(dst);
+    const fllm_model_desc& d = s->m->d;
+    if (!s->debug) return fail(FLLM_E_INVALID_OP, "debug capture is off (fllm_seq_set_debug)");
+    if (layer < 0 || layer > d.n_layers) return fail(FLLM_E_ARG_RANGE, "layer %d outside [0, %d]", layer, d.n_layers);
+    if (n < d.hidden) return fail(FLLM_E_ARG, "destination must hold %d floats", d.hidden);
+    HIP_TRY(hipMemcpyAsync(dst, s->hidden_dbg + (size_t)layer * d.hidden, sizeof(float) * (size_t)d.hidden,
+                           hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_kv_read(fllm_seq* s, int32_t layer, int32_t kind, float* dst, int64_t n) {
+    NOT_NULL(s);
+    NOT_NULL(dst);
+    const fllm_model_desc& d = s->m->d;
+    if (layer < 0 || layer >= d.n_layers) return fail(FLLM_E_ARG_RANGE, "Layer index must be in [0, %d].", d.n_layers - 1);
+    if (kind != 0 && kind != 1) return fail(FLLM_E_ARG_RANGE, "kind must be 0 (keys) or 1 (values)");
+    int64_t cnt = (int64_t)s->cur_len * s->m->kvdim;
+    if (n < cnt) return fail(FLLM_E_ARG, "destination must hold %lld floats", (long long)cnt);
+    if (cnt == 0) return FLLM_OK;
+    const float* src = (kind == 0 ? s->kc : s->vc) + (size_t)layer * s->max_seq * s->m->kvdim;
+    HIP_TRY(hipMemcpyAsync(dst, src, sizeof(float) * (size_t)cnt, hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_set_profile(fllm_seq* s, int32_t enable) {
+    NOT_NULL(s);
+    s->profile = enable != 0;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_profile_count(fllm_seq* s, int32_t* n) {
+    NOT_NULL(s);
+    NOT_NULL(n);
+    *n = (int32_t)s->agg_order.size();
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_profile_entry(fllm_seq* s, int32_t i, char* name, int32_t name_cap, int64_t* launches,
+                                          double* total_ms, double* total_bytes) {
+    NOT_NULL(s);
+    if (i < 0 || i >= (int32_t)s->agg_order.size()) return fail(FLLM_E_ARG_RANGE, "entry %d out of range", i);
+    const std::string& nm = s->agg_order[(size_t)i];
+    const ProfAgg& a = s->agg[nm];
+    if (name && name_cap > 0) {
+        snprintf(name, (size_t)name_cap, "%s", nm.c_str());
+    }
+    if (launches) *launches = a.launches;
+    if (total_ms) *total_ms = a.ms;
+    if (total_bytes) *total_bytes = a.bytes;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_profile_reset(fllm_seq* s) {
+    NOT_NULL(s);
+    s->agg.clear();
+    s->agg_order.clear();
+    s->pending.clear();
+    return FLLM_OK;
+}

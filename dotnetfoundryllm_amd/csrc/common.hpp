@@ -1,0 +1,83 @@
+// common.hpp — shared definitions for the gfx950 decode library (device + host side).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fllm.h"
+
+namespace fllm {
+
+// ---- GGML block geometry (Dequantizer.cs:21-43; GgufFile.ComputeByteSize GgufFile.cs:99-122)
+struct TypeInfo {
+    int block_bytes;
+    int block_elems;
+};
+
+__host__ __device__ inline bool type_supported(int t) {
+    return t == FLLM_TYPE_F32 || t == FLLM_TYPE_F16 || t == FLLM_TYPE_BF16 || t == FLLM_TYPE_Q4_0 ||
+           t == FLLM_TYPE_Q8_0 || t == FLLM_TYPE_Q4_K || t == FLLM_TYPE_Q5_K || t == FLLM_TYPE_Q6_K ||
+           t == FLLM_TYPE_Q8_K;
+}
+
+__host__ __device__ inline TypeInfo type_info(int t) {
+    switch (t) {
+        case FLLM_TYPE_F32: return {4, 1};
+        case FLLM_TYPE_F16: return {2, 1};
+        case FLLM_TYPE_BF16: return {2, 1};
+        case FLLM_TYPE_Q4_0: return {18, 32};
+        case FLLM_TYPE_Q8_0: return {34, 32};
+        case FLLM_TYPE_Q4_K: return {144, 256};
+        case FLLM_TYPE_Q5_K: return {176, 256};
+        case FLLM_TYPE_Q6_K: return {210, 256};
+        case FLLM_TYPE_Q8_K: return {292, 256};
+        default: return {0, 0};
+    }
+}
+
+// Bytes occupied by n elements of type t (n must be a whole number of blocks).
+__host__ __device__ inline uint64_t type_bytes(int t, int64_t n) {
+    TypeInfo ti = type_info(t);
+    if (ti.block_elems == 0) return 0;
+    return (uint64_t)(n / ti.block_elems) * (uint64_t)ti.block_bytes;
+}
+
+// ---- exact scalar conversions (Dequantizer.HalfToFloat / BFloat16ToFloat, Dequantizer.cs:49-59)
+__host__ __device__ inline float bits_f32(uint32_t u) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return __uint_as_float(u);
+#else
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+#endif
+}
+
+// Integer-exact binary16 -> binary32 (keeps NaN payloads, independent of FP modes).
+__host__ __device__ inline float half_exact(uint32_t h) {
+    uint32_t sign = (h >> 15) << 31;
+    uint32_t ex = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    if (ex == 0) {
+        float v = (float)man * 5.9604644775390625e-08f;  // man * 2^-24, exact
+        return sign ? -v : v;
+    }
+    if (ex == 31) return bits_f32(sign | 0x7F800000u | (man << 13));
+    return bits_f32(sign | ((ex + 112u) << 23) | (man << 13));
+}
+
+__host__ __device__ inline float bf16_exact(uint32_t b) { return bits_f32(b << 16); }
+
+// DecodeKScaleMin (Dequantizer.cs:506-521) over the 12 packed scale bytes.
+__host__ __device__ inline void kscale_min(const uint8_t* p, int g, int& sc, int& mn) {
+    if (g < 4) {
+        sc = p[g] & 0x3F;
+        mn = p[g + 4] & 0x3F;
+    } else {
+        int i = g - 4;
+        sc = (p[g + 4] & 0x0F) | ((p[i] >> 6) << 4);
+        mn = (p[g + 4] >> 4) | ((p[i + 4] >> 6) << 4);
+    }
+}
+
+}  // namespace fllm

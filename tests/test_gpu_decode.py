@@ -1,0 +1,295 @@
+"""GPU parity of the decode step (IForwardPass.Forward on the device) against the oracle.
+
+Bars (float32 accumulation): per-layer hidden states and logits within normwise relative error
+1e-3; greedy token sequences identical; KV cache contents within 1e-3; graph replay
+bit-identical to eager launches; error codes as the reference's exceptions.
+"""
+import numpy as np
+import pytest
+
+import dotnetfoundryllm_amd as F
+import dotnetfoundryllm_amd._native as N
+import oracle_bind as O
+from dotnetfoundryllm_amd.configs import CONFIGS, desc_of
+from fixtures import REF_TOKENS, reference_fixture, synthetic, upload
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def device_model(ctx, desc, tensors):
+    m = F.Model(ctx, desc)
+    upload(m, tensors)
+    return m
+
+
+@pytest.mark.parametrize("arch", [N.ARCH_LLAMA, N.ARCH_MISTRAL, N.ARCH_QWEN2, N.ARCH_GEMMA2])
+def test_reference_fixtures(ctx, arch):
+    desc, tensors = reference_fixture(arch)
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors)
+    try:
+        for tok, pos in REF_TOKENS:
+            fwd.forward(tok, pos, kv)
+            assert orc.forward(tok, pos) == 0
+            got, want = fwd.logits, orc.logits()
+            assert got.shape == (16,) and np.all(np.isfinite(got))
+            assert O.normwise_rel_err(got, want) <= TOL
+        assert kv.current_length == 3
+        for l in range(desc.n_layers):
+            assert O.normwise_rel_err(kv.get_keys(l), orc.kv(l, 0)) <= TOL
+            assert O.normwise_rel_err(kv.get_values(l), orc.kv(l, 1)) <= TOL
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
+
+
+SMALL = ["test-llama", "test-llama-straddle", "test-mistral", "test-qwen2", "test-gemma2", "test-mixed"]
+
+
+@pytest.mark.parametrize("name", SMALL)
+def test_small_models_hidden_logits_and_greedy(ctx, name):
+    cfg, desc, tensors = synthetic(name)
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    F.set_debug(kv, True)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors)
+    prompt = F.synth_tokens(cfg["seed"], 1, desc.vocab, 12)
+    worst = 0.0
+    try:
+        pos = 0
+        for t in prompt:
+            fwd.forward(int(t), pos, kv)
+            assert orc.forward(int(t), pos) == 0
+            for l in range(desc.n_layers + 1):
+                worst = max(worst, O.normwise_rel_err(fwd.hidden(l), orc.hidden(l)))
+            worst = max(worst, O.normwise_rel_err(fwd.logits, orc.logits()))
+            pos += 1
+        # greedy decode: identical tokens
+        nxt_d = nxt_o = int(prompt[-1])
+        for step in range(min(24, desc.max_ctx - pos)):
+            fwd.forward(nxt_d, pos, kv)
+            assert orc.forward(nxt_o, pos) == 0
+            lg = orc.logits()
+            worst = max(worst, O.normwise_rel_err(fwd.logits, lg))
+            nxt_d = fwd.sample_greedy()
+            nxt_o = int(O.lib.orc_argmax(O.fp(lg), lg.size))
+            assert nxt_d == nxt_o, f"step {step}"
+            pos += 1
+        print(f"{name}: worst normwise rel err {worst:.2e}")
+        assert worst <= TOL
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
+
+
+def test_tiny_llama_64_greedy_tokens(ctx):
+    """The tiny Llama Q4_K workload: 128-token prompt, then greedy decode; the first 64 tokens
+    equal the oracle's."""
+    cfg, desc, tensors = synthetic("tiny-llama-q4k")
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    orc = O.OracleModel(desc, tensors)
+    prompt = F.synth_tokens(cfg["seed"], 0, desc.vocab, 128)
+    lm = F.LlamaLanguageModel(m, kv)
+    sampler = F.SamplerPipeline(0.0)
+    try:
+        toks, stats = lm.generate(prompt, 64, sampler, stop_at_eos=False)
+        assert len(toks) == 64 and stats.completion_tokens == 64
+        pos = 0
+        for t in prompt[:-1]:
+            assert orc.forward(int(t), pos) == 0
+            pos += 1
+        nxt = int(prompt[-1])
+        ref = []
+        for _ in range(64):
+            assert orc.forward(nxt, pos) == 0
+            pos += 1
+            lg = orc.logits()
+            nxt = int(O.lib.orc_argmax(O.fp(lg), lg.size))
+            ref.append(nxt)
+        assert list(toks) == ref
+    finally:
+        sampler.close()
+        orc.close()
+        kv.close()
+        m.close()
+
+
+def test_graph_replay_matches_eager(ctx):
+    cfg, desc, tensors = synthetic("test-qwen2")
+    m = device_model(ctx, desc, tensors)
+    kv_g, kv_e = F.HipKvCache(m), F.HipKvCache(m)
+    F.set_graph(kv_e, False)
+    fg, fe = F.HipForwardPass(m), F.HipForwardPass(m)
+    try:
+        for pos, t in enumerate(F.synth_tokens(3, 3, desc.vocab, 20)):
+            fg.forward(int(t), pos, kv_g)
+            fe.forward(int(t), pos, kv_e)
+            assert np.array_equal(fg.logits, fe.logits)
+    finally:
+        kv_g.close()
+        kv_e.close()
+        m.close()
+
+
+def test_forward_error_contract(ctx):
+    cfg, desc, tensors = synthetic("test-llama")
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m, 4)
+    fwd = F.HipForwardPass(m)
+    try:
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.forward(desc.vocab, 0, kv)
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.forward(-1, 0, kv)
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.forward(3, 1, kv)  # position beyond the cached length
+        for p in range(4):
+            fwd.forward(3 + p, p, kv)
+        assert kv.current_length == 4 and kv.max_sequence_length == 4
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.forward(3, 4, kv)  # cache full
+        kv.clear()
+        assert kv.current_length == 0
+        fwd.forward(3, 0, kv)
+        assert np.all(np.isfinite(fwd.logits))
+        with pytest.raises(F.ArgumentNullException):
+            fwd.forward(3, 0, None)
+    finally:
+        kv.close()
+        m.close()
+
+
+def test_model_upload_contract(ctx):
+    cfg, desc, tensors = synthetic("test-llama")
+    m = F.Model(ctx, desc)
+    try:
+        entry, data = tensors["blk.0.attn_q.weight"]
+        with pytest.raises(F.ArgumentException):
+            m.upload(entry[1], 0, entry[3], data[:-1])
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            m.upload(entry[1], desc.n_layers, entry[3], data)
+        with pytest.raises(F.NotSupportedException):
+            m.upload(entry[1], 0, 3, data)
+        with pytest.raises(F.InvalidOperationException):
+            m.finalize()  # required tensors missing
+    finally:
+        m.close()
+    bad = N.ModelDesc.from_buffer_copy(desc)
+    bad.n_kv_heads = 3
+    with pytest.raises(F.ArgumentOutOfRangeException):
+        F.Model(ctx, bad)
+
+
+def test_device_sampling_matches_oracle(ctx):
+    cfg, desc, tensors = synthetic("test-llama")
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    fwd.forward(1, 0, kv)
+    rng = np.random.default_rng(5)
+    try:
+        for i in range(40):
+            lg = (rng.standard_normal(desc.vocab) * 3).astype(np.float32)
+            if i % 2:
+                lg = np.round(lg, 1)  # ties
+            if i == 7:
+                lg[[3, 9]] = lg.max() + 1  # tie at the maximum: first index wins
+            fwd.write_logits(lg)
+            assert fwd.sample_greedy() == int(O.lib.orc_argmax(O.fp(lg), lg.size))
+            for inv, k in ((1.0, 40), (1.25, 40), (2.0, 1), (0.5, 7)):
+                fwd.write_logits(lg)
+                ids, vals = fwd.sample_topk(inv, k, cap=desc.vocab)
+                scaled = lg * np.float32(inv) if inv != 1.0 else lg.copy()
+                ref = scaled.copy()
+                O.lib.orc_apply_topk(O.fp(ref), ref.size, k)
+                keep = np.nonzero(ref != -np.inf)[0]
+                assert np.array_equal(ids, keep)
+                assert np.array_equal(vals, scaled[keep])
+        # the whole pipeline on device candidates draws the same tokens as the oracle
+        for temp, k in ((0.8, 40), (1.0, 5), (0.0, 0)):
+            sp = F.SamplerPipeline(temp, k, 1.0, 1234)
+            r = O.Xoshiro(1234)
+            for j in range(50):
+                lg = np.round(rng.standard_normal(desc.vocab) * 2, 2).astype(np.float32)
+                fwd.write_logits(lg)
+                assert sp.sample(kv) == O.sampler_pipeline(lg, temp, k, r)
+            sp.close()
+    finally:
+        kv.close()
+        m.close()
+
+
+@pytest.mark.parametrize("name", ["test-llama", "test-qwen2", "test-gemma2", "test-mistral"])
+def test_gguf_load_path(ctx, tmp_path, name):
+    from dotnetfoundryllm_amd.gguf import write_synthetic_gguf
+    cfg = CONFIGS[name]
+    path = str(tmp_path / f"{name}.gguf")
+    write_synthetic_gguf(path, cfg)
+    m1, info = F.GgufModelLoader.load(ctx, path)
+    _, desc, tensors = synthetic(name)
+    m2 = device_model(ctx, desc, tensors)
+    prompt = F.synth_tokens(cfg["seed"], 2, desc.vocab, 10)
+    outs = []
+    try:
+        for m in (m1, m2):
+            kv = F.HipKvCache(m)
+            sp = F.SamplerPipeline(0.0)
+            toks, st = F.LlamaLanguageModel(m, kv).generate(prompt, 16, sp, stop_at_eos=False)
+            outs.append(list(toks))
+            sp.close()
+            kv.close()
+        assert outs[0] == outs[1]
+    finally:
+        m1.close()
+        m2.close()
+
+
+def test_llama3_8b_shape_two_layers(ctx):
+    """Full Llama-3-8B shapes (dim 4096, 32/8 heads x 128, FFN 14336, vocab 128256, Q4_K + Q6_K),
+    two decoder layers: logits and greedy tokens against the oracle."""
+    cfg, desc, tensors = synthetic("llama3-8b-q4km", n_layers=2)
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m, 64)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors, 64)
+    try:
+        nxt_d = nxt_o = 1234
+        for pos in range(4):
+            fwd.forward(nxt_d, pos, kv)
+            assert orc.forward(nxt_o, pos) == 0
+            lg = orc.logits()
+            err = O.normwise_rel_err(fwd.logits, lg)
+            print(f"pos {pos}: normwise rel err {err:.2e}")
+            assert err <= TOL
+            nxt_d = fwd.sample_greedy()
+            nxt_o = int(O.lib.orc_argmax(O.fp(lg), lg.size))
+            assert nxt_d == nxt_o
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
+
+
+def test_profile_mode_reports_kernels(ctx):
+    cfg, desc, tensors = synthetic("test-llama")
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    F.set_profile(kv, True)
+    fwd = F.HipForwardPass(m)
+    try:
+        for p in range(3):
+            fwd.forward(5, p, kv)
+        ents = {e["name"]: e for e in F.profile_entries(kv)}
+        assert ents["gemv_q4_k"]["launches"] == 3 * (desc.n_layers * 5)
+        assert ents["gemv_q6_k"]["launches"] == 3 * (desc.n_layers * 2 + 1)
+        assert all(e["ms"] > 0 for e in ents.values())
+    finally:
+        kv.close()
+        m.close()

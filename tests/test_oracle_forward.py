@@ -1,0 +1,213 @@
+"""Pins the oracle's forward passes (CPU only).
+
+  - the reference's own fixtures (Qwen2/Mistral/Gemma2ForwardPassTests.cs): three Forward calls
+    give finite logits of vocabulary length;
+  - brute force: an independent float64 numpy restatement of the four forward passes on tiny
+    models agrees with the oracle to float32 accuracy (pins indexing of heads, GQA groups,
+    RoPE pairs, window start, bias/post-norm/softcap placement);
+  - invariants: duplicating K/V heads (GQA group of 2 -> MHA) leaves the logits bit-identical;
+    a window >= context equals no window; with window 1 on a one-layer model the last logits do
+    not depend on the earlier tokens, while an unwindowed second Gemma2 layer makes them depend;
+  - KvCache semantics: length counts positions, evicted/over-capacity and out-of-range calls fail.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import dotnetfoundryllm_amd._native as N
+import oracle_bind as O
+from fixtures import REF_TOKENS, f32_of, reference_fixture, synthetic
+
+ARCHS = [N.ARCH_LLAMA, N.ARCH_MISTRAL, N.ARCH_QWEN2, N.ARCH_GEMMA2]
+
+
+def ref_forward_f64(desc, tensors, tokens):
+    """Float64 restatement of the forward pass for a token sequence; returns per-step logits."""
+    d = desc
+    H, hd, nh, nkv = d.hidden, d.head_dim, d.n_heads, d.n_kv_heads
+    gemma = d.arch == N.ARCH_GEMMA2
+    W = {k: f32_of(tensors, k).astype(np.float64) for k in tensors}
+
+    def mat(name, rows):
+        return W[name].reshape(rows, -1)
+
+    def norm(x, w):
+        if gemma:
+            return x / np.sqrt(np.mean(x * x) + 1e-6) * (1 + w)
+        return x / np.sqrt(np.mean(x * x) + d.norm_eps) * w
+
+    inv = 1.0 / np.power(np.float64(d.rope_base), 2.0 * np.arange(hd // 2) / hd)
+
+    def rope(v, pos):
+        v = v.reshape(-1, hd).copy()
+        th = pos * inv
+        c, s = np.cos(th), np.sin(th)
+        x0, x1 = v[:, 0::2].copy(), v[:, 1::2].copy()
+        v[:, 0::2] = x0 * c - x1 * s
+        v[:, 1::2] = x0 * s + x1 * c
+        return v.reshape(-1)
+
+    K = [[] for _ in range(d.n_layers)]
+    Vc = [[] for _ in range(d.n_layers)]
+    out = []
+    for tok, pos in tokens:
+        x = W["token_embd.weight"].reshape(d.vocab, H)[tok].copy()
+        for l in range(d.n_layers):
+            b = f"blk.{l}."
+            xn = norm(x, W[b + "attn_norm.weight"])
+            q = mat(b + "attn_q.weight", nh * hd) @ xn
+            k = mat(b + "attn_k.weight", nkv * hd) @ xn
+            v = mat(b + "attn_v.weight", nkv * hd) @ xn
+            if d.arch == N.ARCH_QWEN2:
+                q, k, v = q + W[b + "attn_q.bias"], k + W[b + "attn_k.bias"], v + W[b + "attn_v.bias"]
+            sp = pos / d.rope_scale if (d.rope_scaled and d.rope_scale > 0) else pos
+            q, k = rope(q, sp), rope(k, sp)
+            K[l].append(k)
+            Vc[l].append(v)
+            window = 0x7FFFFFFF
+            if d.arch == N.ARCH_MISTRAL or (gemma and l % 2 == 0):
+                window = d.sliding_window
+            seq = pos + 1
+            ws = max(0, seq - window)
+            scale = d.attn_scale if gemma else 1.0 / math.sqrt(hd)
+            att = np.zeros(nh * hd)
+            for hh in range(nh):
+                kh = hh // (nh // nkv)
+                qh = q[hh * hd:(hh + 1) * hd]
+                sc = np.array([qh @ K[l][t][kh * hd:(kh + 1) * hd] for t in range(ws, seq)]) * scale
+                if gemma and d.attn_softcap > 0:
+                    sc = d.attn_softcap * np.tanh(sc / d.attn_softcap)
+                p = np.exp(sc - sc.max())
+                p /= p.sum()
+                att[hh * hd:(hh + 1) * hd] = sum(p[i] * Vc[l][t][kh * hd:(kh + 1) * hd] for i, t in enumerate(range(ws, seq)))
+            o = mat(b + "attn_output.weight", H) @ att
+            if gemma:
+                o = norm(o, W[b + "post_attn_norm.weight"])
+            x = x + o
+            xn = norm(x, W[b + "ffn_norm.weight"])
+            g = mat(b + "ffn_gate.weight", d.ffn) @ xn
+            u = mat(b + "ffn_up.weight", d.ffn) @ xn
+            if gemma:
+                a = 0.5 * g * (1 + np.tanh(0.7978845608 * (g + 0.044715 * g ** 3)))
+            else:
+                a = g / (1 + np.exp(-g))
+            f = mat(b + "ffn_down.weight", H) @ (a * u)
+            if gemma:
+                f = norm(f, W[b + "post_ffn_norm.weight"])
+            x = x + f
+        xn = norm(x, W["output_norm.weight"])
+        head = "output.weight" if "output.weight" in W else "token_embd.weight"
+        lg = mat(head, d.vocab) @ xn
+        if gemma and d.final_softcap > 0:
+            lg = d.final_softcap * np.tanh(lg / d.final_softcap)
+        out.append(lg)
+    return out
+
+
+def run_oracle(desc, tensors, tokens, max_seq=0):
+    m = O.OracleModel(desc, tensors, max_seq)
+    try:
+        res = []
+        for tok, pos in tokens:
+            assert m.forward(tok, pos) == 0
+            res.append(m.logits())
+        return res
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("arch", ARCHS)
+def test_reference_fixture_finite_and_brute_force(arch):
+    desc, tensors = reference_fixture(arch)
+    got = run_oracle(desc, tensors, REF_TOKENS)
+    assert got[-1].shape == (16,) and np.all(np.isfinite(got[-1]))
+    want = ref_forward_f64(desc, tensors, REF_TOKENS)
+    for g, w in zip(got, want):
+        assert O.normwise_rel_err(g, w) < 1e-5
+
+
+@pytest.mark.parametrize("name", ["test-llama", "test-llama-straddle", "test-mistral", "test-qwen2", "test-gemma2",
+                                  "test-mixed"])
+def test_synthetic_models_brute_force(name):
+    cfg, desc, tensors = synthetic(name)
+    toks = [(t, i) for i, t in enumerate([3, 17, 200, 5, 99, 400, 1, 7, 250, 31])]
+    got = run_oracle(desc, tensors, toks)
+    want = ref_forward_f64(desc, tensors, toks)
+    for g, w in zip(got, want):
+        assert O.normwise_rel_err(g, w) < 2e-5
+
+
+def test_gqa_duplication_invariance():
+    cfg, desc, tensors = synthetic("test-mixed")
+    toks = [(t, i) for i, t in enumerate([3, 17, 200, 5, 99])]
+    base = run_oracle(desc, tensors, toks)
+    # MHA model whose K/V heads repeat each GQA head for its query group
+    d2 = N.ModelDesc.from_buffer_copy(desc)
+    d2.n_kv_heads = desc.n_heads
+    group = desc.n_heads // desc.n_kv_heads
+    t2 = dict(tensors)
+    hd, H = desc.head_dim, desc.hidden
+    for l in range(desc.n_layers):
+        for nm, slot in (("attn_k.weight", N.SLOT_ATTN_K), ("attn_v.weight", N.SLOT_ATTN_V)):
+            name = f"blk.{l}.{nm}"
+            w = f32_of(tensors, name).reshape(desc.n_kv_heads, hd, H)
+            w2 = np.repeat(w, group, axis=0).reshape(-1).astype(np.float32)
+            entry = (name, slot, l, N.F32, d2.n_kv_heads * hd, H, (1, 0, 0), 0)
+            t2[name] = (entry, w2.view(np.uint8))
+    dup = run_oracle(d2, t2, toks)
+    for a, b in zip(base, dup):
+        assert np.array_equal(a, b)
+
+
+def test_window_semantics():
+    cfg, desc, tensors = synthetic("test-mistral")
+    toks = [(t, i) for i, t in enumerate([3, 17, 200, 5, 99, 400])]
+    big = N.ModelDesc.from_buffer_copy(desc)
+    big.sliding_window = 1000
+    llama = N.ModelDesc.from_buffer_copy(desc)
+    llama.arch = N.ARCH_LLAMA
+    a = run_oracle(big, tensors, toks)
+    b = run_oracle(llama, tensors, toks)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    # window 1, one layer: history-independent
+    cfg1, d1, t1 = synthetic("test-mistral", n_layers=1)
+    d1.sliding_window = 1
+    s1 = run_oracle(d1, t1, [(3, 0), (17, 1), (42, 2)])
+    s2 = run_oracle(d1, t1, [(9, 0), (250, 1), (42, 2)])
+    assert np.array_equal(s1[-1], s2[-1])
+    d1.sliding_window = 2
+    s3 = run_oracle(d1, t1, [(3, 0), (17, 1), (42, 2)])
+    s4 = run_oracle(d1, t1, [(9, 0), (250, 1), (42, 2)])
+    assert not np.array_equal(s3[-1], s4[-1])
+
+
+def test_gemma2_window_only_on_even_layers():
+    cfg, d, t = synthetic("test-gemma2", n_layers=1)
+    d.sliding_window = 1
+    a = run_oracle(d, t, [(3, 0), (17, 1), (42, 2)])
+    b = run_oracle(d, t, [(9, 0), (250, 1), (42, 2)])
+    assert np.array_equal(a[-1], b[-1])
+    cfg, d2, t2 = synthetic("test-gemma2", n_layers=2)
+    d2.sliding_window = 1
+    a = run_oracle(d2, t2, [(3, 0), (17, 1), (42, 2)])
+    b = run_oracle(d2, t2, [(9, 0), (250, 1), (42, 2)])
+    assert not np.array_equal(a[-1], b[-1])
+
+
+def test_kv_cache_semantics_and_errors():
+    cfg, desc, tensors = synthetic("test-llama")
+    m = O.OracleModel(desc, tensors, max_seq=4)
+    try:
+        assert m.forward(desc.vocab, 0) == -1          # token id out of range
+        for p in range(4):
+            assert m.forward(5 + p, p) == 0
+        assert O.lib.orc_fwd_length(m.f) == 4
+        assert m.kv(0, 0).size == 4 * desc.n_kv_heads * desc.head_dim
+        assert m.forward(9, 4) == -1                   # evict-half then Slice past the cache fails
+        m.reset()
+        assert O.lib.orc_fwd_length(m.f) == 0
+        assert m.forward(5, 1) == -1                   # position beyond the cached length
+    finally:
+        m.close()

@@ -1,0 +1,198 @@
+"""Pins the oracle's tensor operations, sampling and RNG (CPU only).
+
+Reference tests restated: TensorOperationsTests.cs:9-107, GreedySamplerTests.cs,
+TopKSamplerTests.cs:45-71, SamplerPipelineTests.cs:24-70. Beyond those: closed forms
+(RoPE at position 0 is the identity and preserves pair norms; softcap(x) -> x for |x| << cap;
+GELU/SiLU fixed points), float64 brute force for Dot/LinearProjection, numpy's order
+statistic for the top-k threshold, and the published xoshiro256** algorithm (restated with
+Python integers) for the RNG.
+"""
+import math
+
+import numpy as np
+
+import oracle_bind as O
+
+fp = O.fp
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def test_dot_and_linear_against_float64():
+    assert O.lib.orc_dot(fp(f32([1, 2, 3])), fp(f32([4, 5, 6])), 3) == 32.0  # TensorOperationsTests Dot
+    rng = np.random.default_rng(0)
+    for n in (1, 7, 8, 9, 64, 1000, 4097):
+        a, b = f32(rng.standard_normal(n)), f32(rng.standard_normal(n))
+        exact = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+        got = O.lib.orc_dot(fp(a), fp(b), n)
+        bound = n * 2 ** -23 * float(np.dot(np.abs(a), np.abs(b))) + 1e-30
+        assert abs(got - exact) <= bound
+    W = f32(rng.standard_normal((37, 300)))
+    x = f32(rng.standard_normal(300))
+    y = O.linear(W, x)
+    assert np.allclose(y, W.astype(np.float64) @ x.astype(np.float64), rtol=1e-5, atol=1e-4)
+
+
+def test_rmsnorm_and_gemma_norm():
+    x = f32([1, 2, 3, 4])
+    w = f32([1, 1, 1, 1])
+    dst = np.zeros(4, dtype=np.float32)
+    O.lib.orc_rmsnorm(fp(x), fp(w), fp(dst), 4, 1e-5)
+    assert abs(math.sqrt(float(np.mean(dst.astype(np.float64) ** 2))) - 1.0) < 0.01  # TensorOperationsTests
+    rng = np.random.default_rng(1)
+    x = f32(rng.standard_normal(256) * 3)
+    w = f32(rng.standard_normal(256))
+    O.lib.orc_rmsnorm(fp(x), fp(w), fp(dst := np.zeros(256, np.float32)), 256, 1e-5)
+    ref = x / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5) * w
+    assert np.allclose(dst, ref, rtol=1e-5, atol=1e-6)
+    g = np.zeros(256, np.float32)
+    O.lib.orc_gemma_rmsnorm(fp(x), fp(w), fp(g), 256)
+    refg = x / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * (1.0 + w)
+    assert np.allclose(g, refg, rtol=1e-5, atol=1e-6)
+    # Gemma norm applied in place (Gemma2ForwardPass.cs:90 passes the same span twice)
+    xi = x.copy()
+    O.lib.orc_gemma_rmsnorm(fp(xi), fp(w), fp(xi), 256)
+    assert np.array_equal(xi, g)
+
+
+def test_activations_and_softcap():
+    x = f32([100.0])
+    O.lib.orc_silu(fp(x), 1)
+    assert x[0] > 99.0  # TensorOperationsTests Silu
+    z = f32([0.0, -0.0])
+    O.lib.orc_silu(fp(z), 2)
+    assert np.all(z == 0)
+    v = f32(np.linspace(-6, 6, 101))
+    s = v.copy()
+    O.lib.orc_silu(fp(s), s.size)
+    assert np.allclose(s, v / (1 + np.exp(-v.astype(np.float64))), rtol=1e-6, atol=1e-7)
+    g = v.copy()
+    O.lib.orc_gelu(fp(g), g.size)
+    vv = v.astype(np.float64)
+    assert np.allclose(g, 0.5 * vv * (1 + np.tanh(0.7978845608 * (vv + 0.044715 * vv ** 3))), rtol=1e-6, atol=1e-7)
+    c = f32([1e-3, -2e-3, 1000.0, -1000.0])
+    O.lib.orc_softcap(fp(c), 4, 30.0)
+    assert abs(c[0] - 1e-3) < 1e-9 and abs(c[1] + 2e-3) < 1e-9 and abs(c[2] - 30) < 1e-5 and abs(c[3] + 30) < 1e-5
+
+
+def test_softmax():
+    x = f32([1, 2, 3, 4])
+    O.lib.orc_softmax(fp(x), 4)
+    assert abs(float(x.sum()) - 1.0) < 1e-5  # TensorOperationsTests Softmax_SumsToOne
+    y = f32([1, 2, 10, 3])
+    O.lib.orc_softmax(fp(y), 4)
+    assert y[2] == y.max()
+    z = f32([-np.inf, 1.0, -np.inf, 1.0])
+    O.lib.orc_softmax(fp(z), 4)
+    assert list(z) == [0.0, 0.5, 0.0, 0.5]
+
+
+def test_rope_closed_forms():
+    inv = np.zeros(2, dtype=np.float32)
+    O.lib.orc_rope_inv_freqs(10000.0, 4, fp(inv))
+    assert inv[0] == 1.0 and abs(inv[1] - 0.01) < 1e-9  # 1/10000^(2/4)
+    x = f32([1, 0, 1, 0])
+    O.lib.orc_apply_rope(fp(x), 1.0, fp(inv), 2)
+    assert not np.array_equal(x, f32([1, 0, 1, 0]))  # TensorOperationsTests ApplyRope_ChangesVector
+    rng = np.random.default_rng(2)
+    hd = 128
+    inv = np.zeros(hd // 2, dtype=np.float32)
+    O.lib.orc_rope_inv_freqs(500000.0, hd, fp(inv))
+    v = f32(rng.standard_normal(hd))
+    r0 = v.copy()
+    O.lib.orc_apply_rope(fp(r0), 0.0, fp(inv), hd // 2)
+    assert np.array_equal(r0, v)  # identity at position 0
+    r = v.copy()
+    O.lib.orc_apply_rope(fp(r), 37.0, fp(inv), hd // 2)
+    pn = np.hypot(v[0::2].astype(np.float64), v[1::2])
+    assert np.allclose(np.hypot(r[0::2].astype(np.float64), r[1::2]), pn, rtol=1e-6)
+    # interleaved pairs: the first pair rotates by exactly 37 rad
+    ang = math.atan2(r[1], r[0]) - math.atan2(v[1], v[0])
+    assert abs(math.remainder(ang - 37.0, 2 * math.pi)) < 1e-5
+
+
+def test_argmax_semantics():
+    for logits, want in [([1, 5, 3], 1), ([9, 1, 1], 0), ([1, 1, 9], 2), ([7.0], 0), ([2, 5, 5, 1], 1),
+                         ([-0.0, 0.0], 1), ([1, np.nan, 5, np.nan], 1)]:
+        a = f32(logits)
+        assert O.lib.orc_argmax(fp(a), a.size) == want
+
+
+def test_topk_threshold_matches_order_statistic():
+    a = f32([1, 5, 0.5, 3])
+    O.lib.orc_apply_topk(fp(a), 4, 2)  # TopKSamplerTests: keeps indices 1 and 3
+    assert a[0] == -np.inf and a[2] == -np.inf and a[1] == 5 and a[3] == 3
+    b = f32([1, 2, 3])
+    O.lib.orc_apply_topk(fp(b), 3, 10)
+    assert list(b) == [1, 2, 3]
+    rng = np.random.default_rng(3)
+    for n, k in [(100, 1), (1000, 40), (5000, 40), (152064, 40), (64, 64 - 1)]:
+        x = f32(np.round(rng.standard_normal(n) * 4, 1))  # many ties
+        th = O.lib.orc_topk_threshold(fp(x), n, k)
+        assert th == np.sort(x)[::-1][k - 1]
+
+
+def py_xoshiro(seed, count):
+    M = (1 << 64) - 1
+
+    def sm(x):
+        x = (x + 0x9E3779B97F4A7C15) & M
+        z = x
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return x, z ^ (z >> 31)
+
+    s = []
+    x = seed
+    for _ in range(4):
+        x, v = sm(x)
+        s.append(v)
+
+    def rotl(v, k):
+        return ((v << k) | (v >> (64 - k))) & M
+
+    out = []
+    for _ in range(count):
+        r = (rotl((s[1] * 5) & M, 7) * 9) & M
+        t = (s[1] << 17) & M
+        s[2] ^= s[0]
+        s[3] ^= s[1]
+        s[1] ^= s[2]
+        s[0] ^= s[3]
+        s[2] ^= t
+        s[3] = rotl(s[3], 45)
+        out.append(r)
+    return out
+
+
+def test_xoshiro_published_algorithm():
+    for seed in (1, 7, 42, 123, 0xDEADBEEF):
+        r = O.Xoshiro(seed)
+        want = py_xoshiro(seed, 50)
+        assert [r.next() for _ in range(50)] == want
+        r = O.Xoshiro(seed)
+        for w in want[:20]:
+            assert r.next_float() == np.float32((w >> 11) * (1.0 / (1 << 53)))
+
+
+def test_sampler_pipeline_reference_cases():
+    rng = O.Xoshiro(5)
+    assert O.sampler_pipeline(f32([0.1, 5.0, 3.0]), 0.0, 0, rng) == 1  # temperature 0 -> argmax
+    for _ in range(20):
+        assert O.sampler_pipeline(f32([1, 10, 0.5, 3]), 1.0, 1, rng) == 1  # top-k 1 -> argmax
+    a, b = O.Xoshiro(123), O.Xoshiro(123)
+    logits = [0.5, 0.3, 0.9, 0.1]
+    assert [O.sampler_pipeline(f32(logits), 1.0, 0, a) for _ in range(50)] == \
+           [O.sampler_pipeline(f32(logits), 1.0, 0, b) for _ in range(50)]
+    # the draw frequencies follow softmax(logits / T) restricted to the top k
+    r = O.Xoshiro(9)
+    lg = f32([2.0, 1.0, 0.5, 3.0, -1.0])
+    counts = np.zeros(5)
+    for _ in range(20000):
+        counts[O.sampler_pipeline(lg, 0.8, 3, r)] += 1
+    p = np.exp(lg.astype(np.float64) / 0.8)
+    p[[2, 4]] = 0
+    p /= p.sum()
+    assert np.allclose(counts / counts.sum(), p, atol=0.015)
