@@ -809,11 +809,13 @@ static hipError_t enqueue_body(fllm_seq* s) {
              launch_attention(s->q, kc, vc, d.n_heads, d.n_kv_heads, d.head_dim, window, d.attn_scale,
                               gemma ? d.attn_softcap : 0.0f, s->nsplit, s->part_o, s->part_ml, s->att, s->xq_att,
                               s->params, s->st));
+        // the attention combine writes the quantized copy only when head_dim is a multiple of 32
+        XQ att_q = (d.head_dim % 32 == 0) ? s->xq_att : XQ{nullptr, nullptr};
         if (gemma) {
-            if ((e = gemv_step(s, L.o, s->att, s->xq_att, s->tmp, nullptr)) != hipSuccess) return e;
+            if ((e = gemv_step(s, L.o, s->att, att_q, s->tmp, nullptr)) != hipSuccess) return e;
             STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));
         } else {
-            if ((e = gemv_step(s, L.o, s->att, s->xq_att, s->x, s->x)) != hipSuccess) return e;
+            if ((e = gemv_step(s, L.o, s->att, att_q, s->x, s->x)) != hipSuccess) return e;
         }
         STEP("rmsnorm", 12.0 * H, launch_rmsnorm_q(s->x, L.ffn_norm, H, eps, nk, s->xn, s->xq_hidden, s->st));
         if ((e = gemv_step(s, L.gate, s->xn, s->xq_hidden, s->g, nullptr)) != hipSuccess) return e;

@@ -479,9 +479,11 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
 hipError_t launch_gemv(const WMat& m, const float* xf, const XQ& xq, float* y, const float* residual,
                        hipStream_t st) {
     int t = m.type;
+    // the int8 path holds one 32-element group column per lane and at most 16 waves per
+    // workgroup, so it covers rows of up to 1024 groups (32768 elements)
     bool qpath = (t == FLLM_TYPE_Q4_K || t == FLLM_TYPE_Q5_K || t == FLLM_TYPE_Q6_K || t == FLLM_TYPE_Q8_0 ||
                   t == FLLM_TYPE_Q4_0) &&
-                 (m.cols % 32 == 0) && xq.parts != nullptr;
+                 (m.cols % 32 == 0) && m.cols <= 32768 && xq.parts != nullptr;
     if (qpath) {
         int G = (int)(m.cols / 32);
         int nslice = (G + 63) / 64;
