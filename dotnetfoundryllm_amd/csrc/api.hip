@@ -413,7 +413,7 @@ extern "C" int32_t fllm_model_destroy(fllm_model* m) {
     return FLLM_OK;
 }
 
-// Expected (rows, cols) of a slot, as LoadTensor's expectedElements (GgufModelLoader.cs:326-354).
+// Expected (rows, cols) of a slot, as LoadTensor's expectedElements (GgufModelLoader.cs:338-366).
 static bool slot_shape(const fllm_model* m, int slot, int64_t& rows, int64_t& cols, bool& vec) {
     const fllm_model_desc& d = m->d;
     vec = false;
@@ -532,7 +532,7 @@ extern "C" int32_t fllm_model_finalize(fllm_model* m) {
         for (auto& r : req)
             if (!r.ok) return fail(FLLM_E_INVALID_OP, "Required tensor 'blk.%d.%s' not found in GGUF file.", l, r.name);
     }
-    if (!m->output.present()) {  // GgufModelLoader.cs:353-354: tied LM head
+    if (!m->output.present()) {  // GgufModelLoader.cs:365-366: tied LM head
         m->output = m->tok_embd;
         m->output_tied = true;
     }

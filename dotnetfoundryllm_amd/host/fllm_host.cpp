@@ -376,7 +376,7 @@ static int32_t open_gguf(const char* path, GFile& g) {
     return FLLM_OK;
 }
 
-// Metadata helpers with GgufModelLoader's defaults (GgufModelLoader.cs:424-466).
+// Metadata helpers with GgufModelLoader's defaults (GgufModelLoader.cs:436-478).
 static std::string get_str(const GFile& g, const std::string& k, const std::string& def) {
     auto it = g.meta.find(k);
     return (it != g.meta.end() && it->second.type == STR) ? it->second.s : def;
@@ -404,7 +404,7 @@ static bool ieq(const std::string& a, const char* b) {
     return true;
 }
 
-// GgufModelLoader.Build -> BuildConfig / BuildGemma2 (GgufModelLoader.cs:80-89, :198-229, :296-322).
+// GgufModelLoader.Build -> BuildConfig / BuildGemma2 (GgufModelLoader.cs:89-102, :213-241, :296-322).
 static int32_t build_desc(const GFile& g, fllmh_model_info* info) {
     fllm_model_desc d{};
     std::string arch = get_str(g, "general.architecture", "llama");

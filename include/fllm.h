@@ -7,7 +7,7 @@
  *   IKvCache      (src/DotNetFoundryLLM.Abstractions/Interfaces.cs:73-92)
  *   ISampler      (src/DotNetFoundryLLM.Abstractions/Interfaces.cs:66-70)
  * and the loader seam GgufModelLoader.LoadTensor
- *   (src/DotNetFoundryLLM.ModelFormats.Gguf/GgufModelLoader.cs:397-406).
+ *   (src/DotNetFoundryLLM.ModelFormats.Gguf/GgufModelLoader.cs:409-418).
  * A C# HipForwardPass : IForwardPass / HipKvCache : IKvCache binds the functions
  * below with [LibraryImport]; every signature uses plain pointers, sizes and
  * POD structs so that it is blittable.
@@ -63,7 +63,7 @@ enum fllm_type {
     FLLM_TYPE_BF16 = 30
 };
 
-/* Architectures accepted by GgufModelLoader.Build (GgufModelLoader.cs:80-89). */
+/* Architectures accepted by GgufModelLoader.Build (GgufModelLoader.cs:89-102). */
 enum fllm_arch {
     FLLM_ARCH_LLAMA   = 0,   /* LlamaForwardPass.cs */
     FLLM_ARCH_MISTRAL = 1,   /* MistralForwardPass.cs: window on every layer */
@@ -72,7 +72,7 @@ enum fllm_arch {
 };
 
 /* Tensor slots, named after the GGUF tensor names the loader reads
- * (GgufModelLoader.cs:324-360 LoadWeights, :506-540 LoadGemma2Weights, :542-579 LoadQwen2Weights). */
+ * (GgufModelLoader.cs:336-372 LoadWeights, :518-552 LoadGemma2Weights, :554-591 LoadQwen2Weights). */
 enum fllm_slot {
     FLLM_SLOT_TOKEN_EMBD     = 0,   /* token_embd.weight              [vocab x hidden] */
     FLLM_SLOT_OUTPUT_NORM    = 1,   /* output_norm.weight             [hidden] */
@@ -95,8 +95,8 @@ enum fllm_slot {
 
 /* Model description: the fields of LlamaConfig (LlamaConfig.cs:6-65), MistralConfig
  * (MistralConfig.cs) and Gemma2Config (Gemma2Config.cs:6-72) that the forward pass reads.
- * The C# side fills it from the config object the loader built (GgufModelLoader.cs:296-322,
- * :198-229), so every quirk of that mapping (eps not read from GGUF, raw
+ * The C# side fills it from the config object the loader built (GgufModelLoader.cs:308-334,
+ * :213-241), so every quirk of that mapping (eps not read from GGUF, raw
  * query_pre_attn_scalar, head_dim override) stays on the managed side. */
 typedef struct fllm_model_desc {
     int32_t arch;              /* enum fllm_arch */
@@ -138,7 +138,7 @@ FLLM_API int32_t fllm_ctx_device_info(fllm_ctx* ctx, int32_t* n_cu, int64_t* hbm
 FLLM_API int32_t fllm_model_create(fllm_ctx* ctx, const fllm_model_desc* desc, fllm_model** out);
 /* Copies raw GGUF tensor bytes (GgufFile.GetTensorBytes, GgufFile.cs:76-97) to device memory,
  * kept in their quantized block layout. The element count is implied by the slot and the
- * config, as LoadTensor's expectedElements (GgufModelLoader.cs:397-406); nbytes must be the
+ * config, as LoadTensor's expectedElements (GgufModelLoader.cs:409-418); nbytes must be the
  * exact byte size of that many elements of `type`. Returns after the copy, so the caller may
  * reuse `bytes` (the mmap path reuses one scratch array, GgufFile.cs:94-96).
  * layer is ignored for the model-level slots. Norm and bias tensors of any supported type
@@ -146,7 +146,7 @@ FLLM_API int32_t fllm_model_create(fllm_ctx* ctx, const fllm_model_desc* desc, f
 FLLM_API int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer, int32_t type,
                                    const void* bytes, uint64_t nbytes);
 /* Checks that every required slot is present; ties output.weight to token_embd.weight when
- * absent (GgufModelLoader.cs:353-354); builds the RoPE inverse-frequency table. */
+ * absent (GgufModelLoader.cs:365-366); builds the RoPE inverse-frequency table. */
 FLLM_API int32_t fllm_model_finalize(fllm_model* m);
 FLLM_API int32_t fllm_model_destroy(fllm_model* m);
 /* The description the model was created with. */

@@ -480,7 +480,7 @@ void orc_model_destroy(orc_model* m) {
     free(m);
 }
 
-/* LoadTensor (GgufModelLoader.cs:397-406): new float[expected]; Dequantize(type, raw, dst). */
+/* LoadTensor (GgufModelLoader.cs:409-418): new float[expected]; Dequantize(type, raw, dst). */
 int orc_model_set(orc_model* m, int slot, int layer, int type, const uint8_t* bytes, int64_t nbytes) {
     int64_t n = slot_elems(m, slot);
     if (n < 0) return ORC_E_RANGE;
@@ -503,7 +503,7 @@ int orc_model_set(orc_model* m, int slot, int layer, int type, const uint8_t* by
 
 int orc_model_finalize(orc_model* m) {
     if (!m->tok_embd || !m->out_norm) return ORC_E_INVALID;
-    if (!m->output) { m->output = m->tok_embd; m->output_tied = 1; } /* GgufModelLoader.cs:353-354 */
+    if (!m->output) { m->output = m->tok_embd; m->output_tied = 1; } /* GgufModelLoader.cs:365-366 */
     int need[] = {S_ATTN_NORM, S_Q, S_K, S_V, S_O, S_FFN_NORM, S_GATE, S_UP, S_DOWN};
     for (int l = 0; l < m->d.n_layers; l++) {
         for (unsigned i = 0; i < sizeof(need) / sizeof(need[0]); i++)
