@@ -3,7 +3,10 @@
 Workload: random-init weights of the Llama-3-8B shape (dim 4096, 32 layers, 32/8 heads x 128,
 FFN 14336, vocab 128256; Q4_K for q/k/o/gate/up, Q6_K for v/down/output) generated from a
 seed, a 512-token random prompt prefilled token by token, then greedy decode at batch 1.
-A "step" is one decode token: forward pass + device argmax + the 4-byte token read-back.
+A "step" is one decode token: the forward pass and the greedy argmax. The timed steps run as a
+device-side loop (each step's argmax is the next step's input token on the device, one graph
+launch per step, the tokens are read back after the last step); the same tokens come out of the
+host loop (forward + argmax + 4-byte read-back per token), whose rate is reported beside it.
 
 Prints one JSON line with the decode throughput, a roofline entry for the dominant kernel
 (algorithmic bytes per launch / mean launch time from HIP events in a profiled pass of the
@@ -85,6 +88,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--config", default="llama3-8b-q4km")
     ap.add_argument("--profile-steps", type=int, default=8)
+    ap.add_argument("--host-steps", type=int, default=32, help="steps of the host-driven loop timed after the device loop")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     args = ap.parse_args()
@@ -105,7 +109,7 @@ def main():
     t = time.time()
     model, _ = build_model(ctx, cfg)
     log(f"weights generated and uploaded in {time.time() - t:.1f} s")
-    max_seq = min(cfg["max_ctx"], args.prompt + args.warmup + args.steps + args.profile_steps + 8)
+    max_seq = min(cfg["max_ctx"], args.prompt + args.warmup + args.steps + args.host_steps + args.profile_steps + 8)
     kv = F.HipKvCache(model, max_seq)
     if args.no_graph:
         F.set_graph(kv, False)
@@ -122,20 +126,30 @@ def main():
     log(f"prefill {args.prompt - 1} tokens in {prefill_s:.2f} s")
 
     nxt = int(prompt[-1])
-    for _ in range(args.warmup):
+    warm = fwd.decode_greedy(nxt, pos, args.warmup, kv) if args.warmup else []
+    pos += args.warmup
+    nxt = int(warm[-1]) if len(warm) else nxt
+    log(f"warmup {args.warmup} steps done; timing {args.steps} decode steps")
+
+    F._check(F.N.dev.fllm_seq_sync(kv.h))
+    t0 = time.perf_counter()
+    toks = fwd.decode_greedy(nxt, pos, args.steps, kv)  # returns after the last token is on the host
+    elapsed = time.perf_counter() - t0
+    pos += args.steps
+    nxt = int(toks[-1])
+    tok_s = args.steps / elapsed
+    log(f"decode (device loop): {tok_s:.1f} tok/s ({elapsed / args.steps * 1e3:.3f} ms/token)")
+
+    # the same decode driven from the host, one token read-back per step
+    host_steps = min(args.host_steps, args.steps)
+    t0 = time.perf_counter()
+    for _ in range(host_steps):
         fwd.forward(nxt, pos, kv)
         nxt = fwd.sample_greedy()
         pos += 1
-    log(f"warmup {args.warmup} steps done; timing {args.steps} decode steps")
-
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        fwd.forward(nxt, pos, kv)
-        nxt = fwd.sample_greedy()  # device argmax + 4-byte read-back: the step is complete here
-        pos += 1
-    elapsed = time.perf_counter() - t0
-    tok_s = args.steps / elapsed
-    log(f"decode: {tok_s:.1f} tok/s ({elapsed / args.steps * 1e3:.3f} ms/token)")
+    host_tok_s = host_steps / (time.perf_counter() - t0) if host_steps else None
+    if host_tok_s:
+        log(f"decode (host loop): {host_tok_s:.1f} tok/s")
 
     # profiled pass of the same decode steps: HIP events around every launch
     F.set_profile(kv, True)
@@ -179,7 +193,8 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": f"{cfg['name']}: {args.prompt}-token random prompt prefilled token by token, then greedy "
-                        f"decode at batch 1 (positions {args.prompt - 1 + args.warmup}..{args.prompt - 2 + args.warmup + args.steps})",
+                        f"decode at batch 1 (positions {args.prompt - 1 + args.warmup}..{args.prompt - 2 + args.warmup + args.steps}), "
+                        "device-side greedy loop",
             "weights": "Q4_K (q,k,o,gate,up) + Q6_K (v,down,output), seeded random blocks",
             "weight_bytes_per_token": tok_bytes,
             "graph": not args.no_graph,
@@ -187,6 +202,7 @@ def main():
         "roofline": roofline,
         "decode_step_hbm_frac": round(tok_s * tok_bytes / (HBM_PEAK_GBS * 1e9), 4),
         "prefill_tok_s": round((args.prompt - 1) / prefill_s, 2),
+        "host_loop_tok_s": round(host_tok_s, 2) if host_tok_s else None,
         "profiled_step_ms": round(total_ms, 4),
         "cpu_baseline": cpu,
     }

@@ -271,6 +271,16 @@ class HipForwardPass:
         _check(N.dev.fllm_prefill(kv.h, _iptr(t), len(t), pos0))
         self._kv = kv
 
+    def decode_greedy(self, token_id, position, n_steps, kv):
+        """n greedy decode steps from token_id at position, each step's token fed to the next on
+        the device; returns the n generated tokens."""
+        if kv is None:
+            raise ArgumentNullException("kvCache")
+        out = np.zeros(max(int(n_steps), 1), dtype=np.int32)
+        _check(N.dev.fllm_decode_greedy(kv.h, int(token_id), int(position), int(n_steps), _iptr(out)))
+        self._kv = kv
+        return out[: int(n_steps)]
+
     @property
     def logits(self):
         out = np.empty(self.model.desc.vocab, dtype=np.float32)

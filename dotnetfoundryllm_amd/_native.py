@@ -98,6 +98,7 @@ DEVICE_SIGS = {
     "fllm_seq_set_debug": (I32, [P, I32]),
     "fllm_forward": (I32, [P, I32, I32]),
     "fllm_prefill": (I32, [P, PI32, I32, I32]),
+    "fllm_decode_greedy": (I32, [P, I32, I32, I32, PI32]),
     "fllm_seq_sync": (I32, [P]),
     "fllm_logits_copy": (I32, [P, PF32, I64]),
     "fllm_logits_write": (I32, [P, PF32, I64]),

@@ -42,7 +42,7 @@ def _run(cmd, cwd):
 
 
 def build_device_lib(verbose=False):
-    srcs = ["csrc/kernels.hip", "csrc/api.hip"]
+    srcs = ["csrc/kernels.hip", "csrc/gemv.hip", "csrc/attention.hip", "csrc/api.hip"]
     out = "libfllm_hip.so"
     tmp = out + ".tmp"
     log = _run([HIPCC, *HIP_FLAGS, "-o", tmp, *srcs], PKG)

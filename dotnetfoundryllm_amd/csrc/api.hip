@@ -11,6 +11,8 @@
 #include <string>
 #include <vector>
 
+#include "attention.hpp"
+#include "gemv.hpp"
 #include "kernels.hpp"
 
 using namespace fllm;
@@ -52,10 +54,6 @@ struct fllm_ctx {
     hipStream_t stream = nullptr;
     int n_cu = 0;
     int64_t hbm = 0;
-    // scratch for fllm_gemv's activation quantization
-    uint4* xq_parts = nullptr;
-    float4* xq_stats = nullptr;
-    int64_t xq_groups = 0;
 };
 
 struct fllm_buf {
@@ -104,14 +102,23 @@ struct fllm_seq {
     hipStream_t st = nullptr;
     int max_seq = 0;
     int cur_len = 0;
-    int nsplit = 1;
+    int nsplit = 1;               // chunks of the generic attention kernel
+    int attn_nc = 1;              // chunks per kv head of the fast attention kernel
+    size_t attn_lds = 0;
+    bool attn_fast = false;
+    bool fused = false;           // layers run as fused GEMV launches
+    bool head_fused = false;
+    bool argmax_valid = false;    // params->argmax holds the argmax of the current logits
     float *kc = nullptr, *vc = nullptr;
     float2* rope = nullptr;
     StepParams* params = nullptr;
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
     float *g = nullptr, *u = nullptr, *h = nullptr, *tmp = nullptr, *logits = nullptr;
-    XQ xq_hidden{}, xq_att{}, xq_h{};
     float *part_o = nullptr, *part_ml = nullptr;
+    unsigned int* attn_counters = nullptr;
+    unsigned long long* amax_key = nullptr;
+    unsigned int* head_done = nullptr;
+    int* tokens_out = nullptr;
     int *topk_ids = nullptr, *topk_count = nullptr;
     float* topk_vals = nullptr;
     int topk_cap = 0;
@@ -157,8 +164,6 @@ extern "C" int32_t fllm_ctx_destroy(fllm_ctx* ctx) {
     if (!ctx) return FLLM_OK;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
-    if (ctx->xq_parts) hipFree(ctx->xq_parts);
-    if (ctx->xq_stats) hipFree(ctx->xq_stats);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return FLLM_OK;
@@ -270,10 +275,6 @@ extern "C" int32_t fllm_buf_read(fllm_buf* b, uint64_t offset, void* dst, uint64
     return FLLM_OK;
 }
 
-static bool qpath_type(int t) {
-    return t == FLLM_TYPE_Q4_K || t == FLLM_TYPE_Q5_K || t == FLLM_TYPE_Q6_K || t == FLLM_TYPE_Q8_0 || t == FLLM_TYPE_Q4_0;
-}
-
 static int32_t check_gemv_args(int32_t type, fllm_buf* w, uint64_t w_offset, int64_t rows, int64_t cols, fllm_buf* x,
                                fllm_buf* y) {
     NOT_NULL(w);
@@ -291,35 +292,14 @@ static int32_t check_gemv_args(int32_t type, fllm_buf* w, uint64_t w_offset, int
     return FLLM_OK;
 }
 
-static int32_t ctx_xq(fllm_ctx* ctx, int64_t groups, XQ* out) {
-    if (groups > ctx->xq_groups) {
-        if (ctx->xq_parts) hipFree(ctx->xq_parts);
-        if (ctx->xq_stats) hipFree(ctx->xq_stats);
-        ctx->xq_parts = nullptr;
-        ctx->xq_stats = nullptr;
-        HIP_TRY(hipMalloc(&ctx->xq_parts, sizeof(uint4) * 6 * (size_t)groups));
-        HIP_TRY(hipMalloc(&ctx->xq_stats, sizeof(float4) * (size_t)groups));
-        ctx->xq_groups = groups;
-    }
-    out->parts = ctx->xq_parts;
-    out->stats = ctx->xq_stats;
-    return FLLM_OK;
-}
-
 extern "C" int32_t fllm_gemv(fllm_ctx* ctx, int32_t type, fllm_buf* w, uint64_t w_offset, int64_t rows, int64_t cols,
                              fllm_buf* x, fllm_buf* y) {
     NOT_NULL(ctx);
     int32_t rc = check_gemv_args(type, w, w_offset, rows, cols, x, y);
     if (rc) return rc;
     HIP_TRY(hipSetDevice(ctx->device));
-    XQ xq{nullptr, nullptr};
-    if (qpath_type(type) && cols % 32 == 0) {
-        rc = ctx_xq(ctx, cols / 32, &xq);
-        if (rc) return rc;
-        HIP_TRY(launch_quantize((const float*)x->ptr, cols, xq, ctx->stream));
-    }
     WMat m{w->ptr + w_offset, type, rows, cols};
-    HIP_TRY(launch_gemv(m, (const float*)x->ptr, xq, (float*)y->ptr, nullptr, ctx->stream));
+    HIP_TRY(launch_gemv(m, (const float*)x->ptr, (float*)y->ptr, nullptr, ctx->n_cu, ctx->stream));
     return FLLM_OK;
 }
 
@@ -334,19 +314,13 @@ extern "C" int32_t fllm_gemv_time(fllm_ctx* ctx, int32_t type, fllm_buf* const* 
         if (rc) return rc;
     }
     HIP_TRY(hipSetDevice(ctx->device));
-    XQ xq{nullptr, nullptr};
-    if (qpath_type(type) && cols % 32 == 0) {
-        int32_t rc = ctx_xq(ctx, cols / 32, &xq);
-        if (rc) return rc;
-        HIP_TRY(launch_quantize((const float*)x->ptr, cols, xq, ctx->stream));
-    }
     std::vector<hipEvent_t> ev(2 * (size_t)iters);
     for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
     hipError_t err = hipSuccess;
     for (int i = 0; i < iters && err == hipSuccess; i++) {
         WMat m{w[i % n_w]->ptr, type, rows, cols};
         err = hipEventRecord(ev[2 * i], ctx->stream);
-        if (err == hipSuccess) err = launch_gemv(m, (const float*)x->ptr, xq, (float*)y->ptr, nullptr, ctx->stream);
+        if (err == hipSuccess) err = launch_gemv(m, (const float*)x->ptr, (float*)y->ptr, nullptr, ctx->n_cu, ctx->stream);
         if (err == hipSuccess) err = hipEventRecord(ev[2 * i + 1], ctx->stream);
     }
     if (err == hipSuccess) err = hipStreamSynchronize(ctx->stream);
@@ -601,6 +575,15 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     s->m = m;
     s->max_seq = max_seq > 0 ? max_seq : d.max_ctx;
     s->nsplit = (s->max_seq + 255) / 256;
+    s->attn_fast = attn_fast_supported(d.head_dim, d.n_heads / d.n_kv_heads);
+    s->attn_nc = attn_chunks(d.n_kv_heads, s->max_seq, m->ctx->n_cu > 0 ? m->ctx->n_cu : 256);
+    s->attn_lds = attn_lds_bytes(d.head_dim, d.n_heads / d.n_kv_heads, s->attn_nc, s->max_seq);
+    s->fused = s->attn_fast && gemv_fusable_cols(d.hidden) && gemv_fusable_cols(m->qdim) && gemv_fusable_cols(d.ffn);
+    for (const Layer& Lr : m->layers) {
+        const Tensor* ts[] = {&Lr.q, &Lr.k, &Lr.v, &Lr.o, &Lr.gate, &Lr.up, &Lr.down};
+        for (const Tensor* t : ts) s->fused = s->fused && gemv_fusable_type(t->type);
+    }
+    s->head_fused = s->fused && gemv_fusable_type(m->output.type);
     hipError_t e = hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking);
     if (e != hipSuccess) { s->st = nullptr; seq_free(s); return fail(FLLM_E_DEVICE, "hipStreamCreate: %s", hipGetErrorString(e)); }
     size_t L = (size_t)d.n_layers, kv = (size_t)m->kvdim, H = (size_t)d.hidden, F = (size_t)d.ffn;
@@ -624,14 +607,13 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->h, F);
     ALLOC(s->tmp, H);
     ALLOC(s->logits, (size_t)d.vocab);
-    ALLOC(s->xq_hidden.parts, 6 * (H / 32 + 1));
-    ALLOC(s->xq_hidden.stats, H / 32 + 1);
-    ALLOC(s->xq_att.parts, 6 * ((size_t)m->qdim / 32 + 1));
-    ALLOC(s->xq_att.stats, (size_t)m->qdim / 32 + 1);
-    ALLOC(s->xq_h.parts, 6 * (F / 32 + 1));
-    ALLOC(s->xq_h.stats, F / 32 + 1);
-    ALLOC(s->part_o, (size_t)d.n_heads * s->nsplit * d.head_dim);
-    ALLOC(s->part_ml, (size_t)d.n_heads * s->nsplit * 2);
+    size_t nparts = (size_t)(s->nsplit > s->attn_nc ? s->nsplit : s->attn_nc);
+    ALLOC(s->part_o, (size_t)d.n_heads * nparts * d.head_dim);
+    ALLOC(s->part_ml, (size_t)d.n_heads * nparts * 2);
+    ALLOC(s->attn_counters, (size_t)d.n_kv_heads);
+    ALLOC(s->amax_key, 1);
+    ALLOC(s->head_done, 1);
+    ALLOC(s->tokens_out, (size_t)s->max_seq);
     ALLOC(s->topk_ids, (size_t)d.vocab);
     ALLOC(s->topk_vals, (size_t)d.vocab);
     ALLOC(s->topk_count, 1);
@@ -649,6 +631,10 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     }
     e = hipMemcpyAsync(s->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->kc, 0, sizeof(float) * kvsz, s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->attn_counters, 0, sizeof(unsigned int) * (size_t)d.n_kv_heads, s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->amax_key, 0, sizeof(unsigned long long), s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->head_done, 0, sizeof(unsigned int), s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->params, 0, sizeof(StepParams), s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, sizeof(float) * kvsz, s->st);
     if (e == hipSuccess) e = hipStreamSynchronize(s->st);
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_DEVICE, "sequence init: %s", hipGetErrorString(e)); }
@@ -774,14 +760,150 @@ static const char* gemv_name(int type) {
         if (_e != hipSuccess) return _e;                 \
     } while (0)
 
-static hipError_t gemv_step(fllm_seq* s, const Tensor& t, const float* xf, const XQ& xq, float* y, const float* res) {
+static hipError_t gemv_step(fllm_seq* s, const Tensor& t, const float* xf, float* y, const float* res) {
     double bytes = (double)t.bytes + 4.0 * (double)(t.cols + t.rows);
-    STEP(gemv_name(t.type), bytes, launch_gemv(t.mat(), xf, xq, y, res, s->st));
+    STEP(gemv_name(t.type), bytes, launch_gemv(t.mat(), xf, y, res, s->m->ctx->n_cu, s->st));
     return hipSuccess;
 }
 
-// The decode step body (everything after the step-parameter write), launched eagerly or captured.
-static hipError_t enqueue_body(fllm_seq* s) {
+static int layer_window(const fllm_model_desc& d, int l) {
+    if (d.arch == FLLM_ARCH_MISTRAL) return d.sliding_window;             // MistralForwardPass.cs:131
+    if (d.arch == FLLM_ARCH_GEMMA2 && (l % 2) == 0) return d.sliding_window;  // Gemma2ForwardPass.cs:87
+    return 0x7FFFFFFF;
+}
+
+static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const float* vc) {
+    const fllm_model_desc& d = s->m->d;
+    bool gemma = d.arch == FLLM_ARCH_GEMMA2;
+    int window = layer_window(d, l);
+    float softcap = gemma ? d.attn_softcap : 0.0f;
+    // K and V rows attended (at most the whole cache) plus q and the output
+    double bytes = 8.0 * (double)s->m->kvdim * (double)s->max_seq + 8.0 * s->m->qdim;
+    if (s->attn_fast) {
+        AttnArgs a{};
+        a.q = s->q; a.kc = kc; a.vc = vc;
+        a.nh = d.n_heads; a.nkv = d.n_kv_heads; a.hd = d.head_dim; a.kvdim = s->m->kvdim;
+        a.window = window; a.scale = d.attn_scale; a.softcap = softcap;
+        a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml; a.counters = s->attn_counters;
+        a.out = s->att; a.params = s->params;
+        STEP("attention", bytes, launch_attn_decode(a, s->attn_lds, s->st));
+    } else {
+        STEP("attention", bytes,
+             launch_attention(s->q, kc, vc, d.n_heads, d.n_kv_heads, d.head_dim, window, d.attn_scale, softcap,
+                              s->nsplit, s->part_o, s->part_ml, s->att, s->params, s->st));
+    }
+    return hipSuccess;
+}
+
+static GemvSeg seg_of(const Tensor& t, int epi, float* out, const float* bias, const float* resid) {
+    GemvSeg g{};
+    g.w = t.ptr; g.type = t.type; g.rows = (int)t.rows; g.epi = epi; g.out = out; g.bias = bias; g.resid = resid;
+    return g;
+}
+
+static hipError_t fused_step(fllm_seq* s, const char* name, GemvArgs& a, int64_t cols, double bytes) {
+    int threads;
+    size_t lds;
+    int grid = gemv_plan(a, cols, s->m->ctx->n_cu > 0 ? s->m->ctx->n_cu : 256, 0, &threads, &lds);
+    STEP(name, bytes, launch_gemv_fused(a, grid, threads, lds, s->st));
+    return hipSuccess;
+}
+
+// LM head, logits softcap, greedy argmax and the step advance (generic kernels).
+static hipError_t head_generic(fllm_seq* s) {
+    fllm_model* m = s->m;
+    const fllm_model_desc& d = m->d;
+    bool gemma = d.arch == FLLM_ARCH_GEMMA2;
+    float eps = gemma ? 1e-6f : d.norm_eps;
+    int H = d.hidden;
+    STEP("rmsnorm", 12.0 * H, launch_rmsnorm(s->x, m->out_norm, H, eps, gemma ? 1 : 0, s->xn, s->st));
+    if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(s->xn, H, s->hidden_dbg + (size_t)d.n_layers * H, s->st));
+    hipError_t e = gemv_step(s, m->output, s->xn, s->logits, nullptr);
+    if (e != hipSuccess) return e;
+    if (gemma && d.final_softcap > 0.0f) STEP("softcap", 8.0 * d.vocab, launch_softcap(s->logits, d.vocab, d.final_softcap, s->st));
+    STEP("argmax", 4.0 * d.vocab, launch_argmax(s->logits, d.vocab, s->params, s->tokens_out, s->max_seq, s->st));
+    return hipSuccess;
+}
+
+// Decode step as fused launches: per layer [norm + QKV + RoPE + KV store], attention,
+// [Wo + residual], [norm + gate/up + activation], [down + residual]; then [norm + LM head +
+// softcap + argmax + step advance]. Gemma2's post-norms are separate small kernels.
+static hipError_t enqueue_body_fused(fllm_seq* s) {
+    fllm_model* m = s->m;
+    const fllm_model_desc& d = m->d;
+    bool gemma = d.arch == FLLM_ARCH_GEMMA2;
+    int H = d.hidden, kvdim = m->kvdim;
+    float eps = gemma ? 1e-6f : d.norm_eps;
+    int nk = gemma ? 1 : 0;
+    size_t layer_kv = (size_t)s->max_seq * kvdim;
+    for (int l = 0; l < d.n_layers; l++) {
+        const Layer& L = m->layers[(size_t)l];
+        float* kc = s->kc + (size_t)l * layer_kv;
+        float* vc = s->vc + (size_t)l * layer_kv;
+        {
+            GemvArgs a{};
+            a.nseg = 3;
+            a.seg[0] = seg_of(L.q, EPI_Q, s->q, L.bq, nullptr);
+            a.seg[1] = seg_of(L.k, EPI_K, nullptr, L.bk, nullptr);
+            a.seg[2] = seg_of(L.v, EPI_V, nullptr, L.bv, nullptr);
+            a.xin = l == 0 ? XIN_EMBED_NORM : XIN_NORM;
+            a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
+            a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
+            a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
+            double bytes = (double)(L.q.bytes + L.k.bytes + L.v.bytes) + 4.0 * (2.0 * H + m->qdim + 2.0 * kvdim);
+            hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes);
+            if (e != hipSuccess) return e;
+        }
+        hipError_t e = attention_step(s, l, kc, vc);
+        if (e != hipSuccess) return e;
+        {
+            GemvArgs a{};
+            a.nseg = 1;
+            a.seg[0] = gemma ? seg_of(L.o, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.o, EPI_RESID, s->x, nullptr, s->x);
+            a.xin = XIN_F32;
+            a.x = s->att;
+            e = fused_step(s, "attn_output", a, m->qdim, (double)L.o.bytes + 4.0 * (m->qdim + 2.0 * H));
+            if (e != hipSuccess) return e;
+            if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));
+        }
+        {
+            GemvArgs a{};
+            a.nseg = 2;
+            a.glu = 1;
+            a.act = gemma ? 1 : 0;
+            a.seg[0] = seg_of(L.gate, EPI_STORE, s->h, nullptr, nullptr);
+            a.seg[1] = seg_of(L.up, EPI_STORE, nullptr, nullptr, nullptr);
+            a.xin = XIN_NORM;
+            a.x = s->x; a.norm_w = L.ffn_norm; a.eps = eps; a.norm_kind = nk;
+            e = fused_step(s, "ffn_gate_up", a, H, (double)(L.gate.bytes + L.up.bytes) + 4.0 * (2.0 * H + d.ffn));
+            if (e != hipSuccess) return e;
+        }
+        {
+            GemvArgs a{};
+            a.nseg = 1;
+            a.seg[0] = gemma ? seg_of(L.down, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.down, EPI_RESID, s->x, nullptr, s->x);
+            a.xin = XIN_F32;
+            a.x = s->h;
+            e = fused_step(s, "ffn_down", a, d.ffn, (double)L.down.bytes + 4.0 * (d.ffn + 2.0 * H));
+            if (e != hipSuccess) return e;
+            if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, s->x, s->st));
+        }
+        if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(s->x, H, s->hidden_dbg + (size_t)l * H, s->st));
+    }
+    if (!s->head_fused || s->debug) return head_generic(s);
+    GemvArgs a{};
+    a.nseg = 1;
+    a.seg[0] = seg_of(m->output, EPI_LOGITS, s->logits, nullptr, nullptr);
+    a.xin = XIN_NORM;
+    a.x = s->x; a.norm_w = m->out_norm; a.eps = eps; a.norm_kind = nk;
+    a.softcap = (gemma && d.final_softcap > 0.0f) ? d.final_softcap : 0.0f;
+    a.amax_key = s->amax_key; a.done = s->head_done; a.params_rw = s->params; a.params = s->params;
+    a.tokens_out = s->tokens_out; a.tokens_cap = s->max_seq;
+    return fused_step(s, "lm_head_argmax", a, H, (double)m->output.bytes + 4.0 * (2.0 * H + d.vocab));
+}
+
+// The decode step as one kernel per reference op (any tensor type and shape).
+static hipError_t enqueue_body_generic(fllm_seq* s) {
     fllm_model* m = s->m;
     const fllm_model_desc& d = m->d;
     bool gemma = d.arch == FLLM_ARCH_GEMMA2;
@@ -792,53 +914,42 @@ static hipError_t enqueue_body(fllm_seq* s) {
     STEP("embed", 4.0 * H, launch_embed(m->tok_embd.ptr, m->tok_embd.type, H, s->params, s->x, s->st));
     for (int l = 0; l < d.n_layers; l++) {
         const Layer& L = m->layers[(size_t)l];
-        STEP("rmsnorm", 12.0 * H, launch_rmsnorm_q(s->x, L.attn_norm, H, eps, nk, s->xn, s->xq_hidden, s->st));
+        STEP("rmsnorm", 12.0 * H, launch_rmsnorm(s->x, L.attn_norm, H, eps, nk, s->xn, s->st));
         hipError_t e;
-        if ((e = gemv_step(s, L.q, s->xn, s->xq_hidden, s->q, nullptr)) != hipSuccess) return e;
-        if ((e = gemv_step(s, L.k, s->xn, s->xq_hidden, s->k, nullptr)) != hipSuccess) return e;
-        if ((e = gemv_step(s, L.v, s->xn, s->xq_hidden, s->v, nullptr)) != hipSuccess) return e;
+        if ((e = gemv_step(s, L.q, s->xn, s->q, nullptr)) != hipSuccess) return e;
+        if ((e = gemv_step(s, L.k, s->xn, s->k, nullptr)) != hipSuccess) return e;
+        if ((e = gemv_step(s, L.v, s->xn, s->v, nullptr)) != hipSuccess) return e;
         float* kc = s->kc + (size_t)l * layer_kv;
         float* vc = s->vc + (size_t)l * layer_kv;
         STEP("qkv_rope_kvstore", 8.0 * (m->qdim + 2 * kvdim),
              launch_qkv_post(s->q, s->k, s->v, L.bq, L.bk, L.bv, s->rope, d.n_heads, d.n_kv_heads, d.head_dim, kc, vc,
                              s->params, s->st));
-        int window = 0x7FFFFFFF;
-        if (d.arch == FLLM_ARCH_MISTRAL) window = d.sliding_window;
-        if (gemma && (l % 2) == 0) window = d.sliding_window;
-        STEP("attention", 0.0,
-             launch_attention(s->q, kc, vc, d.n_heads, d.n_kv_heads, d.head_dim, window, d.attn_scale,
-                              gemma ? d.attn_softcap : 0.0f, s->nsplit, s->part_o, s->part_ml, s->att, s->xq_att,
-                              s->params, s->st));
-        // the attention combine writes the quantized copy only when head_dim is a multiple of 32
-        XQ att_q = (d.head_dim % 32 == 0) ? s->xq_att : XQ{nullptr, nullptr};
+        if ((e = attention_step(s, l, kc, vc)) != hipSuccess) return e;
         if (gemma) {
-            if ((e = gemv_step(s, L.o, s->att, att_q, s->tmp, nullptr)) != hipSuccess) return e;
+            if ((e = gemv_step(s, L.o, s->att, s->tmp, nullptr)) != hipSuccess) return e;
             STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));
         } else {
-            if ((e = gemv_step(s, L.o, s->att, att_q, s->x, s->x)) != hipSuccess) return e;
+            if ((e = gemv_step(s, L.o, s->att, s->x, s->x)) != hipSuccess) return e;
         }
-        STEP("rmsnorm", 12.0 * H, launch_rmsnorm_q(s->x, L.ffn_norm, H, eps, nk, s->xn, s->xq_hidden, s->st));
-        if ((e = gemv_step(s, L.gate, s->xn, s->xq_hidden, s->g, nullptr)) != hipSuccess) return e;
-        if ((e = gemv_step(s, L.up, s->xn, s->xq_hidden, s->u, nullptr)) != hipSuccess) return e;
-        STEP("ffn_act", 12.0 * d.ffn, launch_act(s->g, s->u, d.ffn, gemma ? 1 : 0, s->h, s->xq_h, s->st));
+        STEP("rmsnorm", 12.0 * H, launch_rmsnorm(s->x, L.ffn_norm, H, eps, nk, s->xn, s->st));
+        if ((e = gemv_step(s, L.gate, s->xn, s->g, nullptr)) != hipSuccess) return e;
+        if ((e = gemv_step(s, L.up, s->xn, s->u, nullptr)) != hipSuccess) return e;
+        STEP("ffn_act", 12.0 * d.ffn, launch_act(s->g, s->u, d.ffn, gemma ? 1 : 0, s->h, s->st));
         if (gemma) {
-            if ((e = gemv_step(s, L.down, s->h, s->xq_h, s->tmp, nullptr)) != hipSuccess) return e;
+            if ((e = gemv_step(s, L.down, s->h, s->tmp, nullptr)) != hipSuccess) return e;
             STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, s->x, s->st));
         } else {
-            if ((e = gemv_step(s, L.down, s->h, s->xq_h, s->x, s->x)) != hipSuccess) return e;
+            if ((e = gemv_step(s, L.down, s->h, s->x, s->x)) != hipSuccess) return e;
         }
         if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(s->x, H, s->hidden_dbg + (size_t)l * H, s->st));
     }
-    STEP("rmsnorm", 12.0 * H, launch_rmsnorm_q(s->x, m->out_norm, H, eps, nk, s->xn, s->xq_hidden, s->st));
-    if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(s->xn, H, s->hidden_dbg + (size_t)d.n_layers * H, s->st));
-    hipError_t e = gemv_step(s, m->output, s->xn, s->xq_hidden, s->logits, nullptr);
-    if (e != hipSuccess) return e;
-    if (gemma && d.final_softcap > 0.0f) STEP("softcap", 8.0 * d.vocab, launch_softcap(s->logits, d.vocab, d.final_softcap, s->st));
-    return hipSuccess;
+    return head_generic(s);
 }
 
+static hipError_t enqueue_body(fllm_seq* s) { return s->fused ? enqueue_body_fused(s) : enqueue_body_generic(s); }
+
 static int32_t enqueue_step(fllm_seq* s, int token, int pos) {
-    HIP_TRY(launch_set_params(s->params, token, pos, s->cur_len, s->st));
+    if (token >= 0) HIP_TRY(launch_set_params(s->params, token, pos, s->cur_len, s->st));
     bool graph = s->use_graph && !s->profile;
     if (!graph) {
         hipError_t e = enqueue_body(s);
@@ -877,6 +988,48 @@ extern "C" int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position) {
     int32_t rc = enqueue_step(s, token, position);
     if (rc) return rc;
     s->cur_len++;
+    s->argmax_valid = true;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_decode_greedy(fllm_seq* s, int32_t token, int32_t position, int32_t n_steps, int32_t* out_tokens) {
+    NOT_NULL(s);
+    const fllm_model_desc& d = s->m->d;
+    if (n_steps < 0) return fail(FLLM_E_ARG_RANGE, "n_steps must be >= 0");
+    if (n_steps == 0) return FLLM_OK;
+    NOT_NULL(out_tokens);
+    if (token < 0 || token >= d.vocab)
+        return fail(FLLM_E_ARG_RANGE, "Token id %d is outside the valid vocabulary range [0, %d].", token, d.vocab - 1);
+    if (position < 0 || position > s->cur_len)
+        return fail(FLLM_E_ARG_RANGE, "position %d outside the cached range [0, %d]", position, s->cur_len);
+    if ((int64_t)s->cur_len + n_steps > s->max_seq)
+        return fail(FLLM_E_ARG_RANGE, "%d steps from length %d exceed the KV cache capacity (%d positions)", n_steps,
+                    s->cur_len, s->max_seq);
+    if (s->profile) return fail(FLLM_E_INVALID_OP, "the device-side decode loop does not run in profile mode");
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    // parameters once; every replayed step then feeds its greedy token to the next on the device
+    HIP_TRY(launch_set_params(s->params, token, position, s->cur_len, s->st));
+    for (int i = 0; i < n_steps; i++) {
+        int32_t rc;
+        if (s->use_graph) {
+            rc = FLLM_OK;
+            if (!s->graph_valid) {
+                // capture without touching the parameters the first step already holds
+                rc = enqueue_step(s, -1, -1);
+            } else {
+                hipError_t e = hipGraphLaunch(s->gexec, s->st);
+                if (e != hipSuccess) rc = fail(FLLM_E_DEVICE, "hipGraphLaunch: %s", hipGetErrorString(e));
+            }
+        } else {
+            hipError_t e = enqueue_body(s);
+            rc = e == hipSuccess ? FLLM_OK : fail(FLLM_E_DEVICE, "decode step: %s", hipGetErrorString(e));
+        }
+        if (rc) return rc;
+        s->cur_len++;
+    }
+    HIP_TRY(hipMemcpyAsync(out_tokens, s->tokens_out, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    s->argmax_valid = true;
     return FLLM_OK;
 }
 
@@ -908,13 +1061,17 @@ extern "C" int32_t fllm_logits_write(fllm_seq* s, const float* src, int64_t n) {
     if (n != V) return fail(FLLM_E_ARG, "source must hold exactly %d floats", V);
     HIP_TRY(hipMemcpyAsync(s->logits, src, sizeof(float) * (size_t)V, hipMemcpyHostToDevice, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));
+    s->argmax_valid = false;
     return FLLM_OK;
 }
 
 extern "C" int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token) {
     NOT_NULL(s);
     NOT_NULL(out_token);
-    HIP_TRY(launch_argmax(s->logits, s->m->d.vocab, s->params, s->st));
+    // the decode step already reduced its logits to the greedy token; recompute only after the
+    // logits were changed on the host or by the top-k sampler
+    if (!s->argmax_valid) HIP_TRY(launch_argmax(s->logits, s->m->d.vocab, s->params, nullptr, 0, s->st));
+    s->argmax_valid = true;
     StepParams hp;
     HIP_TRY(hipMemcpyAsync(&hp, s->params, sizeof(hp), hipMemcpyDeviceToHost, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));
@@ -931,6 +1088,7 @@ extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int3
     int V = s->m->d.vocab;
     int dcap = cap < s->topk_cap ? cap : s->topk_cap;
     HIP_TRY(launch_topk(s->logits, V, inv_temp, k, dcap, s->topk_ids, s->topk_vals, s->topk_count, s->st));
+    if (inv_temp != 1.0f) s->argmax_valid = false;
     int cnt = 0;
     HIP_TRY(hipMemcpyAsync(&cnt, s->topk_count, sizeof(int), hipMemcpyDeviceToHost, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));

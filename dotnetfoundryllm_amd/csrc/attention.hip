@@ -1,0 +1,220 @@
+// attention.hip — decode attention over the device KV cache (gfx950).
+//
+// ComputeAttention (LlamaForwardPass.cs:158-211; Mistral window MistralForwardPass.cs:121-175;
+// Gemma2 scale, score softcap and window Gemma2ForwardPass.cs:126-185): for every query head,
+// scores s_t = Dot(q, k_t) * scale over t in [window_start, position], optional tanh softcap,
+// Softmax, out = sum_t p_t v_t.
+//
+// Split-K ("flash decoding") layout. Workgroup (kv head, chunk) takes a contiguous chunk of
+// the attended range for the whole query group of that kv head, so each K/V row is read from
+// HBM once per group. Lanes split a K/V row into float4 slices (hd/4 lanes per row, 64/(hd/4)
+// rows per wave load, fully coalesced); q for the group stays in registers. Each workgroup
+// writes its unnormalised partial output with the chunk's max and sum; the last workgroup of a
+// kv head to finish (atomic counter, no waiting) merges the partials and writes the output.
+#include "attention.hpp"
+
+#include <math.h>
+
+namespace fllm {
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
+    constexpr int LPR = HD / 4;    // lanes per K/V row
+    constexpr int RPL = 64 / LPR;  // rows per wave load
+    constexpr int GMAX = ATTN_GROUP_MAX;
+    extern __shared__ float sh[];
+    __shared__ int s_last;
+    const int kvh = blockIdx.x, c = blockIdx.y;
+    const int group = a.nh / a.nkv;
+    const int seq = a.params->pos + 1;
+    int ws = seq - a.window;
+    if (ws < 0) ws = 0;
+    const int alen = seq - ws;
+    int ch = (alen + a.nc - 1) / a.nc;
+    ch = (ch + 31) / 32 * 32;
+    const int nchunks = (alen + ch - 1) / ch;
+    if (c >= nchunks) return;
+    const int t0 = ws + c * ch;
+    const int len = min(ch, seq - t0);
+    const int h0 = kvh * group;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane / LPR, dl = lane % LPR;
+
+    float* sc = sh;                                   // [group][ch] scores, then weights
+    float* red = sh + group * ch;                     // [4 waves][group][HD]
+    float* ml = red + 4 * group * HD;                 // [group][2]
+
+    // q slice of every head of the group
+    float4 qv[GMAX];
+#pragma unroll
+    for (int h = 0; h < GMAX; h++)
+        qv[h] = h < group ? *(const float4*)(a.q + (int64_t)(h0 + h) * HD + dl * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+
+    const float* kbase = a.kc + (int64_t)kvh * HD + dl * 4;
+    const float* vbase = a.vc + (int64_t)kvh * HD + dl * 4;
+    const int rstep = 4 * RPL;  // rows covered by one load of the 4 waves
+    const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
+
+    // ---- scores --------------------------------------------------------------------------
+    for (int base = wave * RPL + sub; base < len; base += 4 * rstep) {
+        float4 kr[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            int t = base + u * rstep;
+            kr[u] = t < len ? *(const float4*)(kbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            int t = base + u * rstep;
+#pragma unroll
+            for (int h = 0; h < GMAX; h++) {
+                if (h >= group) break;
+                float s = qv[h].x * kr[u].x;
+                s = fmaf(qv[h].y, kr[u].y, s);
+                s = fmaf(qv[h].z, kr[u].z, s);
+                s = fmaf(qv[h].w, kr[u].w, s);
+#pragma unroll
+                for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
+                if (dl == 0 && t < len) {
+                    s = s * a.scale;
+                    if (a.softcap > 0.0f) s = tanhf(s * inv_cap) * a.softcap;
+                    sc[h * ch + t] = s;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- softmax pieces per head: max, exp(s - max), sum -----------------------------------
+    for (int h = wave; h < group; h += 4) {
+        float m = -INFINITY;
+        for (int t = lane; t < len; t += 64) m = fmaxf(m, sc[h * ch + t]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        float l = 0.0f;
+        for (int t = lane; t < len; t += 64) {
+            float e = expf(sc[h * ch + t] - m);
+            sc[h * ch + t] = e;
+            l += e;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+        if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
+    }
+    __syncthreads();
+
+    // ---- weighted sum of V ------------------------------------------------------------------
+    float4 acc[GMAX];
+#pragma unroll
+    for (int h = 0; h < GMAX; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int base = wave * RPL + sub; base < len; base += 4 * rstep) {
+        float4 vr[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            int t = base + u * rstep;
+            vr[u] = t < len ? *(const float4*)(vbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            int t = base + u * rstep;
+            if (t >= len) break;
+#pragma unroll
+            for (int h = 0; h < GMAX; h++) {
+                if (h >= group) break;
+                float p = sc[h * ch + t];
+                acc[h].x = fmaf(p, vr[u].x, acc[h].x);
+                acc[h].y = fmaf(p, vr[u].y, acc[h].y);
+                acc[h].z = fmaf(p, vr[u].z, acc[h].z);
+                acc[h].w = fmaf(p, vr[u].w, acc[h].w);
+            }
+        }
+    }
+    // reduce over the RPL row slots of the wave, then over the 4 waves through LDS
+#pragma unroll
+    for (int h = 0; h < GMAX; h++) {
+        if (h >= group) break;
+#pragma unroll
+        for (int o = LPR; o < 64; o <<= 1) {
+            acc[h].x += __shfl_xor(acc[h].x, o);
+            acc[h].y += __shfl_xor(acc[h].y, o);
+            acc[h].z += __shfl_xor(acc[h].z, o);
+            acc[h].w += __shfl_xor(acc[h].w, o);
+        }
+        if (sub == 0) *(float4*)(red + ((wave * group + h) * HD) + dl * 4) = acc[h];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < group * HD; idx += blockDim.x) {
+        float o = red[idx] + red[group * HD + idx] + red[2 * group * HD + idx] + red[3 * group * HD + idx];
+        int h = idx / HD, d = idx % HD;
+        a.part_o[((int64_t)(h0 + h) * a.nc + c) * HD + d] = o;
+    }
+    for (int h = threadIdx.x; h < group; h += blockDim.x) {
+        a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2] = ml[2 * h];
+        a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2 + 1] = ml[2 * h + 1];
+    }
+
+    // ---- the last chunk of this kv head to finish merges all chunks ----------------------------
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned prev = atomicAdd(a.counters + kvh, 1u);
+        s_last = (prev == (unsigned)(nchunks - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int idx = threadIdx.x; idx < group * (HD / 4); idx += blockDim.x) {
+        int h = idx / (HD / 4), d4 = idx % (HD / 4);
+        const float* pml = a.part_ml + (int64_t)(h0 + h) * a.nc * 2;
+        const float* po = a.part_o + (int64_t)(h0 + h) * a.nc * HD + d4 * 4;
+        float M = -INFINITY;
+        for (int k = 0; k < nchunks; k++) M = fmaxf(M, pml[2 * k]);
+        float L = 0.0f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < nchunks; k++) {
+            float w = expf(pml[2 * k] - M);
+            L = fmaf(pml[2 * k + 1], w, L);
+            float4 p = *(const float4*)(po + (int64_t)k * HD);
+            o.x = fmaf(p.x, w, o.x);
+            o.y = fmaf(p.y, w, o.y);
+            o.z = fmaf(p.z, w, o.z);
+            o.w = fmaf(p.w, w, o.w);
+        }
+        float inv = 1.0f / L;
+        *(float4*)(a.out + (int64_t)(h0 + h) * HD + d4 * 4) = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    }
+    if (threadIdx.x == 0) atomicExch(a.counters + kvh, 0u);
+}
+
+bool attn_fast_supported(int head_dim, int group) {
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && group >= 1 && group <= ATTN_GROUP_MAX;
+}
+
+int attn_chunks(int n_kv, int max_seq, int n_cu) {
+    // enough chunks to give every CU a workgroup at long context, chunks of at most 256 positions
+    int target = (2 * n_cu + n_kv - 1) / n_kv;
+    int by_min = (max_seq + 31) / 32;
+    int by_max = (max_seq + 255) / 256;
+    int nc = target < by_min ? target : by_min;
+    if (nc < by_max) nc = by_max;
+    if (nc < 1) nc = 1;
+    return nc;
+}
+
+size_t attn_lds_bytes(int head_dim, int group, int nc, int max_seq) {
+    int ch_max = (max_seq + nc - 1) / nc;
+    ch_max = (ch_max + 31) / 32 * 32;
+    return sizeof(float) * ((size_t)group * ch_max + 4 * (size_t)group * head_dim + 2 * (size_t)group);
+}
+
+hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st) {
+    dim3 grid(a.nkv, a.nc);
+    switch (a.hd) {
+        case 64: k_attn_decode<64><<<grid, 256, lds, st>>>(a); break;
+        case 128: k_attn_decode<128><<<grid, 256, lds, st>>>(a); break;
+        default: k_attn_decode<256><<<grid, 256, lds, st>>>(a); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fllm

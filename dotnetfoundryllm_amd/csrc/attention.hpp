@@ -1,0 +1,30 @@
+// attention.hpp — launch interface of the split-K decode attention kernel (attention.hip).
+#pragma once
+
+#include "kernels.hpp"
+
+namespace fllm {
+
+constexpr int ATTN_GROUP_MAX = 8;  // query heads per kv head handled by the fast kernel
+
+struct AttnArgs {
+    const float* q;        // [nh][hd]
+    const float* kc;       // this layer's K cache [pos][kvdim]
+    const float* vc;       // this layer's V cache
+    int nh, nkv, hd, kvdim;
+    int window;            // attend to the last `window` positions (INT32_MAX = all)
+    float scale, softcap;  // softcap 0 = off
+    int nc;                // chunks per kv head (grid.y)
+    float* part_o;         // [nh][nc][hd]
+    float* part_ml;        // [nh][nc][2]
+    unsigned int* counters;  // [nkv], zero between launches
+    float* out;            // [nh][hd]
+    const StepParams* params;
+};
+
+bool attn_fast_supported(int head_dim, int group);
+int attn_chunks(int n_kv, int max_seq, int n_cu);
+size_t attn_lds_bytes(int head_dim, int group, int nc, int max_seq);
+hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st);
+
+}  // namespace fllm

@@ -1,0 +1,64 @@
+// gemv.hpp — launch interface of the fused dequant-GEMV kernel (gemv.hip).
+#pragma once
+
+#include "kernels.hpp"
+
+namespace fllm {
+
+// input of the projection
+enum { XIN_F32 = 0, XIN_NORM = 1, XIN_EMBED_NORM = 2 };
+// epilogue of a segment
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_Q = 2, EPI_K = 3, EPI_V = 4, EPI_LOGITS = 5 };
+
+// One matrix of a fused launch. The segment owns workgroups [wg_begin, next segment's wg_begin).
+struct GemvSeg {
+    const uint8_t* w;      // GGUF blocks, row r = elements [r*cols, (r+1)*cols)
+    int type;
+    int rows;
+    int wg_begin;
+    int epi;
+    float* out;            // EPI_STORE / EPI_RESID / EPI_Q / EPI_LOGITS destination
+    const float* bias;     // optional (Qwen2 q/k/v bias)
+    const float* resid;    // EPI_RESID: out[r] = resid[r] + W x (may alias out)
+};
+
+struct GemvArgs {
+    GemvSeg seg[3];
+    int nseg;
+    int G;                 // groups of 32 columns per row
+    int S;                 // groups per wave slice
+    int rpw;               // rows per workgroup (multiple of 8)
+    int glu;               // 1: seg[0] = gate, seg[1] = up, seg[0].out = act(gate x) * (up x)
+    int act;               // 0 SiLU, 1 GELU (tanh form)
+    // input
+    int xin;
+    const float* x;        // XIN_F32 / XIN_NORM input vector
+    float* x_out;          // XIN_EMBED_NORM: the embedding row is also stored here (workgroup 0)
+    const float* norm_w;   // XIN_NORM / XIN_EMBED_NORM
+    float eps;
+    int norm_kind;         // 0: (x*rms)*w, 1: (x*rms)*(1+w)
+    const uint8_t* emb;
+    int emb_type;
+    const StepParams* params;
+    // RoPE + KV store
+    const float2* rope;
+    int hd;
+    float* kc;             // this layer's K cache [pos][kvdim]
+    float* vc;             // this layer's V cache
+    int kvdim;
+    // logits
+    float softcap;
+    unsigned long long* amax_key;
+    unsigned int* done;
+    StepParams* params_rw;
+    int* tokens_out;       // tokens_out[nstep] = greedy token (when nstep < tokens_cap)
+    int tokens_cap;
+};
+
+bool gemv_fusable_type(int t);
+bool gemv_fusable_cols(int64_t cols);
+// Fills G, S, rpw and the segments' wg_begin; returns the grid size.
+int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_threads, size_t* lds_bytes);
+hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st);
+
+}  // namespace fllm

@@ -5,94 +5,16 @@
 // reference's operation order (the .NET JIT does not contract either).
 #include "kernels.hpp"
 
+#include "deq.hpp"
+#include "gemv.hpp"
+
 #include <math.h>
 
 namespace fllm {
 
-// =====================================================================================
-// Byte access helpers
-// =====================================================================================
-__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
-__device__ __forceinline__ uint32_t ld_u32b(const uint8_t* p) {
-    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
-}
 // Hardware binary16 -> binary32 conversion (exact for every finite input).
 __device__ __forceinline__ float h2f(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-}
-__device__ __forceinline__ uint32_t alignb(uint32_t hi, uint32_t lo, uint32_t bytes) {
-    return __builtin_amdgcn_alignbyte(hi, lo, bytes);
-}
-__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
-}
-
-// =====================================================================================
-// Exact element dequantization (Dequantizer.cs:68-456), one element at a time.
-// Used by fllm_dequantize, the embedding lookup, norm/bias uploads and the generic GEMV.
-// =====================================================================================
-__device__ float deq_elem(int type, const uint8_t* w, int64_t e) {
-    switch (type) {
-        case FLLM_TYPE_F32: return bits_f32(ld_u32b(w + e * 4));
-        case FLLM_TYPE_F16: return half_exact(ld_u16(w + e * 2));
-        case FLLM_TYPE_BF16: return bf16_exact(ld_u16(w + e * 2));
-        case FLLM_TYPE_Q4_0: {  // Dequantizer.cs:172-184
-            const uint8_t* p = w + (e >> 5) * 18;
-            int j = (int)(e & 31);
-            float d = half_exact(ld_u16(p));
-            uint32_t qs = p[2 + (j & 15)];
-            int q = j < 16 ? (int)(qs & 0x0F) : (int)(qs >> 4);
-            return (float)(q - 8) * d;
-        }
-        case FLLM_TYPE_Q8_0: {  // Dequantizer.cs:220-229
-            const uint8_t* p = w + (e >> 5) * 34;
-            float d = half_exact(ld_u16(p));
-            return (float)(int8_t)p[2 + (e & 31)] * d;
-        }
-        case FLLM_TYPE_Q4_K: {  // Dequantizer.cs:268-292
-            const uint8_t* p = w + (e >> 8) * 144;
-            int i = (int)(e & 255), g = i >> 5, ii = i & 31;
-            float d = half_exact(ld_u16(p)), dmin = half_exact(ld_u16(p + 2));
-            int sc, mn;
-            kscale_min(p + 4, g, sc, mn);
-            float dg = d * (float)sc;
-            float mg = dmin * (float)mn;
-            uint32_t packed = p[16 + g * 16 + (ii >> 1)];
-            int q = (ii & 1) == 0 ? (int)(packed & 0x0F) : (int)(packed >> 4);
-            return dg * (float)q - mg;
-        }
-        case FLLM_TYPE_Q5_K: {  // Dequantizer.cs:333-366
-            const uint8_t* p = w + (e >> 8) * 176;
-            int t = (int)(e & 255), g = t >> 5;
-            float d = half_exact(ld_u16(p)), dmin = half_exact(ld_u16(p + 2));
-            int sc, mn;
-            kscale_min(p + 4, g, sc, mn);
-            float dg = d * (float)sc;
-            float mg = dmin * (float)mn;
-            uint32_t pl = p[48 + (t >> 1)];
-            int lo = (t & 1) == 0 ? (int)(pl & 0x0F) : (int)(pl >> 4);
-            int hi = (p[16 + (t >> 3)] >> (t & 7)) & 1;
-            int q = (hi << 4) | lo;
-            return dg * (float)q - mg;
-        }
-        case FLLM_TYPE_Q6_K: {  // Dequantizer.cs:395-416
-            const uint8_t* p = w + (e >> 8) * 210;
-            int i = (int)(e & 255);
-            uint32_t qlb = p[i >> 1];
-            int low = (i & 1) == 0 ? (int)(qlb & 0x0F) : (int)(qlb >> 4);
-            int high = (p[128 + (i >> 2)] >> ((i & 3) * 2)) & 3;
-            int q = ((high << 4) | low) - 32;
-            int scale = (int8_t)p[192 + (i >> 4)];
-            float d = half_exact(ld_u16(p + 208));
-            return d * (float)scale * (float)q;
-        }
-        case FLLM_TYPE_Q8_K: {  // Dequantizer.cs:444-455
-            const uint8_t* p = w + (e >> 8) * 292;
-            float d = bits_f32(ld_u32b(p));
-            return (float)(int8_t)p[4 + (e & 255)] * d;
-        }
-        default: return 0.0f;
-    }
 }
 
 __global__ void k_dequant(int type, const uint8_t* __restrict__ src, int64_t n, float* __restrict__ dst) {
@@ -106,309 +28,6 @@ hipError_t launch_dequant(int type, const uint8_t* src, int64_t nelem, float* ds
     if (blocks > 65536) blocks = 65536;
     k_dequant<<<(unsigned)blocks, 256, 0, st>>>(type, src, nelem, dst);
     return hipGetLastError();
-}
-
-// =====================================================================================
-// Activation quantization for the int8 dot-product GEMV.
-// A group of 32 floats v is written as s = amax/127 and integers X_i = rint(v_i*127/amax*2^16)
-// split into three signed base-256 digits (X = b2*65536 + b1*256 + b0), so that
-// sum_i q_i v_i = s * (D2 + D1/256 + D0/65536) with D_k = sum_i q_i b_k,i computed exactly by
-// v_dot4_i32_i8. The representation error is at most s*2^-17 per element (about 2^-24 of the
-// group's largest magnitude), i.e. float32 resolution. Digits are stored in the element order of
-// the 4-bit formats: dword k (k<4) holds elements 8k+0,2,4,6 and dword 4+k holds 8k+1,3,5,7.
-// =====================================================================================
-__device__ void quantize_group(const float* v, uint4* parts, float4* stats) {
-    float amax = 0.0f, s16a = 0.0f, s16b = 0.0f;
-    for (int i = 0; i < 16; i++) { s16a += v[i]; amax = fmaxf(amax, fabsf(v[i])); }
-    for (int i = 16; i < 32; i++) { s16b += v[i]; amax = fmaxf(amax, fabsf(v[i])); }
-    float s = 0.0f, inv = 0.0f;
-    if (amax > 0.0f) { s = amax / 127.0f; inv = 127.0f / amax; }
-    uint32_t P[24];
-    for (int i = 0; i < 24; i++) P[i] = 0;
-    for (int i = 0; i < 32; i++) {
-        int X = (int)rintf(v[i] * inv * 65536.0f);
-        int b0 = (int)(int8_t)(X & 0xFF);
-        int X1 = (X - b0) >> 8;
-        int b1 = (int)(int8_t)(X1 & 0xFF);
-        int b2 = (X1 - b1) >> 8;
-        int k = i >> 3, j = i & 7;
-        int dw = ((j & 1) ? 4 : 0) + k;
-        int sh = (j >> 1) * 8;
-        P[dw] |= (uint32_t)(b2 & 0xFF) << sh;
-        P[8 + dw] |= (uint32_t)(b1 & 0xFF) << sh;
-        P[16 + dw] |= (uint32_t)(b0 & 0xFF) << sh;
-    }
-    for (int i = 0; i < 6; i++) parts[i] = make_uint4(P[4 * i], P[4 * i + 1], P[4 * i + 2], P[4 * i + 3]);
-    *stats = make_float4(s, s16a + s16b, s16a, s16b);
-}
-
-__global__ void k_quantize(const float* __restrict__ x, int64_t groups, uint4* parts, float4* stats) {
-    int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= groups) return;
-    float v[32];
-    for (int i = 0; i < 32; i++) v[i] = x[g * 32 + i];
-    quantize_group(v, parts + g * 6, stats + g);
-}
-
-hipError_t launch_quantize(const float* x, int64_t n, XQ xq, hipStream_t st) {
-    int64_t groups = n / 32;
-    if (groups <= 0) return hipSuccess;
-    k_quantize<<<(unsigned)((groups + 127) / 128), 128, 0, st>>>(x, groups, xq.parts, xq.stats);
-    return hipGetLastError();
-}
-
-// =====================================================================================
-// Fused dequant-GEMV, int8 dot-product path.
-// One lane owns one 32-element group column j of the row (its activation digits stay in
-// 24 VGPRs for the whole kernel); a wave covers a K-slice of S <= 64 group columns; a
-// workgroup has one wave per K-slice and walks rows_per_wg rows in steps of 8, so each
-// lane has 8 independent block loads in flight. Row sums are reduced across lanes with a
-// transposing butterfly (8 rows per 34 lane operations) and across K-slices through LDS in a
-// fixed order, so results are deterministic.
-// =====================================================================================
-
-// Q4_K group: Dequantizer.cs:268-292 as dg * sum(q x) - mg * sum(x).
-__device__ __forceinline__ float gdot_q4k(const uint8_t* __restrict__ W, int64_t gi, const uint32_t* xp, float4 xs) {
-    const uint8_t* blk = W + (gi >> 3) * 144;
-    int g = (int)(gi & 7);
-    uint4 hdr = *(const uint4*)blk;
-    uint4 qs = *(const uint4*)(blk + 16 + g * 16);
-    float d = h2f(hdr.x & 0xFFFFu), dmin = h2f(hdr.x >> 16);
-    int sh = (g & 3) * 8;
-    uint32_t a = (hdr.y >> sh) & 0xFF, b = (hdr.z >> sh) & 0xFF, c = (hdr.w >> sh) & 0xFF;
-    int sc, mn;
-    if (g < 4) { sc = (int)(a & 63); mn = (int)(b & 63); }
-    else { sc = (int)((c & 15) | ((a >> 6) << 4)); mn = (int)((c >> 4) | ((b >> 6) << 4)); }
-    float dg = d * (float)sc, mg = dmin * (float)mn;
-    uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
-    int D2 = 0, D1 = 0, D0 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
-        D2 = sdot4(lo, xp[k], D2); D2 = sdot4(hi, xp[4 + k], D2);
-        D1 = sdot4(lo, xp[8 + k], D1); D1 = sdot4(hi, xp[12 + k], D1);
-        D0 = sdot4(lo, xp[16 + k], D0); D0 = sdot4(hi, xp[20 + k], D0);
-    }
-    float t = (float)D2 + (float)D1 * 0.00390625f + (float)D0 * 1.52587890625e-05f;
-    return dg * (xs.x * t) - mg * xs.y;
-}
-
-// Q5_K group: Dequantizer.cs:333-366; high bit of element t is bit t of qh dword g.
-__device__ __forceinline__ float gdot_q5k(const uint8_t* __restrict__ W, int64_t gi, const uint32_t* xp, float4 xs) {
-    const uint8_t* blk = W + (gi >> 3) * 176;
-    int g = (int)(gi & 7);
-    uint4 hdr = *(const uint4*)blk;
-    uint32_t qh = *(const uint32_t*)(blk + 16 + g * 4);
-    uint4 qs = *(const uint4*)(blk + 48 + g * 16);
-    float d = h2f(hdr.x & 0xFFFFu), dmin = h2f(hdr.x >> 16);
-    int sh = (g & 3) * 8;
-    uint32_t a = (hdr.y >> sh) & 0xFF, b = (hdr.z >> sh) & 0xFF, c = (hdr.w >> sh) & 0xFF;
-    int sc, mn;
-    if (g < 4) { sc = (int)(a & 63); mn = (int)(b & 63); }
-    else { sc = (int)((c & 15) | ((a >> 6) << 4)); mn = (int)((c >> 4) | ((b >> 6) << 4)); }
-    float dg = d * (float)sc, mg = dmin * (float)mn;
-    uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
-    int D2 = 0, D1 = 0, D0 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t bk = (qh >> (8 * k)) & 0xFFu;
-        uint32_t lo = (q[k] & 0x0F0F0F0Fu) | (((bk & 0x55u) * 0x410410u) & 0x10101010u);
-        uint32_t hi = ((q[k] >> 4) & 0x0F0F0F0Fu) | ((((bk >> 1) & 0x55u) * 0x410410u) & 0x10101010u);
-        D2 = sdot4(lo, xp[k], D2); D2 = sdot4(hi, xp[4 + k], D2);
-        D1 = sdot4(lo, xp[8 + k], D1); D1 = sdot4(hi, xp[12 + k], D1);
-        D0 = sdot4(lo, xp[16 + k], D0); D0 = sdot4(hi, xp[20 + k], D0);
-    }
-    float t = (float)D2 + (float)D1 * 0.00390625f + (float)D0 * 1.52587890625e-05f;
-    return dg * (xs.x * t) - mg * xs.y;
-}
-
-// Spread the 2-bit fields held in nibbles 0..3 of e into bytes 0..3.
-__device__ __forceinline__ uint32_t spread4(uint32_t e) {
-    e = (e | (e << 8)) & 0x00FF00FFu;
-    return (e | (e << 4)) & 0x0F0F0F0Fu;
-}
-
-// Q6_K 32-element chunk c of a block: Dequantizer.cs:395-416 as
-// (d*sc)*(sum(q6 x) - 32 sum(x)) per 16-element scale group. Blocks are 210 bytes, so the
-// block start is only 2-byte aligned: dwords are loaded from the 4-byte-aligned address
-// below it and re-aligned with v_alignbyte.
-__device__ __forceinline__ float gdot_q6k(const uint8_t* __restrict__ W, int64_t gi, const uint32_t* xp, float4 xs) {
-    const uint8_t* blk = W + (gi >> 3) * 210;
-    int c = (int)(gi & 7);
-    uint32_t mis = (uint32_t)((uintptr_t)blk & 3u);
-    const uint32_t* b4 = (const uint32_t*)(blk - mis);
-    uint32_t l0 = b4[4 * c], l1 = b4[4 * c + 1], l2 = b4[4 * c + 2], l3 = b4[4 * c + 3], l4 = b4[4 * c + 4];
-    uint32_t L[4] = {alignb(l1, l0, mis), alignb(l2, l1, mis), alignb(l3, l2, mis), alignb(l4, l3, mis)};
-    uint32_t h0 = b4[32 + 2 * c], h1 = b4[33 + 2 * c], h2 = b4[34 + 2 * c];
-    uint32_t H[2] = {alignb(h1, h0, mis), alignb(h2, h1, mis)};
-    uint32_t so = 192u + 2u * (uint32_t)c + mis;
-    uint32_t sdw = b4[so >> 2];
-    uint32_t ssh = (so & 3u) * 8u;
-    int sca = (int)(int8_t)((sdw >> ssh) & 0xFFu);
-    int scb = (int)(int8_t)((sdw >> (ssh + 8u)) & 0xFFu);
-    float d = h2f((b4[52] >> (8u * mis)) & 0xFFFFu);
-    int A2 = 0, A1 = 0, A0 = 0, B2 = 0, B1 = 0, B0 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t hk = (H[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-        uint32_t lo = (L[k] & 0x0F0F0F0Fu) | (spread4(hk & 0x3333u) << 4);
-        uint32_t hi = ((L[k] >> 4) & 0x0F0F0F0Fu) | (spread4((hk >> 2) & 0x3333u) << 4);
-        if (k < 2) {
-            A2 = sdot4(lo, xp[k], A2); A2 = sdot4(hi, xp[4 + k], A2);
-            A1 = sdot4(lo, xp[8 + k], A1); A1 = sdot4(hi, xp[12 + k], A1);
-            A0 = sdot4(lo, xp[16 + k], A0); A0 = sdot4(hi, xp[20 + k], A0);
-        } else {
-            B2 = sdot4(lo, xp[k], B2); B2 = sdot4(hi, xp[4 + k], B2);
-            B1 = sdot4(lo, xp[8 + k], B1); B1 = sdot4(hi, xp[12 + k], B1);
-            B0 = sdot4(lo, xp[16 + k], B0); B0 = sdot4(hi, xp[20 + k], B0);
-        }
-    }
-    float ta = (float)A2 + (float)A1 * 0.00390625f + (float)A0 * 1.52587890625e-05f;
-    float tb = (float)B2 + (float)B1 * 0.00390625f + (float)B0 * 1.52587890625e-05f;
-    float ra = xs.x * ta - 32.0f * xs.z;
-    float rb = xs.x * tb - 32.0f * xs.w;
-    return (d * (float)sca) * ra + (d * (float)scb) * rb;
-}
-
-// Q8_0 block (34 bytes, 2-byte aligned): Dequantizer.cs:220-229 as d * sum(q x).
-__device__ __forceinline__ float gdot_q8_0(const uint8_t* __restrict__ W, int64_t gi, const uint32_t* xp, float4 xs) {
-    const uint8_t* blk = W + gi * 34;
-    uint32_t mis = (uint32_t)((uintptr_t)blk & 3u);
-    const uint32_t* b4 = (const uint32_t*)(blk - mis);
-    uint32_t dw[10];
-#pragma unroll
-    for (int i = 0; i < 10; i++) dw[i] = b4[i];
-    float d = h2f((dw[0] >> (8u * mis)) & 0xFFFFu);
-    bool shifted = mis != 0;  // qs start: byte mis+2 -> dword (mis+2)>>2, shift (mis+2)&3
-    uint32_t qv[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) qv[i] = shifted ? dw[i + 1] : alignb(dw[i + 1], dw[i], 2);
-    int D2 = 0, D1 = 0, D0 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t ev = __builtin_amdgcn_perm(qv[2 * k + 1], qv[2 * k], 0x06040200u);
-        uint32_t od = __builtin_amdgcn_perm(qv[2 * k + 1], qv[2 * k], 0x07050301u);
-        D2 = sdot4(ev, xp[k], D2); D2 = sdot4(od, xp[4 + k], D2);
-        D1 = sdot4(ev, xp[8 + k], D1); D1 = sdot4(od, xp[12 + k], D1);
-        D0 = sdot4(ev, xp[16 + k], D0); D0 = sdot4(od, xp[20 + k], D0);
-    }
-    float t = (float)D2 + (float)D1 * 0.00390625f + (float)D0 * 1.52587890625e-05f;
-    return d * (xs.x * t);
-}
-
-// Q4_0 block (18 bytes): Dequantizer.cs:172-184 as d * (sum(q x) - 8 sum(x)); low nibble of
-// byte j is element j, high nibble element j+16.
-__device__ __forceinline__ float gdot_q4_0(const uint8_t* __restrict__ W, int64_t gi, const uint32_t* xp, float4 xs) {
-    const uint8_t* blk = W + gi * 18;
-    uint32_t mis = (uint32_t)((uintptr_t)blk & 3u);
-    const uint32_t* b4 = (const uint32_t*)(blk - mis);
-    uint32_t dw[5];
-#pragma unroll
-    for (int i = 0; i < 5; i++) dw[i] = b4[i];
-    float d = h2f((dw[0] >> (8u * mis)) & 0xFFFFu);
-    bool shifted = mis != 0;
-    uint32_t qv[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) qv[i] = shifted ? dw[i + 1] : alignb(dw[i + 1], dw[i], 2);
-    uint32_t nib[8];
-#pragma unroll
-    for (int i = 0; i < 4; i++) { nib[i] = qv[i] & 0x0F0F0F0Fu; nib[4 + i] = (qv[i] >> 4) & 0x0F0F0F0Fu; }
-    int D2 = 0, D1 = 0, D0 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t ev = __builtin_amdgcn_perm(nib[2 * k + 1], nib[2 * k], 0x06040200u);
-        uint32_t od = __builtin_amdgcn_perm(nib[2 * k + 1], nib[2 * k], 0x07050301u);
-        D2 = sdot4(ev, xp[k], D2); D2 = sdot4(od, xp[4 + k], D2);
-        D1 = sdot4(ev, xp[8 + k], D1); D1 = sdot4(od, xp[12 + k], D1);
-        D0 = sdot4(ev, xp[16 + k], D0); D0 = sdot4(od, xp[20 + k], D0);
-    }
-    float t = (float)D2 + (float)D1 * 0.00390625f + (float)D0 * 1.52587890625e-05f;
-    return d * (xs.x * t - 8.0f * xs.y);
-}
-
-template <int T>
-__device__ __forceinline__ float gdot(const uint8_t* __restrict__ W, int64_t gi, const uint32_t* xp, float4 xs) {
-    if constexpr (T == FLLM_TYPE_Q4_K) return gdot_q4k(W, gi, xp, xs);
-    else if constexpr (T == FLLM_TYPE_Q5_K) return gdot_q5k(W, gi, xp, xs);
-    else if constexpr (T == FLLM_TYPE_Q6_K) return gdot_q6k(W, gi, xp, xs);
-    else if constexpr (T == FLLM_TYPE_Q8_0) return gdot_q8_0(W, gi, xp, xs);
-    else return gdot_q4_0(W, gi, xp, xs);
-}
-
-// Sum 8 per-lane values over the 64 lanes of a wave; lane l ends with the total of
-// row ((l>>5)&1)*4 + ((l>>4)&1)*2 + ((l>>3)&1).
-__device__ __forceinline__ float transpose_reduce8(const float* acc, int lane) {
-    float v[4], w[2];
-    bool b = (lane & 32) != 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float keep = b ? acc[i + 4] : acc[i];
-        float send = b ? acc[i] : acc[i + 4];
-        v[i] = keep + __shfl_xor(send, 32);
-    }
-    b = (lane & 16) != 0;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        float keep = b ? v[i + 2] : v[i];
-        float send = b ? v[i] : v[i + 2];
-        w[i] = keep + __shfl_xor(send, 16);
-    }
-    b = (lane & 8) != 0;
-    float keep = b ? w[1] : w[0];
-    float send = b ? w[0] : w[1];
-    float u = keep + __shfl_xor(send, 8);
-    u += __shfl_xor(u, 4);
-    u += __shfl_xor(u, 2);
-    u += __shfl_xor(u, 1);
-    return u;
-}
-
-template <int T>
-__global__ __launch_bounds__(1024) void k_gemv_q(const uint8_t* __restrict__ W, int rows, int G, int S,
-                                                  int rows_per_wg, const uint4* __restrict__ xq,
-                                                  const float4* __restrict__ xs, float* y,
-                                                  const float* residual) {
-    extern __shared__ float part[];  // [nslice][rows_per_wg]
-    int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int nslice = blockDim.x >> 6;
-    int j = wave * S + lane;
-    bool active = lane < S && j < G;
-    uint32_t xp[24];
-    float4 st = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (active) {
-#pragma unroll
-        for (int i = 0; i < 6; i++) {
-            uint4 u = xq[(int64_t)j * 6 + i];
-            xp[4 * i] = u.x; xp[4 * i + 1] = u.y; xp[4 * i + 2] = u.z; xp[4 * i + 3] = u.w;
-        }
-        st = xs[j];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 24; i++) xp[i] = 0;
-    }
-    int r0 = blockIdx.x * rows_per_wg;
-    for (int rb = 0; rb < rows_per_wg; rb += 8) {
-        float acc[8];
-#pragma unroll
-        for (int rr = 0; rr < 8; rr++) {
-            int r = r0 + rb + rr;
-            acc[rr] = (active && r < rows) ? gdot<T>(W, (int64_t)r * G + j, xp, st) : 0.0f;
-        }
-        float tot = transpose_reduce8(acc, lane);
-        if ((lane & 7) == 0) {
-            int rr = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
-            part[wave * rows_per_wg + rb + rr] = tot;
-        }
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < rows_per_wg; t += blockDim.x) {
-        int r = r0 + t;
-        if (r < rows) {
-            float s = 0.0f;
-            for (int sl = 0; sl < nslice; sl++) s += part[sl * rows_per_wg + t];
-            y[r] = residual ? residual[r] + s : s;
-        }
-    }
 }
 
 // =====================================================================================
@@ -476,40 +95,23 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
     if (lane == 0) y[row] = residual ? residual[row] + acc : acc;
 }
 
-hipError_t launch_gemv(const WMat& m, const float* xf, const XQ& xq, float* y, const float* residual,
-                       hipStream_t st) {
+hipError_t launch_gemv(const WMat& m, const float* xf, float* y, const float* residual, int n_cu, hipStream_t st) {
     int t = m.type;
-    // the int8 path holds one 32-element group column per lane and at most 16 waves per
-    // workgroup, so it covers rows of up to 1024 groups (32768 elements)
-    bool qpath = (t == FLLM_TYPE_Q4_K || t == FLLM_TYPE_Q5_K || t == FLLM_TYPE_Q6_K || t == FLLM_TYPE_Q8_0 ||
-                  t == FLLM_TYPE_Q4_0) &&
-                 (m.cols % 32 == 0) && m.cols <= 32768 && xq.parts != nullptr;
-    if (qpath) {
-        int G = (int)(m.cols / 32);
-        int nslice = (G + 63) / 64;
-        int S = (G + nslice - 1) / nslice;
-        int rows_per_wg = m.rows >= 4096 ? 16 : 8;
-        int grid = (int)((m.rows + rows_per_wg - 1) / rows_per_wg);
-        size_t lds = sizeof(float) * (size_t)nslice * rows_per_wg;
-        dim3 blk(64 * nslice);
-        switch (t) {
-            case FLLM_TYPE_Q4_K:
-                k_gemv_q<FLLM_TYPE_Q4_K><<<grid, blk, lds, st>>>(m.w, (int)m.rows, G, S, rows_per_wg, xq.parts, xq.stats, y, residual);
-                break;
-            case FLLM_TYPE_Q5_K:
-                k_gemv_q<FLLM_TYPE_Q5_K><<<grid, blk, lds, st>>>(m.w, (int)m.rows, G, S, rows_per_wg, xq.parts, xq.stats, y, residual);
-                break;
-            case FLLM_TYPE_Q6_K:
-                k_gemv_q<FLLM_TYPE_Q6_K><<<grid, blk, lds, st>>>(m.w, (int)m.rows, G, S, rows_per_wg, xq.parts, xq.stats, y, residual);
-                break;
-            case FLLM_TYPE_Q8_0:
-                k_gemv_q<FLLM_TYPE_Q8_0><<<grid, blk, lds, st>>>(m.w, (int)m.rows, G, S, rows_per_wg, xq.parts, xq.stats, y, residual);
-                break;
-            default:
-                k_gemv_q<FLLM_TYPE_Q4_0><<<grid, blk, lds, st>>>(m.w, (int)m.rows, G, S, rows_per_wg, xq.parts, xq.stats, y, residual);
-                break;
-        }
-        return hipGetLastError();
+    if (gemv_fusable_type(t) && gemv_fusable_cols(m.cols)) {
+        GemvArgs a{};
+        a.nseg = 1;
+        a.seg[0].w = m.w;
+        a.seg[0].type = t;
+        a.seg[0].rows = (int)m.rows;
+        a.seg[0].epi = residual ? EPI_RESID : EPI_STORE;
+        a.seg[0].out = y;
+        a.seg[0].resid = residual;
+        a.xin = XIN_F32;
+        a.x = xf;
+        int threads;
+        size_t lds;
+        int grid = gemv_plan(a, m.cols, n_cu, 0, &threads, &lds);
+        return launch_gemv_fused(a, grid, threads, lds, st);
     }
     unsigned grid = (unsigned)((m.rows + 3) / 4);
     if (t == FLLM_TYPE_F32 && m.cols % 4 == 0)
@@ -531,6 +133,7 @@ __global__ void k_set_params(StepParams* p, int token, int pos, int cur_len) {
     p->pos = pos;
     p->cur_len = cur_len;
     p->argmax = -1;
+    p->nstep = 0;
 }
 
 hipError_t launch_set_params(StepParams* p, int token, int pos, int cur_len, hipStream_t st) {
@@ -561,35 +164,22 @@ __device__ float block_sum(float v, float* red) {
     return t;
 }
 
-// RmsNorm (TensorOperations.cs:42-54) or GemmaRmsNorm (TensorOperations.cs:90-107), then the
-// quantized copy of the normed vector for the next GEMV.
-__global__ __launch_bounds__(1024) void k_rmsnorm_q(const float* __restrict__ x, const float* __restrict__ w, int n,
-                                                     float eps, int kind, float* xn, uint4* parts, float4* stats) {
-    extern __shared__ float sh[];  // n + 16
-    float* red = sh + n;
+// RmsNorm (TensorOperations.cs:42-54) or GemmaRmsNorm (TensorOperations.cs:90-107) into xn.
+__global__ __launch_bounds__(1024) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ w, int n,
+                                                   float eps, int kind, float* xn) {
+    __shared__ float red[16];
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = x[i];
-        sh[i] = v;
-        ss = fmaf(v, v, ss);
-    }
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
     float tot = block_sum(ss, red);
     float rms = 1.0f / sqrtf(tot / (float)n + eps);
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float t = sh[i] * rms;
-        float o = kind ? t * (w[i] + 1.0f) : t * w[i];
-        xn[i] = o;
-        sh[i] = o;
+        float t = x[i] * rms;
+        xn[i] = kind ? t * (w[i] + 1.0f) : t * w[i];
     }
-    __syncthreads();
-    if (parts)
-        for (int g = threadIdx.x; g < n / 32; g += blockDim.x) quantize_group(sh + g * 32, parts + g * 6, stats + g);
 }
 
-hipError_t launch_rmsnorm_q(const float* x, const float* w, int n, float eps, int norm_kind, float* xn, XQ xq,
-                            hipStream_t st) {
-    size_t lds = sizeof(float) * ((size_t)n + 16);
-    k_rmsnorm_q<<<1, 1024, lds, st>>>(x, w, n, eps, norm_kind, xn, (n % 32 == 0) ? xq.parts : nullptr, xq.stats);
+hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, int norm_kind, float* xn, hipStream_t st) {
+    k_rmsnorm<<<1, 1024, 0, st>>>(x, w, n, eps, norm_kind, xn);
     return hipGetLastError();
 }
 
@@ -723,8 +313,7 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
 
 __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ part_o,
                                                        const float* __restrict__ part_ml, int nsplit, int hd,
-                                                       float* out, uint4* parts, float4* stats) {
-    __shared__ float sh[256];
+                                                       float* out) {
     int h = blockIdx.x, d = threadIdx.x;
     float M = -INFINITY;
     for (int s = 0; s < nsplit; s++) {
@@ -740,19 +329,12 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float* __restrict__ 
             if (d < hd) o = fmaf(part_o[((int64_t)h * nsplit + s) * hd + d], wgt, o);
         }
     }
-    float r = o / L;
-    if (d < hd) {
-        out[(int64_t)h * hd + d] = r;
-        sh[d] = r;
-    }
-    __syncthreads();
-    int ng = hd / 32;
-    if (parts && d < ng) quantize_group(sh + d * 32, parts + ((int64_t)h * ng + d) * 6, stats + (int64_t)h * ng + d);
+    if (d < hd) out[(int64_t)h * hd + d] = o / L;
 }
 
 hipError_t launch_attention(const float* q, const float* kcache, const float* vcache, int n_heads, int n_kv,
                             int head_dim, int window, float scale, float softcap, int nsplit, float* part_o,
-                            float* part_ml, float* out, XQ out_q, const StepParams* p, hipStream_t st) {
+                            float* part_ml, float* out, const StepParams* p, hipStream_t st) {
     int group = n_heads / n_kv;
     int chunk_cap = 256;
     size_t lds = sizeof(float) * ((size_t)group * head_dim + (size_t)group * chunk_cap);
@@ -762,8 +344,7 @@ hipError_t launch_attention(const float* q, const float* kcache, const float* vc
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     int bs = head_dim < 64 ? 64 : head_dim;
-    k_attn_combine<<<n_heads, bs, 0, st>>>(part_o, part_ml, nsplit, head_dim, out,
-                                           (head_dim % 32 == 0) ? out_q.parts : nullptr, out_q.stats);
+    k_attn_combine<<<n_heads, bs, 0, st>>>(part_o, part_ml, nsplit, head_dim, out);
     return hipGetLastError();
 }
 
@@ -772,32 +353,23 @@ hipError_t launch_attention(const float* q, const float* kcache, const float* vc
 // (Gemma2ForwardPass.cs:187-199); Silu/Gelu from TensorOperations.cs:57-117.
 // =====================================================================================
 __global__ __launch_bounds__(256) void k_act(const float* __restrict__ g, const float* __restrict__ u, int n,
-                                              int act, float* h, uint4* parts, float4* stats) {
-    __shared__ float sh[256];
+                                              int act, float* h) {
     int i = blockIdx.x * 256 + threadIdx.x;
-    float hv = 0.0f;
-    if (i < n) {
-        float gv = g[i];
-        float a;
-        if (act == 0) {
-            float sig = 1.0f / (1.0f + expf(-gv));
-            a = gv * sig;
-        } else {
-            float inner = 0.7978845608f * (gv + 0.044715f * gv * gv * gv);
-            a = 0.5f * gv * (1.0f + tanhf(inner));
-        }
-        hv = a * u[i];
-        h[i] = hv;
+    if (i >= n) return;
+    float gv = g[i];
+    float a;
+    if (act == 0) {
+        float sig = 1.0f / (1.0f + expf(-gv));
+        a = gv * sig;
+    } else {
+        float inner = 0.7978845608f * (gv + 0.044715f * gv * gv * gv);
+        a = 0.5f * gv * (1.0f + tanhf(inner));
     }
-    sh[threadIdx.x] = hv;
-    __syncthreads();
-    int gidx = blockIdx.x * 8 + threadIdx.x;
-    if (parts && threadIdx.x < 8 && (gidx + 1) * 32 <= n)
-        quantize_group(sh + threadIdx.x * 32, parts + (int64_t)gidx * 6, stats + gidx);
+    h[i] = a * u[i];
 }
 
-hipError_t launch_act(const float* g, const float* u, int n, int act, float* h, XQ hq, hipStream_t st) {
-    k_act<<<(n + 255) / 256, 256, 0, st>>>(g, u, n, act, h, (n % 32 == 0) ? hq.parts : nullptr, hq.stats);
+hipError_t launch_act(const float* g, const float* u, int n, int act, float* h, hipStream_t st) {
+    k_act<<<(n + 255) / 256, 256, 0, st>>>(g, u, n, act, h);
     return hipGetLastError();
 }
 
@@ -844,7 +416,10 @@ __device__ __forceinline__ uint32_t okey(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t n, StepParams* p) {
+// First index of the maximum (IndexOfMax semantics). With tokens_out set, also publishes the
+// token as the next step's input and advances the step parameters (device-side greedy loop).
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t n, StepParams* p, int* tokens_out,
+                                                 int tokens_cap) {
     __shared__ uint32_t sk[16];
     __shared__ int64_t si[16];
     uint32_t bk = 0;
@@ -869,11 +444,18 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
             if (si[w] >= 0 && (idx < 0 || sk[w] > k || (sk[w] == k && si[w] < idx))) { k = sk[w]; idx = si[w]; }
         }
         p->argmax = (int)idx;
+        if (tokens_out) {
+            if (p->nstep >= 0 && p->nstep < tokens_cap) tokens_out[p->nstep] = (int)idx;
+            p->nstep = p->nstep + 1;
+            p->token = (int)idx;
+            p->pos = p->pos + 1;
+            p->cur_len = p->cur_len + 1;
+        }
     }
 }
 
-hipError_t launch_argmax(const float* x, int64_t n, StepParams* p, hipStream_t st) {
-    k_argmax<<<1, 1024, 0, st>>>(x, n, p);
+hipError_t launch_argmax(const float* x, int64_t n, StepParams* p, int* tokens_out, int tokens_cap, hipStream_t st) {
+    k_argmax<<<1, 1024, 0, st>>>(x, n, p, tokens_out, tokens_cap);
     return hipGetLastError();
 }
 

@@ -177,6 +177,14 @@ FLLM_API int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position);
 /* n consecutive Forward calls for tokens[0..n) at positions pos0.. (prefill loop,
  * LlamaLanguageModel.cs:133-137); same results as n fllm_forward calls. */
 FLLM_API int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, int32_t pos0);
+/* The greedy part of LlamaLanguageModel.GenerateAsync's decode loop (LlamaLanguageModel.cs:162-293
+ * with SamplerPipeline Temperature == 0, SamplerPipeline.cs:61-64, no EOS stop): n_steps Forward
+ * calls starting with `token` at `position`, each step's argmax fed to the next step on the device
+ * (no host round trip per token). out_tokens receives the n_steps greedy tokens; the logits of the
+ * last step stay on the device. Same argument contract as fllm_forward; the KV cache must have
+ * room for n_steps positions (FLLM_E_ARG_RANGE otherwise). */
+FLLM_API int32_t fllm_decode_greedy(fllm_seq* s, int32_t token, int32_t position, int32_t n_steps,
+                                    int32_t* out_tokens);
 /* Waits for the sequence's stream. */
 FLLM_API int32_t fllm_seq_sync(fllm_seq* s);
 

@@ -10,7 +10,7 @@ import pytest
 import dotnetfoundryllm_amd as F
 import dotnetfoundryllm_amd._native as N
 import oracle_bind as O
-from dotnetfoundryllm_amd.configs import CONFIGS, desc_of
+from dotnetfoundryllm_amd.configs import CONFIGS, desc_of, synth_bytes, tensor_plan
 from fixtures import REF_TOKENS, reference_fixture, synthetic, upload
 
 pytestmark = pytest.mark.gpu
@@ -287,9 +287,122 @@ def test_profile_mode_reports_kernels(ctx):
         for p in range(3):
             fwd.forward(5, p, kv)
         ents = {e["name"]: e for e in F.profile_entries(kv)}
-        assert ents["gemv_q4_k"]["launches"] == 3 * (desc.n_layers * 5)
-        assert ents["gemv_q6_k"]["launches"] == 3 * (desc.n_layers * 2 + 1)
+        # fused launches: [norm+QKV+RoPE+KV], attention, [Wo+residual], [norm+gate/up+act],
+        # [down+residual] per layer, then [norm+LM head+argmax]
+        for name in ("qkv_rope_kv", "attention", "attn_output", "ffn_gate_up", "ffn_down"):
+            assert ents[name]["launches"] == 3 * desc.n_layers, name
+        assert ents["lm_head_argmax"]["launches"] == 3
         assert all(e["ms"] > 0 for e in ents.values())
     finally:
+        kv.close()
+        m.close()
+
+
+def _oracle_greedy(orc, prompt, n):
+    pos = 0
+    for t in prompt[:-1]:
+        assert orc.forward(int(t), pos) == 0
+        pos += 1
+    nxt, out = int(prompt[-1]), []
+    for _ in range(n):
+        assert orc.forward(nxt, pos) == 0
+        pos += 1
+        lg = orc.logits()
+        nxt = int(O.lib.orc_argmax(O.fp(lg), lg.size))
+        out.append(nxt)
+    return out
+
+
+@pytest.mark.parametrize("name", ["test-llama", "test-qwen2", "test-gemma2", "test-mixed", "test-llama-straddle"])
+@pytest.mark.parametrize("graph", [True, False])
+def test_device_greedy_loop(ctx, name, graph):
+    """fllm_decode_greedy (each step's argmax fed to the next step on the device) produces the
+    tokens of stepwise Forward + greedy sampling, and the oracle's."""
+    cfg, desc, tensors = synthetic(name)
+    m = device_model(ctx, desc, tensors)
+    kv_a, kv_b = F.HipKvCache(m), F.HipKvCache(m)
+    F.set_graph(kv_a, graph)
+    F.set_graph(kv_b, graph)
+    fa, fb = F.HipForwardPass(m), F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors)
+    prompt = F.synth_tokens(cfg["seed"], 7, desc.vocab, 10)
+    n = 20
+    try:
+        fa.prefill(prompt[:-1], 0, kv_a)
+        fb.prefill(prompt[:-1], 0, kv_b)
+        toks = fa.decode_greedy(int(prompt[-1]), len(prompt) - 1, n, kv_a)
+        assert kv_a.current_length == len(prompt) - 1 + n
+        step, nxt, pos = [], int(prompt[-1]), len(prompt) - 1
+        for _ in range(n):
+            fb.forward(nxt, pos, kv_b)
+            nxt = fb.sample_greedy()
+            step.append(nxt)
+            pos += 1
+        assert list(toks) == step
+        # logits of the last step are the same as the stepwise path's
+        assert np.array_equal(fa.logits, fb.logits)
+        assert fa.sample_greedy() == step[-1]
+        assert list(toks) == _oracle_greedy(orc, prompt, n)
+    finally:
+        orc.close()
+        kv_a.close()
+        kv_b.close()
+        m.close()
+
+
+def test_device_greedy_loop_errors(ctx):
+    cfg, desc, tensors = synthetic("test-llama")
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m, 16)
+    fwd = F.HipForwardPass(m)
+    try:
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.decode_greedy(desc.vocab, 0, 4, kv)       # token outside the vocabulary
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.decode_greedy(1, 1, 4, kv)                # position beyond the cached length
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.decode_greedy(1, 0, 17, kv)               # more steps than the cache holds
+        assert kv.current_length == 0
+        assert len(fwd.decode_greedy(1, 0, 16, kv)) == 16
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.forward(1, 16, kv)                        # cache full
+    finally:
+        kv.close()
+        m.close()
+
+
+def test_long_context_windowed_attention(ctx):
+    """Mistral-style window over a 3000-position context with 8 KV heads: the attention splits into
+    47 chunks of 64 positions whose partials are merged by the last chunk; logits, K/V and greedy
+    tokens against the oracle."""
+    from dotnetfoundryllm_amd.configs import _cfg, _types
+    cfg = _cfg("long-mistral", N.ARCH_MISTRAL, 1, 512, 8, 8, 512, 512, 4096, 10000.0,
+               _types(*([N.Q4_K] * 7), N.Q6_K), window=1000, norm_std=0.1, seed=21)
+    desc = desc_of(cfg)
+    tensors = {e[0]: (e, synth_bytes(cfg, e)) for e in tensor_plan(cfg)}
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors)
+    prompt = F.synth_tokens(cfg["seed"], 2, desc.vocab, 3000)
+    try:
+        fwd.prefill(prompt, 0, kv)
+        for pos, t in enumerate(prompt):
+            assert orc.forward(int(t), pos) == 0
+        assert O.normwise_rel_err(fwd.logits, orc.logits()) <= TOL
+        assert O.normwise_rel_err(kv.get_keys(0), orc.kv(0, 0)) <= TOL
+        assert O.normwise_rel_err(kv.get_values(0), orc.kv(0, 1)) <= TOL
+        toks = fwd.decode_greedy(int(prompt[-1]), 3000, 8, kv)
+        ref, pos = [], 3000
+        nxt = int(prompt[-1])
+        for _ in range(8):
+            assert orc.forward(nxt, pos) == 0
+            pos += 1
+            lg = orc.logits()
+            nxt = int(O.lib.orc_argmax(O.fp(lg), lg.size))
+            ref.append(nxt)
+        assert list(toks) == ref
+    finally:
+        orc.close()
         kv.close()
         m.close()
