@@ -115,9 +115,7 @@ struct fllm_seq {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
     float *g = nullptr, *u = nullptr, *h = nullptr, *tmp = nullptr, *logits = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
-    unsigned int* attn_counters = nullptr;
-    unsigned long long* amax_key = nullptr;
-    unsigned int* head_done = nullptr;
+    unsigned long long* head_keys = nullptr;  // per-workgroup argmax keys of the fused LM head
     int* tokens_out = nullptr;
     int *topk_ids = nullptr, *topk_count = nullptr;
     float* topk_vals = nullptr;
@@ -575,13 +573,14 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     s->m = m;
     s->max_seq = max_seq > 0 ? max_seq : d.max_ctx;
     s->nsplit = (s->max_seq + 255) / 256;
-    s->attn_fast = attn_fast_supported(d.head_dim, d.n_heads / d.n_kv_heads);
+    s->attn_fast = attn_fast_supported(d.head_dim, d.n_heads / d.n_kv_heads, s->max_seq);
     s->attn_nc = attn_chunks(d.n_kv_heads, s->max_seq, m->ctx->n_cu > 0 ? m->ctx->n_cu : 256);
     s->attn_lds = attn_lds_bytes(d.head_dim, d.n_heads / d.n_kv_heads, s->attn_nc, s->max_seq);
     s->fused = s->attn_fast && gemv_fusable_cols(d.hidden) && gemv_fusable_cols(m->qdim) && gemv_fusable_cols(d.ffn);
     for (const Layer& Lr : m->layers) {
         const Tensor* ts[] = {&Lr.q, &Lr.k, &Lr.v, &Lr.o, &Lr.gate, &Lr.up, &Lr.down};
         for (const Tensor* t : ts) s->fused = s->fused && gemv_fusable_type(t->type);
+        s->fused = s->fused && Lr.gate.type == Lr.up.type;  // gate and up share one fused launch
     }
     s->head_fused = s->fused && gemv_fusable_type(m->output.type);
     hipError_t e = hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking);
@@ -610,9 +609,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     size_t nparts = (size_t)(s->nsplit > s->attn_nc ? s->nsplit : s->attn_nc);
     ALLOC(s->part_o, (size_t)d.n_heads * nparts * d.head_dim);
     ALLOC(s->part_ml, (size_t)d.n_heads * nparts * 2);
-    ALLOC(s->attn_counters, (size_t)d.n_kv_heads);
-    ALLOC(s->amax_key, 1);
-    ALLOC(s->head_done, 1);
+    ALLOC(s->head_keys, (size_t)d.vocab / 8 + 1);
     ALLOC(s->tokens_out, (size_t)s->max_seq);
     ALLOC(s->topk_ids, (size_t)d.vocab);
     ALLOC(s->topk_vals, (size_t)d.vocab);
@@ -631,9 +628,6 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     }
     e = hipMemcpyAsync(s->rope, tab.data(), sizeof(float2) * tab.size(), hipMemcpyHostToDevice, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->kc, 0, sizeof(float) * kvsz, s->st);
-    if (e == hipSuccess) e = hipMemsetAsync(s->attn_counters, 0, sizeof(unsigned int) * (size_t)d.n_kv_heads, s->st);
-    if (e == hipSuccess) e = hipMemsetAsync(s->amax_key, 0, sizeof(unsigned long long), s->st);
-    if (e == hipSuccess) e = hipMemsetAsync(s->head_done, 0, sizeof(unsigned int), s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->params, 0, sizeof(StepParams), s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, sizeof(float) * kvsz, s->st);
     if (e == hipSuccess) e = hipStreamSynchronize(s->st);
@@ -784,7 +778,7 @@ static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const floa
         a.q = s->q; a.kc = kc; a.vc = vc;
         a.nh = d.n_heads; a.nkv = d.n_kv_heads; a.hd = d.head_dim; a.kvdim = s->m->kvdim;
         a.window = window; a.scale = d.attn_scale; a.softcap = softcap;
-        a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml; a.counters = s->attn_counters;
+        a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml;
         a.out = s->att; a.params = s->params;
         STEP("attention", bytes, launch_attn_decode(a, s->attn_lds, s->st));
     } else {
@@ -836,6 +830,11 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
     float eps = gemma ? 1e-6f : d.norm_eps;
     int nk = gemma ? 1 : 0;
     size_t layer_kv = (size_t)s->max_seq * kvdim;
+    // F32 / F16 / BF16 embedding rows are read by the first projection's prologue; quantized
+    // ones go through the element-wise lookup kernel first
+    int et = m->tok_embd.type;
+    bool emb_fused = et == FLLM_TYPE_F32 || et == FLLM_TYPE_F16 || et == FLLM_TYPE_BF16;
+    if (!emb_fused) STEP("embed", 4.0 * H, launch_embed(m->tok_embd.ptr, et, H, s->params, s->x, s->st));
     for (int l = 0; l < d.n_layers; l++) {
         const Layer& L = m->layers[(size_t)l];
         float* kc = s->kc + (size_t)l * layer_kv;
@@ -846,7 +845,7 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.seg[0] = seg_of(L.q, EPI_Q, s->q, L.bq, nullptr);
             a.seg[1] = seg_of(L.k, EPI_K, nullptr, L.bk, nullptr);
             a.seg[2] = seg_of(L.v, EPI_V, nullptr, L.bv, nullptr);
-            a.xin = l == 0 ? XIN_EMBED_NORM : XIN_NORM;
+            a.xin = (l == 0 && emb_fused) ? XIN_EMBED_NORM : XIN_NORM;
             a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
             a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
             a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
@@ -897,9 +896,13 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
     a.xin = XIN_NORM;
     a.x = s->x; a.norm_w = m->out_norm; a.eps = eps; a.norm_kind = nk;
     a.softcap = (gemma && d.final_softcap > 0.0f) ? d.final_softcap : 0.0f;
-    a.amax_key = s->amax_key; a.done = s->head_done; a.params_rw = s->params; a.params = s->params;
-    a.tokens_out = s->tokens_out; a.tokens_cap = s->max_seq;
-    return fused_step(s, "lm_head_argmax", a, H, (double)m->output.bytes + 4.0 * (2.0 * H + d.vocab));
+    a.wg_keys = s->head_keys; a.params = s->params;
+    int threads;
+    size_t lds;
+    int grid = gemv_plan(a, H, m->ctx->n_cu > 0 ? m->ctx->n_cu : 256, 0, &threads, &lds);
+    STEP("lm_head", (double)m->output.bytes + 4.0 * (2.0 * H + d.vocab), launch_gemv_fused(a, grid, threads, lds, s->st));
+    STEP("argmax", 8.0 * grid, launch_argmax_keys(s->head_keys, grid, s->params, s->tokens_out, s->max_seq, s->st));
+    return hipSuccess;
 }
 
 // The decode step as one kernel per reference op (any tensor type and shape).

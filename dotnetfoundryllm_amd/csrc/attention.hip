@@ -9,8 +9,9 @@
 // the attended range for the whole query group of that kv head, so each K/V row is read from
 // HBM once per group. Lanes split a K/V row into float4 slices (hd/4 lanes per row, 64/(hd/4)
 // rows per wave load, fully coalesced); q for the group stays in registers. Each workgroup
-// writes its unnormalised partial output with the chunk's max and sum; the last workgroup of a
-// kv head to finish (atomic counter, no waiting) merges the partials and writes the output.
+// writes its unnormalised partial output with the chunk's max and sum; a second kernel merges
+// the chunks of every head. (Merging inside the first kernel would need a device-scope release
+// per workgroup, which on a multi-XCD part writes back each XCD's L2.)
 #include "attention.hpp"
 
 #include <math.h>
@@ -23,7 +24,6 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     constexpr int RPL = 64 / LPR;  // rows per wave load
     constexpr int GMAX = ATTN_GROUP_MAX;
     extern __shared__ float sh[];
-    __shared__ int s_last;
     const int kvh = blockIdx.x, c = blockIdx.y;
     const int group = a.nh / a.nkv;
     const int seq = a.params->pos + 1;
@@ -54,6 +54,15 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     const float* vbase = a.vc + (int64_t)kvh * HD + dl * 4;
     const int rstep = 4 * RPL;  // rows covered by one load of the 4 waves
     const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
+
+    // the first V rows of this wave are loaded with the first K rows (one memory round trip for
+    // chunks of up to 4 * rstep positions)
+    float4 vpre[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        int t = wave * RPL + sub + u * rstep;
+        vpre[u] = t < len ? *(const float4*)(vbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 
     // ---- scores --------------------------------------------------------------------------
     for (int base = wave * RPL + sub; base < len; base += 4 * rstep) {
@@ -109,10 +118,12 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     for (int h = 0; h < GMAX; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int base = wave * RPL + sub; base < len; base += 4 * rstep) {
         float4 vr[4];
+        const bool first = base == wave * RPL + sub;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             int t = base + u * rstep;
-            vr[u] = t < len ? *(const float4*)(vbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[u] = first ? vpre[u]
+                          : (t < len ? *(const float4*)(vbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f));
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -152,47 +163,87 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
         a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2] = ml[2 * h];
         a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2 + 1] = ml[2 * h + 1];
     }
+}
 
-    // ---- the last chunk of this kv head to finish merges all chunks ----------------------------
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned prev = atomicAdd(a.counters + kvh, 1u);
-        s_last = (prev == (unsigned)(nchunks - 1)) ? 1 : 0;
+// out[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M) over the chunks of head h. One wave per
+// head: lane k holds chunk k's (m, l) (chunks are at most 256), the weights go through LDS, and
+// every lane then sums its float4 slices of the chunk outputs with all loads of a pass in flight.
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_merge(const AttnArgs a) {
+    __shared__ float wts[256];
+    __shared__ float s_inv;
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int seq = a.params->pos + 1;
+    int ws = seq - a.window;
+    if (ws < 0) ws = 0;
+    const int alen = seq - ws;
+    int ch = (alen + a.nc - 1) / a.nc;
+    ch = (ch + 31) / 32 * 32;
+    const int nchunks = (alen + ch - 1) / ch;
+    const float* pml = a.part_ml + (int64_t)h * a.nc * 2;
+    float mk[4], lk[4];
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int k = lane + 64 * i;
+        mk[i] = k < nchunks ? pml[2 * k] : -INFINITY;
+        lk[i] = k < nchunks ? pml[2 * k + 1] : 0.0f;
+        M = fmaxf(M, mk[i]);
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    float L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int k = lane + 64 * i;
+        float w = k < nchunks ? expf(mk[i] - M) : 0.0f;
+        if (k < 256) wts[k] = w;
+        L = fmaf(lk[i], w, L);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
+    if (lane == 0) s_inv = 1.0f / L;
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int idx = threadIdx.x; idx < group * (HD / 4); idx += blockDim.x) {
-        int h = idx / (HD / 4), d4 = idx % (HD / 4);
-        const float* pml = a.part_ml + (int64_t)(h0 + h) * a.nc * 2;
-        const float* po = a.part_o + (int64_t)(h0 + h) * a.nc * HD + d4 * 4;
-        float M = -INFINITY;
-        for (int k = 0; k < nchunks; k++) M = fmaxf(M, pml[2 * k]);
-        float L = 0.0f;
+    const float inv = s_inv;
+    for (int d4 = lane; d4 < HD / 4; d4 += 64) {
+        const float* po = a.part_o + (int64_t)h * a.nc * HD + d4 * 4;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int k = 0; k < nchunks; k++) {
-            float w = expf(pml[2 * k] - M);
-            L = fmaf(pml[2 * k + 1], w, L);
+        int k = 0;
+        for (; k + 8 <= nchunks; k += 8) {
+            float4 p[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) p[u] = *(const float4*)(po + (int64_t)(k + u) * HD);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                float w = wts[k + u];
+                o.x = fmaf(p[u].x, w, o.x);
+                o.y = fmaf(p[u].y, w, o.y);
+                o.z = fmaf(p[u].z, w, o.z);
+                o.w = fmaf(p[u].w, w, o.w);
+            }
+        }
+        for (; k < nchunks; k++) {
             float4 p = *(const float4*)(po + (int64_t)k * HD);
+            float w = wts[k];
             o.x = fmaf(p.x, w, o.x);
             o.y = fmaf(p.y, w, o.y);
             o.z = fmaf(p.z, w, o.z);
             o.w = fmaf(p.w, w, o.w);
         }
-        float inv = 1.0f / L;
-        *(float4*)(a.out + (int64_t)(h0 + h) * HD + d4 * 4) = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        *(float4*)(a.out + (int64_t)h * HD + d4 * 4) = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
     }
-    if (threadIdx.x == 0) atomicExch(a.counters + kvh, 0u);
 }
 
-bool attn_fast_supported(int head_dim, int group) {
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && group >= 1 && group <= ATTN_GROUP_MAX;
+bool attn_fast_supported(int head_dim, int group, int max_seq) {
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && group >= 1 && group <= ATTN_GROUP_MAX &&
+           max_seq <= 256 * ATTN_MAX_CHUNKS;
 }
 
 int attn_chunks(int n_kv, int max_seq, int n_cu) {
-    // enough chunks to give every CU a workgroup at long context, chunks of at most 256 positions
+    // enough chunks to give every CU a workgroup at long context, chunks of at most 256
+    // positions, and at most 256 chunks (the merge kernel holds one chunk per lane slot)
     int target = (2 * n_cu + n_kv - 1) / n_kv;
+    if (target > ATTN_MAX_CHUNKS) target = ATTN_MAX_CHUNKS;
     int by_min = (max_seq + 31) / 32;
     int by_max = (max_seq + 255) / 256;
     int nc = target < by_min ? target : by_min;
@@ -213,6 +264,13 @@ hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st) {
         case 64: k_attn_decode<64><<<grid, 256, lds, st>>>(a); break;
         case 128: k_attn_decode<128><<<grid, 256, lds, st>>>(a); break;
         default: k_attn_decode<256><<<grid, 256, lds, st>>>(a); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (a.hd) {
+        case 64: k_attn_merge<64><<<a.nh, 64, 0, st>>>(a); break;
+        case 128: k_attn_merge<128><<<a.nh, 64, 0, st>>>(a); break;
+        default: k_attn_merge<256><<<a.nh, 64, 0, st>>>(a); break;
     }
     return hipGetLastError();
 }

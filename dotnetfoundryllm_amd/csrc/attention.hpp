@@ -5,7 +5,8 @@
 
 namespace fllm {
 
-constexpr int ATTN_GROUP_MAX = 8;  // query heads per kv head handled by the fast kernel
+constexpr int ATTN_GROUP_MAX = 8;     // query heads per kv head handled by the fast kernel
+constexpr int ATTN_MAX_CHUNKS = 256;  // position chunks per kv head (chunks hold at most 256 positions)
 
 struct AttnArgs {
     const float* q;        // [nh][hd]
@@ -17,12 +18,11 @@ struct AttnArgs {
     int nc;                // chunks per kv head (grid.y)
     float* part_o;         // [nh][nc][hd]
     float* part_ml;        // [nh][nc][2]
-    unsigned int* counters;  // [nkv], zero between launches
     float* out;            // [nh][hd]
     const StepParams* params;
 };
 
-bool attn_fast_supported(int head_dim, int group);
+bool attn_fast_supported(int head_dim, int group, int max_seq);
 int attn_chunks(int n_kv, int max_seq, int n_cu);
 size_t attn_lds_bytes(int head_dim, int group, int nc, int max_seq);
 hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st);

@@ -9,8 +9,8 @@
 //             (LlamaForwardPass.cs:119,124), RoPE of q / k (TensorOperations.cs:250-260) with the
 //             K/V cache store (KvCache.cs:86-89), SiLU/GELU gating of gate and up
 //             (LlamaForwardPass.cs:217-232, Gemma2ForwardPass.cs:187-199), or LM-head logits with
-//             the final softcap (Gemma2ForwardPass.cs:101-104) and the greedy argmax
-//             (TensorOperations.cs:187-195).
+//             the final softcap (Gemma2ForwardPass.cs:101-104) and each workgroup's share of
+//             the greedy argmax (TensorOperations.cs:187-195).
 //
 // Work split. A row is G = cols/32 groups of 32 elements. A workgroup has nslice waves; lane
 // `lane` of wave `w` owns group column j = w*S + lane for every row it visits, so the
@@ -26,8 +26,6 @@
 // the integer weights q. The representation error is at most 2^-17 * s per element (about 2^-24
 // of the group's largest magnitude), float32 resolution.
 #include "gemv.hpp"
-
-#include "deq.hpp"
 
 #include <math.h>
 
@@ -55,8 +53,9 @@ __device__ __forceinline__ uint32_t fkey(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// 32 consecutive elements [e0, e0+32) of a row of any supported type, exactly dequantized
-// (Dequantizer.cs:68-456); F32 / F16 / BF16 rows use 16-byte loads (e0 is a multiple of 32).
+// 32 consecutive elements [e0, e0+32) of an F32 / F16 / BF16 row, exactly widened
+// (Dequantizer.cs:68-137), with 16-byte loads (e0 is a multiple of 32). Quantized embedding
+// rows are produced by a separate lookup kernel before the first projection.
 __device__ __forceinline__ void deq32(int type, const uint8_t* __restrict__ w, int64_t e0, float* v) {
     if (type == FLLM_TYPE_F32) {
         const float4* p = (const float4*)(w + e0 * 4);
@@ -65,7 +64,8 @@ __device__ __forceinline__ void deq32(int type, const uint8_t* __restrict__ w, i
             float4 t = p[i];
             v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
         }
-    } else if (type == FLLM_TYPE_BF16 || type == FLLM_TYPE_F16) {
+    } else {
+        const bool bf = type == FLLM_TYPE_BF16;
         const uint4* p = (const uint4*)(w + e0 * 2);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -73,13 +73,10 @@ __device__ __forceinline__ void deq32(int type, const uint8_t* __restrict__ w, i
             uint32_t d[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                v[8 * i + 2 * k] = type == FLLM_TYPE_BF16 ? bf16_exact(d[k] & 0xFFFFu) : half_exact(d[k] & 0xFFFFu);
-                v[8 * i + 2 * k + 1] = type == FLLM_TYPE_BF16 ? bf16_exact(d[k] >> 16) : half_exact(d[k] >> 16);
+                v[8 * i + 2 * k] = bf ? bf16_exact(d[k] & 0xFFFFu) : half_exact(d[k] & 0xFFFFu);
+                v[8 * i + 2 * k + 1] = bf ? bf16_exact(d[k] >> 16) : half_exact(d[k] >> 16);
             }
         }
-    } else {
-#pragma unroll 4
-        for (int i = 0; i < 32; i++) v[i] = deq_elem_q(type, w, e0 + i);
     }
 }
 
@@ -118,20 +115,44 @@ __device__ __forceinline__ float digits_total(int D2, int D1, int D0) {
     return (float)D2 + (float)D1 * 0.00390625f + (float)D0 * 1.52587890625e-05f;
 }
 
-// ---- per-type raw loads and group dots ---------------------------------------------------
-// Raw words of one 32-element group (group index gi of the flat stream) are loaded by
-// ld<T>() into a Raw<T>, then dotted by dot<T>(). Splitting the two lets a lane issue the
-// loads of 8 rows before it waits on any of them.
+// ---- per-type block geometry, raw reads and group dots ------------------------------------
+// The raw words of one 32-element group are read from the LDS copy of its block by ld() into a
+// Raw<T>, then dotted by dot(). LDS pointers carry address space 3 so the reads are ds_read.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+typedef __attribute__((address_space(3))) const u32x4 lds_v4;
+typedef __attribute__((address_space(3))) u32x4 lds_v4w;
+__device__ __forceinline__ uint4 lds_ld16(lds_u8* p) {
+    u32x4 t = *(lds_v4*)p;
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+// BB block bytes, GPB 32-element groups per block, N16 16-byte chunks that cover the blocks of a
+// wave's slice of one row (at most 64 groups, plus 15 bytes of alignment), CPL chunks per lane.
+template <int T> struct Geo;
+template <> struct Geo<FLLM_TYPE_Q4_K> { static constexpr int BB = 144, GPB = 8; };
+template <> struct Geo<FLLM_TYPE_Q5_K> { static constexpr int BB = 176, GPB = 8; };
+template <> struct Geo<FLLM_TYPE_Q6_K> { static constexpr int BB = 210, GPB = 8; };
+template <> struct Geo<FLLM_TYPE_Q8_0> { static constexpr int BB = 34, GPB = 1; };
+template <> struct Geo<FLLM_TYPE_Q4_0> { static constexpr int BB = 18, GPB = 1; };
+template <int T> struct Stage {
+    static constexpr int BB = Geo<T>::BB, GPB = Geo<T>::GPB;
+    static constexpr int MAXB = GPB == 8 ? 9 : 64;               // blocks touched by 64 groups
+    static constexpr int N16 = (MAXB * BB + 15 + 15) / 16;       // chunks per row slice
+    static constexpr int CPL = (N16 + 63) / 64;                  // chunks per lane per row
+    static constexpr int RSB = N16 * 16 + 16;                    // LDS bytes per row slice (+ over-read slack)
+};
+
 template <int T> struct Raw;
 
 // Q4_K (Dequantizer.cs:251-294): 144-byte blocks; group g = 32 elements with byte qs[g*16+i/2],
 // low nibble for even i; dg = d*sc, mg = dmin*m; y = dg*q - mg.
 template <> struct Raw<FLLM_TYPE_Q4_K> { uint4 hdr, qs; int g; };
-__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q4_K>& r, const uint8_t* __restrict__ W, int64_t gi) {
-    const uint8_t* blk = W + (gi >> 3) * 144;
-    r.g = (int)(gi & 7);
-    r.hdr = *(const uint4*)blk;
-    r.qs = *(const uint4*)(blk + 16 + r.g * 16);
+__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q4_K>& r, lds_u8* blk, int g) {
+    r.g = g;
+    r.hdr = lds_ld16(blk);
+    r.qs = lds_ld16(blk + 16 + g * 16);
 }
 __device__ __forceinline__ void kscale_regs(const uint4& hdr, int g, int& sc, int& mn) {
     int sh = (g & 3) * 8;
@@ -159,12 +180,11 @@ __device__ __forceinline__ float dot(const Raw<FLLM_TYPE_Q4_K>& r, const uint32_
 // Q5_K (Dequantizer.cs:316-368): 176-byte blocks; high bit of element t is bit t&7 of
 // qh[t>>3], i.e. bit t of the group's qh dword; low nibble from qs[t>>1].
 template <> struct Raw<FLLM_TYPE_Q5_K> { uint4 hdr, qs; uint32_t qh; int g; };
-__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q5_K>& r, const uint8_t* __restrict__ W, int64_t gi) {
-    const uint8_t* blk = W + (gi >> 3) * 176;
-    r.g = (int)(gi & 7);
-    r.hdr = *(const uint4*)blk;
-    r.qh = *(const uint32_t*)(blk + 16 + r.g * 4);
-    r.qs = *(const uint4*)(blk + 48 + r.g * 16);
+__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q5_K>& r, lds_u8* blk, int g) {
+    r.g = g;
+    r.hdr = lds_ld16(blk);
+    r.qh = *(lds_u32*)(blk + 16 + g * 4);
+    r.qs = lds_ld16(blk + 48 + g * 16);
 }
 __device__ __forceinline__ float dot(const Raw<FLLM_TYPE_Q5_K>& r, const uint32_t* xp, float4 xs) {
     float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
@@ -190,12 +210,10 @@ __device__ __forceinline__ float dot(const Raw<FLLM_TYPE_Q5_K>& r, const uint32_
 // y = (d*sc)*(q-32). Blocks are only 2-byte aligned: dwords are read from the 4-byte-aligned
 // address below the block and re-aligned with v_alignbyte.
 template <> struct Raw<FLLM_TYPE_Q6_K> { uint32_t l[5], h[3], s, d; uint32_t mis; int c; };
-__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q6_K>& r, const uint8_t* __restrict__ W, int64_t gi) {
-    const uint8_t* blk = W + (gi >> 3) * 210;
-    int c = (int)(gi & 7);
+__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q6_K>& r, lds_u8* blk, int c) {
     r.c = c;
-    r.mis = (uint32_t)((uintptr_t)blk & 3u);
-    const uint32_t* b4 = (const uint32_t*)(blk - r.mis);
+    r.mis = (uint32_t)(uintptr_t)blk & 3u;
+    lds_u32* b4 = (lds_u32*)(blk - r.mis);
 #pragma unroll
     for (int i = 0; i < 5; i++) r.l[i] = b4[4 * c + i];
 #pragma unroll
@@ -239,10 +257,9 @@ __device__ __forceinline__ float dot(const Raw<FLLM_TYPE_Q6_K>& r, const uint32_
 
 // Q8_0 (Dequantizer.cs:203-231): 34-byte blocks (2-byte aligned), y = (sbyte)q * d.
 template <> struct Raw<FLLM_TYPE_Q8_0> { uint32_t dw[10]; uint32_t mis; };
-__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q8_0>& r, const uint8_t* __restrict__ W, int64_t gi) {
-    const uint8_t* blk = W + gi * 34;
-    r.mis = (uint32_t)((uintptr_t)blk & 3u);
-    const uint32_t* b4 = (const uint32_t*)(blk - r.mis);
+__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q8_0>& r, lds_u8* blk, int) {
+    r.mis = (uint32_t)(uintptr_t)blk & 3u;
+    lds_u32* b4 = (lds_u32*)(blk - r.mis);
 #pragma unroll
     for (int i = 0; i < 10; i++) r.dw[i] = b4[i];
 }
@@ -267,10 +284,9 @@ __device__ __forceinline__ float dot(const Raw<FLLM_TYPE_Q8_0>& r, const uint32_
 // Q4_0 (Dequantizer.cs:155-185): 18-byte blocks, y = (nib-8)*d; low nibble of byte j is
 // element j, high nibble element j+16.
 template <> struct Raw<FLLM_TYPE_Q4_0> { uint32_t dw[5]; uint32_t mis; };
-__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q4_0>& r, const uint8_t* __restrict__ W, int64_t gi) {
-    const uint8_t* blk = W + gi * 18;
-    r.mis = (uint32_t)((uintptr_t)blk & 3u);
-    const uint32_t* b4 = (const uint32_t*)(blk - r.mis);
+__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q4_0>& r, lds_u8* blk, int) {
+    r.mis = (uint32_t)(uintptr_t)blk & 3u;
+    lds_u32* b4 = (lds_u32*)(blk - r.mis);
 #pragma unroll
     for (int i = 0; i < 5; i++) r.dw[i] = b4[i];
 }
@@ -293,30 +309,6 @@ __device__ __forceinline__ float dot(const Raw<FLLM_TYPE_Q4_0>& r, const uint32_
         D0 = sdot4(ev, xp[16 + k], D0); D0 = sdot4(od, xp[20 + k], D0);
     }
     return d * (xs.x * digits_total(D2, D1, D0) - 8.0f * xs.y);
-}
-
-// Q8_K (Dequantizer.cs:427-456): 292-byte blocks (4-byte aligned), f32 d, int8 qs[256];
-// y = (sbyte)q * d.
-template <> struct Raw<FLLM_TYPE_Q8_K> { uint32_t q[8]; uint32_t d; };
-__device__ __forceinline__ void ld(Raw<FLLM_TYPE_Q8_K>& r, const uint8_t* __restrict__ W, int64_t gi) {
-    const uint32_t* b4 = (const uint32_t*)(W + (gi >> 3) * 292);
-    int g = (int)(gi & 7);
-    r.d = b4[0];
-#pragma unroll
-    for (int i = 0; i < 8; i++) r.q[i] = b4[1 + 8 * g + i];
-}
-__device__ __forceinline__ float dot(const Raw<FLLM_TYPE_Q8_K>& r, const uint32_t* xp, float4 xs) {
-    float d = __uint_as_float(r.d);
-    int D2 = 0, D1 = 0, D0 = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t ev = __builtin_amdgcn_perm(r.q[2 * k + 1], r.q[2 * k], 0x06040200u);
-        uint32_t od = __builtin_amdgcn_perm(r.q[2 * k + 1], r.q[2 * k], 0x07050301u);
-        D2 = sdot4(ev, xp[k], D2); D2 = sdot4(od, xp[4 + k], D2);
-        D1 = sdot4(ev, xp[8 + k], D1); D1 = sdot4(od, xp[12 + k], D1);
-        D0 = sdot4(ev, xp[16 + k], D0); D0 = sdot4(od, xp[20 + k], D0);
-    }
-    return d * (xs.x * digits_total(D2, D1, D0));
 }
 
 // Sum NR per-lane values over the 64 lanes of a wave with a transposing butterfly
@@ -350,36 +342,93 @@ template <int NR> struct Log2;
 template <> struct Log2<4> { static constexpr int v = 2; };
 template <> struct Log2<8> { static constexpr int v = 3; };
 
-// NR rows [row0, row0+NR) of one matrix, this lane's group column; the wave's row sums are
-// written to part[0..NR).
+// ---- row batches staged through LDS -----------------------------------------------------------
+// A wave's slice of a row (its S group columns) is a contiguous byte range of the block stream.
+// The wave copies the 16-byte-aligned chunks covering it into its own LDS area with fully
+// coalesced 16-byte loads (64 lanes x 16 B per instruction), then every lane reads its group's
+// block fields from LDS. The loads of the next batch are issued before the current batch is
+// dotted, so HBM latency overlaps the dequant arithmetic.
+struct SliceGeom {
+    int G, S, Sw;   // groups per row, groups per wave slice, groups in this wave's slice
+    int wave;
+};
+
 template <int T, int NR>
-__device__ __forceinline__ void batch_rows(const uint8_t* __restrict__ W, int rows, int row0, int G, int j, bool active,
-                                           const uint32_t* xp, float4 xs, int lane, float* part) {
-    Raw<T> raw[NR];
-    bool ok[NR];
+struct Batch {
+    uint4 c[NR][Stage<T>::CPL];
+    uint32_t a0[NR];  // aligned start byte of each row slice (relative to the matrix)
+    int n16[NR];      // chunks covering each row slice (0 = row outside the matrix)
+};
+
+template <int T, int NR>
+__device__ __forceinline__ void issue_batch(Batch<T, NR>& bt, const uint8_t* __restrict__ W, int rows, int row0,
+                                            const SliceGeom& sg, int lane) {
+    using St = Stage<T>;
 #pragma unroll
     for (int rr = 0; rr < NR; rr++) {
-        ok[rr] = active && (row0 + rr) < rows;
-        if (ok[rr]) ld(raw[rr], W, (int64_t)(row0 + rr) * G + j);
-    }
-    float acc[NR];
+        int row = row0 + rr;
+        bt.n16[rr] = 0;
+        bt.a0[rr] = 0;
+        if (row < rows && sg.Sw > 0) {
+            int64_t g0 = (int64_t)row * sg.G + (int64_t)sg.wave * sg.S;
+            int64_t b0 = g0 / St::GPB, b1 = (g0 + sg.Sw - 1) / St::GPB;
+            int64_t by0 = b0 * St::BB, by1 = (b1 + 1) * St::BB;
+            int64_t a0 = by0 & ~(int64_t)15;
+            bt.a0[rr] = (uint32_t)(a0 & 0xFFFFFFFF);
+            bt.n16[rr] = (int)((by1 - a0 + 15) >> 4);
+            const uint4* src = (const uint4*)(W + a0);
 #pragma unroll
-    for (int rr = 0; rr < NR; rr++) acc[rr] = ok[rr] ? dot(raw[rr], xp, xs) : 0.0f;
-    float tot = transpose_reduce<NR>(acc, lane);
-    if ((lane & (64 / NR - 1)) == 0) part[(lane >> (6 - Log2<NR>::v)) & (NR - 1)] = tot;
+            for (int k = 0; k < St::CPL; k++) {
+                int ch = lane + 64 * k;
+                if (ch < bt.n16[rr]) bt.c[rr][k] = src[ch];
+            }
+        }
+    }
 }
 
-template <int NR>
-__device__ __forceinline__ void batch_any(int type, const uint8_t* W, int rows, int row0, int G, int j, bool active,
-                                          const uint32_t* xp, float4 xs, int lane, float* part) {
-    switch (type) {
-        case FLLM_TYPE_Q4_K: batch_rows<FLLM_TYPE_Q4_K, NR>(W, rows, row0, G, j, active, xp, xs, lane, part); break;
-        case FLLM_TYPE_Q5_K: batch_rows<FLLM_TYPE_Q5_K, NR>(W, rows, row0, G, j, active, xp, xs, lane, part); break;
-        case FLLM_TYPE_Q6_K: batch_rows<FLLM_TYPE_Q6_K, NR>(W, rows, row0, G, j, active, xp, xs, lane, part); break;
-        case FLLM_TYPE_Q8_0: batch_rows<FLLM_TYPE_Q8_0, NR>(W, rows, row0, G, j, active, xp, xs, lane, part); break;
-        case FLLM_TYPE_Q4_0: batch_rows<FLLM_TYPE_Q4_0, NR>(W, rows, row0, G, j, active, xp, xs, lane, part); break;
-        default: batch_rows<FLLM_TYPE_Q8_K, NR>(W, rows, row0, G, j, active, xp, xs, lane, part); break;
+template <int T, int NR>
+__device__ __forceinline__ void stage_batch(const Batch<T, NR>& bt, __attribute__((address_space(3))) uint8_t* wlds, int lane) {
+    using St = Stage<T>;
+#pragma unroll
+    for (int rr = 0; rr < NR; rr++) {
+#pragma unroll
+        for (int k = 0; k < St::CPL; k++) {
+            int ch = lane + 64 * k;
+            if (ch < bt.n16[rr]) {
+                const uint4 c = bt.c[rr][k];
+                u32x4 t = {c.x, c.y, c.z, c.w};
+                *(lds_v4w*)(wlds + rr * St::RSB + ch * 16) = t;
+            }
+        }
     }
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Dot the NR staged rows with this lane's group column; the wave's row sums go to part[0..NR).
+template <int T, int NR>
+__device__ __forceinline__ void dot_batch(const Batch<T, NR>& bt, lds_u8* wlds, int row0, const SliceGeom& sg,
+                                          int j, bool active, const uint32_t* xp, float4 xs, int lane, float* part) {
+    using St = Stage<T>;
+    float acc[NR];
+#pragma unroll
+    for (int rr = 0; rr < NR; rr++) {
+        acc[rr] = 0.0f;
+        if (active && bt.n16[rr] > 0) {
+            int64_t gi = (int64_t)(row0 + rr) * sg.G + j;
+            int64_t blk = gi / St::GPB;
+            uint32_t off = (uint32_t)((blk * St::BB) & 0xFFFFFFFF) - bt.a0[rr];
+            Raw<T> r;
+            ld(r, (lds_u8*)(wlds + rr * St::RSB + off), (int)(gi % St::GPB));
+            acc[rr] = dot(r, xp, xs);
+        }
+    }
+    float tot = transpose_reduce<NR>(acc, lane);
+    if ((lane & (64 / NR - 1)) == 0) part[(lane >> (6 - Log2<NR>::v)) & (NR - 1)] = tot;
 }
 
 __device__ __forceinline__ float act_fn(float g, int act) {
@@ -393,93 +442,13 @@ __device__ __forceinline__ float act_fn(float g, int act) {
 
 // =====================================================================================
 // The fused kernel.
-// LDS: part[nslice][T] row partials (T = row slots of the workgroup), red[16], and for the
-// logits epilogue 16 u64 keys.
+// LDS: part[nslice][T] row partials (T = row slots of the workgroup), red[16], 16 u64 keys for the
+// logits epilogue, then each wave's staging area (GEMV_NR row slices).
 // =====================================================================================
-// NR = rows per batch: 8 for rows of up to 512 groups (at most 8 waves), 4 for wider rows (up
-// to 16 waves, which caps the kernel at 128 VGPRs).
-template <int NR>
-__global__ __launch_bounds__(NR == 8 ? 512 : 1024) void k_gemv_fused(const GemvArgs a) {
-    extern __shared__ float lds[];
-    const int nslice = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int j = wave * a.S + lane;
-    const bool active = lane < a.S && j < a.G;
+constexpr int GEMV_NR = 4;  // rows per batch
 
-    // ---- which segment / rows this workgroup covers ------------------------------------
-    int si = 0;
-    while (si + 1 < a.nseg && (int)blockIdx.x >= a.seg[si + 1].wg_begin) si++;
-    const GemvSeg& sg = a.seg[si];
-    const int wg_in_seg = (int)blockIdx.x - sg.wg_begin;
-    const int R = a.rpw;                 // rows per workgroup (multiple of 8)
-    const int row_base = wg_in_seg * R;  // first row of this workgroup in its matrix (GLU: in gate and up)
-    const int T = a.glu ? 2 * R : R;     // row slots
-    float* part = lds;                   // [nslice][T]
-    float* red = lds + nslice * T;       // [16]
-
-    // ---- prologue: this lane's 32 input values -----------------------------------------
-    float v[32];
-    if (a.xin == XIN_EMBED_NORM) {
-        const int64_t tok = a.params->token;
-        if (active) {
-            deq32(a.emb_type, a.emb, tok * (int64_t)a.G * 32 + j * 32, v);
-            if (blockIdx.x == 0) {
-                float4* xo = (float4*)(a.x_out + j * 32);
-#pragma unroll
-                for (int i = 0; i < 8; i++) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-            }
-        }
-    } else if (active) {
-        const float4* xi = (const float4*)(a.x + j * 32);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float4 t = xi[i];
-            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-        }
-    }
-    if (!active) {
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = 0.0f;
-    }
-    if (a.xin != XIN_F32) {
-        // RmsNorm: rms = 1/sqrt(Dot(x,x)/n + eps); dst = (x*rms)*w  (Gemma: *(1+w), eps 1e-6)
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 32; i++) ss = fmaf(v[i], v[i], ss);
-        ss = wsum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int i = 0; i < nslice; i++) tot += red[i];
-        float rms = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
-        if (active) {
-            const float4* wv = (const float4*)(a.norm_w + j * 32);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float4 w4 = wv[i];
-                float ww[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float t = v[4 * i + e] * rms;
-                    v[4 * i + e] = a.norm_kind ? t * (ww[e] + 1.0f) : t * ww[e];
-                }
-            }
-        }
-    }
-    uint32_t xp[24];
-    float4 xs;
-    quantize32(v, xp, xs);
-
-    // ---- row batches ----------------------------------------------------------------------
-    for (int b = 0; b < T; b += NR) {
-        const GemvSeg* m = &sg;
-        int row0 = row_base + b;
-        if (a.glu && b >= R) { m = &a.seg[1]; row0 = row_base + b - R; }
-        batch_any<NR>(m->type, m->w, m->rows, row0, a.G, j, active, xp, xs, lane, part + wave * T + b);
-    }
-    __syncthreads();
-
-    // ---- epilogue -----------------------------------------------------------------------
+__device__ __forceinline__ void epilogue(const GemvArgs& a, const GemvSeg& sg, const float* part, float* red, int nslice,
+                                         int R, int T, int row_base, int wave, int lane) {
     if (a.glu) {
         // h = act(W_gate x) * (W_up x)
         for (int t = threadIdx.x; t < R; t += blockDim.x) {
@@ -540,24 +509,7 @@ __global__ __launch_bounds__(NR == 8 ? 512 : 1024) void k_gemv_fused(const GemvA
         __syncthreads();
         if (threadIdx.x == 0) {
             for (int w = 1; w < nslice; w++) best = keys[w] > best ? keys[w] : best;
-            atomicMax(a.amax_key, best);
-            __threadfence();
-            unsigned int done = atomicAdd(a.done, 1u);
-            if (done == gridDim.x - 1) {
-                // last workgroup: publish the greedy token and advance the step parameters
-                __threadfence();
-                unsigned long long k = atomicAdd(a.amax_key, 0ull);
-                int tok = (int)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
-                StepParams* P = a.params_rw;
-                P->argmax = tok;
-                if (a.tokens_out && P->nstep >= 0 && P->nstep < a.tokens_cap) a.tokens_out[P->nstep] = tok;
-                P->nstep = P->nstep + 1;
-                P->token = tok;
-                P->pos = P->pos + 1;
-                P->cur_len = P->cur_len + 1;
-                atomicExch(a.amax_key, 0ull);
-                atomicExch(a.done, 0u);
-            }
+            a.wg_keys[blockIdx.x] = best;  // reduced by the argmax kernel that follows
         }
         return;
     }
@@ -578,10 +530,138 @@ __global__ __launch_bounds__(NR == 8 ? 512 : 1024) void k_gemv_fused(const GemvA
     }
 }
 
+// PREFETCH: the next batch's loads are issued before the current batch is dotted (two batches of
+// staging registers); without it the kernel fits the 128 VGPRs of 16-wave workgroups.
+template <int T, bool PREFETCH>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, int wg_in_seg) {
+    constexpr int NR = GEMV_NR;
+    extern __shared__ float lds[];
+    const int nslice = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int j = wave * a.S + lane;
+    const bool active = lane < a.S && j < a.G;
+    const int R = a.rpw;                 // rows per workgroup (multiple of 8)
+    const int row_base = wg_in_seg * R;  // first row of this workgroup in its matrix (GLU: in gate and up)
+    const int T_slots = a.glu ? 2 * R : R;
+    float* part = lds;                   // [nslice][T_slots]
+    float* red = lds + nslice * T_slots; // [16] floats, then 16 u64
+    __attribute__((address_space(3))) uint8_t* wlds =
+        (__attribute__((address_space(3))) uint8_t*)(red + 16 + 32) + wave * NR * Stage<T>::RSB;
+
+    SliceGeom geo;
+    geo.G = a.G;
+    geo.S = a.S;
+    geo.wave = wave;
+    geo.Sw = min(a.S, a.G - wave * a.S);
+    if (geo.Sw < 0) geo.Sw = 0;
+
+    // first batch's weight loads go out before the activation prologue
+    const GemvSeg& s1 = a.glu ? a.seg[1] : sg;
+    Batch<T, NR> cur, nxt;
+    issue_batch<T, NR>(cur, sg.w, sg.rows, row_base, geo, lane);
+
+    // ---- prologue: this lane's 32 input values -----------------------------------------
+    float v[32];
+    if (a.xin == XIN_EMBED_NORM) {
+        const int64_t tok = a.params->token;
+        if (active) {
+            deq32(a.emb_type, a.emb, tok * (int64_t)a.G * 32 + j * 32, v);
+            if (blockIdx.x == 0) {
+                float4* xo = (float4*)(a.x_out + j * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            }
+        }
+    } else if (active) {
+        const float4* xi = (const float4*)(a.x + j * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 t = xi[i];
+            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
+    }
+    if (!active) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = 0.0f;
+    }
+    if (a.xin != XIN_F32) {
+        // RmsNorm: rms = 1/sqrt(Dot(x,x)/n + eps); dst = (x*rms)*w  (Gemma: *(1+w), eps 1e-6)
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) ss = fmaf(v[i], v[i], ss);
+        ss = wsum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < nslice; i++) tot += red[i];
+        float rms = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
+        if (active) {
+            const float4* wv = (const float4*)(a.norm_w + j * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float4 w4 = wv[i];
+                float ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float t = v[4 * i + e] * rms;
+                    v[4 * i + e] = a.norm_kind ? t * (ww[e] + 1.0f) : t * ww[e];
+                }
+            }
+        }
+    }
+    uint32_t xp[24];
+    float4 xs;
+    quantize32(v, xp, xs);
+
+    // ---- row batches --------------------------------------------------------------------------
+    for (int b = 0; b < T_slots; b += NR) {
+        stage_batch<T, NR>(cur, wlds, lane);
+        const int bn = b + NR;
+        const bool more = bn < T_slots;
+        const bool up = a.glu && bn >= R;
+        const GemvSeg& m = up ? s1 : sg;
+        if (PREFETCH && more) issue_batch<T, NR>(nxt, m.w, m.rows, row_base + (up ? bn - R : bn), geo, lane);
+        wave_lds_sync();
+        dot_batch<T, NR>(cur, wlds, row_base + ((a.glu && b >= R) ? b - R : b), geo, j, active, xp, xs, lane,
+                         part + wave * T_slots + b);
+        wave_lds_sync();
+        if (PREFETCH) cur = nxt;
+        else if (more) issue_batch<T, NR>(cur, m.w, m.rows, row_base + (up ? bn - R : bn), geo, lane);
+    }
+    __syncthreads();
+    epilogue(a, sg, part, red, nslice, R, T_slots, row_base, wave, lane);
+}
+
+// WIDE: rows of more than 512 groups (up to 16 waves per workgroup), no prefetch.
+template <bool WIDE>
+__global__ __launch_bounds__(WIDE ? 1024 : 512) __attribute__((amdgpu_waves_per_eu(4))) void k_gemv_fused(const GemvArgs a) {
+    int si = 0;
+    while (si + 1 < a.nseg && (int)blockIdx.x >= a.seg[si + 1].wg_begin) si++;
+    const GemvSeg& sg = a.seg[si];
+    const int wg_in_seg = (int)blockIdx.x - sg.wg_begin;
+    switch (sg.type) {
+        case FLLM_TYPE_Q4_K: gemv_body<FLLM_TYPE_Q4_K, !WIDE>(a, sg, wg_in_seg); break;
+        case FLLM_TYPE_Q5_K: gemv_body<FLLM_TYPE_Q5_K, !WIDE>(a, sg, wg_in_seg); break;
+        case FLLM_TYPE_Q6_K: gemv_body<FLLM_TYPE_Q6_K, !WIDE>(a, sg, wg_in_seg); break;
+        case FLLM_TYPE_Q8_0: gemv_body<FLLM_TYPE_Q8_0, !WIDE>(a, sg, wg_in_seg); break;
+        default: gemv_body<FLLM_TYPE_Q4_0, !WIDE>(a, sg, wg_in_seg); break;
+    }
+}
+
 // ---- host side ------------------------------------------------------------------------
 bool gemv_fusable_type(int t) {
     return t == FLLM_TYPE_Q4_K || t == FLLM_TYPE_Q5_K || t == FLLM_TYPE_Q6_K || t == FLLM_TYPE_Q8_0 ||
-           t == FLLM_TYPE_Q4_0 || t == FLLM_TYPE_Q8_K;
+           t == FLLM_TYPE_Q4_0;
+}
+
+static int stage_rsb(int t) {
+    switch (t) {
+        case FLLM_TYPE_Q4_K: return Stage<FLLM_TYPE_Q4_K>::RSB;
+        case FLLM_TYPE_Q5_K: return Stage<FLLM_TYPE_Q5_K>::RSB;
+        case FLLM_TYPE_Q6_K: return Stage<FLLM_TYPE_Q6_K>::RSB;
+        case FLLM_TYPE_Q8_0: return Stage<FLLM_TYPE_Q8_0>::RSB;
+        default: return Stage<FLLM_TYPE_Q4_0>::RSB;
+    }
 }
 
 bool gemv_fusable_cols(int64_t cols) { return cols % 32 == 0 && cols >= 32 && cols <= 32768; }
@@ -595,8 +675,8 @@ int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_t
     for (int i = 0; i < a.nseg; i++) total_rows += a.glu ? (i == 0 ? a.seg[i].rows : 0) : a.seg[i].rows;
     int rpw = rows_per_wg;
     if (rpw <= 0) {
-        // aim for about 12 waves per CU over the launch, whole batches of 8 rows per workgroup
-        int64_t target_wgs = (int64_t)n_cu * 12 / nslice;
+        // aim for about 16 waves per CU over the launch, whole batches of 8 rows per workgroup
+        int64_t target_wgs = (int64_t)n_cu * 16 / nslice;
         if (target_wgs < 1) target_wgs = 1;
         int64_t slots = a.glu ? 2 * total_rows : total_rows;
         int64_t per = (slots + target_wgs - 1) / target_wgs;
@@ -613,17 +693,20 @@ int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_t
         wg += (int)((a.seg[i].rows + rpw - 1) / rpw);
     }
     int T = a.glu ? 2 * rpw : rpw;
+    int rsb = 0;
+    for (int i = 0; i < a.nseg; i++) rsb = stage_rsb(a.seg[i].type) > rsb ? stage_rsb(a.seg[i].type) : rsb;
     *block_threads = 64 * nslice;
-    *lds_bytes = sizeof(float) * ((size_t)nslice * T + 16) + 16 * sizeof(unsigned long long);
+    // row partials, 16 reduction floats, 16 u64 keys, then every wave's staging area
+    *lds_bytes = sizeof(float) * ((size_t)nslice * T + 48) + (size_t)nslice * GEMV_NR * rsb;
     return wg;
 }
 
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st) {
     if (grid <= 0) return hipSuccess;
     if (block_threads <= 512)
-        k_gemv_fused<8><<<grid, block_threads, lds, st>>>(a);
+        k_gemv_fused<false><<<grid, block_threads, lds, st>>>(a);
     else
-        k_gemv_fused<4><<<grid, block_threads, lds, st>>>(a);
+        k_gemv_fused<true><<<grid, block_threads, lds, st>>>(a);
     return hipGetLastError();
 }
 

@@ -48,11 +48,7 @@ struct GemvArgs {
     int kvdim;
     // logits
     float softcap;
-    unsigned long long* amax_key;
-    unsigned int* done;
-    StepParams* params_rw;
-    int* tokens_out;       // tokens_out[nstep] = greedy token (when nstep < tokens_cap)
-    int tokens_cap;
+    unsigned long long* wg_keys;  // per workgroup: (order key of its largest logit << 32) | ~index
 };
 
 bool gemv_fusable_type(int t);

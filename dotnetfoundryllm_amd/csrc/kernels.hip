@@ -459,6 +459,37 @@ hipError_t launch_argmax(const float* x, int64_t n, StepParams* p, int* tokens_o
     return hipGetLastError();
 }
 
+// Reduce the LM head's per-workgroup keys ((order key << 32) | ~row) to the first index of the
+// maximum, then advance the step like k_argmax with tokens_out.
+__global__ __launch_bounds__(256) void k_argmax_keys(const unsigned long long* __restrict__ keys, int n, StepParams* p,
+                                                     int* tokens_out, int tokens_cap) {
+    __shared__ unsigned long long sk[4];
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
+    for (int o = 32; o > 0; o >>= 1) {
+        unsigned long long ot = __shfl_xor(best, o);
+        best = ot > best ? ot : best;
+    }
+    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = sk[w] > best ? sk[w] : best;
+        int idx = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+        p->argmax = idx;
+        if (p->nstep >= 0 && p->nstep < tokens_cap) tokens_out[p->nstep] = idx;
+        p->nstep = p->nstep + 1;
+        p->token = idx;
+        p->pos = p->pos + 1;
+        p->cur_len = p->cur_len + 1;
+    }
+}
+
+hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams* p, int* tokens_out, int tokens_cap,
+                              hipStream_t st) {
+    k_argmax_keys<<<1, 256, 0, st>>>(keys, n, p, tokens_out, tokens_cap);
+    return hipGetLastError();
+}
+
 // Scale by inv_temp in place (SamplerPipeline.cs:67-70), find the k-th largest value by a
 // 4-pass radix select on order-preserving keys, and emit every index whose value is not
 // below it (ties kept), in ascending index order.

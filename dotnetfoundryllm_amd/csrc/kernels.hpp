@@ -49,6 +49,9 @@ hipError_t launch_softcap(float* x, int64_t n, float cap, hipStream_t st);
 // argmax into p->argmax; with tokens_out also tokens_out[p->nstep] = argmax and the step advance
 // (token = argmax, pos + 1, cur_len + 1, nstep + 1).
 hipError_t launch_argmax(const float* x, int64_t n, StepParams* p, int* tokens_out, int tokens_cap, hipStream_t st);
+// reduce per-workgroup argmax keys of the fused LM head; advances the step as launch_argmax
+hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams* p, int* tokens_out, int tokens_cap,
+                              hipStream_t st);
 hipError_t launch_topk(float* x, int64_t n, float inv_temp, int k, int cap, int* ids, float* vals, int* count,
                        hipStream_t st);
 hipError_t launch_copy_hidden(const float* x, int n, float* dst, hipStream_t st);

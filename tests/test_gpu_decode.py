@@ -288,10 +288,10 @@ def test_profile_mode_reports_kernels(ctx):
             fwd.forward(5, p, kv)
         ents = {e["name"]: e for e in F.profile_entries(kv)}
         # fused launches: [norm+QKV+RoPE+KV], attention, [Wo+residual], [norm+gate/up+act],
-        # [down+residual] per layer, then [norm+LM head+argmax]
+        # [down+residual] per layer, then [norm+LM head] and the argmax over its workgroups
         for name in ("qkv_rope_kv", "attention", "attn_output", "ffn_gate_up", "ffn_down"):
             assert ents[name]["launches"] == 3 * desc.n_layers, name
-        assert ents["lm_head_argmax"]["launches"] == 3
+        assert ents["lm_head"]["launches"] == 3 and ents["argmax"]["launches"] == 3
         assert all(e["ms"] > 0 for e in ents.values())
     finally:
         kv.close()
