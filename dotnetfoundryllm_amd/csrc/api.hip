@@ -840,18 +840,26 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
         float* kc = s->kc + (size_t)l * layer_kv;
         float* vc = s->vc + (size_t)l * layer_kv;
         {
-            GemvArgs a{};
-            a.nseg = 3;
-            a.seg[0] = seg_of(L.q, EPI_Q, s->q, L.bq, nullptr);
-            a.seg[1] = seg_of(L.k, EPI_K, nullptr, L.bk, nullptr);
-            a.seg[2] = seg_of(L.v, EPI_V, nullptr, L.bv, nullptr);
-            a.xin = (l == 0 && emb_fused) ? XIN_EMBED_NORM : XIN_NORM;
-            a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
-            a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
-            a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
-            double bytes = (double)(L.q.bytes + L.k.bytes + L.v.bytes) + 4.0 * (2.0 * H + m->qdim + 2.0 * kvdim);
-            hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes);
-            if (e != hipSuccess) return e;
+            // q, k, v in one launch when they share a weight type, else one launch per run of
+            // equal types (each run's activation table follows its type's fragment order)
+            GemvSeg all[3] = {seg_of(L.q, EPI_Q, s->q, L.bq, nullptr), seg_of(L.k, EPI_K, nullptr, L.bk, nullptr),
+                              seg_of(L.v, EPI_V, nullptr, L.bv, nullptr)};
+            const Tensor* tens[3] = {&L.q, &L.k, &L.v};
+            for (int i0 = 0; i0 < 3;) {
+                int i1 = i0 + 1;
+                while (i1 < 3 && all[i1].type == all[i0].type) i1++;
+                GemvArgs a{};
+                a.nseg = i1 - i0;
+                double bytes = 0;
+                for (int i = i0; i < i1; i++) { a.seg[i - i0] = all[i]; bytes += (double)tens[i]->bytes + 4.0 * tens[i]->rows; }
+                a.xin = (l == 0 && emb_fused) ? XIN_EMBED_NORM : XIN_NORM;
+                a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
+                a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
+                a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
+                hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
+                if (e != hipSuccess) return e;
+                i0 = i1;
+            }
         }
         hipError_t e = attention_step(s, l, kc, vc);
         if (e != hipSuccess) return e;

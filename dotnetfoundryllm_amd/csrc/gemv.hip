@@ -447,8 +447,19 @@ __device__ __forceinline__ float act_fn(float g, int act) {
 // =====================================================================================
 constexpr int GEMV_NR = 4;  // rows per batch
 
-__device__ __forceinline__ void epilogue(const GemvArgs& a, const GemvSeg& sg, const float* part, float* red, int nslice,
-                                         int R, int T, int row_base, int wave, int lane) {
+// Rows [row_base, row_base + R) of segment sg from the waves' partial sums part[nslice][T]. For the
+// LM head, thread 0 folds this range's largest logit key into wg_best.
+// The segment's fields come by value (a by-reference aggregate selected at run time would be
+// copied to scratch memory).
+struct EpiSeg {
+    int rows, epi;
+    float* out;
+    const float* bias;
+    const float* resid;
+};
+
+__device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, const float* part, float* red, int nslice,
+                                         int R, int T, int row_base, int wave, int lane, unsigned long long& wg_best) {
     if (a.glu) {
         // h = act(W_gate x) * (W_up x)
         for (int t = threadIdx.x; t < R; t += blockDim.x) {
@@ -509,7 +520,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const GemvSeg& sg, c
         __syncthreads();
         if (threadIdx.x == 0) {
             for (int w = 1; w < nslice; w++) best = keys[w] > best ? keys[w] : best;
-            a.wg_keys[blockIdx.x] = best;  // reduced by the argmax kernel that follows
+            wg_best = best > wg_best ? best : wg_best;
         }
         return;
     }
@@ -629,7 +640,442 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
         else if (more) issue_batch<T, NR>(cur, m.w, m.rows, row_base + (up ? bn - R : bn), geo, lane);
     }
     __syncthreads();
-    epilogue(a, sg, part, red, nslice, R, T_slots, row_base, wave, lane);
+    unsigned long long best = 0ull;
+    epilogue(a, EpiSeg{sg.rows, sg.epi, sg.out, sg.bias, sg.resid}, part, red, nslice, R, T_slots, row_base, wave, lane, best);
+    if (sg.epi == EPI_LOGITS && threadIdx.x == 0) a.wg_keys[blockIdx.x] = best;  // reduced by the argmax kernel
+}
+
+// =====================================================================================
+// Matrix-core (MFMA) variant for rows that are whole 256-element chunks.
+//
+// v_mfma_i32_16x16x64_i8 computes D[16x16] += A[16x64] B[64x16] in int32. Lane l supplies A row
+// l%16 and B column l%16, both for the 16 k values of quarter l/16, and receives D column l%16,
+// rows 4*(l/16) .. +3. Here B column n is weight row n of a 16-row tile, quarter Q of a chunk is
+// the lane's own share of the chunk's bytes, and A row m = 4Q' + d holds activation digit d of the
+// elements of quarter Q' (zero elsewhere). So lane (n, Q) loads the weights it multiplies and
+// receives the three digit sums of (row n, quarter Q) in its own D registers: digit combination
+// and the per-group block scales are applied lane-locally.
+//
+// In 4 MFMA steps a lane covers groups Q and Q+4 of the chunk (32 elements each); step s covers
+// group Q + 4*(s>>1) and, for the 4-bit K-quants, the elements of parity s&1 (even elements in
+// the low nibbles). The activation table in LDS holds, for every chunk, step, quarter and digit,
+// the 16 digit bytes in that same element order.
+// =====================================================================================
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) f32x4 lds_f4;
+
+constexpr int MF_TILE = 16;  // weight rows per MFMA tile
+
+// bytes of 256 elements (one chunk) for the MFMA-capable types
+__host__ __device__ constexpr int mf_chunk_bytes(int t) {
+    return t == FLLM_TYPE_Q4_K ? 144 : t == FLLM_TYPE_Q6_K ? 210 : 0;
+}
+
+// LDS activation table: per chunk 48 uint4 entries [step][quarter][digit], then per chunk 8
+// float4 group stats {s, sum, sum of elements 0..15, sum of elements 16..31}.
+__device__ __forceinline__ int atab_index(int b, int s, int q, int d) { return ((b * 4 + s) * 4 + q) * 3 + d; }
+
+// k order of a 16-byte MFMA fragment: which element of the 32-element group sits in byte
+// `byte` of dword `j` of step s.
+//  MF_PARITY (Q4_K): t = 4j + byte, element 2t + (s & 1)   (low nibbles hold even elements)
+//  MF_Q6K:           element 16(s & 1) + 4 byte + j        (byte = qh byte, j = its 2-bit field)
+enum { MF_PARITY = 0, MF_Q6K = 1 };
+
+template <int L>
+__device__ __forceinline__ int mf_elem(int s, int j, int byte) {
+    if constexpr (L == MF_PARITY) return 2 * (4 * j + byte) + (s & 1);
+    else return 16 * (s & 1) + 4 * byte + j;
+}
+
+// Digits of group g (0..7) of chunk b, written as the A fragments of the two steps that cover it
+// (steps 2(g>>2) and 2(g>>2)+1 of quarter g&3); returns the group stats.
+template <int L>
+__device__ __forceinline__ void atab_write(__attribute__((address_space(3))) u32x4* atab, int b, int g, const float* v,
+                                           float4* st) {
+    float amax = 0.0f, s16a = 0.0f, s16b = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) { s16a += v[i]; amax = fmaxf(amax, fabsf(v[i])); }
+#pragma unroll
+    for (int i = 16; i < 32; i++) { s16b += v[i]; amax = fmaxf(amax, fabsf(v[i])); }
+    float sc = 0.0f, inv = 0.0f;
+    if (amax > 0.0f) { sc = amax / 127.0f; inv = 127.0f / amax; }
+    int X[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) X[i] = (int)rintf(v[i] * inv * 65536.0f);
+    const int q = g & 3, s0 = 2 * (g >> 2);
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t acc = 0;
+#pragma unroll
+                for (int by = 0; by < 4; by++) {
+                    // signed base-256 digits of X: X = 65536 b2 + 256 b1 + b0
+                    const int x = X[mf_elem<L>(p, j, by)];
+                    const int b0 = (int)(int8_t)(x & 0xFF);
+                    const int x1 = (x - b0) >> 8;
+                    const int b1 = (int)(int8_t)(x1 & 0xFF);
+                    const int dv = d == 0 ? (x1 - b1) >> 8 : d == 1 ? b1 : b0;
+                    acc |= (uint32_t)(dv & 0xFF) << (8 * by);
+                }
+                w[j] = acc;
+            }
+            u32x4 e = {w[0], w[1], w[2], w[3]};
+            atab[atab_index(b, s0 + p, q, d)] = e;
+        }
+    *st = make_float4(sc, s16a + s16b, s16a, s16b);
+}
+
+__device__ __forceinline__ float mf_total(const v4i& D) {
+    return (float)D.x + (float)D.y * 0.00390625f + (float)D.z * 1.52587890625e-05f;
+}
+
+// Per-wave LDS staging area of the MFMA variant: 16 rows x 224 bytes (one Q6_K block per row
+// plus its 16-byte alignment phase).
+constexpr int MF_STAGE_ROW = 224;
+constexpr int MF_STAGE_BYTES = 16 * MF_STAGE_ROW;
+
+// ---- Q4_K (Dequantizer.cs:251-294): 16-byte-aligned 144-byte blocks, loaded directly -------
+struct MfQ4K { uint4 hdr, qa, qb; };
+__device__ __forceinline__ void mf_issue(MfQ4K& r, const uint8_t* __restrict__ W, int64_t rb, int rows, int row0,
+                                         int b, int lane) {
+    const int n = lane & 15, q = lane >> 4;
+    const int row = min(row0 + n, rows - 1);
+    const uint8_t* cb = W + (int64_t)row * rb + (int64_t)b * 144;
+    r.hdr = *(const uint4*)cb;
+    r.qa = *(const uint4*)(cb + 16 + 16 * q);   // group q
+    r.qb = *(const uint4*)(cb + 80 + 16 * q);   // group q + 4
+}
+
+__device__ __forceinline__ v4i nib(const uint4& w, int p) {
+    const int sh = 4 * p;
+    v4i r = {(int)((w.x >> sh) & 0x0F0F0F0Fu), (int)((w.y >> sh) & 0x0F0F0F0Fu), (int)((w.z >> sh) & 0x0F0F0F0Fu),
+             (int)((w.w >> sh) & 0x0F0F0F0Fu)};
+    return r;
+}
+
+// 4 MFMAs over groups q and q+4 and their block scales; this lane's part of row n.
+__device__ __forceinline__ float mf_compute(const MfQ4K& r, const v4i* A, const float4& sA, const float4& sB, int q,
+                                            __attribute__((address_space(3))) uint8_t*, const uint8_t*, int64_t, int,
+                                            int, int) {
+    v4i z = {0, 0, 0, 0};
+    v4i Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], nib(r.qa, 0), z, 0, 0, 0);
+    Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], nib(r.qa, 1), Da, 0, 0, 0);
+    v4i Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], nib(r.qb, 0), z, 0, 0, 0);
+    Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], nib(r.qb, 1), Db, 0, 0, 0);
+    // DecodeKScaleMin (Dequantizer.cs:506-521) for groups q (< 4) and q + 4
+    const int sh = 8 * q;
+    uint32_t a = (r.hdr.y >> sh) & 0xFF, b = (r.hdr.z >> sh) & 0xFF, c = (r.hdr.w >> sh) & 0xFF;
+    int scA = (int)(a & 63), mnA = (int)(b & 63);
+    int scB = (int)((c & 15) | ((a >> 6) << 4)), mnB = (int)((c >> 4) | ((b >> 6) << 4));
+    float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
+    float dgA = d * (float)scA, mgA = dmin * (float)mnA;
+    float dgB = d * (float)scB, mgB = dmin * (float)mnB;
+    float y = dgA * (sA.x * mf_total(Da)) - mgA * sA.y;
+    y = y + (dgB * (sB.x * mf_total(Db)) - mgB * sB.y);
+    return y;
+}
+
+// ---- Q6_K (Dequantizer.cs:378-417): 210-byte blocks, staged through LDS ------------------------
+// The wave copies the 16-byte-aligned window of each tile row's block (224 bytes) with coalesced
+// 16-byte loads; lanes then read their fields from LDS.
+struct MfQ6K { uint4 c[4]; };
+__device__ __forceinline__ void mf_issue(MfQ6K& r, const uint8_t* __restrict__ W, int64_t rb, int rows, int row0,
+                                         int b, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int c = lane + 64 * i;
+        if (c < 16 * 14) {
+            int row = min(row0 + c / 14, rows - 1);
+            uintptr_t bp = (uintptr_t)(W + (int64_t)row * rb + (int64_t)b * 210);
+            r.c[i] = *(const uint4*)((bp & ~(uintptr_t)15) + 16 * (c % 14));
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t ldsw(__attribute__((address_space(3))) const uint8_t* p) {
+    return *(__attribute__((address_space(3))) const uint32_t*)p;
+}
+
+// n realigned dwords starting at LDS byte address p (2-byte aligned)
+template <int N>
+__device__ __forceinline__ void lds_words(__attribute__((address_space(3))) const uint8_t* p, uint32_t* out) {
+    const uint32_t mis = (uint32_t)(uintptr_t)p & 3u;
+    __attribute__((address_space(3))) const uint8_t* a = p - mis;
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; i++) w[i] = ldsw(a + 4 * i);
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], mis);
+}
+
+// fragment of step half h: 8 ql bytes (2 dwords) and the 4 qh bytes of those 16 elements;
+// byte `by` of dword j = element 4by + j: low nibble of ql byte 2by + (j>>1), 2 high bits =
+// field j of qh byte by
+__device__ __forceinline__ v4i q6_frag(uint32_t l0, uint32_t l1, uint32_t hq) {
+    uint32_t E = __builtin_amdgcn_perm(l1, l0, 0x06040200u);  // ql bytes 0,2,4,6
+    uint32_t O = __builtin_amdgcn_perm(l1, l0, 0x07050301u);  // ql bytes 1,3,5,7
+    uint32_t f0 = (E & 0x0F0F0F0Fu) | ((hq & 0x03030303u) << 4);
+    uint32_t f1 = ((E >> 4) & 0x0F0F0F0Fu) | (((hq >> 2) & 0x03030303u) << 4);
+    uint32_t f2 = (O & 0x0F0F0F0Fu) | (((hq >> 4) & 0x03030303u) << 4);
+    uint32_t f3 = ((O >> 4) & 0x0F0F0F0Fu) | (((hq >> 6) & 0x03030303u) << 4);
+    v4i r = {(int)f0, (int)f1, (int)f2, (int)f3};
+    return r;
+}
+
+__device__ __forceinline__ float mf_compute(const MfQ6K& r, const v4i* A, const float4& sA, const float4& sB, int q,
+                                            __attribute__((address_space(3))) uint8_t* stage, const uint8_t* W,
+                                            int64_t rb, int rows, int row0, int b) {
+    const int lane = threadIdx.x & 63, n = lane & 15;
+    // the previous chunk's LDS reads are done before this chunk's staging writes
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int c = lane + 64 * i;
+        if (c < 16 * 14) {
+            uint4 v = r.c[i];
+            u32x4 t = {v.x, v.y, v.z, v.w};
+            *(__attribute__((address_space(3))) u32x4*)(stage + (c / 14) * MF_STAGE_ROW + 16 * (c % 14)) = t;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // row n's block sits at its 16-byte alignment phase inside its staged window
+    const int row = min(row0 + n, rows - 1);
+    const uint32_t ph = (uint32_t)((uintptr_t)(W + (int64_t)row * rb + (int64_t)b * 210) & 15u);
+    __attribute__((address_space(3))) const uint8_t* blk = stage + n * MF_STAGE_ROW + ph;
+    uint32_t la[4], lb[4], ha[2], hb[2];
+    lds_words<4>(blk + 16 * q, la);          // ql of group q
+    lds_words<4>(blk + 64 + 16 * q, lb);     // ql of group q + 4
+    lds_words<2>(blk + 128 + 8 * q, ha);     // qh of group q
+    lds_words<2>(blk + 160 + 8 * q, hb);     // qh of group q + 4
+    const uint32_t sca = *(__attribute__((address_space(3))) const uint16_t*)(blk + 192 + 2 * q);  // scales 2q, 2q+1
+    const uint32_t scb = *(__attribute__((address_space(3))) const uint16_t*)(blk + 200 + 2 * q);  // scales 2q+8, 2q+9
+    const float d = h2f(*(__attribute__((address_space(3))) const uint16_t*)(blk + 208));
+    v4i z = {0, 0, 0, 0};
+    v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], q6_frag(la[0], la[1], ha[0]), z, 0, 0, 0);
+    v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], q6_frag(la[2], la[3], ha[1]), z, 0, 0, 0);
+    v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], q6_frag(lb[0], lb[1], hb[0]), z, 0, 0, 0);
+    v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], q6_frag(lb[2], lb[3], hb[1]), z, 0, 0, 0);
+    // y = (d * sc) * (q - 32) per element: (d * sc) * (s_x T - 32 * sum of the 16 activations)
+    float y = (d * (float)(int8_t)(sca & 0xFF)) * (sA.x * mf_total(D0) - 32.0f * sA.z);
+    y = y + (d * (float)(int8_t)(sca >> 8)) * (sA.x * mf_total(D1) - 32.0f * sA.w);
+    y = y + (d * (float)(int8_t)(scb & 0xFF)) * (sB.x * mf_total(D2) - 32.0f * sB.z);
+    y = y + (d * (float)(int8_t)(scb >> 8)) * (sB.x * mf_total(D3) - 32.0f * sB.w);
+    return y;
+}
+
+template <int T> struct MfPick;
+template <> struct MfPick<FLLM_TYPE_Q4_K> { using Raw = MfQ4K; static constexpr int L = MF_PARITY; static constexpr bool STAGE = false; };
+template <> struct MfPick<FLLM_TYPE_Q6_K> { using Raw = MfQ6K; static constexpr int L = MF_Q6K; static constexpr bool STAGE = true; };
+
+// Persistent workgroup body of the MFMA variant for weight type T. The launch's rows form units:
+// one 16-row tile, or for GLU the gate and up tiles of the same 16 rows. Workgroup w takes units
+// w, w + grid, w + 2 grid, ...; each of its nw waves covers KC = NB / nw consecutive chunks of every
+// row, so all waves walk the same (tile, chunk) item sequence: item i is chunk i % KC of the
+// workgroup's tile i / KC. Items stream through a ring of MF_RING chunk loads in flight that runs
+// across tile and unit boundaries; the first loads go out before the activation prologue.
+constexpr int MF_RING = 4;
+
+// unit u -> matrix of tile ts (0: gate / the segment's own, 1: up), its rows, first row, segment
+__device__ __forceinline__ void mf_tile_of(const GemvArgs& a, int u, int ts, const uint8_t*& W, int& rows, int& row0,
+                                           int& si) {
+    const int ub1 = a.seg[1].wg_begin, ub2 = a.seg[2].wg_begin;
+    si = (a.nseg > 2 && u >= ub2) ? 2 : (a.nseg > 1 && u >= ub1) ? 1 : 0;
+    const int tile = u - (si == 2 ? ub2 : si == 1 ? ub1 : 0);
+    const int mi = si + ts;
+    W = mi == 0 ? a.seg[0].w : (mi == 1 ? a.seg[1].w : a.seg[2].w);
+    rows = mi == 0 ? a.seg[0].rows : (mi == 1 ? a.seg[1].rows : a.seg[2].rows);
+    row0 = tile * MF_TILE;
+}
+
+// workgroup tile index t -> unit and tile-in-unit
+__device__ __forceinline__ void mf_tile_unit(const GemvArgs& a, int t, int& u, int& ts) {
+    const int k = a.glu ? (t >> 1) : t;
+    ts = a.glu ? (t & 1) : 0;
+    u = (int)blockIdx.x + k * (int)gridDim.x;
+}
+
+template <int T, int KC>
+__device__ __forceinline__ void mfma_body(const GemvArgs& a) {
+    using Raw = typename MfPick<T>::Raw;
+    constexpr int L = MfPick<T>::L;
+    constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
+    extern __shared__ float lds[];
+    const int nw = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q = lane >> 4, m = lane & 15;
+    const bool a_live = (m >> 2) == q && (m & 3) < 3;  // A row m = 4Q' + d lives in quarter Q'
+    const int NB = a.G / 8;            // chunks per row (NB == nw * KC)
+    const int kb0 = wave * KC;
+    const int tpu = a.glu ? 2 : 1;     // tiles per unit
+    const int T_slots = tpu * MF_TILE;
+    float* part = lds;                         // [nw][T_slots]
+    float* red = lds + nw * T_slots;           // [16] + 16 u64
+    __attribute__((address_space(3))) u32x4* atab = (__attribute__((address_space(3))) u32x4*)(red + 48);
+    lds_f4* stats = (lds_f4*)(atab + NB * 48);
+    __attribute__((address_space(3))) uint8_t* stage =
+        (__attribute__((address_space(3))) uint8_t*)(stats + NB * 8) + wave * MF_STAGE_BYTES;
+    const int64_t rb = (int64_t)NB * mf_chunk_bytes(T);
+    const int grid = (int)gridDim.x;
+    const int my_units = (a.nunits - (int)blockIdx.x + grid - 1) / grid;
+    const int items = my_units * tpu * KC;
+
+    Raw ring[MF_RING];
+#pragma unroll
+    for (int r = 0; r < MF_RING; r++) {
+        if (r < items) {
+            int u, ts, rows, row0, si;
+            const uint8_t* W;
+            mf_tile_unit(a, r >> LKC, u, ts);
+            mf_tile_of(a, u, ts, W, rows, row0, si);
+            mf_issue(ring[r], W, rb, rows, row0, kb0 + (r & (KC - 1)), lane);
+        }
+    }
+
+    // ---- prologue: (normed) activations -> digit table, one 32-element group per thread --------
+    float scale = 1.0f;
+    if (a.xin != XIN_F32) {
+        float ssq = 0.0f;
+        for (int g = threadIdx.x; g < a.G; g += blockDim.x) {
+            float v[32];
+            if (a.xin == XIN_EMBED_NORM) deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
+            else {
+                const float4* xi = (const float4*)(a.x + g * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
+            }
+#pragma unroll
+            for (int i = 0; i < 32; i++) ssq = fmaf(v[i], v[i], ssq);
+        }
+        ssq = wsum(ssq);
+        if (lane == 0) red[wave] = ssq;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < nw; i++) tot += red[i];
+        scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
+    }
+    for (int g = threadIdx.x; g < a.G; g += blockDim.x) {
+        float v[32];
+        if (a.xin == XIN_EMBED_NORM) {
+            deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
+            if (blockIdx.x == 0) {
+                float4* xo = (float4*)(a.x_out + g * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            }
+        } else {
+            const float4* xi = (const float4*)(a.x + g * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
+        }
+        if (a.xin != XIN_F32) {
+            const float4* wv = (const float4*)(a.norm_w + g * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float4 w4 = wv[i];
+                float ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float t = v[4 * i + e] * scale;
+                    v[4 * i + e] = a.norm_kind ? t * (ww[e] + 1.0f) : t * ww[e];
+                }
+            }
+        }
+        float4 st;
+        atab_write<L>(atab, g >> 3, g & 7, v, &st);
+        f32x4 stv = {st.x, st.y, st.z, st.w};
+        stats[(g >> 3) * 8 + (g & 7)] = stv;
+    }
+    __syncthreads();
+
+    // ---- items ----------------------------------------------------------------------------------
+    unsigned long long best = 0ull;
+    float y = 0.0f;
+    int tu, tts, trows, trow0, tsi;  // the current tile
+    const uint8_t* tW;
+    for (int i0 = 0; i0 < items; i0 += MF_RING) {
+#pragma unroll
+        for (int r = 0; r < MF_RING; r++) {
+            const int i = i0 + r;
+            if (i >= items) break;
+            const int c = i & (KC - 1);
+            if (c == 0) {
+                mf_tile_unit(a, i >> LKC, tu, tts);
+                mf_tile_of(a, tu, tts, tW, trows, trow0, tsi);
+            }
+            const int b = kb0 + c;
+            v4i A[4];
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                v4i z = {0, 0, 0, 0};
+                A[s] = a_live ? *(__attribute__((address_space(3))) const v4i*)&atab[atab_index(b, s, m >> 2, m & 3)] : z;
+            }
+            f32x4 ta = stats[b * 8 + q], tb = stats[b * 8 + q + 4];
+            y += mf_compute(ring[r], A, make_float4(ta.x, ta.y, ta.z, ta.w), make_float4(tb.x, tb.y, tb.z, tb.w), q, stage,
+                            tW, rb, trows, trow0, b);
+            // refill this ring slot with the item MF_RING ahead (possibly of another tile or unit)
+            const int ni = i + MF_RING;
+            if (ni < items) {
+                int u2, ts2, rows2, row02, si2;
+                const uint8_t* W2;
+                mf_tile_unit(a, ni >> LKC, u2, ts2);
+                mf_tile_of(a, u2, ts2, W2, rows2, row02, si2);
+                mf_issue(ring[r], W2, rb, rows2, row02, kb0 + (ni & (KC - 1)), lane);
+            }
+            if (c == KC - 1) {
+                // last chunk of the tile: the four quarters of row n, then this wave's partial
+                float yt = y + __shfl_xor(y, 16);
+                yt += __shfl_xor(yt, 32);
+                if (lane < 16) part[wave * T_slots + tts * MF_TILE + lane] = (trow0 + lane < trows) ? yt : 0.0f;
+                y = 0.0f;
+                if (tts == tpu - 1) {
+                    // last tile of the unit (same item in every wave): combine the waves, epilogue
+                    __syncthreads();
+                    const EpiSeg es{tsi == 0 ? a.seg[0].rows : tsi == 1 ? a.seg[1].rows : a.seg[2].rows,
+                                    tsi == 0 ? a.seg[0].epi : tsi == 1 ? a.seg[1].epi : a.seg[2].epi,
+                                    tsi == 0 ? a.seg[0].out : tsi == 1 ? a.seg[1].out : a.seg[2].out,
+                                    tsi == 0 ? a.seg[0].bias : tsi == 1 ? a.seg[1].bias : a.seg[2].bias,
+                                    tsi == 0 ? a.seg[0].resid : tsi == 1 ? a.seg[1].resid : a.seg[2].resid};
+                    epilogue(a, es, part, red, nw, MF_TILE, T_slots, trow0, wave, lane, best);
+                    __syncthreads();
+                }
+            }
+        }
+    }
+    if (a.seg[0].epi == EPI_LOGITS && threadIdx.x == 0) a.wg_keys[blockIdx.x] = best;  // reduced by the argmax kernel
+}
+
+// one kernel per (weight type, chunks per wave), each with its own register allocation; every
+// segment of an MFMA launch has the same weight type
+template <int T, int KC>
+__global__ __launch_bounds__(512) void k_gemv_mfma(const GemvArgs a) {
+    mfma_body<T, KC>(a);
+}
+
+typedef void (*MfKernel)(const GemvArgs);
+static MfKernel mf_kernel(int type, int kc) {
+    if (type == FLLM_TYPE_Q6_K) {
+        switch (kc) {
+            case 1: return k_gemv_mfma<FLLM_TYPE_Q6_K, 1>;
+            case 2: return k_gemv_mfma<FLLM_TYPE_Q6_K, 2>;
+            case 4: return k_gemv_mfma<FLLM_TYPE_Q6_K, 4>;
+            default: return k_gemv_mfma<FLLM_TYPE_Q6_K, 8>;
+        }
+    }
+    switch (kc) {
+        case 1: return k_gemv_mfma<FLLM_TYPE_Q4_K, 1>;
+        case 2: return k_gemv_mfma<FLLM_TYPE_Q4_K, 2>;
+        case 4: return k_gemv_mfma<FLLM_TYPE_Q4_K, 4>;
+        default: return k_gemv_mfma<FLLM_TYPE_Q4_K, 8>;
+    }
 }
 
 // WIDE: rows of more than 512 groups (up to 16 waves per workgroup), no prefetch.
@@ -666,8 +1112,64 @@ static int stage_rsb(int t) {
 
 bool gemv_fusable_cols(int64_t cols) { return cols % 32 == 0 && cols >= 32 && cols <= 32768; }
 
+// The matrix-core variant takes launches whose rows are whole 256-element chunks, with one
+// MFMA-capable weight type for all segments, and a wave count that divides the chunks per row.
+static int mf_waves(int NB) {
+    // at most 8 waves, each with 1, 2, 4 or 8 chunks; prefer 4 chunks per wave
+    const int order[4] = {4, 8, 2, 1};
+    for (int kc : order)
+        if (NB % kc == 0 && NB / kc <= 8) return NB / kc;
+    return 0;  // no suitable split
+}
+
+static bool mfma_ok(const GemvArgs& a, int64_t cols) {
+    if (cols % 256 != 0 || mf_waves((int)(cols / 256)) == 0) return false;
+    for (int i = 0; i < a.nseg; i++)
+        if (mf_chunk_bytes(a.seg[i].type) == 0 || a.seg[i].type != a.seg[0].type) return false;
+    return true;
+}
+
+static size_t mf_lds(int nw, int NB, bool glu, bool staged) {
+    const int T = (glu ? 2 : 1) * MF_TILE;
+    return sizeof(float) * ((size_t)nw * T + 48) + (size_t)NB * 48 * 16 + (size_t)NB * 8 * 16 +
+           (staged ? (size_t)nw * MF_STAGE_BYTES : 0);
+}
+
+static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, size_t* lds_bytes) {
+    a.mfma = 1;
+    a.G = (int)(cols / 32);
+    a.S = 0;
+    a.rpw = MF_TILE;
+    const int NB = (int)(cols / 256);
+    const int nw = mf_waves(NB);
+    int units = 0;
+    for (int i = 0; i < a.nseg; i++) {
+        a.seg[i].wg_begin = units;  // first unit of the segment
+        if (a.glu && i > 0) { a.seg[i].wg_begin = 1 << 30; continue; }
+        units += (a.seg[i].rows + MF_TILE - 1) / MF_TILE;
+    }
+    a.nunits = units;
+    *block_threads = 64 * nw;
+    *lds_bytes = mf_lds(nw, NB, a.glu != 0, a.seg[0].type == FLLM_TYPE_Q6_K);
+    // persistent grid: as many workgroups as fit on the device at once
+    MfKernel k = mf_kernel(a.seg[0].type, NB / nw);
+    (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, *block_threads, *lds_bytes) != hipSuccess ||
+        per_cu < 1)
+        per_cu = 1;
+    int grid = n_cu * per_cu;
+    return grid < units ? grid : units;
+}
+
 // Fill G, S, rpw and the segments' workgroup ranges; rows_per_wg 0 = choose.
 int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_threads, size_t* lds_bytes) {
+    a.mfma = 0;
+    if (rows_per_wg <= 0 && mfma_ok(a, cols)) {
+        const int NB = (int)(cols / 256);
+        if (mf_lds(mf_waves(NB), NB, a.glu != 0, a.seg[0].type == FLLM_TYPE_Q6_K) <= 160 * 1024)
+            return plan_mfma(a, cols, n_cu, block_threads, lds_bytes);
+    }
     a.G = (int)(cols / 32);
     int nslice = (a.G + 63) / 64;
     a.S = (a.G + nslice - 1) / nslice;
@@ -703,7 +1205,9 @@ int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_t
 
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st) {
     if (grid <= 0) return hipSuccess;
-    if (block_threads <= 512)
+    if (a.mfma)
+        mf_kernel(a.seg[0].type, (a.G / 8) / (block_threads / 64))<<<grid, block_threads, lds, st>>>(a);
+    else if (block_threads <= 512)
         k_gemv_fused<false><<<grid, block_threads, lds, st>>>(a);
     else
         k_gemv_fused<true><<<grid, block_threads, lds, st>>>(a);

@@ -30,6 +30,8 @@ struct GemvArgs {
     int rpw;               // rows per workgroup (multiple of 8)
     int glu;               // 1: seg[0] = gate, seg[1] = up, seg[0].out = act(gate x) * (up x)
     int act;               // 0 SiLU, 1 GELU (tanh form)
+    int mfma;              // set by gemv_plan: 1 = matrix-core variant
+    int nunits;            // matrix-core variant: 16-row units of the launch (seg[i].wg_begin = first unit)
     // input
     int xin;
     const float* x;        // XIN_F32 / XIN_NORM input vector
@@ -53,7 +55,8 @@ struct GemvArgs {
 
 bool gemv_fusable_type(int t);
 bool gemv_fusable_cols(int64_t cols);
-// Fills G, S, rpw and the segments' wg_begin; returns the grid size.
+// Fills G, S, rpw and the segments' wg_begin (or the MFMA variant's units); returns the grid
+// size. The MFMA variant is chosen only when every segment has the same weight type.
 int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_threads, size_t* lds_bytes);
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st);
 
