@@ -116,6 +116,10 @@ struct fllm_seq {
     float *g = nullptr, *u = nullptr, *h = nullptr, *tmp = nullptr, *logits = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
     unsigned long long* head_keys = nullptr;  // per-workgroup argmax keys of the fused LM head
+    // activation tables written by matrix-core epilogues for the next matrix-core launch: of the
+    // residual stream times the next RMSNorm weight (with per-16-row sums of squares), and of the
+    // FFN activation
+    float *tab_x = nullptr, *ssq_x = nullptr, *tab_h = nullptr;
     int* tokens_out = nullptr;
     int *topk_ids = nullptr, *topk_count = nullptr;
     float* topk_vals = nullptr;
@@ -610,6 +614,9 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->part_o, (size_t)d.n_heads * nparts * d.head_dim);
     ALLOC(s->part_ml, (size_t)d.n_heads * nparts * 2);
     ALLOC(s->head_keys, (size_t)d.vocab / 8 + 1);
+    ALLOC(s->tab_x, gemv_tab_bytes(d.hidden) / 4 + 4);
+    ALLOC(s->ssq_x, H / 16 + 1);
+    ALLOC(s->tab_h, gemv_tab_bytes(d.ffn) / 4 + 4);
     ALLOC(s->tokens_out, (size_t)s->max_seq);
     ALLOC(s->topk_ids, (size_t)d.vocab);
     ALLOC(s->topk_vals, (size_t)d.vocab);
@@ -819,9 +826,22 @@ static hipError_t head_generic(fllm_seq* s) {
     return hipSuccess;
 }
 
+// true when a launch over these matrices (GLU: gate, up) runs the matrix-core variant
+static bool mfma_launch(const Tensor* const* t, int n, int glu, int64_t cols) {
+    GemvArgs a{};
+    a.nseg = n;
+    a.glu = glu;
+    for (int i = 0; i < n; i++) { a.seg[i].w = t[i]->ptr; a.seg[i].type = t[i]->type; a.seg[i].rows = (int)t[i]->rows; }
+    return gemv_uses_mfma(a, cols);
+}
+
 // Decode step as fused launches: per layer [norm + QKV + RoPE + KV store], attention,
 // [Wo + residual], [norm + gate/up + activation], [down + residual]; then [norm + LM head +
 // softcap + argmax + step advance]. Gemma2's post-norms are separate small kernels.
+// Between matrix-core launches the activation vector travels as its quantized table: the
+// residual epilogues (Wo, down) write the table of x times the next RMSNorm weight plus partial
+// sums of squares, the gate/up epilogue the table of the FFN activation, and the next launch
+// copies it instead of quantizing the vector in every workgroup.
 static hipError_t enqueue_body_fused(fllm_seq* s) {
     fllm_model* m = s->m;
     const fllm_model_desc& d = m->d;
@@ -835,13 +855,21 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
     int et = m->tok_embd.type;
     bool emb_fused = et == FLLM_TYPE_F32 || et == FLLM_TYPE_F16 || et == FLLM_TYPE_BF16;
     if (!emb_fused) STEP("embed", 4.0 * H, launch_embed(m->tok_embd.ptr, et, H, s->params, s->x, s->st));
+    const Tensor* head_t[1] = {&m->output};
+    const bool head_mf = s->head_fused && !s->debug && mfma_launch(head_t, 1, 0, H);
+    bool xtab = false;  // tab_x / ssq_x hold the table of the current x for the next launch's norm
     for (int l = 0; l < d.n_layers; l++) {
         const Layer& L = m->layers[(size_t)l];
         float* kc = s->kc + (size_t)l * layer_kv;
         float* vc = s->vc + (size_t)l * layer_kv;
+        const Tensor* gu_t[2] = {&L.gate, &L.up};
+        const Tensor* o_t[1] = {&L.o};
+        const Tensor* dn_t[1] = {&L.down};
+        const bool o_mf = mfma_launch(o_t, 1, 0, m->qdim), gu_mf = mfma_launch(gu_t, 2, 1, H);
+        const bool dn_mf = mfma_launch(dn_t, 1, 0, d.ffn);
         {
             // q, k, v in one launch when they share a weight type, else one launch per run of
-            // equal types (each run's activation table follows its type's fragment order)
+            // equal types
             GemvSeg all[3] = {seg_of(L.q, EPI_Q, s->q, L.bq, nullptr), seg_of(L.k, EPI_K, nullptr, L.bk, nullptr),
                               seg_of(L.v, EPI_V, nullptr, L.bv, nullptr)};
             const Tensor* tens[3] = {&L.q, &L.k, &L.v};
@@ -854,6 +882,7 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
                 for (int i = i0; i < i1; i++) { a.seg[i - i0] = all[i]; bytes += (double)tens[i]->bytes + 4.0 * tens[i]->rows; }
                 a.xin = (l == 0 && emb_fused) ? XIN_EMBED_NORM : XIN_NORM;
                 a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
+                if (xtab && gemv_uses_mfma(a, H)) { a.xin = XIN_TAB; a.xtab = s->tab_x; a.xssq = s->ssq_x; }
                 a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
                 a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
                 hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
@@ -869,10 +898,13 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.seg[0] = gemma ? seg_of(L.o, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.o, EPI_RESID, s->x, nullptr, s->x);
             a.xin = XIN_F32;
             a.x = s->att;
+            xtab = !gemma && o_mf && gu_mf;
+            if (xtab) { a.tab_out = s->tab_x; a.ssq_out = s->ssq_x; a.tab_w = L.ffn_norm; a.tab_kind = nk; }
             e = fused_step(s, "attn_output", a, m->qdim, (double)L.o.bytes + 4.0 * (m->qdim + 2.0 * H));
             if (e != hipSuccess) return e;
             if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));
         }
+        const bool htab = gu_mf && dn_mf;
         {
             GemvArgs a{};
             a.nseg = 2;
@@ -882,6 +914,8 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.seg[1] = seg_of(L.up, EPI_STORE, nullptr, nullptr, nullptr);
             a.xin = XIN_NORM;
             a.x = s->x; a.norm_w = L.ffn_norm; a.eps = eps; a.norm_kind = nk;
+            if (xtab) { a.xin = XIN_TAB; a.xtab = s->tab_x; a.xssq = s->ssq_x; }
+            if (htab) a.tab_out = s->tab_h;
             e = fused_step(s, "ffn_gate_up", a, H, (double)(L.gate.bytes + L.up.bytes) + 4.0 * (2.0 * H + d.ffn));
             if (e != hipSuccess) return e;
         }
@@ -891,6 +925,19 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.seg[0] = gemma ? seg_of(L.down, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.down, EPI_RESID, s->x, nullptr, s->x);
             a.xin = XIN_F32;
             a.x = s->h;
+            if (htab) { a.xin = XIN_TAB; a.xtab = s->tab_h; }
+            // the next consumer of x: the next layer's q/k/v, or the LM head
+            bool next_mf = head_mf;
+            const float* next_w = m->out_norm;
+            if (l + 1 < d.n_layers) {
+                const Layer& N = m->layers[(size_t)l + 1];
+                const Tensor* qkv_t[3] = {&N.q, &N.k, &N.v};
+                next_mf = false;
+                for (int i = 0; i < 3; i++) next_mf = next_mf || mfma_launch(qkv_t + i, 1, 0, H);
+                next_w = N.attn_norm;
+            }
+            xtab = !gemma && dn_mf && next_mf;
+            if (xtab) { a.tab_out = s->tab_x; a.ssq_out = s->ssq_x; a.tab_w = next_w; a.tab_kind = nk; }
             e = fused_step(s, "ffn_down", a, d.ffn, (double)L.down.bytes + 4.0 * (d.ffn + 2.0 * H));
             if (e != hipSuccess) return e;
             if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, s->x, s->st));
@@ -903,6 +950,7 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
     a.seg[0] = seg_of(m->output, EPI_LOGITS, s->logits, nullptr, nullptr);
     a.xin = XIN_NORM;
     a.x = s->x; a.norm_w = m->out_norm; a.eps = eps; a.norm_kind = nk;
+    if (xtab && head_mf) { a.xin = XIN_TAB; a.xtab = s->tab_x; a.xssq = s->ssq_x; }
     a.softcap = (gemma && d.final_softcap > 0.0f) ? d.final_softcap : 0.0f;
     a.wg_keys = s->head_keys; a.params = s->params;
     int threads;

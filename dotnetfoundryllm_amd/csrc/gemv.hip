@@ -451,6 +451,8 @@ constexpr int GEMV_NR = 4;  // rows per batch
 // LM head, thread 0 folds this range's largest logit key into wg_best.
 // The segment's fields come by value (a by-reference aggregate selected at run time would be
 // copied to scratch memory).
+__device__ __forceinline__ void tab_emit(const GemvArgs& a, float v, float sq, int row_base, int rows, int lane);
+
 struct EpiSeg {
     int rows, epi;
     float* out;
@@ -460,6 +462,8 @@ struct EpiSeg {
 
 __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, const float* part, float* red, int nslice,
                                          int R, int T, int row_base, int wave, int lane, unsigned long long& wg_best) {
+    // value and squared raw output of this thread's row, for the activation table of the consumer
+    float tv = 0.0f, tq = 0.0f;
     if (a.glu) {
         // h = act(W_gate x) * (W_up x)
         for (int t = threadIdx.x; t < R; t += blockDim.x) {
@@ -467,8 +471,10 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
             if (r >= sg.rows) continue;
             float g = 0.0f, u = 0.0f;
             for (int sl = 0; sl < nslice; sl++) { g += part[sl * T + t]; u += part[sl * T + R + t]; }
-            sg.out[r] = act_fn(g, a.act) * u;
+            tv = act_fn(g, a.act) * u;
+            sg.out[r] = tv;
         }
+        if (a.tab_out && wave == 0) tab_emit(a, tv, 0.0f, row_base, sg.rows, lane);
         return;
     }
     const int epi = sg.epi;
@@ -530,7 +536,10 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
         float y = 0.0f;
         for (int sl = 0; sl < nslice; sl++) y += part[sl * T + t];
         if (epi == EPI_RESID) {
-            sg.out[r] = sg.resid[r] + y;
+            const float xr = sg.resid[r] + y;
+            sg.out[r] = xr;
+            tq = xr * xr;
+            tv = a.tab_w ? xr * (a.tab_kind ? 1.0f + a.tab_w[r] : a.tab_w[r]) : xr;
         } else if (epi == EPI_V) {
             if (sg.bias) y = y + sg.bias[r];
             a.vc[(int64_t)a.params->cur_len * a.kvdim + r] = y;
@@ -539,6 +548,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
             sg.out[r] = y;
         }
     }
+    if (a.tab_out && epi == EPI_RESID && wave == 0) tab_emit(a, tv, tq, row_base, sg.rows, lane);
 }
 
 // PREFETCH: the next batch's loads are issued before the current batch is dotted (two batches of
@@ -656,164 +666,200 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
 // receives the three digit sums of (row n, quarter Q) in its own D registers: digit combination
 // and the per-group block scales are applied lane-locally.
 //
-// In 4 MFMA steps a lane covers groups Q and Q+4 of the chunk (32 elements each); step s covers
-// group Q + 4*(s>>1) and, for the 4-bit K-quants, the elements of parity s&1 (even elements in
-// the low nibbles). The activation table in LDS holds, for every chunk, step, quarter and digit,
-// the 16 digit bytes in that same element order.
+// In 4 MFMA steps a lane covers groups Q and Q+4 of the chunk (32 elements each): step s is half
+// s&1 (elements 16(s&1) .. +15) of group Q + 4*(s>>1). Inside a step's 16-byte fragment, byte `by`
+// of dword j holds element 4*by + j of that half, for the weights (built from the GGUF bytes in
+// registers) and for the activation digits alike.
+//
+// Activation table (LDS, and in global memory when a producer epilogue writes it): per chunk 48
+// uint4 digit entries [step][quarter][digit], then per chunk 8 float4 group stats. Each 16-element
+// half is quantized on its own: X = rint(v * 65536 * 127 / amax), split into signed base-256 digits
+// X = 65536 b2 + 256 b1 + b0 (digit 0 = b2). Stats of group g: {scale of half 0, scale of half 1,
+// sum of half 0, sum of half 1}, scale = amax / 127, sums over the unquantized values.
 // =====================================================================================
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) f32x4 lds_f4;
+typedef __attribute__((address_space(3))) u32x4 lds_tab;
+// 16 and 8 bytes at 4-byte-aligned global addresses (Q6_K blocks are 210 bytes)
+typedef u32x4 u32x4a __attribute__((aligned(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef u32x2 u32x2a __attribute__((aligned(4)));
 
-constexpr int MF_TILE = 16;  // weight rows per MFMA tile
+constexpr int MF_TILE = 16;        // weight rows per MFMA tile
+// zeroed uint4 entries in LDS read as the A operand by lanes that carry no table row: as many as
+// the table entries one wave's KC chunks span
+#define MF_ZERO_ENTRIES(kc) ((kc) * 48)
+constexpr int MF_TAB_ENTRIES = 56; // uint4 entries of the activation table per chunk
 
 // bytes of 256 elements (one chunk) for the MFMA-capable types
 __host__ __device__ constexpr int mf_chunk_bytes(int t) {
     return t == FLLM_TYPE_Q4_K ? 144 : t == FLLM_TYPE_Q6_K ? 210 : 0;
 }
 
-// LDS activation table: per chunk 48 uint4 entries [step][quarter][digit], then per chunk 8
-// float4 group stats {s, sum, sum of elements 0..15, sum of elements 16..31}.
-__device__ __forceinline__ int atab_index(int b, int s, int q, int d) { return ((b * 4 + s) * 4 + q) * 3 + d; }
+__host__ __device__ __forceinline__ int atab_index(int b, int s, int q, int d) { return ((b * 4 + s) * 4 + q) * 3 + d; }
 
-// k order of a 16-byte MFMA fragment: which element of the 32-element group sits in byte
-// `byte` of dword `j` of step s.
-//  MF_PARITY (Q4_K): t = 4j + byte, element 2t + (s & 1)   (low nibbles hold even elements)
-//  MF_Q6K:           element 16(s & 1) + 4 byte + j        (byte = qh byte, j = its 2-bit field)
-enum { MF_PARITY = 0, MF_Q6K = 1 };
-
-template <int L>
-__device__ __forceinline__ int mf_elem(int s, int j, int byte) {
-    if constexpr (L == MF_PARITY) return 2 * (4 * j + byte) + (s & 1);
-    else return 16 * (s & 1) + 4 * byte + j;
+// signed base-256 digits of X = 65536 b2 + 256 b1 + b0
+__device__ __forceinline__ void digits3(int X, int& b2, int& b1, int& b0) {
+    b0 = (int)(int8_t)(X & 0xFF);
+    const int x1 = (X - b0) >> 8;
+    b1 = (int)(int8_t)(x1 & 0xFF);
+    b2 = (x1 - b1) >> 8;
 }
 
-// Digits of group g (0..7) of chunk b, written as the A fragments of the two steps that cover it
-// (steps 2(g>>2) and 2(g>>2)+1 of quarter g&3); returns the group stats.
-template <int L>
-__device__ __forceinline__ void atab_write(__attribute__((address_space(3))) u32x4* atab, int b, int g, const float* v,
-                                           float4* st) {
-    float amax = 0.0f, s16a = 0.0f, s16b = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) { s16a += v[i]; amax = fmaxf(amax, fabsf(v[i])); }
-#pragma unroll
-    for (int i = 16; i < 32; i++) { s16b += v[i]; amax = fmaxf(amax, fabsf(v[i])); }
-    float sc = 0.0f, inv = 0.0f;
-    if (amax > 0.0f) { sc = amax / 127.0f; inv = 127.0f / amax; }
+// One thread: the digit entries of group g (0..7) of chunk b from its 32 values; returns the
+// group stats.
+__device__ __forceinline__ void atab_write(lds_tab* atab, int b, int g, const float* v, float4* st) {
+    float sc[2], sm[2];
     int X[32];
 #pragma unroll
-    for (int i = 0; i < 32; i++) X[i] = (int)rintf(v[i] * inv * 65536.0f);
+    for (int h = 0; h < 2; h++) {
+        float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) { sum += v[16 * h + i]; amax = fmaxf(amax, fabsf(v[16 * h + i])); }
+        float inv = 0.0f;
+        sc[h] = 0.0f;
+        if (amax > 0.0f) { sc[h] = amax / 127.0f; inv = 127.0f / amax; }
+        sm[h] = sum;
+#pragma unroll
+        for (int i = 0; i < 16; i++) X[16 * h + i] = (int)rintf(v[16 * h + i] * inv * 65536.0f);
+    }
     const int q = g & 3, s0 = 2 * (g >> 2);
 #pragma unroll
-    for (int p = 0; p < 2; p++)
+    for (int h = 0; h < 2; h++) {
+        uint32_t w[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            int b2, b1, b0;
+            digits3(X[16 * h + e], b2, b1, b0);
+            const int j = e & 3, sh = 8 * (e >> 2);
+            w[0][j] |= (uint32_t)(b2 & 0xFF) << sh;
+            w[1][j] |= (uint32_t)(b1 & 0xFF) << sh;
+            w[2][j] |= (uint32_t)(b0 & 0xFF) << sh;
+        }
 #pragma unroll
         for (int d = 0; d < 3; d++) {
-            uint32_t w[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                uint32_t acc = 0;
-#pragma unroll
-                for (int by = 0; by < 4; by++) {
-                    // signed base-256 digits of X: X = 65536 b2 + 256 b1 + b0
-                    const int x = X[mf_elem<L>(p, j, by)];
-                    const int b0 = (int)(int8_t)(x & 0xFF);
-                    const int x1 = (x - b0) >> 8;
-                    const int b1 = (int)(int8_t)(x1 & 0xFF);
-                    const int dv = d == 0 ? (x1 - b1) >> 8 : d == 1 ? b1 : b0;
-                    acc |= (uint32_t)(dv & 0xFF) << (8 * by);
-                }
-                w[j] = acc;
-            }
-            u32x4 e = {w[0], w[1], w[2], w[3]};
-            atab[atab_index(b, s0 + p, q, d)] = e;
+            u32x4 e4 = {w[d][0], w[d][1], w[d][2], w[d][3]};
+            atab[atab_index(b, s0 + h, q, d)] = e4;
         }
-    *st = make_float4(sc, s16a + s16b, s16a, s16b);
+    }
+    *st = make_float4(sc[0], sc[1], sm[0], sm[1]);
+}
+
+// Producer side of the table, for a consumer whose columns are this launch's rows: lanes 0..15 of
+// the calling wave hold v for rows row_base .. row_base + 15 (one half of a group; other lanes hold
+// 0) and sq, the square of the raw output for the consumer's RMSNorm. Writes the half's three
+// digit entries, its scale and sum, and its sum of squares.
+__device__ __forceinline__ void tab_emit(const GemvArgs& a, float v, float sq, int row_base, int rows, int lane) {
+    float amax = fabsf(v), sum = v, ssq = sq;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o));
+        sum += __shfl_xor(sum, o);
+        ssq += __shfl_xor(ssq, o);
+    }
+    float sc = 0.0f, inv = 0.0f;
+    if (amax > 0.0f) { sc = amax / 127.0f; inv = 127.0f / amax; }
+    int b2, b1, b0;
+    digits3((int)rintf(v * inv * 65536.0f), b2, b1, b0);
+    const int h16 = row_base >> 4, g32 = h16 >> 1, half = h16 & 1, b = g32 >> 3, gg = g32 & 7;
+    const int s = 2 * (gg >> 2) + half, q = gg & 3, j = lane & 3;
+    // dword j of each digit entry: bytes from elements j, 4 + j, 8 + j, 12 + j
+    uint32_t w2 = 0u, w1 = 0u, w0 = 0u;
+#pragma unroll
+    for (int by = 0; by < 4; by++) {
+        const int src = j + 4 * by;
+        w2 |= (uint32_t)(__shfl(b2, src) & 0xFF) << (8 * by);
+        w1 |= (uint32_t)(__shfl(b1, src) & 0xFF) << (8 * by);
+        w0 |= (uint32_t)(__shfl(b0, src) & 0xFF) << (8 * by);
+    }
+    uint32_t* tab = (uint32_t*)a.tab_out;
+    if (lane < 4) {
+        tab[4 * atab_index(b, s, q, 0) + j] = w2;
+        tab[4 * atab_index(b, s, q, 1) + j] = w1;
+        tab[4 * atab_index(b, s, q, 2) + j] = w0;
+    }
+    if (lane == 0) {
+        float* st = (float*)(tab + 4 * (size_t)(rows / 256) * 48) + 4 * (8 * b + gg);
+        st[half] = sc;
+        st[2 + half] = sum;
+        if (a.ssq_out) a.ssq_out[h16] = ssq;
+    }
 }
 
 __device__ __forceinline__ float mf_total(const v4i& D) {
-    return (float)D.x + (float)D.y * 0.00390625f + (float)D.z * 1.52587890625e-05f;
+    return fmaf((float)D.z, 1.52587890625e-05f, fmaf((float)D.y, 0.00390625f, (float)D.x));
 }
 
-// Per-wave LDS staging area of the MFMA variant: 16 rows x 224 bytes (one Q6_K block per row
-// plus its 16-byte alignment phase).
-constexpr int MF_STAGE_ROW = 224;
-constexpr int MF_STAGE_BYTES = 16 * MF_STAGE_ROW;
-
-// ---- Q4_K (Dequantizer.cs:251-294): 16-byte-aligned 144-byte blocks, loaded directly -------
+// ---- Q4_K (Dequantizer.cs:251-294): 16-byte-aligned 144-byte blocks ---------------------------
+// Group g's 32 elements are bytes 16g .. 16g+15 of qs, element i in the low (even i) or high nibble
+// of byte i/2.
 struct MfQ4K { uint4 hdr, qa, qb; };
-__device__ __forceinline__ void mf_issue(MfQ4K& r, const uint8_t* __restrict__ W, int64_t rb, int rows, int row0,
-                                         int b, int lane) {
-    const int n = lane & 15, q = lane >> 4;
-    const int row = min(row0 + n, rows - 1);
-    const uint8_t* cb = W + (int64_t)row * rb + (int64_t)b * 144;
-    r.hdr = *(const uint4*)cb;
-    r.qa = *(const uint4*)(cb + 16 + 16 * q);   // group q
-    r.qb = *(const uint4*)(cb + 80 + 16 * q);   // group q + 4
+__device__ __forceinline__ void mf_issue(MfQ4K& r, const uint8_t* __restrict__ W, uint32_t off, int c, int, int q) {
+    const uint8_t* p = W + off + (uint32_t)(c * 144);
+    r.hdr = *(const uint4*)p;
+    r.qa = *(const uint4*)(p + 16 + 16 * q);   // group q
+    r.qb = *(const uint4*)(p + 80 + 16 * q);   // group q + 4
 }
 
-__device__ __forceinline__ v4i nib(const uint4& w, int p) {
-    const int sh = 4 * p;
-    v4i r = {(int)((w.x >> sh) & 0x0F0F0F0Fu), (int)((w.y >> sh) & 0x0F0F0F0Fu), (int)((w.z >> sh) & 0x0F0F0F0Fu),
-             (int)((w.w >> sh) & 0x0F0F0F0Fu)};
+// fragment of one half-group from its 8 qs bytes: dword j = elements j, 4+j, 8+j, 12+j
+__device__ __forceinline__ v4i q4_frag(uint32_t w0, uint32_t w1) {
+    const uint32_t E = __builtin_amdgcn_perm(w1, w0, 0x06040200u);  // bytes 0, 2, 4, 6: elements 4by, 4by+1
+    const uint32_t O = __builtin_amdgcn_perm(w1, w0, 0x07050301u);  // bytes 1, 3, 5, 7: elements 4by+2, 4by+3
+    v4i r = {(int)(E & 0x0F0F0F0Fu), (int)((E >> 4) & 0x0F0F0F0Fu), (int)(O & 0x0F0F0F0Fu),
+             (int)((O >> 4) & 0x0F0F0F0Fu)};
     return r;
 }
 
 // 4 MFMAs over groups q and q+4 and their block scales; this lane's part of row n.
-__device__ __forceinline__ float mf_compute(const MfQ4K& r, const v4i* A, const float4& sA, const float4& sB, int q,
-                                            __attribute__((address_space(3))) uint8_t*, const uint8_t*, int64_t, int,
-                                            int, int) {
-    v4i z = {0, 0, 0, 0};
-    v4i Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], nib(r.qa, 0), z, 0, 0, 0);
-    Da = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], nib(r.qa, 1), Da, 0, 0, 0);
-    v4i Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], nib(r.qb, 0), z, 0, 0, 0);
-    Db = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], nib(r.qb, 1), Db, 0, 0, 0);
+__device__ __forceinline__ float mf_compute(const MfQ4K& r, const v4i* A, const f32x4& sA, const f32x4& sB, int q,
+                                            int) {
+    const v4i z = {0, 0, 0, 0};
+    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], q4_frag(r.qa.x, r.qa.y), z, 0, 0, 0);
+    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], q4_frag(r.qa.z, r.qa.w), z, 0, 0, 0);
+    const v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], q4_frag(r.qb.x, r.qb.y), z, 0, 0, 0);
+    const v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], q4_frag(r.qb.z, r.qb.w), z, 0, 0, 0);
     // DecodeKScaleMin (Dequantizer.cs:506-521) for groups q (< 4) and q + 4
     const int sh = 8 * q;
-    uint32_t a = (r.hdr.y >> sh) & 0xFF, b = (r.hdr.z >> sh) & 0xFF, c = (r.hdr.w >> sh) & 0xFF;
-    int scA = (int)(a & 63), mnA = (int)(b & 63);
-    int scB = (int)((c & 15) | ((a >> 6) << 4)), mnB = (int)((c >> 4) | ((b >> 6) << 4));
-    float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
-    float dgA = d * (float)scA, mgA = dmin * (float)mnA;
-    float dgB = d * (float)scB, mgB = dmin * (float)mnB;
-    float y = dgA * (sA.x * mf_total(Da)) - mgA * sA.y;
-    y = y + (dgB * (sB.x * mf_total(Db)) - mgB * sB.y);
-    return y;
+    const uint32_t a = (r.hdr.y >> sh) & 0xFF, b = (r.hdr.z >> sh) & 0xFF, c = (r.hdr.w >> sh) & 0xFF;
+    const int scA = (int)(a & 63), mnA = (int)(b & 63);
+    const int scB = (int)((c & 15) | ((a >> 6) << 4)), mnB = (int)((c >> 4) | ((b >> 6) << 4));
+    const float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
+    const float dgA = d * (float)scA, mgA = dmin * (float)mnA;
+    const float dgB = d * (float)scB, mgB = dmin * (float)mnB;
+    const float tA = fmaf(sA.x, mf_total(D0), sA.y * mf_total(D1));
+    const float tB = fmaf(sB.x, mf_total(D2), sB.y * mf_total(D3));
+    const float y = fmaf(dgA, tA, -mgA * (sA.z + sA.w));
+    return y + fmaf(dgB, tB, -mgB * (sB.z + sB.w));
 }
 
-// ---- Q6_K (Dequantizer.cs:378-417): 210-byte blocks, staged through LDS ------------------------
-// The wave copies the 16-byte-aligned window of each tile row's block (224 bytes) with coalesced
-// 16-byte loads; lanes then read their fields from LDS.
-struct MfQ6K { uint4 c[4]; };
-__device__ __forceinline__ void mf_issue(MfQ6K& r, const uint8_t* __restrict__ W, int64_t rb, int rows, int row0,
-                                         int b, int lane) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int c = lane + 64 * i;
-        if (c < 16 * 14) {
-            int row = min(row0 + c / 14, rows - 1);
-            uintptr_t bp = (uintptr_t)(W + (int64_t)row * rb + (int64_t)b * 210);
-            r.c[i] = *(const uint4*)((bp & ~(uintptr_t)15) + 16 * (c % 14));
-        }
-    }
+// ---- Q6_K (Dequantizer.cs:378-417): 210-byte blocks -------------------------------------------
+// A block starts 0 or 2 bytes past a 4-byte boundary (mis); each lane loads the dword-aligned
+// windows of its fields and realigns them in registers. ql of group g: bytes 16g .. +15, qh of
+// group g: bytes 128 + 8g .. +7, int8 scales at 192 (one per 16 elements), f16 d at 208.
+struct MfQ6K { uint32_t la[5], lb[5], ha[3], hb[3], sa, sb, d; };
+__device__ __forceinline__ void mf_issue(MfQ6K& r, const uint8_t* __restrict__ W, uint32_t off, int c, int mis,
+                                         int q) {
+    const uint8_t* blk = W + off + (uint32_t)(c * 210);
+    const uint8_t* p = blk - mis;
+    u32x4 t = *(const u32x4a*)(p + 16 * q);
+    r.la[0] = t.x; r.la[1] = t.y; r.la[2] = t.z; r.la[3] = t.w;
+    r.la[4] = *(const uint32_t*)(p + 16 + 16 * q);
+    t = *(const u32x4a*)(p + 64 + 16 * q);
+    r.lb[0] = t.x; r.lb[1] = t.y; r.lb[2] = t.z; r.lb[3] = t.w;
+    r.lb[4] = *(const uint32_t*)(p + 80 + 16 * q);
+    u32x2 h = *(const u32x2a*)(p + 128 + 8 * q);
+    r.ha[0] = h.x; r.ha[1] = h.y;
+    r.ha[2] = *(const uint32_t*)(p + 136 + 8 * q);
+    h = *(const u32x2a*)(p + 160 + 8 * q);
+    r.hb[0] = h.x; r.hb[1] = h.y;
+    r.hb[2] = *(const uint32_t*)(p + 168 + 8 * q);
+    r.sa = *(const uint16_t*)(blk + 192 + 2 * q);  // scales 2q, 2q + 1
+    r.sb = *(const uint16_t*)(blk + 200 + 2 * q);  // scales 2q + 8, 2q + 9
+    r.d = *(const uint16_t*)(blk + 208);
 }
 
-__device__ __forceinline__ uint32_t ldsw(__attribute__((address_space(3))) const uint8_t* p) {
-    return *(__attribute__((address_space(3))) const uint32_t*)p;
-}
-
-// n realigned dwords starting at LDS byte address p (2-byte aligned)
-template <int N>
-__device__ __forceinline__ void lds_words(__attribute__((address_space(3))) const uint8_t* p, uint32_t* out) {
-    const uint32_t mis = (uint32_t)(uintptr_t)p & 3u;
-    __attribute__((address_space(3))) const uint8_t* a = p - mis;
-    uint32_t w[N + 1];
-#pragma unroll
-    for (int i = 0; i <= N; i++) w[i] = ldsw(a + 4 * i);
-#pragma unroll
-    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], mis);
-}
-
-// fragment of step half h: 8 ql bytes (2 dwords) and the 4 qh bytes of those 16 elements;
+// fragment of one half-group: 8 ql bytes (2 dwords) and the 4 qh bytes of those 16 elements;
 // byte `by` of dword j = element 4by + j: low nibble of ql byte 2by + (j>>1), 2 high bits =
 // field j of qh byte by
 __device__ __forceinline__ v4i q6_frag(uint32_t l0, uint32_t l1, uint32_t hq) {
@@ -827,61 +873,44 @@ __device__ __forceinline__ v4i q6_frag(uint32_t l0, uint32_t l1, uint32_t hq) {
     return r;
 }
 
-__device__ __forceinline__ float mf_compute(const MfQ6K& r, const v4i* A, const float4& sA, const float4& sB, int q,
-                                            __attribute__((address_space(3))) uint8_t* stage, const uint8_t* W,
-                                            int64_t rb, int rows, int row0, int b) {
-    const int lane = threadIdx.x & 63, n = lane & 15;
-    // the previous chunk's LDS reads are done before this chunk's staging writes
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+__device__ __forceinline__ float mf_compute(const MfQ6K& r, const v4i* A, const f32x4& sA, const f32x4& sB, int,
+                                            int mis) {
+    uint32_t la[4], lb[4], ha[2], hb[2];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        int c = lane + 64 * i;
-        if (c < 16 * 14) {
-            uint4 v = r.c[i];
-            u32x4 t = {v.x, v.y, v.z, v.w};
-            *(__attribute__((address_space(3))) u32x4*)(stage + (c / 14) * MF_STAGE_ROW + 16 * (c % 14)) = t;
-        }
+        la[i] = __builtin_amdgcn_alignbyte(r.la[i + 1], r.la[i], mis);
+        lb[i] = __builtin_amdgcn_alignbyte(r.lb[i + 1], r.lb[i], mis);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // row n's block sits at its 16-byte alignment phase inside its staged window
-    const int row = min(row0 + n, rows - 1);
-    const uint32_t ph = (uint32_t)((uintptr_t)(W + (int64_t)row * rb + (int64_t)b * 210) & 15u);
-    __attribute__((address_space(3))) const uint8_t* blk = stage + n * MF_STAGE_ROW + ph;
-    uint32_t la[4], lb[4], ha[2], hb[2];
-    lds_words<4>(blk + 16 * q, la);          // ql of group q
-    lds_words<4>(blk + 64 + 16 * q, lb);     // ql of group q + 4
-    lds_words<2>(blk + 128 + 8 * q, ha);     // qh of group q
-    lds_words<2>(blk + 160 + 8 * q, hb);     // qh of group q + 4
-    const uint32_t sca = *(__attribute__((address_space(3))) const uint16_t*)(blk + 192 + 2 * q);  // scales 2q, 2q+1
-    const uint32_t scb = *(__attribute__((address_space(3))) const uint16_t*)(blk + 200 + 2 * q);  // scales 2q+8, 2q+9
-    const float d = h2f(*(__attribute__((address_space(3))) const uint16_t*)(blk + 208));
-    v4i z = {0, 0, 0, 0};
-    v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], q6_frag(la[0], la[1], ha[0]), z, 0, 0, 0);
-    v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], q6_frag(la[2], la[3], ha[1]), z, 0, 0, 0);
-    v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], q6_frag(lb[0], lb[1], hb[0]), z, 0, 0, 0);
-    v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], q6_frag(lb[2], lb[3], hb[1]), z, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        ha[i] = __builtin_amdgcn_alignbyte(r.ha[i + 1], r.ha[i], mis);
+        hb[i] = __builtin_amdgcn_alignbyte(r.hb[i + 1], r.hb[i], mis);
+    }
+    const v4i z = {0, 0, 0, 0};
+    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], q6_frag(la[0], la[1], ha[0]), z, 0, 0, 0);
+    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], q6_frag(la[2], la[3], ha[1]), z, 0, 0, 0);
+    const v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], q6_frag(lb[0], lb[1], hb[0]), z, 0, 0, 0);
+    const v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], q6_frag(lb[2], lb[3], hb[1]), z, 0, 0, 0);
     // y = (d * sc) * (q - 32) per element: (d * sc) * (s_x T - 32 * sum of the 16 activations)
-    float y = (d * (float)(int8_t)(sca & 0xFF)) * (sA.x * mf_total(D0) - 32.0f * sA.z);
-    y = y + (d * (float)(int8_t)(sca >> 8)) * (sA.x * mf_total(D1) - 32.0f * sA.w);
-    y = y + (d * (float)(int8_t)(scb & 0xFF)) * (sB.x * mf_total(D2) - 32.0f * sB.z);
-    y = y + (d * (float)(int8_t)(scb >> 8)) * (sB.x * mf_total(D3) - 32.0f * sB.w);
-    return y;
+    const float d = h2f(r.d);
+    float y = (float)(int8_t)(r.sa & 0xFF) * fmaf(sA.x, mf_total(D0), -32.0f * sA.z);
+    y = fmaf((float)(int8_t)(r.sa >> 8), fmaf(sA.y, mf_total(D1), -32.0f * sA.w), y);
+    y = fmaf((float)(int8_t)(r.sb & 0xFF), fmaf(sB.x, mf_total(D2), -32.0f * sB.z), y);
+    y = fmaf((float)(int8_t)(r.sb >> 8), fmaf(sB.y, mf_total(D3), -32.0f * sB.w), y);
+    return d * y;
 }
 
 template <int T> struct MfPick;
-template <> struct MfPick<FLLM_TYPE_Q4_K> { using Raw = MfQ4K; static constexpr int L = MF_PARITY; static constexpr bool STAGE = false; };
-template <> struct MfPick<FLLM_TYPE_Q6_K> { using Raw = MfQ6K; static constexpr int L = MF_Q6K; static constexpr bool STAGE = true; };
+template <> struct MfPick<FLLM_TYPE_Q4_K> { using Raw = MfQ4K; };
+template <> struct MfPick<FLLM_TYPE_Q6_K> { using Raw = MfQ6K; };
 
 // Persistent workgroup body of the MFMA variant for weight type T. The launch's rows form units:
 // one 16-row tile, or for GLU the gate and up tiles of the same 16 rows. Workgroup w takes units
 // w, w + grid, w + 2 grid, ...; each of its nw waves covers KC = NB / nw consecutive chunks of every
 // row, so all waves walk the same (tile, chunk) item sequence: item i is chunk i % KC of the
 // workgroup's tile i / KC. Items stream through a ring of MF_RING chunk loads in flight that runs
-// across tile and unit boundaries; the first loads go out before the activation prologue.
+// across tile and unit boundaries; the first loads go out before the activation prologue. A lane's
+// load addresses are its tile row's offset (computed once per tile) plus constants.
 constexpr int MF_RING = 4;
 
 // unit u -> matrix of tile ts (0: gate / the segment's own, 1: up), its rows, first row, segment
@@ -896,18 +925,22 @@ __device__ __forceinline__ void mf_tile_of(const GemvArgs& a, int u, int ts, con
     row0 = tile * MF_TILE;
 }
 
-// workgroup tile index t -> unit and tile-in-unit
-__device__ __forceinline__ void mf_tile_unit(const GemvArgs& a, int t, int& u, int& ts) {
-    const int k = a.glu ? (t >> 1) : t;
-    ts = a.glu ? (t & 1) : 0;
-    u = (int)blockIdx.x + k * (int)gridDim.x;
+// workgroup tile t: its matrix and this lane's byte offset of chunk kb0 of row n of the tile
+__device__ __forceinline__ uint32_t mf_tile_base(const GemvArgs& a, int t, int ltpu, uint32_t rb, uint32_t kboff,
+                                                 int n, const uint8_t*& W) {
+    const int u = (int)blockIdx.x + (t >> ltpu) * (int)gridDim.x;
+    int rows, row0, si;
+    mf_tile_of(a, u, t & ((1 << ltpu) - 1), W, rows, row0, si);
+    const int row = min(row0 + n, rows - 1);
+    return (uint32_t)row * rb + kboff;
 }
 
 template <int T, int KC>
 __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
     using Raw = typename MfPick<T>::Raw;
-    constexpr int L = MfPick<T>::L;
+    constexpr int CB = mf_chunk_bytes(T);
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
+    constexpr int U = KC > MF_RING ? KC : MF_RING;  // items per unrolled iteration
     extern __shared__ float lds[];
     const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -915,136 +948,154 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
     const bool a_live = (m >> 2) == q && (m & 3) < 3;  // A row m = 4Q' + d lives in quarter Q'
     const int NB = a.G / 8;            // chunks per row (NB == nw * KC)
     const int kb0 = wave * KC;
-    const int tpu = a.glu ? 2 : 1;     // tiles per unit
-    const int T_slots = tpu * MF_TILE;
+    const int ltpu = a.glu ? 1 : 0;    // log2 of tiles per unit
+    const int T_slots = MF_TILE << ltpu;
     float* part = lds;                         // [nw][T_slots]
     float* red = lds + nw * T_slots;           // [16] + 16 u64
-    __attribute__((address_space(3))) u32x4* atab = (__attribute__((address_space(3))) u32x4*)(red + 48);
+    lds_tab* zeros = (lds_tab*)(red + 48);     // A operand of lanes without a table row
+    lds_tab* atab = zeros + MF_ZERO_ENTRIES(KC);
     lds_f4* stats = (lds_f4*)(atab + NB * 48);
-    __attribute__((address_space(3))) uint8_t* stage =
-        (__attribute__((address_space(3))) uint8_t*)(stats + NB * 8) + wave * MF_STAGE_BYTES;
-    const int64_t rb = (int64_t)NB * mf_chunk_bytes(T);
+    // fragment (chunk kb0 + c, step s) of this lane: abase[(4c + s) * 12]
+    lds_tab* const abase = a_live ? atab + atab_index(kb0, 0, m >> 2, m & 3) : zeros;
+    const uint32_t rb = (uint32_t)NB * CB, kboff = (uint32_t)kb0 * CB;
     const int grid = (int)gridDim.x;
     const int my_units = (a.nunits - (int)blockIdx.x + grid - 1) / grid;
-    const int items = my_units * tpu * KC;
+    const int items = (my_units << ltpu) * KC;
 
     Raw ring[MF_RING];
+    const uint8_t* Wr = a.seg[0].w;  // matrix and lane offset of the tile of the latest load
+    uint32_t offr = 0;
 #pragma unroll
     for (int r = 0; r < MF_RING; r++) {
         if (r < items) {
-            int u, ts, rows, row0, si;
-            const uint8_t* W;
-            mf_tile_unit(a, r >> LKC, u, ts);
-            mf_tile_of(a, u, ts, W, rows, row0, si);
-            mf_issue(ring[r], W, rb, rows, row0, kb0 + (r & (KC - 1)), lane);
+            const int c = r & (KC - 1);
+            if (c == 0) offr = mf_tile_base(a, r >> LKC, ltpu, rb, kboff, m, Wr);
+            mf_issue(ring[r], Wr, offr, c, ((kb0 + c) & 1) * 2, q);
         }
     }
 
-    // ---- prologue: (normed) activations -> digit table, one 32-element group per thread --------
-    float scale = 1.0f;
-    if (a.xin != XIN_F32) {
-        float ssq = 0.0f;
+    // ---- prologue: the activation table -------------------------------------------------------
+    for (int e = threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += blockDim.x) {
+        const u32x4 z4 = {0u, 0u, 0u, 0u};
+        zeros[e] = z4;
+    }
+    float xs = 1.0f;  // RMSNorm factor of a table of raw (weighted) values
+    if (a.xin == XIN_TAB) {
+        const u32x4* src = (const u32x4*)a.xtab;
+        for (int e = threadIdx.x; e < NB * MF_TAB_ENTRIES; e += blockDim.x) atab[e] = src[e];
+        if (a.xssq) {
+            float s2 = 0.0f;
+            for (int e = lane; e < 2 * a.G; e += 64) s2 += a.xssq[e];
+            s2 = wsum(s2);
+            xs = 1.0f / sqrtf(s2 / (float)(a.G * 32) + a.eps);
+        }
+    } else {
+        float scale = 1.0f;
+        if (a.xin != XIN_F32) {
+            float ssq = 0.0f;
+            for (int g = threadIdx.x; g < a.G; g += blockDim.x) {
+                float v[32];
+                if (a.xin == XIN_EMBED_NORM) deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
+                else {
+                    const float4* xi = (const float4*)(a.x + g * 32);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
+                }
+#pragma unroll
+                for (int i = 0; i < 32; i++) ssq = fmaf(v[i], v[i], ssq);
+            }
+            ssq = wsum(ssq);
+            if (lane == 0) red[wave] = ssq;
+            __syncthreads();
+            float tot = 0.0f;
+            for (int i = 0; i < nw; i++) tot += red[i];
+            scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
+        }
         for (int g = threadIdx.x; g < a.G; g += blockDim.x) {
             float v[32];
-            if (a.xin == XIN_EMBED_NORM) deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
-            else {
+            if (a.xin == XIN_EMBED_NORM) {
+                deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
+                if (blockIdx.x == 0) {
+                    float4* xo = (float4*)(a.x_out + g * 32);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+                }
+            } else {
                 const float4* xi = (const float4*)(a.x + g * 32);
 #pragma unroll
                 for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
             }
+            if (a.xin != XIN_F32) {
+                const float4* wv = (const float4*)(a.norm_w + g * 32);
 #pragma unroll
-            for (int i = 0; i < 32; i++) ssq = fmaf(v[i], v[i], ssq);
-        }
-        ssq = wsum(ssq);
-        if (lane == 0) red[wave] = ssq;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int i = 0; i < nw; i++) tot += red[i];
-        scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
-    }
-    for (int g = threadIdx.x; g < a.G; g += blockDim.x) {
-        float v[32];
-        if (a.xin == XIN_EMBED_NORM) {
-            deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
-            if (blockIdx.x == 0) {
-                float4* xo = (float4*)(a.x_out + g * 32);
+                for (int i = 0; i < 8; i++) {
+                    float4 w4 = wv[i];
+                    float ww[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-                for (int i = 0; i < 8; i++) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-            }
-        } else {
-            const float4* xi = (const float4*)(a.x + g * 32);
-#pragma unroll
-            for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
-        }
-        if (a.xin != XIN_F32) {
-            const float4* wv = (const float4*)(a.norm_w + g * 32);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float4 w4 = wv[i];
-                float ww[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float t = v[4 * i + e] * scale;
-                    v[4 * i + e] = a.norm_kind ? t * (ww[e] + 1.0f) : t * ww[e];
+                    for (int e = 0; e < 4; e++) {
+                        float t = v[4 * i + e] * scale;
+                        v[4 * i + e] = a.norm_kind ? t * (ww[e] + 1.0f) : t * ww[e];
+                    }
                 }
             }
+            float4 st;
+            atab_write(atab, g >> 3, g & 7, v, &st);
+            f32x4 stv = {st.x, st.y, st.z, st.w};
+            stats[(g >> 3) * 8 + (g & 7)] = stv;
         }
-        float4 st;
-        atab_write<L>(atab, g >> 3, g & 7, v, &st);
-        f32x4 stv = {st.x, st.y, st.z, st.w};
-        stats[(g >> 3) * 8 + (g & 7)] = stv;
     }
     __syncthreads();
 
     // ---- items ----------------------------------------------------------------------------------
     unsigned long long best = 0ull;
     float y = 0.0f;
-    int tu, tts, trows, trow0, tsi;  // the current tile
-    const uint8_t* tW;
-    for (int i0 = 0; i0 < items; i0 += MF_RING) {
+    for (int i0 = 0; i0 < items; i0 += U) {
+        // the fragments are the same for every tile; re-reading them from LDS each time keeps them
+        // out of registers (the base is opaque to the compiler, so the reads stay in the loop)
+        lds_tab* at = abase;
+        lds_f4* stt = stats;
+        __asm__ volatile("" : "+v"(at), "+v"(stt));
 #pragma unroll
-        for (int r = 0; r < MF_RING; r++) {
+        for (int r = 0; r < U; r++) {
             const int i = i0 + r;
-            if (i >= items) break;
-            const int c = i & (KC - 1);
-            if (c == 0) {
-                mf_tile_unit(a, i >> LKC, tu, tts);
-                mf_tile_of(a, tu, tts, tW, trows, trow0, tsi);
-            }
-            const int b = kb0 + c;
+            if (KC < MF_RING && i >= items) break;
+            const int c = r & (KC - 1), slot = r & (MF_RING - 1), b = kb0 + c;
             v4i A[4];
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                v4i z = {0, 0, 0, 0};
-                A[s] = a_live ? *(__attribute__((address_space(3))) const v4i*)&atab[atab_index(b, s, m >> 2, m & 3)] : z;
-            }
-            f32x4 ta = stats[b * 8 + q], tb = stats[b * 8 + q + 4];
-            y += mf_compute(ring[r], A, make_float4(ta.x, ta.y, ta.z, ta.w), make_float4(tb.x, tb.y, tb.z, tb.w), q, stage,
-                            tW, rb, trows, trow0, b);
+            for (int s = 0; s < 4; s++) A[s] = *(__attribute__((address_space(3))) const v4i*)&at[(4 * c + s) * 12];
+            const f32x4 sa = stt[b * 8 + q], sb = stt[b * 8 + q + 4];
+            y += mf_compute(ring[slot], A, sa, sb, q, ((kb0 + c) & 1) * 2);
+            // finish this item's arithmetic here (sinking it to the tile's end keeps every item's
+            // MFMA results live)
+            __asm__ volatile("" : "+v"(y));
             // refill this ring slot with the item MF_RING ahead (possibly of another tile or unit)
-            const int ni = i + MF_RING;
-            if (ni < items) {
-                int u2, ts2, rows2, row02, si2;
-                const uint8_t* W2;
-                mf_tile_unit(a, ni >> LKC, u2, ts2);
-                mf_tile_of(a, u2, ts2, W2, rows2, row02, si2);
-                mf_issue(ring[r], W2, rb, rows2, row02, kb0 + (ni & (KC - 1)), lane);
+            if (i + MF_RING < items) {
+                const int cn = (r + MF_RING) & (KC - 1);
+                if (cn == 0) offr = mf_tile_base(a, (i + MF_RING) >> LKC, ltpu, rb, kboff, m, Wr);
+                mf_issue(ring[slot], Wr, offr, cn, ((kb0 + cn) & 1) * 2, q);
             }
+            // keep each item's fragment reads next to its MFMAs (hoisting them all to the top of the
+            // unrolled iteration costs registers, not time)
+            __builtin_amdgcn_sched_barrier(0);
             if (c == KC - 1) {
                 // last chunk of the tile: the four quarters of row n, then this wave's partial
+                const int ti = i >> LKC, tt = ti & ((1 << ltpu) - 1);
                 float yt = y + __shfl_xor(y, 16);
                 yt += __shfl_xor(yt, 32);
-                if (lane < 16) part[wave * T_slots + tts * MF_TILE + lane] = (trow0 + lane < trows) ? yt : 0.0f;
+                if (lane < 16) part[wave * T_slots + tt * MF_TILE + lane] = yt * xs;
                 y = 0.0f;
-                if (tts == tpu - 1) {
+                if (tt == (1 << ltpu) - 1) {
                     // last tile of the unit (same item in every wave): combine the waves, epilogue
+                    const uint8_t* Wu;
+                    int rows, row0, si;
+                    mf_tile_of(a, (int)blockIdx.x + (ti >> ltpu) * grid, 0, Wu, rows, row0, si);
                     __syncthreads();
-                    const EpiSeg es{tsi == 0 ? a.seg[0].rows : tsi == 1 ? a.seg[1].rows : a.seg[2].rows,
-                                    tsi == 0 ? a.seg[0].epi : tsi == 1 ? a.seg[1].epi : a.seg[2].epi,
-                                    tsi == 0 ? a.seg[0].out : tsi == 1 ? a.seg[1].out : a.seg[2].out,
-                                    tsi == 0 ? a.seg[0].bias : tsi == 1 ? a.seg[1].bias : a.seg[2].bias,
-                                    tsi == 0 ? a.seg[0].resid : tsi == 1 ? a.seg[1].resid : a.seg[2].resid};
-                    epilogue(a, es, part, red, nw, MF_TILE, T_slots, trow0, wave, lane, best);
+                    const EpiSeg es{si == 0 ? a.seg[0].rows : si == 1 ? a.seg[1].rows : a.seg[2].rows,
+                                    si == 0 ? a.seg[0].epi : si == 1 ? a.seg[1].epi : a.seg[2].epi,
+                                    si == 0 ? a.seg[0].out : si == 1 ? a.seg[1].out : a.seg[2].out,
+                                    si == 0 ? a.seg[0].bias : si == 1 ? a.seg[1].bias : a.seg[2].bias,
+                                    si == 0 ? a.seg[0].resid : si == 1 ? a.seg[1].resid : a.seg[2].resid};
+                    epilogue(a, es, part, red, nw, MF_TILE, T_slots, row0, wave, lane, best);
                     __syncthreads();
                 }
             }
@@ -1123,17 +1174,30 @@ static int mf_waves(int NB) {
 }
 
 static bool mfma_ok(const GemvArgs& a, int64_t cols) {
-    if (cols % 256 != 0 || mf_waves((int)(cols / 256)) == 0) return false;
-    for (int i = 0; i < a.nseg; i++)
-        if (mf_chunk_bytes(a.seg[i].type) == 0 || a.seg[i].type != a.seg[0].type) return false;
+    const int NB = (int)(cols / 256);
+    if (cols % 256 != 0 || mf_waves(NB) == 0) return false;
+    for (int i = 0; i < a.nseg; i++) {
+        const int t = a.seg[i].type;
+        if (mf_chunk_bytes(t) == 0 || t != a.seg[0].type) return false;
+        // Q4_K rows are read as aligned 16-byte pieces; Q6_K as dword-aligned windows whose 0-or-2
+        // byte phase follows the chunk index (an even number of chunks per row)
+        const uintptr_t w = (uintptr_t)a.seg[i].w;
+        if (t == FLLM_TYPE_Q4_K && (w & 15) != 0) return false;
+        if (t == FLLM_TYPE_Q6_K && ((w & 3) != 0 || NB % 2 != 0)) return false;
+    }
     return true;
 }
 
-static size_t mf_lds(int nw, int NB, bool glu, bool staged) {
+static size_t mf_lds(int nw, int NB, bool glu) {
     const int T = (glu ? 2 : 1) * MF_TILE;
-    return sizeof(float) * ((size_t)nw * T + 48) + (size_t)NB * 48 * 16 + (size_t)NB * 8 * 16 +
-           (staged ? (size_t)nw * MF_STAGE_BYTES : 0);
+    return sizeof(float) * ((size_t)nw * T + 48) + (size_t)(MF_ZERO_ENTRIES(NB / nw) + NB * MF_TAB_ENTRIES) * 16;
 }
+
+bool gemv_uses_mfma(const GemvArgs& a, int64_t cols) {
+    return mfma_ok(a, cols) && mf_lds(mf_waves((int)(cols / 256)), (int)(cols / 256), a.glu != 0) <= 160 * 1024;
+}
+
+size_t gemv_tab_bytes(int64_t cols) { return (size_t)(cols / 256) * MF_TAB_ENTRIES * 16; }
 
 static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, size_t* lds_bytes) {
     a.mfma = 1;
@@ -1150,7 +1214,7 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
     }
     a.nunits = units;
     *block_threads = 64 * nw;
-    *lds_bytes = mf_lds(nw, NB, a.glu != 0, a.seg[0].type == FLLM_TYPE_Q6_K);
+    *lds_bytes = mf_lds(nw, NB, a.glu != 0);
     // persistent grid: as many workgroups as fit on the device at once
     MfKernel k = mf_kernel(a.seg[0].type, NB / nw);
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -1165,11 +1229,7 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
 // Fill G, S, rpw and the segments' workgroup ranges; rows_per_wg 0 = choose.
 int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_threads, size_t* lds_bytes) {
     a.mfma = 0;
-    if (rows_per_wg <= 0 && mfma_ok(a, cols)) {
-        const int NB = (int)(cols / 256);
-        if (mf_lds(mf_waves(NB), NB, a.glu != 0, a.seg[0].type == FLLM_TYPE_Q6_K) <= 160 * 1024)
-            return plan_mfma(a, cols, n_cu, block_threads, lds_bytes);
-    }
+    if (rows_per_wg <= 0 && gemv_uses_mfma(a, cols)) return plan_mfma(a, cols, n_cu, block_threads, lds_bytes);
     a.G = (int)(cols / 32);
     int nslice = (a.G + 63) / 64;
     a.S = (a.G + nslice - 1) / nslice;

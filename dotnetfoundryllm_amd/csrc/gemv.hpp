@@ -6,7 +6,8 @@
 namespace fllm {
 
 // input of the projection
-enum { XIN_F32 = 0, XIN_NORM = 1, XIN_EMBED_NORM = 2 };
+// XIN_TAB: the matrix-core variant's activation table, written by the producer's epilogue
+enum { XIN_F32 = 0, XIN_NORM = 1, XIN_EMBED_NORM = 2, XIN_TAB = 3 };
 // epilogue of a segment
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_Q = 2, EPI_K = 3, EPI_V = 4, EPI_LOGITS = 5 };
 
@@ -42,6 +43,13 @@ struct GemvArgs {
     const uint8_t* emb;
     int emb_type;
     const StepParams* params;
+    const void* xtab;      // XIN_TAB: activation table of the input
+    const float* xssq;     // XIN_TAB with RMSNorm: per-16-element sums of squares of the raw input
+    // matrix-core EPI_RESID / GLU producers: activation table of the output for the next launch
+    void* tab_out;         // table of out * tab_w (RESID) or of h (GLU); nullptr: none
+    float* ssq_out;        // RESID: per-16-row sums of squares of out
+    const float* tab_w;    // RESID: the consumer's RMSNorm weight
+    int tab_kind;          // 0: w, 1: 1 + w
     // RoPE + KV store
     const float2* rope;
     int hd;
@@ -58,6 +66,11 @@ bool gemv_fusable_cols(int64_t cols);
 // Fills G, S, rpw and the segments' wg_begin (or the MFMA variant's units); returns the grid
 // size. The MFMA variant is chosen only when every segment has the same weight type.
 int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_threads, size_t* lds_bytes);
+// true when gemv_plan picks the matrix-core variant for this launch (only those launches read or
+// write activation tables)
+bool gemv_uses_mfma(const GemvArgs& a, int64_t cols);
+// bytes of the activation table of a vector of `cols` elements
+size_t gemv_tab_bytes(int64_t cols);
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st);
 
 }  // namespace fllm
