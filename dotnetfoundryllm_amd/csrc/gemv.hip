@@ -466,7 +466,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
     float tv = 0.0f, tq = 0.0f;
     if (a.glu) {
         // h = act(W_gate x) * (W_up x)
-        for (int t = threadIdx.x; t < R; t += blockDim.x) {
+        for (int t = threadIdx.x; t < R; t += nslice * 64) {
             int r = row_base + t;
             if (r >= sg.rows) continue;
             float g = 0.0f, u = 0.0f;
@@ -483,7 +483,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
         const int half = a.hd >> 1;
         const float2* rp = a.rope + (int64_t)a.params->pos * half;
         const int slot = a.params->cur_len;
-        for (int p = threadIdx.x; p < (R >> 1); p += blockDim.x) {
+        for (int p = threadIdx.x; p < (R >> 1); p += nslice * 64) {
             int r = row_base + 2 * p;
             if (r >= sg.rows) continue;
             float x0 = 0.0f, x1 = 0.0f;
@@ -505,7 +505,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
     }
     if (epi == EPI_LOGITS) {
         unsigned long long best = 0ull;
-        for (int t = threadIdx.x; t < R; t += blockDim.x) {
+        for (int t = threadIdx.x; t < R; t += nslice * 64) {
             int r = row_base + t;
             if (r >= sg.rows) continue;
             float y = 0.0f;
@@ -530,7 +530,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
         }
         return;
     }
-    for (int t = threadIdx.x; t < R; t += blockDim.x) {
+    for (int t = threadIdx.x; t < R; t += nslice * 64) {
         int r = row_base + t;
         if (r >= sg.rows) continue;
         float y = 0.0f;
@@ -935,65 +935,158 @@ __device__ __forceinline__ uint32_t mf_tile_base(const GemvArgs& a, int t, int l
     return (uint32_t)row * rb + kboff;
 }
 
-template <int T, int KC>
+// read instead of the activation table when there is none (keeps the prologue's loads unconditional)
+__device__ u32x4 mf_tab_dummy[1];
+
+// Per-workgroup state of the MFMA body that the item step reads.
+struct MfCtx {
+    lds_tab* at;        // this lane's A fragments of chunk kb0 (or the zero block)
+    lds_f4* stats;
+    float* part;
+    float* red;
+    uint32_t rb, kboff;
+    float xs;
+    int kb0, q, m, lane, wave, nw, ltpu, T_slots, grid, items;
+};
+
+// One item: chunk c = r % KC of workgroup tile i / KC, from ring slot r % MF_RING. With refill the
+// slot is reloaded with item i + MF_RING. Every item but the last MF_RING of the workgroup refills,
+// and the choice is a compile-time constant of the unrolled item position, so the number of loads
+// in flight at every wait is known at compile time.
+template <int T, int KC, bool REFILL>
+__device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typename MfPick<T>::Raw* ring, int i, int r,
+                                        float& y, uint32_t& offr, const uint8_t*& Wr, unsigned long long& best) {
+    constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
+    const int c = r & (KC - 1), slot = r & (MF_RING - 1), b = x.kb0 + c;
+    v4i A[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) A[s] = *(__attribute__((address_space(3))) const v4i*)&x.at[(4 * c + s) * 12];
+    const f32x4 sa = x.stats[b * 8 + x.q], sb = x.stats[b * 8 + x.q + 4];
+    y += mf_compute(ring[slot], A, sa, sb, x.q, (b & 1) * 2);
+    // finish this item's arithmetic here (sinking it to the tile's end keeps every item's MFMA
+    // results live)
+    __asm__ volatile("" : "+v"(y));
+    if (REFILL) {
+        const int cn = (r + MF_RING) & (KC - 1);
+        if (cn == 0) offr = mf_tile_base(a, (i + MF_RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
+        mf_issue(ring[slot], Wr, offr, cn, ((x.kb0 + cn) & 1) * 2, x.q);
+    }
+    // keep each item's fragment reads next to its MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+    if (c == KC - 1) {
+        // last chunk of the tile: the four quarters of row n, then this wave's partial
+        const int ti = i >> LKC, tt = ti & ((1 << x.ltpu) - 1);
+        float yt = y + __shfl_xor(y, 16);
+        yt += __shfl_xor(yt, 32);
+        if (x.lane < 16) x.part[x.wave * x.T_slots + tt * MF_TILE + x.lane] = yt * x.xs;
+        y = 0.0f;
+        if (tt == (1 << x.ltpu) - 1) {
+            // last tile of the unit (same item in every wave): combine the waves, epilogue
+            const uint8_t* Wu;
+            int rows, row0, si;
+            mf_tile_of(a, (int)blockIdx.x + (ti >> x.ltpu) * x.grid, 0, Wu, rows, row0, si);
+            __syncthreads();
+            const EpiSeg es{si == 0 ? a.seg[0].rows : si == 1 ? a.seg[1].rows : a.seg[2].rows,
+                            si == 0 ? a.seg[0].epi : si == 1 ? a.seg[1].epi : a.seg[2].epi,
+                            si == 0 ? a.seg[0].out : si == 1 ? a.seg[1].out : a.seg[2].out,
+                            si == 0 ? a.seg[0].bias : si == 1 ? a.seg[1].bias : a.seg[2].bias,
+                            si == 0 ? a.seg[0].resid : si == 1 ? a.seg[1].resid : a.seg[2].resid};
+            epilogue(a, es, x.part, x.red, x.nw, MF_TILE, x.T_slots, row0, x.wave, x.lane, best);
+            __syncthreads();
+        }
+    }
+}
+
+// TABIN: the input is an activation table (XIN_TAB); otherwise a vector, quantized here.
+template <int T, int KC, bool TABIN>
 __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
     using Raw = typename MfPick<T>::Raw;
     constexpr int CB = mf_chunk_bytes(T);
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
     constexpr int U = KC > MF_RING ? KC : MF_RING;  // items per unrolled iteration
     extern __shared__ float lds[];
-    const int nw = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int q = lane >> 4, m = lane & 15;
-    const bool a_live = (m >> 2) == q && (m & 3) < 3;  // A row m = 4Q' + d lives in quarter Q'
+    MfCtx x;
+    x.nw = a.nw;  // blockDim.x / 64 (the kernel argument avoids reading the dispatch packet)
+    x.wave = threadIdx.x >> 6;
+    x.lane = threadIdx.x & 63;
+    x.q = x.lane >> 4;
+    x.m = x.lane & 15;
+    const bool a_live = (x.m >> 2) == x.q && (x.m & 3) < 3;  // A row m = 4Q' + d lives in quarter Q'
     const int NB = a.G / 8;            // chunks per row (NB == nw * KC)
-    const int kb0 = wave * KC;
-    const int ltpu = a.glu ? 1 : 0;    // log2 of tiles per unit
-    const int T_slots = MF_TILE << ltpu;
-    float* part = lds;                         // [nw][T_slots]
-    float* red = lds + nw * T_slots;           // [16] + 16 u64
-    lds_tab* zeros = (lds_tab*)(red + 48);     // A operand of lanes without a table row
+    x.kb0 = x.wave * KC;
+    x.ltpu = a.glu ? 1 : 0;            // log2 of tiles per unit
+    x.T_slots = MF_TILE << x.ltpu;
+    x.part = lds;                              // [nw][T_slots]
+    x.red = lds + x.nw * x.T_slots;            // [16] + 16 u64
+    lds_tab* zeros = (lds_tab*)(x.red + 48);   // A operand of lanes without a table row
     lds_tab* atab = zeros + MF_ZERO_ENTRIES(KC);
-    lds_f4* stats = (lds_f4*)(atab + NB * 48);
-    // fragment (chunk kb0 + c, step s) of this lane: abase[(4c + s) * 12]
-    lds_tab* const abase = a_live ? atab + atab_index(kb0, 0, m >> 2, m & 3) : zeros;
-    const uint32_t rb = (uint32_t)NB * CB, kboff = (uint32_t)kb0 * CB;
-    const int grid = (int)gridDim.x;
-    const int my_units = (a.nunits - (int)blockIdx.x + grid - 1) / grid;
-    const int items = (my_units << ltpu) * KC;
+    x.stats = (lds_f4*)(atab + NB * 48);
+    // fragment (chunk kb0 + c, step s) of this lane: x.at[(4c + s) * 12]
+    lds_tab* const abase = a_live ? atab + atab_index(x.kb0, 0, x.m >> 2, x.m & 3) : zeros;
+    x.rb = (uint32_t)NB * CB;
+    x.kboff = (uint32_t)x.kb0 * CB;
+    x.grid = (int)gridDim.x;
+    const int my_units = (a.nunits - (int)blockIdx.x + x.grid - 1) / x.grid;
+    x.items = (my_units << x.ltpu) * KC;
+
+    // ---- a table input: each wave copies the part its own chunks use (digit entries of chunks
+    // kb0 .. kb0 + KC - 1, their stats) and sums its share of the squares. These loads go out before
+    // the weight ring, so waiting for them is not waiting for weights; fixed counts with clamped
+    // indices keep the wait counts exact.
+    constexpr int TDL = (KC * 48 + 63) / 64, TSL = (KC * 16 + 63) / 64;
+    // (without a table the loads all read one dummy entry and go unused)
+    u32x4 tdig[TDL];
+    float tsq[TSL];
+    constexpr bool tab_in = TABIN;
+    const int tm = tab_in ? 1 : 0;
+    const u32x4* tsrc = tab_in ? (const u32x4*)a.xtab : mf_tab_dummy;
+#pragma unroll
+    for (int k = 0; k < TDL; k++) tdig[k] = tsrc[tm * (x.kb0 * 48 + min(x.lane + 64 * k, KC * 48 - 1))];
+    const u32x4 tst = tsrc[tm * (NB * 48 + x.kb0 * 8 + min(x.lane, KC * 8 - 1))];
+    const int sm = (tab_in && a.xssq) ? 1 : 0;
+    const float* sp = sm ? a.xssq : (const float*)mf_tab_dummy;
+#pragma unroll
+    for (int k = 0; k < TSL; k++) tsq[k] = sp[sm * (x.kb0 * 16 + min(x.lane + 64 * k, KC * 16 - 1))];
+    __builtin_amdgcn_sched_barrier(0);
 
     Raw ring[MF_RING];
     const uint8_t* Wr = a.seg[0].w;  // matrix and lane offset of the tile of the latest load
     uint32_t offr = 0;
 #pragma unroll
     for (int r = 0; r < MF_RING; r++) {
-        if (r < items) {
-            const int c = r & (KC - 1);
-            if (c == 0) offr = mf_tile_base(a, r >> LKC, ltpu, rb, kboff, m, Wr);
-            mf_issue(ring[r], Wr, offr, c, ((kb0 + c) & 1) * 2, q);
-        }
+        const int c = r & (KC - 1);
+        // fewer items than ring slots (a single tile of KC < MF_RING chunks): reload its last chunk
+        if (c == 0 && r < x.items) offr = mf_tile_base(a, r >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
+        mf_issue(ring[r], Wr, offr, c, ((x.kb0 + c) & 1) * 2, x.q);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- prologue: the activation table -------------------------------------------------------
-    for (int e = threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += blockDim.x) {
+    for (int e = threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += x.nw * 64) {
         const u32x4 z4 = {0u, 0u, 0u, 0u};
         zeros[e] = z4;
     }
-    float xs = 1.0f;  // RMSNorm factor of a table of raw (weighted) values
-    if (a.xin == XIN_TAB) {
-        const u32x4* src = (const u32x4*)a.xtab;
-        for (int e = threadIdx.x; e < NB * MF_TAB_ENTRIES; e += blockDim.x) atab[e] = src[e];
+    x.xs = 1.0f;  // RMSNorm factor of a table of raw (weighted) values
+    if constexpr (tab_in) {
+#pragma unroll
+        for (int k = 0; k < TDL; k++) atab[x.kb0 * 48 + min(x.lane + 64 * k, KC * 48 - 1)] = tdig[k];
+        x.stats[x.kb0 * 8 + min(x.lane, KC * 8 - 1)] = *(const f32x4*)&tst;
+        float s2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < TSL; k++) s2 += (x.lane + 64 * k < KC * 16 && a.xssq) ? tsq[k] : 0.0f;
+        s2 = wsum(s2);
+        if (x.lane == 0) x.red[x.wave] = s2;
+        __syncthreads();
         if (a.xssq) {
-            float s2 = 0.0f;
-            for (int e = lane; e < 2 * a.G; e += 64) s2 += a.xssq[e];
-            s2 = wsum(s2);
-            xs = 1.0f / sqrtf(s2 / (float)(a.G * 32) + a.eps);
+            float tot = 0.0f;
+            for (int i = 0; i < x.nw; i++) tot += x.red[i];
+            x.xs = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
         }
     } else {
         float scale = 1.0f;
         if (a.xin != XIN_F32) {
             float ssq = 0.0f;
-            for (int g = threadIdx.x; g < a.G; g += blockDim.x) {
+            for (int g = threadIdx.x; g < a.G; g += x.nw * 64) {
                 float v[32];
                 if (a.xin == XIN_EMBED_NORM) deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
                 else {
@@ -1005,13 +1098,13 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
                 for (int i = 0; i < 32; i++) ssq = fmaf(v[i], v[i], ssq);
             }
             ssq = wsum(ssq);
-            if (lane == 0) red[wave] = ssq;
+            if (x.lane == 0) x.red[x.wave] = ssq;
             __syncthreads();
             float tot = 0.0f;
-            for (int i = 0; i < nw; i++) tot += red[i];
+            for (int i = 0; i < x.nw; i++) tot += x.red[i];
             scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
         }
-        for (int g = threadIdx.x; g < a.G; g += blockDim.x) {
+        for (int g = threadIdx.x; g < a.G; g += x.nw * 64) {
             float v[32];
             if (a.xin == XIN_EMBED_NORM) {
                 deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
@@ -1041,7 +1134,7 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
             float4 st;
             atab_write(atab, g >> 3, g & 7, v, &st);
             f32x4 stv = {st.x, st.y, st.z, st.w};
-            stats[(g >> 3) * 8 + (g & 7)] = stv;
+            x.stats[(g >> 3) * 8 + (g & 7)] = stv;
         }
     }
     __syncthreads();
@@ -1049,84 +1142,65 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
     // ---- items ----------------------------------------------------------------------------------
     unsigned long long best = 0ull;
     float y = 0.0f;
-    for (int i0 = 0; i0 < items; i0 += U) {
-        // the fragments are the same for every tile; re-reading them from LDS each time keeps them
-        // out of registers (the base is opaque to the compiler, so the reads stay in the loop)
-        lds_tab* at = abase;
-        lds_f4* stt = stats;
-        __asm__ volatile("" : "+v"(at), "+v"(stt));
+    if constexpr (KC >= MF_RING) {
+        // whole iterations of one tile; the last one refills only its own items MF_RING ahead
+        const int n_it = x.items / U;
+        for (int it = 0; it + 1 < n_it; it++) {
+            x.at = abase;
+            __asm__ volatile("" : "+v"(x.at));  // re-read the fragments from LDS each iteration
 #pragma unroll
-        for (int r = 0; r < U; r++) {
-            const int i = i0 + r;
-            if (KC < MF_RING && i >= items) break;
-            const int c = r & (KC - 1), slot = r & (MF_RING - 1), b = kb0 + c;
-            v4i A[4];
+            for (int r = 0; r < U; r++) mf_item<T, KC, true>(a, x, ring, it * U + r, r, y, offr, Wr, best);
+        }
+        x.at = abase;
+        __asm__ volatile("" : "+v"(x.at));
+        const int i0 = (n_it - 1) * U;
 #pragma unroll
-            for (int s = 0; s < 4; s++) A[s] = *(__attribute__((address_space(3))) const v4i*)&at[(4 * c + s) * 12];
-            const f32x4 sa = stt[b * 8 + q], sb = stt[b * 8 + q + 4];
-            y += mf_compute(ring[slot], A, sa, sb, q, ((kb0 + c) & 1) * 2);
-            // finish this item's arithmetic here (sinking it to the tile's end keeps every item's
-            // MFMA results live)
-            __asm__ volatile("" : "+v"(y));
-            // refill this ring slot with the item MF_RING ahead (possibly of another tile or unit)
-            if (i + MF_RING < items) {
-                const int cn = (r + MF_RING) & (KC - 1);
-                if (cn == 0) offr = mf_tile_base(a, (i + MF_RING) >> LKC, ltpu, rb, kboff, m, Wr);
-                mf_issue(ring[slot], Wr, offr, cn, ((kb0 + cn) & 1) * 2, q);
-            }
-            // keep each item's fragment reads next to its MFMAs (hoisting them all to the top of the
-            // unrolled iteration costs registers, not time)
-            __builtin_amdgcn_sched_barrier(0);
-            if (c == KC - 1) {
-                // last chunk of the tile: the four quarters of row n, then this wave's partial
-                const int ti = i >> LKC, tt = ti & ((1 << ltpu) - 1);
-                float yt = y + __shfl_xor(y, 16);
-                yt += __shfl_xor(yt, 32);
-                if (lane < 16) part[wave * T_slots + tt * MF_TILE + lane] = yt * xs;
-                y = 0.0f;
-                if (tt == (1 << ltpu) - 1) {
-                    // last tile of the unit (same item in every wave): combine the waves, epilogue
-                    const uint8_t* Wu;
-                    int rows, row0, si;
-                    mf_tile_of(a, (int)blockIdx.x + (ti >> ltpu) * grid, 0, Wu, rows, row0, si);
-                    __syncthreads();
-                    const EpiSeg es{si == 0 ? a.seg[0].rows : si == 1 ? a.seg[1].rows : a.seg[2].rows,
-                                    si == 0 ? a.seg[0].epi : si == 1 ? a.seg[1].epi : a.seg[2].epi,
-                                    si == 0 ? a.seg[0].out : si == 1 ? a.seg[1].out : a.seg[2].out,
-                                    si == 0 ? a.seg[0].bias : si == 1 ? a.seg[1].bias : a.seg[2].bias,
-                                    si == 0 ? a.seg[0].resid : si == 1 ? a.seg[1].resid : a.seg[2].resid};
-                    epilogue(a, es, part, red, nw, MF_TILE, T_slots, row0, wave, lane, best);
-                    __syncthreads();
-                }
+        for (int r = 0; r < U - MF_RING; r++) mf_item<T, KC, true>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+#pragma unroll
+        for (int r = U - MF_RING; r < U; r++) mf_item<T, KC, false>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+    } else {
+        for (int i0 = 0; i0 < x.items; i0 += U) {
+            x.at = abase;
+            __asm__ volatile("" : "+v"(x.at));
+#pragma unroll
+            for (int r = 0; r < U; r++) {
+                const int i = i0 + r;
+                if (i >= x.items) break;
+                if (i + MF_RING < x.items) mf_item<T, KC, true>(a, x, ring, i, r, y, offr, Wr, best);
+                else mf_item<T, KC, false>(a, x, ring, i, r, y, offr, Wr, best);
             }
         }
     }
     if (a.seg[0].epi == EPI_LOGITS && threadIdx.x == 0) a.wg_keys[blockIdx.x] = best;  // reduced by the argmax kernel
 }
 
-// one kernel per (weight type, chunks per wave), each with its own register allocation; every
-// segment of an MFMA launch has the same weight type
-template <int T, int KC>
+// one kernel per (weight type, chunks per wave, input kind), each with its own register
+// allocation; every segment of an MFMA launch has the same weight type
+template <int T, int KC, bool TABIN>
 __global__ __launch_bounds__(512) void k_gemv_mfma(const GemvArgs a) {
-    mfma_body<T, KC>(a);
+    mfma_body<T, KC, TABIN>(a);
 }
 
 typedef void (*MfKernel)(const GemvArgs);
-static MfKernel mf_kernel(int type, int kc) {
+template <bool TABIN>
+static MfKernel mf_kernel_in(int type, int kc) {
     if (type == FLLM_TYPE_Q6_K) {
         switch (kc) {
-            case 1: return k_gemv_mfma<FLLM_TYPE_Q6_K, 1>;
-            case 2: return k_gemv_mfma<FLLM_TYPE_Q6_K, 2>;
-            case 4: return k_gemv_mfma<FLLM_TYPE_Q6_K, 4>;
-            default: return k_gemv_mfma<FLLM_TYPE_Q6_K, 8>;
+            case 1: return k_gemv_mfma<FLLM_TYPE_Q6_K, 1, TABIN>;
+            case 2: return k_gemv_mfma<FLLM_TYPE_Q6_K, 2, TABIN>;
+            case 4: return k_gemv_mfma<FLLM_TYPE_Q6_K, 4, TABIN>;
+            default: return k_gemv_mfma<FLLM_TYPE_Q6_K, 8, TABIN>;
         }
     }
     switch (kc) {
-        case 1: return k_gemv_mfma<FLLM_TYPE_Q4_K, 1>;
-        case 2: return k_gemv_mfma<FLLM_TYPE_Q4_K, 2>;
-        case 4: return k_gemv_mfma<FLLM_TYPE_Q4_K, 4>;
-        default: return k_gemv_mfma<FLLM_TYPE_Q4_K, 8>;
+        case 1: return k_gemv_mfma<FLLM_TYPE_Q4_K, 1, TABIN>;
+        case 2: return k_gemv_mfma<FLLM_TYPE_Q4_K, 2, TABIN>;
+        case 4: return k_gemv_mfma<FLLM_TYPE_Q4_K, 4, TABIN>;
+        default: return k_gemv_mfma<FLLM_TYPE_Q4_K, 8, TABIN>;
     }
+}
+static MfKernel mf_kernel(int type, int kc, int xin) {
+    return xin == XIN_TAB ? mf_kernel_in<true>(type, kc) : mf_kernel_in<false>(type, kc);
 }
 
 // WIDE: rows of more than 512 groups (up to 16 waves per workgroup), no prefetch.
@@ -1190,7 +1264,8 @@ static bool mfma_ok(const GemvArgs& a, int64_t cols) {
 
 static size_t mf_lds(int nw, int NB, bool glu) {
     const int T = (glu ? 2 : 1) * MF_TILE;
-    return sizeof(float) * ((size_t)nw * T + 48) + (size_t)(MF_ZERO_ENTRIES(NB / nw) + NB * MF_TAB_ENTRIES) * 16;
+    // row partials, 48 floats, zero block, table, and one wave's worth of padding after the table
+    return sizeof(float) * ((size_t)nw * T + 48) + (size_t)(MF_ZERO_ENTRIES(NB / nw) + NB * MF_TAB_ENTRIES + 64) * 16;
 }
 
 bool gemv_uses_mfma(const GemvArgs& a, int64_t cols) {
@@ -1214,9 +1289,10 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
     }
     a.nunits = units;
     *block_threads = 64 * nw;
+    a.nw = nw;
     *lds_bytes = mf_lds(nw, NB, a.glu != 0);
     // persistent grid: as many workgroups as fit on the device at once
-    MfKernel k = mf_kernel(a.seg[0].type, NB / nw);
+    MfKernel k = mf_kernel(a.seg[0].type, NB / nw, a.xin);
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, *block_threads, *lds_bytes) != hipSuccess ||
@@ -1265,8 +1341,10 @@ int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_t
 
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st) {
     if (grid <= 0) return hipSuccess;
+    // the matrix-core prologue always reads its input: the table, or the vector (cols floats)
+    if (a.mfma && (a.xin == XIN_TAB ? a.xtab == nullptr : a.x == nullptr)) return hipErrorInvalidValue;
     if (a.mfma)
-        mf_kernel(a.seg[0].type, (a.G / 8) / (block_threads / 64))<<<grid, block_threads, lds, st>>>(a);
+        mf_kernel(a.seg[0].type, (a.G / 8) / (block_threads / 64), a.xin)<<<grid, block_threads, lds, st>>>(a);
     else if (block_threads <= 512)
         k_gemv_fused<false><<<grid, block_threads, lds, st>>>(a);
     else

@@ -33,6 +33,7 @@ struct GemvArgs {
     int act;               // 0 SiLU, 1 GELU (tanh form)
     int mfma;              // set by gemv_plan: 1 = matrix-core variant
     int nunits;            // matrix-core variant: 16-row units of the launch (seg[i].wg_begin = first unit)
+    int nw;                // matrix-core variant: waves per workgroup
     // input
     int xin;
     const float* x;        // XIN_F32 / XIN_NORM input vector
