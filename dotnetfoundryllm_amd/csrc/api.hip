@@ -868,27 +868,20 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
         const bool o_mf = mfma_launch(o_t, 1, 0, m->qdim), gu_mf = mfma_launch(gu_t, 2, 1, H);
         const bool dn_mf = mfma_launch(dn_t, 1, 0, d.ffn);
         {
-            // q, k, v in one launch when they share a weight type, else one launch per run of
-            // equal types
-            GemvSeg all[3] = {seg_of(L.q, EPI_Q, s->q, L.bq, nullptr), seg_of(L.k, EPI_K, nullptr, L.bk, nullptr),
-                              seg_of(L.v, EPI_V, nullptr, L.bv, nullptr)};
-            const Tensor* tens[3] = {&L.q, &L.k, &L.v};
-            for (int i0 = 0; i0 < 3;) {
-                int i1 = i0 + 1;
-                while (i1 < 3 && all[i1].type == all[i0].type) i1++;
-                GemvArgs a{};
-                a.nseg = i1 - i0;
-                double bytes = 0;
-                for (int i = i0; i < i1; i++) { a.seg[i - i0] = all[i]; bytes += (double)tens[i]->bytes + 4.0 * tens[i]->rows; }
-                a.xin = (l == 0 && emb_fused) ? XIN_EMBED_NORM : XIN_NORM;
-                a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
-                if (xtab && gemv_uses_mfma(a, H)) { a.xin = XIN_TAB; a.xtab = s->tab_x; a.xssq = s->ssq_x; }
-                a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
-                a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
-                hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
-                if (e != hipSuccess) return e;
-                i0 = i1;
-            }
+            // q, k and v in one launch (the matrix-core variant takes Q4_K q/k with a Q6_K v)
+            GemvArgs a{};
+            a.nseg = 3;
+            a.seg[0] = seg_of(L.q, EPI_Q, s->q, L.bq, nullptr);
+            a.seg[1] = seg_of(L.k, EPI_K, nullptr, L.bk, nullptr);
+            a.seg[2] = seg_of(L.v, EPI_V, nullptr, L.bv, nullptr);
+            const double bytes = (double)(L.q.bytes + L.k.bytes + L.v.bytes) + 4.0 * (L.q.rows + L.k.rows + L.v.rows);
+            a.xin = (l == 0 && emb_fused) ? XIN_EMBED_NORM : XIN_NORM;
+            a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
+            if (xtab && gemv_uses_mfma(a, H)) { a.xin = XIN_TAB; a.xtab = s->tab_x; a.xssq = s->ssq_x; }
+            a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
+            a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
+            hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
+            if (e != hipSuccess) return e;
         }
         hipError_t e = attention_step(s, l, kc, vc);
         if (e != hipSuccess) return e;
@@ -932,8 +925,7 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             if (l + 1 < d.n_layers) {
                 const Layer& N = m->layers[(size_t)l + 1];
                 const Tensor* qkv_t[3] = {&N.q, &N.k, &N.v};
-                next_mf = false;
-                for (int i = 0; i < 3; i++) next_mf = next_mf || mfma_launch(qkv_t + i, 1, 0, H);
+                next_mf = mfma_launch(qkv_t, 3, 0, H);
                 next_w = N.attn_norm;
             }
             xtab = !gemma && dn_mf && next_mf;

@@ -925,10 +925,11 @@ __device__ __forceinline__ void mf_tile_of(const GemvArgs& a, int u, int ts, con
     row0 = tile * MF_TILE;
 }
 
-// workgroup tile t: its matrix and this lane's byte offset of chunk kb0 of row n of the tile
-__device__ __forceinline__ uint32_t mf_tile_base(const GemvArgs& a, int t, int ltpu, uint32_t rb, uint32_t kboff,
-                                                 int n, const uint8_t*& W) {
-    const int u = (int)blockIdx.x + (t >> ltpu) * (int)gridDim.x;
+// workgroup tile t (its units are ufirst, ufirst + ustride, ...): its matrix and this lane's byte
+// offset of chunk kb0 of row n of the tile
+__device__ __forceinline__ uint32_t mf_tile_base(const GemvArgs& a, int ufirst, int ustride, int t, int ltpu,
+                                                 uint32_t rb, uint32_t kboff, int n, const uint8_t*& W) {
+    const int u = ufirst + (t >> ltpu) * ustride;
     int rows, row0, si;
     mf_tile_of(a, u, t & ((1 << ltpu) - 1), W, rows, row0, si);
     const int row = min(row0 + n, rows - 1);
@@ -946,7 +947,7 @@ struct MfCtx {
     float* red;
     uint32_t rb, kboff;
     float xs;
-    int kb0, q, m, lane, wave, nw, ltpu, T_slots, grid, items;
+    int kb0, q, m, lane, wave, nw, ltpu, T_slots, ufirst, ustride, items;
 };
 
 // One item: chunk c = r % KC of workgroup tile i / KC, from ring slot r % MF_RING. With refill the
@@ -968,7 +969,7 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
     __asm__ volatile("" : "+v"(y));
     if (REFILL) {
         const int cn = (r + MF_RING) & (KC - 1);
-        if (cn == 0) offr = mf_tile_base(a, (i + MF_RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
+        if (cn == 0) offr = mf_tile_base(a, x.ufirst, x.ustride, (i + MF_RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
         mf_issue(ring[slot], Wr, offr, cn, ((x.kb0 + cn) & 1) * 2, x.q);
     }
     // keep each item's fragment reads next to its MFMAs
@@ -984,7 +985,7 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
             // last tile of the unit (same item in every wave): combine the waves, epilogue
             const uint8_t* Wu;
             int rows, row0, si;
-            mf_tile_of(a, (int)blockIdx.x + (ti >> x.ltpu) * x.grid, 0, Wu, rows, row0, si);
+            mf_tile_of(a, x.ufirst + (ti >> x.ltpu) * x.ustride, 0, Wu, rows, row0, si);
             __syncthreads();
             const EpiSeg es{si == 0 ? a.seg[0].rows : si == 1 ? a.seg[1].rows : a.seg[2].rows,
                             si == 0 ? a.seg[0].epi : si == 1 ? a.seg[1].epi : a.seg[2].epi,
@@ -997,9 +998,10 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
     }
 }
 
-// TABIN: the input is an activation table (XIN_TAB); otherwise a vector, quantized here.
+// TABIN: the input is an activation table (XIN_TAB); otherwise a vector, quantized here. The
+// workgroup is number wg of ng that share units [u0, u0 + nu) of the launch.
 template <int T, int KC, bool TABIN>
-__device__ __forceinline__ void mfma_body(const GemvArgs& a) {
+__device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int wg, int ng) {
     using Raw = typename MfPick<T>::Raw;
     constexpr int CB = mf_chunk_bytes(T);
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
@@ -1025,8 +1027,9 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
     lds_tab* const abase = a_live ? atab + atab_index(x.kb0, 0, x.m >> 2, x.m & 3) : zeros;
     x.rb = (uint32_t)NB * CB;
     x.kboff = (uint32_t)x.kb0 * CB;
-    x.grid = (int)gridDim.x;
-    const int my_units = (a.nunits - (int)blockIdx.x + x.grid - 1) / x.grid;
+    x.ufirst = u0 + wg;
+    x.ustride = ng;
+    const int my_units = (nu - wg + ng - 1) / ng;
     x.items = (my_units << x.ltpu) * KC;
 
     // ---- a table input: each wave copies the part its own chunks use (digit entries of chunks
@@ -1056,7 +1059,7 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
     for (int r = 0; r < MF_RING; r++) {
         const int c = r & (KC - 1);
         // fewer items than ring slots (a single tile of KC < MF_RING chunks): reload its last chunk
-        if (c == 0 && r < x.items) offr = mf_tile_base(a, r >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
+        if (c == 0 && r < x.items) offr = mf_tile_base(a, x.ufirst, x.ustride, r >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
         mf_issue(ring[r], Wr, offr, c, ((x.kb0 + c) & 1) * 2, x.q);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1175,32 +1178,48 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a) {
 }
 
 // one kernel per (weight type, chunks per wave, input kind), each with its own register
-// allocation; every segment of an MFMA launch has the same weight type
+// allocation; every segment of such a launch has the same weight type
 template <int T, int KC, bool TABIN>
 __global__ __launch_bounds__(512) void k_gemv_mfma(const GemvArgs a) {
-    mfma_body<T, KC, TABIN>(a);
+    mfma_body<T, KC, TABIN>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
+}
+
+// Two weight types in one launch (q and k in Q4_K, v in Q6_K): the first mix_wg workgroups take the
+// Q4_K units [0, mix_unit), the others the Q6_K units after them.
+template <int KC, bool TABIN>
+__global__ __launch_bounds__(512) void k_gemv_mfma_mix(const GemvArgs a) {
+    if ((int)blockIdx.x < a.mix_wg)
+        mfma_body<FLLM_TYPE_Q4_K, KC, TABIN>(a, 0, a.mix_unit, (int)blockIdx.x, a.mix_wg);
+    else
+        mfma_body<FLLM_TYPE_Q6_K, KC, TABIN>(a, a.mix_unit, a.nunits - a.mix_unit, (int)blockIdx.x - a.mix_wg,
+                                            (int)gridDim.x - a.mix_wg);
 }
 
 typedef void (*MfKernel)(const GemvArgs);
-template <bool TABIN>
-static MfKernel mf_kernel_in(int type, int kc) {
-    if (type == FLLM_TYPE_Q6_K) {
-        switch (kc) {
-            case 1: return k_gemv_mfma<FLLM_TYPE_Q6_K, 1, TABIN>;
-            case 2: return k_gemv_mfma<FLLM_TYPE_Q6_K, 2, TABIN>;
-            case 4: return k_gemv_mfma<FLLM_TYPE_Q6_K, 4, TABIN>;
-            default: return k_gemv_mfma<FLLM_TYPE_Q6_K, 8, TABIN>;
-        }
-    }
+template <int T, bool TABIN>
+static MfKernel mf_kernel_in(int kc) {
     switch (kc) {
-        case 1: return k_gemv_mfma<FLLM_TYPE_Q4_K, 1, TABIN>;
-        case 2: return k_gemv_mfma<FLLM_TYPE_Q4_K, 2, TABIN>;
-        case 4: return k_gemv_mfma<FLLM_TYPE_Q4_K, 4, TABIN>;
-        default: return k_gemv_mfma<FLLM_TYPE_Q4_K, 8, TABIN>;
+        case 1: return k_gemv_mfma<T, 1, TABIN>;
+        case 2: return k_gemv_mfma<T, 2, TABIN>;
+        case 4: return k_gemv_mfma<T, 4, TABIN>;
+        default: return k_gemv_mfma<T, 8, TABIN>;
     }
 }
-static MfKernel mf_kernel(int type, int kc, int xin) {
-    return xin == XIN_TAB ? mf_kernel_in<true>(type, kc) : mf_kernel_in<false>(type, kc);
+template <bool TABIN>
+static MfKernel mf_kernel_mix(int kc) {
+    switch (kc) {
+        case 1: return k_gemv_mfma_mix<1, TABIN>;
+        case 2: return k_gemv_mfma_mix<2, TABIN>;
+        case 4: return k_gemv_mfma_mix<4, TABIN>;
+        default: return k_gemv_mfma_mix<8, TABIN>;
+    }
+}
+// the kernel of a planned launch (a.mix_wg > 0: two weight types)
+static MfKernel mf_kernel(const GemvArgs& a, int kc) {
+    const bool tab = a.xin == XIN_TAB;
+    if (a.mix_wg > 0) return tab ? mf_kernel_mix<true>(kc) : mf_kernel_mix<false>(kc);
+    if (a.seg[0].type == FLLM_TYPE_Q6_K) return tab ? mf_kernel_in<FLLM_TYPE_Q6_K, true>(kc) : mf_kernel_in<FLLM_TYPE_Q6_K, false>(kc);
+    return tab ? mf_kernel_in<FLLM_TYPE_Q4_K, true>(kc) : mf_kernel_in<FLLM_TYPE_Q4_K, false>(kc);
 }
 
 // WIDE: rows of more than 512 groups (up to 16 waves per workgroup), no prefetch.
@@ -1252,7 +1271,10 @@ static bool mfma_ok(const GemvArgs& a, int64_t cols) {
     if (cols % 256 != 0 || mf_waves(NB) == 0) return false;
     for (int i = 0; i < a.nseg; i++) {
         const int t = a.seg[i].type;
-        if (mf_chunk_bytes(t) == 0 || t != a.seg[0].type) return false;
+        if (mf_chunk_bytes(t) == 0) return false;
+        // one type, or Q4_K segments followed by Q6_K ones (the two-type kernel; not for GLU)
+        if (t != a.seg[0].type && (a.glu || t != FLLM_TYPE_Q6_K || a.seg[0].type != FLLM_TYPE_Q4_K)) return false;
+        if (i > 0 && t == FLLM_TYPE_Q4_K && a.seg[i - 1].type != FLLM_TYPE_Q4_K) return false;
         // Q4_K rows are read as aligned 16-byte pieces; Q6_K as dword-aligned windows whose 0-or-2
         // byte phase follows the chunk index (an even number of chunks per row)
         const uintptr_t w = (uintptr_t)a.seg[i].w;
@@ -1288,18 +1310,34 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
         units += (a.seg[i].rows + MF_TILE - 1) / MF_TILE;
     }
     a.nunits = units;
+    // two weight types: units of the Q6_K segments come after the Q4_K ones
+    a.mix_wg = 0;
+    a.mix_unit = units;
+    for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].type != a.seg[0].type) { a.mix_unit = a.seg[i].wg_begin; a.mix_wg = 1; break; }
     *block_threads = 64 * nw;
     a.nw = nw;
     *lds_bytes = mf_lds(nw, NB, a.glu != 0);
     // persistent grid: as many workgroups as fit on the device at once
-    MfKernel k = mf_kernel(a.seg[0].type, NB / nw, a.xin);
+    MfKernel k = mf_kernel(a, NB / nw);
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, *block_threads, *lds_bytes) != hipSuccess ||
         per_cu < 1)
         per_cu = 1;
     int grid = n_cu * per_cu;
-    return grid < units ? grid : units;
+    if (grid > units) grid = units;
+    if (a.mix_wg > 0) {
+        // workgroups for each type in proportion to its units, at least one each
+        if (grid < 2) grid = 2;
+        int ga = (int)(((int64_t)grid * a.mix_unit + units / 2) / units);
+        if (ga < 1) ga = 1;
+        if (ga > grid - 1) ga = grid - 1;
+        if (ga > a.mix_unit) ga = a.mix_unit;
+        if (grid - ga > units - a.mix_unit) grid = ga + (units - a.mix_unit);
+        a.mix_wg = ga;
+    }
+    return grid;
 }
 
 // Fill G, S, rpw and the segments' workgroup ranges; rows_per_wg 0 = choose.
@@ -1344,7 +1382,7 @@ hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, siz
     // the matrix-core prologue always reads its input: the table, or the vector (cols floats)
     if (a.mfma && (a.xin == XIN_TAB ? a.xtab == nullptr : a.x == nullptr)) return hipErrorInvalidValue;
     if (a.mfma)
-        mf_kernel(a.seg[0].type, (a.G / 8) / (block_threads / 64), a.xin)<<<grid, block_threads, lds, st>>>(a);
+        mf_kernel(a, (a.G / 8) / (block_threads / 64))<<<grid, block_threads, lds, st>>>(a);
     else if (block_threads <= 512)
         k_gemv_fused<false><<<grid, block_threads, lds, st>>>(a);
     else

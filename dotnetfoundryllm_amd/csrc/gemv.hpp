@@ -34,6 +34,7 @@ struct GemvArgs {
     int mfma;              // set by gemv_plan: 1 = matrix-core variant
     int nunits;            // matrix-core variant: 16-row units of the launch (seg[i].wg_begin = first unit)
     int nw;                // matrix-core variant: waves per workgroup
+    int mix_unit, mix_wg;  // matrix-core variant with Q4_K then Q6_K segments: first Q6_K unit and workgroup (0: one type)
     // input
     int xin;
     const float* x;        // XIN_F32 / XIN_NORM input vector
