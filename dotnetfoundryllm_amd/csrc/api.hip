@@ -120,6 +120,7 @@ struct fllm_seq {
     // residual stream times the next RMSNorm weight (with per-16-row sums of squares), and of the
     // FFN activation
     float *tab_x = nullptr, *ssq_x = nullptr, *tab_h = nullptr;
+    float* tab_att = nullptr;  // table of the attention output, written by the attention merge
     int* tokens_out = nullptr;
     int *topk_ids = nullptr, *topk_count = nullptr;
     float* topk_vals = nullptr;
@@ -617,6 +618,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->tab_x, gemv_tab_bytes(d.hidden) / 4 + 4);
     ALLOC(s->ssq_x, H / 16 + 1);
     ALLOC(s->tab_h, gemv_tab_bytes(d.ffn) / 4 + 4);
+    ALLOC(s->tab_att, gemv_tab_bytes(m->qdim) / 4 + 4);
     ALLOC(s->tokens_out, (size_t)s->max_seq);
     ALLOC(s->topk_ids, (size_t)d.vocab);
     ALLOC(s->topk_vals, (size_t)d.vocab);
@@ -773,7 +775,7 @@ static int layer_window(const fllm_model_desc& d, int l) {
     return 0x7FFFFFFF;
 }
 
-static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const float* vc) {
+static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const float* vc, bool tab) {
     const fllm_model_desc& d = s->m->d;
     bool gemma = d.arch == FLLM_ARCH_GEMMA2;
     int window = layer_window(d, l);
@@ -787,6 +789,7 @@ static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const floa
         a.window = window; a.scale = d.attn_scale; a.softcap = softcap;
         a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml;
         a.out = s->att; a.params = s->params;
+        a.tab_out = tab ? s->tab_att : nullptr;
         STEP("attention", bytes, launch_attn_decode(a, s->attn_lds, s->st));
     } else {
         STEP("attention", bytes,
@@ -883,7 +886,10 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
             if (e != hipSuccess) return e;
         }
-        hipError_t e = attention_step(s, l, kc, vc);
+        // the attention merge writes the output projection's activation table when that runs on
+        // the matrix cores
+        const bool atab = s->attn_fast && o_mf;
+        hipError_t e = attention_step(s, l, kc, vc, atab);
         if (e != hipSuccess) return e;
         {
             GemvArgs a{};
@@ -891,6 +897,7 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.seg[0] = gemma ? seg_of(L.o, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.o, EPI_RESID, s->x, nullptr, s->x);
             a.xin = XIN_F32;
             a.x = s->att;
+            if (atab) { a.xin = XIN_TAB; a.xtab = s->tab_att; }
             xtab = !gemma && o_mf && gu_mf;
             if (xtab) { a.tab_out = s->tab_x; a.ssq_out = s->ssq_x; a.tab_w = L.ffn_norm; a.tab_kind = nk; }
             e = fused_step(s, "attn_output", a, m->qdim, (double)L.o.bytes + 4.0 * (m->qdim + 2.0 * H));
@@ -975,7 +982,7 @@ static hipError_t enqueue_body_generic(fllm_seq* s) {
         STEP("qkv_rope_kvstore", 8.0 * (m->qdim + 2 * kvdim),
              launch_qkv_post(s->q, s->k, s->v, L.bq, L.bk, L.bv, s->rope, d.n_heads, d.n_kv_heads, d.head_dim, kc, vc,
                              s->params, s->st));
-        if ((e = attention_step(s, l, kc, vc)) != hipSuccess) return e;
+        if ((e = attention_step(s, l, kc, vc, false)) != hipSuccess) return e;
         if (gemma) {
             if ((e = gemv_step(s, L.o, s->att, s->tmp, nullptr)) != hipSuccess) return e;
             STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));

@@ -13,6 +13,7 @@
 // the chunks of every head. (Merging inside the first kernel would need a device-scope release
 // per workgroup, which on a multi-XCD part writes back each XCD's L2.)
 #include "attention.hpp"
+#include "actab.hpp"
 
 #include <math.h>
 
@@ -205,6 +206,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(const AttnArgs a) {
     if (lane == 0) s_inv = 1.0f / L;
     __syncthreads();
     const float inv = s_inv;
+    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's output slice (HD / 4 <= 64 lanes)
     for (int d4 = lane; d4 < HD / 4; d4 += 64) {
         const float* po = a.part_o + (int64_t)h * a.nc * HD + d4 * 4;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -230,7 +232,52 @@ __global__ __launch_bounds__(64) void k_attn_merge(const AttnArgs a) {
             o.z = fmaf(p.z, w, o.z);
             o.w = fmaf(p.w, w, o.w);
         }
-        *(float4*)(a.out + (int64_t)h * HD + d4 * 4) = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        res = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+        *(float4*)(a.out + (int64_t)h * HD + d4 * 4) = res;
+    }
+    if (a.tab_out) {
+        // the head's part of the activation table of out, for the output projection: lanes
+        // 4k .. 4k + 3 hold the 16 elements of half k (one float4 each, HD / 4 lanes in all)
+        __shared__ __attribute__((aligned(16))) uint8_t stg[HD / 16][3][16];
+        const bool live = lane < HD / 4;
+        const float4 v = res;
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        float sum = (v.x + v.y) + (v.z + v.w);
+#pragma unroll
+        for (int o = 1; o < 4; o <<= 1) {
+            amax = fmaxf(amax, __shfl_xor(amax, o));
+            sum += __shfl_xor(sum, o);
+        }
+        float sc, qinv;
+        half_scale(amax, sc, qinv);
+        const int hl = lane >> 2, by = lane & 3;  // element 4 by + j of half hl, j = component
+        if (live) {
+            const float c4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                int b2, b1, b0;
+                digits3(quant_x(c4[j], qinv), b2, b1, b0);
+                stg[hl][0][4 * j + by] = (uint8_t)b2;
+                stg[hl][1][4 * j + by] = (uint8_t)b1;
+                stg[hl][2][4 * j + by] = (uint8_t)b0;
+            }
+        }
+        __syncthreads();
+        const int n = a.nh * HD;
+        uint4* tab = (uint4*)a.tab_out;
+        if (lane < (HD / 16) * 3) {
+            const int k = lane / 3, d = lane % 3;
+            int entry0, byte, stat, half;
+            tab_pos(h * HD + 16 * k, n, entry0, byte, stat, half);
+            tab[entry0 + d] = *(const uint4*)&stg[k][d][0];
+        }
+        if (live && by == 0) {
+            int entry0, byte, stat, half;
+            tab_pos(h * HD + 16 * hl, n, entry0, byte, stat, half);
+            float* st = (float*)(tab + stat);
+            st[half] = sc;
+            st[2 + half] = sum;
+        }
     }
 }
 

@@ -20,6 +20,7 @@ struct AttnArgs {
     float* part_ml;        // [nh][nc][2]
     float* out;            // [nh][hd]
     const StepParams* params;
+    void* tab_out;         // optional: activation table of out (nh * hd elements, a multiple of 256)
 };
 
 bool attn_fast_supported(int head_dim, int group, int max_seq);

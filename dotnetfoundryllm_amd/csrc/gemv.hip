@@ -26,6 +26,7 @@
 // the integer weights q. The representation error is at most 2^-17 * s per element (about 2^-24
 // of the group's largest magnitude), float32 resolution.
 #include "gemv.hpp"
+#include "actab.hpp"
 
 #include <math.h>
 
@@ -690,22 +691,12 @@ constexpr int MF_TILE = 16;        // weight rows per MFMA tile
 // zeroed uint4 entries in LDS read as the A operand by lanes that carry no table row: as many as
 // the table entries one wave's KC chunks span
 #define MF_ZERO_ENTRIES(kc) ((kc) * 48)
-constexpr int MF_TAB_ENTRIES = 56; // uint4 entries of the activation table per chunk
 
 // bytes of 256 elements (one chunk) for the MFMA-capable types
 __host__ __device__ constexpr int mf_chunk_bytes(int t) {
     return t == FLLM_TYPE_Q4_K ? 144 : t == FLLM_TYPE_Q6_K ? 210 : 0;
 }
 
-__host__ __device__ __forceinline__ int atab_index(int b, int s, int q, int d) { return ((b * 4 + s) * 4 + q) * 3 + d; }
-
-// signed base-256 digits of X = 65536 b2 + 256 b1 + b0
-__device__ __forceinline__ void digits3(int X, int& b2, int& b1, int& b0) {
-    b0 = (int)(int8_t)(X & 0xFF);
-    const int x1 = (X - b0) >> 8;
-    b1 = (int)(int8_t)(x1 & 0xFF);
-    b2 = (x1 - b1) >> 8;
-}
 
 // One thread: the digit entries of group g (0..7) of chunk b from its 32 values; returns the
 // group stats.
@@ -717,12 +708,11 @@ __device__ __forceinline__ void atab_write(lds_tab* atab, int b, int g, const fl
         float amax = 0.0f, sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; i++) { sum += v[16 * h + i]; amax = fmaxf(amax, fabsf(v[16 * h + i])); }
-        float inv = 0.0f;
-        sc[h] = 0.0f;
-        if (amax > 0.0f) { sc[h] = amax / 127.0f; inv = 127.0f / amax; }
+        float inv;
+        half_scale(amax, sc[h], inv);
         sm[h] = sum;
 #pragma unroll
-        for (int i = 0; i < 16; i++) X[16 * h + i] = (int)rintf(v[16 * h + i] * inv * 65536.0f);
+        for (int i = 0; i < 16; i++) X[16 * h + i] = quant_x(v[16 * h + i], inv);
     }
     const int q = g & 3, s0 = 2 * (g >> 2);
 #pragma unroll
@@ -758,10 +748,10 @@ __device__ __forceinline__ void tab_emit(const GemvArgs& a, float v, float sq, i
         sum += __shfl_xor(sum, o);
         ssq += __shfl_xor(ssq, o);
     }
-    float sc = 0.0f, inv = 0.0f;
-    if (amax > 0.0f) { sc = amax / 127.0f; inv = 127.0f / amax; }
+    float sc, inv;
+    half_scale(amax, sc, inv);
     int b2, b1, b0;
-    digits3((int)rintf(v * inv * 65536.0f), b2, b1, b0);
+    digits3(quant_x(v, inv), b2, b1, b0);
     const int h16 = row_base >> 4, g32 = h16 >> 1, half = h16 & 1, b = g32 >> 3, gg = g32 & 7;
     const int s = 2 * (gg >> 2) + half, q = gg & 3, j = lane & 3;
     // dword j of each digit entry: bytes from elements j, 4 + j, 8 + j, 12 + j
