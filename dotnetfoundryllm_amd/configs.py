@@ -70,6 +70,9 @@ CONFIGS = {
     "test-gemma2": _cfg("test-gemma2", N.ARCH_GEMMA2, 3, 256, 4, 2, 512, 512, 64, 10000.0,
                         _types(*([Q8_0] * 8)), head_dim=128, emb_type=BF16, window=6, attn_softcap=50.0,
                         final_softcap=30.0, tied=True, norm_std=0.1, seed=15),
+    "test-gemma2-hd256": _cfg("test-gemma2-hd256", N.ARCH_GEMMA2, 2, 256, 4, 2, 512, 512, 64, 10000.0,
+                              _types(*([Q8_0] * 8)), head_dim=256, emb_type=BF16, window=6, attn_softcap=50.0,
+                              final_softcap=30.0, tied=True, norm_std=0.1, seed=17),
     "test-mixed": _cfg("test-mixed", N.ARCH_LLAMA, 2, 256, 4, 2, 512, 512, 64, 10000.0,
                        _types(Q4_0, Q8_K, F16, BF16, F32, Q4_0, Q5_K, F16), emb_type=F16, norm_std=0.1, seed=16),
 }

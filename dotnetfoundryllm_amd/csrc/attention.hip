@@ -19,14 +19,97 @@
 
 namespace fllm {
 
-template <int HD>
+// Cross-lane reductions with DPP row operations (VALU, no LDS round trip). dpp<CTRL, ROWS>(old, v):
+// v moved by the DPP control CTRL in the rows of mask ROWS, old elsewhere.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+enum { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_BCAST15 = 0x142,
+       DPP_BCAST31 = 0x143 };
+
+// sum over each group of N lanes (16, 32 or 64); the total is in the group's last lane
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp<DPP_XOR1>(0.0f, v);
+    v += dpp<DPP_XOR2>(0.0f, v);
+    v += dpp<DPP_HALF_MIRROR>(0.0f, v);
+    v += dpp<DPP_MIRROR>(0.0f, v);  // every lane: its 16-lane row
+    if (N >= 32) v += dpp<DPP_BCAST15, 0xA>(0.0f, v);  // rows 1, 3: rows 0 + 1, 2 + 3
+    if (N >= 64) v += dpp<DPP_BCAST31, 0xC>(0.0f, v);  // rows 2, 3: adds rows 0 + 1 (row 3 = all)
+    return v;
+}
+// maximum over the wave, in every lane
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<DPP_XOR1>(v, v));
+    v = fmaxf(v, dpp<DPP_XOR2>(v, v));
+    v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v, v));
+    v = fmaxf(v, dpp<DPP_MIRROR>(v, v));
+    v = fmaxf(v, dpp<DPP_BCAST15, 0xA>(v, v));
+    v = fmaxf(v, dpp<DPP_BCAST31, 0xC>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum<64>(v)), 63));
+}
+
+// dot of q with the K row slice kr for every head of the group, reduced over the row's lanes; the
+// row's last lane stores the scaled (and capped) score of row t
+template <int HD, int G>
+__device__ __forceinline__ void attn_scores(const float4* qv, const float4& kr, int t, int len, int dl, float* sc,
+                                            int ch, float scale, float softcap, float inv_cap) {
+    constexpr int LPR = HD / 4;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        float s = qv[h].x * kr.x;
+        s = fmaf(qv[h].y, kr.y, s);
+        s = fmaf(qv[h].z, kr.z, s);
+        s = fmaf(qv[h].w, kr.w, s);
+        s = group_sum<LPR>(s);
+        if (dl == LPR - 1 && t < len) {
+            s = s * scale;
+            if (softcap > 0.0f) s = tanhf(s * inv_cap) * softcap;
+            sc[h * ch + t] = s;
+        }
+    }
+}
+
+// acc[h] += p_t v_t for the rows of the group's heads
+template <int G>
+__device__ __forceinline__ void attn_pv(float4* acc, const float4& vr, int t, int len, const float* sc, int ch) {
+    if (t >= len) return;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float p = sc[h * ch + t];
+        acc[h].x = fmaf(p, vr.x, acc[h].x);
+        acc[h].y = fmaf(p, vr.y, acc[h].y);
+        acc[h].z = fmaf(p, vr.z, acc[h].z);
+        acc[h].w = fmaf(p, vr.w, acc[h].w);
+    }
+}
+
+// G = query heads per kv head. Rows of the chunk go in blocks of BLK = 4 rows per lane; the K and V
+// rows of the first two blocks are loaded together up front (row indices clamped to the chunk, so
+// every load is unconditional and all are in flight at once), later blocks in a loop.
+template <int HD, int G>
 __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     constexpr int LPR = HD / 4;    // lanes per K/V row
     constexpr int RPL = 64 / LPR;  // rows per wave load
-    constexpr int GMAX = ATTN_GROUP_MAX;
+    constexpr int RPP = 4 * RPL;   // rows per load of the 4 waves
+    constexpr int NP = 4;          // rows per lane per block
+    constexpr int BLK = NP * RPP;  // rows per block
     extern __shared__ float sh[];
     const int kvh = blockIdx.x, c = blockIdx.y;
-    const int group = a.nh / a.nkv;
+    const int h0 = kvh * G;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane / LPR, dl = lane % LPR;
+    const int r0 = wave * RPL + sub;  // this lane's rows in a block: r0 + u * RPP
+
+    // q slice of every head of the group (independent of the position)
+    float4 qv[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) qv[h] = *(const float4*)(a.q + (int64_t)(h0 + h) * HD + dl * 4);
+
     const int seq = a.params->pos + 1;
     int ws = seq - a.window;
     if (ws < 0) ws = 0;
@@ -37,130 +120,84 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     if (c >= nchunks) return;
     const int t0 = ws + c * ch;
     const int len = min(ch, seq - t0);
-    const int h0 = kvh * group;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int sub = lane / LPR, dl = lane % LPR;
 
-    float* sc = sh;                                   // [group][ch] scores, then weights
-    float* red = sh + group * ch;                     // [4 waves][group][HD]
-    float* ml = red + 4 * group * HD;                 // [group][2]
+    float* sc = sh;                                   // [G][ch] scores, then weights
+    float* red = sh + G * ch;                         // [4 waves * RPL row slots][G][HD] = 1024 G floats
+    float* ml = red + 4 * RPL * G * HD;               // [G][2]
 
-    // q slice of every head of the group
-    float4 qv[GMAX];
-#pragma unroll
-    for (int h = 0; h < GMAX; h++)
-        qv[h] = h < group ? *(const float4*)(a.q + (int64_t)(h0 + h) * HD + dl * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-
-    const float* kbase = a.kc + (int64_t)kvh * HD + dl * 4;
-    const float* vbase = a.vc + (int64_t)kvh * HD + dl * 4;
-    const int rstep = 4 * RPL;  // rows covered by one load of the 4 waves
+    const float* kbase = a.kc + (int64_t)t0 * a.kvdim + (int64_t)kvh * HD + dl * 4;
+    const float* vbase = a.vc + (int64_t)t0 * a.kvdim + (int64_t)kvh * HD + dl * 4;
     const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
 
-    // the first V rows of this wave are loaded with the first K rows (one memory round trip for
-    // chunks of up to 4 * rstep positions)
-    float4 vpre[4];
+    // ---- K and V rows of blocks 0 and 1 -------------------------------------------------------
+    float4 kA[NP], kB[NP], vA[NP], vB[NP];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        int t = wave * RPL + sub + u * rstep;
-        vpre[u] = t < len ? *(const float4*)(vbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int u = 0; u < NP; u++) kA[u] = *(const float4*)(kbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
+#pragma unroll
+    for (int u = 0; u < NP; u++) kB[u] = *(const float4*)(kbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
+#pragma unroll
+    for (int u = 0; u < NP; u++) vA[u] = *(const float4*)(vbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
+#pragma unroll
+    for (int u = 0; u < NP; u++) vB[u] = *(const float4*)(vbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
 
-    // ---- scores --------------------------------------------------------------------------
-    for (int base = wave * RPL + sub; base < len; base += 4 * rstep) {
-        float4 kr[4];
+    // ---- scores ---------------------------------------------------------------------------------
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            int t = base + u * rstep;
-            kr[u] = t < len ? *(const float4*)(kbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+    for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kA[u], r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            int t = base + u * rstep;
+    for (int u = 0; u < NP; u++)
+        attn_scores<HD, G>(qv, kB[u], BLK + r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
+    for (int b0 = 2 * BLK; b0 < len; b0 += BLK) {
+        float4 kr[NP];
 #pragma unroll
-            for (int h = 0; h < GMAX; h++) {
-                if (h >= group) break;
-                float s = qv[h].x * kr[u].x;
-                s = fmaf(qv[h].y, kr[u].y, s);
-                s = fmaf(qv[h].z, kr[u].z, s);
-                s = fmaf(qv[h].w, kr[u].w, s);
+        for (int u = 0; u < NP; u++) kr[u] = *(const float4*)(kbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
 #pragma unroll
-                for (int o = LPR / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
-                if (dl == 0 && t < len) {
-                    s = s * a.scale;
-                    if (a.softcap > 0.0f) s = tanhf(s * inv_cap) * a.softcap;
-                    sc[h * ch + t] = s;
-                }
-            }
-        }
+        for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kr[u], b0 + r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
     }
     __syncthreads();
 
     // ---- softmax pieces per head: max, exp(s - max), sum -----------------------------------
-    for (int h = wave; h < group; h += 4) {
+    for (int h = wave; h < G; h += 4) {
         float m = -INFINITY;
         for (int t = lane; t < len; t += 64) m = fmaxf(m, sc[h * ch + t]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = wave_max(m);
         float l = 0.0f;
         for (int t = lane; t < len; t += 64) {
             float e = expf(sc[h * ch + t] - m);
             sc[h * ch + t] = e;
             l += e;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+        l = wave_sum(l);
         if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
     }
     __syncthreads();
 
     // ---- weighted sum of V ------------------------------------------------------------------
-    float4 acc[GMAX];
+    float4 acc[G];
 #pragma unroll
-    for (int h = 0; h < GMAX; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int base = wave * RPL + sub; base < len; base += 4 * rstep) {
-        float4 vr[4];
-        const bool first = base == wave * RPL + sub;
+    for (int h = 0; h < G; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            int t = base + u * rstep;
-            vr[u] = first ? vpre[u]
-                          : (t < len ? *(const float4*)(vbase + (int64_t)(t0 + t) * a.kvdim) : make_float4(0.f, 0.f, 0.f, 0.f));
-        }
+    for (int u = 0; u < NP; u++) attn_pv<G>(acc, vA[u], r0 + u * RPP, len, sc, ch);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            int t = base + u * rstep;
-            if (t >= len) break;
+    for (int u = 0; u < NP; u++) attn_pv<G>(acc, vB[u], BLK + r0 + u * RPP, len, sc, ch);
+    for (int b0 = 2 * BLK; b0 < len; b0 += BLK) {
+        float4 vr[NP];
 #pragma unroll
-            for (int h = 0; h < GMAX; h++) {
-                if (h >= group) break;
-                float p = sc[h * ch + t];
-                acc[h].x = fmaf(p, vr[u].x, acc[h].x);
-                acc[h].y = fmaf(p, vr[u].y, acc[h].y);
-                acc[h].z = fmaf(p, vr[u].z, acc[h].z);
-                acc[h].w = fmaf(p, vr[u].w, acc[h].w);
-            }
-        }
+        for (int u = 0; u < NP; u++) vr[u] = *(const float4*)(vbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
+#pragma unroll
+        for (int u = 0; u < NP; u++) attn_pv<G>(acc, vr[u], b0 + r0 + u * RPP, len, sc, ch);
     }
-    // reduce over the RPL row slots of the wave, then over the 4 waves through LDS
+    // every (wave, row slot) leaves its partial sums in LDS; 4 * RPL slots are then summed
 #pragma unroll
-    for (int h = 0; h < GMAX; h++) {
-        if (h >= group) break;
-#pragma unroll
-        for (int o = LPR; o < 64; o <<= 1) {
-            acc[h].x += __shfl_xor(acc[h].x, o);
-            acc[h].y += __shfl_xor(acc[h].y, o);
-            acc[h].z += __shfl_xor(acc[h].z, o);
-            acc[h].w += __shfl_xor(acc[h].w, o);
-        }
-        if (sub == 0) *(float4*)(red + ((wave * group + h) * HD) + dl * 4) = acc[h];
-    }
+    for (int h = 0; h < G; h++) *(float4*)(red + (((wave * RPL + sub) * G + h) * HD) + dl * 4) = acc[h];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < group * HD; idx += blockDim.x) {
-        float o = red[idx] + red[group * HD + idx] + red[2 * group * HD + idx] + red[3 * group * HD + idx];
+    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
+        float o = 0.0f;
+#pragma unroll
+        for (int sl = 0; sl < 4 * RPL; sl++) o += red[sl * G * HD + idx];
         int h = idx / HD, d = idx % HD;
         a.part_o[((int64_t)(h0 + h) * a.nc + c) * HD + d] = o;
     }
-    for (int h = threadIdx.x; h < group; h += blockDim.x) {
+    for (int h = threadIdx.x; h < G; h += blockDim.x) {
         a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2] = ml[2 * h];
         a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2 + 1] = ml[2 * h + 1];
     }
@@ -302,15 +339,33 @@ int attn_chunks(int n_kv, int max_seq, int n_cu) {
 size_t attn_lds_bytes(int head_dim, int group, int nc, int max_seq) {
     int ch_max = (max_seq + nc - 1) / nc;
     ch_max = (ch_max + 31) / 32 * 32;
-    return sizeof(float) * ((size_t)group * ch_max + 4 * (size_t)group * head_dim + 2 * (size_t)group);
+    // scores, the partial sums of the 4 waves' row slots (4 * 256 / head_dim slots of head_dim), m and l
+    (void)head_dim;
+    return sizeof(float) * ((size_t)group * ch_max + 1024 * (size_t)group + 2 * (size_t)group);
+}
+
+template <int HD>
+static void attn_decode_g(const AttnArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+    switch (a.nh / a.nkv) {
+        case 1: k_attn_decode<HD, 1><<<grid, 256, lds, st>>>(a); break;
+        case 2: k_attn_decode<HD, 2><<<grid, 256, lds, st>>>(a); break;
+        case 3: k_attn_decode<HD, 3><<<grid, 256, lds, st>>>(a); break;
+        case 4: k_attn_decode<HD, 4><<<grid, 256, lds, st>>>(a); break;
+        case 5: k_attn_decode<HD, 5><<<grid, 256, lds, st>>>(a); break;
+        case 6: k_attn_decode<HD, 6><<<grid, 256, lds, st>>>(a); break;
+        case 7: k_attn_decode<HD, 7><<<grid, 256, lds, st>>>(a); break;
+        default: k_attn_decode<HD, 8><<<grid, 256, lds, st>>>(a); break;
+    }
 }
 
 hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st) {
     dim3 grid(a.nkv, a.nc);
+    const int g = a.nh / a.nkv;
+    if (g < 1 || g > ATTN_GROUP_MAX || g * a.nkv != a.nh) return hipErrorInvalidValue;
     switch (a.hd) {
-        case 64: k_attn_decode<64><<<grid, 256, lds, st>>>(a); break;
-        case 128: k_attn_decode<128><<<grid, 256, lds, st>>>(a); break;
-        default: k_attn_decode<256><<<grid, 256, lds, st>>>(a); break;
+        case 64: attn_decode_g<64>(a, grid, lds, st); break;
+        case 128: attn_decode_g<128>(a, grid, lds, st); break;
+        default: attn_decode_g<256>(a, grid, lds, st); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

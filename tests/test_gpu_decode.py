@@ -47,7 +47,8 @@ def test_reference_fixtures(ctx, arch):
         m.close()
 
 
-SMALL = ["test-llama", "test-llama-straddle", "test-mistral", "test-qwen2", "test-gemma2", "test-mixed"]
+SMALL = ["test-llama", "test-llama-straddle", "test-mistral", "test-qwen2", "test-gemma2", "test-gemma2-hd256",
+         "test-mixed"]
 
 
 @pytest.mark.parametrize("name", SMALL)
