@@ -8,15 +8,28 @@ device-side loop (each step's argmax is the next step's input token on the devic
 launch per step, the tokens are read back after the last step); the same tokens come out of the
 host loop (forward + argmax + 4-byte read-back per token), whose rate is reported beside it.
 
-Prints one JSON line with the decode throughput, a roofline entry for the dominant kernel
-(algorithmic bytes per launch / mean launch time from HIP events in a profiled pass of the
-same decode steps) and a CPU baseline (the oracle's reference-order F32 forward pass on a
-bounded sample, one thread). Progress goes to stderr.
+Prints one JSON line with the decode throughput, a roofline entry for the dominant kernel and a
+CPU baseline (the oracle's reference-order F32 forward pass on a bounded sample, one thread).
+Progress goes to stderr.
+
+Roofline: the dominant kernel is the one with the largest share of a profiled decode step (HIP
+events around every launch). Its achieved bandwidth is its algorithmic bytes per launch (the weight
+blocks it streams plus its activation reads and writes) over its mean duration. When rocprofv3 is
+on PATH, the duration and the HBM traffic come from short child runs of this script under the
+profiler (kernel trace; FETCH_SIZE; WRITE_SIZE), the counters scaled by what they read for a device
+copy of known size in the same child; otherwise the duration is the HIP-event mean (which includes
+the launch) and the traffic is null.
 """
 import argparse
+import csv
+import ctypes
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -29,7 +42,7 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg_name, ctx_positions=8):
+def cpu_baseline(cfg_name, ctx_positions=384):
     """The oracle (reference-order restatement, F32 weights dequantized at load, one thread) on a
     bounded sample of the same workload: one decoder layer of the model shape and 1/16 of the
     LM-head rows, timed separately and scaled to a whole token."""
@@ -45,7 +58,7 @@ def cpu_baseline(cfg_name, ctx_positions=8):
     tensors = {e[0]: (e, synth_bytes(cfg, e)) for e in tensor_plan(cfg)}
     desc = desc_of(cfg)
     t0 = time.time()
-    m = O.OracleModel(desc, tensors, 64)
+    m = O.OracleModel(desc, tensors, ctx_positions + 8)
     load_s = time.time() - t0
     del tensors
     head_rows = desc.vocab // 16
@@ -80,6 +93,124 @@ def cpu_baseline(cfg_name, ctx_positions=8):
     }
 
 
+COPY_BYTES = 256 << 20  # calibration copy of the traffic counters
+
+
+def device_copy_calibration():
+    """A plain device-to-device copy of COPY_BYTES (the HIP runtime's copy kernel): what the traffic
+    counters read for it calibrates them."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(a), ctypes.c_size_t(COPY_BYTES)) or hip.hipMalloc(ctypes.byref(b), ctypes.c_size_t(COPY_BYTES)):
+        raise RuntimeError("hipMalloc failed")
+    hip.hipMemset(a, 1, ctypes.c_size_t(COPY_BYTES))
+    for _ in range(3):
+        hip.hipMemcpy(b, a, ctypes.c_size_t(COPY_BYTES), 3)  # hipMemcpyDeviceToDevice
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+
+
+def child_profile(args):
+    """The workload profiled by the roofline child runs: a short prompt, a few eager decode steps with
+    per-launch events (so the launch names come out in order), then the calibration copy."""
+    import dotnetfoundryllm_amd as F
+    from dotnetfoundryllm_amd.configs import CONFIGS, build_model
+
+    cfg = CONFIGS[args.config]
+    ctx = F.Context(0)
+    model, _ = build_model(ctx, cfg)
+    kv = F.HipKvCache(model, 64)
+    F.set_graph(kv, False)
+    fwd = F.HipForwardPass(model)
+    nxt, pos = 11, 0
+    for _ in range(4):
+        fwd.forward(nxt, pos, kv)
+        nxt = fwd.sample_greedy()
+        pos += 1
+    F.set_profile(kv, True)
+    for _ in range(args.profile_steps):
+        fwd.forward(nxt, pos, kv)
+        nxt = fwd.sample_greedy()
+        pos += 1
+    F.set_profile(kv, False)
+    ctx.sync()
+    print(json.dumps({"launch_names": F.profile_launches(kv)}), flush=True)
+    device_copy_calibration()
+    kv.close()
+    model.close()
+    ctx.close()
+
+
+def rocprof_child(args, mode, tmp):
+    """Runs this script's child workload under rocprofv3; returns the rows of its CSV output."""
+    out = os.path.join(tmp, mode)
+    cmd = ["rocprofv3"]
+    if mode == "trace":
+        cmd += ["--kernel-trace"]
+    else:
+        cmd += ["--pmc", mode]
+    cmd += ["--output-format", "csv", "-d", out, "-o", "run", "--",
+            sys.executable, os.path.abspath(__file__), "--child-profile", "--config", args.config,
+            "--profile-steps", str(args.profile_steps)]
+    env = dict(os.environ, TMPDIR=tmp)
+    r = subprocess.run(cmd, cwd=tmp, env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+    files = glob.glob(os.path.join(out, "**", "*kernel_trace.csv" if mode == "trace" else "*counter_collection.csv"),
+                      recursive=True)
+    if not files:
+        raise RuntimeError(f"rocprofv3 {mode}: no output (rc {r.returncode}): {r.stderr[-400:]}")
+    return list(csv.DictReader(open(files[0])))
+
+
+def kernel_key(row):
+    return (row["Kernel_Name"].split("(")[0], row.get("Grid_Size", row.get("Grid_Size_X", "")))
+
+
+def profiler_roofline(args, bytes_per_launch, dom_name, steps_launches):
+    """Mean duration and HBM traffic of the dominant launch from rocprofv3 child runs. The dominant
+    launch is identified by position: the profiled steps' launches in order are the HIP-event
+    names, so the kernel (and grid) at the positions named dom_name is the dominant one."""
+    tmp = tempfile.mkdtemp(prefix="fllm_roofline_")
+    try:
+        trace = rocprof_child(args, "trace", tmp)
+        trace.sort(key=lambda r: int(r["Start_Timestamp"]))
+        # the profiled launches (one kernel each, names in order) are the child's last fllm kernels
+        # (the step-parameter write at the start of each forward is not a profiled launch)
+        mine = [r for r in trace if "fllm::" in r["Kernel_Name"] and "k_set_params" not in r["Kernel_Name"]]
+        n_prof = len(steps_launches)
+        if n_prof == 0 or len(mine) < n_prof:
+            raise RuntimeError("kernel trace shorter than the profiled launches")
+        prof = mine[-n_prof:]
+        keys = {kernel_key(r) for r, nm in zip(prof, steps_launches) if nm == dom_name}
+        durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r, nm in zip(prof, steps_launches) if nm == dom_name]
+        avg_us = sum(durs) / len(durs) / 1e3
+        res = {"avg_launch_us": round(avg_us, 2), "duration_source": "rocprofv3 kernel trace",
+               "kernel_symbol": sorted(k[0] for k in keys)[0] if keys else None}
+        traffic = 0.0
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            rows = rocprof_child(args, counter, tmp)
+            per = {}
+            for r in rows:
+                if r["Counter_Name"] != counter:
+                    continue
+                k = (r["Dispatch_Id"], r["Kernel_Name"].split("(")[0], r.get("Grid_Size", ""))
+                per[k] = per.get(k, 0.0) + float(r["Counter_Value"])
+            copy = [v for (d, n, g), v in per.items() if "copyBuffer" in n]
+            dom = [v for (d, n, g), v in per.items() if (n, g) in keys]
+            if not copy or not dom:
+                raise RuntimeError(f"{counter}: missing copy or dominant-kernel dispatches")
+            # the copy reads and writes COPY_BYTES: counts per byte of that copy
+            factor = COPY_BYTES / (max(copy) * 1024.0)
+            kib = sum(dom) / len(dom)
+            res[counter.lower() + "_kib_raw"] = round(kib, 1)
+            res[counter.lower() + "_copy_factor"] = round(factor, 4)
+            traffic += kib * 1024.0 * factor
+        res["traffic"] = int(traffic)
+        return res
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,7 +222,12 @@ def main():
     ap.add_argument("--host-steps", type=int, default=32, help="steps of the host-driven loop timed after the device loop")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-rocprof", action="store_true", help="roofline from HIP events only (no profiler child runs)")
+    ap.add_argument("--child-profile", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.child_profile:
+        child_profile(args)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the decode path runs on a single MI355X)", file=sys.stderr)
@@ -167,10 +303,23 @@ def main():
     dom = ents[0]
     avg_ms = dom["ms"] / dom["launches"]
     bytes_launch = dom["bytes"] / dom["launches"]
-    achieved = bytes_launch / (avg_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "bytes_per_launch": int(bytes_launch), "avg_launch_us": round(avg_ms * 1e3, 2)}
+    roofline = {"bound": "hbm", "kernel": dom["name"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "traffic": None,
+                "bytes_per_launch": int(bytes_launch), "avg_launch_us": round(avg_ms * 1e3, 2),
+                "duration_source": "HIP events around each launch (eager profiled steps)"}
+    if not args.no_rocprof and shutil.which("rocprofv3"):
+        log("roofline: rocprofv3 child runs (kernel trace, FETCH_SIZE, WRITE_SIZE) ...")
+        try:
+            names = json.loads(subprocess.run([sys.executable, os.path.abspath(__file__), "--child-profile",
+                                               "--config", args.config, "--profile-steps", str(args.profile_steps)],
+                                              stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True,
+                                              timeout=300).stdout.strip().splitlines()[-1])["launch_names"]
+            roofline.update(profiler_roofline(args, bytes_launch, dom["name"], names))
+            roofline["event_avg_launch_us"] = round(avg_ms * 1e3, 2)
+        except Exception as e:  # the profiler is optional: keep the event timing
+            log(f"roofline: profiler runs failed ({e}); using HIP-event durations")
+    achieved = bytes_launch / (roofline["avg_launch_us"] * 1e-6) / 1e9
+    roofline["achieved"] = round(achieved, 1)
+    roofline["frac"] = round(achieved / HBM_PEAK_GBS, 4)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -339,6 +339,17 @@ def profile_reset(kv):
     _check(N.dev.fllm_seq_profile_reset(kv.h))
 
 
+def profile_launches(kv):
+    """Names of the profiled launches in launch order (one kernel each) since the last reset."""
+    out = []
+    name = C.create_string_buffer(64)
+    i = 0
+    while N.dev.fllm_seq_profile_launch(kv.h, i, name, 64) == 0:
+        out.append(name.value.decode())
+        i += 1
+    return out
+
+
 # ----------------------------------------------------------------------------------------
 class XoshiroRandom:
     def __init__(self, seed=0):

@@ -118,6 +118,7 @@ DEVICE_SIGS = {
     "fllm_seq_profile_count": (I32, [P, PI32]),
     "fllm_seq_profile_entry": (I32, [P, I32, C.c_char_p, I32, PI64, PF64, PF64]),
     "fllm_seq_profile_reset": (I32, [P]),
+    "fllm_seq_profile_launch": (I32, [P, I32, C.c_char_p, I32]),
 }
 
 HOST_SIGS = {

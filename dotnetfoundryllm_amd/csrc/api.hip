@@ -137,6 +137,7 @@ struct fllm_seq {
     std::vector<std::pair<std::string, double>> pending;  // name, bytes per pending launch
     std::map<std::string, ProfAgg> agg;
     std::vector<std::string> agg_order;
+    std::vector<std::string> launch_names;  // every profiled launch in order (bounded)
     std::vector<void*> allocs;
 };
 
@@ -711,6 +712,7 @@ static hipError_t prof_begin(fllm_seq* s, const char* name, double bytes) {
         s->ev.push_back(e);
     }
     s->pending.emplace_back(name, bytes);
+    if (s->launch_names.size() < (1u << 20)) s->launch_names.emplace_back(name);
     return hipEventRecord(s->ev[2 * i], s->st);
 }
 
@@ -790,7 +792,9 @@ static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const floa
         a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml;
         a.out = s->att; a.params = s->params;
         a.tab_out = tab ? s->tab_att : nullptr;
-        STEP("attention", bytes, launch_attn_decode(a, s->attn_lds, s->st));
+        STEP("attention", bytes, launch_attn_partial(a, s->attn_lds, s->st));
+        const double merge_bytes = 4.0 * (double)d.n_heads * s->attn_nc * (d.head_dim + 2) + 4.0 * s->m->qdim;
+        STEP("attention_merge", merge_bytes, launch_attn_merge(a, s->st));
     } else {
         STEP("attention", bytes,
              launch_attention(s->q, kc, vc, d.n_heads, d.n_kv_heads, d.head_dim, window, d.attn_scale, softcap,
@@ -1221,5 +1225,14 @@ extern "C" int32_t fllm_seq_profile_reset(fllm_seq* s) {
     s->agg.clear();
     s->agg_order.clear();
     s->pending.clear();
+    s->launch_names.clear();
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_seq_profile_launch(fllm_seq* s, int32_t i, char* name, int32_t name_cap) {
+    NOT_NULL(s);
+    NOT_NULL(name);
+    if (i < 0 || i >= (int32_t)s->launch_names.size()) return fail(FLLM_E_ARG_RANGE, "launch %d out of range", i);
+    if (name_cap > 0) snprintf(name, (size_t)name_cap, "%s", s->launch_names[(size_t)i].c_str());
     return FLLM_OK;
 }

@@ -358,7 +358,7 @@ static void attn_decode_g(const AttnArgs& a, dim3 grid, size_t lds, hipStream_t 
     }
 }
 
-hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st) {
+hipError_t launch_attn_partial(const AttnArgs& a, size_t lds, hipStream_t st) {
     dim3 grid(a.nkv, a.nc);
     const int g = a.nh / a.nkv;
     if (g < 1 || g > ATTN_GROUP_MAX || g * a.nkv != a.nh) return hipErrorInvalidValue;
@@ -367,14 +367,21 @@ hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st) {
         case 128: attn_decode_g<128>(a, grid, lds, st); break;
         default: attn_decode_g<256>(a, grid, lds, st); break;
     }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t st) {
     switch (a.hd) {
         case 64: k_attn_merge<64><<<a.nh, 64, 0, st>>>(a); break;
         case 128: k_attn_merge<128><<<a.nh, 64, 0, st>>>(a); break;
         default: k_attn_merge<256><<<a.nh, 64, 0, st>>>(a); break;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st) {
+    hipError_t e = launch_attn_partial(a, lds, st);
+    return e != hipSuccess ? e : launch_attn_merge(a, st);
 }
 
 }  // namespace fllm

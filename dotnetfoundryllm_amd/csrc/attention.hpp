@@ -26,6 +26,9 @@ struct AttnArgs {
 bool attn_fast_supported(int head_dim, int group, int max_seq);
 int attn_chunks(int n_kv, int max_seq, int n_cu);
 size_t attn_lds_bytes(int head_dim, int group, int nc, int max_seq);
+// the two kernels of the decode attention: per-chunk partials, then the merge over chunks
+hipError_t launch_attn_partial(const AttnArgs& a, size_t lds, hipStream_t st);
+hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t st);
 hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st);
 
 }  // namespace fllm

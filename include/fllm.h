@@ -251,6 +251,8 @@ FLLM_API int32_t fllm_seq_profile_count(fllm_seq* s, int32_t* n);
 FLLM_API int32_t fllm_seq_profile_entry(fllm_seq* s, int32_t i, char* name, int32_t name_cap,
                                         int64_t* launches, double* total_ms, double* total_bytes);
 FLLM_API int32_t fllm_seq_profile_reset(fllm_seq* s);
+/* Name of profiled launch i (0-based, in launch order since the last reset; one kernel each). */
+FLLM_API int32_t fllm_seq_profile_launch(fllm_seq* s, int32_t i, char* name, int32_t name_cap);
 
 #ifdef __cplusplus
 }
