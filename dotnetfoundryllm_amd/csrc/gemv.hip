@@ -898,10 +898,12 @@ template <> struct MfPick<FLLM_TYPE_Q6_K> { using Raw = MfQ6K; };
 // one 16-row tile, or for GLU the gate and up tiles of the same 16 rows. Workgroup w takes units
 // w, w + grid, w + 2 grid, ...; each of its nw waves covers KC = NB / nw consecutive chunks of every
 // row, so all waves walk the same (tile, chunk) item sequence: item i is chunk i % KC of the
-// workgroup's tile i / KC. Items stream through a ring of MF_RING chunk loads in flight that runs
+// workgroup's tile i / KC. Items stream through a ring of chunk loads in flight (MfRing) that runs
 // across tile and unit boundaries; the first loads go out before the activation prologue. A lane's
 // load addresses are its tile row's offset (computed once per tile) plus constants.
 constexpr int MF_RING = 4;
+// ring depth of a kernel (measured: deeper rings do not pay, a Q6_K ring of 8 is slower)
+template <int T, int KC> struct MfRing { static constexpr int v = MF_RING; };
 
 // unit u -> matrix of tile ts (0: gate / the segment's own, 1: up), its rows, first row, segment
 __device__ __forceinline__ void mf_tile_of(const GemvArgs& a, int u, int ts, const uint8_t*& W, int& rows, int& row0,
@@ -940,15 +942,16 @@ struct MfCtx {
     int kb0, q, m, lane, wave, nw, ltpu, T_slots, ufirst, ustride, items;
 };
 
-// One item: chunk c = r % KC of workgroup tile i / KC, from ring slot r % MF_RING. With refill the
-// slot is reloaded with item i + MF_RING. Every item but the last MF_RING of the workgroup refills,
+// One item: chunk c = r % KC of workgroup tile i / KC, from ring slot r % RING. With refill the
+// slot is reloaded with item i + RING. Every item but the last RING of the workgroup refills,
 // and the choice is a compile-time constant of the unrolled item position, so the number of loads
 // in flight at every wait is known at compile time.
 template <int T, int KC, bool REFILL>
 __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typename MfPick<T>::Raw* ring, int i, int r,
                                         float& y, uint32_t& offr, const uint8_t*& Wr, unsigned long long& best) {
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
-    const int c = r & (KC - 1), slot = r & (MF_RING - 1), b = x.kb0 + c;
+    constexpr int RING = MfRing<T, KC>::v;
+    const int c = r & (KC - 1), slot = r & (RING - 1), b = x.kb0 + c;
     v4i A[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) A[s] = *(__attribute__((address_space(3))) const v4i*)&x.at[(4 * c + s) * 12];
@@ -958,8 +961,8 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
     // results live)
     __asm__ volatile("" : "+v"(y));
     if (REFILL) {
-        const int cn = (r + MF_RING) & (KC - 1);
-        if (cn == 0) offr = mf_tile_base(a, x.ufirst, x.ustride, (i + MF_RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
+        const int cn = (r + RING) & (KC - 1);
+        if (cn == 0) offr = mf_tile_base(a, x.ufirst, x.ustride, (i + RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
         mf_issue(ring[slot], Wr, offr, cn, ((x.kb0 + cn) & 1) * 2, x.q);
     }
     // keep each item's fragment reads next to its MFMAs
@@ -995,7 +998,8 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     using Raw = typename MfPick<T>::Raw;
     constexpr int CB = mf_chunk_bytes(T);
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
-    constexpr int U = KC > MF_RING ? KC : MF_RING;  // items per unrolled iteration
+    constexpr int RING = MfRing<T, KC>::v;
+    constexpr int U = KC > RING ? KC : RING;  // items per unrolled iteration
     extern __shared__ float lds[];
     MfCtx x;
     x.nw = a.nw;  // blockDim.x / 64 (the kernel argument avoids reading the dispatch packet)
@@ -1042,13 +1046,13 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     for (int k = 0; k < TSL; k++) tsq[k] = sp[sm * (x.kb0 * 16 + min(x.lane + 64 * k, KC * 16 - 1))];
     __builtin_amdgcn_sched_barrier(0);
 
-    Raw ring[MF_RING];
+    Raw ring[RING];
     const uint8_t* Wr = a.seg[0].w;  // matrix and lane offset of the tile of the latest load
     uint32_t offr = 0;
 #pragma unroll
-    for (int r = 0; r < MF_RING; r++) {
+    for (int r = 0; r < RING; r++) {
         const int c = r & (KC - 1);
-        // fewer items than ring slots (a single tile of KC < MF_RING chunks): reload its last chunk
+        // fewer items than ring slots (a single tile of KC < RING chunks): reload its last chunk
         if (c == 0 && r < x.items) offr = mf_tile_base(a, x.ufirst, x.ustride, r >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
         mf_issue(ring[r], Wr, offr, c, ((x.kb0 + c) & 1) * 2, x.q);
     }
@@ -1135,8 +1139,8 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     // ---- items ----------------------------------------------------------------------------------
     unsigned long long best = 0ull;
     float y = 0.0f;
-    if constexpr (KC >= MF_RING) {
-        // whole iterations of one tile; the last one refills only its own items MF_RING ahead
+    if constexpr (KC >= RING) {
+        // whole iterations of one tile; the last one refills only its own items RING ahead
         const int n_it = x.items / U;
         for (int it = 0; it + 1 < n_it; it++) {
             x.at = abase;
@@ -1148,9 +1152,9 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
         __asm__ volatile("" : "+v"(x.at));
         const int i0 = (n_it - 1) * U;
 #pragma unroll
-        for (int r = 0; r < U - MF_RING; r++) mf_item<T, KC, true>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        for (int r = 0; r < U - RING; r++) mf_item<T, KC, true>(a, x, ring, i0 + r, r, y, offr, Wr, best);
 #pragma unroll
-        for (int r = U - MF_RING; r < U; r++) mf_item<T, KC, false>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        for (int r = U - RING; r < U; r++) mf_item<T, KC, false>(a, x, ring, i0 + r, r, y, offr, Wr, best);
     } else {
         for (int i0 = 0; i0 < x.items; i0 += U) {
             x.at = abase;
@@ -1159,7 +1163,7 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             for (int r = 0; r < U; r++) {
                 const int i = i0 + r;
                 if (i >= x.items) break;
-                if (i + MF_RING < x.items) mf_item<T, KC, true>(a, x, ring, i, r, y, offr, Wr, best);
+                if (i + RING < x.items) mf_item<T, KC, true>(a, x, ring, i, r, y, offr, Wr, best);
                 else mf_item<T, KC, false>(a, x, ring, i, r, y, offr, Wr, best);
             }
         }
