@@ -66,6 +66,7 @@ static const uint64_t kPad = 256;  // slack after every weight allocation for al
 
 struct Tensor {
     uint8_t* ptr = nullptr;
+    int layout = LAYOUT_ROWS;  // LAYOUT_TILES once finalize regroups it for the matrix-core GEMV
     int type = -1;
     int64_t rows = 0, cols = 0;
     uint64_t bytes = 0;
@@ -488,6 +489,36 @@ extern "C" int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer,
     return FLLM_OK;
 }
 
+// true when the decode launch over these matrices (GLU: gate, up) runs the matrix-core variant with
+// them regrouped into LAYOUT_TILES
+static bool tiles_launch_ok(const Tensor* const* t, int n, int glu) {
+    GemvArgs a{};
+    a.nseg = n;
+    a.glu = glu;
+    for (int i = 0; i < n; i++) {
+        if (!gemv_tiles_shape_ok(t[i]->type, t[i]->rows, t[i]->cols) || t[i]->cols != t[0]->cols) return false;
+        a.seg[i].w = t[i]->ptr; a.seg[i].layout = LAYOUT_TILES; a.seg[i].type = t[i]->type; a.seg[i].rows = (int)t[i]->rows;
+    }
+    return gemv_uses_mfma(a, t[0]->cols);
+}
+
+// regroup one matrix into LAYOUT_TILES on the device (same bytes, new allocation)
+static hipError_t pack_tiles(fllm_model* m, Tensor& t) {
+    if (t.layout == LAYOUT_TILES) return hipSuccess;
+    uint8_t* dev = nullptr;
+    hipError_t e = hipMalloc(&dev, t.bytes + kPad);
+    if (e != hipSuccess) return e;
+    hipStream_t st = m->ctx->stream;
+    e = launch_pack_tiles(t.type, t.ptr, dev, t.rows, t.cols, st);
+    if (e == hipSuccess) e = hipMemsetAsync(dev + t.bytes, 0, kPad, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) { hipFree(dev); return e; }
+    hipFree(t.ptr);
+    t.ptr = dev;
+    t.layout = LAYOUT_TILES;
+    return hipSuccess;
+}
+
 extern "C" int32_t fllm_model_finalize(fllm_model* m) {
     NOT_NULL(m);
     if (m->finalized) return FLLM_OK;
@@ -513,6 +544,27 @@ extern "C" int32_t fllm_model_finalize(fllm_model* m) {
     if (!m->output.present()) {  // GgufModelLoader.cs:365-366: tied LM head
         m->output = m->tok_embd;
         m->output_tied = true;
+    }
+    // Matrices whose decode launches run on the matrix cores are regrouped by 16-row tile, so that
+    // every load instruction of a wave reads contiguous memory; the token embedding (and a head
+    // tied to it) keeps its rows for the lookup.
+    std::vector<Tensor*> to_pack;
+    for (Layer& L : m->layers) {
+        const Tensor* qkv[3] = {&L.q, &L.k, &L.v};
+        if (tiles_launch_ok(qkv, 3, 0)) { to_pack.push_back(&L.q); to_pack.push_back(&L.k); to_pack.push_back(&L.v); }
+        const Tensor* gu[2] = {&L.gate, &L.up};
+        if (tiles_launch_ok(gu, 2, 1)) { to_pack.push_back(&L.gate); to_pack.push_back(&L.up); }
+        const Tensor* o[1] = {&L.o};
+        if (tiles_launch_ok(o, 1, 0)) to_pack.push_back(&L.o);
+        const Tensor* dn[1] = {&L.down};
+        if (tiles_launch_ok(dn, 1, 0)) to_pack.push_back(&L.down);
+    }
+    const Tensor* head[1] = {&m->output};
+    if (!m->output_tied && tiles_launch_ok(head, 1, 0)) to_pack.push_back(&m->output);
+    HIP_TRY(hipSetDevice(m->ctx->device));
+    for (Tensor* t : to_pack) {
+        hipError_t e = pack_tiles(m, *t);
+        if (e != hipSuccess) return fail(FLLM_E_DEVICE, "weight regrouping: %s", hipGetErrorString(e));
     }
     // RoPE inverse frequencies (LlamaForwardPass.cs:64-70), computed on the host with powf.
     int half = d.head_dim / 2;
@@ -765,12 +817,6 @@ static const char* gemv_name(int type) {
         if (_e != hipSuccess) return _e;                 \
     } while (0)
 
-static hipError_t gemv_step(fllm_seq* s, const Tensor& t, const float* xf, float* y, const float* res) {
-    double bytes = (double)t.bytes + 4.0 * (double)(t.cols + t.rows);
-    STEP(gemv_name(t.type), bytes, launch_gemv(t.mat(), xf, y, res, s->m->ctx->n_cu, s->st));
-    return hipSuccess;
-}
-
 static int layer_window(const fllm_model_desc& d, int l) {
     if (d.arch == FLLM_ARCH_MISTRAL) return d.sliding_window;             // MistralForwardPass.cs:131
     if (d.arch == FLLM_ARCH_GEMMA2 && (l % 2) == 0) return d.sliding_window;  // Gemma2ForwardPass.cs:87
@@ -805,7 +851,8 @@ static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const floa
 
 static GemvSeg seg_of(const Tensor& t, int epi, float* out, const float* bias, const float* resid) {
     GemvSeg g{};
-    g.w = t.ptr; g.type = t.type; g.rows = (int)t.rows; g.epi = epi; g.out = out; g.bias = bias; g.resid = resid;
+    g.w = t.ptr; g.layout = t.layout; g.type = t.type; g.rows = (int)t.rows;
+    g.epi = epi; g.out = out; g.bias = bias; g.resid = resid;
     return g;
 }
 
@@ -814,6 +861,22 @@ static hipError_t fused_step(fllm_seq* s, const char* name, GemvArgs& a, int64_t
     size_t lds;
     int grid = gemv_plan(a, cols, s->m->ctx->n_cu > 0 ? s->m->ctx->n_cu : 256, 0, &threads, &lds);
     STEP(name, bytes, launch_gemv_fused(a, grid, threads, lds, s->st));
+    return hipSuccess;
+}
+
+// y = W x (+ res), one launch per matrix
+static hipError_t gemv_step(fllm_seq* s, const Tensor& t, const float* xf, float* y, const float* res) {
+    double bytes = (double)t.bytes + 4.0 * (double)(t.cols + t.rows);
+    if (t.layout == LAYOUT_TILES) {
+        // a regrouped matrix is read by the matrix-core variant, as a one-segment launch
+        GemvArgs a{};
+        a.nseg = 1;
+        a.seg[0] = seg_of(t, res ? EPI_RESID : EPI_STORE, y, nullptr, res);
+        a.xin = XIN_F32;
+        a.x = xf;
+        return fused_step(s, gemv_name(t.type), a, t.cols, bytes);
+    }
+    STEP(gemv_name(t.type), bytes, launch_gemv(t.mat(), xf, y, res, s->m->ctx->n_cu, s->st));
     return hipSuccess;
 }
 
@@ -838,7 +901,9 @@ static bool mfma_launch(const Tensor* const* t, int n, int glu, int64_t cols) {
     GemvArgs a{};
     a.nseg = n;
     a.glu = glu;
-    for (int i = 0; i < n; i++) { a.seg[i].w = t[i]->ptr; a.seg[i].type = t[i]->type; a.seg[i].rows = (int)t[i]->rows; }
+    for (int i = 0; i < n; i++) {
+        a.seg[i].w = t[i]->ptr; a.seg[i].layout = t[i]->layout; a.seg[i].type = t[i]->type; a.seg[i].rows = (int)t[i]->rows;
+    }
     return gemv_uses_mfma(a, cols);
 }
 

@@ -791,6 +791,12 @@ __device__ __forceinline__ void mf_issue(MfQ4K& r, const uint8_t* __restrict__ W
     r.qa = *(const uint4*)(p + 16 + 16 * q);   // group q
     r.qb = *(const uint4*)(p + 80 + 16 * q);   // group q + 4
 }
+// the same fields from a LAYOUT_TILES region (lane = 16 q + n)
+__device__ __forceinline__ void mf_issue_tiles(MfQ4K& r, const uint8_t* __restrict__ reg, int lane, int n) {
+    r.hdr = *(const uint4*)(reg + 2048 + 16 * n);
+    r.qa = *(const uint4*)(reg + 16 * lane);
+    r.qb = *(const uint4*)(reg + 1024 + 16 * lane);
+}
 
 // fragment of one half-group from its 8 qs bytes: dword j = elements j, 4+j, 8+j, 12+j
 __device__ __forceinline__ v4i q4_frag(uint32_t w0, uint32_t w1) {
@@ -890,9 +896,36 @@ __device__ __forceinline__ float mf_compute(const MfQ6K& r, const v4i* A, const 
     return d * y;
 }
 
-template <int T> struct MfPick;
-template <> struct MfPick<FLLM_TYPE_Q4_K> { using Raw = MfQ4K; };
-template <> struct MfPick<FLLM_TYPE_Q6_K> { using Raw = MfQ6K; };
+// Q6_K from a LAYOUT_TILES region: the lane's ql, qh and scale bytes are 4-byte aligned there
+struct MfQ6KT { uint4 la, lb, h; uint32_t s, d; };
+__device__ __forceinline__ void mf_issue_tiles(MfQ6KT& r, const uint8_t* __restrict__ reg, int lane, int n) {
+    r.la = *(const uint4*)(reg + 16 * lane);           // ql 16q .. 16q + 15
+    r.lb = *(const uint4*)(reg + 1024 + 16 * lane);    // ql 64 + 16q ..
+    r.h = *(const uint4*)(reg + 2048 + 16 * lane);     // qh 8q .. 8q + 7, qh 32 + 8q .. 32 + 8q + 7
+    r.s = *(const uint32_t*)(reg + 3072 + 4 * lane);   // scales 2q, 2q + 1, 8 + 2q, 9 + 2q
+    r.d = *(const uint16_t*)(reg + 3328 + 2 * n);
+}
+
+__device__ __forceinline__ float mf_compute(const MfQ6KT& r, const v4i* A, const f32x4& sA, const f32x4& sB, int,
+                                            int) {
+    const v4i z = {0, 0, 0, 0};
+    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], q6_frag(r.la.x, r.la.y, r.h.x), z, 0, 0, 0);
+    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], q6_frag(r.la.z, r.la.w, r.h.y), z, 0, 0, 0);
+    const v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], q6_frag(r.lb.x, r.lb.y, r.h.z), z, 0, 0, 0);
+    const v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], q6_frag(r.lb.z, r.lb.w, r.h.w), z, 0, 0, 0);
+    const float d = h2f(r.d);
+    float y = (float)(int8_t)(r.s & 0xFF) * fmaf(sA.x, mf_total(D0), -32.0f * sA.z);
+    y = fmaf((float)(int8_t)((r.s >> 8) & 0xFF), fmaf(sA.y, mf_total(D1), -32.0f * sA.w), y);
+    y = fmaf((float)(int8_t)((r.s >> 16) & 0xFF), fmaf(sB.x, mf_total(D2), -32.0f * sB.z), y);
+    y = fmaf((float)(int8_t)(r.s >> 24), fmaf(sB.y, mf_total(D3), -32.0f * sB.w), y);
+    return d * y;
+}
+
+// register image of one chunk of one lane, per weight type and layout
+template <int T, bool IL> struct MfPick;
+template <bool IL> struct MfPick<FLLM_TYPE_Q4_K, IL> { using Raw = MfQ4K; };
+template <> struct MfPick<FLLM_TYPE_Q6_K, false> { using Raw = MfQ6K; };
+template <> struct MfPick<FLLM_TYPE_Q6_K, true> { using Raw = MfQ6KT; };
 
 // Persistent workgroup body of the MFMA variant for weight type T. The launch's rows form units:
 // one 16-row tile, or for GLU the gate and up tiles of the same 16 rows. Workgroup w takes units
@@ -900,7 +933,9 @@ template <> struct MfPick<FLLM_TYPE_Q6_K> { using Raw = MfQ6K; };
 // row, so all waves walk the same (tile, chunk) item sequence: item i is chunk i % KC of the
 // workgroup's tile i / KC. Items stream through a ring of chunk loads in flight (MfRing) that runs
 // across tile and unit boundaries; the first loads go out before the activation prologue. A lane's
-// load addresses are its tile row's offset (computed once per tile) plus constants.
+// load addresses are its tile row's offset (computed once per tile) plus constants; with
+// LAYOUT_TILES (IL) the tile offset is the same for all lanes of a wave and each load instruction
+// of a wave reads one contiguous piece.
 constexpr int MF_RING = 4;
 // ring depth of a kernel (measured: deeper rings do not pay, a Q6_K ring of 8 is slower)
 template <int T, int KC> struct MfRing { static constexpr int v = MF_RING; };
@@ -917,14 +952,16 @@ __device__ __forceinline__ void mf_tile_of(const GemvArgs& a, int u, int ts, con
     row0 = tile * MF_TILE;
 }
 
-// workgroup tile t (its units are ufirst, ufirst + ustride, ...): its matrix and this lane's byte
-// offset of chunk kb0 of row n of the tile
+// workgroup tile t (its units are ufirst, ufirst + ustride, ...): its matrix and the byte offset of
+// chunk kb0 of row n of the tile (IL: of the tile's region of chunk kb0; rb is the bytes of a row,
+// so row0 * rb is where the tile's regions start)
+template <bool IL>
 __device__ __forceinline__ uint32_t mf_tile_base(const GemvArgs& a, int ufirst, int ustride, int t, int ltpu,
                                                  uint32_t rb, uint32_t kboff, int n, const uint8_t*& W) {
     const int u = ufirst + (t >> ltpu) * ustride;
     int rows, row0, si;
     mf_tile_of(a, u, t & ((1 << ltpu) - 1), W, rows, row0, si);
-    const int row = min(row0 + n, rows - 1);
+    const int row = IL ? row0 : min(row0 + n, rows - 1);
     return (uint32_t)row * rb + kboff;
 }
 
@@ -942,12 +979,20 @@ struct MfCtx {
     int kb0, q, m, lane, wave, nw, ltpu, T_slots, ufirst, ustride, items;
 };
 
+// issue the loads of chunk kb0 + c of the tile at offset off of W into r
+template <int T, bool IL>
+__device__ __forceinline__ void mf_load(typename MfPick<T, IL>::Raw& r, const uint8_t* W, uint32_t off, int c,
+                                        const MfCtx& x) {
+    if constexpr (IL) mf_issue_tiles(r, W + off + (uint32_t)(c * MF_TILE * mf_chunk_bytes(T)), x.lane, x.m);
+    else mf_issue(r, W, off, c, ((x.kb0 + c) & 1) * 2, x.q);
+}
+
 // One item: chunk c = r % KC of workgroup tile i / KC, from ring slot r % RING. With refill the
 // slot is reloaded with item i + RING. Every item but the last RING of the workgroup refills,
 // and the choice is a compile-time constant of the unrolled item position, so the number of loads
 // in flight at every wait is known at compile time.
-template <int T, int KC, bool REFILL>
-__device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typename MfPick<T>::Raw* ring, int i, int r,
+template <int T, int KC, bool IL, bool REFILL>
+__device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typename MfPick<T, IL>::Raw* ring, int i, int r,
                                         float& y, uint32_t& offr, const uint8_t*& Wr, unsigned long long& best) {
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
     constexpr int RING = MfRing<T, KC>::v;
@@ -962,8 +1007,8 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
     __asm__ volatile("" : "+v"(y));
     if (REFILL) {
         const int cn = (r + RING) & (KC - 1);
-        if (cn == 0) offr = mf_tile_base(a, x.ufirst, x.ustride, (i + RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
-        mf_issue(ring[slot], Wr, offr, cn, ((x.kb0 + cn) & 1) * 2, x.q);
+        if (cn == 0) offr = mf_tile_base<IL>(a, x.ufirst, x.ustride, (i + RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
+        mf_load<T, IL>(ring[slot], Wr, offr, cn, x);
     }
     // keep each item's fragment reads next to its MFMAs
     __builtin_amdgcn_sched_barrier(0);
@@ -993,9 +1038,9 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
 
 // TABIN: the input is an activation table (XIN_TAB); otherwise a vector, quantized here. The
 // workgroup is number wg of ng that share units [u0, u0 + nu) of the launch.
-template <int T, int KC, bool TABIN>
+template <int T, int KC, bool TABIN, bool IL>
 __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int wg, int ng) {
-    using Raw = typename MfPick<T>::Raw;
+    using Raw = typename MfPick<T, IL>::Raw;
     constexpr int CB = mf_chunk_bytes(T);
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
     constexpr int RING = MfRing<T, KC>::v;
@@ -1020,7 +1065,7 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     // fragment (chunk kb0 + c, step s) of this lane: x.at[(4c + s) * 12]
     lds_tab* const abase = a_live ? atab + atab_index(x.kb0, 0, x.m >> 2, x.m & 3) : zeros;
     x.rb = (uint32_t)NB * CB;
-    x.kboff = (uint32_t)x.kb0 * CB;
+    x.kboff = (uint32_t)x.kb0 * (IL ? MF_TILE * CB : CB);
     x.ufirst = u0 + wg;
     x.ustride = ng;
     const int my_units = (nu - wg + ng - 1) / ng;
@@ -1053,8 +1098,8 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     for (int r = 0; r < RING; r++) {
         const int c = r & (KC - 1);
         // fewer items than ring slots (a single tile of KC < RING chunks): reload its last chunk
-        if (c == 0 && r < x.items) offr = mf_tile_base(a, x.ufirst, x.ustride, r >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
-        mf_issue(ring[r], Wr, offr, c, ((x.kb0 + c) & 1) * 2, x.q);
+        if (c == 0 && r < x.items) offr = mf_tile_base<IL>(a, x.ufirst, x.ustride, r >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
+        mf_load<T, IL>(ring[r], Wr, offr, c, x);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -1146,15 +1191,15 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             x.at = abase;
             __asm__ volatile("" : "+v"(x.at));  // re-read the fragments from LDS each iteration
 #pragma unroll
-            for (int r = 0; r < U; r++) mf_item<T, KC, true>(a, x, ring, it * U + r, r, y, offr, Wr, best);
+            for (int r = 0; r < U; r++) mf_item<T, KC, IL, true>(a, x, ring, it * U + r, r, y, offr, Wr, best);
         }
         x.at = abase;
         __asm__ volatile("" : "+v"(x.at));
         const int i0 = (n_it - 1) * U;
 #pragma unroll
-        for (int r = 0; r < U - RING; r++) mf_item<T, KC, true>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        for (int r = 0; r < U - RING; r++) mf_item<T, KC, IL, true>(a, x, ring, i0 + r, r, y, offr, Wr, best);
 #pragma unroll
-        for (int r = U - RING; r < U; r++) mf_item<T, KC, false>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        for (int r = U - RING; r < U; r++) mf_item<T, KC, IL, false>(a, x, ring, i0 + r, r, y, offr, Wr, best);
     } else {
         for (int i0 = 0; i0 < x.items; i0 += U) {
             x.at = abase;
@@ -1163,57 +1208,62 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             for (int r = 0; r < U; r++) {
                 const int i = i0 + r;
                 if (i >= x.items) break;
-                if (i + RING < x.items) mf_item<T, KC, true>(a, x, ring, i, r, y, offr, Wr, best);
-                else mf_item<T, KC, false>(a, x, ring, i, r, y, offr, Wr, best);
+                if (i + RING < x.items) mf_item<T, KC, IL, true>(a, x, ring, i, r, y, offr, Wr, best);
+                else mf_item<T, KC, IL, false>(a, x, ring, i, r, y, offr, Wr, best);
             }
         }
     }
     if (a.seg[0].epi == EPI_LOGITS && threadIdx.x == 0) a.wg_keys[blockIdx.x] = best;  // reduced by the argmax kernel
 }
 
-// one kernel per (weight type, chunks per wave, input kind), each with its own register
-// allocation; every segment of such a launch has the same weight type
-template <int T, int KC, bool TABIN>
+// one kernel per (weight type, chunks per wave, input kind, weight layout), each with its own
+// register allocation; every segment of such a launch has the same weight type and layout
+template <int T, int KC, bool TABIN, bool IL>
 __global__ __launch_bounds__(512) void k_gemv_mfma(const GemvArgs a) {
-    mfma_body<T, KC, TABIN>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
+    mfma_body<T, KC, TABIN, IL>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // Two weight types in one launch (q and k in Q4_K, v in Q6_K): the first mix_wg workgroups take the
 // Q4_K units [0, mix_unit), the others the Q6_K units after them.
-template <int KC, bool TABIN>
+template <int KC, bool TABIN, bool IL>
 __global__ __launch_bounds__(512) void k_gemv_mfma_mix(const GemvArgs a) {
     if ((int)blockIdx.x < a.mix_wg)
-        mfma_body<FLLM_TYPE_Q4_K, KC, TABIN>(a, 0, a.mix_unit, (int)blockIdx.x, a.mix_wg);
+        mfma_body<FLLM_TYPE_Q4_K, KC, TABIN, IL>(a, 0, a.mix_unit, (int)blockIdx.x, a.mix_wg);
     else
-        mfma_body<FLLM_TYPE_Q6_K, KC, TABIN>(a, a.mix_unit, a.nunits - a.mix_unit, (int)blockIdx.x - a.mix_wg,
-                                            (int)gridDim.x - a.mix_wg);
+        mfma_body<FLLM_TYPE_Q6_K, KC, TABIN, IL>(a, a.mix_unit, a.nunits - a.mix_unit, (int)blockIdx.x - a.mix_wg,
+                                                (int)gridDim.x - a.mix_wg);
 }
 
 typedef void (*MfKernel)(const GemvArgs);
-template <int T, bool TABIN>
+template <int T, bool TABIN, bool IL>
 static MfKernel mf_kernel_in(int kc) {
     switch (kc) {
-        case 1: return k_gemv_mfma<T, 1, TABIN>;
-        case 2: return k_gemv_mfma<T, 2, TABIN>;
-        case 4: return k_gemv_mfma<T, 4, TABIN>;
-        default: return k_gemv_mfma<T, 8, TABIN>;
+        case 1: return k_gemv_mfma<T, 1, TABIN, IL>;
+        case 2: return k_gemv_mfma<T, 2, TABIN, IL>;
+        case 4: return k_gemv_mfma<T, 4, TABIN, IL>;
+        default: return k_gemv_mfma<T, 8, TABIN, IL>;
     }
 }
-template <bool TABIN>
+template <bool TABIN, bool IL>
 static MfKernel mf_kernel_mix(int kc) {
     switch (kc) {
-        case 1: return k_gemv_mfma_mix<1, TABIN>;
-        case 2: return k_gemv_mfma_mix<2, TABIN>;
-        case 4: return k_gemv_mfma_mix<4, TABIN>;
-        default: return k_gemv_mfma_mix<8, TABIN>;
+        case 1: return k_gemv_mfma_mix<1, TABIN, IL>;
+        case 2: return k_gemv_mfma_mix<2, TABIN, IL>;
+        case 4: return k_gemv_mfma_mix<4, TABIN, IL>;
+        default: return k_gemv_mfma_mix<8, TABIN, IL>;
     }
+}
+template <bool IL>
+static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
+    const bool tab = a.xin == XIN_TAB;
+    if (a.mix_wg > 0) return tab ? mf_kernel_mix<true, IL>(kc) : mf_kernel_mix<false, IL>(kc);
+    if (a.seg[0].type == FLLM_TYPE_Q6_K)
+        return tab ? mf_kernel_in<FLLM_TYPE_Q6_K, true, IL>(kc) : mf_kernel_in<FLLM_TYPE_Q6_K, false, IL>(kc);
+    return tab ? mf_kernel_in<FLLM_TYPE_Q4_K, true, IL>(kc) : mf_kernel_in<FLLM_TYPE_Q4_K, false, IL>(kc);
 }
 // the kernel of a planned launch (a.mix_wg > 0: two weight types)
 static MfKernel mf_kernel(const GemvArgs& a, int kc) {
-    const bool tab = a.xin == XIN_TAB;
-    if (a.mix_wg > 0) return tab ? mf_kernel_mix<true>(kc) : mf_kernel_mix<false>(kc);
-    if (a.seg[0].type == FLLM_TYPE_Q6_K) return tab ? mf_kernel_in<FLLM_TYPE_Q6_K, true>(kc) : mf_kernel_in<FLLM_TYPE_Q6_K, false>(kc);
-    return tab ? mf_kernel_in<FLLM_TYPE_Q4_K, true>(kc) : mf_kernel_in<FLLM_TYPE_Q4_K, false>(kc);
+    return a.seg[0].layout == LAYOUT_TILES ? mf_kernel_layout<true>(a, kc) : mf_kernel_layout<false>(a, kc);
 }
 
 // WIDE: rows of more than 512 groups (up to 16 waves per workgroup), no prefetch.
@@ -1266,6 +1316,16 @@ static bool mfma_ok(const GemvArgs& a, int64_t cols) {
     for (int i = 0; i < a.nseg; i++) {
         const int t = a.seg[i].type;
         if (mf_chunk_bytes(t) == 0) return false;
+        // byte offsets within a matrix are 32-bit
+        if ((uint64_t)a.seg[i].rows * (uint64_t)NB * (uint64_t)mf_chunk_bytes(t) >= (1ull << 32)) return false;
+        // one layout per launch; tiles hold whole 16-row tiles
+        if (a.seg[i].layout != a.seg[0].layout) return false;
+        if (a.seg[i].layout == LAYOUT_TILES) {
+            if (a.seg[i].rows % MF_TILE != 0 || ((uintptr_t)a.seg[i].w & 15) != 0) return false;
+            if (t != a.seg[0].type && (a.glu || t != FLLM_TYPE_Q6_K || a.seg[0].type != FLLM_TYPE_Q4_K)) return false;
+            if (i > 0 && t == FLLM_TYPE_Q4_K && a.seg[i - 1].type != FLLM_TYPE_Q4_K) return false;
+            continue;
+        }
         // one type, or Q4_K segments followed by Q6_K ones (the two-type kernel; not for GLU)
         if (t != a.seg[0].type && (a.glu || t != FLLM_TYPE_Q6_K || a.seg[0].type != FLLM_TYPE_Q4_K)) return false;
         if (i > 0 && t == FLLM_TYPE_Q4_K && a.seg[i - 1].type != FLLM_TYPE_Q4_K) return false;
@@ -1371,10 +1431,72 @@ int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_t
     return wg;
 }
 
+bool gemv_tiles_shape_ok(int type, int64_t rows, int64_t cols) {
+    if (mf_chunk_bytes(type) == 0 || rows <= 0 || rows % MF_TILE != 0 || rows > (1 << 30) || cols % 256 != 0) return false;
+    const int NB = (int)(cols / 256);
+    if (mf_waves(NB) == 0 || mf_lds(mf_waves(NB), NB, true) > 160 * 1024) return false;
+    return (uint64_t)rows * (uint64_t)NB * (uint64_t)mf_chunk_bytes(type) < (1ull << 32);
+}
+
+// LAYOUT_TILES of a Q4_K or Q6_K matrix (rows a multiple of 16, NB chunks per row): the blocks of
+// tile t (rows 16t .. 16t + 15) in chunk column kb fill region t * NB + kb of 16 block sizes, laid
+// out so that matrix-core lane L = 16 q + n (tile row n, quarter q) finds its part of row n as
+// 16-byte pieces at 16 L of 1 KiB slices, and the fields a row's four lanes share at n:
+//   Q4_K, 2304 B: [0, 1024) qs bytes 16q .. 16q + 15; [1024, 2048) qs bytes 64 + 16q .. ;
+//                 [2048, 2304) block bytes 0 .. 15 (d, dmin, scales) at 16 n
+//   Q6_K, 3360 B: [0, 1024) ql 16q .. ; [1024, 2048) ql 64 + 16q .. ; [2048, 3072) qh 8q .. 8q + 7
+//                 then qh 32 + 8q .. ; [3072, 3328) scales 2q, 2q + 1, 8 + 2q, 9 + 2q at 4 L;
+//                 [3328, 3360) d at 2 n
+// Every block byte has exactly one place, so the regrouped matrix dequantizes to the same values.
+// One thread per block.
+__global__ void k_pack_tiles(int type, const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int rows, int NB) {
+    const int64_t nblk = (int64_t)rows * NB;
+    const int bpb = type == FLLM_TYPE_Q6_K ? 210 : 144;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nblk; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / NB;
+        const int kb = (int)(i % NB), n = (int)(r & 15);
+        const uint8_t* b = src + i * bpb;
+        uint8_t* reg = dst + ((r >> 4) * NB + kb) * 16 * bpb;
+        for (int q = 0; q < 4; q++) {
+            const int L = 16 * q + n;
+            if (type == FLLM_TYPE_Q6_K) {
+                for (int j = 0; j < 16; j++) reg[16 * L + j] = b[16 * q + j];
+                for (int j = 0; j < 16; j++) reg[1024 + 16 * L + j] = b[64 + 16 * q + j];
+                for (int j = 0; j < 8; j++) reg[2048 + 16 * L + j] = b[128 + 8 * q + j];
+                for (int j = 0; j < 8; j++) reg[2048 + 16 * L + 8 + j] = b[160 + 8 * q + j];
+                reg[3072 + 4 * L] = b[192 + 2 * q];
+                reg[3072 + 4 * L + 1] = b[193 + 2 * q];
+                reg[3072 + 4 * L + 2] = b[200 + 2 * q];
+                reg[3072 + 4 * L + 3] = b[201 + 2 * q];
+            } else {
+                for (int j = 0; j < 16; j++) reg[16 * L + j] = b[16 + 16 * q + j];
+                for (int j = 0; j < 16; j++) reg[1024 + 16 * L + j] = b[80 + 16 * q + j];
+            }
+        }
+        if (type == FLLM_TYPE_Q6_K) {
+            reg[3328 + 2 * n] = b[208];
+            reg[3328 + 2 * n + 1] = b[209];
+        } else {
+            for (int j = 0; j < 16; j++) reg[2048 + 16 * n + j] = b[j];
+        }
+    }
+}
+
+hipError_t launch_pack_tiles(int type, const uint8_t* src, uint8_t* dst, int64_t rows, int64_t cols, hipStream_t st) {
+    if (!gemv_tiles_shape_ok(type, rows, cols)) return hipErrorInvalidValue;
+    const int64_t nblk = rows * (cols / 256);
+    const int64_t grid = (nblk + 255) / 256 < 65536 ? (nblk + 255) / 256 : 65536;
+    k_pack_tiles<<<(int)grid, 256, 0, st>>>(type, src, dst, (int)rows, (int)(cols / 256));
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st) {
     if (grid <= 0) return hipSuccess;
     // the matrix-core prologue always reads its input: the table, or the vector (cols floats)
     if (a.mfma && (a.xin == XIN_TAB ? a.xtab == nullptr : a.x == nullptr)) return hipErrorInvalidValue;
+    // LAYOUT_TILES matrices are read only by the matrix-core variant
+    for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].layout == LAYOUT_TILES && !a.mfma) return hipErrorInvalidValue;
     if (a.mfma)
         mf_kernel(a, (a.G / 8) / (block_threads / 64))<<<grid, block_threads, lds, st>>>(a);
     else if (block_threads <= 512)

@@ -11,9 +11,16 @@ enum { XIN_F32 = 0, XIN_NORM = 1, XIN_EMBED_NORM = 2, XIN_TAB = 3 };
 // epilogue of a segment
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_Q = 2, EPI_K = 3, EPI_V = 4, EPI_LOGITS = 5 };
 
+// weight layout of a matrix
+// LAYOUT_ROWS: GGUF rows, row r = elements [r*cols, (r+1)*cols) of the block stream.
+// LAYOUT_TILES: the same blocks regrouped by 16-row tile (launch_pack_tiles), read only by the
+// matrix-core variant.
+enum { LAYOUT_ROWS = 0, LAYOUT_TILES = 1 };
+
 // One matrix of a fused launch. The segment owns workgroups [wg_begin, next segment's wg_begin).
 struct GemvSeg {
-    const uint8_t* w;      // GGUF blocks, row r = elements [r*cols, (r+1)*cols)
+    const uint8_t* w;      // weight blocks in `layout`
+    int layout;
     int type;
     int rows;
     int wg_begin;
@@ -73,6 +80,11 @@ int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_t
 bool gemv_uses_mfma(const GemvArgs& a, int64_t cols);
 // bytes of the activation table of a vector of `cols` elements
 size_t gemv_tab_bytes(int64_t cols);
+// true when a Q4_K / Q6_K matrix of this shape can be stored as LAYOUT_TILES (rows a multiple of 16,
+// whole 256-element chunks per row, a matrix-core wave split of the row)
+bool gemv_tiles_shape_ok(int type, int64_t rows, int64_t cols);
+// regroup a GGUF-row matrix (src) into LAYOUT_TILES (dst, same byte count); a byte permutation
+hipError_t launch_pack_tiles(int type, const uint8_t* src, uint8_t* dst, int64_t rows, int64_t cols, hipStream_t st);
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st);
 
 }  // namespace fllm
