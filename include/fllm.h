@@ -146,7 +146,9 @@ FLLM_API int32_t fllm_model_create(fllm_ctx* ctx, const fllm_model_desc* desc, f
 FLLM_API int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer, int32_t type,
                                    const void* bytes, uint64_t nbytes);
 /* Checks that every required slot is present; ties output.weight to token_embd.weight when
- * absent (GgufModelLoader.cs:365-366); builds the RoPE inverse-frequency table. */
+ * absent (GgufModelLoader.cs:365-366); builds the RoPE inverse-frequency table. Q4_K / Q6_K
+ * matrices whose decode launches run on the matrix cores are regrouped on the device by 16-row
+ * tile (the same blocks, permuted; one temporary copy of a matrix at a time). */
 FLLM_API int32_t fllm_model_finalize(fllm_model* m);
 FLLM_API int32_t fllm_model_destroy(fllm_model* m);
 /* The description the model was created with. */
