@@ -2,7 +2,8 @@
 
 Workload: random-init weights of the Llama-3-8B shape (dim 4096, 32 layers, 32/8 heads x 128,
 FFN 14336, vocab 128256; Q4_K for q/k/o/gate/up, Q6_K for v/down/output) generated from a
-seed, a 512-token random prompt prefilled token by token, then greedy decode at batch 1.
+seed, a 512-token random prompt prefilled in one batched pass (fllm_prefill), then greedy decode
+at batch 1.
 A "step" is one decode token: the forward pass and the greedy argmax. The timed steps run as a
 device-side loop (each step's argmax is the next step's input token on the device, one graph
 launch per step, the tokens are read back after the last step); the same tokens come out of the
@@ -252,7 +253,11 @@ def main():
     fwd = F.HipForwardPass(model)
     prompt = F.synth_tokens(cfg["seed"], 0, cfg["vocab"], args.prompt)
 
-    # prefill: Forward on prompt[0..n-2] (LlamaLanguageModel.cs:133-137)
+    # prefill: Forward on prompt[0..n-2] (LlamaLanguageModel.cs:133-137). A first pass pays the
+    # one-time costs (scratch allocation, kernel loading); the timed pass starts from an empty cache.
+    fwd.prefill(prompt[:-1], 0, kv)
+    F._check(F.N.dev.fllm_seq_sync(kv.h))
+    kv.clear()
     t = time.perf_counter()
     fwd.prefill(prompt[:-1], 0, kv)
     ctx.sync()
@@ -341,7 +346,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"{cfg['name']}: {args.prompt}-token random prompt prefilled token by token, then greedy "
+            "workload": f"{cfg['name']}: {args.prompt}-token random prompt, batched prefill, then greedy "
                         f"decode at batch 1 (positions {args.prompt - 1 + args.warmup}..{args.prompt - 2 + args.warmup + args.steps}), "
                         "device-side greedy loop",
             "weights": "Q4_K (q,k,o,gate,up) + Q6_K (v,down,output), seeded random blocks",

@@ -1,12 +1,14 @@
 """Build step for the native libraries (gfx950 HIP device library + C++ host library).
 
 Compiles in-tree so the built .so files sit next to the sources:
-  dotnetfoundryllm_amd/libfllm_hip.so   <- csrc/kernels.hip csrc/api.hip   (hipcc, gfx950)
+  dotnetfoundryllm_amd/libfllm_hip.so   <- csrc/*.hip (hipcc, gfx950; one object per source, compiled
+                                           in parallel under _build/, then linked)
   dotnetfoundryllm_amd/libfllm_host.so  <- host/fllm_host.cpp              (g++, links the above)
 """
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
@@ -19,7 +21,6 @@ HIP_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-fvisibility=hidden",
     # a*b+c stays two roundings unless fmaf() is written: dequantized values and the RoPE
     # rotation must follow the reference's operation order bit for bit
@@ -41,11 +42,23 @@ def _run(cmd, cwd):
     return out
 
 
+DEVICE_SRCS = ["csrc/kernels.hip", "csrc/gemv.hip", "csrc/attention.hip", "csrc/prefill.hip", "csrc/api.hip"]
+
+
 def build_device_lib(verbose=False):
-    srcs = ["csrc/kernels.hip", "csrc/gemv.hip", "csrc/attention.hip", "csrc/api.hip"]
+    objdir = os.path.join(PKG, "_build")
+    os.makedirs(objdir, exist_ok=True)
+
+    def compile_one(src):
+        obj = os.path.join("_build", os.path.splitext(os.path.basename(src))[0] + ".o")
+        return obj, _run([HIPCC, *HIP_FLAGS, "-c", "-o", obj, src], PKG)
+
+    with ThreadPoolExecutor(max_workers=min(len(DEVICE_SRCS), os.cpu_count() or 1)) as pool:
+        results = list(pool.map(compile_one, DEVICE_SRCS))
     out = "libfllm_hip.so"
     tmp = out + ".tmp"
-    log = _run([HIPCC, *HIP_FLAGS, "-o", tmp, *srcs], PKG)
+    log = "\n".join(r[1] for r in results)
+    log += _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[r[0] for r in results]], PKG)
     os.replace(os.path.join(PKG, tmp), os.path.join(PKG, out))
     if verbose and log.strip():
         print(log)

@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -14,6 +15,7 @@
 #include "attention.hpp"
 #include "gemv.hpp"
 #include "kernels.hpp"
+#include "prefill.hpp"
 
 using namespace fllm;
 
@@ -140,6 +142,10 @@ struct fllm_seq {
     std::vector<std::string> agg_order;
     std::vector<std::string> launch_names;  // every profiled launch in order (bounded)
     std::vector<void*> allocs;
+    // batched prefill scratch for chunks of up to pf_cap tokens (allocated on first use)
+    int pf_cap = 0, pf_ldx = 0;
+    float *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_gu = nullptr, *pf_tmp = nullptr;
+    int* pf_tok = nullptr;
 };
 
 // =====================================================================================
@@ -1160,14 +1166,150 @@ extern "C" int32_t fllm_decode_greedy(fllm_seq* s, int32_t token, int32_t positi
     return FLLM_OK;
 }
 
+// ---- batched prefill ---------------------------------------------------------------------------
+static const int kPrefillChunk = 512;  // tokens per pass through the layers
+
+// the batched path covers the fast attention's head dims and 32-aligned projection widths
+static bool prefill_batched_ok(const fllm_seq* s) {
+    const fllm_model_desc& d = s->m->d;
+    const int hd = d.head_dim;
+    return (hd == 64 || hd == 128 || hd == 256) && d.n_kv_heads > 0 && d.n_heads % d.n_kv_heads == 0 &&
+           d.hidden % 32 == 0 && s->m->qdim % 32 == 0 && d.ffn % 32 == 0;
+}
+
+static hipError_t prefill_alloc(fllm_seq* s) {
+    if (s->pf_cap > 0) return hipSuccess;
+    const fllm_model& m = *s->m;
+    const int cap = s->max_seq < kPrefillChunk ? s->max_seq : kPrefillChunk;
+    size_t ldx = (size_t)std::max(m.d.hidden, m.d.ffn);
+    ldx = (ldx + 3) / 4 * 4;
+    const size_t H = (size_t)m.d.hidden, C = (size_t)cap;
+    hipError_t e = hipSuccess;
+#define PF_ALLOC(ptr, count) \
+    if (e == hipSuccess) e = seq_alloc(s, &(ptr), (count))
+    PF_ALLOC(s->pf_x, C * H);
+    PF_ALLOC(s->pf_qkv, C * (size_t)(m.qdim + 2 * m.kvdim));
+    PF_ALLOC(s->pf_att, C * (size_t)m.qdim);
+    PF_ALLOC(s->pf_gu, C * 2 * (size_t)m.d.ffn);
+    PF_ALLOC(s->pf_tmp, C * H);
+    PF_ALLOC(s->pf_xn, C * ldx);
+    PF_ALLOC(s->pf_tok, C);
+#undef PF_ALLOC
+    if (e == hipSuccess) {
+        s->pf_cap = cap;
+        s->pf_ldx = (int)ldx;
+    }
+    return e;
+}
+
+// y (+)= X W^T over the chunk's rows; X = pf_xn (row stride pf_ldx) or the given rows
+static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor& w, int T, float* y, int ldy, bool add,
+                          const float* x = nullptr, int ldx = 0) {
+    PfGemm g{};
+    g.x = x ? x : s->pf_xn;
+    g.ldx = x ? ldx : s->pf_ldx;
+    g.w = w.ptr; g.type = w.type; g.layout = w.layout;
+    g.N = (int)w.rows; g.K = (int)w.cols;
+    g.y = y; g.ldy = ldy; g.T = T; g.add = add ? 1 : 0;
+    STEP(name, (double)w.bytes + 8.0 * T * (double)(w.rows + w.cols), launch_pf_gemm(g, s->m->ctx->n_cu, s->st));
+    return hipSuccess;
+}
+
+// T prompt tokens (device copy in pf_tok) at positions pos0.. through every layer; leaves the
+// residual stream of the T rows in pf_x and their K / V in the cache.
+static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
+    fllm_model* m = s->m;
+    const fllm_model_desc& d = m->d;
+    const bool gemma = d.arch == FLLM_ARCH_GEMMA2;
+    const int H = d.hidden, qdim = m->qdim, kvdim = m->kvdim, F = d.ffn, ldx = s->pf_ldx;
+    const float eps = gemma ? 1e-6f : d.norm_eps;
+    const int nk = gemma ? 1 : 0;
+    const int ldq = qdim + 2 * kvdim;
+    const size_t layer_kv = (size_t)s->max_seq * kvdim;
+    hipError_t e;
+    STEP("pf_embed", 4.0 * T * H, launch_pf_embed(s->pf_tok, T, m->tok_embd.ptr, m->tok_embd.type, H, s->pf_x, s->st));
+    for (int l = 0; l < d.n_layers; l++) {
+        const Layer& L = m->layers[(size_t)l];
+        float* kc = s->kc + (size_t)l * layer_kv;
+        float* vc = s->vc + (size_t)l * layer_kv;
+        STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.attn_norm, eps, nk, s->pf_xn, ldx, s->st));
+        if ((e = pf_gemm(s, "pf_q", L.q, T, s->pf_qkv, ldq, false)) != hipSuccess) return e;
+        if ((e = pf_gemm(s, "pf_k", L.k, T, s->pf_qkv + qdim, ldq, false)) != hipSuccess) return e;
+        if ((e = pf_gemm(s, "pf_v", L.v, T, s->pf_qkv + qdim + kvdim, ldq, false)) != hipSuccess) return e;
+        STEP("pf_qkv_post", 8.0 * T * ldq,
+             launch_pf_qkv_post(s->pf_qkv, ldq, T, pos0, L.bq, L.bk, L.bv, s->rope, d.n_heads, d.n_kv_heads, d.head_dim,
+                                kc, vc, s->st));
+        PfAttn at{};
+        at.q = s->pf_qkv; at.ldq = ldq; at.kc = kc; at.vc = vc; at.out = s->pf_att;
+        at.T = T; at.pos0 = pos0; at.nh = d.n_heads; at.nkv = d.n_kv_heads; at.hd = d.head_dim; at.kvdim = kvdim;
+        at.window = layer_window(d, l); at.scale = d.attn_scale; at.softcap = gemma ? d.attn_softcap : 0.0f;
+        STEP("pf_attention", 8.0 * (double)kvdim * (pos0 + T) + 8.0 * T * qdim, launch_pf_attn(at, s->st));
+        if (gemma) {
+            if ((e = pf_gemm(s, "pf_o", L.o, T, s->pf_tmp, H, false, s->pf_att, qdim)) != hipSuccess) return e;
+            STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_attn, s->pf_x, s->st));
+        } else {
+            if ((e = pf_gemm(s, "pf_o", L.o, T, s->pf_x, H, true, s->pf_att, qdim)) != hipSuccess) return e;
+        }
+        STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.ffn_norm, eps, nk, s->pf_xn, ldx, s->st));
+        if ((e = pf_gemm(s, "pf_gate", L.gate, T, s->pf_gu, 2 * F, false)) != hipSuccess) return e;
+        if ((e = pf_gemm(s, "pf_up", L.up, T, s->pf_gu + F, 2 * F, false)) != hipSuccess) return e;
+        STEP("pf_act", 12.0 * T * F, launch_pf_act(s->pf_gu, T, F, gemma ? 1 : 0, s->pf_xn, ldx, s->st));
+        if (gemma) {
+            if ((e = pf_gemm(s, "pf_down", L.down, T, s->pf_tmp, H, false)) != hipSuccess) return e;
+            STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_ffn, s->pf_x, s->st));
+        } else {
+            if ((e = pf_gemm(s, "pf_down", L.down, T, s->pf_x, H, true)) != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
 extern "C" int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, int32_t pos0) {
     NOT_NULL(s);
     if (n < 0) return fail(FLLM_E_ARG_RANGE, "n must be >= 0");
     if (n > 0) NOT_NULL(tokens);
-    for (int i = 0; i < n; i++) {
-        int32_t rc = fllm_forward(s, tokens[i], pos0 + i);
-        if (rc) return rc;
+    const fllm_model_desc& d = s->m->d;
+    // The batched path runs when the positions continue the cache (the case of a prompt); with
+    // debug capture, a single token, or positions that rewrite earlier slots it is n Forward calls.
+    const bool batched = n >= 2 && pos0 == s->cur_len && !s->debug && prefill_batched_ok(s);
+    if (!batched) {
+        for (int i = 0; i < n; i++) {
+            int32_t rc = fllm_forward(s, tokens[i], pos0 + i);
+            if (rc) return rc;
+        }
+        return FLLM_OK;
     }
+    // the checks of n Forward calls, before anything runs
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= d.vocab)
+            return fail(FLLM_E_ARG_RANGE, "Token id %d is outside the valid vocabulary range [0, %d].", tokens[i],
+                        d.vocab - 1);
+    if ((int64_t)s->cur_len + n > s->max_seq)
+        return fail(FLLM_E_ARG_RANGE, "KV cache full (%d positions)", s->max_seq);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    hipError_t e = prefill_alloc(s);
+    if (e != hipSuccess) return fail(FLLM_E_OOM, "prefill scratch: %s", hipGetErrorString(e));
+    int done = 0;
+    while (done < n) {
+        const int T = n - done < s->pf_cap ? n - done : s->pf_cap;
+        e = hipMemcpyAsync(s->pf_tok, tokens + done, sizeof(int32_t) * (size_t)T, hipMemcpyHostToDevice, s->st);
+        if (e == hipSuccess) e = prefill_chunk(s, T, pos0 + done);
+        if (e == hipSuccess) e = prof_collect(s);
+        // the host buffer of the token ids is reused by the next chunk
+        if (e == hipSuccess) e = hipStreamSynchronize(s->st);
+        if (e != hipSuccess) return fail(FLLM_E_DEVICE, "prefill: %s", hipGetErrorString(e));
+        done += T;
+        s->cur_len = pos0 + done;
+    }
+    // the last token's logits and greedy token, with the step parameters of its Forward call
+    const int T_last = n - ((n - 1) / s->pf_cap) * s->pf_cap;
+    e = hipMemcpyAsync(s->x, s->pf_x + (size_t)(T_last - 1) * d.hidden, sizeof(float) * (size_t)d.hidden,
+                       hipMemcpyDeviceToDevice, s->st);
+    if (e == hipSuccess) e = launch_set_params(s->params, tokens[n - 1], pos0 + n - 1, pos0 + n - 1, s->st);
+    if (e == hipSuccess) e = head_generic(s);
+    if (e == hipSuccess) e = prof_collect(s);
+    if (e != hipSuccess) return fail(FLLM_E_DEVICE, "prefill head: %s", hipGetErrorString(e));
+    s->argmax_valid = true;
     return FLLM_OK;
 }
 

@@ -80,4 +80,14 @@ __host__ __device__ inline void kscale_min(const uint8_t* p, int g, int& sc, int
     }
 }
 
+// FFN activation: 0 = SiLU, x * Sigmoid(x) (TensorOperations.cs:57-87); 1 = GELU, tanh form
+// (TensorOperations.cs:110-117)
+__device__ __forceinline__ float act_fn(float g, int act) {
+    if (act == 0) {
+        float sig = 1.0f / (1.0f + expf(-g));
+        return g * sig;
+    }
+    return 0.5f * g * (1.0f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g)));
+}
+
 }  // namespace fllm

@@ -432,15 +432,6 @@ __device__ __forceinline__ void dot_batch(const Batch<T, NR>& bt, lds_u8* wlds, 
     if ((lane & (64 / NR - 1)) == 0) part[(lane >> (6 - Log2<NR>::v)) & (NR - 1)] = tot;
 }
 
-__device__ __forceinline__ float act_fn(float g, int act) {
-    if (act == 0) {  // SiLU = x * Sigmoid(x) (TensorOperations.cs:57-87)
-        float sig = 1.0f / (1.0f + expf(-g));
-        return g * sig;
-    }
-    // GELU, tanh form (TensorOperations.cs:110-117)
-    return 0.5f * g * (1.0f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g)));
-}
-
 // =====================================================================================
 // The fused kernel.
 // LDS: part[nslice][T] row partials (T = row slots of the workgroup), red[16], 16 u64 keys for the

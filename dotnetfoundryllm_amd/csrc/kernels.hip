@@ -356,16 +356,7 @@ __global__ __launch_bounds__(256) void k_act(const float* __restrict__ g, const 
                                               int act, float* h) {
     int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    float gv = g[i];
-    float a;
-    if (act == 0) {
-        float sig = 1.0f / (1.0f + expf(-gv));
-        a = gv * sig;
-    } else {
-        float inner = 0.7978845608f * (gv + 0.044715f * gv * gv * gv);
-        a = 0.5f * gv * (1.0f + tanhf(inner));
-    }
-    h[i] = a * u[i];
+    h[i] = act_fn(g[i], act) * u[i];
 }
 
 hipError_t launch_act(const float* g, const float* u, int n, int act, float* h, hipStream_t st) {

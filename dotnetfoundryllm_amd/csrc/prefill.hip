@@ -1,0 +1,458 @@
+// prefill.hip — batched prefill kernels (gfx950).
+//
+// The reference's prefill is n consecutive Forward calls (LlamaLanguageModel.cs:133-137). Here the
+// n prompt tokens go through each layer together: every projection is one GEMM over the tokens,
+// Y[t][n] = sum_k X[t][k] W[n][k] (LinearProjection, LlamaForwardPass.cs:237-260, for all rows at
+// once), and the element-wise steps of the layer run over all rows.
+//
+// GEMM numerics. Weights are dequantized exactly (the Dequantizer arithmetic, as the device
+// dequant kernels do) while they are staged into LDS, and multiplied with the f32 activations on the
+// matrix cores in f32 (v_mfma_f32_16x16x4f32): the products of the reference's F32 path, summed in
+// f32 in the matrix core's order.
+#include "prefill.hpp"
+#include "deq.hpp"
+#include "gemv.hpp"
+
+#include <math.h>
+
+namespace fllm {
+
+typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float pf_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float pf_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+// sum over a 256-thread workgroup (called once per kernel by every thread)
+__device__ __forceinline__ float pf_block_sum(float v, float* red) {
+    v = pf_wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+// LDS written by lanes of a wave, then read by other lanes of the same wave
+__device__ __forceinline__ void pf_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- exact dequantization of 32 weights [k0, k0 + 32) of row r (k0 a multiple of 32) -----------
+template <int WT> struct PfW;
+
+// LAYOUT_TILES Q4_K (DequantizeQ4_K, Dequantizer.cs:251-294): group g of the row's block kb is the
+// 16 qs bytes of lane 16 (g & 3) + n in the region's first (g < 4) or second KiB; the row's header
+// (d, dmin, 12 scale bytes) sits at 2048 + 16 n.
+template <> struct PfW<FLLM_TYPE_Q4_K> {
+    __device__ static void deq(const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const int NB = K >> 8, kb = k0 >> 8, g = (k0 >> 5) & 7, n = r & 15;
+        const uint8_t* reg = w + ((size_t)(r >> 4) * NB + kb) * (16 * 144);
+        const uint4 qs = *(const uint4*)(reg + (g < 4 ? 0 : 1024) + 16 * (16 * (g & 3) + n));
+        const uint8_t* hdr = reg + 2048 + 16 * n;
+        const float d = half_exact(deq_ld_u16(hdr)), dmin = half_exact(deq_ld_u16(hdr + 2));
+        int sc, mn;
+        kscale_min(hdr + 4, g, sc, mn);
+        const float dg = d * (float)sc;
+        const float mg = dmin * (float)mn;
+        const uint32_t wd[4] = {qs.x, qs.y, qs.z, qs.w};
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t byte = (wd[i >> 3] >> (8 * ((i >> 1) & 3))) & 0xFFu;
+            const int q = (i & 1) ? (int)(byte >> 4) : (int)(byte & 15u);
+            v[i] = dg * (float)q - mg;
+        }
+    }
+};
+
+// LAYOUT_TILES Q6_K (DequantizeQ6_K, Dequantizer.cs:378-417): lane L = 16 (g & 3) + n holds ql of
+// group g (16 bytes, first or second KiB), qh of group g (8 bytes at 2048 + 16 L, +8 for g >= 4),
+// the group's two scales (bytes 0-1 or 2-3 of the dword at 3072 + 4 L); d at 3328 + 2 n.
+template <> struct PfW<FLLM_TYPE_Q6_K> {
+    __device__ static void deq(const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const int NB = K >> 8, kb = k0 >> 8, g = (k0 >> 5) & 7, n = r & 15, L = 16 * (g & 3) + n;
+        const uint8_t* reg = w + ((size_t)(r >> 4) * NB + kb) * (16 * 210);
+        const uint4 ql = *(const uint4*)(reg + (g < 4 ? 0 : 1024) + 16 * L);
+        const uint2 qh = *(const uint2*)(reg + 2048 + 16 * L + (g < 4 ? 0 : 8));
+        const uint32_t s4 = *(const uint32_t*)(reg + 3072 + 4 * L);
+        const uint32_t sc2 = g < 4 ? (s4 & 0xFFFFu) : (s4 >> 16);
+        const float d = half_exact(deq_ld_u16(reg + 3328 + 2 * n));
+        const uint32_t l4[4] = {ql.x, ql.y, ql.z, ql.w}, h2[2] = {qh.x, qh.y};
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t lb = (l4[i >> 3] >> (8 * ((i >> 1) & 3))) & 0xFFu;
+            const int low = (i & 1) ? (int)(lb >> 4) : (int)(lb & 15u);
+            const uint32_t hb = (h2[i >> 4] >> (8 * ((i >> 2) & 3))) & 0xFFu;
+            const int high = (int)((hb >> (2 * (i & 3))) & 3u);
+            const int q = ((high << 4) | low) - 32;
+            const int scale = (int)(int8_t)((sc2 >> (8 * (i >> 4))) & 0xFFu);
+            v[i] = d * (float)scale * (float)q;
+        }
+    }
+};
+
+// GGUF rows of any supported type: element r * K + k of the flat block stream
+template <> struct PfW<-1> {
+    __device__ static void deq(const uint8_t* __restrict__ w, int type, int K, int r, int k0, float* v) {
+        const int64_t e0 = (int64_t)r * K + k0;
+        for (int i = 0; i < 32; i++) v[i] = deq_elem(type, w, e0 + i);
+    }
+};
+
+// ---- GEMM ---------------------------------------------------------------------------------------
+// Workgroup tile: BM tokens (128 or 64) x 128 weight rows, 4 waves in a 2 x 2 arrangement, each
+// (BM / 2) x 64 (BM / 32 x 4 MFMA tiles of 16 x 16). Per K step of 64 the workgroup stages X
+// (copied) and W (dequantized, one 32-weight group per thread) into LDS as f32 rows. The K step is
+// 4 blocks of 16; within a block, MFMA slice s (K = 4) takes from lane l the k index 4 (l >> 4) + s,
+// so a lane reads its 4 slices' values as one 16-byte LDS load (the same permutation of k for A and
+// B leaves the sum unchanged). MFMA 16x16x4 f32: lane l holds A row (l & 15) and B column (l & 15);
+// D lane l holds rows 4 (l >> 4) .. + 3 of column l & 15.
+constexpr int PF_BN = 128, PF_BK = 64;
+constexpr int PF_LDF = PF_BK + 4;  // LDS row stride in floats (16 bytes of padding per row)
+
+template <int BM>
+static constexpr size_t pf_gemm_lds() {
+    return sizeof(float) * (size_t)(BM + PF_BN) * PF_LDF;
+}
+
+template <int WT, int BM>
+__global__ __launch_bounds__(256) void k_pf_gemm(const PfGemm a) {
+    constexpr int WM = BM / 2;   // tokens per wave
+    constexpr int TI = WM / 16;  // MFMA tiles along the tokens
+    extern __shared__ __attribute__((aligned(16))) float pf_lds[];
+    float* sx = pf_lds;            // [BM][PF_LDF]
+    float* sw = sx + BM * PF_LDF;  // [PF_BN][PF_LDF]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * PF_BN, t0 = blockIdx.y * BM;
+    const int wm = wave >> 1, wn = wave & 1;
+    pf_f32x4 acc[TI][4];
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int k0 = 0; k0 < a.K; k0 += PF_BK) {
+        __syncthreads();  // the previous step's operands have been read
+        // X: BM rows x 16 pieces of 4 floats
+        for (int c = tid; c < BM * 16; c += 256) {
+            const int row = c >> 4, col = (c & 15) * 4, t = t0 + row, k = k0 + col;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (t < a.T && k < a.K) v = *(const float4*)(a.x + (size_t)t * a.ldx + k);
+            *(float4*)(sx + row * PF_LDF + col) = v;
+        }
+        // W: thread = (row, group of 32)
+        {
+            const int row = tid >> 1, grp = tid & 1, r = n0 + row, k = k0 + 32 * grp;
+            float v[32];
+            if (r < a.N && k < a.K) {
+                PfW<WT>::deq(a.w, a.type, a.K, r, k, v);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; i++) v[i] = 0.0f;
+            }
+            float4* dst = (float4*)(sw + row * PF_LDF + 32 * grp);
+#pragma unroll
+            for (int i = 0; i < 8; i++) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < PF_BK; kk += 16) {
+            const int ko = kk + 4 * (lane >> 4);
+            float4 av[TI], bv[4];
+#pragma unroll
+            for (int i = 0; i < TI; i++) av[i] = *(const float4*)(sx + (WM * wm + 16 * i + (lane & 15)) * PF_LDF + ko);
+#pragma unroll
+            for (int j = 0; j < 4; j++) bv[j] = *(const float4*)(sw + (64 * wn + 16 * j + (lane & 15)) * PF_LDF + ko);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float as = s == 0 ? av[i].x : s == 1 ? av[i].y : s == 2 ? av[i].z : av[i].w;
+                        const float bs = s == 0 ? bv[j].x : s == 1 ? bv[j].y : s == 2 ? bv[j].z : bv[j].w;
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, bs, acc[i][j], 0, 0, 0);
+                    }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int t = t0 + WM * wm + 16 * i + 4 * (lane >> 4) + e;
+                const int n = n0 + 64 * wn + 16 * j + (lane & 15);
+                if (t < a.T && n < a.N) {
+                    float* p = a.y + (size_t)t * a.ldy + n;
+                    *p = a.add ? *p + acc[i][j][e] : acc[i][j][e];
+                }
+            }
+}
+
+typedef void (*PfGemmKernel)(const PfGemm);
+static hipError_t pf_lds_attr(const void* k, size_t bytes) {
+    return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+template <int BM>
+static PfGemmKernel pf_gemm_kernel(const PfGemm& a) {
+    if (a.layout != LAYOUT_TILES) return k_pf_gemm<-1, BM>;
+    if (a.type == FLLM_TYPE_Q4_K) return k_pf_gemm<FLLM_TYPE_Q4_K, BM>;
+    if (a.type == FLLM_TYPE_Q6_K) return k_pf_gemm<FLLM_TYPE_Q6_K, BM>;
+    return nullptr;
+}
+
+hipError_t launch_pf_gemm(const PfGemm& a, int n_cu, hipStream_t st) {
+    if (a.T <= 0 || a.N <= 0) return hipSuccess;
+    if (a.K <= 0 || a.K % 32 != 0 || a.ldx < a.K || a.ldx % 4 != 0 || a.ldy < a.N) return hipErrorInvalidValue;
+    if (a.layout == LAYOUT_TILES && (a.K % 256 != 0 || a.N % 16 != 0)) return hipErrorInvalidValue;
+    // 128-token tiles unless that leaves fewer than two workgroups per CU
+    const int64_t col_tiles = (a.N + PF_BN - 1) / PF_BN;
+    const bool tall = col_tiles * ((a.T + 127) / 128) >= 2 * (int64_t)(n_cu > 0 ? n_cu : 256);
+    const PfGemmKernel k = tall ? pf_gemm_kernel<128>(a) : pf_gemm_kernel<64>(a);
+    if (!k) return hipErrorInvalidValue;
+    const size_t lds = tall ? pf_gemm_lds<128>() : pf_gemm_lds<64>();
+    hipError_t e = pf_lds_attr((const void*)k, lds);
+    if (e != hipSuccess) return e;
+    const int bm = tall ? 128 : 64;
+    dim3 grid((unsigned)col_tiles, (unsigned)((a.T + bm - 1) / bm));
+    k<<<grid, 256, lds, st>>>(a);
+    return hipGetLastError();
+}
+
+// ---- element-wise steps over the rows ----------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pf_embed(const int* __restrict__ tok, const uint8_t* __restrict__ emb, int type,
+                                                  int H, float* __restrict__ x) {
+    const int t = blockIdx.x;
+    const int64_t base = (int64_t)tok[t] * H;
+    for (int i = threadIdx.x; i < H; i += 256) x[(size_t)t * H + i] = deq_elem(type, emb, base + i);
+}
+
+hipError_t launch_pf_embed(const int* tokens, int T, const uint8_t* emb, int type, int H, float* x, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    k_pf_embed<<<T, 256, 0, st>>>(tokens, emb, type, H, x);
+    return hipGetLastError();
+}
+
+// RmsNorm (TensorOperations.cs:42-54) / GemmaRmsNorm (:90-107) of row blockIdx.x
+__global__ __launch_bounds__(256) void k_pf_norm(const float* __restrict__ x, int n, const float* __restrict__ w, float eps,
+                                                 int kind, float* __restrict__ xn, int ldx) {
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    const float* xr = x + (size_t)t * n;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    const float tot = pf_block_sum(ss, red);
+    const float rms = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float tv = xr[i] * rms;
+        xn[(size_t)t * ldx + i] = kind ? tv * (w[i] + 1.0f) : tv * w[i];
+    }
+}
+
+hipError_t launch_pf_norm(const float* x, int T, int n, const float* w, float eps, int kind, float* xn, int ldx,
+                          hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    k_pf_norm<<<T, 256, 0, st>>>(x, n, w, eps, kind, xn, ldx);
+    return hipGetLastError();
+}
+
+// ComputeSiluFfn / ComputeGeluFfn gating (LlamaForwardPass.cs:217-232; Gemma2ForwardPass.cs:187-199)
+__global__ __launch_bounds__(256) void k_pf_act(const float* __restrict__ gu, int ffn, int act, float* __restrict__ h,
+                                                int ldx) {
+    const int t = blockIdx.y;
+    const float* row = gu + (size_t)t * 2 * ffn;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < ffn; i += gridDim.x * 256)
+        h[(size_t)t * ldx + i] = act_fn(row[i], act) * row[ffn + i];
+}
+
+hipError_t launch_pf_act(const float* gu, int T, int ffn, int act, float* h, int ldx, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    dim3 grid((unsigned)((ffn + 255) / 256 < 64 ? (ffn + 255) / 256 : 64), (unsigned)T);
+    k_pf_act<<<grid, 256, 0, st>>>(gu, ffn, act, h, ldx);
+    return hipGetLastError();
+}
+
+// Qwen2 bias (Qwen2ForwardPass.cs:83-85), RoPE on interleaved pairs (TensorOperations.cs:250-260)
+// at position pos0 + t, KvCache.Append into slot pos0 + t (KvCache.cs:86-89)
+__global__ __launch_bounds__(256) void k_pf_qkv_post(float* __restrict__ qkv, int ldq, int pos0,
+                                                     const float* __restrict__ bq, const float* __restrict__ bk,
+                                                     const float* __restrict__ bv, const float2* __restrict__ rope,
+                                                     int nh, int nkv, int hd, float* __restrict__ kc,
+                                                     float* __restrict__ vc) {
+    const int t = blockIdx.x, pos = pos0 + t, half = hd >> 1, qdim = nh * hd, kvdim = nkv * hd;
+    float* row = qkv + (size_t)t * ldq;
+    const float2* rp = rope + (size_t)pos * half;
+    const int npairs = (nh + nkv) * half;
+    for (int idx = threadIdx.x; idx < npairs; idx += 256) {
+        const bool isq = idx < nh * half;
+        const int li = isq ? idx : idx - nh * half;
+        const int head = li / half, i = li % half, o = head * hd + 2 * i;
+        const float* src = row + (isq ? 0 : qdim);
+        float x0 = src[o], x1 = src[o + 1];
+        const float* b = isq ? bq : bk;
+        if (b) { x0 = x0 + b[o]; x1 = x1 + b[o + 1]; }
+        const float2 cs = rp[i];
+        const float y0 = x0 * cs.x - x1 * cs.y;
+        const float y1 = x0 * cs.y + x1 * cs.x;
+        if (isq) {
+            row[o] = y0;
+            row[o + 1] = y1;
+        } else {
+            kc[(size_t)pos * kvdim + o] = y0;
+            kc[(size_t)pos * kvdim + o + 1] = y1;
+        }
+    }
+    for (int i = threadIdx.x; i < kvdim; i += 256) {
+        float v = row[qdim + kvdim + i];
+        if (bv) v = v + bv[i];
+        vc[(size_t)pos * kvdim + i] = v;
+    }
+}
+
+hipError_t launch_pf_qkv_post(float* qkv, int ldq, int T, int pos0, const float* bq, const float* bk, const float* bv,
+                              const float2* rope, int nh, int nkv, int hd, float* kc, float* vc, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    k_pf_qkv_post<<<T, 256, 0, st>>>(qkv, ldq, pos0, bq, bk, bv, rope, nh, nkv, hd, kc, vc);
+    return hipGetLastError();
+}
+
+// Gemma2 post-norm: x += GemmaRmsNorm(tmp, w), eps 1e-6 (Gemma2ForwardPass.cs:90-96)
+__global__ __launch_bounds__(256) void k_pf_postnorm_add(const float* __restrict__ tmp, int n, const float* __restrict__ w,
+                                                         float* __restrict__ x) {
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    const float* tr = tmp + (size_t)t * n;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(tr[i], tr[i], ss);
+    const float tot = pf_block_sum(ss, red);
+    const float rms = 1.0f / sqrtf(tot / (float)n + 1e-6f);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float o = (tr[i] * rms) * (w[i] + 1.0f);
+        x[(size_t)t * n + i] = x[(size_t)t * n + i] + o;
+    }
+}
+
+hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w, float* x, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    k_pf_postnorm_add<<<T, 256, 0, st>>>(tmp, n, w, x);
+    return hipGetLastError();
+}
+
+// ---- causal attention over the cache (ComputeAttention, LlamaForwardPass.cs:158-211 and the
+// Mistral / Qwen2 / Gemma2 variants) ----------------------------------------------------------------
+// Workgroup = (query head, block of 8 consecutive queries), one wave per query. Keys go in blocks
+// of 64 rows of the head's kv head, staged in LDS (K rows padded to HD + 1 floats so that lane j
+// reading row j is conflict-free). Per block a wave scores its 64 keys (lane = key), updates the
+// running max / sum (online softmax) and adds p_j v_j to its output slice (lane = dims d, d + 64, ..).
+constexpr int PF_AQ = 8, PF_AK = 64;
+
+template <int HD>
+static constexpr size_t pf_attn_lds() {
+    return sizeof(float) * ((size_t)PF_AK * (HD + 1) + (size_t)PF_AK * HD + PF_AQ * PF_AK + PF_AQ * HD);
+}
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_pf_attn(const PfAttn a) {
+    constexpr int DPL = HD / 64;  // output dims per lane
+    extern __shared__ float pa_lds[];
+    float* sk = pa_lds;                  // [PF_AK][HD + 1]
+    float* sv = sk + PF_AK * (HD + 1);   // [PF_AK][HD]
+    float* sp = sv + PF_AK * HD;         // [PF_AQ][PF_AK]
+    float* sq = sp + PF_AQ * PF_AK;      // [PF_AQ][HD]
+    const int h = blockIdx.x, qb = blockIdx.y * PF_AQ;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int kvh = h / (a.nh / a.nkv);
+    const int t = qb + wave;
+    const bool live = t < a.T;
+    const int pos = a.pos0 + (live ? t : a.T - 1);
+    const int ws = pos + 1 - a.window > 0 ? pos + 1 - a.window : 0;
+    for (int d = lane; d < HD; d += 64) sq[wave * HD + d] = live ? a.q[(size_t)t * a.ldq + h * HD + d] : 0.0f;
+    // keys of the workgroup: from the first query's window start to the last live query
+    const int tl = (qb + PF_AQ < a.T ? qb + PF_AQ : a.T) - 1;
+    const int kend = a.pos0 + tl;
+    const int kstart = a.pos0 + qb + 1 - a.window > 0 ? a.pos0 + qb + 1 - a.window : 0;
+    const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    float acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.0f;
+    for (int kb = kstart; kb <= kend; kb += PF_AK) {
+        __syncthreads();  // the previous block's rows have been read (and sq is written)
+        for (int c = threadIdx.x; c < PF_AK * (HD / 4); c += 512) {
+            const int j = c / (HD / 4), d4 = (c % (HD / 4)) * 4;
+            const int key = kb + j < kend ? kb + j : kend;
+            const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
+            const float4 kv = *(const float4*)(a.kc + off);
+            float* kr = sk + j * (HD + 1) + d4;
+            kr[0] = kv.x; kr[1] = kv.y; kr[2] = kv.z; kr[3] = kv.w;
+            *(float4*)(sv + j * HD + d4) = *(const float4*)(a.vc + off);
+        }
+        __syncthreads();
+        if (live && kb <= pos && kb + PF_AK - 1 >= ws) {  // the block meets [ws, pos]
+            const int key = kb + lane;
+            const bool valid = key >= ws && key <= pos;
+            float s = -INFINITY;
+            if (valid) {
+                float dot = 0.0f;
+                const float* qr = sq + wave * HD;
+                const float* kr = sk + lane * (HD + 1);
+#pragma unroll 8
+                for (int d = 0; d < HD; d++) dot = fmaf(qr[d], kr[d], dot);
+                s = dot * a.scale;
+                if (a.softcap > 0.0f) s = tanhf(s * inv_cap) * a.softcap;
+            }
+            const float m_new = fmaxf(m, pf_wave_max(s));
+            const float corr = expf(m - m_new);
+            const float p = valid ? expf(s - m_new) : 0.0f;
+            l = l * corr + pf_wave_sum(p);
+            sp[wave * PF_AK + lane] = p;
+            pf_wave_sync();
+#pragma unroll
+            for (int e = 0; e < DPL; e++) acc[e] *= corr;
+            for (int j = 0; j < PF_AK; j++) {
+                const float pj = sp[wave * PF_AK + j];
+#pragma unroll
+                for (int e = 0; e < DPL; e++) acc[e] = fmaf(pj, sv[j * HD + lane + 64 * e], acc[e]);
+            }
+            pf_wave_sync();  // sp is rewritten for the next block
+            m = m_new;
+        }
+    }
+    if (live) {
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) a.out[(size_t)t * a.nh * HD + h * HD + lane + 64 * e] = acc[e] * inv;
+    }
+}
+
+hipError_t launch_pf_attn(const PfAttn& a, hipStream_t st) {
+    if (a.T <= 0) return hipSuccess;
+    if (a.nkv <= 0 || a.nh % a.nkv != 0 || a.kvdim != a.nkv * a.hd) return hipErrorInvalidValue;
+    dim3 grid((unsigned)a.nh, (unsigned)((a.T + PF_AQ - 1) / PF_AQ));
+    hipError_t e;
+    switch (a.hd) {
+        case 64:
+            if ((e = pf_lds_attr((const void*)k_pf_attn<64>, pf_attn_lds<64>())) != hipSuccess) return e;
+            k_pf_attn<64><<<grid, 512, pf_attn_lds<64>(), st>>>(a);
+            break;
+        case 128:
+            if ((e = pf_lds_attr((const void*)k_pf_attn<128>, pf_attn_lds<128>())) != hipSuccess) return e;
+            k_pf_attn<128><<<grid, 512, pf_attn_lds<128>(), st>>>(a);
+            break;
+        case 256:
+            if ((e = pf_lds_attr((const void*)k_pf_attn<256>, pf_attn_lds<256>())) != hipSuccess) return e;
+            k_pf_attn<256><<<grid, 512, pf_attn_lds<256>(), st>>>(a);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fllm

@@ -1,0 +1,54 @@
+// prefill.hpp — launch interface of the batched prefill kernels (prefill.hip): the prompt's
+// tokens pass through each layer together, the projections as f32 matrix-core GEMMs.
+#pragma once
+
+#include "kernels.hpp"
+
+namespace fllm {
+
+// Y[t][n] (+)= sum_k X[t][k] W[n][k] for t < T, n < N, in f32 on the matrix cores. X: f32 rows of
+// stride ldx; W in its stored layout (LAYOUT_TILES Q4_K / Q6_K, or GGUF rows of any supported
+// type), dequantized exactly in the kernel. K is a multiple of 32.
+struct PfGemm {
+    const float* x;
+    int ldx;
+    const uint8_t* w;
+    int type, layout;
+    int N, K;
+    float* y;
+    int ldy;
+    int T;
+    int add;  // 1: y += X W^T (residual add), 0: y = X W^T
+};
+hipError_t launch_pf_gemm(const PfGemm& a, int n_cu, hipStream_t st);
+
+// X[t] = embedding row tokens[t] (exact dequantization of any supported type)
+hipError_t launch_pf_embed(const int* tokens, int T, const uint8_t* emb, int type, int H, float* x, hipStream_t st);
+// RmsNorm / GemmaRmsNorm (kind 1) of every row of X [T][n] into xn (row stride ldx)
+hipError_t launch_pf_norm(const float* x, int T, int n, const float* w, float eps, int kind, float* xn, int ldx,
+                          hipStream_t st);
+// h = act(gate) * up per row of gu [T][2 ffn] (gate columns, then up columns), row stride ldx
+hipError_t launch_pf_act(const float* gu, int T, int ffn, int act, float* h, int ldx, hipStream_t st);
+// rows of qkv [T][ldq] = (q | k | v): bias, RoPE at position pos0 + t on q and k, q written back,
+// k and v stored in cache slot pos0 + t of this layer's K / V cache
+hipError_t launch_pf_qkv_post(float* qkv, int ldq, int T, int pos0, const float* bq, const float* bk, const float* bv,
+                              const float2* rope, int nh, int nkv, int hd, float* kc, float* vc, hipStream_t st);
+// x[t] += GemmaRmsNorm(tmp[t], w) for every row
+hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w, float* x, hipStream_t st);
+
+// Causal attention of T query rows (positions pos0 + t) over this layer's cache, which already
+// holds the T new rows: out[t][h*hd + d].
+struct PfAttn {
+    const float* q;  // [T][ldq], head h at h * hd
+    int ldq;
+    const float* kc;
+    const float* vc;
+    float* out;      // [T][nh * hd]
+    int T, pos0;
+    int nh, nkv, hd, kvdim;
+    int window;      // attend to the last `window` positions (INT32_MAX = all)
+    float scale, softcap;
+};
+hipError_t launch_pf_attn(const PfAttn& a, hipStream_t st);
+
+}  // namespace fllm
