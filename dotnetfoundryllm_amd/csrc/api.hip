@@ -1202,16 +1202,29 @@ static hipError_t prefill_alloc(fllm_seq* s) {
     return e;
 }
 
-// y (+)= X W^T over the chunk's rows; X = pf_xn (row stride pf_ldx) or the given rows
-static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor& w, int T, float* y, int ldy, bool add,
-                          const float* x = nullptr, int ldx = 0) {
+// y_i (+)= X W_i^T over the chunk's rows for the matrices w[0..n) (one launch when their layouts
+// agree); X = pf_xn (row stride pf_ldx) or the given rows
+static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w, float* const* y, int n, int ldy, int T,
+                          bool add, const float* x = nullptr, int ldx = 0) {
     PfGemm g{};
     g.x = x ? x : s->pf_xn;
     g.ldx = x ? ldx : s->pf_ldx;
-    g.w = w.ptr; g.type = w.type; g.layout = w.layout;
-    g.N = (int)w.rows; g.K = (int)w.cols;
-    g.y = y; g.ldy = ldy; g.T = T; g.add = add ? 1 : 0;
-    STEP(name, (double)w.bytes + 8.0 * T * (double)(w.rows + w.cols), launch_pf_gemm(g, s->m->ctx->n_cu, s->st));
+    g.K = (int)w[0]->cols;
+    g.T = T;
+    g.add = add ? 1 : 0;
+    double bytes = 0.0;
+    for (int i = 0; i < n; i++) {
+        if (g.nseg > 0 && (w[i]->layout == LAYOUT_TILES) != (g.seg[0].layout == LAYOUT_TILES)) {
+            STEP(name, bytes, launch_pf_gemm(g, s->m->ctx->n_cu, s->st));
+            g.nseg = 0;
+            bytes = 0.0;
+        }
+        PfSeg& sg = g.seg[g.nseg++];
+        sg.w = w[i]->ptr; sg.type = w[i]->type; sg.layout = w[i]->layout; sg.N = (int)w[i]->rows;
+        sg.y = y[i]; sg.ldy = ldy;
+        bytes += (double)w[i]->bytes + 8.0 * T * (double)(w[i]->rows + w[i]->cols);
+    }
+    STEP(name, bytes, launch_pf_gemm(g, s->m->ctx->n_cu, s->st));
     return hipSuccess;
 }
 
@@ -1233,9 +1246,11 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         float* kc = s->kc + (size_t)l * layer_kv;
         float* vc = s->vc + (size_t)l * layer_kv;
         STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.attn_norm, eps, nk, s->pf_xn, ldx, s->st));
-        if ((e = pf_gemm(s, "pf_q", L.q, T, s->pf_qkv, ldq, false)) != hipSuccess) return e;
-        if ((e = pf_gemm(s, "pf_k", L.k, T, s->pf_qkv + qdim, ldq, false)) != hipSuccess) return e;
-        if ((e = pf_gemm(s, "pf_v", L.v, T, s->pf_qkv + qdim + kvdim, ldq, false)) != hipSuccess) return e;
+        {
+            const Tensor* w[3] = {&L.q, &L.k, &L.v};
+            float* y[3] = {s->pf_qkv, s->pf_qkv + qdim, s->pf_qkv + qdim + kvdim};
+            if ((e = pf_gemm(s, "pf_qkv", w, y, 3, ldq, T, false)) != hipSuccess) return e;
+        }
         STEP("pf_qkv_post", 8.0 * T * ldq,
              launch_pf_qkv_post(s->pf_qkv, ldq, T, pos0, L.bq, L.bk, L.bv, s->rope, d.n_heads, d.n_kv_heads, d.head_dim,
                                 kc, vc, s->st));
@@ -1244,21 +1259,24 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         at.T = T; at.pos0 = pos0; at.nh = d.n_heads; at.nkv = d.n_kv_heads; at.hd = d.head_dim; at.kvdim = kvdim;
         at.window = layer_window(d, l); at.scale = d.attn_scale; at.softcap = gemma ? d.attn_softcap : 0.0f;
         STEP("pf_attention", 8.0 * (double)kvdim * (pos0 + T) + 8.0 * T * qdim, launch_pf_attn(at, s->st));
-        if (gemma) {
-            if ((e = pf_gemm(s, "pf_o", L.o, T, s->pf_tmp, H, false, s->pf_att, qdim)) != hipSuccess) return e;
-            STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_attn, s->pf_x, s->st));
-        } else {
-            if ((e = pf_gemm(s, "pf_o", L.o, T, s->pf_x, H, true, s->pf_att, qdim)) != hipSuccess) return e;
+        {
+            const Tensor* w[1] = {&L.o};
+            float* y[1] = {gemma ? s->pf_tmp : s->pf_x};
+            if ((e = pf_gemm(s, "pf_o", w, y, 1, H, T, !gemma, s->pf_att, qdim)) != hipSuccess) return e;
+            if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_attn, s->pf_x, s->st));
         }
         STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.ffn_norm, eps, nk, s->pf_xn, ldx, s->st));
-        if ((e = pf_gemm(s, "pf_gate", L.gate, T, s->pf_gu, 2 * F, false)) != hipSuccess) return e;
-        if ((e = pf_gemm(s, "pf_up", L.up, T, s->pf_gu + F, 2 * F, false)) != hipSuccess) return e;
+        {
+            const Tensor* w[2] = {&L.gate, &L.up};
+            float* y[2] = {s->pf_gu, s->pf_gu + F};
+            if ((e = pf_gemm(s, "pf_gate_up", w, y, 2, 2 * F, T, false)) != hipSuccess) return e;
+        }
         STEP("pf_act", 12.0 * T * F, launch_pf_act(s->pf_gu, T, F, gemma ? 1 : 0, s->pf_xn, ldx, s->st));
-        if (gemma) {
-            if ((e = pf_gemm(s, "pf_down", L.down, T, s->pf_tmp, H, false)) != hipSuccess) return e;
-            STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_ffn, s->pf_x, s->st));
-        } else {
-            if ((e = pf_gemm(s, "pf_down", L.down, T, s->pf_x, H, true)) != hipSuccess) return e;
+        {
+            const Tensor* w[1] = {&L.down};
+            float* y[1] = {gemma ? s->pf_tmp : s->pf_x};
+            if ((e = pf_gemm(s, "pf_down", w, y, 1, H, T, !gemma)) != hipSuccess) return e;
+            if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_ffn, s->pf_x, s->st));
         }
     }
     return hipSuccess;

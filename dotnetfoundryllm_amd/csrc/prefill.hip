@@ -44,23 +44,41 @@ __device__ __forceinline__ void pf_wave_sync() {
 }
 
 // ---- exact dequantization of 32 weights [k0, k0 + 32) of row r (k0 a multiple of 32) -----------
+// load() fetches the raw bytes of the group (issued a K step ahead), deq() decodes them.
 template <int WT> struct PfW;
 
 // LAYOUT_TILES Q4_K (DequantizeQ4_K, Dequantizer.cs:251-294): group g of the row's block kb is the
 // 16 qs bytes of lane 16 (g & 3) + n in the region's first (g < 4) or second KiB; the row's header
 // (d, dmin, 12 scale bytes) sits at 2048 + 16 n.
 template <> struct PfW<FLLM_TYPE_Q4_K> {
-    __device__ static void deq(const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    struct Raw { uint4 qs, hdr; };
+    __device__ static void load(Raw& w4, const uint8_t* __restrict__ w, int K, int r, int k0) {
         const int NB = K >> 8, kb = k0 >> 8, g = (k0 >> 5) & 7, n = r & 15;
         const uint8_t* reg = w + ((size_t)(r >> 4) * NB + kb) * (16 * 144);
-        const uint4 qs = *(const uint4*)(reg + (g < 4 ? 0 : 1024) + 16 * (16 * (g & 3) + n));
-        const uint8_t* hdr = reg + 2048 + 16 * n;
-        const float d = half_exact(deq_ld_u16(hdr)), dmin = half_exact(deq_ld_u16(hdr + 2));
+        w4.qs = *(const uint4*)(reg + (g < 4 ? 0 : 1024) + 16 * (16 * (g & 3) + n));
+        w4.hdr = *(const uint4*)(reg + 2048 + 16 * n);
+    }
+    // byte idx of the 16-byte header
+    __device__ static uint32_t hbyte(const uint4& h, int idx) {
+        const uint32_t w = idx < 8 ? (idx < 4 ? h.x : h.y) : (idx < 12 ? h.z : h.w);
+        return (w >> (8 * (idx & 3))) & 0xFFu;
+    }
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+        const int g = (k0 >> 5) & 7;
+        const float d = half_exact(w4.hdr.x & 0xFFFFu), dmin = half_exact(w4.hdr.x >> 16);
+        // DecodeKScaleMin (Dequantizer.cs:506-521) on scale bytes 4..15 of the header
         int sc, mn;
-        kscale_min(hdr + 4, g, sc, mn);
+        if (g < 4) {
+            sc = (int)(hbyte(w4.hdr, 4 + g) & 63u);
+            mn = (int)(hbyte(w4.hdr, 8 + g) & 63u);
+        } else {
+            const uint32_t b = hbyte(w4.hdr, 8 + g), lo = hbyte(w4.hdr, g), hi = hbyte(w4.hdr, 4 + g);
+            sc = (int)((b & 15u) | ((lo >> 6) << 4));
+            mn = (int)((b >> 4) | ((hi >> 6) << 4));
+        }
         const float dg = d * (float)sc;
         const float mg = dmin * (float)mn;
-        const uint32_t wd[4] = {qs.x, qs.y, qs.z, qs.w};
+        const uint32_t wd[4] = {w4.qs.x, w4.qs.y, w4.qs.z, w4.qs.w};
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const uint32_t byte = (wd[i >> 3] >> (8 * ((i >> 1) & 3))) & 0xFFu;
@@ -74,15 +92,20 @@ template <> struct PfW<FLLM_TYPE_Q4_K> {
 // group g (16 bytes, first or second KiB), qh of group g (8 bytes at 2048 + 16 L, +8 for g >= 4),
 // the group's two scales (bytes 0-1 or 2-3 of the dword at 3072 + 4 L); d at 3328 + 2 n.
 template <> struct PfW<FLLM_TYPE_Q6_K> {
-    __device__ static void deq(const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    struct Raw { uint4 ql; uint2 qh; uint32_t s4, d; };
+    __device__ static void load(Raw& w4, const uint8_t* __restrict__ w, int K, int r, int k0) {
         const int NB = K >> 8, kb = k0 >> 8, g = (k0 >> 5) & 7, n = r & 15, L = 16 * (g & 3) + n;
         const uint8_t* reg = w + ((size_t)(r >> 4) * NB + kb) * (16 * 210);
-        const uint4 ql = *(const uint4*)(reg + (g < 4 ? 0 : 1024) + 16 * L);
-        const uint2 qh = *(const uint2*)(reg + 2048 + 16 * L + (g < 4 ? 0 : 8));
-        const uint32_t s4 = *(const uint32_t*)(reg + 3072 + 4 * L);
-        const uint32_t sc2 = g < 4 ? (s4 & 0xFFFFu) : (s4 >> 16);
-        const float d = half_exact(deq_ld_u16(reg + 3328 + 2 * n));
-        const uint32_t l4[4] = {ql.x, ql.y, ql.z, ql.w}, h2[2] = {qh.x, qh.y};
+        w4.ql = *(const uint4*)(reg + (g < 4 ? 0 : 1024) + 16 * L);
+        w4.qh = *(const uint2*)(reg + 2048 + 16 * L + (g < 4 ? 0 : 8));
+        w4.s4 = *(const uint32_t*)(reg + 3072 + 4 * L);
+        w4.d = *(const uint16_t*)(reg + 3328 + 2 * n);
+    }
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+        const int g = (k0 >> 5) & 7;
+        const uint32_t sc2 = g < 4 ? (w4.s4 & 0xFFFFu) : (w4.s4 >> 16);
+        const float d = half_exact(w4.d);
+        const uint32_t l4[4] = {w4.ql.x, w4.ql.y, w4.ql.z, w4.ql.w}, h2[2] = {w4.qh.x, w4.qh.y};
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const uint32_t lb = (l4[i >> 3] >> (8 * ((i >> 1) & 3))) & 0xFFu;
@@ -96,9 +119,11 @@ template <> struct PfW<FLLM_TYPE_Q6_K> {
     }
 };
 
-// GGUF rows of any supported type: element r * K + k of the flat block stream
+// GGUF rows of any supported type: element r * K + k of the flat block stream, read when decoded
 template <> struct PfW<-1> {
-    __device__ static void deq(const uint8_t* __restrict__ w, int type, int K, int r, int k0, float* v) {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int type, int K, int r, int k0, float* v) {
         const int64_t e0 = (int64_t)r * K + k0;
         for (int i = 0; i < 32; i++) v[i] = deq_elem(type, w, e0 + i);
     }
@@ -120,15 +145,12 @@ static constexpr size_t pf_gemm_lds() {
     return sizeof(float) * (size_t)(BM + PF_BN) * PF_LDF;
 }
 
+// one 128-row column tile (rows n0.., tokens t0..) of segment sg
 template <int WT, int BM>
-__global__ __launch_bounds__(256) void k_pf_gemm(const PfGemm a) {
+__device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, int n0, int t0, float* sx, float* sw) {
     constexpr int WM = BM / 2;   // tokens per wave
     constexpr int TI = WM / 16;  // MFMA tiles along the tokens
-    extern __shared__ __attribute__((aligned(16))) float pf_lds[];
-    float* sx = pf_lds;            // [BM][PF_LDF]
-    float* sw = sx + BM * PF_LDF;  // [PF_BN][PF_LDF]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * PF_BN, t0 = blockIdx.y * BM;
     const int wm = wave >> 1, wn = wave & 1;
     pf_f32x4 acc[TI][4];
 #pragma unroll
@@ -136,29 +158,44 @@ __global__ __launch_bounds__(256) void k_pf_gemm(const PfGemm a) {
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // this thread's share of a K step: X pieces c = tid + 256 i, and W group (row tid / 2, tid % 2)
+    constexpr int XP = BM * 16 / 256;
+    const int wrow = tid >> 1, wgrp = tid & 1, wr = n0 + wrow;
+    const bool wlive = wr < sg.N;
+    using Raw = typename PfW<WT>::Raw;
+    float4 xr[XP];
+    Raw wraw;
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 4, t = t0 + row, k = k0 + col;
+            xr[i] = (t < a.T && k < a.K) ? *(const float4*)(a.x + (size_t)t * a.ldx + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        if (wlive && k0 + 32 * wgrp < a.K) PfW<WT>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
+    };
+    fetch(0);
     for (int k0 = 0; k0 < a.K; k0 += PF_BK) {
         __syncthreads();  // the previous step's operands have been read
-        // X: BM rows x 16 pieces of 4 floats
-        for (int c = tid; c < BM * 16; c += 256) {
-            const int row = c >> 4, col = (c & 15) * 4, t = t0 + row, k = k0 + col;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (t < a.T && k < a.K) v = *(const float4*)(a.x + (size_t)t * a.ldx + k);
-            *(float4*)(sx + row * PF_LDF + col) = v;
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int c = tid + 256 * i;
+            *(float4*)(sx + (c >> 4) * PF_LDF + (c & 15) * 4) = xr[i];
         }
-        // W: thread = (row, group of 32)
         {
-            const int row = tid >> 1, grp = tid & 1, r = n0 + row, k = k0 + 32 * grp;
             float v[32];
-            if (r < a.N && k < a.K) {
-                PfW<WT>::deq(a.w, a.type, a.K, r, k, v);
+            const int k = k0 + 32 * wgrp;
+            if (wlive && k < a.K) {
+                PfW<WT>::deq(wraw, sg.w, sg.type, a.K, wr, k, v);
             } else {
 #pragma unroll
                 for (int i = 0; i < 32; i++) v[i] = 0.0f;
             }
-            float4* dst = (float4*)(sw + row * PF_LDF + 32 * grp);
+            float4* dst = (float4*)(sw + wrow * PF_LDF + 32 * wgrp);
 #pragma unroll
             for (int i = 0; i < 8; i++) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
         }
+        // the next step's global loads fly while this step multiplies
+        if (k0 + PF_BK < a.K) fetch(k0 + PF_BK);
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < PF_BK; kk += 16) {
@@ -188,11 +225,43 @@ __global__ __launch_bounds__(256) void k_pf_gemm(const PfGemm a) {
             for (int e = 0; e < 4; e++) {
                 const int t = t0 + WM * wm + 16 * i + 4 * (lane >> 4) + e;
                 const int n = n0 + 64 * wn + 16 * j + (lane & 15);
-                if (t < a.T && n < a.N) {
-                    float* p = a.y + (size_t)t * a.ldy + n;
+                if (t < a.T && n < sg.N) {
+                    float* p = sg.y + (size_t)t * sg.ldy + n;
                     *p = a.add ? *p + acc[i][j][e] : acc[i][j][e];
                 }
             }
+}
+
+// workgroup (x, y): column tile x of the launch's segments, token tile y
+__device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
+    int si = 0;
+    while (si + 1 < a.nseg && bx >= a.seg[si].tiles) {
+        bx -= a.seg[si].tiles;
+        si++;
+    }
+    return si;
+}
+
+// tile-interleaved Q4_K / Q6_K segments
+template <int BM>
+__global__ __launch_bounds__(256) void k_pf_gemm_tiles(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) float pf_lds[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    const PfSeg& sg = a.seg[si];
+    if (sg.type == FLLM_TYPE_Q6_K)
+        pf_gemm_tile<FLLM_TYPE_Q6_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
+    else
+        pf_gemm_tile<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
+}
+
+// GGUF-row segments of any type
+template <int BM>
+__global__ __launch_bounds__(256) void k_pf_gemm_rows(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) float pf_lds[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    pf_gemm_tile<-1, BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
 }
 
 typedef void (*PfGemmKernel)(const PfGemm);
@@ -200,23 +269,24 @@ static hipError_t pf_lds_attr(const void* k, size_t bytes) {
     return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
-template <int BM>
-static PfGemmKernel pf_gemm_kernel(const PfGemm& a) {
-    if (a.layout != LAYOUT_TILES) return k_pf_gemm<-1, BM>;
-    if (a.type == FLLM_TYPE_Q4_K) return k_pf_gemm<FLLM_TYPE_Q4_K, BM>;
-    if (a.type == FLLM_TYPE_Q6_K) return k_pf_gemm<FLLM_TYPE_Q6_K, BM>;
-    return nullptr;
-}
-
-hipError_t launch_pf_gemm(const PfGemm& a, int n_cu, hipStream_t st) {
-    if (a.T <= 0 || a.N <= 0) return hipSuccess;
-    if (a.K <= 0 || a.K % 32 != 0 || a.ldx < a.K || a.ldx % 4 != 0 || a.ldy < a.N) return hipErrorInvalidValue;
-    if (a.layout == LAYOUT_TILES && (a.K % 256 != 0 || a.N % 16 != 0)) return hipErrorInvalidValue;
+hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
+    if (a.T <= 0 || a.nseg <= 0) return hipSuccess;
+    if (a.nseg > 3 || a.K <= 0 || a.K % 32 != 0 || a.ldx < a.K || a.ldx % 4 != 0) return hipErrorInvalidValue;
+    const bool tiles = a.seg[0].layout == LAYOUT_TILES;
+    int64_t col_tiles = 0;
+    for (int i = 0; i < a.nseg; i++) {
+        PfSeg& g = a.seg[i];
+        if (g.N <= 0 || g.ldy < g.N || (g.layout == LAYOUT_TILES) != tiles) return hipErrorInvalidValue;
+        if (tiles && (a.K % 256 != 0 || g.N % 16 != 0 || (g.type != FLLM_TYPE_Q4_K && g.type != FLLM_TYPE_Q6_K)))
+            return hipErrorInvalidValue;
+        g.tiles = (g.N + PF_BN - 1) / PF_BN;
+        col_tiles += g.tiles;
+    }
     // 128-token tiles unless that leaves fewer than two workgroups per CU
-    const int64_t col_tiles = (a.N + PF_BN - 1) / PF_BN;
     const bool tall = col_tiles * ((a.T + 127) / 128) >= 2 * (int64_t)(n_cu > 0 ? n_cu : 256);
-    const PfGemmKernel k = tall ? pf_gemm_kernel<128>(a) : pf_gemm_kernel<64>(a);
-    if (!k) return hipErrorInvalidValue;
+    PfGemmKernel k;
+    if (tiles) k = tall ? k_pf_gemm_tiles<128> : k_pf_gemm_tiles<64>;
+    else k = tall ? k_pf_gemm_rows<128> : k_pf_gemm_rows<64>;
     const size_t lds = tall ? pf_gemm_lds<128>() : pf_gemm_lds<64>();
     hipError_t e = pf_lds_attr((const void*)k, lds);
     if (e != hipSuccess) return e;

@@ -6,21 +6,28 @@
 
 namespace fllm {
 
-// Y[t][n] (+)= sum_k X[t][k] W[n][k] for t < T, n < N, in f32 on the matrix cores. X: f32 rows of
-// stride ldx; W in its stored layout (LAYOUT_TILES Q4_K / Q6_K, or GGUF rows of any supported
-// type), dequantized exactly in the kernel. K is a multiple of 32.
+// Y[t][n] (+)= sum_k X[t][k] W[n][k] for t < T, n < N, in f32 on the matrix cores, for up to three
+// matrices that share X (one launch: q, k, v or gate, up). X: f32 rows of stride ldx; each W in its
+// stored layout (LAYOUT_TILES Q4_K / Q6_K, or GGUF rows of any supported type), dequantized exactly
+// in the kernel; all segments of a launch are tile-interleaved or none is. K is a multiple of 32.
+struct PfSeg {
+    const uint8_t* w;
+    int type, layout;
+    int N;
+    float* y;   // [T][ldy], column 0 = weight row 0
+    int ldy;
+    int tiles;  // set by launch_pf_gemm: 128-row column tiles of the segment
+};
 struct PfGemm {
     const float* x;
     int ldx;
-    const uint8_t* w;
-    int type, layout;
-    int N, K;
-    float* y;
-    int ldy;
+    int K;
     int T;
     int add;  // 1: y += X W^T (residual add), 0: y = X W^T
+    int nseg;
+    PfSeg seg[3];
 };
-hipError_t launch_pf_gemm(const PfGemm& a, int n_cu, hipStream_t st);
+hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st);
 
 // X[t] = embedding row tokens[t] (exact dequantization of any supported type)
 hipError_t launch_pf_embed(const int* tokens, int T, const uint8_t* emb, int type, int H, float* x, hipStream_t st);
