@@ -212,6 +212,25 @@ def profiler_roofline(args, bytes_per_launch, dom_name, steps_launches):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+
+
+def prefill_report(cfg, n, seconds):
+    """Arithmetic rate of the batched prefill (f32 matrix-core GEMMs): the projections' 2 flop per
+    weight per token plus the causal attention's 4 * heads * head_dim flop per (query, key) pair, over
+    the wall time of the whole prefill call (norms, element-wise steps and the last token's LM head
+    included, so the fraction is a lower bound for the GEMMs)."""
+    H, L, F = cfg["hidden"], cfg["n_layers"], cfg["ffn"]
+    hd = cfg["head_dim"]
+    qdim, kvdim = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
+    weights = L * (qdim * H + 2 * kvdim * H + H * qdim + 3 * F * H)
+    pairs = n * (n + 1) // 2
+    flops = 2.0 * n * weights + 4.0 * cfg["n_heads"] * hd * pairs * L
+    tf = flops / seconds / 1e12
+    return {"tokens": n, "tok_s": round(n / seconds, 2), "tflops": round(tf, 2), "dtype": "f32",
+            "mfma_peak_tflops": FP32_MFMA_PEAK_TFLOPS, "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -356,6 +375,7 @@ def main():
         "roofline": roofline,
         "decode_step_hbm_frac": round(tok_s * tok_bytes / (HBM_PEAK_GBS * 1e9), 4),
         "prefill_tok_s": round((args.prompt - 1) / prefill_s, 2),
+        "prefill": prefill_report(cfg, args.prompt - 1, prefill_s),
         "host_loop_tok_s": round(host_tok_s, 2) if host_tok_s else None,
         "profiled_step_ms": round(total_ms, 4),
         "cpu_baseline": cpu,

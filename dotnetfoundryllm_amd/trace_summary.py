@@ -2,9 +2,11 @@
 launch shape: launches, mean and minimum duration, and the idle time between consecutive
 dispatches.
 
-    python -m dotnetfoundryllm_amd.trace_summary <run_kernel_trace.csv> [--last N]
+    python -m dotnetfoundryllm_amd.trace_summary <run_kernel_trace.csv> [--last N] [--from NAME] [--match TEXT]
 
-``--last N`` keeps only the last N dispatches (the timed decode steps at the end of a bench run).
+``--last N`` keeps only the last N dispatches (the timed decode steps at the end of a bench run);
+``--from NAME`` starts at the last dispatch of kernel NAME (e.g. ``k_pf_embed``: the last batched
+prefill); ``--match TEXT`` keeps the kernels whose name contains TEXT.
 """
 import argparse
 import collections
@@ -15,9 +17,14 @@ def _short(name):
     return name.split("(")[0].replace("void ", "").replace("fllm::", "")
 
 
-def summarise(path, last=0):
+def summarise(path, last=0, start=None, match=None):
     rows = list(csv.DictReader(open(path)))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    if start:
+        idx = [i for i, r in enumerate(rows) if _short(r["Kernel_Name"]).startswith(start)]
+        rows = rows[idx[-1]:] if idx else []
+    if match:
+        rows = [r for r in rows if match in r["Kernel_Name"]]
     if last:
         rows = rows[-last:]
     agg = collections.OrderedDict()
@@ -40,8 +47,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
     ap.add_argument("--last", type=int, default=0)
+    ap.add_argument("--from", dest="start", default=None)
+    ap.add_argument("--match", default=None)
     a = ap.parse_args()
-    agg, gaps = summarise(a.trace, a.last)
+    agg, gaps = summarise(a.trace, a.last, a.start, a.match)
     total = sum(v["ns"] for v in agg.values())
     print("| kernel | grid (threads) | workgroup | VGPRs | launches | mean us | min us | share |")
     print("|---|---|---|---|---|---|---|---|")
@@ -49,8 +58,9 @@ def main():
         grid = f"{gx}x{gy}" if gy > 1 else f"{gx}"
         print(f"| {name} | {grid} | {wg} | {v['vgpr']} | {v['n']} | {v['ns'] / v['n'] / 1e3:.2f} | "
               f"{v['min'] / 1e3:.2f} | {100.0 * v['ns'] / total:.1f}% |")
+    print(f"\nkernel time {total / 1e6:.2f} ms over {sum(v['n'] for v in agg.values())} dispatches")
     if gaps:
-        print(f"\nidle between dispatches: median {gaps[len(gaps) // 2] / 1e3:.2f} us, "
+        print(f"idle between dispatches: median {gaps[len(gaps) // 2] / 1e3:.2f} us, "
               f"p90 {gaps[(9 * len(gaps)) // 10] / 1e3:.2f} us over {len(gaps)} gaps")
 
 
