@@ -177,7 +177,11 @@ FLLM_API int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable);
  * Slice fails the same way, LlamaForwardPass.cs:186-188 after KvCache.cs:82-85). */
 FLLM_API int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position);
 /* n consecutive Forward calls for tokens[0..n) at positions pos0.. (prefill loop,
- * LlamaLanguageModel.cs:133-137); same results as n fllm_forward calls. */
+ * LlamaLanguageModel.cs:133-137), with their results: the K/V rows of every position, the last
+ * position's logits and greedy token. When pos0 is the cache's current length (a prompt) and debug
+ * capture is off, the tokens go through each layer together in chunks of up to 512 (f32
+ * matrix-core GEMMs over the chunk, causal attention over the cache); otherwise, and for n = 1,
+ * it is n fllm_forward calls. Token ids and the cache capacity are checked before anything runs. */
 FLLM_API int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, int32_t pos0);
 /* The greedy part of LlamaLanguageModel.GenerateAsync's decode loop (LlamaLanguageModel.cs:162-293
  * with SamplerPipeline Temperature == 0, SamplerPipeline.cs:61-64, no EOS stop): n_steps Forward
