@@ -1214,7 +1214,10 @@ static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w,
     g.add = add ? 1 : 0;
     double bytes = 0.0;
     for (int i = 0; i < n; i++) {
-        if (g.nseg > 0 && (w[i]->layout == LAYOUT_TILES) != (g.seg[0].layout == LAYOUT_TILES)) {
+        // one launch per run of tile-interleaved matrices, or of GGUF-row matrices of one type
+        const bool split = g.nseg > 0 && ((w[i]->layout == LAYOUT_TILES) != (g.seg[0].layout == LAYOUT_TILES) ||
+                                          (w[i]->layout != LAYOUT_TILES && w[i]->type != g.seg[0].type));
+        if (split) {
             STEP(name, bytes, launch_pf_gemm(g, s->m->ctx->n_cu, s->st));
             g.nseg = 0;
             bytes = 0.0;

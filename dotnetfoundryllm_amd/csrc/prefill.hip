@@ -119,13 +119,148 @@ template <> struct PfW<FLLM_TYPE_Q6_K> {
     }
 };
 
-// GGUF rows of any supported type: element r * K + k of the flat block stream, read when decoded
+// GGUF rows: elements e0 = r * K + k0 .. e0 + 31 of the flat block stream (K % 32 == 0, so the
+// group lies in one block of every format), decoded from memory when staged. PF_ROWS + type: one
+// decoder per format with the block header read once per group; PfW<-1> is element-wise for the
+// remaining types.
+constexpr int PF_ROWS = 100;
+
 template <> struct PfW<-1> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
     __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int type, int K, int r, int k0, float* v) {
         const int64_t e0 = (int64_t)r * K + k0;
         for (int i = 0; i < 32; i++) v[i] = deq_elem(type, w, e0 + i);
+    }
+};
+
+// Q8_0 (Dequantizer.cs:203-231): (sbyte)q * d, one 34-byte block per group
+template <> struct PfW<PF_ROWS + FLLM_TYPE_Q8_0> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const uint8_t* p = w + (((int64_t)r * K + k0) >> 5) * 34;
+        const float d = half_exact(deq_ld_u16(p));
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = (float)(int8_t)p[2 + i] * d;
+    }
+};
+
+// Q4_0 (Dequantizer.cs:155-185): (nibble - 8) * d, low nibbles are elements 0..15
+template <> struct PfW<PF_ROWS + FLLM_TYPE_Q4_0> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const uint8_t* p = w + (((int64_t)r * K + k0) >> 5) * 18;
+        const float d = half_exact(deq_ld_u16(p));
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t b = p[2 + j];
+            v[j] = (float)((int)(b & 15u) - 8) * d;
+            v[16 + j] = (float)((int)(b >> 4) - 8) * d;
+        }
+    }
+};
+
+// Q4_K (Dequantizer.cs:251-294) in GGUF rows
+template <> struct PfW<PF_ROWS + FLLM_TYPE_Q4_K> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const int64_t e0 = (int64_t)r * K + k0;
+        const uint8_t* p = w + (e0 >> 8) * 144;
+        const int g = (int)((e0 & 255) >> 5);
+        const float d = half_exact(deq_ld_u16(p)), dmin = half_exact(deq_ld_u16(p + 2));
+        int sc, mn;
+        kscale_min(p + 4, g, sc, mn);
+        const float dg = d * (float)sc;
+        const float mg = dmin * (float)mn;
+        const uint8_t* qs = p + 16 + 16 * g;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t b = qs[j];
+            v[2 * j] = dg * (float)(int)(b & 15u) - mg;
+            v[2 * j + 1] = dg * (float)(int)(b >> 4) - mg;
+        }
+    }
+};
+
+// Q5_K (Dequantizer.cs:316-368): low nibble from qs, bit 4 from qh[t >> 3] bit (t & 7)
+template <> struct PfW<PF_ROWS + FLLM_TYPE_Q5_K> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const int64_t e0 = (int64_t)r * K + k0;
+        const uint8_t* p = w + (e0 >> 8) * 176;
+        const int t0 = (int)(e0 & 255), g = t0 >> 5;
+        const float d = half_exact(deq_ld_u16(p)), dmin = half_exact(deq_ld_u16(p + 2));
+        int sc, mn;
+        kscale_min(p + 4, g, sc, mn);
+        const float dg = d * (float)sc;
+        const float mg = dmin * (float)mn;
+        const uint32_t qh = deq_ld_u32(p + 16 + (t0 >> 3));  // bits of elements t0 .. t0 + 31
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t b = p[48 + (t0 >> 1) + j];
+            const int lo0 = (int)(b & 15u), lo1 = (int)(b >> 4);
+            const int hi0 = (int)((qh >> (2 * j)) & 1u), hi1 = (int)((qh >> (2 * j + 1)) & 1u);
+            v[2 * j] = dg * (float)((hi0 << 4) | lo0) - mg;
+            v[2 * j + 1] = dg * (float)((hi1 << 4) | lo1) - mg;
+        }
+    }
+};
+
+// Q6_K (Dequantizer.cs:378-417) in GGUF rows
+template <> struct PfW<PF_ROWS + FLLM_TYPE_Q6_K> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const int64_t e0 = (int64_t)r * K + k0;
+        const uint8_t* p = w + (e0 >> 8) * 210;
+        const int i0 = (int)(e0 & 255);
+        const float d = half_exact(deq_ld_u16(p + 208));
+        const uint32_t qh = deq_ld_u32(p + 128 + (i0 >> 2));
+        const uint32_t qh2 = deq_ld_u32(p + 128 + (i0 >> 2) + 4);
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const int i = i0 + j;
+            const uint32_t lb = p[i >> 1];
+            const int low = (j & 1) ? (int)(lb >> 4) : (int)(lb & 15u);
+            const uint32_t hw = j < 16 ? qh : qh2;
+            const int high = (int)((hw >> (2 * (j & 15))) & 3u);
+            const int q = ((high << 4) | low) - 32;
+            const int scale = (int)(int8_t)p[192 + (i >> 4)];
+            v[j] = d * (float)scale * (float)q;
+        }
+    }
+};
+
+// F16 / BF16 / F32 rows: exact widening (Dequantizer.cs:68-137)
+template <> struct PfW<PF_ROWS + FLLM_TYPE_F32> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const uint8_t* p = w + ((int64_t)r * K + k0) * 4;
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = bits_f32(deq_ld_u32(p + 4 * i));
+    }
+};
+template <> struct PfW<PF_ROWS + FLLM_TYPE_F16> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const uint8_t* p = w + ((int64_t)r * K + k0) * 2;
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = half_exact(deq_ld_u16(p + 2 * i));
+    }
+};
+template <> struct PfW<PF_ROWS + FLLM_TYPE_BF16> {
+    struct Raw {};
+    __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+        const uint8_t* p = w + ((int64_t)r * K + k0) * 2;
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = bf16_exact(deq_ld_u16(p + 2 * i));
     }
 };
 
@@ -232,6 +367,8 @@ __device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, i
             }
 }
 
+typedef void (*PfGemmKernel)(const PfGemm);
+
 // workgroup (x, y): column tile x of the launch's segments, token tile y
 __device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
     int si = 0;
@@ -255,16 +392,30 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tiles(const PfGemm a) {
         pf_gemm_tile<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
 }
 
-// GGUF-row segments of any type
-template <int BM>
+// GGUF-row segments, all of type RT - PF_ROWS (RT = -1: any type, element-wise)
+template <int BM, int RT>
 __global__ __launch_bounds__(256) void k_pf_gemm_rows(const PfGemm a) {
     extern __shared__ __attribute__((aligned(16))) float pf_lds[];
     int bx = blockIdx.x;
     const int si = pf_seg_of(a, bx);
-    pf_gemm_tile<-1, BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
+    pf_gemm_tile<RT, BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
 }
 
-typedef void (*PfGemmKernel)(const PfGemm);
+template <int BM>
+static PfGemmKernel pf_rows_kernel(int type) {
+    switch (type) {
+        case FLLM_TYPE_Q8_0: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q8_0>;
+        case FLLM_TYPE_Q4_0: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q4_0>;
+        case FLLM_TYPE_Q4_K: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q4_K>;
+        case FLLM_TYPE_Q5_K: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q5_K>;
+        case FLLM_TYPE_Q6_K: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q6_K>;
+        case FLLM_TYPE_F32: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_F32>;
+        case FLLM_TYPE_F16: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_F16>;
+        case FLLM_TYPE_BF16: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_BF16>;
+        default: return k_pf_gemm_rows<BM, -1>;
+    }
+}
+
 static hipError_t pf_lds_attr(const void* k, size_t bytes) {
     return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
@@ -277,6 +428,7 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
     for (int i = 0; i < a.nseg; i++) {
         PfSeg& g = a.seg[i];
         if (g.N <= 0 || g.ldy < g.N || (g.layout == LAYOUT_TILES) != tiles) return hipErrorInvalidValue;
+        if (!tiles && g.type != a.seg[0].type) return hipErrorInvalidValue;  // one decoder per row launch
         if (tiles && (a.K % 256 != 0 || g.N % 16 != 0 || (g.type != FLLM_TYPE_Q4_K && g.type != FLLM_TYPE_Q6_K)))
             return hipErrorInvalidValue;
         g.tiles = (g.N + PF_BN - 1) / PF_BN;
@@ -286,7 +438,7 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
     const bool tall = col_tiles * ((a.T + 127) / 128) >= 2 * (int64_t)(n_cu > 0 ? n_cu : 256);
     PfGemmKernel k;
     if (tiles) k = tall ? k_pf_gemm_tiles<128> : k_pf_gemm_tiles<64>;
-    else k = tall ? k_pf_gemm_rows<128> : k_pf_gemm_rows<64>;
+    else k = tall ? pf_rows_kernel<128>(a.seg[0].type) : pf_rows_kernel<64>(a.seg[0].type);
     const size_t lds = tall ? pf_gemm_lds<128>() : pf_gemm_lds<64>();
     hipError_t e = pf_lds_attr((const void*)k, lds);
     if (e != hipSuccess) return e;
