@@ -685,7 +685,7 @@ constexpr int MF_TILE = 16;        // weight rows per MFMA tile
 
 // bytes of 256 elements (one chunk) for the MFMA-capable types
 __host__ __device__ constexpr int mf_chunk_bytes(int t) {
-    return t == FLLM_TYPE_Q4_K ? 144 : t == FLLM_TYPE_Q6_K ? 210 : 0;
+    return t == FLLM_TYPE_Q4_K ? 144 : t == FLLM_TYPE_Q6_K ? 210 : t == FLLM_TYPE_Q8_0 ? 272 : 0;
 }
 
 
@@ -917,6 +917,35 @@ template <int T, bool IL> struct MfPick;
 template <bool IL> struct MfPick<FLLM_TYPE_Q4_K, IL> { using Raw = MfQ4K; };
 template <> struct MfPick<FLLM_TYPE_Q6_K, false> { using Raw = MfQ6K; };
 template <> struct MfPick<FLLM_TYPE_Q6_K, true> { using Raw = MfQ6KT; };
+
+// ---- Q8_0 (Dequantizer.cs:203-231), tile-interleaved only: 8 blocks of 34 bytes per chunk ------
+// In LAYOUT_TILES each 16-element half of a group is stored in the activation table's element
+// order (byte 4 j + by = element 4 by + j), so the loaded dwords are the MFMA operand as they are;
+// the lane's two block scales (groups q and q + 4) share one dword.
+struct MfQ8T { uint4 a0, a1, b0, b1; uint32_t d; };
+__device__ __forceinline__ void mf_issue_tiles(MfQ8T& r, const uint8_t* __restrict__ reg, int lane, int n) {
+    r.a0 = *(const uint4*)(reg + 16 * lane);         // group q, elements 0 .. 15
+    r.a1 = *(const uint4*)(reg + 1024 + 16 * lane);  // group q, elements 16 .. 31
+    r.b0 = *(const uint4*)(reg + 2048 + 16 * lane);  // group q + 4
+    r.b1 = *(const uint4*)(reg + 3072 + 16 * lane);
+    r.d = *(const uint32_t*)(reg + 4096 + 16 * n + 4 * (lane >> 4));
+}
+__device__ __forceinline__ v4i mf_v4i(const uint4& u) {
+    v4i r = {(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+    return r;
+}
+// y = d_q * sum over group q of q_i x_i + d_{q+4} * (group q + 4): (sbyte)q * d per element
+__device__ __forceinline__ float mf_compute(const MfQ8T& r, const v4i* A, const f32x4& sA, const f32x4& sB, int,
+                                            int) {
+    const v4i z = {0, 0, 0, 0};
+    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], mf_v4i(r.a0), z, 0, 0, 0);
+    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], mf_v4i(r.a1), z, 0, 0, 0);
+    const v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], mf_v4i(r.b0), z, 0, 0, 0);
+    const v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], mf_v4i(r.b1), z, 0, 0, 0);
+    const float dq = h2f(r.d & 0xFFFFu), dq4 = h2f(r.d >> 16);
+    return fmaf(dq, fmaf(sA.x, mf_total(D0), sA.y * mf_total(D1)), dq4 * fmaf(sB.x, mf_total(D2), sB.y * mf_total(D3)));
+}
+template <> struct MfPick<FLLM_TYPE_Q8_0, true> { using Raw = MfQ8T; };
 
 // Persistent workgroup body of the MFMA variant for weight type T. The launch's rows form units:
 // one 16-row tile, or for GLU the gate and up tiles of the same 16 rows. Workgroup w takes units
@@ -1248,6 +1277,10 @@ template <bool IL>
 static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
     const bool tab = a.xin == XIN_TAB;
     if (a.mix_wg > 0) return tab ? mf_kernel_mix<true, IL>(kc) : mf_kernel_mix<false, IL>(kc);
+    if constexpr (IL) {
+        if (a.seg[0].type == FLLM_TYPE_Q8_0)
+            return tab ? mf_kernel_in<FLLM_TYPE_Q8_0, true, true>(kc) : mf_kernel_in<FLLM_TYPE_Q8_0, false, true>(kc);
+    }
     if (a.seg[0].type == FLLM_TYPE_Q6_K)
         return tab ? mf_kernel_in<FLLM_TYPE_Q6_K, true, IL>(kc) : mf_kernel_in<FLLM_TYPE_Q6_K, false, IL>(kc);
     return tab ? mf_kernel_in<FLLM_TYPE_Q4_K, true, IL>(kc) : mf_kernel_in<FLLM_TYPE_Q4_K, false, IL>(kc);
@@ -1317,6 +1350,7 @@ static bool mfma_ok(const GemvArgs& a, int64_t cols) {
             if (i > 0 && t == FLLM_TYPE_Q4_K && a.seg[i - 1].type != FLLM_TYPE_Q4_K) return false;
             continue;
         }
+        if (t == FLLM_TYPE_Q8_0) return false;  // Q8_0 is read tile-interleaved only
         // one type, or Q4_K segments followed by Q6_K ones (the two-type kernel; not for GLU)
         if (t != a.seg[0].type && (a.glu || t != FLLM_TYPE_Q6_K || a.seg[0].type != FLLM_TYPE_Q4_K)) return false;
         if (i > 0 && t == FLLM_TYPE_Q4_K && a.seg[i - 1].type != FLLM_TYPE_Q4_K) return false;
@@ -1429,25 +1463,41 @@ bool gemv_tiles_shape_ok(int type, int64_t rows, int64_t cols) {
     return (uint64_t)rows * (uint64_t)NB * (uint64_t)mf_chunk_bytes(type) < (1ull << 32);
 }
 
-// LAYOUT_TILES of a Q4_K or Q6_K matrix (rows a multiple of 16, NB chunks per row): the blocks of
-// tile t (rows 16t .. 16t + 15) in chunk column kb fill region t * NB + kb of 16 block sizes, laid
-// out so that matrix-core lane L = 16 q + n (tile row n, quarter q) finds its part of row n as
-// 16-byte pieces at 16 L of 1 KiB slices, and the fields a row's four lanes share at n:
+// LAYOUT_TILES of a Q4_K, Q6_K or Q8_0 matrix (rows a multiple of 16, NB chunks of 256 elements per
+// row): the blocks of tile t (rows 16t .. 16t + 15) in chunk column kb fill region t * NB + kb of 16
+// chunk sizes, laid out so that matrix-core lane L = 16 q + n (tile row n, quarter q) finds its part
+// of row n as 16-byte pieces at 16 L of 1 KiB slices, and the fields a row's four lanes share at n:
 //   Q4_K, 2304 B: [0, 1024) qs bytes 16q .. 16q + 15; [1024, 2048) qs bytes 64 + 16q .. ;
 //                 [2048, 2304) block bytes 0 .. 15 (d, dmin, scales) at 16 n
 //   Q6_K, 3360 B: [0, 1024) ql 16q .. ; [1024, 2048) ql 64 + 16q .. ; [2048, 3072) qh 8q .. 8q + 7
 //                 then qh 32 + 8q .. ; [3072, 3328) scales 2q, 2q + 1, 8 + 2q, 9 + 2q at 4 L;
 //                 [3328, 3360) d at 2 n
+//   Q8_0, 4352 B: [0, 1024) int8 0 .. 15 of block q; [1024, 2048) its 16 .. 31; [2048, 4096) the same
+//                 for block q + 4; each 16-byte piece in element order 4 by + j at byte 4 j + by (the
+//                 activation table's); [4096, 4352) d of blocks q and q + 4 as one dword at 16 n + 4 q
 // Every block byte has exactly one place, so the regrouped matrix dequantizes to the same values.
-// One thread per block.
+// One thread per (row, chunk).
 __global__ void k_pack_tiles(int type, const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int rows, int NB) {
-    const int64_t nblk = (int64_t)rows * NB;
-    const int bpb = type == FLLM_TYPE_Q6_K ? 210 : 144;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nblk; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t nchunk = (int64_t)rows * NB;
+    const int cb = mf_chunk_bytes(type);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nchunk; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / NB;
         const int kb = (int)(i % NB), n = (int)(r & 15);
-        const uint8_t* b = src + i * bpb;
-        uint8_t* reg = dst + ((r >> 4) * NB + kb) * 16 * bpb;
+        const uint8_t* b = src + i * cb;  // the row's chunk kb: one K-quant block, or 8 Q8_0 blocks
+        uint8_t* reg = dst + ((r >> 4) * NB + kb) * 16 * cb;
+        if (type == FLLM_TYPE_Q8_0) {
+            for (int g = 0; g < 8; g++) {
+                const uint8_t* blk = b + 34 * g;
+                const int q = g & 3, L = 16 * q + n, base = (g < 4 ? 0 : 2048) + 16 * L;
+                for (int e = 0; e < 32; e++) {
+                    const int h = e >> 4, ee = e & 15;
+                    reg[base + 1024 * h + 4 * (ee & 3) + (ee >> 2)] = blk[2 + e];
+                }
+                reg[4096 + 16 * n + 4 * q + (g < 4 ? 0 : 2)] = blk[0];
+                reg[4096 + 16 * n + 4 * q + (g < 4 ? 0 : 2) + 1] = blk[1];
+            }
+            continue;
+        }
         for (int q = 0; q < 4; q++) {
             const int L = 16 * q + n;
             if (type == FLLM_TYPE_Q6_K) {

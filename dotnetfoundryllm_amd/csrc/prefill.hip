@@ -119,6 +119,30 @@ template <> struct PfW<FLLM_TYPE_Q6_K> {
     }
 };
 
+// LAYOUT_TILES Q8_0: block g & 3 (+4) of the row's chunk; its 32 int8 as two 16-byte pieces in
+// element order 4 by + j at byte 4 j + by; d of blocks q and q + 4 in one dword at 4096 + 16 n + 4 q
+template <> struct PfW<FLLM_TYPE_Q8_0> {
+    struct Raw { uint4 h0, h1; uint32_t d; };
+    __device__ static void load(Raw& w4, const uint8_t* __restrict__ w, int K, int r, int k0) {
+        const int NB = K >> 8, kb = k0 >> 8, g = (k0 >> 5) & 7, n = r & 15, q = g & 3, L = 16 * q + n;
+        const uint8_t* reg = w + ((size_t)(r >> 4) * NB + kb) * (16 * 272);
+        const uint8_t* base = reg + (g < 4 ? 0 : 2048) + 16 * L;
+        w4.h0 = *(const uint4*)base;
+        w4.h1 = *(const uint4*)(base + 1024);
+        w4.d = *(const uint32_t*)(reg + 4096 + 16 * n + 4 * q);
+    }
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+        const int g = (k0 >> 5) & 7;
+        const float d = half_exact(g < 4 ? (w4.d & 0xFFFFu) : (w4.d >> 16));
+        const uint32_t hw[8] = {w4.h0.x, w4.h0.y, w4.h0.z, w4.h0.w, w4.h1.x, w4.h1.y, w4.h1.z, w4.h1.w};
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            const int h = e >> 4, ee = e & 15, j = ee & 3, by = ee >> 2;  // byte 4 j + by of half h
+            v[e] = (float)(int8_t)((hw[4 * h + j] >> (8 * by)) & 0xFFu) * d;
+        }
+    }
+};
+
 // GGUF rows: elements e0 = r * K + k0 .. e0 + 31 of the flat block stream (K % 32 == 0, so the
 // group lies in one block of every format), decoded from memory when staged. PF_ROWS + type: one
 // decoder per format with the block header read once per group; PfW<-1> is element-wise for the
@@ -388,6 +412,8 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tiles(const PfGemm a) {
     const PfSeg& sg = a.seg[si];
     if (sg.type == FLLM_TYPE_Q6_K)
         pf_gemm_tile<FLLM_TYPE_Q6_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
+    else if (sg.type == FLLM_TYPE_Q8_0)
+        pf_gemm_tile<FLLM_TYPE_Q8_0, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
     else
         pf_gemm_tile<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
 }
@@ -429,7 +455,8 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         PfSeg& g = a.seg[i];
         if (g.N <= 0 || g.ldy < g.N || (g.layout == LAYOUT_TILES) != tiles) return hipErrorInvalidValue;
         if (!tiles && g.type != a.seg[0].type) return hipErrorInvalidValue;  // one decoder per row launch
-        if (tiles && (a.K % 256 != 0 || g.N % 16 != 0 || (g.type != FLLM_TYPE_Q4_K && g.type != FLLM_TYPE_Q6_K)))
+        if (tiles && (a.K % 256 != 0 || g.N % 16 != 0 ||
+                      (g.type != FLLM_TYPE_Q4_K && g.type != FLLM_TYPE_Q6_K && g.type != FLLM_TYPE_Q8_0)))
             return hipErrorInvalidValue;
         g.tiles = (g.N + PF_BN - 1) / PF_BN;
         col_tiles += g.tiles;
