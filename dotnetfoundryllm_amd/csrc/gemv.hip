@@ -685,7 +685,7 @@ constexpr int MF_TILE = 16;        // weight rows per MFMA tile
 
 // bytes of 256 elements (one chunk) for the MFMA-capable types
 __host__ __device__ constexpr int mf_chunk_bytes(int t) {
-    return t == FLLM_TYPE_Q4_K ? 144 : t == FLLM_TYPE_Q6_K ? 210 : t == FLLM_TYPE_Q8_0 ? 272 : 0;
+    return t == FLLM_TYPE_Q4_K ? 144 : t == FLLM_TYPE_Q6_K ? 210 : t == FLLM_TYPE_Q8_0 ? 272 : t == FLLM_TYPE_Q5_K ? 176 : 0;
 }
 
 
@@ -946,6 +946,48 @@ __device__ __forceinline__ float mf_compute(const MfQ8T& r, const v4i* A, const 
     return fmaf(dq, fmaf(sA.x, mf_total(D0), sA.y * mf_total(D1)), dq4 * fmaf(sB.x, mf_total(D2), sB.y * mf_total(D3)));
 }
 template <> struct MfPick<FLLM_TYPE_Q8_0, true> { using Raw = MfQ8T; };
+
+// ---- Q5_K (Dequantizer.cs:316-368), tile-interleaved only ---------------------------------------
+// Low nibbles as Q4_K (group g = qs bytes 16 g .. 16 g + 15); the 32 high bits of a group are
+// regrouped at pack time so that bit 8 by + 4 h + j is the bit of element 16 h + 4 by + j: the high
+// bits of fragment dword j of half h are then (H >> (4 h + j)) & 0x01010101, shifted to bit 4.
+struct MfQ5KT { uint4 hdr, qa, qb; uint2 h; };
+__device__ __forceinline__ void mf_issue_tiles(MfQ5KT& r, const uint8_t* __restrict__ reg, int lane, int n) {
+    r.qa = *(const uint4*)(reg + 16 * lane);          // qs of group q
+    r.qb = *(const uint4*)(reg + 1024 + 16 * lane);   // qs of group q + 4
+    r.h = *(const uint2*)(reg + 2048 + 8 * lane);     // high bits of groups q and q + 4
+    r.hdr = *(const uint4*)(reg + 2560 + 16 * n);     // d, dmin, scales
+}
+// q4_frag with bit 4 of each byte from the regrouped high bits of half h
+__device__ __forceinline__ v4i q5_frag(uint32_t w0, uint32_t w1, uint32_t H, int h) {
+    v4i f = q4_frag(w0, w1);
+    f.x |= (int)(((H >> (4 * h + 0)) & 0x01010101u) << 4);
+    f.y |= (int)(((H >> (4 * h + 1)) & 0x01010101u) << 4);
+    f.z |= (int)(((H >> (4 * h + 2)) & 0x01010101u) << 4);
+    f.w |= (int)(((H >> (4 * h + 3)) & 0x01010101u) << 4);
+    return f;
+}
+__device__ __forceinline__ float mf_compute(const MfQ5KT& r, const v4i* A, const f32x4& sA, const f32x4& sB, int q,
+                                            int) {
+    const v4i z = {0, 0, 0, 0};
+    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], q5_frag(r.qa.x, r.qa.y, r.h.x, 0), z, 0, 0, 0);
+    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], q5_frag(r.qa.z, r.qa.w, r.h.x, 1), z, 0, 0, 0);
+    const v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], q5_frag(r.qb.x, r.qb.y, r.h.y, 0), z, 0, 0, 0);
+    const v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], q5_frag(r.qb.z, r.qb.w, r.h.y, 1), z, 0, 0, 0);
+    // DecodeKScaleMin (Dequantizer.cs:506-521) for groups q (< 4) and q + 4, as Q4_K
+    const int sh = 8 * q;
+    const uint32_t a = (r.hdr.y >> sh) & 0xFF, b = (r.hdr.z >> sh) & 0xFF, c = (r.hdr.w >> sh) & 0xFF;
+    const int scA = (int)(a & 63), mnA = (int)(b & 63);
+    const int scB = (int)((c & 15) | ((a >> 6) << 4)), mnB = (int)((c >> 4) | ((b >> 6) << 4));
+    const float d = h2f(r.hdr.x & 0xFFFFu), dmin = h2f(r.hdr.x >> 16);
+    const float dgA = d * (float)scA, mgA = dmin * (float)mnA;
+    const float dgB = d * (float)scB, mgB = dmin * (float)mnB;
+    const float tA = fmaf(sA.x, mf_total(D0), sA.y * mf_total(D1));
+    const float tB = fmaf(sB.x, mf_total(D2), sB.y * mf_total(D3));
+    const float y = fmaf(dgA, tA, -mgA * (sA.z + sA.w));
+    return y + fmaf(dgB, tB, -mgB * (sB.z + sB.w));
+}
+template <> struct MfPick<FLLM_TYPE_Q5_K, true> { using Raw = MfQ5KT; };
 
 // Persistent workgroup body of the MFMA variant for weight type T. The launch's rows form units:
 // one 16-row tile, or for GLU the gate and up tiles of the same 16 rows. Workgroup w takes units
@@ -1280,6 +1322,8 @@ static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
     if constexpr (IL) {
         if (a.seg[0].type == FLLM_TYPE_Q8_0)
             return tab ? mf_kernel_in<FLLM_TYPE_Q8_0, true, true>(kc) : mf_kernel_in<FLLM_TYPE_Q8_0, false, true>(kc);
+        if (a.seg[0].type == FLLM_TYPE_Q5_K)
+            return tab ? mf_kernel_in<FLLM_TYPE_Q5_K, true, true>(kc) : mf_kernel_in<FLLM_TYPE_Q5_K, false, true>(kc);
     }
     if (a.seg[0].type == FLLM_TYPE_Q6_K)
         return tab ? mf_kernel_in<FLLM_TYPE_Q6_K, true, IL>(kc) : mf_kernel_in<FLLM_TYPE_Q6_K, false, IL>(kc);
@@ -1350,7 +1394,7 @@ static bool mfma_ok(const GemvArgs& a, int64_t cols) {
             if (i > 0 && t == FLLM_TYPE_Q4_K && a.seg[i - 1].type != FLLM_TYPE_Q4_K) return false;
             continue;
         }
-        if (t == FLLM_TYPE_Q8_0) return false;  // Q8_0 is read tile-interleaved only
+        if (t == FLLM_TYPE_Q8_0 || t == FLLM_TYPE_Q5_K) return false;  // read tile-interleaved only
         // one type, or Q4_K segments followed by Q6_K ones (the two-type kernel; not for GLU)
         if (t != a.seg[0].type && (a.glu || t != FLLM_TYPE_Q6_K || a.seg[0].type != FLLM_TYPE_Q4_K)) return false;
         if (i > 0 && t == FLLM_TYPE_Q4_K && a.seg[i - 1].type != FLLM_TYPE_Q4_K) return false;
@@ -1475,7 +1519,12 @@ bool gemv_tiles_shape_ok(int type, int64_t rows, int64_t cols) {
 //   Q8_0, 4352 B: [0, 1024) int8 0 .. 15 of block q; [1024, 2048) its 16 .. 31; [2048, 4096) the same
 //                 for block q + 4; each 16-byte piece in element order 4 by + j at byte 4 j + by (the
 //                 activation table's); [4096, 4352) d of blocks q and q + 4 as one dword at 16 n + 4 q
-// Every block byte has exactly one place, so the regrouped matrix dequantizes to the same values.
+//   Q5_K, 2816 B: [0, 1024) qs bytes 16q .. ; [1024, 2048) qs bytes 64 + 16q .. ; [2048, 2560) the high
+//                 bits of groups q and q + 4 (qh bits 32 g .. 32 g + 31) as two dwords at 8 L, each with
+//                 the bit of element 16 h + 4 by + j at bit 8 by + 4 h + j; [2560, 2816) block bytes
+//                 0 .. 15 at 16 n
+// Every block byte (for Q5_K's high bits: every bit) has exactly one place, so the regrouped matrix
+// dequantizes to the same values.
 // One thread per (row, chunk).
 __global__ void k_pack_tiles(int type, const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int rows, int NB) {
     const int64_t nchunk = (int64_t)rows * NB;
@@ -1485,6 +1534,23 @@ __global__ void k_pack_tiles(int type, const uint8_t* __restrict__ src, uint8_t*
         const int kb = (int)(i % NB), n = (int)(r & 15);
         const uint8_t* b = src + i * cb;  // the row's chunk kb: one K-quant block, or 8 Q8_0 blocks
         uint8_t* reg = dst + ((r >> 4) * NB + kb) * 16 * cb;
+        if (type == FLLM_TYPE_Q5_K) {
+            for (int g = 0; g < 8; g++) {
+                const int q = g & 3, L = 16 * q + n;
+                for (int j = 0; j < 16; j++) reg[(g < 4 ? 0 : 1024) + 16 * L + j] = b[48 + 16 * g + j];
+                const uint32_t hs = (uint32_t)b[16 + 4 * g] | ((uint32_t)b[17 + 4 * g] << 8) |
+                                    ((uint32_t)b[18 + 4 * g] << 16) | ((uint32_t)b[19 + 4 * g] << 24);
+                uint32_t hr = 0u;
+                for (int e = 0; e < 32; e++) {
+                    const int h = e >> 4, by = (e >> 2) & 3, j = e & 3;
+                    hr |= ((hs >> e) & 1u) << (8 * by + 4 * h + j);
+                }
+                uint8_t* hp = reg + 2048 + 8 * L + (g < 4 ? 0 : 4);
+                hp[0] = (uint8_t)hr; hp[1] = (uint8_t)(hr >> 8); hp[2] = (uint8_t)(hr >> 16); hp[3] = (uint8_t)(hr >> 24);
+            }
+            for (int j = 0; j < 16; j++) reg[2560 + 16 * n + j] = b[j];
+            continue;
+        }
         if (type == FLLM_TYPE_Q8_0) {
             for (int g = 0; g < 8; g++) {
                 const uint8_t* blk = b + 34 * g;

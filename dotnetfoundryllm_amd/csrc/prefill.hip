@@ -143,6 +143,43 @@ template <> struct PfW<FLLM_TYPE_Q8_0> {
     }
 };
 
+// LAYOUT_TILES Q5_K: low nibbles as Q4_K, the group's regrouped high bits (bit 8 by + 4 h + j =
+// element 16 h + 4 by + j) in the dword at 2048 + 8 L (+4 for g >= 4), header at 2560 + 16 n
+template <> struct PfW<FLLM_TYPE_Q5_K> {
+    struct Raw { uint4 qs, hdr; uint32_t h; };
+    __device__ static void load(Raw& w4, const uint8_t* __restrict__ w, int K, int r, int k0) {
+        const int NB = K >> 8, kb = k0 >> 8, g = (k0 >> 5) & 7, n = r & 15, L = 16 * (g & 3) + n;
+        const uint8_t* reg = w + ((size_t)(r >> 4) * NB + kb) * (16 * 176);
+        w4.qs = *(const uint4*)(reg + (g < 4 ? 0 : 1024) + 16 * L);
+        w4.h = *(const uint32_t*)(reg + 2048 + 8 * L + (g < 4 ? 0 : 4));
+        w4.hdr = *(const uint4*)(reg + 2560 + 16 * n);
+    }
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+        const int g = (k0 >> 5) & 7;
+        const float d = half_exact(w4.hdr.x & 0xFFFFu), dmin = half_exact(w4.hdr.x >> 16);
+        int sc, mn;
+        if (g < 4) {
+            sc = (int)(PfW<FLLM_TYPE_Q4_K>::hbyte(w4.hdr, 4 + g) & 63u);
+            mn = (int)(PfW<FLLM_TYPE_Q4_K>::hbyte(w4.hdr, 8 + g) & 63u);
+        } else {
+            const uint32_t b = PfW<FLLM_TYPE_Q4_K>::hbyte(w4.hdr, 8 + g), lo = PfW<FLLM_TYPE_Q4_K>::hbyte(w4.hdr, g),
+                           hi = PfW<FLLM_TYPE_Q4_K>::hbyte(w4.hdr, 4 + g);
+            sc = (int)((b & 15u) | ((lo >> 6) << 4));
+            mn = (int)((b >> 4) | ((hi >> 6) << 4));
+        }
+        const float dg = d * (float)sc;
+        const float mg = dmin * (float)mn;
+        const uint32_t wd[4] = {w4.qs.x, w4.qs.y, w4.qs.z, w4.qs.w};
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            const uint32_t byte = (wd[e >> 3] >> (8 * ((e >> 1) & 3))) & 0xFFu;
+            const int lo = (e & 1) ? (int)(byte >> 4) : (int)(byte & 15u);
+            const int hi = (int)((w4.h >> (8 * ((e >> 2) & 3) + 4 * (e >> 4) + (e & 3))) & 1u);
+            v[e] = dg * (float)((hi << 4) | lo) - mg;
+        }
+    }
+};
+
 // GGUF rows: elements e0 = r * K + k0 .. e0 + 31 of the flat block stream (K % 32 == 0, so the
 // group lies in one block of every format), decoded from memory when staged. PF_ROWS + type: one
 // decoder per format with the block header read once per group; PfW<-1> is element-wise for the
@@ -414,6 +451,8 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tiles(const PfGemm a) {
         pf_gemm_tile<FLLM_TYPE_Q6_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
     else if (sg.type == FLLM_TYPE_Q8_0)
         pf_gemm_tile<FLLM_TYPE_Q8_0, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
+    else if (sg.type == FLLM_TYPE_Q5_K)
+        pf_gemm_tile<FLLM_TYPE_Q5_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
     else
         pf_gemm_tile<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
 }
@@ -456,7 +495,8 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         if (g.N <= 0 || g.ldy < g.N || (g.layout == LAYOUT_TILES) != tiles) return hipErrorInvalidValue;
         if (!tiles && g.type != a.seg[0].type) return hipErrorInvalidValue;  // one decoder per row launch
         if (tiles && (a.K % 256 != 0 || g.N % 16 != 0 ||
-                      (g.type != FLLM_TYPE_Q4_K && g.type != FLLM_TYPE_Q6_K && g.type != FLLM_TYPE_Q8_0)))
+                      (g.type != FLLM_TYPE_Q4_K && g.type != FLLM_TYPE_Q6_K && g.type != FLLM_TYPE_Q8_0 &&
+                       g.type != FLLM_TYPE_Q5_K)))
             return hipErrorInvalidValue;
         g.tiles = (g.N + PF_BN - 1) / PF_BN;
         col_tiles += g.tiles;
