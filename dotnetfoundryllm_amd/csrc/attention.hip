@@ -111,12 +111,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     for (int h = 0; h < G; h++) qv[h] = *(const float4*)(a.q + (int64_t)(h0 + h) * HD + dl * 4);
 
     const int seq = a.params->pos + 1;
-    int ws = seq - a.window;
-    if (ws < 0) ws = 0;
-    const int alen = seq - ws;
-    int ch = (alen + a.nc - 1) / a.nc;
-    ch = (ch + 31) / 32 * 32;
-    const int nchunks = (alen + ch - 1) / ch;
+    const AttnRange rg = attn_range(a.params->pos, a.window, a.nc);
+    const int ws = rg.ws, ch = rg.ch, nchunks = rg.nchunks;
     if (c >= nchunks) return;
     const int t0 = ws + c * ch;
     const int len = min(ch, seq - t0);
@@ -203,6 +199,88 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     }
 }
 
+// The head's part of the activation table of out, for the output projection: lanes 4k .. 4k + 3
+// hold the 16 elements of half k (res: one float4 each, HD / 4 lanes in all). Called by all 64
+// lanes of the workgroup.
+template <int HD>
+__device__ __forceinline__ void merge_emit_table(const AttnArgs& a, int h, int lane, const float4 res) {
+    __shared__ __attribute__((aligned(16))) uint8_t stg[HD / 16][3][16];
+    const bool live = lane < HD / 4;
+    const float4 v = res;
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float sum = (v.x + v.y) + (v.z + v.w);
+#pragma unroll
+    for (int o = 1; o < 4; o <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o));
+        sum += __shfl_xor(sum, o);
+    }
+    float sc, qinv;
+    half_scale(amax, sc, qinv);
+    const int hl = lane >> 2, by = lane & 3;  // element 4 by + j of half hl, j = component
+    if (live) {
+        const float c4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int b2, b1, b0;
+            digits3(quant_x(c4[j], qinv), b2, b1, b0);
+            stg[hl][0][4 * j + by] = (uint8_t)b2;
+            stg[hl][1][4 * j + by] = (uint8_t)b1;
+            stg[hl][2][4 * j + by] = (uint8_t)b0;
+        }
+    }
+    __syncthreads();
+    const int n = a.nh * HD;
+    uint4* tab = (uint4*)a.tab_out;
+    if (lane < (HD / 16) * 3) {
+        const int k = lane / 3, d = lane % 3;
+        int entry0, byte, stat, half;
+        tab_pos(h * HD + 16 * k, n, entry0, byte, stat, half);
+        tab[entry0 + d] = *(const uint4*)&stg[k][d][0];
+    }
+    if (live && by == 0) {
+        int entry0, byte, stat, half;
+        tab_pos(h * HD + 16 * hl, n, entry0, byte, stat, half);
+        float* st = (float*)(tab + stat);
+        st[half] = sc;
+        st[2 + half] = sum;
+    }
+}
+
+// Merge for at most NCM chunks: every load that does not depend on the step (the chunks' (m, l) and
+// this lane's slices of their outputs for all nc chunk slots) goes out at the start, beside the
+// read of the step's position; the weights reach the lanes by readlane.
+template <int HD, int NCM>
+__global__ __launch_bounds__(64) void k_attn_merge_fast(const AttnArgs a) {
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const float2 ml = *(const float2*)(a.part_ml + ((int64_t)h * a.nc + (lane < a.nc ? lane : a.nc - 1)) * 2);
+    const float* po = a.part_o + (int64_t)h * a.nc * HD + (lane < HD / 4 ? lane : 0) * 4;
+    // unconditional loads (slots past nc re-read the last one) so that all of them are in flight
+    float4 p[NCM];
+#pragma unroll
+    for (int k = 0; k < NCM; k++) p[k] = *(const float4*)(po + (int64_t)(k < a.nc ? k : a.nc - 1) * HD);
+    const int nchunks = attn_range(a.params->pos, a.window, a.nc).nchunks;
+    const bool valid = lane < nchunks;
+    const float M = wave_max(valid ? ml.x : -INFINITY);
+    const float w = valid ? expf(ml.x - M) : 0.0f;
+    const float L = wave_sum(valid ? ml.y * w : 0.0f);
+    // slots from nchunks on hold no partial of this step (possibly never-written memory): skipped,
+    // not weighted by zero
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < NCM; k++) {
+        const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k));
+        const bool use = k < nchunks;
+        o.x = use ? fmaf(p[k].x, wk, o.x) : o.x;
+        o.y = use ? fmaf(p[k].y, wk, o.y) : o.y;
+        o.z = use ? fmaf(p[k].z, wk, o.z) : o.z;
+        o.w = use ? fmaf(p[k].w, wk, o.w) : o.w;
+    }
+    const float inv = 1.0f / L;
+    const float4 res = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    if (lane < HD / 4) *(float4*)(a.out + (int64_t)h * HD + lane * 4) = res;
+    if (a.tab_out) merge_emit_table<HD>(a, h, lane, res);
+}
+
 // out[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M) over the chunks of head h. One wave per
 // head: lane k holds chunk k's (m, l) (chunks are at most 256), the weights go through LDS, and
 // every lane then sums its float4 slices of the chunk outputs with all loads of a pass in flight.
@@ -211,13 +289,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(const AttnArgs a) {
     __shared__ float wts[256];
     __shared__ float s_inv;
     const int h = blockIdx.x, lane = threadIdx.x;
-    const int seq = a.params->pos + 1;
-    int ws = seq - a.window;
-    if (ws < 0) ws = 0;
-    const int alen = seq - ws;
-    int ch = (alen + a.nc - 1) / a.nc;
-    ch = (ch + 31) / 32 * 32;
-    const int nchunks = (alen + ch - 1) / ch;
+    const int nchunks = attn_range(a.params->pos, a.window, a.nc).nchunks;
     const float* pml = a.part_ml + (int64_t)h * a.nc * 2;
     float mk[4], lk[4];
     float M = -INFINITY;
@@ -272,50 +344,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(const AttnArgs a) {
         res = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
         *(float4*)(a.out + (int64_t)h * HD + d4 * 4) = res;
     }
-    if (a.tab_out) {
-        // the head's part of the activation table of out, for the output projection: lanes
-        // 4k .. 4k + 3 hold the 16 elements of half k (one float4 each, HD / 4 lanes in all)
-        __shared__ __attribute__((aligned(16))) uint8_t stg[HD / 16][3][16];
-        const bool live = lane < HD / 4;
-        const float4 v = res;
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        float sum = (v.x + v.y) + (v.z + v.w);
-#pragma unroll
-        for (int o = 1; o < 4; o <<= 1) {
-            amax = fmaxf(amax, __shfl_xor(amax, o));
-            sum += __shfl_xor(sum, o);
-        }
-        float sc, qinv;
-        half_scale(amax, sc, qinv);
-        const int hl = lane >> 2, by = lane & 3;  // element 4 by + j of half hl, j = component
-        if (live) {
-            const float c4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                int b2, b1, b0;
-                digits3(quant_x(c4[j], qinv), b2, b1, b0);
-                stg[hl][0][4 * j + by] = (uint8_t)b2;
-                stg[hl][1][4 * j + by] = (uint8_t)b1;
-                stg[hl][2][4 * j + by] = (uint8_t)b0;
-            }
-        }
-        __syncthreads();
-        const int n = a.nh * HD;
-        uint4* tab = (uint4*)a.tab_out;
-        if (lane < (HD / 16) * 3) {
-            const int k = lane / 3, d = lane % 3;
-            int entry0, byte, stat, half;
-            tab_pos(h * HD + 16 * k, n, entry0, byte, stat, half);
-            tab[entry0 + d] = *(const uint4*)&stg[k][d][0];
-        }
-        if (live && by == 0) {
-            int entry0, byte, stat, half;
-            tab_pos(h * HD + 16 * hl, n, entry0, byte, stat, half);
-            float* st = (float*)(tab + stat);
-            st[half] = sc;
-            st[2 + half] = sum;
-        }
-    }
+    if (a.tab_out) merge_emit_table<HD>(a, h, lane, res);
 }
 
 bool attn_fast_supported(int head_dim, int group, int max_seq) {
@@ -371,6 +400,14 @@ hipError_t launch_attn_partial(const AttnArgs& a, size_t lds, hipStream_t st) {
 }
 
 hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t st) {
+    if (a.nc <= 32) {
+        switch (a.hd) {
+            case 64: k_attn_merge_fast<64, 32><<<a.nh, 64, 0, st>>>(a); break;
+            case 128: k_attn_merge_fast<128, 32><<<a.nh, 64, 0, st>>>(a); break;
+            default: k_attn_merge_fast<256, 32><<<a.nh, 64, 0, st>>>(a); break;
+        }
+        return hipGetLastError();
+    }
     switch (a.hd) {
         case 64: k_attn_merge<64><<<a.nh, 64, 0, st>>>(a); break;
         case 128: k_attn_merge<128><<<a.nh, 64, 0, st>>>(a); break;

@@ -23,6 +23,20 @@ struct AttnArgs {
     void* tab_out;         // optional: activation table of out (nh * hd elements, a multiple of 256)
 };
 
+// The attended positions [ws, pos] of a step split into nchunks chunks of ch positions (ch =
+// ceil(len / nc) rounded up to 32; the last chunk may be shorter): the split of the attention
+// kernel and of every reader of its partials.
+struct AttnRange { int ws, ch, nchunks; };
+__host__ __device__ __forceinline__ AttnRange attn_range(int pos, int window, int nc) {
+    const int seq = pos + 1;
+    int ws = seq - window;
+    if (ws < 0) ws = 0;
+    const int alen = seq - ws;
+    int ch = (alen + nc - 1) / nc;
+    ch = (ch + 31) / 32 * 32;
+    return AttnRange{ws, ch, (alen + ch - 1) / ch};
+}
+
 bool attn_fast_supported(int head_dim, int group, int max_seq);
 int attn_chunks(int n_kv, int max_seq, int n_cu);
 size_t attn_lds_bytes(int head_dim, int group, int nc, int max_seq);
