@@ -450,6 +450,10 @@ struct EpiSeg {
     float* out;
     const float* bias;
     const float* resid;
+    // pre: this thread's residual (pr) and consumer norm weight (pw) of a residual add were
+    // loaded ahead (the matrix-core kernels load them for a workgroup's first tile with its table)
+    int pre;
+    float pr, pw;
 };
 
 __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, const float* part, float* red, int nslice,
@@ -528,10 +532,15 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
         float y = 0.0f;
         for (int sl = 0; sl < nslice; sl++) y += part[sl * T + t];
         if (epi == EPI_RESID) {
-            const float xr = sg.resid[r] + y;
+            const float xr = (sg.pre ? sg.pr : sg.resid[r]) + y;
             sg.out[r] = xr;
             tq = xr * xr;
-            tv = a.tab_w ? xr * (a.tab_kind ? 1.0f + a.tab_w[r] : a.tab_w[r]) : xr;
+            if (a.tab_w) {
+                const float w = sg.pre ? sg.pw : a.tab_w[r];
+                tv = xr * (a.tab_kind ? 1.0f + w : w);
+            } else {
+                tv = xr;
+            }
         } else if (epi == EPI_V) {
             if (sg.bias) y = y + sg.bias[r];
             a.vc[(int64_t)a.params->cur_len * a.kvdim + r] = y;
@@ -1039,6 +1048,10 @@ struct MfCtx {
     uint32_t rb, kboff;
     float xs;
     int kb0, q, m, lane, wave, nw, ltpu, T_slots, ufirst, ustride, items;
+    // residual and norm weight of row 16 * tile + (thread & 15) of the first tile (pre_on: it is a
+    // residual add), loaded with the table
+    int pre_on;
+    float pre_r, pre_w;
 };
 
 // issue the loads of chunk kb0 + c of the tile at offset off of W into r
@@ -1091,7 +1104,8 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
                             si == 0 ? a.seg[0].epi : si == 1 ? a.seg[1].epi : a.seg[2].epi,
                             si == 0 ? a.seg[0].out : si == 1 ? a.seg[1].out : a.seg[2].out,
                             si == 0 ? a.seg[0].bias : si == 1 ? a.seg[1].bias : a.seg[2].bias,
-                            si == 0 ? a.seg[0].resid : si == 1 ? a.seg[1].resid : a.seg[2].resid};
+                            si == 0 ? a.seg[0].resid : si == 1 ? a.seg[1].resid : a.seg[2].resid,
+                            x.pre_on && (ti >> x.ltpu) == 0, x.pre_r, x.pre_w};
             epilogue(a, es, x.part, x.red, x.nw, MF_TILE, x.T_slots, row0, x.wave, x.lane, best);
             __syncthreads();
         }
@@ -1151,6 +1165,22 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     const float* sp = sm ? a.xssq : (const float*)mf_tab_dummy;
 #pragma unroll
     for (int k = 0; k < TSL; k++) tsq[k] = sp[sm * (x.kb0 * 16 + min(x.lane + 64 * k, KC * 16 - 1))];
+    // the residual and the consumer's norm weight of the first tile's rows, when it is a residual
+    // add: written by earlier launches, so they go out with the table rather than after the last
+    // weights (where they would add a round trip to the epilogue)
+    {
+        const uint8_t* Wu;
+        int rows_u, row0_u, si_u;
+        mf_tile_of(a, x.ufirst, 0, Wu, rows_u, row0_u, si_u);
+        const float* rs = si_u == 0 ? a.seg[0].resid : si_u == 1 ? a.seg[1].resid : a.seg[2].resid;
+        const int epi_u = si_u == 0 ? a.seg[0].epi : si_u == 1 ? a.seg[1].epi : a.seg[2].epi;
+        x.pre_on = (!a.glu && epi_u == EPI_RESID && rs != nullptr && x.items > 0) ? 1 : 0;
+        const int rr = min(row0_u + (int)(threadIdx.x & 15), rows_u - 1);
+        const float* rp = x.pre_on ? rs + rr : (const float*)mf_tab_dummy;
+        const float* wp = (x.pre_on && a.tab_w) ? a.tab_w + rr : (const float*)mf_tab_dummy;
+        x.pre_r = *rp;
+        x.pre_w = *wp;
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     Raw ring[RING];
