@@ -792,10 +792,25 @@ __device__ __forceinline__ void mf_issue(MfQ4K& r, const uint8_t* __restrict__ W
     r.qb = *(const uint4*)(p + 80 + 16 * q);   // group q + 4
 }
 // the same fields from a LAYOUT_TILES region (lane = 16 q + n)
+// Weight loads of the tile-interleaved layout, with the non-temporal hint: every weight byte is read
+// once per step, so they need not displace the activation tables, the epilogue operands and the
+// kernels' code from the caches.
+typedef uint32_t nt_u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 nt16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 nt8(const uint8_t* p) {
+    const nt_u2 v = __builtin_nontemporal_load((const nt_u2*)p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t nt4(const uint8_t* p) { return __builtin_nontemporal_load((const uint32_t*)p); }
+__device__ __forceinline__ uint16_t nt2(const uint8_t* p) { return __builtin_nontemporal_load((const uint16_t*)p); }
+
 __device__ __forceinline__ void mf_issue_tiles(MfQ4K& r, const uint8_t* __restrict__ reg, int lane, int n) {
-    r.hdr = *(const uint4*)(reg + 2048 + 16 * n);
-    r.qa = *(const uint4*)(reg + 16 * lane);
-    r.qb = *(const uint4*)(reg + 1024 + 16 * lane);
+    r.hdr = nt16(reg + 2048 + 16 * n);
+    r.qa = nt16(reg + 16 * lane);
+    r.qb = nt16(reg + 1024 + 16 * lane);
 }
 
 // fragment of one half-group from its 8 qs bytes: dword j = elements j, 4+j, 8+j, 12+j
@@ -899,11 +914,11 @@ __device__ __forceinline__ float mf_compute(const MfQ6K& r, const v4i* A, const 
 // Q6_K from a LAYOUT_TILES region: the lane's ql, qh and scale bytes are 4-byte aligned there
 struct MfQ6KT { uint4 la, lb, h; uint32_t s, d; };
 __device__ __forceinline__ void mf_issue_tiles(MfQ6KT& r, const uint8_t* __restrict__ reg, int lane, int n) {
-    r.la = *(const uint4*)(reg + 16 * lane);           // ql 16q .. 16q + 15
-    r.lb = *(const uint4*)(reg + 1024 + 16 * lane);    // ql 64 + 16q ..
-    r.h = *(const uint4*)(reg + 2048 + 16 * lane);     // qh 8q .. 8q + 7, qh 32 + 8q .. 32 + 8q + 7
-    r.s = *(const uint32_t*)(reg + 3072 + 4 * lane);   // scales 2q, 2q + 1, 8 + 2q, 9 + 2q
-    r.d = *(const uint16_t*)(reg + 3328 + 2 * n);
+    r.la = nt16(reg + 16 * lane);         // ql 16q .. 16q + 15
+    r.lb = nt16(reg + 1024 + 16 * lane);  // ql 64 + 16q ..
+    r.h = nt16(reg + 2048 + 16 * lane);   // qh 8q .. 8q + 7, qh 32 + 8q .. 32 + 8q + 7
+    r.s = nt4(reg + 3072 + 4 * lane);     // scales 2q, 2q + 1, 8 + 2q, 9 + 2q
+    r.d = nt2(reg + 3328 + 2 * n);
 }
 
 __device__ __forceinline__ float mf_compute(const MfQ6KT& r, const v4i* A, const f32x4& sA, const f32x4& sB, int,
@@ -933,11 +948,11 @@ template <> struct MfPick<FLLM_TYPE_Q6_K, true> { using Raw = MfQ6KT; };
 // the lane's two block scales (groups q and q + 4) share one dword.
 struct MfQ8T { uint4 a0, a1, b0, b1; uint32_t d; };
 __device__ __forceinline__ void mf_issue_tiles(MfQ8T& r, const uint8_t* __restrict__ reg, int lane, int n) {
-    r.a0 = *(const uint4*)(reg + 16 * lane);         // group q, elements 0 .. 15
-    r.a1 = *(const uint4*)(reg + 1024 + 16 * lane);  // group q, elements 16 .. 31
-    r.b0 = *(const uint4*)(reg + 2048 + 16 * lane);  // group q + 4
-    r.b1 = *(const uint4*)(reg + 3072 + 16 * lane);
-    r.d = *(const uint32_t*)(reg + 4096 + 16 * n + 4 * (lane >> 4));
+    r.a0 = nt16(reg + 16 * lane);         // group q, elements 0 .. 15
+    r.a1 = nt16(reg + 1024 + 16 * lane);  // group q, elements 16 .. 31
+    r.b0 = nt16(reg + 2048 + 16 * lane);  // group q + 4
+    r.b1 = nt16(reg + 3072 + 16 * lane);
+    r.d = nt4(reg + 4096 + 16 * n + 4 * (lane >> 4));
 }
 __device__ __forceinline__ v4i mf_v4i(const uint4& u) {
     v4i r = {(int)u.x, (int)u.y, (int)u.z, (int)u.w};
@@ -962,10 +977,10 @@ template <> struct MfPick<FLLM_TYPE_Q8_0, true> { using Raw = MfQ8T; };
 // bits of fragment dword j of half h are then (H >> (4 h + j)) & 0x01010101, shifted to bit 4.
 struct MfQ5KT { uint4 hdr, qa, qb; uint2 h; };
 __device__ __forceinline__ void mf_issue_tiles(MfQ5KT& r, const uint8_t* __restrict__ reg, int lane, int n) {
-    r.qa = *(const uint4*)(reg + 16 * lane);          // qs of group q
-    r.qb = *(const uint4*)(reg + 1024 + 16 * lane);   // qs of group q + 4
-    r.h = *(const uint2*)(reg + 2048 + 8 * lane);     // high bits of groups q and q + 4
-    r.hdr = *(const uint4*)(reg + 2560 + 16 * n);     // d, dmin, scales
+    r.qa = nt16(reg + 16 * lane);         // qs of group q
+    r.qb = nt16(reg + 1024 + 16 * lane);  // qs of group q + 4
+    r.h = nt8(reg + 2048 + 8 * lane);     // high bits of groups q and q + 4
+    r.hdr = nt16(reg + 2560 + 16 * n);    // d, dmin, scales
 }
 // q4_frag with bit 4 of each byte from the regrouped high bits of half h
 __device__ __forceinline__ v4i q5_frag(uint32_t w0, uint32_t w1, uint32_t H, int h) {
