@@ -91,6 +91,14 @@ __device__ __forceinline__ void attn_pv(float4* acc, const float4& vr, int t, in
 // G = query heads per kv head. Rows of the chunk go in blocks of BLK = 4 rows per lane; the K and V
 // rows of the first two blocks are loaded together up front (row indices clamped to the chunk, so
 // every load is unconditional and all are in flight at once), later blocks in a loop.
+// K / V cache rows, read once per step: non-temporal, so that they do not displace the weights'
+// neighbours in L2 (activation tables, epilogue operands, code)
+typedef float kv_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 kv_ld(const float* p) {
+    const kv_f4 v = __builtin_nontemporal_load((const kv_f4*)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 template <int HD, int G>
 __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     constexpr int LPR = HD / 4;    // lanes per K/V row
@@ -128,13 +136,13 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     // ---- K and V rows of blocks 0 and 1 -------------------------------------------------------
     float4 kA[NP], kB[NP], vA[NP], vB[NP];
 #pragma unroll
-    for (int u = 0; u < NP; u++) kA[u] = *(const float4*)(kbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
+    for (int u = 0; u < NP; u++) kA[u] = kv_ld(kbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
 #pragma unroll
-    for (int u = 0; u < NP; u++) kB[u] = *(const float4*)(kbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
+    for (int u = 0; u < NP; u++) kB[u] = kv_ld(kbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
 #pragma unroll
-    for (int u = 0; u < NP; u++) vA[u] = *(const float4*)(vbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
+    for (int u = 0; u < NP; u++) vA[u] = kv_ld(vbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
 #pragma unroll
-    for (int u = 0; u < NP; u++) vB[u] = *(const float4*)(vbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
+    for (int u = 0; u < NP; u++) vB[u] = kv_ld(vbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
 
     // ---- scores ---------------------------------------------------------------------------------
 #pragma unroll
@@ -145,7 +153,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     for (int b0 = 2 * BLK; b0 < len; b0 += BLK) {
         float4 kr[NP];
 #pragma unroll
-        for (int u = 0; u < NP; u++) kr[u] = *(const float4*)(kbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
+        for (int u = 0; u < NP; u++) kr[u] = kv_ld(kbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
 #pragma unroll
         for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kr[u], b0 + r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
     }
@@ -178,7 +186,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     for (int b0 = 2 * BLK; b0 < len; b0 += BLK) {
         float4 vr[NP];
 #pragma unroll
-        for (int u = 0; u < NP; u++) vr[u] = *(const float4*)(vbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
+        for (int u = 0; u < NP; u++) vr[u] = kv_ld(vbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
 #pragma unroll
         for (int u = 0; u < NP; u++) attn_pv<G>(acc, vr[u], b0 + r0 + u * RPP, len, sc, ch);
     }
