@@ -343,6 +343,31 @@ template <int NR> struct Log2;
 template <> struct Log2<4> { static constexpr int v = 2; };
 template <> struct Log2<8> { static constexpr int v = 3; };
 
+// Weight loads with the non-temporal hint: every weight byte is read once per step, so the weight
+// stream need not displace the activation tables, the epilogue operands and the kernels' code from
+// the caches. nt16a / nt8a: 4-byte aligned (raw GGUF rows).
+typedef uint32_t nt_u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t nt_u4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t nt_u2a __attribute__((ext_vector_type(2), aligned(4)));
+__device__ __forceinline__ uint4 nt16(const uint8_t* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 nt16a(const uint8_t* p) {
+    const nt_u4a v = __builtin_nontemporal_load((const nt_u4a*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 nt8(const uint8_t* p) {
+    const nt_u2 v = __builtin_nontemporal_load((const nt_u2*)p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint2 nt8a(const uint8_t* p) {
+    const nt_u2a v = __builtin_nontemporal_load((const nt_u2a*)p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t nt4(const uint8_t* p) { return __builtin_nontemporal_load((const uint32_t*)p); }
+__device__ __forceinline__ uint16_t nt2(const uint8_t* p) { return __builtin_nontemporal_load((const uint16_t*)p); }
+
 // ---- row batches staged through LDS -----------------------------------------------------------
 // A wave's slice of a row (its S group columns) is a contiguous byte range of the block stream.
 // The wave copies the 16-byte-aligned chunks covering it into its own LDS area with fully
@@ -381,7 +406,7 @@ __device__ __forceinline__ void issue_batch(Batch<T, NR>& bt, const uint8_t* __r
 #pragma unroll
             for (int k = 0; k < St::CPL; k++) {
                 int ch = lane + 64 * k;
-                if (ch < bt.n16[rr]) bt.c[rr][k] = src[ch];
+                if (ch < bt.n16[rr]) bt.c[rr][k] = nt16((const uint8_t*)(src + ch));
             }
         }
     }
@@ -787,26 +812,11 @@ __device__ __forceinline__ float mf_total(const v4i& D) {
 struct MfQ4K { uint4 hdr, qa, qb; };
 __device__ __forceinline__ void mf_issue(MfQ4K& r, const uint8_t* __restrict__ W, uint32_t off, int c, int, int q) {
     const uint8_t* p = W + off + (uint32_t)(c * 144);
-    r.hdr = *(const uint4*)p;
-    r.qa = *(const uint4*)(p + 16 + 16 * q);   // group q
-    r.qb = *(const uint4*)(p + 80 + 16 * q);   // group q + 4
+    r.hdr = nt16(p);
+    r.qa = nt16(p + 16 + 16 * q);   // group q
+    r.qb = nt16(p + 80 + 16 * q);   // group q + 4
 }
 // the same fields from a LAYOUT_TILES region (lane = 16 q + n)
-// Weight loads of the tile-interleaved layout, with the non-temporal hint: every weight byte is read
-// once per step, so they need not displace the activation tables, the epilogue operands and the
-// kernels' code from the caches.
-typedef uint32_t nt_u2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint4 nt16(const uint8_t* p) {
-    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint2 nt8(const uint8_t* p) {
-    const nt_u2 v = __builtin_nontemporal_load((const nt_u2*)p);
-    return make_uint2(v.x, v.y);
-}
-__device__ __forceinline__ uint32_t nt4(const uint8_t* p) { return __builtin_nontemporal_load((const uint32_t*)p); }
-__device__ __forceinline__ uint16_t nt2(const uint8_t* p) { return __builtin_nontemporal_load((const uint16_t*)p); }
-
 __device__ __forceinline__ void mf_issue_tiles(MfQ4K& r, const uint8_t* __restrict__ reg, int lane, int n) {
     r.hdr = nt16(reg + 2048 + 16 * n);
     r.qa = nt16(reg + 16 * lane);
@@ -853,21 +863,21 @@ __device__ __forceinline__ void mf_issue(MfQ6K& r, const uint8_t* __restrict__ W
                                          int q) {
     const uint8_t* blk = W + off + (uint32_t)(c * 210);
     const uint8_t* p = blk - mis;
-    u32x4 t = *(const u32x4a*)(p + 16 * q);
+    uint4 t = nt16a(p + 16 * q);
     r.la[0] = t.x; r.la[1] = t.y; r.la[2] = t.z; r.la[3] = t.w;
-    r.la[4] = *(const uint32_t*)(p + 16 + 16 * q);
-    t = *(const u32x4a*)(p + 64 + 16 * q);
+    r.la[4] = nt4(p + 16 + 16 * q);
+    t = nt16a(p + 64 + 16 * q);
     r.lb[0] = t.x; r.lb[1] = t.y; r.lb[2] = t.z; r.lb[3] = t.w;
-    r.lb[4] = *(const uint32_t*)(p + 80 + 16 * q);
-    u32x2 h = *(const u32x2a*)(p + 128 + 8 * q);
+    r.lb[4] = nt4(p + 80 + 16 * q);
+    uint2 h = nt8a(p + 128 + 8 * q);
     r.ha[0] = h.x; r.ha[1] = h.y;
-    r.ha[2] = *(const uint32_t*)(p + 136 + 8 * q);
-    h = *(const u32x2a*)(p + 160 + 8 * q);
+    r.ha[2] = nt4(p + 136 + 8 * q);
+    h = nt8a(p + 160 + 8 * q);
     r.hb[0] = h.x; r.hb[1] = h.y;
-    r.hb[2] = *(const uint32_t*)(p + 168 + 8 * q);
-    r.sa = *(const uint16_t*)(blk + 192 + 2 * q);  // scales 2q, 2q + 1
-    r.sb = *(const uint16_t*)(blk + 200 + 2 * q);  // scales 2q + 8, 2q + 9
-    r.d = *(const uint16_t*)(blk + 208);
+    r.hb[2] = nt4(p + 168 + 8 * q);
+    r.sa = nt2(blk + 192 + 2 * q);  // scales 2q, 2q + 1
+    r.sb = nt2(blk + 200 + 2 * q);  // scales 2q + 8, 2q + 9
+    r.d = nt2(blk + 208);
 }
 
 // fragment of one half-group: 8 ql bytes (2 dwords) and the 4 qh bytes of those 16 elements;

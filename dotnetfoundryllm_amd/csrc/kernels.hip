@@ -39,6 +39,9 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// weight rows are read once per step: non-temporal loads keep them from displacing what is reused
+typedef uint32_t kf_u4 __attribute__((ext_vector_type(4)));
+
 template <int T>
 __global__ __launch_bounds__(256) void k_gemv_f(const uint8_t* __restrict__ W, int64_t rows, int64_t cols,
                                                  const float* __restrict__ x, float* y, const float* residual) {
@@ -52,7 +55,8 @@ __global__ __launch_bounds__(256) void k_gemv_f(const uint8_t* __restrict__ W, i
     const float4* x4 = (const float4*)x;
     float acc = 0.0f;
     for (int64_t v = lane; v < nvec; v += 64) {
-        uint4 u = rp[v];
+        const kf_u4 uv = __builtin_nontemporal_load((const kf_u4*)(rp + v));
+        const uint4 u = make_uint4(uv.x, uv.y, uv.z, uv.w);
         if constexpr (T == FLLM_TYPE_F32) {
             float4 xv = x4[v];
             acc = fmaf(__uint_as_float(u.x), xv.x, acc);
