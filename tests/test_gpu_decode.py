@@ -278,6 +278,43 @@ def test_llama3_8b_shape_two_layers(ctx):
         m.close()
 
 
+@pytest.mark.parametrize("name", ["qwen2-7b-q5k", "gemma2-9b-q8"])
+def test_full_width_shapes_two_layers(ctx, name):
+    """The other full-size configurations at full width, two decoder layers: Qwen2-7B (dim 3584,
+    28/4 heads, FFN 18944, Q5_K with q/k/v bias, vocab 152064) and Gemma-2-9B (16/8 heads x 256,
+    GeGLU FFN 14336, Q8_0, BF16 embedding as the tied LM head, attention and final softcaps,
+    vocab 256000). A 24-token prompt through the batched prefill, then 4 decode steps: logits,
+    K/V and greedy tokens against the oracle."""
+    cfg, desc, tensors = synthetic(name, n_layers=2)
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m, 64)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors, 64)
+    prompt = F.synth_tokens(cfg["seed"], 6, desc.vocab, 24)
+    try:
+        fwd.prefill(prompt[:-1], 0, kv)
+        for pos, t in enumerate(prompt[:-1]):
+            assert orc.forward(int(t), pos) == 0
+        for l in range(desc.n_layers):
+            assert O.normwise_rel_err(kv.get_keys(l), orc.kv(l, 0)) <= TOL, l
+            assert O.normwise_rel_err(kv.get_values(l), orc.kv(l, 1)) <= TOL, l
+        nxt_d = nxt_o = int(prompt[-1])
+        for pos in range(23, 27):
+            fwd.forward(nxt_d, pos, kv)
+            assert orc.forward(nxt_o, pos) == 0
+            lg = orc.logits()
+            err = O.normwise_rel_err(fwd.logits, lg)
+            print(f"{name} pos {pos}: normwise rel err {err:.2e}")
+            assert err <= TOL
+            nxt_d = fwd.sample_greedy()
+            nxt_o = int(O.lib.orc_argmax(O.fp(lg), lg.size))
+            assert nxt_d == nxt_o
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
+
+
 def test_profile_mode_reports_kernels(ctx):
     cfg, desc, tensors = synthetic("test-llama")
     m = device_model(ctx, desc, tensors)
@@ -375,8 +412,8 @@ def test_device_greedy_loop_errors(ctx):
 
 
 def test_long_context_windowed_attention(ctx):
-    """Mistral-style window over a 3000-position context with 8 KV heads: the attention splits into
-    47 chunks of 64 positions whose partials are merged by the last chunk; logits, K/V and greedy
+    """Mistral-style 1000-position window over a 3000-position context with 8 KV heads: the window
+    is split into position chunks whose partials the merge kernel combines; logits, K/V and greedy
     tokens against the oracle."""
     from dotnetfoundryllm_amd.configs import _cfg, _types
     cfg = _cfg("long-mistral", N.ARCH_MISTRAL, 1, 512, 8, 8, 512, 512, 4096, 10000.0,
