@@ -145,6 +145,8 @@ struct fllm_seq {
     // batched prefill scratch for chunks of up to pf_cap tokens (allocated on first use)
     int pf_cap = 0, pf_ldx = 0;
     float *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_gu = nullptr, *pf_tmp = nullptr;
+    float* pf_part = nullptr;  // K-split partial products of the short GEMM launches
+    size_t pf_part_cap = 0;
     int* pf_tok = nullptr;
 };
 
@@ -1194,10 +1196,13 @@ static hipError_t prefill_alloc(fllm_seq* s) {
     PF_ALLOC(s->pf_tmp, C * H);
     PF_ALLOC(s->pf_xn, C * ldx);
     PF_ALLOC(s->pf_tok, C);
+    const size_t part_cap = 3 * C * std::max(H, (size_t)(m.qdim + 2 * m.kvdim));
+    PF_ALLOC(s->pf_part, part_cap);
 #undef PF_ALLOC
     if (e == hipSuccess) {
         s->pf_cap = cap;
         s->pf_ldx = (int)ldx;
+        s->pf_part_cap = part_cap;
     }
     return e;
 }
@@ -1212,6 +1217,8 @@ static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w,
     g.K = (int)w[0]->cols;
     g.T = T;
     g.add = add ? 1 : 0;
+    g.part = s->pf_part;
+    g.part_cap = s->pf_part_cap;
     double bytes = 0.0;
     for (int i = 0; i < n; i++) {
         // one launch per run of tile-interleaved matrices, or of GGUF-row matrices of one type

@@ -369,8 +369,10 @@ __device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, i
         }
         if (wlive && k0 + 32 * wgrp < a.K) PfW<WT>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
     };
-    fetch(0);
-    for (int k0 = 0; k0 < a.K; k0 += PF_BK) {
+    // this workgroup's part of K (the whole row unless the launch splits K)
+    const int kb = (int)blockIdx.z * a.kpart, ke = kb + a.kpart < a.K ? kb + a.kpart : a.K;
+    fetch(kb);
+    for (int k0 = kb; k0 < ke; k0 += PF_BK) {
         __syncthreads();  // the previous step's operands have been read
 #pragma unroll
         for (int i = 0; i < XP; i++) {
@@ -391,7 +393,7 @@ __device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, i
             for (int i = 0; i < 8; i++) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
         }
         // the next step's global loads fly while this step multiplies
-        if (k0 + PF_BK < a.K) fetch(k0 + PF_BK);
+        if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < PF_BK; kk += 16) {
@@ -422,13 +424,29 @@ __device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, i
                 const int t = t0 + WM * wm + 16 * i + 4 * (lane >> 4) + e;
                 const int n = n0 + 64 * wn + 16 * j + (lane & 15);
                 if (t < a.T && n < sg.N) {
-                    float* p = sg.y + (size_t)t * sg.ldy + n;
-                    *p = a.add ? *p + acc[i][j][e] : acc[i][j][e];
+                    if (blockIdx.z == 0) {
+                        float* p = sg.y + (size_t)t * sg.ldy + n;
+                        *p = a.add ? *p + acc[i][j][e] : acc[i][j][e];
+                    } else {
+                        // K part z > 0: its slice of the scratch, at y's place in the shared rows
+                        const size_t col = (size_t)(sg.y - a.seg[0].y);
+                        a.part[(size_t)(blockIdx.z - 1) * a.T * sg.ldy + (size_t)t * sg.ldy + col + n] = acc[i][j][e];
+                    }
                 }
             }
 }
 
 typedef void (*PfGemmKernel)(const PfGemm);
+
+// y[i] += part[0][i] + part[1][i] + ... (in that order) over n = T * ldy values
+__global__ __launch_bounds__(256) void k_pf_split_add(float* __restrict__ y, const float* __restrict__ part, int nsp,
+                                                      int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        float v = y[i];
+        for (int z = 0; z < nsp; z++) v += part[(int64_t)z * n + i];
+        y[i] = v;
+    }
+}
 
 // workgroup (x, y): column tile x of the launch's segments, token tile y
 __device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
@@ -510,8 +528,33 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
     hipError_t e = pf_lds_attr((const void*)k, lds);
     if (e != hipSuccess) return e;
     const int bm = tall ? 128 : 64;
-    dim3 grid((unsigned)col_tiles, (unsigned)((a.T + bm - 1) / bm));
+    // a short grid splits K (parts of whole 512-element multiples) when the segments fill the rows
+    // of one buffer side by side and the scratch holds the extra parts
+    int nsplit = 1;
+    if (!tall && a.part != nullptr) {
+        const int64_t base = col_tiles * ((a.T + bm - 1) / bm), want = 2 * (int64_t)(n_cu > 0 ? n_cu : 256);
+        bool side_by_side = true;
+        int64_t off = 0;
+        for (int i = 0; i < a.nseg; i++) {
+            const PfSeg& g = a.seg[i];
+            side_by_side = side_by_side && g.ldy == a.seg[0].ldy && g.y - a.seg[0].y == off;
+            off += g.N;
+        }
+        side_by_side = side_by_side && off == a.seg[0].ldy;
+        while (side_by_side && nsplit < 4 && base * nsplit < want && a.K % (512 * nsplit) == 0 &&
+               (size_t)(2 * nsplit - 1) * (size_t)a.T * (size_t)a.seg[0].ldy <= a.part_cap)
+            nsplit *= 2;
+    }
+    a.nsplit = nsplit;
+    a.kpart = a.K / nsplit;
+    dim3 grid((unsigned)col_tiles, (unsigned)((a.T + bm - 1) / bm), (unsigned)nsplit);
     k<<<grid, 256, lds, st>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess || nsplit == 1) return e;
+    const int64_t n = (int64_t)a.T * a.seg[0].ldy;
+    int blocks = (int)((n + 255) / 256);
+    if (blocks > 2048) blocks = 2048;
+    k_pf_split_add<<<blocks, 256, 0, st>>>(a.seg[0].y, a.part, nsplit - 1, n);
     return hipGetLastError();
 }
 
