@@ -519,8 +519,10 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         g.tiles = (g.N + PF_BN - 1) / PF_BN;
         col_tiles += g.tiles;
     }
-    // 128-token tiles unless that leaves fewer than two workgroups per CU
-    const bool tall = col_tiles * ((a.T + 127) / 128) >= 2 * (int64_t)(n_cu > 0 ? n_cu : 256);
+    // 128-token tiles only for grids of at least four of them per CU: the 64-token tiles fit three
+    // workgroups per CU (128-token ones two), and their finer grain wins below that (gate/up at
+    // 511 tokens: 896 tiles of 128 tokens ran 3% slower than 1792 of 64)
+    const bool tall = col_tiles * ((a.T + 127) / 128) >= 4 * (int64_t)(n_cu > 0 ? n_cu : 256);
     PfGemmKernel k;
     if (tiles) k = tall ? k_pf_gemm_tiles<128> : k_pf_gemm_tiles<64>;
     else k = tall ? pf_rows_kernel<128>(a.seg[0].type) : pf_rows_kernel<64>(a.seg[0].type);
