@@ -1025,11 +1025,12 @@ template <> struct MfPick<FLLM_TYPE_Q5_K, true> { using Raw = MfQ5KT; };
 
 // Persistent workgroup body of the MFMA variant for weight type T. The launch's rows form units:
 // one 16-row tile, or for GLU the gate and up tiles of the same 16 rows. Workgroup w takes units
-// w, w + grid, w + 2 grid, ...; each of its nw waves covers KC = NB / nw consecutive chunks of every
-// row, so all waves walk the same (tile, chunk) item sequence: item i is chunk i % KC of the
-// workgroup's tile i / KC. Items stream through a ring of chunk loads in flight (MfRing) that runs
-// across tile and unit boundaries; the first loads go out before the activation prologue. A lane's
-// load addresses are its tile row's offset (computed once per tile) plus constants; with
+// w, w + grid, w + 2 grid, ...; each of its nw waves covers KC consecutive chunks of every row
+// (NB = nw KC chunks, or fewer for a ragged row), so all waves walk the same (tile, chunk) item
+// sequence: item i is chunk i % KC of the workgroup's tile i / KC. Items stream through a ring of
+// chunk loads in flight (MfRing) that runs across tile and unit boundaries; the first loads go out
+// before the activation prologue. A lane's load addresses are its tile row's offset (computed once
+// per tile) plus constants; with
 // LAYOUT_TILES (IL) the tile offset is the same for all lanes of a wave and each load instruction
 // of a wave reads one contiguous piece.
 constexpr int MF_RING = 4;
@@ -1073,6 +1074,7 @@ struct MfCtx {
     uint32_t rb, kboff;
     float xs;
     int kb0, q, m, lane, wave, nw, ltpu, T_slots, ufirst, ustride, items;
+    int cmax;  // ragged rows: chunks kb0 + c with c > cmax lie past the row (padding of the last wave)
     // residual and norm weight of row 16 * tile + (thread & 15) of the first tile (pre_on: it is a
     // residual add), loaded with the table
     int pre_on;
@@ -1080,9 +1082,11 @@ struct MfCtx {
 };
 
 // issue the loads of chunk kb0 + c of the tile at offset off of W into r
-template <int T, bool IL>
+template <int T, bool IL, bool RAGGED = false>
 __device__ __forceinline__ void mf_load(typename MfPick<T, IL>::Raw& r, const uint8_t* W, uint32_t off, int c,
                                         const MfCtx& x) {
+    // ragged rows: a padding chunk re-reads the row's last one (its activations are zero)
+    if constexpr (RAGGED) c = c < x.cmax ? c : x.cmax;
     if constexpr (IL) mf_issue_tiles(r, W + off + (uint32_t)(c * MF_TILE * mf_chunk_bytes(T)), x.lane, x.m);
     else mf_issue(r, W, off, c, ((x.kb0 + c) & 1) * 2, x.q);
 }
@@ -1091,7 +1095,7 @@ __device__ __forceinline__ void mf_load(typename MfPick<T, IL>::Raw& r, const ui
 // slot is reloaded with item i + RING. Every item but the last RING of the workgroup refills,
 // and the choice is a compile-time constant of the unrolled item position, so the number of loads
 // in flight at every wait is known at compile time.
-template <int T, int KC, bool IL, bool REFILL>
+template <int T, int KC, bool IL, bool REFILL, bool RAGGED = false>
 __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typename MfPick<T, IL>::Raw* ring, int i, int r,
                                         float& y, uint32_t& offr, const uint8_t*& Wr, unsigned long long& best) {
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
@@ -1108,7 +1112,7 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
     if (REFILL) {
         const int cn = (r + RING) & (KC - 1);
         if (cn == 0) offr = mf_tile_base<IL>(a, x.ufirst, x.ustride, (i + RING) >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
-        mf_load<T, IL>(ring[slot], Wr, offr, cn, x);
+        mf_load<T, IL, RAGGED>(ring[slot], Wr, offr, cn, x);
     }
     // keep each item's fragment reads next to its MFMAs
     __builtin_amdgcn_sched_barrier(0);
@@ -1139,7 +1143,10 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
 
 // TABIN: the input is an activation table (XIN_TAB); otherwise a vector, quantized here. The
 // workgroup is number wg of ng that share units [u0, u0 + nu) of the launch.
-template <int T, int KC, bool TABIN, bool IL>
+// RAGGED: the row's NB chunks do not split evenly: the nw waves of KC chunks cover nw * KC >= NB,
+// and the last wave's chunks past the row have zero activations (their weight loads re-read the
+// row's last chunk), so they add nothing.
+template <int T, int KC, bool TABIN, bool IL, bool RAGGED = false>
 __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int wg, int ng) {
     using Raw = typename MfPick<T, IL>::Raw;
     constexpr int CB = mf_chunk_bytes(T);
@@ -1154,15 +1161,17 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     x.q = x.lane >> 4;
     x.m = x.lane & 15;
     const bool a_live = (x.m >> 2) == x.q && (x.m & 3) < 3;  // A row m = 4Q' + d lives in quarter Q'
-    const int NB = a.G / 8;            // chunks per row (NB == nw * KC)
+    const int NB = a.G / 8;            // chunks per row (NB == nw * KC unless RAGGED)
+    const int NBP = RAGGED ? x.nw * KC : NB;  // chunk slots of the table in LDS
     x.kb0 = x.wave * KC;
+    x.cmax = NB - 1 - x.kb0;
     x.ltpu = a.glu ? 1 : 0;            // log2 of tiles per unit
     x.T_slots = MF_TILE << x.ltpu;
     x.part = lds;                              // [nw][T_slots]
     x.red = lds + x.nw * x.T_slots;            // [16] + 16 u64
     lds_tab* zeros = (lds_tab*)(x.red + 48);   // A operand of lanes without a table row
     lds_tab* atab = zeros + MF_ZERO_ENTRIES(KC);
-    x.stats = (lds_f4*)(atab + NB * 48);
+    x.stats = (lds_f4*)(atab + NBP * 48);
     // fragment (chunk kb0 + c, step s) of this lane: x.at[(4c + s) * 12]
     lds_tab* const abase = a_live ? atab + atab_index(x.kb0, 0, x.m >> 2, x.m & 3) : zeros;
     x.rb = (uint32_t)NB * CB;
@@ -1183,13 +1192,34 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     constexpr bool tab_in = TABIN;
     const int tm = tab_in ? 1 : 0;
     const u32x4* tsrc = tab_in ? (const u32x4*)a.xtab : mf_tab_dummy;
+    // (ragged rows: entries of chunks past the row read entry 0 and are replaced by zeros)
 #pragma unroll
-    for (int k = 0; k < TDL; k++) tdig[k] = tsrc[tm * (x.kb0 * 48 + min(x.lane + 64 * k, KC * 48 - 1))];
-    const u32x4 tst = tsrc[tm * (NB * 48 + x.kb0 * 8 + min(x.lane, KC * 8 - 1))];
+    for (int k = 0; k < TDL; k++) {
+        const int e = min(x.lane + 64 * k, KC * 48 - 1);
+        const bool live = !RAGGED || x.kb0 + e / 48 < NB;
+        tdig[k] = tsrc[tm * (live ? x.kb0 * 48 + e : 0)];
+    }
+    const int es = min(x.lane, KC * 8 - 1);
+    const bool st_live = !RAGGED || x.kb0 + es / 8 < NB;
+    u32x4 tst = tsrc[tm * (st_live ? NB * 48 + x.kb0 * 8 + es : 0)];
     const int sm = (tab_in && a.xssq) ? 1 : 0;
     const float* sp = sm ? a.xssq : (const float*)mf_tab_dummy;
 #pragma unroll
-    for (int k = 0; k < TSL; k++) tsq[k] = sp[sm * (x.kb0 * 16 + min(x.lane + 64 * k, KC * 16 - 1))];
+    for (int k = 0; k < TSL; k++) {
+        const int e = min(x.lane + 64 * k, KC * 16 - 1);
+        const bool live = !RAGGED || x.kb0 + e / 16 < NB;
+        tsq[k] = sp[sm * (live ? x.kb0 * 16 + e : 0)];
+    }
+    if constexpr (RAGGED) {
+        const u32x4 z4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < TDL; k++)
+            if (x.kb0 + min(x.lane + 64 * k, KC * 48 - 1) / 48 >= NB) tdig[k] = z4;
+        if (!st_live) tst = z4;
+#pragma unroll
+        for (int k = 0; k < TSL; k++)
+            if (x.kb0 + min(x.lane + 64 * k, KC * 16 - 1) / 16 >= NB) tsq[k] = 0.0f;
+    }
     // the residual and the consumer's norm weight of the first tile's rows, when it is a residual
     // add: written by earlier launches, so they go out with the table rather than after the last
     // weights (where they would add a round trip to the epilogue)
@@ -1216,7 +1246,7 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
         const int c = r & (KC - 1);
         // fewer items than ring slots (a single tile of KC < RING chunks): reload its last chunk
         if (c == 0 && r < x.items) offr = mf_tile_base<IL>(a, x.ufirst, x.ustride, r >> LKC, x.ltpu, x.rb, x.kboff, x.m, Wr);
-        mf_load<T, IL>(ring[r], Wr, offr, c, x);
+        mf_load<T, IL, RAGGED>(ring[r], Wr, offr, c, x);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -1224,6 +1254,14 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     for (int e = threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += x.nw * 64) {
         const u32x4 z4 = {0u, 0u, 0u, 0u};
         zeros[e] = z4;
+    }
+    if constexpr (RAGGED && !TABIN) {
+        // the vector prologue below fills the row's chunks; the padding chunks' digits and stats
+        // are zero
+        const u32x4 z4 = {0u, 0u, 0u, 0u};
+        for (int e = NB * 48 + threadIdx.x; e < NBP * 48; e += x.nw * 64) atab[e] = z4;
+        const f32x4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int e = NB * 8 + threadIdx.x; e < NBP * 8; e += x.nw * 64) x.stats[e] = zf;
     }
     x.xs = 1.0f;  // RMSNorm factor of a table of raw (weighted) values
     if constexpr (tab_in) {
@@ -1308,15 +1346,15 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             x.at = abase;
             __asm__ volatile("" : "+v"(x.at));  // re-read the fragments from LDS each iteration
 #pragma unroll
-            for (int r = 0; r < U; r++) mf_item<T, KC, IL, true>(a, x, ring, it * U + r, r, y, offr, Wr, best);
+            for (int r = 0; r < U; r++) mf_item<T, KC, IL, true, RAGGED>(a, x, ring, it * U + r, r, y, offr, Wr, best);
         }
         x.at = abase;
         __asm__ volatile("" : "+v"(x.at));
         const int i0 = (n_it - 1) * U;
 #pragma unroll
-        for (int r = 0; r < U - RING; r++) mf_item<T, KC, IL, true>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        for (int r = 0; r < U - RING; r++) mf_item<T, KC, IL, true, RAGGED>(a, x, ring, i0 + r, r, y, offr, Wr, best);
 #pragma unroll
-        for (int r = U - RING; r < U; r++) mf_item<T, KC, IL, false>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        for (int r = U - RING; r < U; r++) mf_item<T, KC, IL, false, RAGGED>(a, x, ring, i0 + r, r, y, offr, Wr, best);
     } else {
         for (int i0 = 0; i0 < x.items; i0 += U) {
             x.at = abase;
@@ -1325,8 +1363,8 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             for (int r = 0; r < U; r++) {
                 const int i = i0 + r;
                 if (i >= x.items) break;
-                if (i + RING < x.items) mf_item<T, KC, IL, true>(a, x, ring, i, r, y, offr, Wr, best);
-                else mf_item<T, KC, IL, false>(a, x, ring, i, r, y, offr, Wr, best);
+                if (i + RING < x.items) mf_item<T, KC, IL, true, RAGGED>(a, x, ring, i, r, y, offr, Wr, best);
+                else mf_item<T, KC, IL, false, RAGGED>(a, x, ring, i, r, y, offr, Wr, best);
             }
         }
     }
@@ -1351,6 +1389,44 @@ __global__ __launch_bounds__(512) void k_gemv_mfma_mix(const GemvArgs a) {
                                                 (int)gridDim.x - a.mix_wg);
 }
 
+// waves per workgroup and chunks per wave (*kc) for rows of NB chunks: an even split over at most 8
+// waves of 1, 2, 4 or 8 chunks (4 preferred), else 8 chunks per wave over up to 10 waves with the
+// last one partly past the row (a ragged row, e.g. 74 chunks); 0: no split
+static int mf_split(int NB, int* kc) {
+    const int order[4] = {4, 8, 2, 1};
+    for (int c : order)
+        if (NB % c == 0 && NB / c <= 8) {
+            *kc = c;
+            return NB / c;
+        }
+    if (NB > 64 && NB <= 80) {
+        *kc = 8;
+        return (NB + 7) / 8;
+    }
+    *kc = 0;
+    return 0;
+}
+static int mf_waves(int NB) {
+    int kc;
+    return mf_split(NB, &kc);
+}
+static int mf_kc(int NB) {
+    int kc;
+    mf_split(NB, &kc);
+    return kc;
+}
+static bool mf_ragged(int NB) {
+    int kc;
+    const int nw = mf_split(NB, &kc);
+    return nw > 0 && nw * kc != NB;
+}
+
+// rows whose chunks do not split evenly over at most 8 waves: 8 chunks per wave, up to 10 waves
+template <int T, bool TABIN>
+__global__ __launch_bounds__(640) void k_gemv_mfma_r(const GemvArgs a) {
+    mfma_body<T, 8, TABIN, true, true>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
+}
+
 typedef void (*MfKernel)(const GemvArgs);
 template <int T, bool TABIN, bool IL>
 static MfKernel mf_kernel_in(int kc) {
@@ -1370,9 +1446,23 @@ static MfKernel mf_kernel_mix(int kc) {
         default: return k_gemv_mfma_mix<8, TABIN, IL>;
     }
 }
+template <int T>
+static MfKernel mf_kernel_ragged(bool tab) {
+    return tab ? k_gemv_mfma_r<T, true> : k_gemv_mfma_r<T, false>;
+}
 template <bool IL>
 static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
     const bool tab = a.xin == XIN_TAB;
+    if constexpr (IL) {
+        if (mf_ragged(a.G / 8)) {
+            switch (a.seg[0].type) {
+                case FLLM_TYPE_Q4_K: return mf_kernel_ragged<FLLM_TYPE_Q4_K>(tab);
+                case FLLM_TYPE_Q6_K: return mf_kernel_ragged<FLLM_TYPE_Q6_K>(tab);
+                case FLLM_TYPE_Q8_0: return mf_kernel_ragged<FLLM_TYPE_Q8_0>(tab);
+                default: return mf_kernel_ragged<FLLM_TYPE_Q5_K>(tab);
+            }
+        }
+    }
     if (a.mix_wg > 0) return tab ? mf_kernel_mix<true, IL>(kc) : mf_kernel_mix<false, IL>(kc);
     if constexpr (IL) {
         if (a.seg[0].type == FLLM_TYPE_Q8_0)
@@ -1425,18 +1515,14 @@ bool gemv_fusable_cols(int64_t cols) { return cols % 32 == 0 && cols >= 32 && co
 
 // The matrix-core variant takes launches whose rows are whole 256-element chunks, with one
 // MFMA-capable weight type for all segments, and a wave count that divides the chunks per row.
-static int mf_waves(int NB) {
-    // at most 8 waves, each with 1, 2, 4 or 8 chunks; prefer 4 chunks per wave
-    const int order[4] = {4, 8, 2, 1};
-    for (int kc : order)
-        if (NB % kc == 0 && NB / kc <= 8) return NB / kc;
-    return 0;  // no suitable split
-}
 
 static bool mfma_ok(const GemvArgs& a, int64_t cols) {
     const int NB = (int)(cols / 256);
     if (cols % 256 != 0 || mf_waves(NB) == 0) return false;
+    // ragged rows: tile-interleaved matrices of one type, no GLU
+    if (mf_ragged(NB) && a.glu) return false;
     for (int i = 0; i < a.nseg; i++) {
+        if (mf_ragged(NB) && (a.seg[i].layout != LAYOUT_TILES || a.seg[i].type != a.seg[0].type)) return false;
         const int t = a.seg[i].type;
         if (mf_chunk_bytes(t) == 0) return false;
         // byte offsets within a matrix are 32-bit
@@ -1462,14 +1548,17 @@ static bool mfma_ok(const GemvArgs& a, int64_t cols) {
     return true;
 }
 
-static size_t mf_lds(int nw, int NB, bool glu) {
+static size_t mf_lds(int NB, bool glu) {
     const int T = (glu ? 2 : 1) * MF_TILE;
-    // row partials, 48 floats, zero block, table, and one wave's worth of padding after the table
-    return sizeof(float) * ((size_t)nw * T + 48) + (size_t)(MF_ZERO_ENTRIES(NB / nw) + NB * MF_TAB_ENTRIES + 64) * 16;
+    int kc;
+    const int nw = mf_split(NB, &kc);
+    // row partials, 48 floats, zero block, table (nw * kc chunk slots), and one wave's worth of
+    // padding after the table
+    return sizeof(float) * ((size_t)nw * T + 48) + (size_t)(MF_ZERO_ENTRIES(kc) + (size_t)nw * kc * MF_TAB_ENTRIES + 64) * 16;
 }
 
 bool gemv_uses_mfma(const GemvArgs& a, int64_t cols) {
-    return mfma_ok(a, cols) && mf_lds(mf_waves((int)(cols / 256)), (int)(cols / 256), a.glu != 0) <= 160 * 1024;
+    return mfma_ok(a, cols) && mf_lds((int)(cols / 256), a.glu != 0) <= 160 * 1024;
 }
 
 size_t gemv_tab_bytes(int64_t cols) { return (size_t)(cols / 256) * MF_TAB_ENTRIES * 16; }
@@ -1495,9 +1584,9 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
         if (a.seg[i].type != a.seg[0].type) { a.mix_unit = a.seg[i].wg_begin; a.mix_wg = 1; break; }
     *block_threads = 64 * nw;
     a.nw = nw;
-    *lds_bytes = mf_lds(nw, NB, a.glu != 0);
+    *lds_bytes = mf_lds(NB, a.glu != 0);
     // persistent grid: as many workgroups as fit on the device at once
-    MfKernel k = mf_kernel(a, NB / nw);
+    MfKernel k = mf_kernel(a, mf_kc(NB));
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, *block_threads, *lds_bytes) != hipSuccess ||
@@ -1558,7 +1647,7 @@ int gemv_plan(GemvArgs& a, int64_t cols, int n_cu, int rows_per_wg, int* block_t
 bool gemv_tiles_shape_ok(int type, int64_t rows, int64_t cols) {
     if (mf_chunk_bytes(type) == 0 || rows <= 0 || rows % MF_TILE != 0 || rows > (1 << 30) || cols % 256 != 0) return false;
     const int NB = (int)(cols / 256);
-    if (mf_waves(NB) == 0 || mf_lds(mf_waves(NB), NB, true) > 160 * 1024) return false;
+    if (mf_waves(NB) == 0 || mf_lds(NB, true) > 160 * 1024) return false;
     return (uint64_t)rows * (uint64_t)NB * (uint64_t)mf_chunk_bytes(type) < (1ull << 32);
 }
 
@@ -1660,7 +1749,7 @@ hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, siz
     for (int i = 0; i < a.nseg; i++)
         if (a.seg[i].layout == LAYOUT_TILES && !a.mfma) return hipErrorInvalidValue;
     if (a.mfma)
-        mf_kernel(a, (a.G / 8) / (block_threads / 64))<<<grid, block_threads, lds, st>>>(a);
+        mf_kernel(a, mf_kc(a.G / 8))<<<grid, block_threads, lds, st>>>(a);
     else if (block_threads <= 512)
         k_gemv_fused<false><<<grid, block_threads, lds, st>>>(a);
     else
