@@ -75,6 +75,10 @@ CONFIGS = {
                               final_softcap=30.0, tied=True, norm_std=0.1, seed=17),
     "test-mixed": _cfg("test-mixed", N.ARCH_LLAMA, 2, 256, 4, 2, 512, 512, 64, 10000.0,
                        _types(Q4_0, Q8_K, F16, BF16, F32, Q4_0, Q5_K, F16), emb_type=F16, norm_std=0.1, seed=16),
+    # FFN 16640 = 65 chunks of 256: down's rows split into 9 waves of 8 chunks, the last one with 1
+    # chunk of the row and 7 past it
+    "test-ragged": _cfg("test-ragged", N.ARCH_LLAMA, 2, 256, 4, 2, 16640, 512, 64, 10000.0,
+                        _types(Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K, Q6_K), norm_std=0.1, seed=18),
 }
 
 

@@ -48,7 +48,7 @@ def test_reference_fixtures(ctx, arch):
 
 
 SMALL = ["test-llama", "test-llama-straddle", "test-mistral", "test-qwen2", "test-gemma2", "test-gemma2-hd256",
-         "test-mixed"]
+         "test-mixed", "test-ragged"]
 
 
 @pytest.mark.parametrize("name", SMALL)
