@@ -116,6 +116,7 @@ struct fllm_seq {
     float2* rope = nullptr;
     StepParams* params = nullptr;
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
+    float* x2 = nullptr;  // second residual buffer of the fused Gemma-2 post-norms
     float *g = nullptr, *u = nullptr, *h = nullptr, *tmp = nullptr, *logits = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
     unsigned long long* head_keys = nullptr;  // per-workgroup argmax keys of the fused LM head
@@ -685,6 +686,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->topk_vals, (size_t)d.vocab);
     ALLOC(s->topk_count, 1);
     ALLOC(s->hidden_dbg, (L + 1) * H);
+    ALLOC(s->x2, H);
 #undef ALLOC
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_OOM, "sequence allocation: %s", hipGetErrorString(e)); }
     // RoPE table: theta = scaledPos * inv[i] (LlamaForwardPass.cs:137-147), cos/sin on the host.
@@ -938,6 +940,26 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
     const Tensor* head_t[1] = {&m->output};
     const bool head_mf = s->head_fused && !s->debug && mfma_launch(head_t, 1, 0, H);
     bool xtab = false;  // tab_x / ssq_x hold the table of the current x for the next launch's norm
+    // Gemma-2 post-norms (x += GemmaRmsNorm(tmp, w) after o and after down): the pending one (its
+    // weight pend) is folded into the prologue of the next launch that normalizes x on the matrix
+    // cores (XIN_POST), which stores the new residual in the other of two buffers; cur is the
+    // current residual buffer. The last one of the step goes into s->x, the head's input.
+    const bool post_fuse = gemma && !s->debug;
+    float* cur = s->x;
+    float* alt = s->x2;
+    const float* pend = nullptr;
+    auto fold_post = [&](GemvArgs& a, int cols) -> hipError_t {
+        if (pend == nullptr) return hipSuccess;
+        if (a.xin == XIN_NORM && gemv_uses_mfma(a, cols)) {
+            a.xin = XIN_POST;
+            a.x = cur; a.x2 = s->tmp; a.post_w = pend; a.x_out = alt;
+            std::swap(cur, alt);
+        } else {
+            STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, pend, H, cur, cur, s->st));
+        }
+        pend = nullptr;
+        return hipSuccess;
+    };
     for (int l = 0; l < d.n_layers; l++) {
         const Layer& L = m->layers[(size_t)l];
         float* kc = s->kc + (size_t)l * layer_kv;
@@ -956,11 +978,13 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.seg[2] = seg_of(L.v, EPI_V, nullptr, L.bv, nullptr);
             const double bytes = (double)(L.q.bytes + L.k.bytes + L.v.bytes) + 4.0 * (L.q.rows + L.k.rows + L.v.rows);
             a.xin = (l == 0 && emb_fused) ? XIN_EMBED_NORM : XIN_NORM;
-            a.x = s->x; a.x_out = s->x; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
+            a.x = cur; a.x_out = cur; a.norm_w = L.attn_norm; a.eps = eps; a.norm_kind = nk;
             if (xtab && gemv_uses_mfma(a, H)) { a.xin = XIN_TAB; a.xtab = s->tab_x; a.xssq = s->ssq_x; }
             a.emb = m->tok_embd.ptr; a.emb_type = m->tok_embd.type; a.params = s->params;
             a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
-            hipError_t e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
+            hipError_t e = fold_post(a, H);
+            if (e != hipSuccess) return e;
+            e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
             if (e != hipSuccess) return e;
         }
         // the attention merge writes the output projection's activation table when that runs on
@@ -971,7 +995,7 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
         {
             GemvArgs a{};
             a.nseg = 1;
-            a.seg[0] = gemma ? seg_of(L.o, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.o, EPI_RESID, s->x, nullptr, s->x);
+            a.seg[0] = gemma ? seg_of(L.o, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.o, EPI_RESID, cur, nullptr, cur);
             a.xin = XIN_F32;
             a.x = s->att;
             if (atab) { a.xin = XIN_TAB; a.xtab = s->tab_att; }
@@ -979,7 +1003,8 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             if (xtab) { a.tab_out = s->tab_x; a.ssq_out = s->ssq_x; a.tab_w = L.ffn_norm; a.tab_kind = nk; }
             e = fused_step(s, "attn_output", a, m->qdim, (double)L.o.bytes + 4.0 * (m->qdim + 2.0 * H));
             if (e != hipSuccess) return e;
-            if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));
+            if (gemma && post_fuse) pend = L.post_attn;
+            else if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, cur, cur, s->st));
         }
         const bool htab = gu_mf && dn_mf;
         {
@@ -990,16 +1015,17 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.seg[0] = seg_of(L.gate, EPI_STORE, s->h, nullptr, nullptr);
             a.seg[1] = seg_of(L.up, EPI_STORE, nullptr, nullptr, nullptr);
             a.xin = XIN_NORM;
-            a.x = s->x; a.norm_w = L.ffn_norm; a.eps = eps; a.norm_kind = nk;
+            a.x = cur; a.norm_w = L.ffn_norm; a.eps = eps; a.norm_kind = nk;
             if (xtab) { a.xin = XIN_TAB; a.xtab = s->tab_x; a.xssq = s->ssq_x; }
             if (htab) a.tab_out = s->tab_h;
+            if ((e = fold_post(a, H)) != hipSuccess) return e;
             e = fused_step(s, "ffn_gate_up", a, H, (double)(L.gate.bytes + L.up.bytes) + 4.0 * (2.0 * H + d.ffn));
             if (e != hipSuccess) return e;
         }
         {
             GemvArgs a{};
             a.nseg = 1;
-            a.seg[0] = gemma ? seg_of(L.down, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.down, EPI_RESID, s->x, nullptr, s->x);
+            a.seg[0] = gemma ? seg_of(L.down, EPI_STORE, s->tmp, nullptr, nullptr) : seg_of(L.down, EPI_RESID, cur, nullptr, cur);
             a.xin = XIN_F32;
             a.x = s->h;
             if (htab) { a.xin = XIN_TAB; a.xtab = s->tab_h; }
@@ -1016,9 +1042,16 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             if (xtab) { a.tab_out = s->tab_x; a.ssq_out = s->ssq_x; a.tab_w = next_w; a.tab_kind = nk; }
             e = fused_step(s, "ffn_down", a, d.ffn, (double)L.down.bytes + 4.0 * (d.ffn + 2.0 * H));
             if (e != hipSuccess) return e;
-            if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, s->x, s->st));
+            if (gemma && post_fuse) pend = L.post_ffn;
+            else if (gemma) STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, cur, cur, s->st));
         }
-        if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(s->x, H, s->hidden_dbg + (size_t)l * H, s->st));
+        if (s->debug) STEP("debug_copy", 8.0 * H, launch_copy_hidden(cur, H, s->hidden_dbg + (size_t)l * H, s->st));
+    }
+    // the step's last post-norm, into s->x (where the head reads the residual)
+    if (pend != nullptr) {
+        STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, pend, H, cur, s->x, s->st));
+        pend = nullptr;
+        cur = s->x;
     }
     if (!s->head_fused || s->debug) return head_generic(s);
     GemvArgs a{};
@@ -1062,7 +1095,7 @@ static hipError_t enqueue_body_generic(fllm_seq* s) {
         if ((e = attention_step(s, l, kc, vc, false)) != hipSuccess) return e;
         if (gemma) {
             if ((e = gemv_step(s, L.o, s->att, s->tmp, nullptr)) != hipSuccess) return e;
-            STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->st));
+            STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_attn, H, s->x, s->x, s->st));
         } else {
             if ((e = gemv_step(s, L.o, s->att, s->x, s->x)) != hipSuccess) return e;
         }
@@ -1072,7 +1105,7 @@ static hipError_t enqueue_body_generic(fllm_seq* s) {
         STEP("ffn_act", 12.0 * d.ffn, launch_act(s->g, s->u, d.ffn, gemma ? 1 : 0, s->h, s->st));
         if (gemma) {
             if ((e = gemv_step(s, L.down, s->h, s->tmp, nullptr)) != hipSuccess) return e;
-            STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, s->x, s->st));
+            STEP("postnorm_add", 12.0 * H, launch_postnorm_add(s->tmp, L.post_ffn, H, s->x, s->x, s->st));
         } else {
             if ((e = gemv_step(s, L.down, s->h, s->x, s->x)) != hipSuccess) return e;
         }

@@ -1279,18 +1279,128 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             for (int i = 0; i < x.nw; i++) tot += x.red[i];
             x.xs = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
         }
+    } else if (a.xin == XIN_POST && a.G <= x.nw * 64) {
+        // Gemma-2 post-norm folded in (Gemma2ForwardPass.cs:90-96), one 32-element group per
+        // thread: x2 and x stay in registers across the two reductions, so every vector is read
+        // once. The new residual is x + (x2 * rms(x2)) * (post_w + 1), the operation order of the
+        // separate post-norm kernel, then normalized as XIN_NORM.
+        const int g = (int)threadIdx.x;
+        const bool live = g < a.G;
+        float t2[32], xv[32];
+        float ss = 0.0f;
+        if (live) {
+            const float4* ti = (const float4*)(a.x2 + g * 32);
+            const float4* xi = (const float4*)(a.x + g * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 t = ti[i], u = xi[i];
+                t2[4 * i] = t.x; t2[4 * i + 1] = t.y; t2[4 * i + 2] = t.z; t2[4 * i + 3] = t.w;
+                xv[4 * i] = u.x; xv[4 * i + 1] = u.y; xv[4 * i + 2] = u.z; xv[4 * i + 3] = u.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 32; i++) ss = fmaf(t2[i], t2[i], ss);
+        }
+        ss = wsum(ss);
+        if (x.lane == 0) x.red[x.wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < x.nw; i++) tot += x.red[i];
+        const float prms = 1.0f / sqrtf(tot / (float)(a.G * 32) + 1e-6f);
+        __syncthreads();  // x.red is reused below
+        float ssq = 0.0f;
+        if (live) {
+            const float4* pw = (const float4*)(a.post_w + g * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 w4 = pw[i];
+                const float ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) xv[4 * i + e] = xv[4 * i + e] + (t2[4 * i + e] * prms) * (ww[e] + 1.0f);
+            }
+#pragma unroll
+            for (int i = 0; i < 32; i++) ssq = fmaf(xv[i], xv[i], ssq);
+        }
+        ssq = wsum(ssq);
+        if (x.lane == 0) x.red[x.wave] = ssq;
+        __syncthreads();
+        tot = 0.0f;
+        for (int i = 0; i < x.nw; i++) tot += x.red[i];
+        const float scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
+        if (live) {
+            if (blockIdx.x == 0) {
+                float4* xo = (float4*)(a.x_out + g * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) xo[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
+            }
+            const float4* wv = (const float4*)(a.norm_w + g * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 w4 = wv[i];
+                const float ww[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float t = xv[4 * i + e] * scale;
+                    xv[4 * i + e] = a.norm_kind ? t * (ww[e] + 1.0f) : t * ww[e];
+                }
+            }
+            float4 st;
+            atab_write(atab, g >> 3, g & 7, xv, &st);
+            f32x4 stv = {st.x, st.y, st.z, st.w};
+            x.stats[(g >> 3) * 8 + (g & 7)] = stv;
+        }
     } else {
+        // XIN_POST over more groups than threads: the scale of the post-norm over x2 first, then
+        // the rows below recompute the new residual
+        float prms = 1.0f;
+        if (a.xin == XIN_POST) {
+            float ss = 0.0f;
+            for (int g = threadIdx.x; g < a.G; g += x.nw * 64) {
+                const float4* ti = (const float4*)(a.x2 + g * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float4 t = ti[i];
+                    ss = fmaf(t.x, t.x, ss);
+                    ss = fmaf(t.y, t.y, ss);
+                    ss = fmaf(t.z, t.z, ss);
+                    ss = fmaf(t.w, t.w, ss);
+                }
+            }
+            ss = wsum(ss);
+            if (x.lane == 0) x.red[x.wave] = ss;
+            __syncthreads();
+            float tot = 0.0f;
+            for (int i = 0; i < x.nw; i++) tot += x.red[i];
+            prms = 1.0f / sqrtf(tot / (float)(a.G * 32) + 1e-6f);
+            __syncthreads();  // x.red is reused below
+        }
+        // this group's input row: the embedding row, x, or (XIN_POST) the new residual
+        auto row = [&](int g, float* v) {
+            if (a.xin == XIN_EMBED_NORM) {
+                deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
+                return;
+            }
+            const float4* xi = (const float4*)(a.x + g * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
+            if (a.xin == XIN_POST) {
+                const float4* ti = (const float4*)(a.x2 + g * 32);
+                const float4* pw = (const float4*)(a.post_w + g * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float4 t = ti[i], w4 = pw[i];
+                    v[4 * i] = v[4 * i] + (t.x * prms) * (w4.x + 1.0f);
+                    v[4 * i + 1] = v[4 * i + 1] + (t.y * prms) * (w4.y + 1.0f);
+                    v[4 * i + 2] = v[4 * i + 2] + (t.z * prms) * (w4.z + 1.0f);
+                    v[4 * i + 3] = v[4 * i + 3] + (t.w * prms) * (w4.w + 1.0f);
+                }
+            }
+        };
         float scale = 1.0f;
         if (a.xin != XIN_F32) {
             float ssq = 0.0f;
             for (int g = threadIdx.x; g < a.G; g += x.nw * 64) {
                 float v[32];
-                if (a.xin == XIN_EMBED_NORM) deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
-                else {
-                    const float4* xi = (const float4*)(a.x + g * 32);
-#pragma unroll
-                    for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
-                }
+                row(g, v);
 #pragma unroll
                 for (int i = 0; i < 32; i++) ssq = fmaf(v[i], v[i], ssq);
             }
@@ -1303,17 +1413,11 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
         }
         for (int g = threadIdx.x; g < a.G; g += x.nw * 64) {
             float v[32];
-            if (a.xin == XIN_EMBED_NORM) {
-                deq32(a.emb_type, a.emb, (int64_t)a.params->token * a.G * 32 + g * 32, v);
-                if (blockIdx.x == 0) {
-                    float4* xo = (float4*)(a.x_out + g * 32);
+            row(g, v);
+            if ((a.xin == XIN_EMBED_NORM || a.xin == XIN_POST) && blockIdx.x == 0) {
+                float4* xo = (float4*)(a.x_out + g * 32);
 #pragma unroll
-                    for (int i = 0; i < 8; i++) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-                }
-            } else {
-                const float4* xi = (const float4*)(a.x + g * 32);
-#pragma unroll
-                for (int i = 0; i < 8; i++) { float4 t = xi[i]; v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w; }
+                for (int i = 0; i < 8; i++) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
             }
             if (a.xin != XIN_F32) {
                 const float4* wv = (const float4*)(a.norm_w + g * 32);
@@ -1748,6 +1852,8 @@ hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, siz
     // LAYOUT_TILES matrices are read only by the matrix-core variant
     for (int i = 0; i < a.nseg; i++)
         if (a.seg[i].layout == LAYOUT_TILES && !a.mfma) return hipErrorInvalidValue;
+    if (a.xin == XIN_POST && (!a.mfma || a.x2 == nullptr || a.post_w == nullptr || a.x_out == nullptr || a.x_out == a.x))
+        return hipErrorInvalidValue;
     if (a.mfma)
         mf_kernel(a, mf_kc(a.G / 8))<<<grid, block_threads, lds, st>>>(a);
     else if (block_threads <= 512)

@@ -7,7 +7,9 @@ namespace fllm {
 
 // input of the projection
 // XIN_TAB: the matrix-core variant's activation table, written by the producer's epilogue
-enum { XIN_F32 = 0, XIN_NORM = 1, XIN_EMBED_NORM = 2, XIN_TAB = 3 };
+// XIN_POST (matrix-core variant only): x + GemmaRmsNorm(x2, post_w) is the new residual (stored to
+// x_out by workgroup 0), then normalized as XIN_NORM: a Gemma-2 post-norm folded into its consumer
+enum { XIN_F32 = 0, XIN_NORM = 1, XIN_EMBED_NORM = 2, XIN_TAB = 3, XIN_POST = 4 };
 // epilogue of a segment
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_Q = 2, EPI_K = 3, EPI_V = 4, EPI_LOGITS = 5 };
 
@@ -44,8 +46,9 @@ struct GemvArgs {
     int mix_unit, mix_wg;  // matrix-core variant with Q4_K then Q6_K segments: first Q6_K unit and workgroup (0: one type)
     // input
     int xin;
-    const float* x;        // XIN_F32 / XIN_NORM input vector
-    float* x_out;          // XIN_EMBED_NORM: the embedding row is also stored here (workgroup 0)
+    const float* x;        // XIN_F32 / XIN_NORM input vector (XIN_POST: the residual)
+    float* x_out;          // XIN_EMBED_NORM: the embedding row is also stored here (workgroup 0);
+                           // XIN_POST: the new residual (workgroup 0; not x: others still read it)
     const float* norm_w;   // XIN_NORM / XIN_EMBED_NORM
     float eps;
     int norm_kind;         // 0: (x*rms)*w, 1: (x*rms)*(1+w)
@@ -68,6 +71,9 @@ struct GemvArgs {
     // logits
     float softcap;
     unsigned long long* wg_keys;  // per workgroup: (order key of its largest logit << 32) | ~index
+    // XIN_POST
+    const float* x2;       // the output whose post-norm is added to x
+    const float* post_w;   // the post-norm weight (1 + w)
 };
 
 bool gemv_fusable_type(int t);

@@ -370,7 +370,7 @@ hipError_t launch_act(const float* g, const float* u, int n, int act, float* h, 
 
 // Gemma2 post-norms: x += GemmaRmsNorm(t, w) (Gemma2ForwardPass.cs:90-91, 95-96).
 __global__ __launch_bounds__(1024) void k_postnorm_add(const float* __restrict__ t, const float* __restrict__ w,
-                                                        int n, float* x) {
+                                                        int n, const float* xi, float* xo) {
     __shared__ float red[16];
     float ss = 0.0f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(t[i], t[i], ss);
@@ -378,12 +378,12 @@ __global__ __launch_bounds__(1024) void k_postnorm_add(const float* __restrict__
     float rms = 1.0f / sqrtf(tot / (float)n + 1e-6f);
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         float o = (t[i] * rms) * (w[i] + 1.0f);
-        x[i] = x[i] + o;
+        xo[i] = xi[i] + o;
     }
 }
 
-hipError_t launch_postnorm_add(const float* t, const float* w, int n, float* x, hipStream_t st) {
-    k_postnorm_add<<<1, 1024, 0, st>>>(t, w, n, x);
+hipError_t launch_postnorm_add(const float* t, const float* w, int n, const float* x_in, float* x_out, hipStream_t st) {
+    k_postnorm_add<<<1, 1024, 0, st>>>(t, w, n, x_in, x_out);
     return hipGetLastError();
 }
 

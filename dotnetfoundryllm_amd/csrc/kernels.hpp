@@ -44,7 +44,8 @@ hipError_t launch_attention(const float* q, const float* kcache, const float* vc
 // h = act(g) * u, act 0 = SiLU, 1 = GELU(tanh).
 hipError_t launch_act(const float* g, const float* u, int n, int act, float* h, hipStream_t st);
 // x += GemmaRmsNorm(t, w)
-hipError_t launch_postnorm_add(const float* t, const float* w, int n, float* x, hipStream_t st);
+// x_out = x_in + GemmaRmsNorm(t, w) (x_out may be x_in)
+hipError_t launch_postnorm_add(const float* t, const float* w, int n, const float* x_in, float* x_out, hipStream_t st);
 hipError_t launch_softcap(float* x, int64_t n, float cap, hipStream_t st);
 // argmax into p->argmax; with tokens_out also tokens_out[p->nstep] = argmax and the step advance
 // (token = argmax, pos + 1, cur_len + 1, nstep + 1).
