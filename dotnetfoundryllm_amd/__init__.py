@@ -157,16 +157,35 @@ class DeviceBuffer:
             self.h = None
 
 
-def gemv(ctx, tensor_type, w_buf, rows, cols, x_buf, y_buf, w_offset=0):
-    """LinearProjection on device buffers (enqueued on the context stream)."""
-    _check(N.dev.fllm_gemv(ctx.h, tensor_type, w_buf.h, w_offset, rows, cols, x_buf.h, y_buf.h))
+LAYOUT_GGUF, LAYOUT_TILES = 0, 1  # fllm_layout
 
 
-def gemv_time(ctx, tensor_type, w_bufs, rows, cols, x_buf, y_buf, iters):
+def gemv(ctx, tensor_type, w_buf, rows, cols, x_buf, y_buf, w_offset=0, layout=LAYOUT_GGUF):
+    """LinearProjection on device buffers (enqueued on the context stream); layout
+    LAYOUT_TILES reads a matrix written by gemv_pack."""
+    if layout == LAYOUT_GGUF:
+        _check(N.dev.fllm_gemv(ctx.h, tensor_type, w_buf.h, w_offset, rows, cols, x_buf.h, y_buf.h))
+    else:
+        _check(N.dev.fllm_gemv_ex(ctx.h, tensor_type, w_buf.h, w_offset, rows, cols, x_buf.h, y_buf.h, layout))
+
+
+def gemv_pack(ctx, tensor_type, src_buf, rows, cols, dst_buf, src_offset=0):
+    """Regroups a GGUF matrix into the tile-interleaved layout of the matrix-core GEMV."""
+    _check(N.dev.fllm_gemv_pack(ctx.h, tensor_type, src_buf.h, src_offset, rows, cols, dst_buf.h))
+
+
+def gemv_time(ctx, tensor_type, w_bufs, rows, cols, x_buf, y_buf, iters, layout=None):
+    """Mean microseconds per launch over `iters` launches cycling through w_bufs: with layout
+    None, one HIP event pair per launch (fllm_gemv_time, GGUF rows); with a layout, one pair around
+    all launches back to back (fllm_gemv_time_ex)."""
     arr = (C.c_void_p * len(w_bufs))(*[b.h.value for b in w_bufs])
     out = C.c_double()
-    _check(N.dev.fllm_gemv_time(ctx.h, tensor_type, C.cast(arr, C.POINTER(C.c_void_p)), len(w_bufs), rows, cols,
-                                x_buf.h, y_buf.h, iters, C.byref(out)))
+    if layout is None:
+        _check(N.dev.fllm_gemv_time(ctx.h, tensor_type, C.cast(arr, C.POINTER(C.c_void_p)), len(w_bufs), rows, cols,
+                                    x_buf.h, y_buf.h, iters, C.byref(out)))
+    else:
+        _check(N.dev.fllm_gemv_time_ex(ctx.h, tensor_type, C.cast(arr, C.POINTER(C.c_void_p)), len(w_bufs), rows,
+                                       cols, x_buf.h, y_buf.h, iters, layout, C.byref(out)))
     return out.value
 
 

@@ -114,6 +114,9 @@ DEVICE_SIGS = {
     "fllm_buf_read": (I32, [P, U64, P, U64]),
     "fllm_gemv": (I32, [P, I32, P, U64, I64, I64, P, P]),
     "fllm_gemv_time": (I32, [P, I32, PP, I32, I64, I64, P, P, I32, PF64]),
+    "fllm_gemv_pack": (I32, [P, I32, P, U64, I64, I64, P]),
+    "fllm_gemv_ex": (I32, [P, I32, P, U64, I64, I64, P, P, I32]),
+    "fllm_gemv_time_ex": (I32, [P, I32, PP, I32, I64, I64, P, P, I32, I32, PF64]),
     "fllm_seq_set_profile": (I32, [P, I32]),
     "fllm_seq_profile_count": (I32, [P, PI32]),
     "fllm_seq_profile_entry": (I32, [P, I32, C.c_char_p, I32, PI64, PF64, PF64]),

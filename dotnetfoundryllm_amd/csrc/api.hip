@@ -317,6 +317,80 @@ extern "C" int32_t fllm_gemv(fllm_ctx* ctx, int32_t type, fllm_buf* w, uint64_t 
     return FLLM_OK;
 }
 
+extern "C" int32_t fllm_gemv_pack(fllm_ctx* ctx, int32_t type, fllm_buf* src, uint64_t src_offset, int64_t rows,
+                                  int64_t cols, fllm_buf* dst) {
+    NOT_NULL(ctx);
+    NOT_NULL(src);
+    NOT_NULL(dst);
+    if (!type_supported(type)) return fail(FLLM_E_NOT_SUPPORTED, "Tensor type %d is not supported.", type);
+    if (rows <= 0 || cols <= 0) return fail(FLLM_E_ARG, "rows and cols must be positive");
+    if (!gemv_tiles_shape_ok(type, rows, cols))
+        return fail(FLLM_E_NOT_SUPPORTED, "no tile layout for type %d, %lld x %lld", type, (long long)rows, (long long)cols);
+    if (src_offset % 16 != 0) return fail(FLLM_E_ARG, "source offset must be 16-byte aligned");
+    const uint64_t nb = type_bytes(type, rows * cols);
+    if (src_offset > src->n || nb > src->n - src_offset) return fail(FLLM_E_ARG, "source buffer too small");
+    if (nb > dst->n) return fail(FLLM_E_ARG, "destination buffer too small");
+    if (dst == src) return fail(FLLM_E_ARG, "the regrouping is not in place");
+    HIP_TRY(hipSetDevice(ctx->device));
+    HIP_TRY(launch_pack_tiles(type, src->ptr + src_offset, dst->ptr, rows, cols, ctx->stream));
+    return FLLM_OK;
+}
+
+static int32_t check_layout(int32_t type, int64_t rows, int64_t cols, uint64_t w_offset, int32_t layout) {
+    if (layout == FLLM_LAYOUT_GGUF) return FLLM_OK;
+    if (layout != FLLM_LAYOUT_TILES) return fail(FLLM_E_ARG_RANGE, "unknown layout %d", layout);
+    if (w_offset != 0) return fail(FLLM_E_ARG, "a tile-interleaved matrix starts at offset 0");
+    if (!gemv_tiles_shape_ok(type, rows, cols))
+        return fail(FLLM_E_NOT_SUPPORTED, "no tile layout for type %d, %lld x %lld", type, (long long)rows, (long long)cols);
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_gemv_ex(fllm_ctx* ctx, int32_t type, fllm_buf* w, uint64_t w_offset, int64_t rows, int64_t cols,
+                                fllm_buf* x, fllm_buf* y, int32_t layout) {
+    NOT_NULL(ctx);
+    int32_t rc = check_gemv_args(type, w, w_offset, rows, cols, x, y);
+    if (rc == FLLM_OK) rc = check_layout(type, rows, cols, w_offset, layout);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(ctx->device));
+    WMat m{w->ptr + w_offset, type, rows, cols};
+    if (layout == FLLM_LAYOUT_TILES) HIP_TRY(launch_gemv_tiles(m, (const float*)x->ptr, (float*)y->ptr, ctx->n_cu, ctx->stream));
+    else HIP_TRY(launch_gemv(m, (const float*)x->ptr, (float*)y->ptr, nullptr, ctx->n_cu, ctx->stream));
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_gemv_time_ex(fllm_ctx* ctx, int32_t type, fllm_buf* const* w, int32_t n_w, int64_t rows,
+                                     int64_t cols, fllm_buf* x, fllm_buf* y, int32_t iters, int32_t layout,
+                                     double* avg_us) {
+    NOT_NULL(ctx);
+    NOT_NULL(w);
+    NOT_NULL(avg_us);
+    if (n_w <= 0 || iters <= 0) return fail(FLLM_E_ARG, "n_w and iters must be positive");
+    for (int i = 0; i < n_w; i++) {
+        int32_t rc = check_gemv_args(type, w[i], 0, rows, cols, x, y);
+        if (rc == FLLM_OK) rc = check_layout(type, rows, cols, 0, layout);
+        if (rc) return rc;
+    }
+    HIP_TRY(hipSetDevice(ctx->device));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t err = hipEventCreate(&e0);
+    if (err == hipSuccess) err = hipEventCreate(&e1);
+    if (err == hipSuccess) err = hipEventRecord(e0, ctx->stream);
+    for (int i = 0; i < iters && err == hipSuccess; i++) {
+        WMat m{w[i % n_w]->ptr, type, rows, cols};
+        err = layout == FLLM_LAYOUT_TILES ? launch_gemv_tiles(m, (const float*)x->ptr, (float*)y->ptr, ctx->n_cu, ctx->stream)
+                                          : launch_gemv(m, (const float*)x->ptr, (float*)y->ptr, nullptr, ctx->n_cu, ctx->stream);
+    }
+    if (err == hipSuccess) err = hipEventRecord(e1, ctx->stream);
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (err != hipSuccess) return fail(FLLM_E_DEVICE, "gemv_time: %s", hipGetErrorString(err));
+    *avg_us = ms * 1000.0 / iters;
+    return FLLM_OK;
+}
+
 extern "C" int32_t fllm_gemv_time(fllm_ctx* ctx, int32_t type, fllm_buf* const* w, int32_t n_w, int64_t rows,
                                   int64_t cols, fllm_buf* x, fllm_buf* y, int32_t iters, double* avg_us) {
     NOT_NULL(ctx);

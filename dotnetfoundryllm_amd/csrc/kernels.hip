@@ -99,6 +99,24 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
     if (lane == 0) y[row] = residual ? residual[row] + acc : acc;
 }
 
+hipError_t launch_gemv_tiles(const WMat& m, const float* xf, float* y, int n_cu, hipStream_t st) {
+    GemvArgs a{};
+    a.nseg = 1;
+    a.seg[0].w = m.w;
+    a.seg[0].type = m.type;
+    a.seg[0].layout = LAYOUT_TILES;
+    a.seg[0].rows = (int)m.rows;
+    a.seg[0].epi = EPI_STORE;
+    a.seg[0].out = y;
+    a.xin = XIN_F32;
+    a.x = xf;
+    if (!gemv_tiles_shape_ok(m.type, m.rows, m.cols) || !gemv_uses_mfma(a, m.cols)) return hipErrorInvalidValue;
+    int threads;
+    size_t lds;
+    const int grid = gemv_plan(a, m.cols, n_cu, 0, &threads, &lds);
+    return launch_gemv_fused(a, grid, threads, lds, st);
+}
+
 hipError_t launch_gemv(const WMat& m, const float* xf, float* y, const float* residual, int n_cu, hipStream_t st) {
     int t = m.type;
     if (gemv_fusable_type(t) && gemv_fusable_cols(m.cols)) {

@@ -29,6 +29,8 @@ hipError_t launch_dequant(int type, const uint8_t* src, int64_t nelem, float* ds
 
 // y = W x (+ residual when non-null; residual may alias y).
 hipError_t launch_gemv(const WMat& m, const float* xf, float* y, const float* residual, int n_cu, hipStream_t st);
+// y = W x for a matrix in the tile-interleaved layout (launch_pack_tiles): matrix-core variant only
+hipError_t launch_gemv_tiles(const WMat& m, const float* xf, float* y, int n_cu, hipStream_t st);
 
 hipError_t launch_set_params(StepParams* p, int token, int pos, int cur_len, hipStream_t st);
 hipError_t launch_embed(const uint8_t* emb, int type, int hidden, const StepParams* p, float* x,

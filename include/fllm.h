@@ -247,6 +247,30 @@ FLLM_API int32_t fllm_gemv_time(fllm_ctx* ctx, int32_t type, fllm_buf* const* w,
                                 int64_t rows, int64_t cols, fllm_buf* x, fllm_buf* y,
                                 int32_t iters, double* avg_us);
 
+/* Weight layouts of the GEMV entry points: GGUF rows as uploaded, or the matrix-core layout
+ * that fllm_model_finalize gives model weights (16-row tiles interleaved per 256-column chunk). */
+enum fllm_layout {
+    FLLM_LAYOUT_GGUF = 0,
+    FLLM_LAYOUT_TILES = 1
+};
+/* Regroups a rows x cols matrix of `type` (GGUF layout at src + src_offset) into
+ * FLLM_LAYOUT_TILES at dst (the same number of bytes; every byte kept), for a caller that
+ * multiplies one matrix many times. FLLM_E_NOT_SUPPORTED where the layout does not apply (types
+ * other than Q4_K, Q5_K, Q6_K, Q8_0; rows not a multiple of 16; cols not a multiple of 256).
+ * No counterpart in the reference, whose weights are F32 after load (GgufModelLoader.cs:409-418);
+ * it is the standalone form of the regrouping fllm_model_finalize does. */
+FLLM_API int32_t fllm_gemv_pack(fllm_ctx* ctx, int32_t type, fllm_buf* src, uint64_t src_offset,
+                                int64_t rows, int64_t cols, fllm_buf* dst);
+/* fllm_gemv for a matrix in `layout` (FLLM_LAYOUT_TILES: as written by fllm_gemv_pack, at
+ * offset 0). LinearProjection (LlamaForwardPass.cs:237-260). */
+FLLM_API int32_t fllm_gemv_ex(fllm_ctx* ctx, int32_t type, fllm_buf* w, uint64_t w_offset,
+                              int64_t rows, int64_t cols, fllm_buf* x, fllm_buf* y, int32_t layout);
+/* Times `iters` launches back to back cycling through n_w weight buffers in `layout`: the mean
+ * time per launch between one HIP event pair around all of them (launch gaps included). */
+FLLM_API int32_t fllm_gemv_time_ex(fllm_ctx* ctx, int32_t type, fllm_buf* const* w, int32_t n_w,
+                                   int64_t rows, int64_t cols, fllm_buf* x, fllm_buf* y,
+                                   int32_t iters, int32_t layout, double* avg_us);
+
 /* ---- per-kernel timing of the decode step ----------------------------------- */
 /* When enabled, fllm_forward launches kernels one by one (no graph) with a HIP event pair
  * around every launch on the sequence's stream, and aggregates per kernel name the number of

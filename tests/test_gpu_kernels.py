@@ -102,6 +102,53 @@ def test_gemv_microbenchmark_shapes(ctx, t, shape):
     assert err <= 1e-5
 
 
+@pytest.mark.parametrize("t", [N.Q4_K, N.Q8_0, N.Q6_K, N.Q5_K])
+@pytest.mark.parametrize("shape", C1 + [(64, 18944), (16, 256)])
+def test_gemv_tiles_layout(ctx, t, shape):
+    """fllm_gemv_pack + fllm_gemv_ex(FLLM_LAYOUT_TILES) against the oracle's F32 dot (18944
+    columns: 74 chunks, the ragged wave split)."""
+    rows, cols = shape
+    raw = synth(t, rows * cols, seed=5, tid=rows + 1)
+    x = np.random.default_rng(5).standard_normal(cols).astype(np.float32)
+    wb, tb = F.DeviceBuffer(ctx, raw.nbytes), F.DeviceBuffer(ctx, raw.nbytes)
+    xb, yb = F.DeviceBuffer(ctx, x.nbytes), F.DeviceBuffer(ctx, rows * 4)
+    try:
+        wb.write(raw)
+        xb.write(x)
+        F.gemv_pack(ctx, t, wb, rows, cols, tb)
+        F.gemv(ctx, t, tb, rows, cols, xb, yb, layout=F.LAYOUT_TILES)
+        ctx.sync()
+        y = yb.read(rows * 4)
+    finally:
+        for b in (wb, tb, xb, yb):
+            b.close()
+    rc, wf = O.dequantize(t, raw, rows * cols)
+    assert rc == 0
+    ref = wf.reshape(rows, cols).astype(np.float64) @ x.astype(np.float64)
+    err = O.normwise_rel_err(y, ref)
+    print(f"type {t} {shape} tiles: normwise rel err {err:.2e}")
+    assert err <= 1e-5
+
+
+def test_gemv_tiles_contract(ctx):
+    raw = synth(N.Q4_K, 32 * 512, seed=6, tid=1)
+    wb, tb = F.DeviceBuffer(ctx, raw.nbytes), F.DeviceBuffer(ctx, raw.nbytes)
+    xb, yb = F.DeviceBuffer(ctx, 512 * 4), F.DeviceBuffer(ctx, 32 * 4)
+    try:
+        wb.write(raw)
+        with pytest.raises(F.NotSupportedException):
+            F.gemv_pack(ctx, N.Q4_0, wb, 32, 512, tb)             # no tile layout for Q4_0
+        with pytest.raises(F.NotSupportedException):
+            F.gemv_pack(ctx, N.Q4_K, wb, 24, 512, tb)             # rows not a multiple of 16
+        with pytest.raises(F.ArgumentException):
+            F.gemv_pack(ctx, N.Q4_K, wb, 32, 512, wb)             # not in place
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            F.gemv(ctx, N.Q4_K, wb, 32, 512, xb, yb, layout=7)    # unknown layout
+    finally:
+        for b in (wb, tb, xb, yb):
+            b.close()
+
+
 @pytest.mark.parametrize("t,rows,cols", [
     (N.Q4_K, 512, 1408),     # rows straddle Q4_K blocks (5.5 blocks per row)
     (N.Q6_K, 300, 3584),     # rows only 4-byte aligned (2940 bytes)
