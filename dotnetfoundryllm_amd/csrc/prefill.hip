@@ -354,9 +354,11 @@ __device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, i
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // this thread's share of a K step: X pieces c = tid + 256 i, and W group (row tid / 2, tid % 2)
+    // this thread's share of a K step: X pieces c = tid + 256 i, and W group (row tid % 128, group
+    // tid / 128): neighbouring lanes store neighbouring rows (68-float stride, 4 banks apart), so
+    // the W tile goes into LDS without bank conflicts
     constexpr int XP = BM * 16 / 256;
-    const int wrow = tid >> 1, wgrp = tid & 1, wr = n0 + wrow;
+    const int wrow = tid & (PF_BN - 1), wgrp = tid / PF_BN, wr = n0 + wrow;
     const bool wlive = wr < sg.N;
     using Raw = typename PfW<WT>::Raw;
     float4 xr[XP];
