@@ -324,6 +324,22 @@ class HipForwardPass:
         _check(N.dev.fllm_sample_topk(self._kv.h, inv_temp, k, _iptr(ids), _fptr(vals), cap, C.byref(n)))
         return ids[: n.value], vals[: n.value]
 
+    def penalize(self, ids, penalty):
+        """LlamaLanguageModel.ApplyRepetitionPenalty over `ids` on the device logits."""
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        _check(N.dev.fllm_logits_penalize(self._kv.h, _iptr(a), a.size, penalty))
+
+    def sample_nucleus(self, inv_temp, top_p, u):
+        """SamplerPipeline stages 1, 3, 4, 5 (no top-k) on the device with the draw's u."""
+        v = C.c_int32()
+        _check(N.dev.fllm_sample_nucleus(self._kv.h, inv_temp, top_p, u, C.byref(v)))
+        return v.value
+
+    def probs(self):
+        out = np.empty(self.model.desc.vocab, dtype=np.float32)
+        _check(N.dev.fllm_probs_copy(self._kv.h, _fptr(out), out.size))
+        return out
+
     def hidden(self, layer):
         out = np.empty(self.model.desc.hidden, dtype=np.float32)
         _check(N.dev.fllm_debug_hidden(self._kv.h, layer, _fptr(out), out.size))

@@ -104,6 +104,9 @@ DEVICE_SIGS = {
     "fllm_logits_write": (I32, [P, PF32, I64]),
     "fllm_sample_greedy": (I32, [P, PI32]),
     "fllm_sample_topk": (I32, [P, F32_, I32, PI32, PF32, I32, PI32]),
+    "fllm_logits_penalize": (I32, [P, PI32, I32, F32_]),
+    "fllm_sample_nucleus": (I32, [P, F32_, F32_, F32_, PI32]),
+    "fllm_probs_copy": (I32, [P, PF32, I64]),
     "fllm_debug_hidden": (I32, [P, I32, PF32, I64]),
     "fllm_kv_read": (I32, [P, I32, I32, PF32, I64]),
     "fllm_dequantize": (I32, [P, I32, P, U64, PF32, I64]),

@@ -129,6 +129,11 @@ struct fllm_seq {
     int *topk_ids = nullptr, *topk_count = nullptr;
     float* topk_vals = nullptr;
     int topk_cap = 0;
+    float* probs = nullptr;       // distribution left by the nucleus sampler (vocab floats)
+    int* samp_token = nullptr;    // its drawn token
+    int* pen_counts = nullptr;    // repetition-penalty counters (vocab ints, zero between calls)
+    int* pen_ids = nullptr;       // the penalised ids of the last call (device copy)
+    int pen_cap = 0;
     float* hidden_dbg = nullptr;
     bool debug = false;
     bool use_graph = true;
@@ -759,6 +764,9 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->topk_ids, (size_t)d.vocab);
     ALLOC(s->topk_vals, (size_t)d.vocab);
     ALLOC(s->topk_count, 1);
+    ALLOC(s->probs, (size_t)d.vocab);
+    ALLOC(s->samp_token, 1);
+    ALLOC(s->pen_counts, (size_t)d.vocab);
     ALLOC(s->hidden_dbg, (L + 1) * H);
     ALLOC(s->x2, H);
 #undef ALLOC
@@ -776,6 +784,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     if (e == hipSuccess) e = hipMemsetAsync(s->kc, 0, sizeof(float) * kvsz, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->params, 0, sizeof(StepParams), s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, sizeof(float) * kvsz, s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->pen_counts, 0, sizeof(int) * (size_t)d.vocab, s->st);
     if (e == hipSuccess) e = hipStreamSynchronize(s->st);
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_DEVICE, "sequence init: %s", hipGetErrorString(e)); }
     *out = s;
@@ -1503,6 +1512,60 @@ extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int3
         HIP_TRY(hipMemcpyAsync(vals, s->topk_vals, sizeof(float) * (size_t)cnt, hipMemcpyDeviceToHost, s->st));
         HIP_TRY(hipStreamSynchronize(s->st));
     }
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_logits_penalize(fllm_seq* s, const int32_t* ids, int32_t n_ids, float penalty) {
+    NOT_NULL(s);
+    if (n_ids < 0) return fail(FLLM_E_ARG_RANGE, "n_ids must be >= 0");
+    if (n_ids > 0) NOT_NULL(ids);
+    if (!(penalty > 0.0f)) return fail(FLLM_E_ARG_RANGE, "Penalty must be greater than zero.");
+    if (penalty == 1.0f || n_ids == 0) return FLLM_OK;  // every logit unchanged
+    if (n_ids > s->pen_cap) {
+        int cap = n_ids > 4096 ? n_ids : 4096;
+        HIP_TRY(hipStreamSynchronize(s->st));
+        int* p = nullptr;
+        HIP_TRY(hipMalloc((void**)&p, sizeof(int) * (size_t)cap));
+        if (s->pen_ids) {
+            for (auto& a : s->allocs)
+                if (a == (void*)s->pen_ids) a = (void*)p;
+            hipFree(s->pen_ids);
+        } else {
+            s->allocs.push_back(p);
+        }
+        s->pen_ids = p;
+        s->pen_cap = cap;
+    }
+    HIP_TRY(hipMemcpyAsync(s->pen_ids, ids, sizeof(int32_t) * (size_t)n_ids, hipMemcpyHostToDevice, s->st));
+    HIP_TRY(launch_rep_penalty(s->logits, s->m->d.vocab, s->pen_ids, n_ids, penalty, s->pen_counts, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));  // the host's id array may be reused once this returns
+    s->argmax_valid = false;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p, float u, int32_t* out_token) {
+    NOT_NULL(s);
+    NOT_NULL(out_token);
+    if (!(top_p > 0.0f && top_p <= 1.0f)) return fail(FLLM_E_ARG_RANGE, "topP must be in (0, 1].");
+    if (!(u >= 0.0f && u < 1.0f)) return fail(FLLM_E_ARG_RANGE, "u must be in [0, 1).");
+    if (!(inv_temp > 0.0f) || isinf(inv_temp)) return fail(FLLM_E_ARG_RANGE, "inv_temp must be positive and finite.");
+    int V = s->m->d.vocab;
+    HIP_TRY(launch_sample_nucleus(s->logits, V, inv_temp, top_p, u, s->probs, s->samp_token, s->st));
+    if (inv_temp != 1.0f) s->argmax_valid = false;
+    int tok = 0;
+    HIP_TRY(hipMemcpyAsync(&tok, s->samp_token, sizeof(int), hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    *out_token = tok;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_probs_copy(fllm_seq* s, float* dst, int64_t n) {
+    NOT_NULL(s);
+    NOT_NULL(dst);
+    int V = s->m->d.vocab;
+    if (n < V) return fail(FLLM_E_ARG, "destination must hold %d floats", V);
+    HIP_TRY(hipMemcpyAsync(dst, s->probs, sizeof(float) * (size_t)V, hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
     return FLLM_OK;
 }
 

@@ -576,6 +576,202 @@ hipError_t launch_topk(float* x, int64_t n, float inv_temp, int k, int cap, int*
     return hipGetLastError();
 }
 
+// LlamaLanguageModel.ApplyRepetitionPenalty (LlamaLanguageModel.cs:357-373): for each listed id
+// in [0, n), in list order, l > 0 ? l / penalty : l * penalty, repeats applying again. Distinct ids
+// are independent, so the repeats of one id are counted first and then applied in sequence by a
+// single thread, which gives the list-order result bit for bit. counts holds n zeros on entry and
+// is left zeroed: exactly one exchange per id returns its count, every other returns 0.
+__global__ __launch_bounds__(1024) void k_rep_penalty(float* x, int n, const int* __restrict__ ids, int n_ids,
+                                                      float penalty, int* counts) {
+    for (int j = threadIdx.x; j < n_ids; j += blockDim.x) {
+        int id = ids[j];
+        if ((unsigned)id < (unsigned)n) atomicAdd(&counts[id], 1);
+    }
+    __threadfence();  // every add has completed before any thread exchanges a counter
+    __syncthreads();
+    for (int j = threadIdx.x; j < n_ids; j += blockDim.x) {
+        int id = ids[j];
+        if ((unsigned)id >= (unsigned)n) continue;
+        int c = atomicExch(&counts[id], 0);
+        if (c == 0) continue;
+        float v = x[id];
+        for (int r = 0; r < c; r++) v = v > 0.0f ? v / penalty : v * penalty;
+        x[id] = v;
+    }
+}
+
+hipError_t launch_rep_penalty(float* x, int n, const int* ids, int n_ids, float penalty, int* counts,
+                              hipStream_t st) {
+    k_rep_penalty<<<1, 1024, 0, st>>>(x, n, ids, n_ids, penalty, counts);
+    return hipGetLastError();
+}
+
+// ---- nucleus sampler ------------------------------------------------------------------
+// Probability masses as unsigned 64-bit fixed point with 2^63 = 1: integer sums are exact and
+// independent of the order they are formed in.
+__device__ __forceinline__ unsigned long long fix63(float p) {
+    return (unsigned long long)((double)p * 9223372036854775808.0);
+}
+
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, T* red, Op op) {
+    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o));
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (int)(blockDim.x >> 6);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    T r = red[0];
+    for (int w = 1; w < nw; w++) r = op(r, red[w]);  // same order in every thread
+    return r;
+}
+
+// Exclusive prefix over the block of one value per thread (Hillis-Steele in LDS); returns the
+// thread's exclusive prefix and writes the block total.
+__device__ __forceinline__ unsigned long long block_excl_scan(unsigned long long v, unsigned long long* buf,
+                                                              unsigned long long* total) {
+    int t = threadIdx.x, nt = blockDim.x;
+    buf[t] = v;
+    __syncthreads();
+    for (int o = 1; o < nt; o <<= 1) {
+        unsigned long long a = t >= o ? buf[t - o] : 0ull;
+        __syncthreads();
+        buf[t] += a;
+        __syncthreads();
+    }
+    unsigned long long incl = buf[t];
+    *total = buf[nt - 1];
+    __syncthreads();
+    return incl - v;
+}
+
+// SamplerPipeline.Sample (SamplerPipeline.cs:58-89) with topK disabled, on the device logits:
+// scale by inv_temp in place (stage 1), softmax (stage 3, TensorOperations.cs:23-39: max,
+// exp(x - max), divide by the sum) into pr, nucleus of top_p (stage 4, TopPSampler.ApplyTopP
+// TopPSampler.cs:60-110: the shortest prefix of the descending order whose mass reaches top_p,
+// equal probabilities by ascending index, then divided by the kept sum), and the draw (stage 5,
+// TemperatureSampler.SampleFromProbabilities TemperatureSampler.cs:53-70: the first index whose
+// running sum exceeds u, else the last nonzero index). Running sums and masses are exact
+// fixed-point integers where the reference accumulates in f32 order, so the chosen token can
+// differ only where u or top_p lies within f32 rounding of a boundary.
+// One workgroup; thread t owns the contiguous index range [t*per, (t+1)*per) for the ordered
+// passes.
+__global__ __launch_bounds__(1024) void k_sample_nucleus(float* x, int n, float inv_temp, float top_p, float u,
+                                                         float* pr, int* out_token) {
+    __shared__ float redf[16];
+    __shared__ unsigned long long redu[16];
+    __shared__ unsigned long long hist[256];
+    __shared__ unsigned long long scanbuf[1024];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ unsigned long long s_above;
+    __shared__ int s_all;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    if (inv_temp != 1.0f)
+        for (int i = tid; i < n; i += nt) x[i] = x[i] * inv_temp;
+    float mx = -INFINITY;
+    for (int i = tid; i < n; i += nt) mx = fmaxf(mx, x[i]);
+    mx = block_reduce(mx, redf, [](float a, float b) { return fmaxf(a, b); });
+    float sum = 0.0f;
+    for (int i = tid; i < n; i += nt) {
+        float e = expf(x[i] + (-mx));
+        pr[i] = e;
+        sum += e;
+    }
+    sum = block_reduce(sum, redf, [](float a, float b) { return a + b; });
+    for (int i = tid; i < n; i += nt) pr[i] = pr[i] / sum;
+    const int per = (n + nt - 1) / nt;
+    const int beg = min(tid * per, n), end = min(beg + per, n);
+    __syncthreads();
+    if (top_p < 1.0f) {
+        // threshold tau = probability at the nucleus edge: radix select from the top over the
+        // probabilities' bit patterns (non-negative floats order as integers), weighing each
+        // 8-bit bucket by its mass
+        const unsigned long long P = fix63(top_p);
+        if (tid == 0) { s_prefix = 0; s_mask = 0; s_above = 0; s_all = 0; }
+        for (int pass = 0; pass < 4; pass++) {
+            const int shift = 24 - 8 * pass;
+            for (int b = tid; b < 256; b += nt) hist[b] = 0ull;
+            __syncthreads();
+            const uint32_t prefix = s_prefix, mask = s_mask;
+            for (int i = tid; i < n; i += nt) {
+                float p = pr[i];
+                uint32_t key = __float_as_uint(p);
+                if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], fix63(p));
+            }
+            __syncthreads();
+            if (tid == 0 && !s_all) {
+                unsigned long long acc = s_above;
+                int b = 255;
+                for (; b >= 0; b--) {
+                    if (acc + hist[b] >= P) break;
+                    acc += hist[b];
+                }
+                if (b < 0) s_all = 1;  // the whole mass stays below top_p: keep everything
+                else {
+                    s_prefix = prefix | ((uint32_t)b << shift);
+                    s_mask = mask | (255u << shift);
+                    s_above = acc;
+                }
+            }
+            __syncthreads();
+        }
+        const uint32_t tau = s_prefix;
+        const bool all = s_all != 0;
+        // equal probabilities at the edge: the first m of them in index order
+        unsigned long long ties = 0;
+        if (!all)
+            for (int i = beg; i < end; i++) ties += __float_as_uint(pr[i]) == tau ? 1ull : 0ull;
+        unsigned long long ntie = 0;
+        unsigned long long tie0 = block_excl_scan(ties, scanbuf, &ntie);
+        unsigned long long m = ntie;
+        if (!all) {
+            unsigned long long ft = fix63(__uint_as_float(tau)), need = P - s_above;
+            if (ft > 0) {
+                unsigned long long q = (need + ft - 1) / ft;
+                m = q < ntie ? q : ntie;
+            }
+        }
+        float kept = 0.0f;
+        unsigned long long r = tie0;
+        for (int i = beg; i < end; i++) {
+            float p = pr[i];
+            uint32_t key = __float_as_uint(p);
+            bool keep = all || key > tau || (key == tau && r++ < m);
+            if (!keep) pr[i] = 0.0f;
+            else kept += p;
+        }
+        kept = block_reduce(kept, redf, [](float a, float b) { return a + b; });
+        if (kept > 0.0f)
+            for (int i = beg; i < end; i++) pr[i] = pr[i] / kept;
+        __syncthreads();
+    }
+    // draw: first index whose running mass exceeds u
+    const unsigned long long U = fix63(u);
+    unsigned long long part = 0;
+    for (int i = beg; i < end; i++) part += fix63(pr[i]);
+    unsigned long long total = 0;
+    unsigned long long base = block_excl_scan(part, scanbuf, &total);
+    int found = 0x7fffffff;
+    if (U < base + part && U >= base) {
+        unsigned long long run = base;
+        for (int i = beg; i < end; i++) {
+            run += fix63(pr[i]);
+            if (U < run) { found = i; break; }
+        }
+    }
+    int last = -1;  // fallback: the last nonzero probability
+    for (int i = beg; i < end; i++)
+        if (pr[i] > 0.0f) last = i;
+    found = block_reduce(found, (int*)redu, [](int a, int b) { return a < b ? a : b; });
+    last = block_reduce(last, (int*)redu + 16, [](int a, int b) { return a > b ? a : b; });
+    if (tid == 0) *out_token = found != 0x7fffffff ? found : (last >= 0 ? last : n - 1);
+}
+
+hipError_t launch_sample_nucleus(float* x, int n, float inv_temp, float top_p, float u, float* pr, int* out_token,
+                                 hipStream_t st) {
+    k_sample_nucleus<<<1, 1024, 0, st>>>(x, n, inv_temp, top_p, u, pr, out_token);
+    return hipGetLastError();
+}
+
 __global__ void k_copy(const float* __restrict__ x, int n, float* dst) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = x[i];

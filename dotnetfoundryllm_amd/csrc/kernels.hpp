@@ -57,6 +57,13 @@ hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams*
                               hipStream_t st);
 hipError_t launch_topk(float* x, int64_t n, float inv_temp, int k, int cap, int* ids, float* vals, int* count,
                        hipStream_t st);
+// LlamaLanguageModel.ApplyRepetitionPenalty on device logits; counts: n zeroed ints, left zeroed.
+hipError_t launch_rep_penalty(float* x, int n, const int* ids, int n_ids, float penalty, int* counts,
+                              hipStream_t st);
+// SamplerPipeline stages 1, 3, 4, 5 (temperature, softmax, top-p, draw with u) over x; pr: n floats
+// of scratch (left holding the final distribution); the token goes to *out_token.
+hipError_t launch_sample_nucleus(float* x, int n, float inv_temp, float top_p, float u, float* pr, int* out_token,
+                                 hipStream_t st);
 hipError_t launch_copy_hidden(const float* x, int n, float* dst, hipStream_t st);
 
 }  // namespace fllm

@@ -737,10 +737,12 @@ extern "C" int32_t fllmh_sampler_sample(fllmh_sampler* s, fllm_seq* seq, int32_t
         *out_token = sample_cdf(&s->rng, s->ids.data(), s->buf.data(), cnt, V);
         return FLLM_OK;
     }
-    s->buf.resize((size_t)V);
-    rc = fllm_logits_copy(seq, s->buf.data(), V);
-    if (rc) return dfail(rc);
-    return fllmh_sampler_sample_host(s, s->buf.data(), V, out_token);
+    // no top-k: stages 1 and 3-5 over the whole vocabulary on the device (no logits copy); the
+    // draw's u comes from this pipeline's generator, one NextFloat per token as in the reference
+    float inv = s->temperature != 1.0f ? 1.0f / s->temperature : 1.0f;
+    float u = fllmh_xoshiro_next_float(&s->rng);
+    rc = fllm_sample_nucleus(seq, inv, s->top_p, u, out_token);
+    return rc ? dfail(rc) : FLLM_OK;
 }
 
 // =====================================================================================
@@ -758,9 +760,10 @@ extern "C" int32_t fllmh_generate(fllm_seq* seq, const int32_t* prompt, int32_t 
     if (rc) return dfail(rc);
     auto t0 = clk::now();
     int position = 0;
-    for (int i = 0; i < n_prompt - 1; i++) {  // prefill n-1 tokens one at a time (:133-137)
-        rc = fllm_forward(seq, prompt[i], position++);
+    if (n_prompt > 1) {  // the n-1 prefill Forward calls (:133-137) as one batched prefill
+        rc = fllm_prefill(seq, prompt, n_prompt - 1, 0);
         if (rc) return dfail(rc);
+        position = n_prompt - 1;
     }
     rc = fllm_seq_sync(seq);
     if (rc) return dfail(rc);
@@ -768,30 +771,13 @@ extern "C" int32_t fllmh_generate(fllm_seq* seq, const int32_t* prompt, int32_t 
     int next = n_prompt > 0 ? prompt[n_prompt - 1] : bos_token_id;  // :152
     int generated = 0;
     int finish = 0;
-    std::vector<float> logits;
     for (int step = 0; step < max_tokens; step++) {  // :162-293
         rc = fllm_forward(seq, next, position++);
         if (rc) return dfail(rc);
-        if (repetition_penalty != 1.0f) {
-            // ApplyRepetitionPenalty (:357-373) runs on host logits, then the pipeline samples them
-            int32_t V = 0;
-            rc = seq_vocab(seq, &V);
-            if (rc) return rc;
-            logits.resize((size_t)V);
-            rc = fllm_logits_copy(seq, logits.data(), V);
+        if (repetition_penalty != 1.0f && generated > 0) {
+            // ApplyRepetitionPenalty (:183-186, 357-373) over the generated ids, on the device logits
+            rc = fllm_logits_penalize(seq, out_tokens, generated, repetition_penalty);
             if (rc) return dfail(rc);
-            for (int i = 0; i < generated; i++) {
-                int id = out_tokens[i];
-                if (id >= 0 && id < V) {
-                    if (logits[(size_t)id] > 0.0f) logits[(size_t)id] /= repetition_penalty;
-                    else logits[(size_t)id] *= repetition_penalty;
-                }
-            }
-            rc = fllmh_sampler_sample_host(sampler, logits.data(), V, &next);
-            if (rc) return rc;
-            out_tokens[generated++] = next;
-            if (eos_token_id >= 0 && next == eos_token_id) { finish = 1; break; }
-            continue;
         }
         rc = fllmh_sampler_sample(sampler, seq, &next);
         if (rc) return rc;

@@ -210,6 +210,25 @@ FLLM_API int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token);
  * values. cap is the capacity of ids/vals; FLLM_E_ARG if more than cap survive. */
 FLLM_API int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k,
                                   int32_t* ids, float* vals, int32_t cap, int32_t* n_out);
+/* LlamaLanguageModel.ApplyRepetitionPenalty (LlamaLanguageModel.cs:183-186, 357-373) on the device
+ * logits: for every id of ids[0..n_ids) in order, l > 0 ? l / penalty : l * penalty, an id listed
+ * k times is penalised k times, ids outside [0, vocab) are skipped. Bit-identical to the host loop.
+ * penalty <= 0 -> FLLM_E_ARG_RANGE (RepetitionPenaltySampler.cs:27-28); penalty == 1 changes
+ * nothing. Replaces the vocab-sized logits round trip of fllm_logits_copy + fllm_logits_write. */
+FLLM_API int32_t fllm_logits_penalize(fllm_seq* s, const int32_t* ids, int32_t n_ids, float penalty);
+/* SamplerPipeline.Sample (SamplerPipeline.cs:58-89) with topK disabled, on the device: scales the
+ * logits by inv_temp in place (stage 1), softmax (stage 3), nucleus of top_p (stage 4,
+ * TopPSampler.ApplyTopP TopPSampler.cs:60-110; top_p == 1 keeps everything, equal probabilities at
+ * the edge are taken in ascending index order), and draws the first index whose running
+ * probability exceeds u (stage 5, TemperatureSampler.SampleFromProbabilities
+ * TemperatureSampler.cs:53-70), u being the pipeline's XoshiroRandom.NextFloat() for this draw.
+ * Running sums are exact fixed-point where the reference sums f32 in order: the token can differ
+ * from the reference only when u or top_p falls within f32 rounding of a boundary.
+ * Errors: top_p outside (0,1], u outside [0,1), inv_temp not positive and finite -> FLLM_E_ARG_RANGE. */
+FLLM_API int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p, float u, int32_t* out_token);
+/* The distribution fllm_sample_nucleus drew from (vocab floats: the renormalised nucleus, zeros
+ * elsewhere); a parity hook. */
+FLLM_API int32_t fllm_probs_copy(fllm_seq* s, float* dst, int64_t n);
 
 /* ---- parity hooks -------------------------------------------------------- */
 /* Residual stream x after layer `layer` of the last step (requires fllm_seq_set_debug(1)

@@ -73,8 +73,10 @@ typedef struct fllmh_sampler fllmh_sampler;
  * (SamplerPipeline.cs:14-23). Errors: FLLM_E_ARG_RANGE for invalid temperature / top_p. */
 FLLM_API int32_t fllmh_sampler_create(float temperature, int32_t top_k, float top_p, uint64_t seed, fllmh_sampler** out);
 FLLM_API int32_t fllmh_sampler_destroy(fllmh_sampler* s);
-/* Samples from the sequence's current logits: greedy -> device argmax; top-k -> device
- * candidates + host softmax/CDF walk; otherwise full logits on the host. */
+/* Samples from the sequence's current logits: greedy -> device argmax (fllm_sample_greedy);
+ * top-k -> device candidates (fllm_sample_topk) + host softmax / top-p / CDF walk over them;
+ * otherwise temperature, softmax, top-p and the draw on the device (fllm_sample_nucleus, u from
+ * this sampler's generator). No vocab-sized copy on any path. */
 FLLM_API int32_t fllmh_sampler_sample(fllmh_sampler* s, fllm_seq* seq, int32_t* out_token);
 /* The same pipeline over host logits (modified in place), for parity tests. */
 FLLM_API int32_t fllmh_sampler_sample_host(fllmh_sampler* s, float* logits, int32_t n, int32_t* out_token);
@@ -89,9 +91,11 @@ typedef struct fllmh_generate_stats {
     int32_t finish_reason;     /* 0 = length, 1 = stop (EOS) */
 } fllmh_generate_stats;
 /* LlamaLanguageModel.GenerateAsync over already-tokenized ids: clears the KV cache,
- * runs Forward on prompt[0..n-2] at positions 0.., then decodes from prompt[n-1] for up to
- * max_tokens steps, sampling each step and stopping at eos_token_id (eos < 0 disables).
- * repetition_penalty != 1 applies LlamaLanguageModel.ApplyRepetitionPenalty on host logits. */
+ * runs the Forward calls of prompt[0..n-2] at positions 0.. as one batched fllm_prefill, then
+ * decodes from prompt[n-1] for up to max_tokens steps, sampling each step and stopping at
+ * eos_token_id (eos < 0 disables). repetition_penalty != 1 applies
+ * LlamaLanguageModel.ApplyRepetitionPenalty over the generated ids on the device logits
+ * (fllm_logits_penalize) before sampling; penalty <= 0 -> FLLM_E_ARG_RANGE. */
 FLLM_API int32_t fllmh_generate(fllm_seq* seq, const int32_t* prompt, int32_t n_prompt, int32_t max_tokens,
                                 fllmh_sampler* sampler, int32_t eos_token_id, int32_t bos_token_id,
                                 float repetition_penalty, int32_t* out_tokens, fllmh_generate_stats* stats);

@@ -17,6 +17,13 @@
  *    parity with TensorPrimitives' vectorised Exp/Tanh/Sigmoid is unpinned.
  *  - argmax / top-k / xoshiro256**: integer-exact; pinned by the reference's sampler tests
  *    and the published xoshiro256** / SplitMix64 algorithm.
+ *  - top-p (orc_apply_top_p): pinned by TopPSamplerTests.cs's cases and by the nucleus
+ *    invariants (kept mass reaches p, dropping the smallest kept entry falls below it, every
+ *    kept probability is at least every dropped one); the order among equal probabilities at
+ *    the edge follows a stable sort, where the reference's Array.Sort is unstable (unpinned).
+ *  - repetition penalty (orc_repetition_penalty): IEEE division / multiplication per listed
+ *    id, pinned by RepetitionPenaltySamplerTests.cs's cases and closed forms (k repeats of a
+ *    positive logit divide it k times).
  *  - forward pass: invariants (context of one => attention returns v0, GQA mapping,
  *    window start) and the reference's deterministic 2-layer fixtures.
  */
@@ -399,6 +406,49 @@ int64_t orc_sample_from_probs(const float* probs, int64_t n, orc_xoshiro* r) {
 
 /* SamplerPipeline.Sample (SamplerPipeline.cs:58-89) with topP == 1. */
 int64_t orc_sampler_pipeline(float* logits, int64_t n, float temperature, int top_k, orc_xoshiro* r) {
+    return orc_sampler_pipeline_p(logits, n, temperature, top_k, 1.0f, r);
+}
+
+/* Descending probability, ties by ascending index: the order a stable sort gives. The reference
+ * sorts with Array.Sort (introsort, unstable), so which of several equal probabilities at the
+ * nucleus edge come first is not pinned; distinct values order the same either way. */
+static const float* g_topp_probs;
+static int cmp_desc_prob(const void* a, const void* b) {
+    int64_t ia = *(const int64_t*)a, ib = *(const int64_t*)b;
+    float pa = g_topp_probs[ia], pb = g_topp_probs[ib];
+    if (pa > pb) return -1;
+    if (pa < pb) return 1;
+    return ia < ib ? -1 : (ia > ib ? 1 : 0);
+}
+
+/* TopPSampler.ApplyTopP (TopPSampler.cs:60-110): keep the smallest prefix of the descending order
+ * whose running f32 sum reaches p, zero the rest, divide by the f32 sum of what is left. */
+void orc_apply_top_p(float* probs, int64_t n, float p) {
+    if (p >= 1.0f || n <= 0) return;
+    int64_t* idx = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+    float* copy = (float*)malloc(sizeof(float) * (size_t)n);
+    for (int64_t i = 0; i < n; i++) { idx[i] = i; copy[i] = probs[i]; }
+    g_topp_probs = copy;
+    qsort(idx, (size_t)n, sizeof(int64_t), cmp_desc_prob);
+    float cum = 0.0f;
+    int reached = 0;
+    for (int64_t r = 0; r < n; r++) {
+        if (reached) probs[idx[r]] = 0.0f;
+        else {
+            cum += probs[idx[r]];
+            if (cum >= p) reached = 1;
+        }
+    }
+    float sum = 0.0f; /* TensorPrimitives.Sum order unpinned */
+    for (int64_t i = 0; i < n; i++) sum += probs[i];
+    if (sum > 0.0f)
+        for (int64_t i = 0; i < n; i++) probs[i] = probs[i] / sum;
+    free(idx);
+    free(copy);
+}
+
+/* SamplerPipeline.Sample (SamplerPipeline.cs:58-89): temperature, top-k, softmax, top-p, draw. */
+int64_t orc_sampler_pipeline_p(float* logits, int64_t n, float temperature, int top_k, float top_p, orc_xoshiro* r) {
     if (temperature == 0.0f) return orc_argmax(logits, n);
     if (temperature != 1.0f) {
         float inv = 1.0f / temperature;
@@ -406,7 +456,21 @@ int64_t orc_sampler_pipeline(float* logits, int64_t n, float temperature, int to
     }
     if (top_k > 0) orc_apply_topk(logits, n, top_k);
     orc_softmax(logits, n);
+    if (top_p < 1.0f) orc_apply_top_p(logits, n, top_p);
     return orc_sample_from_probs(logits, n, r);
+}
+
+/* LlamaLanguageModel.ApplyRepetitionPenalty (LlamaLanguageModel.cs:357-373): for every id of the
+ * generated list in order (repeats apply again), l > 0 ? l / penalty : l * penalty; ids outside
+ * [0, n) are skipped. */
+void orc_repetition_penalty(float* logits, int64_t n, const int32_t* ids, int64_t n_ids, float penalty) {
+    for (int64_t j = 0; j < n_ids; j++) {
+        int32_t id = ids[j];
+        if ((uint32_t)id < (uint64_t)n) {
+            if (logits[id] > 0.0f) logits[id] = logits[id] / penalty;
+            else logits[id] = logits[id] * penalty;
+        }
+    }
 }
 
 /* ---------------------------------------------------------------------------------

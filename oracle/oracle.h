@@ -49,6 +49,12 @@ void     orc_apply_topk(float* logits, int64_t n, int k);
 int64_t  orc_sample_from_probs(const float* probs, int64_t n, orc_xoshiro* r);
 /* SamplerPipeline.Sample with topP == 1 (greedy when temperature == 0). Modifies logits. */
 int64_t  orc_sampler_pipeline(float* logits, int64_t n, float temperature, int top_k, orc_xoshiro* r);
+/* SamplerPipeline.Sample with every stage, top-p included. Modifies logits. */
+int64_t  orc_sampler_pipeline_p(float* logits, int64_t n, float temperature, int top_k, float top_p, orc_xoshiro* r);
+/* TopPSampler.ApplyTopP on probabilities (in place). */
+void     orc_apply_top_p(float* probs, int64_t n, float p);
+/* LlamaLanguageModel.ApplyRepetitionPenalty (in place). */
+void     orc_repetition_penalty(float* logits, int64_t n, const int32_t* ids, int64_t n_ids, float penalty);
 
 /* Model + forward pass */
 typedef struct orc_desc {

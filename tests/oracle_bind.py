@@ -57,6 +57,9 @@ _sigs = {
     "orc_apply_topk": (None, [PF, I64, C.c_int]),
     "orc_sample_from_probs": (I64, [PF, I64, C.POINTER(OrcXoshiro)]),
     "orc_sampler_pipeline": (I64, [PF, I64, F32, C.c_int, C.POINTER(OrcXoshiro)]),
+    "orc_sampler_pipeline_p": (I64, [PF, I64, F32, C.c_int, F32, C.POINTER(OrcXoshiro)]),
+    "orc_apply_top_p": (None, [PF, I64, F32]),
+    "orc_repetition_penalty": (None, [PF, I64, C.POINTER(C.c_int32), I64, F32]),
     "orc_model_create": (P, [C.POINTER(OrcDesc)]),
     "orc_model_destroy": (None, [P]),
     "orc_model_set": (C.c_int, [P, C.c_int, C.c_int, C.c_int, P, I64]),
@@ -118,6 +121,24 @@ class Xoshiro:
 def sampler_pipeline(logits, temperature, top_k, rng):
     a = np.ascontiguousarray(logits, dtype=np.float32).copy()
     return int(lib.orc_sampler_pipeline(fp(a), a.size, temperature, top_k, C.byref(rng.s)))
+
+
+def sampler_pipeline_p(logits, temperature, top_k, top_p, rng):
+    a = np.ascontiguousarray(logits, dtype=np.float32).copy()
+    return int(lib.orc_sampler_pipeline_p(fp(a), a.size, temperature, top_k, top_p, C.byref(rng.s)))
+
+
+def apply_top_p(probs, p):
+    a = np.ascontiguousarray(probs, dtype=np.float32).copy()
+    lib.orc_apply_top_p(fp(a), a.size, p)
+    return a
+
+
+def repetition_penalty(logits, ids, penalty):
+    a = np.ascontiguousarray(logits, dtype=np.float32).copy()
+    i = np.ascontiguousarray(ids, dtype=np.int32)
+    lib.orc_repetition_penalty(fp(a), a.size, i.ctypes.data_as(C.POINTER(C.c_int32)), i.size, penalty)
+    return a
 
 
 def desc_from(d):

@@ -1,7 +1,8 @@
 """Pins the oracle's tensor operations, sampling and RNG (CPU only).
 
 Reference tests restated: TensorOperationsTests.cs:9-107, GreedySamplerTests.cs,
-TopKSamplerTests.cs:45-71, SamplerPipelineTests.cs:24-70. Beyond those: closed forms
+TopKSamplerTests.cs:45-71, SamplerPipelineTests.cs:24-70, TopPSamplerTests.cs,
+RepetitionPenaltySamplerTests.cs. Beyond those: closed forms
 (RoPE at position 0 is the identity and preserves pair norms; softcap(x) -> x for |x| << cap;
 GELU/SiLU fixed points), float64 brute force for Dot/LinearProjection, numpy's order
 statistic for the top-k threshold, and the published xoshiro256** algorithm (restated with
@@ -10,6 +11,7 @@ Python integers) for the RNG.
 import math
 
 import numpy as np
+import pytest
 
 import oracle_bind as O
 
@@ -196,3 +198,52 @@ def test_sampler_pipeline_reference_cases():
     p[[2, 4]] = 0
     p /= p.sum()
     assert np.allclose(counts / counts.sum(), p, atol=0.015)
+
+
+def test_top_p_reference_cases():
+    # TopPSamplerTests.cs: ApplyTopP_SmallP_ZeroesOutLowProbTokens
+    q = O.apply_top_p(f32([0.02, 0.90, 0.05, 0.03]), 0.91)
+    assert q[0] == 0 and q[3] == 0 and q[1] > 0 and q[2] > 0
+    # ApplyTopP_RenormalizesRemainingProbabilities
+    q = O.apply_top_p(f32([0.1, 0.6, 0.2, 0.1]), 0.8)
+    assert abs(float(q.sum()) - 1.0) < 1e-5
+    assert q[0] == 0 and q[3] == 0  # 0.6f + 0.2f rounds to 0.8f, which reaches p (>=, not >)
+    assert q[1] > 0 and q[2] > 0
+    # ApplyTopP_P1_LeavesDistributionUnchanged
+    a = f32([0.1, 0.6, 0.2, 0.1])
+    assert np.array_equal(O.apply_top_p(a, 1.0), a)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_top_p_nucleus_invariants(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(2, 400))
+    e = np.exp(rng.normal(0, 1.5, n)).astype(np.float32)
+    probs = (e / e.sum()).astype(np.float32)
+    for p in (0.05, 0.3, 0.7, 0.9, 0.99):
+        q = O.apply_top_p(probs, p)
+        kept = q > 0
+        assert kept.any()
+        # every kept probability is at least every dropped one
+        if (~kept).any():
+            assert probs[kept].min() >= probs[~kept].max()
+        # minimal prefix: the kept mass reaches p, the kept mass without its smallest entry does not
+        mass = float(np.sum(probs[kept], dtype=np.float64))
+        assert mass >= p - 1e-5
+        assert mass - float(probs[kept].min()) < p + 1e-5
+        # renormalised over the nucleus, in proportion to the input
+        assert abs(float(q.sum(dtype=np.float64)) - 1.0) < 1e-5
+        np.testing.assert_allclose(q[kept], probs[kept] / mass, rtol=2e-6)
+
+
+def test_repetition_penalty_reference_cases():
+    # RepetitionPenaltySamplerTests.cs (the model loop applies the same rule, LlamaLanguageModel.cs:357-373)
+    lg = O.repetition_penalty(f32([0.1, 5.0, 4.0]), [1], 1.5)
+    assert lg[1] == np.float32(5.0) / np.float32(1.5) and O.lib.orc_argmax(fp(lg), 3) == 2
+    lg = O.repetition_penalty(f32([-2.0, 0.0, 1.0]), [0], 2.0)
+    assert lg[0] == -4.0 and O.lib.orc_argmax(fp(lg), 3) == 2
+    lg = O.repetition_penalty(f32([5.0, 5.0, 0.5]), [0, 1], 10.0)
+    assert lg[0] == lg[1] == 0.5
+    # repeats apply again, zero takes the multiply branch, ids out of range are skipped
+    lg = O.repetition_penalty(f32([8.0, 0.0, -1.0]), [0, 0, 0, 1, 2, 2, 3, -1], 2.0)
+    assert lg.tolist() == [1.0, 0.0, -4.0]
