@@ -231,6 +231,54 @@ def prefill_report(cfg, n, seconds):
             "mfma_peak_tflops": FP32_MFMA_PEAK_TFLOPS, "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
 
 
+def sampling_report(F, fwd, kv, cfg, seed, reps=50):
+    """Wall time per call of the sampling stages on the last step's logits (each call returns its
+    token on the host): the device paths of SamplerPipeline (top-k candidates + host walk; the
+    nucleus on the device), the device repetition penalty over 256 ids, and the host pipeline over
+    a vocab-sized logits copy for comparison."""
+    import numpy as np
+    saved = fwd.logits
+    ids = np.arange(0, 256 * 97, 97, dtype=np.int32) % cfg["vocab"]
+    out = {}
+
+    def timed(name, fn):
+        fwd.write_logits(saved)
+        fn()  # first call: one-time costs
+        t = 0.0
+        for _ in range(reps):
+            fwd.write_logits(saved)
+            t0 = time.perf_counter()
+            fn()
+            t += time.perf_counter() - t0
+        out[name] = round(t / reps * 1e6, 1)
+
+    sp_k = F.SamplerPipeline(0.8, 40, 1.0, seed)
+    sp_p = F.SamplerPipeline(0.8, 0, 0.9, seed)
+    sp_h = F.SamplerPipeline(0.8, 0, 0.9, seed)
+    try:
+        timed("top_k40_T0.8_device", lambda: sp_k.sample(kv))
+        timed("top_p0.9_T0.8_device", lambda: sp_p.sample(kv))
+        timed("repetition_penalty_256_ids_device", lambda: fwd.penalize(ids, 1.1))
+        timed("top_p0.9_T0.8_host_with_logits_copy", lambda: sp_h.sample_host(fwd.logits))
+    finally:
+        sp_k.close()
+        sp_p.close()
+        sp_h.close()
+    fwd.write_logits(saved)
+    return out
+
+
+def weights_text(cfg):
+    """'Q4_K (q,k,o,gate,up) + Q6_K (v,down,output), seeded random blocks' from the config's types."""
+    from dotnetfoundryllm_amd._native import TYPE_NAMES
+    groups = {}
+    for slot in ("q", "k", "v", "o", "gate", "up", "down", "out"):
+        groups.setdefault(cfg["types"][slot], []).append("output" if slot == "out" else slot)
+    parts = [f"{TYPE_NAMES.get(t, t)} ({','.join(v)})" for t, v in groups.items()]
+    emb = TYPE_NAMES.get(cfg.get("emb_type"), cfg.get("emb_type"))
+    return " + ".join(parts) + f", {emb} embedding, seeded random blocks"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,6 +288,12 @@ def main():
     ap.add_argument("--config", default="llama3-8b-q4km")
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--host-steps", type=int, default=32, help="steps of the host-driven loop timed after the device loop")
+    ap.add_argument("--temperature", type=float, default=0.0,
+                    help="> 0: the timed decode samples with SamplerPipeline(temperature, top-k, top-p, seed) "
+                         "from the host loop (one forward and one device sampling call per token)")
+    ap.add_argument("--top-k", type=int, default=0)
+    ap.add_argument("--top-p", type=float, default=1.0)
+    ap.add_argument("--seed", type=int, default=0x5EED)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-rocprof", action="store_true", help="roofline from HIP events only (no profiler child runs)")
@@ -286,19 +340,43 @@ def main():
     log(f"prefill {args.prompt - 1} tokens in {prefill_s:.2f} s")
 
     nxt = int(prompt[-1])
-    warm = fwd.decode_greedy(nxt, pos, args.warmup, kv) if args.warmup else []
+    sampled = args.temperature > 0.0
+    if sampled:
+        # LlamaLanguageModel's loop with SamplerPipeline(T, k, p, seed): Forward, then the sampler on
+        # the device logits (top-k candidates or the nucleus on the device), one token read back
+        sampler = F.SamplerPipeline(args.temperature, args.top_k, args.top_p, args.seed)
+
+        def run_steps(n, nxt, pos):
+            out = []
+            for _ in range(n):
+                fwd.forward(nxt, pos, kv)
+                nxt = sampler.sample(kv)
+                pos += 1
+                out.append(nxt)
+            return out
+
+        warm = run_steps(args.warmup, nxt, pos)
+    else:
+        warm = fwd.decode_greedy(nxt, pos, args.warmup, kv) if args.warmup else []
     pos += args.warmup
     nxt = int(warm[-1]) if len(warm) else nxt
     log(f"warmup {args.warmup} steps done; timing {args.steps} decode steps")
 
     F._check(F.N.dev.fllm_seq_sync(kv.h))
     t0 = time.perf_counter()
-    toks = fwd.decode_greedy(nxt, pos, args.steps, kv)  # returns after the last token is on the host
+    if sampled:
+        toks = run_steps(args.steps, nxt, pos)
+    else:
+        toks = fwd.decode_greedy(nxt, pos, args.steps, kv)  # returns after the last token is on the host
     elapsed = time.perf_counter() - t0
     pos += args.steps
     nxt = int(toks[-1])
     tok_s = args.steps / elapsed
-    log(f"decode (device loop): {tok_s:.1f} tok/s ({elapsed / args.steps * 1e3:.3f} ms/token)")
+    mode = (f"host loop, SamplerPipeline(T={args.temperature}, top-k={args.top_k}, top-p={args.top_p}, "
+            f"seed={args.seed})" if sampled else "device-side greedy loop")
+    log(f"decode ({mode}): {tok_s:.1f} tok/s ({elapsed / args.steps * 1e3:.3f} ms/token)")
+    if sampled:
+        sampler.close()
 
     # the same decode driven from the host, one token read-back per step
     host_steps = min(args.host_steps, args.steps)
@@ -345,6 +423,9 @@ def main():
     roofline["achieved"] = round(achieved, 1)
     roofline["frac"] = round(achieved / HBM_PEAK_GBS, 4)
 
+    sampling = sampling_report(F, fwd, kv, cfg, args.seed)
+    log(f"sampling per call (us): {sampling}")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, one thread, bounded sample) ...")
@@ -365,10 +446,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"{cfg['name']}: {args.prompt}-token random prompt, batched prefill, then greedy "
-                        f"decode at batch 1 (positions {args.prompt - 1 + args.warmup}..{args.prompt - 2 + args.warmup + args.steps}), "
-                        "device-side greedy loop",
-            "weights": "Q4_K (q,k,o,gate,up) + Q6_K (v,down,output), seeded random blocks",
+            "workload": f"{cfg['name']}: {args.prompt}-token random prompt, batched prefill, then "
+                        f"{'sampled' if sampled else 'greedy'} decode at batch 1 (positions "
+                        f"{args.prompt - 1 + args.warmup}..{args.prompt - 2 + args.warmup + args.steps}), {mode}",
+            "weights": weights_text(cfg),
             "weight_bytes_per_token": tok_bytes,
             "graph": not args.no_graph,
         },
@@ -378,6 +459,7 @@ def main():
         "prefill": prefill_report(cfg, args.prompt - 1, prefill_s),
         "host_loop_tok_s": round(host_tok_s, 2) if host_tok_s else None,
         "profiled_step_ms": round(total_ms, 4),
+        "sampling_us_per_call": sampling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -133,6 +133,7 @@ struct fllm_seq {
     int* samp_token = nullptr;    // its drawn token
     int* pen_counts = nullptr;    // repetition-penalty counters (vocab ints, zero between calls)
     int* pen_ids = nullptr;       // the penalised ids of the last call (device copy)
+    TopkScratch* topk_sc = nullptr;  // grid top-k: threshold, segment counts, candidates
     int pen_cap = 0;
     float* hidden_dbg = nullptr;
     bool debug = false;
@@ -767,6 +768,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->probs, (size_t)d.vocab);
     ALLOC(s->samp_token, 1);
     ALLOC(s->pen_counts, (size_t)d.vocab);
+    ALLOC(s->topk_sc, 1);
     ALLOC(s->hidden_dbg, (L + 1) * H);
     ALLOC(s->x2, H);
 #undef ALLOC
@@ -1499,17 +1501,27 @@ extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int3
     if (k < 1) return fail(FLLM_E_ARG_RANGE, "k must be at least 1.");
     if (cap > 0) { NOT_NULL(ids); NOT_NULL(vals); }
     int V = s->m->d.vocab;
+    if (V > SAMPLE_MAX_VOCAB) return fail(FLLM_E_NOT_SUPPORTED, "device top-k handles vocabularies up to %d", SAMPLE_MAX_VOCAB);
     int dcap = cap < s->topk_cap ? cap : s->topk_cap;
-    HIP_TRY(launch_topk(s->logits, V, inv_temp, k, dcap, s->topk_ids, s->topk_vals, s->topk_count, s->st));
+    HIP_TRY(launch_topk(s->logits, V, inv_temp, k, dcap, s->topk_ids, s->topk_vals, s->topk_count, s->topk_sc, s->st));
     if (inv_temp != 1.0f) s->argmax_valid = false;
+    // one round trip for the usual case: the count and the first candidates (as many as k, at
+    // least 64, at most cap) come back together; only more survivors than that need a second copy
     int cnt = 0;
+    int first = k < 64 ? 64 : k;
+    first = first < dcap ? first : dcap;
     HIP_TRY(hipMemcpyAsync(&cnt, s->topk_count, sizeof(int), hipMemcpyDeviceToHost, s->st));
+    if (first > 0) {
+        HIP_TRY(hipMemcpyAsync(ids, s->topk_ids, sizeof(int) * (size_t)first, hipMemcpyDeviceToHost, s->st));
+        HIP_TRY(hipMemcpyAsync(vals, s->topk_vals, sizeof(float) * (size_t)first, hipMemcpyDeviceToHost, s->st));
+    }
     HIP_TRY(hipStreamSynchronize(s->st));
     *n_out = cnt;
     if (cnt > cap) return fail(FLLM_E_ARG, "%d candidates survive top-%d, capacity %d", cnt, k, cap);
-    if (cnt > 0) {
-        HIP_TRY(hipMemcpyAsync(ids, s->topk_ids, sizeof(int) * (size_t)cnt, hipMemcpyDeviceToHost, s->st));
-        HIP_TRY(hipMemcpyAsync(vals, s->topk_vals, sizeof(float) * (size_t)cnt, hipMemcpyDeviceToHost, s->st));
+    if (cnt > first) {
+        size_t rest = (size_t)(cnt - first);
+        HIP_TRY(hipMemcpyAsync(ids + first, s->topk_ids + first, sizeof(int) * rest, hipMemcpyDeviceToHost, s->st));
+        HIP_TRY(hipMemcpyAsync(vals + first, s->topk_vals + first, sizeof(float) * rest, hipMemcpyDeviceToHost, s->st));
         HIP_TRY(hipStreamSynchronize(s->st));
     }
     return FLLM_OK;
@@ -1550,6 +1562,7 @@ extern "C" int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p,
     if (!(u >= 0.0f && u < 1.0f)) return fail(FLLM_E_ARG_RANGE, "u must be in [0, 1).");
     if (!(inv_temp > 0.0f) || isinf(inv_temp)) return fail(FLLM_E_ARG_RANGE, "inv_temp must be positive and finite.");
     int V = s->m->d.vocab;
+    if (V > SAMPLE_MAX_VOCAB) return fail(FLLM_E_NOT_SUPPORTED, "device nucleus sampling handles vocabularies up to %d", SAMPLE_MAX_VOCAB);
     HIP_TRY(launch_sample_nucleus(s->logits, V, inv_temp, top_p, u, s->probs, s->samp_token, s->st));
     if (inv_temp != 1.0f) s->argmax_valid = false;
     int tok = 0;

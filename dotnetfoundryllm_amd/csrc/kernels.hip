@@ -437,9 +437,17 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
     __shared__ int64_t si[16];
     uint32_t bk = 0;
     int64_t bi = -1;
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-        uint32_t k = okey(x[i]);
-        if (bi < 0 || k > bk) { bk = k; bi = i; }
+    const int64_t nt = blockDim.x, step = nt * 8;
+    for (int64_t base = threadIdx.x; base < n; base += step) {  // 8 loads in flight per thread
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = base + j * nt < n ? x[base + j * nt] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {  // ascending index within the thread: the first maximum stays
+            int64_t i = base + j * nt;
+            uint32_t k = okey(v[j]);
+            if (i < n && (bi < 0 || k > bk)) { bk = k; bi = i; }
+        }
     }
     int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int o = 32; o > 0; o >>= 1) {
@@ -503,33 +511,147 @@ hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams*
     return hipGetLastError();
 }
 
-// Scale by inv_temp in place (SamplerPipeline.cs:67-70), find the k-th largest value by a
-// 4-pass radix select on order-preserving keys, and emit every index whose value is not
-// below it (ties kept), in ascending index order.
-__global__ __launch_bounds__(1024) void k_topk(float* x, int64_t n, float inv_temp, int k, int cap, int* ids,
-                                                float* vals, int* count) {
+// ---- helpers of the one-workgroup sampling kernels (1024 threads, 16 waves) ---------------
+// The ordered passes (stable compaction, running sums) work on 64-element chunks: a wave takes
+// chunks wave, wave + 16, ... with coalesced loads, a ballot gives the chunk's count and each
+// lane's rank inside it, and a block scan over the per-chunk totals (in LDS) gives each chunk's
+// offset. SAMPLE_MAX_CHUNKS bounds the vocabulary at 262144 entries.
+constexpr int SAMPLE_MAX_CHUNKS = SAMPLE_MAX_VOCAB / 64;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ unsigned long long lanes_below() {
+    int l = lane_id();
+    return l ? (~0ull >> (64 - l)) : 0ull;
+}
+
+// Exclusive prefix over the block of one value per thread (Hillis-Steele in LDS); returns the
+// thread's exclusive prefix and writes the block total.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T* buf, T* total) {
+    int t = threadIdx.x, nt = blockDim.x;
+    buf[t] = v;
+    __syncthreads();
+    for (int o = 1; o < nt; o <<= 1) {
+        T a = t >= o ? buf[t - o] : (T)0;
+        __syncthreads();
+        buf[t] += a;
+        __syncthreads();
+    }
+    T incl = buf[t];
+    *total = buf[nt - 1];
+    __syncthreads();
+    return incl - v;
+}
+
+// In place exclusive prefix over arr[0..nch) (nch <= 4 * blockDim.x); returns the total.
+template <typename T>
+__device__ __forceinline__ T chunks_excl_scan(T* arr, int nch, T* buf) {
+    const int per = 4, b0 = threadIdx.x * per;
+    T loc = 0;
+    for (int c = b0; c < b0 + per && c < nch; c++) loc += arr[c];
+    T total;
+    T run = block_excl_scan(loc, buf, &total);
+    for (int c = b0; c < b0 + per && c < nch; c++) {
+        T v = arr[c];
+        arr[c] = run;
+        run += v;
+    }
+    __syncthreads();
+    return total;
+}
+
+// hist[bin] += 1 for every lane with `take`, one LDS atomic per distinct bin of the wave (the bins
+// of nearby logits coincide, and same-address atomics from many lanes serialise). Called with all
+// 64 lanes of the wave active.
+__device__ __forceinline__ void wave_hist_add(int* hist, bool take, uint32_t bin) {
+    unsigned long long act = __ballot(take);
+    while (act) {
+        int leader = __ffsll((long long)act) - 1;
+        uint32_t lb = __shfl(bin, leader);
+        unsigned long long same = __ballot(take && bin == lb);
+        if (lane_id() == leader) atomicAdd(&hist[lb], (int)__popcll(same));
+        act &= ~same;
+    }
+}
+
+// One pass of a one-workgroup kernel over src[0..n): f(i, v) for i = tid, tid + nt, ... with
+// v = src[i] (0 past n, where f must check i < n itself). A thread's loads of a batch are issued
+// together, so a pass costs one memory round trip per B elements of a thread rather than one per
+// element. The trip count is uniform, so f may use wave-wide ballots and shuffles.
+template <int B, typename F>
+__device__ __forceinline__ void pass_strided(const float* __restrict__ src, int n, F f) {
+    const int nt = blockDim.x, tid = threadIdx.x;
+    for (int base = 0; base < n; base += nt * B) {
+        float v[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            int i = base + j * nt + tid;
+            v[j] = i < n ? src[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < B; j++) f(base + j * nt + tid, v[j]);
+    }
+}
+
+// The same over 64-element chunks: wave w takes chunks w, w + 16, ..., lane l element 64c + l;
+// f(c, i, v) runs for every chunk c < nch with the whole wave active.
+template <int B, typename F>
+__device__ __forceinline__ void pass_chunks(const float* __restrict__ src, int n, int nch, F f) {
+    const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int c0 = wave; c0 < nch; c0 += nw * B) {
+        float v[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            int c = c0 + j * nw, i = (c << 6) + lane;
+            v[j] = (c < nch && i < n) ? src[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            int c = c0 + j * nw;
+            if (c < nch) f(c, (c << 6) + lane, v[j]);
+        }
+    }
+}
+constexpr int SAMPLE_BATCH = 16;
+
+// ---- top-k (SamplerPipeline.cs:67-74, TopKSampler.ApplyTopK TopKSampler.cs:42-71) ------------
+// Scale by inv_temp in place, then emit every index whose scaled value is at least the k-th
+// largest (ties kept), in ascending index order, with its value. Two forms:
+//  - sample select over a grid (k <= 256, n >= 4096): one workgroup takes a threshold t from an
+//    evenly spaced sample of the scaled values, ranked so that a few hundred entries reach it;
+//    segments of 4096 entries (one workgroup each) scale their entries and count those reaching
+//    t, then gather them in index order into a candidate buffer; one workgroup finds the exact
+//    k-th largest among the candidates and emits. When fewer than k or more than 4096 entries
+//    reach t, that last workgroup runs the full select instead. A pass over the logits by one
+//    workgroup is bound by one CU's outstanding misses (about 25 us for 150k entries), so the
+//    full-width passes run on the grid;
+//  - the full select in one workgroup: a 4-pass radix select on order-preserving keys and a
+//    stable compaction.
+constexpr int TOPK_NS = 2048, TOPK_SEG = 4096;
+
+// Full radix select + stable compaction over x[0..n) (already scaled); one workgroup of 1024.
+__device__ void topk_radix_emit(const float* __restrict__ x, int n, int k, int cap, int* ids, float* vals,
+                                int* count) {
     __shared__ int hist[256];
     __shared__ uint32_t s_prefix, s_mask;
     __shared__ int s_remain;
+    __shared__ int chunk[SAMPLE_MAX_CHUNKS];
     __shared__ int scan[1024];
-    int tid = threadIdx.x, nt = blockDim.x;
-    if (inv_temp != 1.0f) {
-        for (int64_t i = tid; i < n; i += nt) x[i] = x[i] * inv_temp;
-        __threadfence_block();
-    }
+    const int tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
+    const int nch = (n + 63) >> 6;
     if (tid == 0) { s_prefix = 0; s_mask = 0; s_remain = k; }
     __syncthreads();
     uint32_t thr = 0;
     if (k < n) {
         for (int pass = 0; pass < 4; pass++) {
-            int shift = 24 - 8 * pass;
+            const int shift = 24 - 8 * pass;
             for (int b = tid; b < 256; b += nt) hist[b] = 0;
             __syncthreads();
-            uint32_t prefix = s_prefix, mask = s_mask;
-            for (int64_t i = tid; i < n; i += nt) {
-                uint32_t key = okey(x[i]);
-                if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-            }
+            const uint32_t prefix = s_prefix, mask = s_mask;
+            pass_strided<SAMPLE_BATCH>(x, n, [&](int i, float v) {
+                uint32_t key = okey(v);
+                wave_hist_add(hist, i < n && (key & mask) == prefix, (key >> shift) & 255u);
+            });
             __syncthreads();
             if (tid == 0) {
                 int cum = 0, rem = s_remain;
@@ -547,32 +669,204 @@ __global__ __launch_bounds__(1024) void k_topk(float* x, int64_t n, float inv_te
         }
         thr = s_prefix;
     }
-    // stable compaction: thread t owns indices [t*per, (t+1)*per)
-    int64_t per = (n + nt - 1) / nt;
-    int64_t beg = (int64_t)tid * per, end = min(beg + per, n);
-    int c = 0;
-    for (int64_t i = beg; i < end; i++) c += okey(x[i]) >= thr ? 1 : 0;
-    scan[tid] = c;
+    // stable compaction: survivors per 64-element chunk, chunk offsets, then ranks by ballot
+    pass_chunks<SAMPLE_BATCH>(x, n, nch, [&](int c, int i, float v) {
+        unsigned long long m = __ballot(i < n && okey(v) >= thr);
+        if (lane == 0) chunk[c] = (int)__popcll(m);
+    });
     __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int t = 0; t < nt; t++) { int v = scan[t]; scan[t] = run; run += v; }
-        *count = run;
+    int total = chunks_excl_scan(chunk, nch, scan);
+    if (tid == 0) *count = total;
+    pass_chunks<SAMPLE_BATCH>(x, n, nch, [&](int c, int i, float v) {
+        bool keep = i < n && okey(v) >= thr;
+        unsigned long long m = __ballot(keep);
+        if (keep) {
+            int off = chunk[c] + (int)__popcll(m & lanes_below());
+            if (off < cap) { ids[off] = i; vals[off] = v; }
+        }
+    });
+}
+
+// Exact k-th largest among the nc candidates (values cv, indices ci, in ascending index order)
+// and the survivors emitted in that order; one workgroup of 1024, nc <= TOPK_CMAX.
+__device__ void topk_select_candidates(const float* __restrict__ cv, const int* __restrict__ ci, int nc, int k,
+                                       int cap, int* ids, float* vals, int* count) {
+    __shared__ float lv[TOPK_CMAX];
+    __shared__ int hist[256];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ int s_remain;
+    __shared__ int scan[1024];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int j = tid; j < nc; j += nt) lv[j] = cv[j];
+    if (tid == 0) { s_prefix = 0; s_mask = 0; s_remain = k; }
+    __syncthreads();
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        for (int b = tid; b < 256; b += nt) hist[b] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+        for (int j = tid; j < nc; j += nt) {
+            uint32_t key = okey(lv[j]);
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int cum = 0, rem = s_remain;
+            for (int b = 255; b >= 0; b--) {
+                if (cum + hist[b] >= rem) {
+                    s_prefix = prefix | ((uint32_t)b << shift);
+                    s_mask = mask | (255u << shift);
+                    s_remain = rem - cum;
+                    break;
+                }
+                cum += hist[b];
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t thr = s_prefix;
+    const int per = (TOPK_CMAX + nt - 1) / nt, b0 = tid * per;
+    int cnt = 0;
+    for (int j = b0; j < b0 + per && j < nc; j++) cnt += okey(lv[j]) >= thr ? 1 : 0;
+    int total;
+    int off = block_excl_scan(cnt, scan, &total);
+    for (int j = b0; j < b0 + per && j < nc; j++) {
+        float v = lv[j];
+        if (okey(v) >= thr) {
+            if (off < cap) { ids[off] = ci[j]; vals[off] = v; }
+            off++;
+        }
+    }
+    if (tid == 0) *count = total;
+}
+
+__global__ __launch_bounds__(1024) void k_topk(float* x, int64_t n64, float inv_temp, int k, int cap, int* ids,
+                                                float* vals, int* count) {
+    const int n = (int)n64;
+    if (inv_temp != 1.0f)
+        pass_strided<SAMPLE_BATCH>(x, n, [&](int i, float v) { if (i < n) x[i] = v * inv_temp; });
+    __syncthreads();
+    topk_radix_emit(x, n, k, cap, ids, vals, count);
+}
+
+// The sample's threshold: keys of the scaled values at j * n / NS, sorted descending (bitonic), the
+// r-th largest with r = 4 k NS / n + 8 (about 4 k + 8 n / NS entries of the whole reach it).
+__global__ __launch_bounds__(1024) void k_topk_sample(const float* __restrict__ x, int n, float inv_temp, int k,
+                                                      TopkScratch* sc) {
+    __shared__ uint32_t samp[TOPK_NS];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int j = tid; j < TOPK_NS; j += nt) {
+        float v = x[(int)(((int64_t)j * n) / TOPK_NS)];
+        samp[j] = okey(inv_temp != 1.0f ? v * inv_temp : v);
     }
     __syncthreads();
-    int off = scan[tid];
-    for (int64_t i = beg; i < end; i++) {
-        float v = x[i];
-        if (okey(v) >= thr) {
-            if (off < cap) { ids[off] = (int)i; vals[off] = v; }
-            off++;
+    for (int size = 2; size <= TOPK_NS; size <<= 1)
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = tid; t < TOPK_NS / 2; t += nt) {
+                int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
+                bool up = (i & size) == 0;
+                uint32_t a = samp[i], b = samp[j];
+                if ((a < b) == up) { samp[i] = b; samp[j] = a; }
+            }
+            __syncthreads();
+        }
+    const int r = (int)min((int64_t)TOPK_NS, (int64_t)4 * k * TOPK_NS / n + 8);
+    if (tid == 0) sc->t = samp[r - 1];
+}
+
+// Segment blockIdx.x (TOPK_SEG entries, 16 per thread): scale in place, count keys >= t.
+__global__ __launch_bounds__(256) void k_topk_count(float* x, int n, float inv_temp, TopkScratch* sc) {
+    __shared__ int red[4];
+    const uint32_t t = sc->t;
+    const int beg = blockIdx.x * TOPK_SEG, tid = threadIdx.x;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + j * 256 + tid;
+        v[j] = i < n ? x[i] : 0.0f;
+    }
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + j * 256 + tid;
+        if (i < n) {
+            float w = v[j];
+            if (inv_temp != 1.0f) {
+                w = w * inv_temp;
+                x[i] = w;
+            }
+            c += okey(w) >= t ? 1 : 0;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+    if (lane_id() == 0) red[tid >> 6] = c;
+    __syncthreads();
+    if (tid == 0) sc->wg_cnt[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// Segment blockIdx.x: its offset among the candidates (counts of the segments before it), then
+// its entries with keys >= t written there in index order (64-entry chunks ranked by ballot).
+__global__ __launch_bounds__(256) void k_topk_gather(const float* __restrict__ x, int n, int k, int nseg,
+                                                     TopkScratch* sc) {
+    __shared__ int cc[TOPK_SEG / 64];
+    const uint32_t t = sc->t;
+    int off = 0, total = 0;
+    for (int h = 0; h < nseg; h++) {
+        int c = sc->wg_cnt[h];
+        off += h < (int)blockIdx.x ? c : 0;
+        total += c;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) sc->nc = total;
+    if (total < k || total > TOPK_CMAX) return;  // uniform: the finishing kernel runs the full select
+    const int wave = threadIdx.x >> 6, lane = lane_id(), beg = blockIdx.x * TOPK_SEG;
+    float v[16];
+    unsigned long long m[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + ((wave * 16 + j) << 6) + lane;
+        v[j] = i < n ? x[i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + ((wave * 16 + j) << 6) + lane;
+        m[j] = __ballot(i < n && okey(v[j]) >= t);
+        if (lane == 0) cc[wave * 16 + j] = (int)__popcll(m[j]);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int q = 0; q < TOPK_SEG / 64; q++) { int c = cc[q]; cc[q] = run; run += c; }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        if ((m[j] >> lane) & 1ull) {
+            int i = beg + ((wave * 16 + j) << 6) + lane;
+            int o = off + cc[wave * 16 + j] + (int)__popcll(m[j] & lanes_below());
+            sc->cand_v[o] = v[j];
+            sc->cand_i[o] = i;
         }
     }
 }
 
+__global__ __launch_bounds__(1024) void k_topk_finish(const float* __restrict__ x, int n, int k, int cap, int* ids,
+                                                       float* vals, int* count, const TopkScratch* sc) {
+    const int nc = sc->nc;
+    if (nc >= k && nc <= TOPK_CMAX) topk_select_candidates(sc->cand_v, sc->cand_i, nc, k, cap, ids, vals, count);
+    else topk_radix_emit(x, n, k, cap, ids, vals, count);  // x was scaled by k_topk_count
+}
+
 hipError_t launch_topk(float* x, int64_t n, float inv_temp, int k, int cap, int* ids, float* vals, int* count,
-                       hipStream_t st) {
-    k_topk<<<1, 1024, 0, st>>>(x, n, inv_temp, k, cap, ids, vals, count);
+                       TopkScratch* sc, hipStream_t st) {
+    const int nseg = (int)((n + TOPK_SEG - 1) / TOPK_SEG);
+    if (sc && k <= 256 && k < n && n >= 2 * TOPK_NS && nseg <= TOPK_MAX_SEG) {
+        k_topk_sample<<<1, 1024, 0, st>>>(x, (int)n, inv_temp, k, sc);
+        k_topk_count<<<nseg, 256, 0, st>>>(x, (int)n, inv_temp, sc);
+        k_topk_gather<<<nseg, 256, 0, st>>>(x, (int)n, k, nseg, sc);
+        k_topk_finish<<<1, 1024, 0, st>>>(x, (int)n, k, cap, ids, vals, count, sc);
+    } else {
+        k_topk<<<1, 1024, 0, st>>>(x, n, inv_temp, k, cap, ids, vals, count);
+    }
     return hipGetLastError();
 }
 
@@ -625,25 +919,6 @@ __device__ __forceinline__ T block_reduce(T v, T* red, Op op) {
     return r;
 }
 
-// Exclusive prefix over the block of one value per thread (Hillis-Steele in LDS); returns the
-// thread's exclusive prefix and writes the block total.
-__device__ __forceinline__ unsigned long long block_excl_scan(unsigned long long v, unsigned long long* buf,
-                                                              unsigned long long* total) {
-    int t = threadIdx.x, nt = blockDim.x;
-    buf[t] = v;
-    __syncthreads();
-    for (int o = 1; o < nt; o <<= 1) {
-        unsigned long long a = t >= o ? buf[t - o] : 0ull;
-        __syncthreads();
-        buf[t] += a;
-        __syncthreads();
-    }
-    unsigned long long incl = buf[t];
-    *total = buf[nt - 1];
-    __syncthreads();
-    return incl - v;
-}
-
 // SamplerPipeline.Sample (SamplerPipeline.cs:58-89) with topK disabled, on the device logits:
 // scale by inv_temp in place (stage 1), softmax (stage 3, TensorOperations.cs:23-39: max,
 // exp(x - max), divide by the sum) into pr, nucleus of top_p (stage 4, TopPSampler.ApplyTopP
@@ -652,50 +927,64 @@ __device__ __forceinline__ unsigned long long block_excl_scan(unsigned long long
 // TemperatureSampler.SampleFromProbabilities TemperatureSampler.cs:53-70: the first index whose
 // running sum exceeds u, else the last nonzero index). Running sums and masses are exact
 // fixed-point integers where the reference accumulates in f32 order, so the chosen token can
-// differ only where u or top_p lies within f32 rounding of a boundary.
-// One workgroup; thread t owns the contiguous index range [t*per, (t+1)*per) for the ordered
-// passes.
+// differ only where u or top_p lies within f32 rounding of a boundary. One workgroup.
 __global__ __launch_bounds__(1024) void k_sample_nucleus(float* x, int n, float inv_temp, float top_p, float u,
                                                          float* pr, int* out_token) {
     __shared__ float redf[16];
-    __shared__ unsigned long long redu[16];
+    __shared__ int redi[32];
     __shared__ unsigned long long hist[256];
+    __shared__ unsigned long long chunk[SAMPLE_MAX_CHUNKS];
     __shared__ unsigned long long scanbuf[1024];
     __shared__ uint32_t s_prefix, s_mask;
     __shared__ unsigned long long s_above;
-    __shared__ int s_all;
-    const int tid = threadIdx.x, nt = blockDim.x;
-    if (inv_temp != 1.0f)
-        for (int i = tid; i < n; i += nt) x[i] = x[i] * inv_temp;
+    __shared__ int s_all, s_chunk;
+    const int tid = threadIdx.x, nt = blockDim.x, wave = tid >> 6, lane = lane_id(), nw = nt >> 6;
+    const int nch = (n + 63) >> 6;
     float mx = -INFINITY;
-    for (int i = tid; i < n; i += nt) mx = fmaxf(mx, x[i]);
+    pass_strided<SAMPLE_BATCH>(x, n, [&](int i, float v) {
+        if (i < n) {
+            if (inv_temp != 1.0f) {
+                v = v * inv_temp;
+                x[i] = v;  // read back below by this same thread
+            }
+            mx = fmaxf(mx, v);
+        }
+    });
     mx = block_reduce(mx, redf, [](float a, float b) { return fmaxf(a, b); });
     float sum = 0.0f;
-    for (int i = tid; i < n; i += nt) {
-        float e = expf(x[i] + (-mx));
-        pr[i] = e;
-        sum += e;
-    }
+    pass_strided<SAMPLE_BATCH>(x, n, [&](int i, float v) {
+        if (i < n) {
+            float e = expf(v + (-mx));
+            pr[i] = e;
+            sum += e;
+        }
+    });
     sum = block_reduce(sum, redf, [](float a, float b) { return a + b; });
-    for (int i = tid; i < n; i += nt) pr[i] = pr[i] / sum;
-    const int per = (n + nt - 1) / nt;
-    const int beg = min(tid * per, n), end = min(beg + per, n);
+    pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float v) { if (i < n) pr[i] = v / sum; });
     __syncthreads();
     if (top_p < 1.0f) {
         // threshold tau = probability at the nucleus edge: radix select from the top over the
         // probabilities' bit patterns (non-negative floats order as integers), weighing each
         // 8-bit bucket by its mass
         const unsigned long long P = fix63(top_p);
+        unsigned long long* whist = chunk + wave * 256;  // per-wave histograms (the chunk array is free here)
         if (tid == 0) { s_prefix = 0; s_mask = 0; s_above = 0; s_all = 0; }
         for (int pass = 0; pass < 4; pass++) {
             const int shift = 24 - 8 * pass;
-            for (int b = tid; b < 256; b += nt) hist[b] = 0ull;
+            for (int b = tid; b < 16 * 256; b += nt) chunk[b] = 0ull;
             __syncthreads();
             const uint32_t prefix = s_prefix, mask = s_mask;
-            for (int i = tid; i < n; i += nt) {
-                float p = pr[i];
-                uint32_t key = __float_as_uint(p);
-                if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], fix63(p));
+            if (!s_all) {
+                pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float p) {
+                    uint32_t key = __float_as_uint(p);
+                    if (i < n && (key & mask) == prefix) atomicAdd(&whist[(key >> shift) & 255u], fix63(p));
+                });
+            }
+            __syncthreads();
+            for (int b = tid; b < 256; b += nt) {
+                unsigned long long h = 0;
+                for (int w = 0; w < 16; w++) h += chunk[w * 256 + b];
+                hist[b] = h;
             }
             __syncthreads();
             if (tid == 0 && !s_all) {
@@ -716,12 +1005,14 @@ __global__ __launch_bounds__(1024) void k_sample_nucleus(float* x, int n, float 
         }
         const uint32_t tau = s_prefix;
         const bool all = s_all != 0;
-        // equal probabilities at the edge: the first m of them in index order
-        unsigned long long ties = 0;
-        if (!all)
-            for (int i = beg; i < end; i++) ties += __float_as_uint(pr[i]) == tau ? 1ull : 0ull;
-        unsigned long long ntie = 0;
-        unsigned long long tie0 = block_excl_scan(ties, scanbuf, &ntie);
+        // equal probabilities at the edge: the first m of them in index order (tie ranks from
+        // per-chunk counts and ballots)
+        pass_chunks<SAMPLE_BATCH>(pr, n, nch, [&](int c, int i, float p) {
+            unsigned long long m = __ballot(!all && i < n && __float_as_uint(p) == tau);
+            if (lane == 0) chunk[c] = __popcll(m);
+        });
+        __syncthreads();
+        unsigned long long ntie = chunks_excl_scan(chunk, nch, scanbuf);
         unsigned long long m = ntie;
         if (!all) {
             unsigned long long ft = fix63(__uint_as_float(tau)), need = P - s_above;
@@ -731,38 +1022,54 @@ __global__ __launch_bounds__(1024) void k_sample_nucleus(float* x, int n, float 
             }
         }
         float kept = 0.0f;
-        unsigned long long r = tie0;
-        for (int i = beg; i < end; i++) {
-            float p = pr[i];
+        pass_chunks<SAMPLE_BATCH>(pr, n, nch, [&](int c, int i, float p) {
             uint32_t key = __float_as_uint(p);
-            bool keep = all || key > tau || (key == tau && r++ < m);
-            if (!keep) pr[i] = 0.0f;
-            else kept += p;
-        }
+            bool tie = !all && i < n && key == tau;
+            unsigned long long tm = __ballot(tie);
+            bool keep = i < n && (all || key > tau || (tie && chunk[c] + __popcll(tm & lanes_below()) < m));
+            if (i < n) {
+                if (!keep) pr[i] = 0.0f;
+                else kept += p;
+            }
+        });
         kept = block_reduce(kept, redf, [](float a, float b) { return a + b; });
         if (kept > 0.0f)
-            for (int i = beg; i < end; i++) pr[i] = pr[i] / kept;
+            pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float v) { if (i < n) pr[i] = v / kept; });
         __syncthreads();
     }
-    // draw: first index whose running mass exceeds u
+    // draw: first index whose running mass exceeds u. Chunk masses, their prefix, the chunk that
+    // holds u, then the lane inside it.
     const unsigned long long U = fix63(u);
-    unsigned long long part = 0;
-    for (int i = beg; i < end; i++) part += fix63(pr[i]);
-    unsigned long long total = 0;
-    unsigned long long base = block_excl_scan(part, scanbuf, &total);
+    pass_chunks<SAMPLE_BATCH>(pr, n, nch, [&](int c, int i, float p) {
+        unsigned long long v = i < n ? fix63(p) : 0ull;
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        if (lane == 0) chunk[c] = v;
+    });
+    __syncthreads();
+    if (tid == 0) s_chunk = -1;
+    __syncthreads();
+    unsigned long long total = chunks_excl_scan(chunk, nch, scanbuf);
+    for (int c = tid; c < nch; c += nt) {
+        unsigned long long hi = c + 1 < nch ? chunk[c + 1] : total;
+        if (chunk[c] <= U && U < hi) s_chunk = c;  // exactly one chunk can hold U
+    }
+    __syncthreads();
     int found = 0x7fffffff;
-    if (U < base + part && U >= base) {
-        unsigned long long run = base;
-        for (int i = beg; i < end; i++) {
-            run += fix63(pr[i]);
-            if (U < run) { found = i; break; }
+    const int cs = s_chunk;
+    if (cs >= 0 && wave == 0) {
+        int i = (cs << 6) + lane;
+        unsigned long long v = i < n ? fix63(pr[i]) : 0ull, incl = v;
+        for (int o = 1; o < 64; o <<= 1) {
+            unsigned long long a = __shfl_up(incl, o);
+            if (lane >= o) incl += a;
         }
+        unsigned long long hit = __ballot(i < n && U < chunk[cs] + incl);
+        if (hit) found = (cs << 6) + (__ffsll((long long)hit) - 1);
     }
     int last = -1;  // fallback: the last nonzero probability
-    for (int i = beg; i < end; i++)
-        if (pr[i] > 0.0f) last = i;
-    found = block_reduce(found, (int*)redu, [](int a, int b) { return a < b ? a : b; });
-    last = block_reduce(last, (int*)redu + 16, [](int a, int b) { return a > b ? a : b; });
+    pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float p) { if (i < n && p > 0.0f) last = i; });
+    found = block_reduce(found, redi, [](int a, int b) { return a < b ? a : b; });
+    last = block_reduce(last, redi + 16, [](int a, int b) { return a > b ? a : b; });
     if (tid == 0) *out_token = found != 0x7fffffff ? found : (last >= 0 ? last : n - 1);
 }
 

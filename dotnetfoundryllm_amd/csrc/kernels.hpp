@@ -55,8 +55,21 @@ hipError_t launch_argmax(const float* x, int64_t n, StepParams* p, int* tokens_o
 // reduce per-workgroup argmax keys of the fused LM head; advances the step as launch_argmax
 hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams* p, int* tokens_out, int tokens_cap,
                               hipStream_t st);
+// largest vocabulary of the one-workgroup samplers (launch_topk, launch_sample_nucleus)
+constexpr int SAMPLE_MAX_VOCAB = 262144;
+// Device scratch of the grid form of launch_topk: the sample's threshold key, per-segment counts
+// (segments of 4096 entries), the candidates reaching the threshold in index order.
+constexpr int TOPK_CMAX = 4096, TOPK_MAX_SEG = SAMPLE_MAX_VOCAB / 4096;
+struct TopkScratch {
+    uint32_t t;
+    int nc;
+    int wg_cnt[TOPK_MAX_SEG];
+    float cand_v[TOPK_CMAX];
+    int cand_i[TOPK_CMAX];
+};
+// sc may be null (one-workgroup form only)
 hipError_t launch_topk(float* x, int64_t n, float inv_temp, int k, int cap, int* ids, float* vals, int* count,
-                       hipStream_t st);
+                       TopkScratch* sc, hipStream_t st);
 // LlamaLanguageModel.ApplyRepetitionPenalty on device logits; counts: n zeroed ints, left zeroed.
 hipError_t launch_rep_penalty(float* x, int n, const int* ids, int n_ids, float penalty, int* counts,
                               hipStream_t st);

@@ -715,6 +715,12 @@ extern "C" int32_t fllmh_sampler_sample(fllmh_sampler* s, fllm_seq* seq, int32_t
     int32_t V = 0;
     int32_t rc = seq_vocab(seq, &V);
     if (rc) return rc;
+    if (V > 262144) {  // beyond the device samplers' one-workgroup limit: the pipeline on the host
+        s->buf.resize((size_t)V);
+        rc = fllm_logits_copy(seq, s->buf.data(), V);
+        if (rc) return dfail(rc);
+        return fllmh_sampler_sample_host(s, s->buf.data(), V, out_token);
+    }
     if (s->top_k > 0 && s->top_k < V) {
         // stages 1-2 on the device (scale, top-k with ties kept), stages 3-5 on the survivors:
         // every filtered logit is -inf, so its probability is exactly 0 and the CDF walk in

@@ -207,7 +207,8 @@ FLLM_API int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token);
  * TopKSampler.ApplyTopK TopKSampler.cs:42-71): scales the logits by inv_temp in place
  * (when inv_temp != 1), finds the k-th largest scaled value and returns every index whose
  * scaled logit is >= that threshold (ties kept), in ascending index order, with the scaled
- * values. cap is the capacity of ids/vals; FLLM_E_ARG if more than cap survive. */
+ * values. cap is the capacity of ids/vals; FLLM_E_ARG if more than cap survive. One workgroup;
+ * vocabularies above 262144 -> FLLM_E_NOT_SUPPORTED. */
 FLLM_API int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k,
                                   int32_t* ids, float* vals, int32_t cap, int32_t* n_out);
 /* LlamaLanguageModel.ApplyRepetitionPenalty (LlamaLanguageModel.cs:183-186, 357-373) on the device
@@ -224,7 +225,8 @@ FLLM_API int32_t fllm_logits_penalize(fllm_seq* s, const int32_t* ids, int32_t n
  * TemperatureSampler.cs:53-70), u being the pipeline's XoshiroRandom.NextFloat() for this draw.
  * Running sums are exact fixed-point where the reference sums f32 in order: the token can differ
  * from the reference only when u or top_p falls within f32 rounding of a boundary.
- * Errors: top_p outside (0,1], u outside [0,1), inv_temp not positive and finite -> FLLM_E_ARG_RANGE. */
+ * Errors: top_p outside (0,1], u outside [0,1), inv_temp not positive and finite -> FLLM_E_ARG_RANGE;
+ * vocabularies above 262144 -> FLLM_E_NOT_SUPPORTED (one workgroup). */
 FLLM_API int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p, float u, int32_t* out_token);
 /* The distribution fllm_sample_nucleus drew from (vocab floats: the renormalised nucleus, zeros
  * elsewhere); a parity hook. */

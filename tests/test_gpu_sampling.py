@@ -230,3 +230,37 @@ def test_token_loop_with_repetition_penalty(ctx, penalty):
         orc.close()
         kv.close()
         m.close()
+
+
+def test_topk_sample_select_and_fallback(big_vocab):
+    """Top-k over the 32000 vocabulary: the sample-select path (a threshold from 2048 evenly spaced
+    entries, then an exact select among the entries reaching it) and both of its fallbacks to the
+    full radix select (too few entries reach the sample's threshold; too many, with all logits
+    equal) give the oracle's survivors, ties kept, in index order."""
+    desc, m, kv, fwd = big_vocab
+    V = desc.vocab
+    rng = np.random.default_rng(17)
+    sampled = (np.arange(2048, dtype=np.int64) * V) // 2048
+    cases = []
+    lg = rng.standard_normal(V).astype(np.float32)
+    cases.append((lg, 40))
+    lg = lg.copy()
+    # the sample's top is the array's top: its 18th largest (the threshold for k = 40 over 32000)
+    # is reached by 18 entries only, fewer than k
+    lg[sampled[:30]] = 100.0 + np.arange(30, dtype=np.float32)
+    cases.append((lg, 40))
+    cases.append((np.full(V, 0.5, dtype=np.float32), 40))  # every entry ties
+    lg = np.round(rng.standard_normal(V) * 2, 1).astype(np.float32)
+    cases.append((lg, 256))
+    cases.append((lg, 1))
+    for lg, k in cases:
+        for inv in (1.0, 1.25):
+            fwd.write_logits(lg)
+            ids, vals = fwd.sample_topk(inv, k, cap=V)
+            scaled = lg * np.float32(inv) if inv != 1.0 else lg.copy()
+            ref = scaled.copy()
+            O.lib.orc_apply_topk(O.fp(ref), ref.size, k)
+            keep = np.nonzero(ref != -np.inf)[0]
+            assert np.array_equal(ids, keep)
+            assert np.array_equal(vals, scaled[keep])
+            assert np.array_equal(fwd.logits, scaled)
