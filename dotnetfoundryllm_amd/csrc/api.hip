@@ -134,6 +134,7 @@ struct fllm_seq {
     int* pen_counts = nullptr;    // repetition-penalty counters (vocab ints, zero between calls)
     int* pen_ids = nullptr;       // the penalised ids of the last call (device copy)
     TopkScratch* topk_sc = nullptr;  // grid top-k: threshold, segment counts, candidates
+    NucleusScratch* nuc_sc = nullptr;  // grid nucleus sampler: edge histograms, segment results
     int pen_cap = 0;
     float* hidden_dbg = nullptr;
     bool debug = false;
@@ -769,6 +770,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->samp_token, 1);
     ALLOC(s->pen_counts, (size_t)d.vocab);
     ALLOC(s->topk_sc, 1);
+    ALLOC(s->nuc_sc, 1);
     ALLOC(s->hidden_dbg, (L + 1) * H);
     ALLOC(s->x2, H);
 #undef ALLOC
@@ -787,6 +789,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     if (e == hipSuccess) e = hipMemsetAsync(s->params, 0, sizeof(StepParams), s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, sizeof(float) * kvsz, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->pen_counts, 0, sizeof(int) * (size_t)d.vocab, s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->nuc_sc, 0, sizeof(NucleusScratch), s->st);
     if (e == hipSuccess) e = hipStreamSynchronize(s->st);
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_DEVICE, "sequence init: %s", hipGetErrorString(e)); }
     *out = s;
@@ -1563,7 +1566,7 @@ extern "C" int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p,
     if (!(inv_temp > 0.0f) || isinf(inv_temp)) return fail(FLLM_E_ARG_RANGE, "inv_temp must be positive and finite.");
     int V = s->m->d.vocab;
     if (V > SAMPLE_MAX_VOCAB) return fail(FLLM_E_NOT_SUPPORTED, "device nucleus sampling handles vocabularies up to %d", SAMPLE_MAX_VOCAB);
-    HIP_TRY(launch_sample_nucleus(s->logits, V, inv_temp, top_p, u, s->probs, s->samp_token, s->st));
+    HIP_TRY(launch_sample_nucleus(s->logits, V, inv_temp, top_p, u, s->probs, s->samp_token, s->nuc_sc, s->st));
     if (inv_temp != 1.0f) s->argmax_valid = false;
     int tok = 0;
     HIP_TRY(hipMemcpyAsync(&tok, s->samp_token, sizeof(int), hipMemcpyDeviceToHost, s->st));

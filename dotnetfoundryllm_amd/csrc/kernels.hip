@@ -629,6 +629,14 @@ constexpr int SAMPLE_BATCH = 16;
 //    stable compaction.
 constexpr int TOPK_NS = 2048, TOPK_SEG = 4096;
 
+// Copies the first nseg entries of a per-segment array into LDS (nseg <= blockDim.x), one load per
+// thread, so that one thread can then combine them in order without a chain of memory loads.
+template <typename T>
+__device__ __forceinline__ void load_segs(const T* __restrict__ src, int nseg, T* dst) {
+    if ((int)threadIdx.x < nseg) dst[threadIdx.x] = src[threadIdx.x];
+    __syncthreads();
+}
+
 // Full radix select + stable compaction over x[0..n) (already scaled); one workgroup of 1024.
 __device__ void topk_radix_emit(const float* __restrict__ x, int n, int k, int cap, int* ids, float* vals,
                                 int* count) {
@@ -809,13 +817,21 @@ __global__ __launch_bounds__(256) void k_topk_count(float* x, int n, float inv_t
 __global__ __launch_bounds__(256) void k_topk_gather(const float* __restrict__ x, int n, int k, int nseg,
                                                      TopkScratch* sc) {
     __shared__ int cc[TOPK_SEG / 64];
+    __shared__ int segc[TOPK_MAX_SEG];
+    __shared__ int s_off, s_total;
     const uint32_t t = sc->t;
-    int off = 0, total = 0;
-    for (int h = 0; h < nseg; h++) {
-        int c = sc->wg_cnt[h];
-        off += h < (int)blockIdx.x ? c : 0;
-        total += c;
+    load_segs(sc->wg_cnt, nseg, segc);
+    if (threadIdx.x == 0) {
+        int o = 0, tot = 0;
+        for (int h = 0; h < nseg; h++) {
+            o += h < (int)blockIdx.x ? segc[h] : 0;
+            tot += segc[h];
+        }
+        s_off = o;
+        s_total = tot;
     }
+    __syncthreads();
+    const int off = s_off, total = s_total;
     if (blockIdx.x == 0 && threadIdx.x == 0) sc->nc = total;
     if (total < k || total > TOPK_CMAX) return;  // uniform: the finishing kernel runs the full select
     const int wave = threadIdx.x >> 6, lane = lane_id(), beg = blockIdx.x * TOPK_SEG;
@@ -925,157 +941,391 @@ __device__ __forceinline__ T block_reduce(T v, T* red, Op op) {
 // TopPSampler.cs:60-110: the shortest prefix of the descending order whose mass reaches top_p,
 // equal probabilities by ascending index, then divided by the kept sum), and the draw (stage 5,
 // TemperatureSampler.SampleFromProbabilities TemperatureSampler.cs:53-70: the first index whose
-// running sum exceeds u, else the last nonzero index). Running sums and masses are exact
+// running sum exceeds u, else the last nonzero index). Masses and running sums are exact
 // fixed-point integers where the reference accumulates in f32 order, so the chosen token can
-// differ only where u or top_p lies within f32 rounding of a boundary. One workgroup.
-__global__ __launch_bounds__(1024) void k_sample_nucleus(float* x, int n, float inv_temp, float top_p, float u,
-                                                         float* pr, int* out_token) {
-    __shared__ float redf[16];
-    __shared__ int redi[32];
-    __shared__ unsigned long long hist[256];
-    __shared__ unsigned long long chunk[SAMPLE_MAX_CHUNKS];
-    __shared__ unsigned long long scanbuf[1024];
-    __shared__ uint32_t s_prefix, s_mask;
-    __shared__ unsigned long long s_above;
-    __shared__ int s_all, s_chunk;
-    const int tid = threadIdx.x, nt = blockDim.x, wave = tid >> 6, lane = lane_id(), nw = nt >> 6;
-    const int nch = (n + 63) >> 6;
-    float mx = -INFINITY;
-    pass_strided<SAMPLE_BATCH>(x, n, [&](int i, float v) {
-        if (i < n) {
-            if (inv_temp != 1.0f) {
-                v = v * inv_temp;
-                x[i] = v;  // read back below by this same thread
+// differ only where u or top_p lies within f32 rounding of a boundary.
+// Every full-width pass runs over segments of NUC_SEG entries, one workgroup of 256 each (16
+// entries per thread); per-segment results (max, sums, tie counts, masses) go through the
+// scratch, whose f32 sums are taken in segment order, so results are deterministic. The nucleus
+// edge tau comes from a 4-level radix select over the probabilities' bit patterns weighted by
+// mass: each level's segments add their workgroup histogram into the scratch, and every
+// workgroup of the next level re-derives the selection from the levels before it.
+constexpr int NUC_SEG = 4096;
+
+template <typename T>
+__device__ __forceinline__ T wg256_sum(T v, T* red) {  // ordered: lanes by xor tree, then waves 0..3
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+// Loads the first `levels` mass histograms and derives the selection: tau's bits so far (prefix
+// under mask), the mass strictly above them (above), or `all` when the whole mass stays below P.
+struct NucSel {
+    uint32_t prefix, mask;
+    unsigned long long above;
+    int all;
+};
+__device__ NucSel nuc_select(const NucleusScratch* sc, int levels, unsigned long long P, unsigned long long* lh,
+                             NucSel* out) {
+    for (int j = threadIdx.x; j < levels * 256; j += blockDim.x) lh[j] = sc->hist[j >> 8][j & 255];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        NucSel r{0u, 0u, 0ull, 0};
+        for (int L = 0; L < levels && !r.all; L++) {
+            const int shift = 24 - 8 * L;
+            unsigned long long acc = r.above;
+            int b = 255;
+            for (; b >= 0; b--) {
+                if (acc + lh[L * 256 + b] >= P) break;
+                acc += lh[L * 256 + b];
             }
-            mx = fmaxf(mx, v);
+            if (b < 0) r.all = 1;
+            else {
+                r.prefix |= (uint32_t)b << shift;
+                r.mask |= 255u << shift;
+                r.above = acc;
+            }
         }
-    });
-    mx = block_reduce(mx, redf, [](float a, float b) { return fmaxf(a, b); });
-    float sum = 0.0f;
-    pass_strided<SAMPLE_BATCH>(x, n, [&](int i, float v) {
+        *out = r;
+    }
+    __syncthreads();
+    return *out;
+}
+
+__global__ __launch_bounds__(256) void k_nuc_max(float* x, int n, float inv_temp, NucleusScratch* sc) {
+    __shared__ float red[4];
+    const int beg = blockIdx.x * NUC_SEG, tid = threadIdx.x;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) { int i = beg + j * 256 + tid; v[j] = i < n ? x[i] : -INFINITY; }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + j * 256 + tid;
         if (i < n) {
-            float e = expf(v + (-mx));
+            if (inv_temp != 1.0f) { v[j] = v[j] * inv_temp; x[i] = v[j]; }
+            m = fmaxf(m, v[j]);
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) sc->seg_max[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(256) void k_nuc_exp(const float* __restrict__ x, int n, float* pr, int nseg,
+                                                 NucleusScratch* sc) {
+    __shared__ float red[4];
+    __shared__ float segv[NUC_MAX_SEG];
+    __shared__ float s_m;
+    const int beg = blockIdx.x * NUC_SEG, tid = threadIdx.x;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) { int i = beg + j * 256 + tid; v[j] = i < n ? x[i] : 0.0f; }
+    load_segs(sc->seg_max, nseg, segv);
+    if (tid == 0) {
+        float m = -INFINITY;
+        for (int h = 0; h < nseg; h++) m = fmaxf(m, segv[h]);
+        s_m = m;
+    }
+    __syncthreads();
+    const float mx = s_m;
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + j * 256 + tid;
+        if (i < n) {
+            float e = expf(v[j] + (-mx));
             pr[i] = e;
             sum += e;
         }
-    });
-    sum = block_reduce(sum, redf, [](float a, float b) { return a + b; });
-    pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float v) { if (i < n) pr[i] = v / sum; });
+    }
+    sum = wg256_sum(sum, red);
+    if (tid == 0) sc->seg_sum[blockIdx.x] = sum;
+}
+
+// p = e / sum; with top_p < 1 the level-0 mass histogram, else the draw's segment masses.
+__global__ __launch_bounds__(256) void k_nuc_norm(float* pr, int n, float top_p, int nseg, NucleusScratch* sc) {
+    __shared__ unsigned long long hist[256];
+    __shared__ unsigned long long redu[4];
+    __shared__ int redi[4];
+    __shared__ float s_sum;
+    __shared__ float segv[NUC_MAX_SEG];
+    const int beg = blockIdx.x * NUC_SEG, tid = threadIdx.x;
+    hist[tid] = 0ull;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) { int i = beg + j * 256 + tid; v[j] = i < n ? pr[i] : 0.0f; }
+    load_segs(sc->seg_sum, nseg, segv);
+    if (tid == 0) {
+        float t = 0.0f;
+        for (int h = 0; h < nseg; h++) t += segv[h];
+        s_sum = t;
+    }
     __syncthreads();
+    const float sum = s_sum;
+    unsigned long long mass = 0;
+    int last = -1;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + j * 256 + tid;
+        if (i < n) {
+            float p = v[j] / sum;
+            pr[i] = p;
+            if (top_p < 1.0f) atomicAdd(&hist[__float_as_uint(p) >> 24], fix63(p));
+            else {
+                mass += fix63(p);
+                if (p > 0.0f) last = i;
+            }
+        }
+    }
     if (top_p < 1.0f) {
-        // threshold tau = probability at the nucleus edge: radix select from the top over the
-        // probabilities' bit patterns (non-negative floats order as integers), weighing each
-        // 8-bit bucket by its mass
-        const unsigned long long P = fix63(top_p);
-        unsigned long long* whist = chunk + wave * 256;  // per-wave histograms (the chunk array is free here)
-        if (tid == 0) { s_prefix = 0; s_mask = 0; s_above = 0; s_all = 0; }
-        for (int pass = 0; pass < 4; pass++) {
-            const int shift = 24 - 8 * pass;
-            for (int b = tid; b < 16 * 256; b += nt) chunk[b] = 0ull;
-            __syncthreads();
-            const uint32_t prefix = s_prefix, mask = s_mask;
-            if (!s_all) {
-                pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float p) {
-                    uint32_t key = __float_as_uint(p);
-                    if (i < n && (key & mask) == prefix) atomicAdd(&whist[(key >> shift) & 255u], fix63(p));
-                });
-            }
-            __syncthreads();
-            for (int b = tid; b < 256; b += nt) {
-                unsigned long long h = 0;
-                for (int w = 0; w < 16; w++) h += chunk[w * 256 + b];
-                hist[b] = h;
-            }
-            __syncthreads();
-            if (tid == 0 && !s_all) {
-                unsigned long long acc = s_above;
-                int b = 255;
-                for (; b >= 0; b--) {
-                    if (acc + hist[b] >= P) break;
-                    acc += hist[b];
-                }
-                if (b < 0) s_all = 1;  // the whole mass stays below top_p: keep everything
-                else {
-                    s_prefix = prefix | ((uint32_t)b << shift);
-                    s_mask = mask | (255u << shift);
-                    s_above = acc;
-                }
-            }
-            __syncthreads();
-        }
-        const uint32_t tau = s_prefix;
-        const bool all = s_all != 0;
-        // equal probabilities at the edge: the first m of them in index order (tie ranks from
-        // per-chunk counts and ballots)
-        pass_chunks<SAMPLE_BATCH>(pr, n, nch, [&](int c, int i, float p) {
-            unsigned long long m = __ballot(!all && i < n && __float_as_uint(p) == tau);
-            if (lane == 0) chunk[c] = __popcll(m);
-        });
         __syncthreads();
-        unsigned long long ntie = chunks_excl_scan(chunk, nch, scanbuf);
-        unsigned long long m = ntie;
-        if (!all) {
-            unsigned long long ft = fix63(__uint_as_float(tau)), need = P - s_above;
-            if (ft > 0) {
-                unsigned long long q = (need + ft - 1) / ft;
-                m = q < ntie ? q : ntie;
-            }
-        }
-        float kept = 0.0f;
-        pass_chunks<SAMPLE_BATCH>(pr, n, nch, [&](int c, int i, float p) {
-            uint32_t key = __float_as_uint(p);
-            bool tie = !all && i < n && key == tau;
-            unsigned long long tm = __ballot(tie);
-            bool keep = i < n && (all || key > tau || (tie && chunk[c] + __popcll(tm & lanes_below()) < m));
-            if (i < n) {
-                if (!keep) pr[i] = 0.0f;
-                else kept += p;
-            }
-        });
-        kept = block_reduce(kept, redf, [](float a, float b) { return a + b; });
-        if (kept > 0.0f)
-            pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float v) { if (i < n) pr[i] = v / kept; });
+        if (hist[tid]) atomicAdd(&sc->hist[0][tid], hist[tid]);
+    } else {
+        mass = wg256_sum(mass, redu);
+        for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o));
+        if ((tid & 63) == 0) redi[tid >> 6] = last;
         __syncthreads();
+        if (tid == 0) {
+            sc->seg_mass[blockIdx.x] = mass;
+            sc->seg_last[blockIdx.x] = max(max(redi[0], redi[1]), max(redi[2], redi[3]));
+        }
     }
-    // draw: first index whose running mass exceeds u. Chunk masses, their prefix, the chunk that
-    // holds u, then the lane inside it.
+}
+
+// Radix level `level` (1..3) of the nucleus edge over the entries that match the levels before.
+__global__ __launch_bounds__(256) void k_nuc_hist(const float* __restrict__ pr, int n, float top_p, int level,
+                                                  NucleusScratch* sc) {
+    __shared__ unsigned long long lh[3 * 256];
+    __shared__ unsigned long long hist[256];
+    __shared__ NucSel s_sel;
+    const int beg = blockIdx.x * NUC_SEG, tid = threadIdx.x;
+    hist[tid] = 0ull;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) { int i = beg + j * 256 + tid; v[j] = i < n ? pr[i] : 0.0f; }
+    const NucSel sel = nuc_select(sc, level, fix63(top_p), lh, &s_sel);
+    if (sel.all) return;  // uniform
+    const int shift = 24 - 8 * level;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + j * 256 + tid;
+        uint32_t key = __float_as_uint(v[j]);
+        if (i < n && (key & sel.mask) == sel.prefix) atomicAdd(&hist[(key >> shift) & 255u], fix63(v[j]));
+    }
+    __syncthreads();
+    if (hist[tid]) atomicAdd(&sc->hist[level][tid], hist[tid]);
+}
+
+// Entries equal to the edge tau in each segment.
+__global__ __launch_bounds__(256) void k_nuc_ties(const float* __restrict__ pr, int n, float top_p,
+                                                  NucleusScratch* sc) {
+    __shared__ unsigned long long lh[4 * 256];
+    __shared__ int red[4];
+    __shared__ NucSel s_sel;
+    const int beg = blockIdx.x * NUC_SEG, tid = threadIdx.x;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) { int i = beg + j * 256 + tid; v[j] = i < n ? pr[i] : 0.0f; }
+    const NucSel sel = nuc_select(sc, 4, fix63(top_p), lh, &s_sel);
+    int c = 0;
+    if (!sel.all) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            int i = beg + j * 256 + tid;
+            c += (i < n && __float_as_uint(v[j]) == sel.prefix) ? 1 : 0;
+        }
+    }
+    c = wg256_sum(c, red);
+    if (tid == 0) sc->seg_tie[blockIdx.x] = c;
+}
+
+// Keep the nucleus (entries above tau, and the first m entries equal to it in index order),
+// zero the rest, and the kept f32 sum per segment.
+__global__ __launch_bounds__(256) void k_nuc_keep(float* pr, int n, float top_p, int nseg, NucleusScratch* sc) {
+    __shared__ unsigned long long lh[4 * 256];
+    __shared__ int cc[NUC_SEG / 64];
+    __shared__ float red[4];
+    __shared__ NucSel s_sel;
+    __shared__ unsigned long long s_tie0, s_ntie;
+    __shared__ int segt[NUC_MAX_SEG];
+    const int beg = blockIdx.x * NUC_SEG, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // 64-entry chunks: wave w takes chunks 16w .. 16w+15 of the segment, lane l entry l of each
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + ((wave * 16 + j) << 6) + lane;
+        v[j] = i < n ? pr[i] : 0.0f;
+    }
+    load_segs(sc->seg_tie, nseg, segt);
+    if (tid == 0) {
+        unsigned long long t0 = 0, nt = 0;
+        for (int h = 0; h < nseg; h++) {
+            unsigned long long c = (unsigned long long)segt[h];
+            t0 += h < (int)blockIdx.x ? c : 0ull;
+            nt += c;
+        }
+        s_tie0 = t0;
+        s_ntie = nt;
+    }
+    const NucSel sel = nuc_select(sc, 4, fix63(top_p), lh, &s_sel);
+    const uint32_t tau = sel.prefix;
+    const bool all = sel.all != 0;
+    unsigned long long tm[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + ((wave * 16 + j) << 6) + lane;
+        tm[j] = __ballot(!all && i < n && __float_as_uint(v[j]) == tau);
+        if (lane == 0) cc[wave * 16 + j] = (int)__popcll(tm[j]);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int q = 0; q < NUC_SEG / 64; q++) { int c = cc[q]; cc[q] = run; run += c; }
+    }
+    __syncthreads();
+    const unsigned long long ntie = s_ntie, tie0 = s_tie0;
+    unsigned long long m = ntie;
+    if (!all) {
+        unsigned long long ft = fix63(__uint_as_float(tau)), need = fix63(top_p) - sel.above;
+        if (ft > 0) {
+            unsigned long long q = (need + ft - 1) / ft;
+            m = q < ntie ? q : ntie;
+        }
+    }
+    float kept = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + ((wave * 16 + j) << 6) + lane;
+        if (i < n) {
+            uint32_t key = __float_as_uint(v[j]);
+            bool tie = (tm[j] >> lane) & 1ull;
+            bool keep = all || key > tau ||
+                        (tie && tie0 + (unsigned long long)cc[wave * 16 + j] + __popcll(tm[j] & lanes_below()) < m);
+            if (!keep) pr[i] = 0.0f;
+            else kept += v[j];
+        }
+    }
+    kept = wg256_sum(kept, red);
+    if (tid == 0) sc->seg_kept[blockIdx.x] = kept;
+}
+
+// Divide by the kept sum; the draw's segment masses and last nonzero entries.
+__global__ __launch_bounds__(256) void k_nuc_renorm(float* pr, int n, int nseg, NucleusScratch* sc) {
+    __shared__ unsigned long long redu[4];
+    __shared__ int redi[4];
+    __shared__ float s_kept;
+    __shared__ float segv[NUC_MAX_SEG];
+    const int beg = blockIdx.x * NUC_SEG, tid = threadIdx.x;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) { int i = beg + j * 256 + tid; v[j] = i < n ? pr[i] : 0.0f; }
+    load_segs(sc->seg_kept, nseg, segv);
+    if (tid == 0) {
+        float t = 0.0f;
+        for (int h = 0; h < nseg; h++) t += segv[h];
+        s_kept = t;
+    }
+    __syncthreads();
+    const float kept = s_kept;
+    unsigned long long mass = 0;
+    int last = -1;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int i = beg + j * 256 + tid;
+        if (i < n) {
+            float p = v[j];
+            if (kept > 0.0f) {
+                p = p / kept;
+                pr[i] = p;
+            }
+            mass += fix63(p);
+            if (p > 0.0f) last = i;
+        }
+    }
+    mass = wg256_sum(mass, redu);
+    for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o));
+    if ((tid & 63) == 0) redi[tid >> 6] = last;
+    __syncthreads();
+    if (tid == 0) {
+        sc->seg_mass[blockIdx.x] = mass;
+        sc->seg_last[blockIdx.x] = max(max(redi[0], redi[1]), max(redi[2], redi[3]));
+    }
+}
+
+// The draw: the segment whose running mass passes U, then the entry inside it (thread t walks
+// entries 16t .. 16t+15 of the segment after an exclusive scan of the threads' masses); the last
+// nonzero entry when rounding leaves the total below U. Leaves the mass histograms zeroed.
+__global__ __launch_bounds__(256) void k_nuc_draw(const float* __restrict__ pr, int n, float u, int nseg,
+                                                  NucleusScratch* sc, int* out_token) {
+    __shared__ unsigned long long buf[256];
+    __shared__ int s_seg, s_last, s_found;
+    __shared__ unsigned long long s_base;
+    __shared__ unsigned long long segm[NUC_MAX_SEG];
+    __shared__ int segl[NUC_MAX_SEG];
+    const int tid = threadIdx.x;
     const unsigned long long U = fix63(u);
-    pass_chunks<SAMPLE_BATCH>(pr, n, nch, [&](int c, int i, float p) {
-        unsigned long long v = i < n ? fix63(p) : 0ull;
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-        if (lane == 0) chunk[c] = v;
-    });
-    __syncthreads();
-    if (tid == 0) s_chunk = -1;
-    __syncthreads();
-    unsigned long long total = chunks_excl_scan(chunk, nch, scanbuf);
-    for (int c = tid; c < nch; c += nt) {
-        unsigned long long hi = c + 1 < nch ? chunk[c + 1] : total;
-        if (chunk[c] <= U && U < hi) s_chunk = c;  // exactly one chunk can hold U
-    }
-    __syncthreads();
-    int found = 0x7fffffff;
-    const int cs = s_chunk;
-    if (cs >= 0 && wave == 0) {
-        int i = (cs << 6) + lane;
-        unsigned long long v = i < n ? fix63(pr[i]) : 0ull, incl = v;
-        for (int o = 1; o < 64; o <<= 1) {
-            unsigned long long a = __shfl_up(incl, o);
-            if (lane >= o) incl += a;
+    load_segs(sc->seg_mass, nseg, segm);
+    load_segs(sc->seg_last, nseg, segl);
+    if (tid == 0) {
+        unsigned long long run = 0;
+        int seg = -1, last = -1;
+        for (int h = 0; h < nseg; h++) {
+            unsigned long long mh = segm[h];
+            if (seg < 0 && U < run + mh) { seg = h; s_base = run; }
+            run += mh;
+            last = max(last, segl[h]);
         }
-        unsigned long long hit = __ballot(i < n && U < chunk[cs] + incl);
-        if (hit) found = (cs << 6) + (__ffsll((long long)hit) - 1);
+        s_seg = seg;
+        s_last = last;
+        s_found = 0x7fffffff;
     }
-    int last = -1;  // fallback: the last nonzero probability
-    pass_strided<SAMPLE_BATCH>(pr, n, [&](int i, float p) { if (i < n && p > 0.0f) last = i; });
-    found = block_reduce(found, redi, [](int a, int b) { return a < b ? a : b; });
-    last = block_reduce(last, redi + 16, [](int a, int b) { return a > b ? a : b; });
-    if (tid == 0) *out_token = found != 0x7fffffff ? found : (last >= 0 ? last : n - 1);
+    __syncthreads();
+    const int seg = s_seg;
+    if (seg >= 0) {
+        const int b0 = seg * NUC_SEG + tid * 16;
+        float v[16];
+        unsigned long long part = 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            v[j] = b0 + j < n ? pr[b0 + j] : 0.0f;
+            part += fix63(v[j]);
+        }
+        unsigned long long total;
+        unsigned long long run = s_base + block_excl_scan(part, buf, &total);
+        if (U >= run && U < run + part) {
+            for (int j = 0; j < 16; j++) {
+                run += fix63(v[j]);
+                if (U < run) { s_found = b0 + j; break; }
+            }
+        }
+    }
+    for (int j = tid; j < 4 * 256; j += blockDim.x) sc->hist[j >> 8][j & 255] = 0ull;
+    __syncthreads();
+    if (tid == 0) {
+        int f = s_found;
+        *out_token = f != 0x7fffffff ? f : (s_last >= 0 ? s_last : n - 1);
+    }
 }
 
 hipError_t launch_sample_nucleus(float* x, int n, float inv_temp, float top_p, float u, float* pr, int* out_token,
-                                 hipStream_t st) {
-    k_sample_nucleus<<<1, 1024, 0, st>>>(x, n, inv_temp, top_p, u, pr, out_token);
+                                 NucleusScratch* sc, hipStream_t st) {
+    const int nseg = (n + NUC_SEG - 1) / NUC_SEG;
+    if (nseg > NUC_MAX_SEG) return hipErrorInvalidValue;
+    k_nuc_max<<<nseg, 256, 0, st>>>(x, n, inv_temp, sc);
+    k_nuc_exp<<<nseg, 256, 0, st>>>(x, n, pr, nseg, sc);
+    k_nuc_norm<<<nseg, 256, 0, st>>>(pr, n, top_p, nseg, sc);
+    if (top_p < 1.0f) {
+        for (int level = 1; level < 4; level++) k_nuc_hist<<<nseg, 256, 0, st>>>(pr, n, top_p, level, sc);
+        k_nuc_ties<<<nseg, 256, 0, st>>>(pr, n, top_p, sc);
+        k_nuc_keep<<<nseg, 256, 0, st>>>(pr, n, top_p, nseg, sc);
+        k_nuc_renorm<<<nseg, 256, 0, st>>>(pr, n, nseg, sc);
+    }
+    k_nuc_draw<<<1, 256, 0, st>>>(pr, n, u, nseg, sc, out_token);
     return hipGetLastError();
 }
 

@@ -73,10 +73,23 @@ hipError_t launch_topk(float* x, int64_t n, float inv_temp, int k, int cap, int*
 // LlamaLanguageModel.ApplyRepetitionPenalty on device logits; counts: n zeroed ints, left zeroed.
 hipError_t launch_rep_penalty(float* x, int n, const int* ids, int n_ids, float penalty, int* counts,
                               hipStream_t st);
+// Device scratch of launch_sample_nucleus: the edge's mass histograms (zero between calls) and the
+// per-segment results of its passes (segments of 4096 entries).
+constexpr int NUC_MAX_SEG = SAMPLE_MAX_VOCAB / 4096;
+struct NucleusScratch {
+    unsigned long long hist[4][256];
+    float seg_max[NUC_MAX_SEG];
+    float seg_sum[NUC_MAX_SEG];
+    float seg_kept[NUC_MAX_SEG];
+    unsigned long long seg_mass[NUC_MAX_SEG];
+    int seg_tie[NUC_MAX_SEG];
+    int seg_last[NUC_MAX_SEG];
+};
 // SamplerPipeline stages 1, 3, 4, 5 (temperature, softmax, top-p, draw with u) over x; pr: n floats
-// of scratch (left holding the final distribution); the token goes to *out_token.
+// of scratch (left holding the final distribution); the token goes to *out_token. sc: zeroed once
+// at allocation.
 hipError_t launch_sample_nucleus(float* x, int n, float inv_temp, float top_p, float u, float* pr, int* out_token,
-                                 hipStream_t st);
+                                 NucleusScratch* sc, hipStream_t st);
 hipError_t launch_copy_hidden(const float* x, int n, float* dst, hipStream_t st);
 
 }  // namespace fllm
