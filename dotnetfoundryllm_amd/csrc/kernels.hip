@@ -629,6 +629,39 @@ constexpr int SAMPLE_BATCH = 16;
 //    stable compaction.
 constexpr int TOPK_NS = 2048, TOPK_SEG = 4096;
 
+// The bucket of a descending radix-select step: with `above` already counted above this digit's
+// buckets, the bucket b whose range holds the P-th unit from the top, i.e.
+// above + sum(hist[b+1..255]) < P <= above + sum(hist[b..255]). Threads 0..255 each take one bin
+// (wave prefix sums over bins 255, 254, ...; blockDim.x >= 256); all threads return b (or -1 when
+// the total stays below P) and *before = above + sum(hist[b+1..255]). Two barriers, no serial scan.
+template <typename T>
+__device__ int find_bucket_desc(const T* hist, T above, T P, T* before_out, T* wtot, int* s_b) {
+    const int t = threadIdx.x, lane = t & 63;
+    T h = 0, incl = 0;
+    if (t < 256) {
+        h = hist[255 - t];
+        incl = h;
+        for (int o = 1; o < 64; o <<= 1) {
+            T a = __shfl_up(incl, o);
+            if (lane >= o) incl += a;
+        }
+        if (lane == 63) wtot[t >> 6] = incl;
+    }
+    if (t == 0) *s_b = -1;
+    __syncthreads();
+    if (t < 256) {
+        T before = above;
+        for (int w = 0; w < (t >> 6); w++) before += wtot[w];
+        before += incl - h;
+        if (before < P && P - before <= h) {  // exactly one bin: the running sum is monotone
+            *s_b = 255 - t;
+            *before_out = before;
+        }
+    }
+    __syncthreads();
+    return *s_b;
+}
+
 // Copies the first nseg entries of a per-segment array into LDS (nseg <= blockDim.x), one load per
 // thread, so that one thread can then combine them in order without a chain of memory loads.
 template <typename T>
@@ -642,7 +675,7 @@ __device__ void topk_radix_emit(const float* __restrict__ x, int n, int k, int c
                                 int* count) {
     __shared__ int hist[256];
     __shared__ uint32_t s_prefix, s_mask;
-    __shared__ int s_remain;
+    __shared__ int s_remain, s_before, s_wtot[4], s_b;
     __shared__ int chunk[SAMPLE_MAX_CHUNKS];
     __shared__ int scan[1024];
     const int tid = threadIdx.x, nt = blockDim.x, lane = lane_id();
@@ -661,17 +694,12 @@ __device__ void topk_radix_emit(const float* __restrict__ x, int n, int k, int c
                 wave_hist_add(hist, i < n && (key & mask) == prefix, (key >> shift) & 255u);
             });
             __syncthreads();
-            if (tid == 0) {
-                int cum = 0, rem = s_remain;
-                for (int b = 255; b >= 0; b--) {
-                    if (cum + hist[b] >= rem) {
-                        s_prefix = prefix | ((uint32_t)b << shift);
-                        s_mask = mask | (255u << shift);
-                        s_remain = rem - cum;
-                        break;
-                    }
-                    cum += hist[b];
-                }
+            const int rem = s_remain;
+            const int b = find_bucket_desc(hist, 0, rem, &s_before, s_wtot, &s_b);
+            if (tid == 0) {  // b >= 0: the counts above the prefix sum to at least rem
+                s_prefix = prefix | ((uint32_t)b << shift);
+                s_mask = mask | (255u << shift);
+                s_remain = rem - s_before;
             }
             __syncthreads();
         }
@@ -702,7 +730,7 @@ __device__ void topk_select_candidates(const float* __restrict__ cv, const int* 
     __shared__ float lv[TOPK_CMAX];
     __shared__ int hist[256];
     __shared__ uint32_t s_prefix, s_mask;
-    __shared__ int s_remain;
+    __shared__ int s_remain, s_before, s_wtot[4], s_b;
     __shared__ int scan[1024];
     const int tid = threadIdx.x, nt = blockDim.x;
     for (int j = tid; j < nc; j += nt) lv[j] = cv[j];
@@ -718,17 +746,12 @@ __device__ void topk_select_candidates(const float* __restrict__ cv, const int* 
             if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
         }
         __syncthreads();
+        const int rem = s_remain;
+        const int b = find_bucket_desc(hist, 0, rem, &s_before, s_wtot, &s_b);
         if (tid == 0) {
-            int cum = 0, rem = s_remain;
-            for (int b = 255; b >= 0; b--) {
-                if (cum + hist[b] >= rem) {
-                    s_prefix = prefix | ((uint32_t)b << shift);
-                    s_mask = mask | (255u << shift);
-                    s_remain = rem - cum;
-                    break;
-                }
-                cum += hist[b];
-            }
+            s_prefix = prefix | ((uint32_t)b << shift);
+            s_mask = mask | (255u << shift);
+            s_remain = rem - s_before;
         }
         __syncthreads();
     }
@@ -757,29 +780,44 @@ __global__ __launch_bounds__(1024) void k_topk(float* x, int64_t n64, float inv_
     topk_radix_emit(x, n, k, cap, ids, vals, count);
 }
 
-// The sample's threshold: keys of the scaled values at j * n / NS, sorted descending (bitonic), the
-// r-th largest with r = 4 k NS / n + 8 (about 4 k + 8 n / NS entries of the whole reach it).
+// The sample's threshold: among the keys of the scaled values at j * n / NS, the r-th largest
+// (radix select) with r = 4 k NS / n + 8 (about 4 k + 8 n / NS entries of the whole reach it).
 __global__ __launch_bounds__(1024) void k_topk_sample(const float* __restrict__ x, int n, float inv_temp, int k,
                                                       TopkScratch* sc) {
     __shared__ uint32_t samp[TOPK_NS];
+    __shared__ int hist[256];
+    __shared__ uint32_t s_prefix, s_mask;
+    __shared__ int s_remain, s_before, s_wtot[4], s_b;
     const int tid = threadIdx.x, nt = blockDim.x;
     for (int j = tid; j < TOPK_NS; j += nt) {
         float v = x[(int)(((int64_t)j * n) / TOPK_NS)];
         samp[j] = okey(inv_temp != 1.0f ? v * inv_temp : v);
     }
-    __syncthreads();
-    for (int size = 2; size <= TOPK_NS; size <<= 1)
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int t = tid; t < TOPK_NS / 2; t += nt) {
-                int i = 2 * stride * (t / stride) + (t % stride), j = i + stride;
-                bool up = (i & size) == 0;
-                uint32_t a = samp[i], b = samp[j];
-                if ((a < b) == up) { samp[i] = b; samp[j] = a; }
-            }
-            __syncthreads();
+    if (tid == 0) {
+        s_prefix = 0;
+        s_mask = 0;
+        s_remain = (int)min((int64_t)TOPK_NS, (int64_t)4 * k * TOPK_NS / n + 8);  // rank r in the sample
+    }
+    for (int pass = 0; pass < 4; pass++) {  // radix select of the sample's r-th largest key
+        const int shift = 24 - 8 * pass;
+        for (int b = tid; b < 256; b += nt) hist[b] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+        for (int j = tid; j < TOPK_NS; j += nt) {
+            uint32_t key = samp[j];
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
         }
-    const int r = (int)min((int64_t)TOPK_NS, (int64_t)4 * k * TOPK_NS / n + 8);
-    if (tid == 0) sc->t = samp[r - 1];
+        __syncthreads();
+        const int rem = s_remain;
+        const int b = find_bucket_desc(hist, 0, rem, &s_before, s_wtot, &s_b);
+        if (tid == 0) {
+            s_prefix = prefix | ((uint32_t)b << shift);
+            s_mask = mask | (255u << shift);
+            s_remain = rem - s_before;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) sc->t = s_prefix;
 }
 
 // Segment blockIdx.x (TOPK_SEG entries, 16 per thread): scale in place, count keys >= t.
@@ -970,29 +1008,26 @@ struct NucSel {
 };
 __device__ NucSel nuc_select(const NucleusScratch* sc, int levels, unsigned long long P, unsigned long long* lh,
                              NucSel* out) {
+    __shared__ unsigned long long s_before, s_wtot[4];
+    __shared__ int s_b;
     for (int j = threadIdx.x; j < levels * 256; j += blockDim.x) lh[j] = sc->hist[j >> 8][j & 255];
     __syncthreads();
-    if (threadIdx.x == 0) {
-        NucSel r{0u, 0u, 0ull, 0};
-        for (int L = 0; L < levels && !r.all; L++) {
-            const int shift = 24 - 8 * L;
-            unsigned long long acc = r.above;
-            int b = 255;
-            for (; b >= 0; b--) {
-                if (acc + lh[L * 256 + b] >= P) break;
-                acc += lh[L * 256 + b];
-            }
-            if (b < 0) r.all = 1;
-            else {
-                r.prefix |= (uint32_t)b << shift;
-                r.mask |= 255u << shift;
-                r.above = acc;
-            }
+    NucSel r{0u, 0u, 0ull, 0};
+    for (int L = 0; L < levels; L++) {  // every thread follows the same selections
+        const int b = find_bucket_desc(lh + L * 256, r.above, P, &s_before, s_wtot, &s_b);
+        if (b < 0) {
+            r.all = 1;
+            break;
         }
-        *out = r;
+        const int shift = 24 - 8 * L;
+        r.prefix |= (uint32_t)b << shift;
+        r.mask |= 255u << shift;
+        r.above = s_before;
+        __syncthreads();  // s_before is rewritten by the next level
     }
+    if (threadIdx.x == 0) *out = r;
     __syncthreads();
-    return *out;
+    return r;
 }
 
 __global__ __launch_bounds__(256) void k_nuc_max(float* x, int n, float inv_temp, NucleusScratch* sc) {
