@@ -194,10 +194,17 @@ def profiler_roofline(args, bytes_per_launch, dom_name, steps_launches):
             for r in rows:
                 if r["Counter_Name"] != counter:
                     continue
-                k = (r["Dispatch_Id"], r["Kernel_Name"].split("(")[0], r.get("Grid_Size", ""))
-                per[k] = per.get(k, 0.0) + float(r["Counter_Value"])
-            copy = [v for (d, n, g), v in per.items() if "copyBuffer" in n]
-            dom = [v for (d, n, g), v in per.items() if (n, g) in keys]
+                d = int(r["Dispatch_Id"])
+                name = r["Kernel_Name"]
+                per[d] = (name, per.get(d, (name, 0.0))[1] + float(r["Counter_Value"]))
+            order = [per[d] for d in sorted(per)]  # dispatch order = launch order
+            copy = [v for n, v in order if "copyBuffer" in n]
+            # the dominant launch by position among the profiled launches, as for the durations (one
+            # kernel can serve several launches of a step with the same grid: e.g. o and gate/up)
+            fl = [(n, v) for n, v in order if "fllm::" in n and "k_set_params" not in n]
+            if len(fl) < n_prof:
+                raise RuntimeError(f"{counter}: fewer dispatches than the profiled launches")
+            dom = [v for (n, v), nm in zip(fl[-n_prof:], steps_launches) if nm == dom_name]
             if not copy or not dom:
                 raise RuntimeError(f"{counter}: missing copy or dominant-kernel dispatches")
             # the copy reads and writes COPY_BYTES: counts per byte of that copy
