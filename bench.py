@@ -275,6 +275,25 @@ def sampling_report(F, fwd, kv, cfg, seed, reps=50):
     return out
 
 
+def upload_report(F, ctx, load, probe_bytes=1 << 30):
+    """Host-to-device rate of the weight upload (fllm_model_upload: raw GGUF blocks from host memory,
+    large tensors through the pinned staging ring) against one direct pageable copy of 1 GiB
+    (fllm_buf_write), and the time finalize takes to regroup the matrices on the device."""
+    import numpy as np
+    src = np.random.default_rng(1).integers(0, 255, probe_bytes, dtype=np.uint8)
+    buf = F.DeviceBuffer(ctx, probe_bytes)
+    try:
+        buf.write(src)  # first touch
+        t = time.perf_counter()
+        buf.write(src)
+        direct = probe_bytes / (time.perf_counter() - t) / 1e9
+    finally:
+        buf.close()
+    return {"bytes": load["upload_bytes"], "seconds": round(load["upload_s"], 3),
+            "GB_s": round(load["upload_bytes"] / load["upload_s"] / 1e9, 2),
+            "direct_pageable_copy_GB_s": round(direct, 2), "finalize_s": round(load["finalize_s"], 3)}
+
+
 def weights_text(cfg):
     """'Q4_K (q,k,o,gate,up) + Q6_K (v,down,output), seeded random blocks' from the config's types."""
     from dotnetfoundryllm_amd._native import TYPE_NAMES
@@ -324,8 +343,11 @@ def main():
     n_cu, hbm = ctx.device_info()
     log(f"device: {n_cu} CUs, {hbm / 2**30:.0f} GiB; building {cfg['name']} ({tok_bytes / 1e9:.3f} GB of weights)")
     t = time.time()
-    model, _ = build_model(ctx, cfg)
+    load = {}
+    model, _ = build_model(ctx, cfg, stats=load)
     log(f"weights generated and uploaded in {time.time() - t:.1f} s")
+    load_report = upload_report(F, ctx, load)
+    log(f"upload: {load_report}")
     max_seq = min(cfg["max_ctx"], args.prompt + args.warmup + args.steps + args.host_steps + args.profile_steps + 8)
     kv = F.HipKvCache(model, max_seq)
     if args.no_graph:
@@ -467,6 +489,7 @@ def main():
         "host_loop_tok_s": round(host_tok_s, 2) if host_tok_s else None,
         "profiled_step_ms": round(total_ms, 4),
         "sampling_us_per_call": sampling,
+        "weight_upload": load_report,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

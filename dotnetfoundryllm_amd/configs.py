@@ -170,21 +170,30 @@ def weight_bytes_per_token(cfg):
     return layers, head
 
 
-def build_model(ctx, cfg, keep_bytes=False, threads=0, n_layers=None):
-    """Generate every tensor of cfg from its seed and upload it; returns (Model, {name: bytes})."""
+def build_model(ctx, cfg, keep_bytes=False, threads=0, n_layers=None, stats=None):
+    """Generate every tensor of cfg from its seed and upload it; returns (Model, {name: bytes}).
+    With a dict as stats, adds the bytes uploaded and the seconds spent in the upload calls."""
+    import time
     from . import Model
     c = dict(cfg)
     if n_layers is not None:
         c["n_layers"] = n_layers
     m = Model(ctx, desc_of(c))
     kept = {}
+    up_s, up_b = 0.0, 0
     for entry in tensor_plan(c):
         data = synth_bytes(c, entry, threads)
+        t = time.perf_counter()
         m.upload(entry[1], entry[2], entry[3], data)
+        up_s += time.perf_counter() - t
+        up_b += len(data)
         if keep_bytes:
             kept[entry[0]] = (entry, data)
         del data
+    t = time.perf_counter()
     m.finalize()
+    if stats is not None:
+        stats.update(upload_s=up_s, upload_bytes=up_b, finalize_s=time.perf_counter() - t)
     return m, kept
 
 

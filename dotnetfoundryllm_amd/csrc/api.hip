@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <map>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "attention.hpp"
@@ -51,12 +52,60 @@ extern "C" int32_t fllm_version(void) { return 100; }
 // =====================================================================================
 // objects
 // =====================================================================================
+// Pinned staging of large host-to-device uploads: the host copies chunk i into buffer i % 2 (with
+// several threads) while the DMA engine moves chunk i - 1, so a pageable source (a mapped GGUF
+// file) streams at the rate of the slower of the two instead of their sum.
+struct Staging {
+    static const size_t kChunk = 32u << 20;
+    uint8_t* buf[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+};
+
 struct fllm_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     int n_cu = 0;
     int64_t hbm = 0;
+    Staging stage;
 };
+
+// Copies n bytes of host memory to the device through the context's pinned staging buffers
+// (allocated on first use); returns when the last chunk's copy has been enqueued and the source
+// may be reused.
+static hipError_t staged_upload(fllm_ctx* ctx, uint8_t* dst, const uint8_t* src, size_t n) {
+    Staging& S = ctx->stage;
+    for (int b = 0; b < 2; b++) {
+        if (!S.buf[b]) {
+            hipError_t e = hipHostMalloc((void**)&S.buf[b], Staging::kChunk, hipHostMallocDefault);
+            if (e != hipSuccess) { S.buf[b] = nullptr; return e; }
+        }
+        if (!S.done[b]) {
+            hipError_t e = hipEventCreateWithFlags(&S.done[b], hipEventDisableTiming);
+            if (e != hipSuccess) { S.done[b] = nullptr; return e; }
+        }
+    }
+    const unsigned nthr = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+    size_t off = 0;
+    for (int i = 0; off < n; i++) {
+        const int b = i & 1;
+        const size_t len = std::min(Staging::kChunk, n - off);
+        hipError_t e = hipEventSynchronize(S.done[b]);  // the DMA from this buffer two chunks ago
+        if (e != hipSuccess) return e;
+        uint8_t* stage = S.buf[b];
+        const uint8_t* from = src + off;
+        const size_t part = (len + nthr - 1) / nthr;
+        std::vector<std::thread> pool;
+        for (unsigned t = 1; t < nthr && t * part < len; t++)
+            pool.emplace_back([=] { memcpy(stage + t * part, from + t * part, std::min(part, len - t * part)); });
+        memcpy(stage, from, std::min(part, len));
+        for (auto& th : pool) th.join();
+        e = hipMemcpyAsync(dst + off, stage, len, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipEventRecord(S.done[b], ctx->stream);
+        if (e != hipSuccess) return e;
+        off += len;
+    }
+    return hipSuccess;
+}
 
 struct fllm_buf {
     fllm_ctx* ctx = nullptr;
@@ -185,6 +234,10 @@ extern "C" int32_t fllm_ctx_destroy(fllm_ctx* ctx) {
     if (!ctx) return FLLM_OK;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
+    for (int b = 0; b < 2; b++) {
+        if (ctx->stage.done[b]) hipEventDestroy(ctx->stage.done[b]);
+        if (ctx->stage.buf[b]) hipHostFree(ctx->stage.buf[b]);
+    }
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return FLLM_OK;
@@ -526,7 +579,9 @@ extern "C" int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer,
     uint8_t* dev = nullptr;
     hipError_t e = hipMalloc(&dev, nbytes + kPad);
     if (e != hipSuccess) return fail(FLLM_E_OOM, "hipMalloc(%llu): %s", (unsigned long long)nbytes, hipGetErrorString(e));
-    e = hipMemcpyAsync(dev, bytes, nbytes, hipMemcpyHostToDevice, st);
+    // large tensors through the pinned staging ring, small ones as one pageable copy
+    if (nbytes >= Staging::kChunk) e = staged_upload(m->ctx, dev, (const uint8_t*)bytes, nbytes);
+    else e = hipMemcpyAsync(dev, bytes, nbytes, hipMemcpyHostToDevice, st);
     if (e == hipSuccess) e = hipMemsetAsync(dev + nbytes, 0, kPad, st);
     if (e != hipSuccess) { hipFree(dev); return fail(FLLM_E_DEVICE, "upload: %s", hipGetErrorString(e)); }
     if (vec) {
