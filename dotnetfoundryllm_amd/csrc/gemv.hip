@@ -1652,13 +1652,16 @@ static bool mfma_ok(const GemvArgs& a, int64_t cols) {
     return true;
 }
 
-static size_t mf_lds(int NB, bool glu) {
+static size_t mf_lds_split(int nw, int kc, bool glu) {
     const int T = (glu ? 2 : 1) * MF_TILE;
-    int kc;
-    const int nw = mf_split(NB, &kc);
     // row partials, 48 floats, zero block, table (nw * kc chunk slots), and one wave's worth of
     // padding after the table
     return sizeof(float) * ((size_t)nw * T + 48) + (size_t)(MF_ZERO_ENTRIES(kc) + (size_t)nw * kc * MF_TAB_ENTRIES + 64) * 16;
+}
+static size_t mf_lds(int NB, bool glu) {
+    int kc;
+    const int nw = mf_split(NB, &kc);
+    return mf_lds_split(nw, kc, glu);
 }
 
 bool gemv_uses_mfma(const GemvArgs& a, int64_t cols) {
@@ -1673,7 +1676,8 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
     a.S = 0;
     a.rpw = MF_TILE;
     const int NB = (int)(cols / 256);
-    const int nw = mf_waves(NB);
+    int kc;
+    const int nw = mf_split(NB, &kc);
     int units = 0;
     for (int i = 0; i < a.nseg; i++) {
         a.seg[i].wg_begin = units;  // first unit of the segment
@@ -1681,6 +1685,7 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
         units += (a.seg[i].rows + MF_TILE - 1) / MF_TILE;
     }
     a.nunits = units;
+    a.chunks_per_wave = kc;
     // two weight types: units of the Q6_K segments come after the Q4_K ones
     a.mix_wg = 0;
     a.mix_unit = units;
@@ -1688,9 +1693,9 @@ static int plan_mfma(GemvArgs& a, int64_t cols, int n_cu, int* block_threads, si
         if (a.seg[i].type != a.seg[0].type) { a.mix_unit = a.seg[i].wg_begin; a.mix_wg = 1; break; }
     *block_threads = 64 * nw;
     a.nw = nw;
-    *lds_bytes = mf_lds(NB, a.glu != 0);
+    *lds_bytes = mf_lds_split(nw, kc, a.glu != 0);
     // persistent grid: as many workgroups as fit on the device at once
-    MfKernel k = mf_kernel(a, mf_kc(NB));
+    MfKernel k = mf_kernel(a, kc);
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, *block_threads, *lds_bytes) != hipSuccess ||
@@ -1855,7 +1860,7 @@ hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, siz
     if (a.xin == XIN_POST && (!a.mfma || a.x2 == nullptr || a.post_w == nullptr || a.x_out == nullptr || a.x_out == a.x))
         return hipErrorInvalidValue;
     if (a.mfma)
-        mf_kernel(a, mf_kc(a.G / 8))<<<grid, block_threads, lds, st>>>(a);
+        mf_kernel(a, a.chunks_per_wave)<<<grid, block_threads, lds, st>>>(a);
     else if (block_threads <= 512)
         k_gemv_fused<false><<<grid, block_threads, lds, st>>>(a);
     else

@@ -74,6 +74,7 @@ struct GemvArgs {
     // XIN_POST
     const float* x2;       // the output whose post-norm is added to x
     const float* post_w;   // the post-norm weight (1 + w)
+    int chunks_per_wave;   // matrix-core variant: chunks per wave (nw * chunks_per_wave = chunks per row)
 };
 
 bool gemv_fusable_type(int t);
