@@ -109,6 +109,22 @@ def test_host_sampler_matches_oracle_pipeline(temp, k):
     s.close()
 
 
+@pytest.mark.parametrize("temp,k,top_p", [(1.0, 0, 0.9), (0.8, 40, 0.5), (1.2, 0, 0.05), (0.7, 200, 0.95)])
+def test_host_top_p_pipeline_matches_oracle(temp, k, top_p):
+    """The host pipeline (what runs over the device's top-k survivors) with top-p: the same tokens
+    as the oracle's SamplerPipeline for the same seed, bit for bit (both sum in index order and
+    order equal probabilities by index)."""
+    rng = np.random.default_rng(12)
+    s = F.SamplerPipeline(temp, k, top_p, 91)
+    r = O.Xoshiro(91)
+    for i in range(60):
+        lg = (rng.standard_normal(3000) * 3).astype(np.float32)
+        if i % 3 == 0:
+            lg = np.round(lg, 1)  # ties, also at the nucleus edge
+        assert s.sample_host(lg) == O.sampler_pipeline_p(lg, temp, k, top_p, r)
+    s.close()
+
+
 def test_sampler_argument_checks():
     with pytest.raises(F.ArgumentOutOfRangeException):
         F.SamplerPipeline(-1.0)
