@@ -264,3 +264,45 @@ def test_topk_sample_select_and_fallback(big_vocab):
             assert np.array_equal(ids, keep)
             assert np.array_equal(vals, scaled[keep])
             assert np.array_equal(fwd.logits, scaled)
+
+
+def test_nucleus_and_topk_small_vocab(ctx):
+    """A vocabulary of 512 (one partly filled 4096-entry segment; top-k takes the one-workgroup
+    select): the nucleus is the oracle's where its edge is unambiguous, the draw sits where u falls
+    in the device's running sum, and top-k survivors are bit-exact."""
+    cfg, desc, tensors = synthetic("test-llama")
+    m = F.Model(ctx, desc)
+    upload(m, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    fwd.forward(1, 0, kv)
+    rng = np.random.default_rng(8)
+    r = O.Xoshiro(5)
+    try:
+        for j in range(40):
+            lg = (rng.standard_normal(desc.vocab) * 2).astype(np.float32)
+            temp, top_p = (0.8, 0.9) if j % 2 else (1.0, 1.0)
+            sm = _oracle_probs(lg, temp, 1.0)
+            want = O.apply_top_p(sm, top_p)
+            u = r.next_float()
+            fwd.write_logits(lg)
+            tok = fwd.sample_nucleus(float(_inv_temp(temp)), top_p, u)
+            got = fwd.probs()
+            _check_draw(got, u, tok)
+            drift = 2 * desc.vocab * 2.0**-24
+            kd, ko = got > 0, want > 0
+            if not np.array_equal(kd, ko):  # only at an edge within the oracle's f32 drift
+                sm64 = sm.astype(np.float64) / np.sum(sm, dtype=np.float64)
+                assert abs(float(sm64[kd & ko].sum()) - top_p) < drift + float(sm64[kd ^ ko].max())
+            else:
+                np.testing.assert_allclose(got.astype(np.float64) / got.sum(dtype=np.float64),
+                                           want.astype(np.float64) / want.sum(dtype=np.float64), rtol=2e-6, atol=1e-15)
+            fwd.write_logits(lg)
+            ids, vals = fwd.sample_topk(1.0, 7, cap=desc.vocab)
+            ref = lg.copy()
+            O.lib.orc_apply_topk(O.fp(ref), ref.size, 7)
+            keep = np.nonzero(ref != -np.inf)[0]
+            assert np.array_equal(ids, keep) and np.array_equal(vals, lg[keep])
+    finally:
+        kv.close()
+        m.close()
