@@ -223,25 +223,48 @@ class Model:
 
 
 class HipKvCache:
-    """IKvCache over the device KV cache of one sequence (fllm_seq)."""
+    """IKvCache over the device KV cache of one sequence (fllm_seq): MaxSequenceLength,
+    CurrentLength, Append, GetKeys / GetValues, Clear, WasEvicted, Dispose (KvCache.cs:14-174)."""
 
     def __init__(self, model, max_sequence_length=0):
+        if max_sequence_length < 0:
+            raise ArgumentOutOfRangeException("maxSequenceLength")
         h = C.c_void_p()
         _check(N.dev.fllm_seq_create(model.h, max_sequence_length, C.byref(h)))
         self.h = h
         self.model = model
+        self.kv_dim = model.desc.n_kv_heads * model.desc.head_dim
+
+    def _handle(self):
+        # ObjectDisposedException.ThrowIf(_disposed, this) (KvCache.cs:61,102,121,140)
+        if not self.h:
+            raise ObjectDisposedException("KvCache")
+        return self.h
 
     @property
     def max_sequence_length(self):
         v = C.c_int32()
-        _check(N.dev.fllm_seq_capacity(self.h, C.byref(v)))
+        _check(N.dev.fllm_seq_capacity(self._handle(), C.byref(v)))
         return v.value
 
     @property
     def current_length(self):
         v = C.c_int32()
-        _check(N.dev.fllm_seq_length(self.h, C.byref(v)))
+        _check(N.dev.fllm_seq_length(self._handle(), C.byref(v)))
         return v.value
+
+    @property
+    def was_evicted(self):
+        v = C.c_int32()
+        _check(N.dev.fllm_kv_was_evicted(self._handle(), C.byref(v)))
+        return bool(v.value)
+
+    def append(self, layer, key_slice, value_slice):
+        """KvCache.Append(layer, keySlice, valueSlice) (KvCache.cs:59-97)."""
+        h = self._handle()
+        k = np.ascontiguousarray(key_slice, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(value_slice, dtype=np.float32).reshape(-1)
+        _check(N.dev.fllm_kv_append(h, int(layer), _fptr(k), k.size, _fptr(v), v.size))
 
     def get_keys(self, layer):
         return self._kv(layer, 0)
@@ -250,14 +273,16 @@ class HipKvCache:
         return self._kv(layer, 1)
 
     def _kv(self, layer, kind):
-        d = self.model.desc
-        n = max(self.current_length * d.n_kv_heads * d.head_dim, 1)
-        out = np.zeros(n, dtype=np.float32)
-        _check(N.dev.fllm_kv_read(self.h, layer, kind, _fptr(out), n))
-        return out[: self.current_length * d.n_kv_heads * d.head_dim]
+        h = self._handle()
+        n_pos = C.c_int32()
+        _check(N.dev.fllm_kv_length(h, int(layer), C.byref(n_pos)))
+        n = n_pos.value * self.kv_dim
+        out = np.zeros(max(n, 1), dtype=np.float32)
+        _check(N.dev.fllm_kv_read(h, int(layer), kind, _fptr(out), out.size))
+        return out[:n]
 
     def clear(self):
-        _check(N.dev.fllm_seq_reset(self.h))
+        _check(N.dev.fllm_seq_reset(self._handle()))
 
     def dispose(self):
         if self.h:
@@ -282,7 +307,10 @@ class HipForwardPass:
     def forward(self, token_id, position, kv):
         if kv is None:
             raise ArgumentNullException("kvCache")
-        _check(N.dev.fllm_forward(kv.h, int(token_id), int(position)))
+        if not isinstance(kv, HipKvCache):
+            # the device forward pass appends to and attends over a device-resident cache only
+            raise ArgumentException("kvCache must be a HipKvCache created from this model")
+        _check(N.dev.fllm_forward(kv._handle(), int(token_id), int(position)))
         self._kv = kv
 
     def prefill(self, tokens, pos0, kv):

@@ -109,6 +109,9 @@ DEVICE_SIGS = {
     "fllm_probs_copy": (I32, [P, PF32, I64]),
     "fllm_debug_hidden": (I32, [P, I32, PF32, I64]),
     "fllm_kv_read": (I32, [P, I32, I32, PF32, I64]),
+    "fllm_kv_length": (I32, [P, I32, PI32]),
+    "fllm_kv_append": (I32, [P, I32, PF32, I64, PF32, I64]),
+    "fllm_kv_was_evicted": (I32, [P, PI32]),
     "fllm_dequantize": (I32, [P, I32, P, U64, PF32, I64]),
     "fllm_element_count": (I32, [I32, I64, PI64]),
     "fllm_buf_create": (I32, [P, U64, PP]),

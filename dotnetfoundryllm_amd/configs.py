@@ -75,6 +75,14 @@ CONFIGS = {
                               final_softcap=30.0, tied=True, norm_std=0.1, seed=17),
     "test-mixed": _cfg("test-mixed", N.ARCH_LLAMA, 2, 256, 4, 2, 512, 512, 64, 10000.0,
                        _types(Q4_0, Q8_K, F16, BF16, F32, Q4_0, Q5_K, F16), emb_type=F16, norm_std=0.1, seed=16),
+    # the Qwen2-7B vocabulary (152064 = 37.1 sampler segments of 4096) on one narrow layer
+    "test-qwen2-v152k": _cfg("test-qwen2-v152k", N.ARCH_QWEN2, 1, 256, 4, 2, 512, 152064, 64, 1000000.0,
+                             _types(*([Q5_K] * 7), Q6_K), norm_std=0.1, seed=19),
+    # Gemma-2-9B attention at a narrow width: head_dim 256, 16 query / 8 kv heads, softcaps 50 / 30,
+    # window 4096 on the even layer, an 8192-position cache
+    "test-gemma2-long": _cfg("test-gemma2-long", N.ARCH_GEMMA2, 2, 512, 16, 8, 1024, 512, 8192, 10000.0,
+                             _types(*([Q8_0] * 8)), head_dim=256, emb_type=BF16, window=4096, attn_softcap=50.0,
+                             final_softcap=30.0, norm_std=0.1, seed=20),
     # FFN 16640 = 65 chunks of 256: down's rows split into 9 waves of 8 chunks, the last one with 1
     # chunk of the row and 7 past it
     "test-ragged": _cfg("test-ragged", N.ARCH_LLAMA, 2, 256, 4, 2, 16640, 512, 64, 10000.0,

@@ -142,6 +142,10 @@ struct fllm_model {
     std::vector<float> inv_freq;
     bool finalized = false;
     uint64_t layer_bytes = 0, head_bytes = 0;
+    // LlamaWeights.Dispose (LlamaWeights.cs:93-107): fllm_model_destroy marks the model disposed;
+    // its device memory is released when the last sequence created from it is destroyed
+    int n_seqs = 0;
+    bool disposed = false;
 };
 
 struct ProfAgg {
@@ -154,6 +158,8 @@ struct fllm_seq {
     hipStream_t st = nullptr;
     int max_seq = 0;
     int cur_len = 0;
+    int next_layer = 0;           // KvCache._nextLayerToAppend (KvCache.cs:69-96)
+    bool was_evicted = false;     // KvCache.WasEvicted (KvCache.cs:56)
     int nsplit = 1;               // chunks of the generic attention kernel
     int attn_nc = 1;              // chunks per kv head of the fast attention kernel
     size_t attn_lds = 0;
@@ -517,8 +523,7 @@ static void free_tensor(Tensor& t) {
     t = Tensor();
 }
 
-extern "C" int32_t fllm_model_destroy(fllm_model* m) {
-    if (!m) return FLLM_OK;
+static void model_free(fllm_model* m) {
     hipSetDevice(m->ctx->device);
     hipDeviceSynchronize();
     free_tensor(m->tok_embd);
@@ -532,6 +537,20 @@ extern "C" int32_t fllm_model_destroy(fllm_model* m) {
             if (p) hipFree(p);
     }
     delete m;
+}
+
+// ObjectDisposedException.ThrowIf(_disposed, this) of LlamaWeights.ThrowIfDisposed
+// (LlamaWeights.cs:138-139), checked by Forward before anything runs (LlamaForwardPass.cs:87).
+#define NOT_DISPOSED(m)                                                                                \
+    do {                                                                                               \
+        if ((m)->disposed) return fail(FLLM_E_DISPOSED, "Cannot access a disposed object. Object name: 'LlamaWeights'."); \
+    } while (0)
+
+extern "C" int32_t fllm_model_destroy(fllm_model* m) {
+    if (!m) return FLLM_OK;
+    if (m->disposed) return FLLM_OK;  // Dispose is idempotent (LlamaWeights.cs:95-98)
+    m->disposed = true;
+    if (m->n_seqs == 0) model_free(m);
     return FLLM_OK;
 }
 
@@ -558,6 +577,7 @@ static bool slot_shape(const fllm_model* m, int slot, int64_t& rows, int64_t& co
 extern "C" int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer, int32_t type, const void* bytes,
                                      uint64_t nbytes) {
     NOT_NULL(m);
+    NOT_DISPOSED(m);
     if (m->finalized) return fail(FLLM_E_INVALID_OP, "model already finalized");
     int64_t rows, cols;
     bool vec;
@@ -666,6 +686,7 @@ static hipError_t pack_tiles(fllm_model* m, Tensor& t) {
 
 extern "C" int32_t fllm_model_finalize(fllm_model* m) {
     NOT_NULL(m);
+    NOT_DISPOSED(m);
     if (m->finalized) return FLLM_OK;
     const fllm_model_desc& d = m->d;
     if (!m->tok_embd.present()) return fail(FLLM_E_INVALID_OP, "Required tensor 'token_embd.weight' not found in GGUF file.");
@@ -768,6 +789,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     NOT_NULL(m);
     NOT_NULL(out);
     *out = nullptr;
+    NOT_DISPOSED(m);
     if (!m->finalized) return fail(FLLM_E_INVALID_OP, "model not finalized");
     if (max_seq < 0) return fail(FLLM_E_ARG_RANGE, "max_seq must be >= 0");
     const fllm_model_desc& d = m->d;
@@ -847,22 +869,106 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     if (e == hipSuccess) e = hipMemsetAsync(s->nuc_sc, 0, sizeof(NucleusScratch), s->st);
     if (e == hipSuccess) e = hipStreamSynchronize(s->st);
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_DEVICE, "sequence init: %s", hipGetErrorString(e)); }
+    m->n_seqs++;
     *out = s;
     return FLLM_OK;
 }
 
 extern "C" int32_t fllm_seq_destroy(fllm_seq* s) {
     if (!s) return FLLM_OK;
-    hipSetDevice(s->m->ctx->device);
+    fllm_model* m = s->m;
+    hipSetDevice(m->ctx->device);
     hipStreamSynchronize(s->st);
     seq_free(s);
+    // the last sequence of a disposed model releases its weights
+    if (--m->n_seqs == 0 && m->disposed) model_free(m);
     return FLLM_OK;
 }
 
+// KvCache.Clear (KvCache.cs:138-144)
 extern "C" int32_t fllm_seq_reset(fllm_seq* s) {
     NOT_NULL(s);
     HIP_TRY(hipStreamSynchronize(s->st));
     s->cur_len = 0;
+    s->next_layer = 0;
+    s->was_evicted = false;
+    return FLLM_OK;
+}
+
+extern "C" int32_t fllm_kv_was_evicted(fllm_seq* s, int32_t* out) {
+    NOT_NULL(s);
+    NOT_NULL(out);
+    *out = s->was_evicted ? 1 : 0;
+    return FLLM_OK;
+}
+
+// KvCache.EvictOldestHalf (KvCache.cs:152-173): in every layer, positions [keep, max) move down to
+// [0, max - keep) and [max - keep, max) are cleared; the length becomes keep = max / 2. For an odd
+// capacity the two ranges share one position, so the move is split in two copies that do not
+// overlap (the first reads that position before the second overwrites it; both are stream-ordered).
+static hipError_t kv_evict(fllm_seq* s) {
+    const size_t kvb = sizeof(float) * (size_t)s->m->kvdim;
+    const size_t pitch = kvb * (size_t)s->max_seq;
+    const int max = s->max_seq, keep = max / 2, len = max - keep;
+    const size_t L = (size_t)s->m->d.n_layers;
+    hipError_t e = hipSuccess;
+    for (float* c : {s->kc, s->vc}) {
+        uint8_t* base = (uint8_t*)c;
+        if (keep > 0 && e == hipSuccess)
+            e = hipMemcpy2DAsync(base, pitch, base + keep * kvb, pitch, keep * kvb, L, hipMemcpyDeviceToDevice, s->st);
+        if (len > keep && keep > 0 && e == hipSuccess)  // capacity 1 keeps nothing: the row stays
+            e = hipMemcpy2DAsync(base + keep * kvb, pitch, base + (size_t)(2 * keep) * kvb, pitch,
+                                 (size_t)(len - keep) * kvb, L, hipMemcpyDeviceToDevice, s->st);
+        if (keep > 0 && e == hipSuccess)
+            e = hipMemset2DAsync(base + (size_t)len * kvb, pitch, 0, (size_t)keep * kvb, L, s->st);
+    }
+    if (e != hipSuccess) return e;
+    s->cur_len = keep;
+    s->was_evicted = true;
+    return hipSuccess;
+}
+
+// The length GetKeys / GetValues return for a layer (KvCache.cs:109-115): one more than the
+// current length for the layers already appended at the position being filled.
+static int kv_effective(const fllm_seq* s, int layer) {
+    return s->cur_len + ((s->next_layer > 0 && layer < s->next_layer) ? 1 : 0);
+}
+
+extern "C" int32_t fllm_kv_length(fllm_seq* s, int32_t layer, int32_t* out) {
+    NOT_NULL(s);
+    NOT_NULL(out);
+    if (layer < 0 || layer >= s->m->d.n_layers)
+        return fail(FLLM_E_ARG_RANGE, "Layer index must be in [0, %d].", s->m->d.n_layers - 1);
+    *out = kv_effective(s, layer);
+    return FLLM_OK;
+}
+
+// KvCache.Append (KvCache.cs:59-97): host slices of kv_dim floats, layers in order, the oldest half
+// evicted when the cache is full.
+extern "C" int32_t fllm_kv_append(fllm_seq* s, int32_t layer, const float* keys, int64_t n_keys,
+                                  const float* values, int64_t n_values) {
+    NOT_NULL(s);
+    const int L = s->m->d.n_layers, kvdim = s->m->kvdim;
+    if (layer < 0 || layer >= L) return fail(FLLM_E_ARG_RANGE, "Layer index must be in [0, %d].", L - 1);
+    if (layer != s->next_layer)
+        return fail(FLLM_E_INVALID_OP,
+                    "KV cache append order violation: expected layer %d but received layer %d. "
+                    "Append layers sequentially for each token position.", s->next_layer, layer);
+    if (n_keys != kvdim || n_values != kvdim)
+        return fail(FLLM_E_ARG, "Key/value slice length must be %d but got key=%lld, value=%lld.", kvdim,
+                    (long long)n_keys, (long long)n_values);
+    NOT_NULL(keys);
+    NOT_NULL(values);
+    HIP_TRY(hipSetDevice(s->m->ctx->device));
+    if (s->cur_len >= s->max_seq) HIP_TRY(kv_evict(s));
+    size_t off = ((size_t)layer * s->max_seq + (size_t)s->cur_len) * kvdim;
+    HIP_TRY(hipMemcpyAsync(s->kc + off, keys, sizeof(float) * kvdim, hipMemcpyHostToDevice, s->st));
+    HIP_TRY(hipMemcpyAsync(s->vc + off, values, sizeof(float) * kvdim, hipMemcpyHostToDevice, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    if (++s->next_layer == L) {
+        s->next_layer = 0;
+        s->cur_len++;
+    }
     return FLLM_OK;
 }
 
@@ -1286,16 +1392,38 @@ static int32_t enqueue_step(fllm_seq* s, int token, int pos) {
     return FLLM_OK;
 }
 
+// KvCache.Append's order check for layer 0 (KvCache.cs:69-74), the first thing a Forward call
+// does to the cache.
+#define APPEND_ORDER_OK(s)                                                                               \
+    do {                                                                                                 \
+        if ((s)->next_layer != 0)                                                                        \
+            return fail(FLLM_E_INVALID_OP,                                                               \
+                        "KV cache append order violation: expected layer %d but received layer 0. "      \
+                        "Append layers sequentially for each token position.", (s)->next_layer);        \
+    } while (0)
+
 extern "C" int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position) {
     NOT_NULL(s);
+    NOT_DISPOSED(s->m);
     const fllm_model_desc& d = s->m->d;
     if (token < 0 || token >= d.vocab)
         return fail(FLLM_E_ARG_RANGE, "Token id %d is outside the valid vocabulary range [0, %d].", token, d.vocab - 1);
-    if (position < 0 || position > s->cur_len)
-        return fail(FLLM_E_ARG_RANGE, "position %d outside the cached range [0, %d]", position, s->cur_len);
-    if (s->cur_len >= s->max_seq)
-        return fail(FLLM_E_ARG_RANGE, "KV cache full (%d positions)", s->max_seq);
+    if (position < 0) return fail(FLLM_E_ARG_RANGE, "position %d must be >= 0", position);
+    APPEND_ORDER_OK(s);
     HIP_TRY(hipSetDevice(s->m->ctx->device));
+    // Layer 0's Append evicts the oldest half of a full cache (KvCache.cs:82-85).
+    if (s->cur_len >= s->max_seq) HIP_TRY(kv_evict(s));
+    if (position > s->cur_len) {
+        // The reference appends layer 0 at the current length, then attention slices positions
+        // [0, position] of a cache that holds cur_len + 1 and throws (LlamaForwardPass.cs:186-188):
+        // the cache is left expecting layer 1. That state is kept here (the row of layer 0 holds
+        // zeros instead of the failed token's keys); nothing is launched.
+        if (++s->next_layer == d.n_layers) {
+            s->next_layer = 0;
+            s->cur_len++;
+        }
+        return fail(FLLM_E_ARG_RANGE, "position %d outside the cached range [0, %d]", position, kv_effective(s, 0) - 1);
+    }
     int32_t rc = enqueue_step(s, token, position);
     if (rc) return rc;
     s->cur_len++;
@@ -1307,8 +1435,10 @@ extern "C" int32_t fllm_decode_greedy(fllm_seq* s, int32_t token, int32_t positi
     NOT_NULL(s);
     const fllm_model_desc& d = s->m->d;
     if (n_steps < 0) return fail(FLLM_E_ARG_RANGE, "n_steps must be >= 0");
+    NOT_DISPOSED(s->m);
     if (n_steps == 0) return FLLM_OK;
     NOT_NULL(out_tokens);
+    APPEND_ORDER_OK(s);
     if (token < 0 || token >= d.vocab)
         return fail(FLLM_E_ARG_RANGE, "Token id %d is outside the valid vocabulary range [0, %d].", token, d.vocab - 1);
     if (position < 0 || position > s->cur_len)
@@ -1472,6 +1602,8 @@ extern "C" int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, i
     NOT_NULL(s);
     if (n < 0) return fail(FLLM_E_ARG_RANGE, "n must be >= 0");
     if (n > 0) NOT_NULL(tokens);
+    NOT_DISPOSED(s->m);
+    APPEND_ORDER_OK(s);
     const fllm_model_desc& d = s->m->d;
     // The batched path runs when the positions continue the cache (the case of a prompt); with
     // debug capture, a single token, or positions that rewrite earlier slots it is n Forward calls.
@@ -1557,6 +1689,9 @@ extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int3
     NOT_NULL(s);
     NOT_NULL(n_out);
     if (k < 1) return fail(FLLM_E_ARG_RANGE, "k must be at least 1.");
+    // 1/Temperature of SamplerPipeline (SamplerPipeline.cs:67-70): finite and >= 0 (an infinite
+    // temperature scales every logit to zero)
+    if (!(inv_temp >= 0.0f) || isinf(inv_temp)) return fail(FLLM_E_ARG_RANGE, "inv_temp must be finite and >= 0.");
     if (cap > 0) { NOT_NULL(ids); NOT_NULL(vals); }
     int V = s->m->d.vocab;
     if (V > SAMPLE_MAX_VOCAB) return fail(FLLM_E_NOT_SUPPORTED, "device top-k handles vocabularies up to %d", SAMPLE_MAX_VOCAB);
@@ -1618,7 +1753,7 @@ extern "C" int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p,
     NOT_NULL(out_token);
     if (!(top_p > 0.0f && top_p <= 1.0f)) return fail(FLLM_E_ARG_RANGE, "topP must be in (0, 1].");
     if (!(u >= 0.0f && u < 1.0f)) return fail(FLLM_E_ARG_RANGE, "u must be in [0, 1).");
-    if (!(inv_temp > 0.0f) || isinf(inv_temp)) return fail(FLLM_E_ARG_RANGE, "inv_temp must be positive and finite.");
+    if (!(inv_temp >= 0.0f) || isinf(inv_temp)) return fail(FLLM_E_ARG_RANGE, "inv_temp must be finite and >= 0.");
     int V = s->m->d.vocab;
     if (V > SAMPLE_MAX_VOCAB) return fail(FLLM_E_NOT_SUPPORTED, "device nucleus sampling handles vocabularies up to %d", SAMPLE_MAX_VOCAB);
     HIP_TRY(launch_sample_nucleus(s->logits, V, inv_temp, top_p, u, s->probs, s->samp_token, s->nuc_sc, s->st));
@@ -1659,7 +1794,7 @@ extern "C" int32_t fllm_kv_read(fllm_seq* s, int32_t layer, int32_t kind, float*
     const fllm_model_desc& d = s->m->d;
     if (layer < 0 || layer >= d.n_layers) return fail(FLLM_E_ARG_RANGE, "Layer index must be in [0, %d].", d.n_layers - 1);
     if (kind != 0 && kind != 1) return fail(FLLM_E_ARG_RANGE, "kind must be 0 (keys) or 1 (values)");
-    int64_t cnt = (int64_t)s->cur_len * s->m->kvdim;
+    int64_t cnt = (int64_t)kv_effective(s, layer) * s->m->kvdim;
     if (n < cnt) return fail(FLLM_E_ARG, "destination must hold %lld floats", (long long)cnt);
     if (cnt == 0) return FLLM_OK;
     const float* src = (kind == 0 ? s->kc : s->vc) + (size_t)layer * s->max_seq * s->m->kvdim;

@@ -429,6 +429,10 @@ __device__ __forceinline__ uint32_t okey(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// Key of the top-k selection: TopKSampler compares floats with > and < (TopKSampler.cs:55-60,
+// 93-105), under which -0 equals +0, so both zeros map to the key of +0.
+__device__ __forceinline__ uint32_t tkey(float v) { return okey(v == 0.0f ? 0.0f : v); }
+
 // First index of the maximum (IndexOfMax semantics). With tokens_out set, also publishes the
 // token as the next step's input and advances the step parameters (device-side greedy loop).
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t n, StepParams* p, int* tokens_out,
@@ -690,7 +694,7 @@ __device__ void topk_radix_emit(const float* __restrict__ x, int n, int k, int c
             __syncthreads();
             const uint32_t prefix = s_prefix, mask = s_mask;
             pass_strided<SAMPLE_BATCH>(x, n, [&](int i, float v) {
-                uint32_t key = okey(v);
+                uint32_t key = tkey(v);
                 wave_hist_add(hist, i < n && (key & mask) == prefix, (key >> shift) & 255u);
             });
             __syncthreads();
@@ -707,14 +711,14 @@ __device__ void topk_radix_emit(const float* __restrict__ x, int n, int k, int c
     }
     // stable compaction: survivors per 64-element chunk, chunk offsets, then ranks by ballot
     pass_chunks<SAMPLE_BATCH>(x, n, nch, [&](int c, int i, float v) {
-        unsigned long long m = __ballot(i < n && okey(v) >= thr);
+        unsigned long long m = __ballot(i < n && tkey(v) >= thr);
         if (lane == 0) chunk[c] = (int)__popcll(m);
     });
     __syncthreads();
     int total = chunks_excl_scan(chunk, nch, scan);
     if (tid == 0) *count = total;
     pass_chunks<SAMPLE_BATCH>(x, n, nch, [&](int c, int i, float v) {
-        bool keep = i < n && okey(v) >= thr;
+        bool keep = i < n && tkey(v) >= thr;
         unsigned long long m = __ballot(keep);
         if (keep) {
             int off = chunk[c] + (int)__popcll(m & lanes_below());
@@ -742,7 +746,7 @@ __device__ void topk_select_candidates(const float* __restrict__ cv, const int* 
         __syncthreads();
         const uint32_t prefix = s_prefix, mask = s_mask;
         for (int j = tid; j < nc; j += nt) {
-            uint32_t key = okey(lv[j]);
+            uint32_t key = tkey(lv[j]);
             if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
         }
         __syncthreads();
@@ -758,12 +762,12 @@ __device__ void topk_select_candidates(const float* __restrict__ cv, const int* 
     const uint32_t thr = s_prefix;
     const int per = (TOPK_CMAX + nt - 1) / nt, b0 = tid * per;
     int cnt = 0;
-    for (int j = b0; j < b0 + per && j < nc; j++) cnt += okey(lv[j]) >= thr ? 1 : 0;
+    for (int j = b0; j < b0 + per && j < nc; j++) cnt += tkey(lv[j]) >= thr ? 1 : 0;
     int total;
     int off = block_excl_scan(cnt, scan, &total);
     for (int j = b0; j < b0 + per && j < nc; j++) {
         float v = lv[j];
-        if (okey(v) >= thr) {
+        if (tkey(v) >= thr) {
             if (off < cap) { ids[off] = ci[j]; vals[off] = v; }
             off++;
         }
@@ -791,7 +795,7 @@ __global__ __launch_bounds__(1024) void k_topk_sample(const float* __restrict__ 
     const int tid = threadIdx.x, nt = blockDim.x;
     for (int j = tid; j < TOPK_NS; j += nt) {
         float v = x[(int)(((int64_t)j * n) / TOPK_NS)];
-        samp[j] = okey(inv_temp != 1.0f ? v * inv_temp : v);
+        samp[j] = tkey(inv_temp != 1.0f ? v * inv_temp : v);
     }
     if (tid == 0) {
         s_prefix = 0;
@@ -841,7 +845,7 @@ __global__ __launch_bounds__(256) void k_topk_count(float* x, int n, float inv_t
                 w = w * inv_temp;
                 x[i] = w;
             }
-            c += okey(w) >= t ? 1 : 0;
+            c += tkey(w) >= t ? 1 : 0;
         }
     }
     for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
@@ -883,7 +887,7 @@ __global__ __launch_bounds__(256) void k_topk_gather(const float* __restrict__ x
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         int i = beg + ((wave * 16 + j) << 6) + lane;
-        m[j] = __ballot(i < n && okey(v[j]) >= t);
+        m[j] = __ballot(i < n && tkey(v[j]) >= t);
         if (lane == 0) cc[wave * 16 + j] = (int)__popcll(m[j]);
     }
     __syncthreads();

@@ -150,6 +150,12 @@ FLLM_API int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer, i
  * matrices whose decode launches run on the matrix cores are regrouped on the device by 16-row
  * tile (the same blocks, permuted; one temporary copy of a matrix at a time). */
 FLLM_API int32_t fllm_model_finalize(fllm_model* m);
+/* LlamaWeights.Dispose (LlamaWeights.cs:93-107): marks the model disposed. Forward, prefill and
+ * decode on a sequence of a disposed model return FLLM_E_DISPOSED before anything runs
+ * (LlamaForwardPass.cs:87, LlamaWeights.cs:138-139), as do upload, finalize and seq_create while
+ * the handle is still valid. The device memory is released at once when no sequence of the model
+ * is alive, otherwise when the last one is destroyed (sequences keep using the weights until
+ * then, so destroy never frees memory a sequence still reads). Idempotent. */
 FLLM_API int32_t fllm_model_destroy(fllm_model* m);
 /* The description the model was created with. */
 FLLM_API int32_t fllm_model_get_desc(fllm_model* m, fllm_model_desc* out);
@@ -161,7 +167,7 @@ FLLM_API int32_t fllm_model_weight_bytes(fllm_model* m, uint64_t* layer_bytes, u
  * LlamaLanguageModel.cs:129); 0 = desc.max_ctx. */
 FLLM_API int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** out);
 FLLM_API int32_t fllm_seq_destroy(fllm_seq* s);
-FLLM_API int32_t fllm_seq_reset(fllm_seq* s);                         /* KvCache.Clear */
+FLLM_API int32_t fllm_seq_reset(fllm_seq* s);                         /* KvCache.Clear (also clears WasEvicted) */
 FLLM_API int32_t fllm_seq_length(fllm_seq* s, int32_t* len);          /* KvCache.CurrentLength */
 FLLM_API int32_t fllm_seq_capacity(fllm_seq* s, int32_t* cap);        /* KvCache.MaxSequenceLength */
 FLLM_API int32_t fllm_seq_get_model(fllm_seq* s, fllm_model** out);
@@ -172,9 +178,17 @@ FLLM_API int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable);
 
 /* IForwardPass.Forward(tokenId, position, kv): one decode step. Appends K/V at the current
  * length, attends over positions [window_start, position], leaves logits on the device.
- * Errors: token outside [0,vocab) -> FLLM_E_ARG_RANGE (LlamaForwardPass.cs:89-93);
- * position > current length, or a full cache -> FLLM_E_ARG_RANGE (the reference's
- * Slice fails the same way, LlamaForwardPass.cs:186-188 after KvCache.cs:82-85). */
+ * A full cache first evicts its oldest half, as KvCache.Append does for layer 0
+ * (KvCache.cs:82-85, 152-173); the RoPE position stays `position`.
+ * Errors, in the reference's order:
+ *  - disposed model -> FLLM_E_DISPOSED (LlamaForwardPass.cs:87);
+ *  - token outside [0,vocab) -> FLLM_E_ARG_RANGE (LlamaForwardPass.cs:89-93);
+ *  - a cache part-way through a position's layers (fllm_kv_append) -> FLLM_E_INVALID_OP
+ *    (KvCache.cs:69-74);
+ *  - position > current length (after any eviction) -> FLLM_E_ARG_RANGE: the reference has then
+ *    appended layer 0 and its attention Slice throws (LlamaForwardPass.cs:186-188), leaving the
+ *    cache expecting layer 1; the same state is kept here (layer 0's row at that slot is zeros),
+ *    so later Forward calls fail with FLLM_E_INVALID_OP until fllm_seq_reset. */
 FLLM_API int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position);
 /* n consecutive Forward calls for tokens[0..n) at positions pos0.. (prefill loop,
  * LlamaLanguageModel.cs:133-137), with their results: the K/V rows of every position, the last
@@ -206,9 +220,12 @@ FLLM_API int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token);
 /* Top-k candidate selection of SamplerPipeline.Sample stages 1-2 (SamplerPipeline.cs:67-74,
  * TopKSampler.ApplyTopK TopKSampler.cs:42-71): scales the logits by inv_temp in place
  * (when inv_temp != 1), finds the k-th largest scaled value and returns every index whose
- * scaled logit is >= that threshold (ties kept), in ascending index order, with the scaled
- * values. cap is the capacity of ids/vals; FLLM_E_ARG if more than cap survive. One workgroup;
- * vocabularies above 262144 -> FLLM_E_NOT_SUPPORTED. */
+ * scaled logit is >= that threshold (ties kept, -0 and +0 equal as in float comparison), in
+ * ascending index order, with the scaled values. cap is the capacity of ids/vals; FLLM_E_ARG if
+ * more than cap survive. A grid of 4096-entry segments samples, counts and gathers the
+ * candidates; one workgroup selects among them (or over the whole vocabulary when the sample
+ * misses). inv_temp must be finite and >= 0 (FLLM_E_ARG_RANGE otherwise); vocabularies above
+ * 262144 -> FLLM_E_NOT_SUPPORTED. */
 FLLM_API int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k,
                                   int32_t* ids, float* vals, int32_t cap, int32_t* n_out);
 /* LlamaLanguageModel.ApplyRepetitionPenalty (LlamaLanguageModel.cs:183-186, 357-373) on the device
@@ -225,7 +242,8 @@ FLLM_API int32_t fllm_logits_penalize(fllm_seq* s, const int32_t* ids, int32_t n
  * TemperatureSampler.cs:53-70), u being the pipeline's XoshiroRandom.NextFloat() for this draw.
  * Running sums are exact fixed-point where the reference sums f32 in order: the token can differ
  * from the reference only when u or top_p falls within f32 rounding of a boundary.
- * Errors: top_p outside (0,1], u outside [0,1), inv_temp not positive and finite -> FLLM_E_ARG_RANGE;
+ * Errors: top_p outside (0,1], u outside [0,1), inv_temp not finite or negative -> FLLM_E_ARG_RANGE
+ * (inv_temp 0, an infinite temperature, makes every logit 0: the draw is uniform);
  * vocabularies above 262144 -> FLLM_E_NOT_SUPPORTED (one workgroup). */
 FLLM_API int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p, float u, int32_t* out_token);
 /* The distribution fllm_sample_nucleus drew from (vocab floats: the renormalised nucleus, zeros
@@ -237,8 +255,23 @@ FLLM_API int32_t fllm_probs_copy(fllm_seq* s, float* dst, int64_t n);
  * before that step); layer == n_layers gives the final-normed vector fed to the LM head. */
 FLLM_API int32_t fllm_debug_hidden(fllm_seq* s, int32_t layer, float* dst, int64_t n);
 /* KvCache.GetKeys / GetValues (KvCache.cs:100-135): kind 0 = keys, 1 = values.
- * Copies current_length * kv_dim floats. */
+ * Copies effective_length * kv_dim floats, effective_length being the current length plus one
+ * for the layers already appended at the position being filled (KvCache.cs:109-115).
+ * Layer outside [0, n_layers) -> FLLM_E_ARG_RANGE; n too small -> FLLM_E_ARG. */
 FLLM_API int32_t fllm_kv_read(fllm_seq* s, int32_t layer, int32_t kind, float* dst, int64_t n);
+/* KvCache.Append (KvCache.cs:59-97) for a caller that fills the device cache itself (a C# forward
+ * pass over HipKvCache): copies kv_dim host floats of keys and of values to the slot at the current
+ * length of `layer`. Layers go in order 0..n_layers-1 for each position; the last one advances the
+ * length. A full cache first evicts its oldest half (KvCache.cs:82-85, 152-173) and sets
+ * WasEvicted. Errors, in the reference's order: layer outside [0, n_layers) -> FLLM_E_ARG_RANGE;
+ * layer out of order -> FLLM_E_INVALID_OP; n_keys or n_values != kv_dim -> FLLM_E_ARG. */
+FLLM_API int32_t fllm_kv_append(fllm_seq* s, int32_t layer, const float* keys, int64_t n_keys,
+                                const float* values, int64_t n_values);
+/* Positions GetKeys / GetValues of `layer` hold (the effective length above: the span length over
+ * kv_dim, KvCache.cs:109-115). Layer outside [0, n_layers) -> FLLM_E_ARG_RANGE. */
+FLLM_API int32_t fllm_kv_length(fllm_seq* s, int32_t layer, int32_t* out);
+/* KvCache.WasEvicted (KvCache.cs:56): 1 once an eviction happened since creation or the last reset. */
+FLLM_API int32_t fllm_kv_was_evicted(fllm_seq* s, int32_t* out);
 
 /* ---- kernels exposed for verification and microbenchmarks ------------------ */
 /* Dequantizer.Dequantize(type, src, dst) (Dequantizer.cs:488-504) on the device:

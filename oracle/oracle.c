@@ -26,10 +26,13 @@
  *    positive logit divide it k times).
  *  - forward pass: invariants (context of one => attention returns v0, GQA mapping,
  *    window start) and the reference's deterministic 2-layer fixtures.
+ *  - row-parallel mode (orc_set_threads): pinned by bit-equality with one thread on every
+ *    function it splits (tests/test_oracle_forward.py).
  */
 #include "oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -38,6 +41,97 @@
 #define ORC_E_ARG (-2)
 #define ORC_E_INVALID (-3)
 #define ORC_E_NOTSUP (-4)
+
+/* ---------------------------------------------------------------------------------
+ * Row-parallel mode (orc_set_threads). The reference is single-threaded; splitting the rows
+ * of a projection, the heads of an attention or the blocks of a dequantization over threads
+ * leaves every output element computed by the same function on the same operands in the same
+ * order, so results are bit-identical to one thread. It only makes the full-size models
+ * tractable as a checker.
+ * ------------------------------------------------------------------------------- */
+#define ORC_MAX_THREADS 64
+typedef void (*orc_task)(void* arg, int64_t begin, int64_t end);
+
+static struct {
+    int n;                         /* threads including the caller */
+    pthread_t th[ORC_MAX_THREADS];
+    pthread_mutex_t mu;
+    pthread_cond_t go, done;
+    unsigned long gen;
+    int pending, quit;
+    orc_task fn;
+    void* arg;
+    int64_t total;
+} pool = {1, {0}, PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER, 0, 0, 0, 0, 0, 0};
+
+static void pool_slice(int i, int n, int64_t total, int64_t* b, int64_t* e) {
+    *b = total * i / n;
+    *e = total * (i + 1) / n;
+}
+
+static void* pool_worker(void* p) {
+    int id = (int)(intptr_t)p;
+    unsigned long seen = 0;
+    for (;;) {
+        pthread_mutex_lock(&pool.mu);
+        while (pool.gen == seen && !pool.quit) pthread_cond_wait(&pool.go, &pool.mu);
+        if (pool.quit) { pthread_mutex_unlock(&pool.mu); return NULL; }
+        seen = pool.gen;
+        orc_task fn = pool.fn;
+        void* arg = pool.arg;
+        int64_t total = pool.total, b, e;
+        int n = pool.n;
+        pthread_mutex_unlock(&pool.mu);
+        pool_slice(id, n, total, &b, &e);
+        if (b < e) fn(arg, b, e);
+        pthread_mutex_lock(&pool.mu);
+        if (--pool.pending == 0) pthread_cond_signal(&pool.done);
+        pthread_mutex_unlock(&pool.mu);
+    }
+}
+
+/* Runs fn over [0, total) split into pool.n contiguous ranges, the caller taking the first. */
+static void pool_run(orc_task fn, void* arg, int64_t total) {
+    int n = pool.n;
+    if (n <= 1 || total < 2) { if (total > 0) fn(arg, 0, total); return; }
+    pthread_mutex_lock(&pool.mu);
+    pool.fn = fn;
+    pool.arg = arg;
+    pool.total = total;
+    pool.pending = n - 1;
+    pool.gen++;
+    pthread_cond_broadcast(&pool.go);
+    pthread_mutex_unlock(&pool.mu);
+    int64_t b, e;
+    pool_slice(0, n, total, &b, &e);
+    if (b < e) fn(arg, b, e);
+    pthread_mutex_lock(&pool.mu);
+    while (pool.pending > 0) pthread_cond_wait(&pool.done, &pool.mu);
+    pthread_mutex_unlock(&pool.mu);
+}
+
+int orc_set_threads(int n) {
+    if (n < 1) n = 1;
+    if (n > ORC_MAX_THREADS) n = ORC_MAX_THREADS;
+    if (n == pool.n) return n;
+    if (pool.n > 1) {
+        pthread_mutex_lock(&pool.mu);
+        pool.quit = 1;
+        pthread_cond_broadcast(&pool.go);
+        pthread_mutex_unlock(&pool.mu);
+        for (int i = 1; i < pool.n; i++) pthread_join(pool.th[i], NULL);
+    }
+    pool.quit = 0;
+    pool.gen = 0;
+    pool.n = 1;
+    for (int i = 1; i < n; i++) {
+        if (pthread_create(&pool.th[i], NULL, pool_worker, (void*)(intptr_t)i) != 0) break;
+        pool.n = i + 1;
+    }
+    return pool.n;
+}
+
+int orc_get_threads(void) { return pool.n; }
 
 /* ---------------------------------------------------------------------------------
  * Scalar conversions. Dequantizer.HalfToFloat (Dequantizer.cs:49-51) is the exact
@@ -94,25 +188,25 @@ int orc_element_count(int type, int64_t nbytes, int64_t* out) {
     }
 }
 
-/* Dequantizer.Dequantize dispatch (Dequantizer.cs:488-504) and the per-type routines. */
-int orc_dequantize(int type, const uint8_t* src, int64_t nbytes, float* dst, int64_t n) {
-    int64_t bb, be;
+static int block_geometry(int type, int64_t* bb, int64_t* be) {
     switch (type) {
-        case 0: bb = 4; be = 1; break;
-        case 1: case 30: bb = 2; be = 1; break;
-        case 2: bb = 18; be = 32; break;
-        case 8: bb = 34; be = 32; break;
-        case 12: bb = 144; be = 256; break;
-        case 13: bb = 176; be = 256; break;
-        case 14: bb = 210; be = 256; break;
-        case 15: bb = 292; be = 256; break;
+        case 0: *bb = 4; *be = 1; return ORC_OK;
+        case 1: case 30: *bb = 2; *be = 1; return ORC_OK;
+        case 2: *bb = 18; *be = 32; return ORC_OK;
+        case 8: *bb = 34; *be = 32; return ORC_OK;
+        case 12: *bb = 144; *be = 256; return ORC_OK;
+        case 13: *bb = 176; *be = 256; return ORC_OK;
+        case 14: *bb = 210; *be = 256; return ORC_OK;
+        case 15: *bb = 292; *be = 256; return ORC_OK;
         default: return ORC_E_NOTSUP;
     }
-    if (nbytes % bb != 0) return ORC_E_ARG;           /* "Source length must be a multiple" */
-    int64_t nblk = nbytes / bb;
-    if (n < nblk * be) return ORC_E_ARG;              /* "Destination must hold at least" */
+}
 
-    for (int64_t b = 0; b < nblk; b++) {
+/* The per-type routines of Dequantizer.cs over blocks [b0, b1). */
+static void dequant_blocks(int type, const uint8_t* src, float* dst, int64_t b0, int64_t b1) {
+    int64_t bb = 1, be = 1;
+    block_geometry(type, &bb, &be);
+    for (int64_t b = b0; b < b1; b++) {
         const uint8_t* blk = src + b * bb;
         float* o = dst + b * be;
         switch (type) {
@@ -201,6 +295,24 @@ int orc_dequantize(int type, const uint8_t* src, int64_t nbytes, float* dst, int
             }
         }
     }
+}
+
+typedef struct { int type; const uint8_t* src; float* dst; } dequant_job;
+static void dequant_task(void* a, int64_t b0, int64_t b1) {
+    dequant_job* j = (dequant_job*)a;
+    dequant_blocks(j->type, j->src, j->dst, b0, b1);
+}
+
+/* Dequantizer.Dequantize dispatch (Dequantizer.cs:488-504) and the per-type routines. */
+int orc_dequantize(int type, const uint8_t* src, int64_t nbytes, float* dst, int64_t n) {
+    int64_t bb, be;
+    if (block_geometry(type, &bb, &be) != ORC_OK) return ORC_E_NOTSUP;
+    if (nbytes % bb != 0) return ORC_E_ARG;           /* "Source length must be a multiple" */
+    int64_t nblk = nbytes / bb;
+    if (n < nblk * be) return ORC_E_ARG;              /* "Destination must hold at least" */
+    dequant_job j = {type, src, dst};
+    if (nblk >= 4096) pool_run(dequant_task, &j, nblk);
+    else dequant_blocks(type, src, dst, 0, nblk);
     return ORC_OK;
 }
 
@@ -220,9 +332,18 @@ float orc_dot(const float* a, const float* b, int64_t n) {
     return s;
 }
 
-/* LinearProjection (LlamaForwardPass.cs:237-260): y[i] = Dot(x, W[i*cols .. +cols]). */
+typedef struct { const float* x; const float* W; float* y; int64_t cols; } linear_job;
+static void linear_task(void* a, int64_t r0, int64_t r1) {
+    linear_job* j = (linear_job*)a;
+    for (int64_t i = r0; i < r1; i++) j->y[i] = orc_dot(j->x, j->W + (size_t)i * (size_t)j->cols, j->cols);
+}
+
+/* LinearProjection (LlamaForwardPass.cs:237-260): y[i] = Dot(x, W[i*cols .. +cols]).
+ * Rows are split over the row-parallel threads; each row is the same orc_dot call. */
 void orc_linear(const float* x, const float* W, float* y, int64_t rows, int64_t cols) {
-    for (int64_t i = 0; i < rows; i++) y[i] = orc_dot(x, W + (size_t)i * (size_t)cols, cols);
+    linear_job j = {x, W, y, cols};
+    if (rows * cols >= (1 << 16)) pool_run(linear_task, &j, rows);
+    else linear_task(&j, 0, rows);
 }
 
 /* RmsNorm (TensorOperations.cs:42-54). */
@@ -601,7 +722,8 @@ orc_fwd* orc_fwd_create(orc_model* m, int32_t max_seq) {
     f->ffa = (float*)calloc((size_t)d->ffn, sizeof(float));
     f->ffb = (float*)calloc((size_t)d->ffn, sizeof(float));
     f->logits = (float*)calloc((size_t)d->vocab, sizeof(float));
-    f->scores = (float*)calloc((size_t)f->max_seq + 1, sizeof(float));
+    /* one score row per query head, so heads can run on separate threads */
+    f->scores = (float*)calloc(((size_t)f->max_seq + 1) * (size_t)d->n_heads, sizeof(float));
     f->hidden = (float*)calloc((size_t)(d->n_layers + 1) * (size_t)d->hidden, sizeof(float));
     f->lim_layers = d->n_layers;
     f->lim_head = d->vocab;
@@ -652,35 +774,51 @@ static int kv_effective(const orc_fwd* f, int layer) {
     return e;
 }
 
+typedef struct { orc_fwd* f; int layer, ws, seq_len; float scale; } attn_job;
+
+/* One query head of ComputeAttention: scores over [ws, seq_len), optional Gemma softcap,
+ * softmax, weighted sum of values. */
+static void attn_heads(void* a, int64_t h0, int64_t h1) {
+    attn_job* j = (attn_job*)a;
+    orc_fwd* f = j->f;
+    orc_model* m = f->m;
+    const orc_desc* d = &m->d;
+    int hd = d->head_dim, kvdim = m->kvdim, group = d->n_heads / d->n_kv_heads;
+    int ws = j->ws, seq_len = j->seq_len, alen = seq_len - ws;
+    const float* K = f->keys[j->layer];
+    const float* V = f->vals[j->layer];
+    for (int64_t h = h0; h < h1; h++) {
+        int kh = (int)h / group;
+        float* scores = f->scores + (size_t)h * ((size_t)f->max_seq + 1);
+        const float* qh = f->q + (size_t)h * hd;
+        for (int t = ws; t < seq_len; t++)
+            scores[t - ws] = orc_dot(qh, K + (size_t)t * kvdim + (size_t)kh * hd, hd) * j->scale;
+        if (d->arch == A_GEMMA2 && d->attn_softcap > 0.0f) orc_softcap(scores, alen, d->attn_softcap);
+        orc_softmax(scores, alen);
+        float* out = f->att + (size_t)h * hd;
+        for (int t = ws; t < seq_len; t++) {
+            const float* vv = V + (size_t)t * kvdim + (size_t)kh * hd;
+            float w = scores[t - ws];
+            for (int e = 0; e < hd; e++) out[e] += w * vv[e];
+        }
+    }
+}
+
 /* ComputeAttention (LlamaForwardPass.cs:158-211; MistralForwardPass.cs:121-175 window;
- * Gemma2ForwardPass.cs:126-185 scale, softcap, window). */
+ * Gemma2ForwardPass.cs:126-185 scale, softcap, window). Heads are independent and may run on
+ * the row-parallel threads. */
 static int attention(orc_fwd* f, int layer, int seq_len, int window) {
     orc_model* m = f->m;
     const orc_desc* d = &m->d;
-    int hd = d->head_dim, nh = d->n_heads, nkv = d->n_kv_heads, kvdim = m->kvdim;
-    int group = nh / nkv;
+    int hd = d->head_dim;
     float scale = d->arch == A_GEMMA2 ? d->attn_scale : 1.0f / sqrtf((float)hd);
     if (seq_len > kv_effective(f, layer)) return ORC_E_RANGE; /* Span.Slice past the cache */
     int ws = seq_len - window;
     if (ws < 0) ws = 0;
-    int alen = seq_len - ws;
-    const float* K = f->keys[layer];
-    const float* V = f->vals[layer];
     memset(f->att, 0, sizeof(float) * (size_t)m->qdim);
-    for (int h = 0; h < nh; h++) {
-        int kh = h / group;
-        const float* qh = f->q + (size_t)h * hd;
-        for (int t = ws; t < seq_len; t++)
-            f->scores[t - ws] = orc_dot(qh, K + (size_t)t * kvdim + (size_t)kh * hd, hd) * scale;
-        if (d->arch == A_GEMMA2 && d->attn_softcap > 0.0f) orc_softcap(f->scores, alen, d->attn_softcap);
-        orc_softmax(f->scores, alen);
-        float* out = f->att + (size_t)h * hd;
-        for (int t = ws; t < seq_len; t++) {
-            const float* vv = V + (size_t)t * kvdim + (size_t)kh * hd;
-            float w = f->scores[t - ws];
-            for (int e = 0; e < hd; e++) out[e] += w * vv[e];
-        }
-    }
+    attn_job j = {f, layer, ws, seq_len, scale};
+    if ((int64_t)(seq_len - ws) * m->qdim >= 4096) pool_run(attn_heads, &j, d->n_heads);
+    else attn_heads(&j, 0, d->n_heads);
     return ORC_OK;
 }
 

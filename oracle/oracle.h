@@ -17,6 +17,12 @@
 extern "C" {
 #endif
 
+/* Row-parallel mode: n threads (1 = the reference's single thread, the default). Rows of a
+ * projection, heads of an attention and blocks of a dequantization are split over them; every
+ * output element is computed exactly as with one thread. Returns the thread count in effect. */
+int orc_set_threads(int n);
+int orc_get_threads(void);
+
 /* scalar conversions */
 float orc_half_to_float(uint16_t h);
 float orc_bf16_to_float(uint16_t b);

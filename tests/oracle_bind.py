@@ -34,6 +34,8 @@ class OrcXoshiro(C.Structure):
 
 
 _sigs = {
+    "orc_set_threads": (C.c_int, [C.c_int]),
+    "orc_get_threads": (C.c_int, []),
     "orc_half_to_float": (F32, [C.c_uint16]),
     "orc_bf16_to_float": (F32, [C.c_uint16]),
     "orc_dequantize": (C.c_int, [C.c_int, P, I64, PF, I64]),

@@ -150,14 +150,18 @@ def test_forward_error_contract(ctx):
         with pytest.raises(F.ArgumentOutOfRangeException):
             fwd.forward(-1, 0, kv)
         with pytest.raises(F.ArgumentOutOfRangeException):
-            fwd.forward(3, 1, kv)  # position beyond the cached length
+            fwd.forward(3, 1, kv)  # position beyond the cached length: layer 0 appended, then the Slice throws
+        with pytest.raises(F.InvalidOperationException):
+            fwd.forward(3, 0, kv)  # the cache now expects layer 1 (KvCache.cs:69-74)
+        kv.clear()
         for p in range(4):
             fwd.forward(3 + p, p, kv)
-        assert kv.current_length == 4 and kv.max_sequence_length == 4
+        assert kv.current_length == 4 and kv.max_sequence_length == 4 and not kv.was_evicted
         with pytest.raises(F.ArgumentOutOfRangeException):
-            fwd.forward(3, 4, kv)  # cache full
+            fwd.forward(3, 4, kv)  # full: evicts the oldest half, then position 4 is past the 2 kept
+        assert kv.was_evicted and kv.current_length == 2
         kv.clear()
-        assert kv.current_length == 0
+        assert kv.current_length == 0 and not kv.was_evicted
         fwd.forward(3, 0, kv)
         assert np.all(np.isfinite(fwd.logits))
         with pytest.raises(F.ArgumentNullException):

@@ -114,6 +114,50 @@ def test_batched_prefill_several_chunks(ctx):
         m.close()
 
 
+@pytest.mark.parametrize("arch", [N.ARCH_MISTRAL, N.ARCH_GEMMA2])
+def test_batched_prefill_window_across_chunks(ctx, arch):
+    """A sliding window of 700 over a 1100-token prompt (chunks of 512, 512, 76): from position 700
+    on, the first keys a row may attend are in an earlier chunk, so the window start of the batched
+    attention is checked against keys other chunks stored (Mistral: every layer windowed; Gemma-2:
+    the even layer, with softcaps). Logits, K/V rows on both sides of the edge and the greedy tokens
+    after it against the oracle."""
+    from dotnetfoundryllm_amd.configs import _cfg, _types
+    if arch == N.ARCH_MISTRAL:
+        cfg = _cfg("window-mistral", arch, 2, 256, 4, 2, 512, 512, 1200, 10000.0, _types(*([N.Q8_0] * 8)),
+                   window=700, norm_std=0.1, seed=24)
+    else:
+        cfg = _cfg("window-gemma2", arch, 2, 256, 4, 2, 512, 512, 1200, 10000.0, _types(*([N.Q8_0] * 8)),
+                   head_dim=128, emb_type=N.BF16, window=700, attn_softcap=50.0, final_softcap=30.0,
+                   norm_std=0.1, seed=25)
+    desc = desc_of(cfg)
+    tensors = {e[0]: (e, synth_bytes(cfg, e)) for e in tensor_plan(cfg)}
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors)
+    prompt = F.synth_tokens(cfg["seed"], 3, desc.vocab, 1100)
+    try:
+        fwd.prefill(prompt, 0, kv)
+        _oracle_prefill(orc, prompt)
+        assert kv.current_length == 1100
+        assert O.normwise_rel_err(fwd.logits, orc.logits()) <= TOL
+        kvdim = desc.n_kv_heads * desc.head_dim
+        for l in range(desc.n_layers):
+            k, v = kv.get_keys(l), kv.get_values(l)
+            kr, vr = orc.kv(l, 0), orc.kv(l, 1)
+            assert O.normwise_rel_err(k, kr) <= TOL and O.normwise_rel_err(v, vr) <= TOL
+            for pos in (0, 511, 512, 699, 700, 701, 1023, 1024, 1099):
+                row = slice(pos * kvdim, (pos + 1) * kvdim)
+                assert O.normwise_rel_err(k[row], kr[row]) <= TOL, (l, pos)
+                assert O.normwise_rel_err(v[row], vr[row]) <= TOL, (l, pos)
+        toks = fwd.decode_greedy(int(prompt[-1]), 1100, 6, kv)
+        assert list(toks) == _oracle_continue(orc, prompt[-1], 1100, 6)
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
+
+
 def test_batched_prefill_llama3_8b_shape(ctx):
     """Full Llama-3-8B shapes (Q4_K + Q6_K, tile-interleaved weights), two layers, a 24-token
     prompt: logits, K/V and the next greedy tokens against the oracle."""

@@ -186,7 +186,8 @@ def test_nucleus_edge_cases(big_vocab):
     # the running sum below u picks the last nonzero probability)
     fwd.write_logits(lg)
     assert fwd.sample_nucleus(1.0, 1.0, float(np.nextafter(np.float32(1), np.float32(0)))) in (V - 1, V - 2)
-    for bad in ((1.0, 0.0, 0.5), (1.0, 1.1, 0.5), (1.0, 0.9, 1.0), (1.0, 0.9, -0.1), (0.0, 0.9, 0.5)):
+    # (inv_temp 0 is an infinite temperature, accepted: test_inverse_temperature_contract)
+    for bad in ((1.0, 0.0, 0.5), (1.0, 1.1, 0.5), (1.0, 0.9, 1.0), (1.0, 0.9, -0.1), (-1.0, 0.9, 0.5)):
         with pytest.raises(F.ArgumentOutOfRangeException):
             fwd.sample_nucleus(*bad)
 
@@ -306,3 +307,104 @@ def test_nucleus_and_topk_small_vocab(ctx):
     finally:
         kv.close()
         m.close()
+
+
+def test_topk_at_qwen2_vocabulary(ctx):
+    """Top-k 40 at temperature 0.8 over the Qwen2-7B vocabulary (152064 entries, 38 segments of the
+    grid sampler, the last one partly filled): survivors bit-exact with the oracle's ApplyTopK on
+    the scaled logits, and SamplerPipeline(0.8, 40, 1.0, seed) draws the oracle pipeline's tokens
+    with the same XoshiroRandom stream, on the model's own logits and on synthetic ones."""
+    cfg, desc, tensors = synthetic("test-qwen2-v152k")
+    assert desc.vocab == 152064
+    m = F.Model(ctx, desc)
+    upload(m, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    rng = np.random.default_rng(152064)
+    inv = float(_inv_temp(0.8))
+    try:
+        cases = []
+        for p, t in enumerate((5, 151999, 77)):
+            fwd.forward(t, p, kv)
+            cases.append(fwd.logits)
+        cases.append(rng.standard_normal(desc.vocab).astype(np.float32))
+        lg = np.round(rng.standard_normal(desc.vocab) * 3, 1).astype(np.float32)  # many ties at the edge
+        cases.append(lg)
+        lg = lg.copy()
+        lg[-5:] = 50.0  # the top entries in the partly filled last segment
+        cases.append(lg)
+        for lg in cases:
+            fwd.write_logits(lg, kv)
+            ids, vals = fwd.sample_topk(inv, 40, cap=desc.vocab)
+            scaled = lg * np.float32(inv)
+            ref = scaled.copy()
+            O.lib.orc_apply_topk(O.fp(ref), ref.size, 40)
+            keep = np.nonzero(ref != -np.inf)[0]
+            assert np.array_equal(ids, keep) and np.array_equal(vals, scaled[keep])
+        sp = F.SamplerPipeline(0.8, 40, 1.0, 0x5EED)
+        r = O.Xoshiro(0x5EED)
+        try:
+            for lg in cases * 4:
+                fwd.write_logits(lg, kv)
+                assert sp.sample(kv) == O.sampler_pipeline_p(lg, 0.8, 40, 1.0, r)
+        finally:
+            sp.close()
+    finally:
+        kv.close()
+        m.close()
+
+
+def test_topk_signed_zero_threshold(big_vocab):
+    """TopKSampler compares floats (TopKSampler.cs:55-60, 93-105), so -0 and +0 tie: when the k-th
+    largest value is a zero, every zero of either sign survives, as in the oracle."""
+    desc, m, kv, fwd = big_vocab
+    V = desc.vocab
+    rng = np.random.default_rng(40)
+    for k, neg_first in ((40, True), (40, False), (7, True)):
+        lg = -np.abs(rng.standard_normal(V)).astype(np.float32) - 1.0
+        lg[rng.choice(V, k // 2, replace=False)] = 5.0
+        zeros = rng.choice(np.nonzero(lg < 0)[0], 300, replace=False)
+        lg[zeros] = 0.0
+        lg[zeros[::2]] = -0.0
+        if neg_first:
+            lg[zeros.min()] = -0.0
+        else:
+            lg[zeros.min()] = 0.0
+        fwd.write_logits(lg)
+        ids, vals = fwd.sample_topk(1.0, k, cap=V)
+        ref = lg.copy()
+        O.lib.orc_apply_topk(O.fp(ref), ref.size, k)
+        keep = np.nonzero(ref != -np.inf)[0]
+        assert keep.size == k // 2 + 300
+        assert np.array_equal(ids, keep)
+        assert np.array_equal(vals.view(np.uint32), lg[keep].view(np.uint32))
+
+
+def test_inverse_temperature_contract(big_vocab):
+    """inv_temp = 1/Temperature (SamplerPipeline.cs:67-70) must be finite and >= 0 on both device
+    samplers; 0 (an infinite temperature) makes every logit zero, so top-k keeps every entry and the
+    nucleus is the uniform distribution."""
+    desc, m, kv, fwd = big_vocab
+    V = desc.vocab
+    lg = np.random.default_rng(2).standard_normal(V).astype(np.float32)
+    for bad in (float("nan"), -1.0, float("inf")):
+        fwd.write_logits(lg)
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.sample_topk(bad, 40, cap=V)
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.sample_nucleus(bad, 1.0, 0.5)
+    fwd.write_logits(lg)
+    ids, vals = fwd.sample_topk(0.0, 40, cap=V)
+    assert np.array_equal(ids, np.arange(V)) and np.all(vals == 0.0)
+    fwd.write_logits(lg)
+    tok = fwd.sample_nucleus(0.0, 1.0, 0.6180339)
+    got = fwd.probs()
+    assert np.all(got == got[0]) and abs(float(got.sum(dtype=np.float64)) - 1.0) < 1e-5
+    assert abs(tok - int(0.6180339 * V)) <= 1
+    sp = F.SamplerPipeline(float("inf"), 0, 1.0, 7)
+    try:
+        fwd.write_logits(lg)
+        tok = sp.sample(kv)
+        assert 0 <= tok < V
+    finally:
+        sp.close()

@@ -211,3 +211,50 @@ def test_kv_cache_semantics_and_errors():
         assert m.forward(5, 1) == -1                   # position beyond the cached length
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("name", ["test-llama", "test-gemma2-hd256", "test-qwen2"])
+def test_row_parallel_mode_is_bit_identical(name):
+    """orc_set_threads splits rows, heads and dequantized blocks over threads; every logit, hidden
+    state and KV row must equal the single-thread run bit for bit (the mode that makes the
+    full-size goldens tractable changes nothing)."""
+    cfg, desc, tensors = synthetic(name)
+    prompt = [int(t) for t in np.random.default_rng(3).integers(0, desc.vocab, 40)]
+    runs = []
+    for threads in (1, 5):
+        assert O.lib.orc_set_threads(threads) == threads
+        m = O.OracleModel(desc, tensors)
+        try:
+            logits, hid = [], []
+            for pos, t in enumerate(prompt):
+                assert m.forward(t, pos) == 0
+                logits.append(m.logits())
+                hid.append(np.stack([m.hidden(l) for l in range(desc.n_layers + 1)]))
+            kv = [m.kv(l, k) for l in range(desc.n_layers) for k in (0, 1)]
+            runs.append((np.stack(logits), np.stack(hid), kv))
+        finally:
+            m.close()
+    O.lib.orc_set_threads(1)
+    (l1, h1, kv1), (l5, h5, kv5) = runs
+    assert np.array_equal(l1.view(np.uint32), l5.view(np.uint32))
+    assert np.array_equal(h1.view(np.uint32), h5.view(np.uint32))
+    for a, b in zip(kv1, kv5):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_row_parallel_linear_and_dequant_bit_identical():
+    rng = np.random.default_rng(5)
+    W = rng.standard_normal((777, 1031)).astype(np.float32)
+    x = rng.standard_normal(1031).astype(np.float32)
+    raw = rng.integers(0, 256, 144 * 5000, dtype=np.uint8)
+    raw[0::144] = 0x10  # finite f16 scales
+    raw[1::144] = 0x1C
+    out = []
+    for threads in (1, 7):
+        O.lib.orc_set_threads(threads)
+        rc, deq = O.dequantize(N.Q4_K, raw)
+        assert rc == 0
+        out.append((O.linear(W, x), deq))
+    O.lib.orc_set_threads(1)
+    assert np.array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
