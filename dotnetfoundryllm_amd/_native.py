@@ -32,6 +32,10 @@ BLOCK = {F32: (4, 1), F16: (2, 1), BF16: (2, 1), Q4_0: (18, 32), Q8_0: (34, 32),
 
 ARCH_LLAMA, ARCH_MISTRAL, ARCH_QWEN2, ARCH_GEMMA2 = 0, 1, 2, 3
 
+# limits of fllm_dequantize_noalloc (FLLM_NOALLOC_MAX_BYTES / FLLM_NOALLOC_MAX_ELEMS)
+NOALLOC_MAX_BYTES = 2 << 20
+NOALLOC_MAX_ELEMS = 2 << 20
+
 SLOT_TOKEN_EMBD, SLOT_OUTPUT_NORM, SLOT_OUTPUT = 0, 1, 2
 SLOT_ATTN_NORM, SLOT_ATTN_Q, SLOT_ATTN_K, SLOT_ATTN_V, SLOT_ATTN_OUTPUT = 10, 11, 12, 13, 14
 SLOT_ATTN_Q_BIAS, SLOT_ATTN_K_BIAS, SLOT_ATTN_V_BIAS, SLOT_POST_ATTN_NORM = 15, 16, 17, 18
@@ -113,6 +117,7 @@ DEVICE_SIGS = {
     "fllm_kv_append": (I32, [P, I32, PF32, I64, PF32, I64]),
     "fllm_kv_was_evicted": (I32, [P, PI32]),
     "fllm_dequantize": (I32, [P, I32, P, U64, PF32, I64]),
+    "fllm_dequantize_noalloc": (I32, [P, I32, P, U64, PF32, I64]),
     "fllm_element_count": (I32, [I32, I64, PI64]),
     "fllm_buf_create": (I32, [P, U64, PP]),
     "fllm_buf_destroy": (I32, [P]),

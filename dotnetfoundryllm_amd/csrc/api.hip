@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <map>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -67,7 +68,35 @@ struct fllm_ctx {
     int n_cu = 0;
     int64_t hbm = 0;
     Staging stage;
+    uint8_t* scratch = nullptr;  // this device's address of the no-allocation scratch array
+    hipError_t scratch_err = hipSuccess;  // why it could not be resolved, if so
 };
+
+// Scratch of fllm_dequantize_noalloc: the staged source blocks (kNoallocSrcBytes plus the slack the
+// dequant kernel may read past them) and the dequantized floats (kNoallocElems). Each device holds
+// its own copy for the life of the process. On the host the array's name is no device address: its
+// per-device address comes from hipGetSymbolAddress at context creation (g_scratch_dev).
+static const size_t kNoallocSrcBytes = FLLM_NOALLOC_MAX_BYTES;
+static const size_t kNoallocElems = FLLM_NOALLOC_MAX_ELEMS;
+static const size_t kNoallocSrcRegion = kNoallocSrcBytes + 256;
+static __device__ __align__(256) uint8_t scratch[kNoallocSrcRegion + kNoallocElems * sizeof(float)];
+
+static const int kMaxDevices = 64;
+static uint8_t* g_scratch_dev[kMaxDevices];  // per device, set once with that device current
+static std::mutex g_scratch_mu;
+
+// Resolves this device's scratch address once (the device is current).
+static hipError_t scratch_init(int device, uint8_t** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[device]) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_dev[device] = (uint8_t*)ptr;
+    }
+    *out = g_scratch_dev[device];
+    return hipSuccess;
+}
 
 // Copies n bytes of host memory to the device through the context's pinned staging buffers
 // (allocated on first use); returns when the last chunk's copy has been enqueued and the source
@@ -222,9 +251,13 @@ extern "C" int32_t fllm_ctx_create(int32_t device, fllm_ctx** out) {
     int n = 0;
     HIP_TRY(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail(FLLM_E_ARG_RANGE, "device %d outside [0,%d)", device, n);
+    if (device >= kMaxDevices) return fail(FLLM_E_NOT_SUPPORTED, "device %d: at most %d devices", device, kMaxDevices);
     HIP_TRY(hipSetDevice(device));
     fllm_ctx* c = new fllm_ctx();
     c->device = device;
+    // only fllm_dequantize_noalloc needs the scratch address: a failure is kept for it to report
+    c->scratch_err = scratch_init(device, &c->scratch);
+    if (c->scratch_err != hipSuccess) (void)hipGetLastError();
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) { delete c; return fail(FLLM_E_DEVICE, "hipStreamCreate: %s", hipGetErrorString(e)); }
     hipDeviceProp_t prop;
@@ -297,6 +330,41 @@ extern "C" int32_t fllm_dequantize(fllm_ctx* ctx, int32_t type, const void* src,
     hipFree(dsrc);
     hipFree(ddst);
     if (e != hipSuccess) return fail(FLLM_E_DEVICE, "dequantize: %s", hipGetErrorString(e));
+    return FLLM_OK;
+}
+
+// fllm_dequantize without allocating: the source blocks and the floats go through this device's
+// scratch array (its address resolved at context creation), so nothing is allocated or freed.
+// Calls that overlap on one device (other threads or streams) share the array and race.
+extern "C" int32_t fllm_dequantize_noalloc(fllm_ctx* ctx, int32_t type, const void* src, uint64_t nbytes, float* dst,
+                                           int64_t n) {
+    NOT_NULL(ctx);
+    if (!type_supported(type)) return fail(FLLM_E_NOT_SUPPORTED, "Tensor type %d is not supported for dequantization.", type);
+    TypeInfo ti = type_info(type);
+    if (nbytes % (uint64_t)ti.block_bytes != 0)
+        return fail(FLLM_E_ARG, "Source length must be a multiple of %d for type %d.", ti.block_bytes, type);
+    int64_t elems = (int64_t)(nbytes / ti.block_bytes) * ti.block_elems;
+    if (n < elems) return fail(FLLM_E_ARG, "Destination must hold at least %lld floats.", (long long)elems);
+    if (nbytes > kNoallocSrcBytes || elems > (int64_t)kNoallocElems)
+        return fail(FLLM_E_ARG,
+                    "fllm_dequantize_noalloc takes at most %llu source bytes and %llu elements (got %llu bytes, %lld "
+                    "elements); use fllm_dequantize",
+                    (unsigned long long)kNoallocSrcBytes, (unsigned long long)kNoallocElems,
+                    (unsigned long long)nbytes, (long long)elems);
+    if (elems == 0) return FLLM_OK;
+    NOT_NULL(src);
+    NOT_NULL(dst);
+    if (!ctx->scratch)
+        return fail(FLLM_E_DEVICE, "hipGetSymbolAddress(scratch) failed at context creation: %s",
+                    hipGetErrorString(ctx->scratch_err));
+    HIP_TRY(hipSetDevice(ctx->device));
+    uint8_t* dsrc = ctx->scratch;
+    float* ddst = (float*)(ctx->scratch + kNoallocSrcRegion);
+    hipError_t e = hipMemcpyAsync(dsrc, src, nbytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = launch_dequant(type, dsrc, elems, ddst, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, ddst, sizeof(float) * (size_t)elems, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail(FLLM_E_DEVICE, "dequantize_noalloc: %s", hipGetErrorString(e));
     return FLLM_OK;
 }
 

@@ -280,6 +280,17 @@ FLLM_API int32_t fllm_kv_was_evicted(fllm_seq* s, int32_t* out);
  * dst too small -> FLLM_E_ARG. */
 FLLM_API int32_t fllm_dequantize(fllm_ctx* ctx, int32_t type, const void* src, uint64_t nbytes,
                                  float* dst, int64_t n);
+/* fllm_dequantize without any device allocation, for callers that cannot allocate (harnesses that
+ * forbid it, tight serving loops). No counterpart in the reference. The source blocks and the
+ * floats are staged through a fixed scratch array in device memory that the library holds per
+ * device for the life of the process (FLLM_NOALLOC_MAX_BYTES source bytes and FLLM_NOALLOC_MAX_ELEMS
+ * floats); larger calls return FLLM_E_ARG. Same results and error contract as fllm_dequantize
+ * otherwise. Every call on one device uses the same array: calls that overlap on one device (from
+ * several threads or contexts) race. */
+#define FLLM_NOALLOC_MAX_BYTES (2u << 20)
+#define FLLM_NOALLOC_MAX_ELEMS (2u << 20)
+FLLM_API int32_t fllm_dequantize_noalloc(fllm_ctx* ctx, int32_t type, const void* src, uint64_t nbytes,
+                                         float* dst, int64_t n);
 /* Dequantizer.ElementCount (Dequantizer.cs:466-479). */
 FLLM_API int32_t fllm_element_count(int32_t type, int64_t nbytes, int64_t* out);
 
