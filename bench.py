@@ -17,9 +17,15 @@ Roofline: the dominant kernel is the one with the largest share of a profiled de
 events around every launch). Its achieved bandwidth is its algorithmic bytes per launch (the weight
 blocks it streams plus its activation reads and writes) over its mean duration. When rocprofv3 is
 on PATH, the duration and the HBM traffic come from short child runs of this script under the
-profiler (kernel trace; FETCH_SIZE; WRITE_SIZE), the counters scaled by what they read for a device
-copy of known size in the same child; otherwise the duration is the HIP-event mean (which includes
-the launch) and the traffic is null.
+profiler at the timed run's context (the same prompt prefilled into a cache of the same capacity,
+then eager decode steps): kernel trace; FETCH_SIZE; WRITE_SIZE, each scaled by what it reads for a
+device copy of known size in the same child; and the read requests by size with the DRAM-side
+32-byte read and write units, which show where that scale comes from. Without the profiler the
+duration is the HIP-event mean (which includes the launch) and the traffic is null.
+
+The second half of the metric, the isolated GEMV sweep (Q4_K, Q8_0, Q6_K at 4096x4096, 14336x4096 and
+4096x14336, dotnetfoundryllm_amd.gemv_bench), goes into "gemv_sweep": algorithmic GB/s per launch
+over at least 1 GiB of distinct copies, and the counted traffic per launch of the tile layout.
 """
 import argparse
 import csv
@@ -83,15 +89,33 @@ def cpu_baseline(cfg_name, ctx_positions=384):
         m.close()
     t_head = max(t_mixed - t_layer, 0.0) * (desc.vocab / head_rows)
     t_token = full_layers * t_layer + t_head
+    # the reference prefills with one Forward per prompt token (LlamaLanguageModel.cs:133-137): its
+    # prefill rate is the per-token rate over the prompt's positions (the sample's positions 2..386
+    # average 194, the 511-token prompt's 255; attention is under 2% of a token at these lengths)
     return {
         "value": round(1.0 / t_token, 4),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
+        "prefill_tok_s": round(1.0 / t_token, 4),
+        "cpu_model": host_cpu_model(),
+        "nproc": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
         "sample": (f"oracle F32 forward (weights dequantized at load, reference operation order), one thread: "
                    f"1 decoder layer x {full_layers} ({t_layer * 1e3:.1f} ms) + {head_rows}/{desc.vocab} LM-head "
-                   f"rows scaled x16 ({t_head * 1e3:.1f} ms), {ctx_positions} positions each; load {load_s:.1f} s"),
+                   f"rows scaled x16 ({t_head * 1e3:.1f} ms), {ctx_positions} positions each; load {load_s:.1f} s. "
+                   f"Prefill = the same per-token Forward, as the reference prefills"),
     }
+
+
+def host_cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 COPY_BYTES = 256 << 20  # calibration copy of the traffic counters
@@ -112,23 +136,32 @@ def device_copy_calibration():
     hip.hipFree(b)
 
 
+def timed_capacity(args, cfg):
+    """KV capacity of the timed run (it sets the attention's chunking, so the profiled children use
+    it too)."""
+    return min(cfg["max_ctx"], args.prompt + args.warmup + args.steps + args.host_steps + args.profile_steps + 8)
+
+
 def child_profile(args):
-    """The workload profiled by the roofline child runs: a short prompt, a few eager decode steps with
-    per-launch events (so the launch names come out in order), then the calibration copy."""
+    """The workload profiled by the roofline child runs, at the timed run's context: the same
+    prompt through the batched prefill into a cache of the same capacity, the warmup's decode steps,
+    then eager decode steps with per-launch events (so the launch names come out in order) and the
+    calibration copy."""
     import dotnetfoundryllm_amd as F
     from dotnetfoundryllm_amd.configs import CONFIGS, build_model
 
     cfg = CONFIGS[args.config]
     ctx = F.Context(0)
     model, _ = build_model(ctx, cfg)
-    kv = F.HipKvCache(model, 64)
-    F.set_graph(kv, False)
+    kv = F.HipKvCache(model, timed_capacity(args, cfg))
     fwd = F.HipForwardPass(model)
-    nxt, pos = 11, 0
-    for _ in range(4):
-        fwd.forward(nxt, pos, kv)
-        nxt = fwd.sample_greedy()
-        pos += 1
+    prompt = F.synth_tokens(cfg["seed"], 0, cfg["vocab"], args.prompt)
+    fwd.prefill(prompt[:-1], 0, kv)
+    nxt, pos = int(prompt[-1]), args.prompt - 1
+    if args.warmup:
+        nxt = int(fwd.decode_greedy(nxt, pos, args.warmup, kv)[-1])
+        pos += args.warmup
+    F.set_graph(kv, False)
     F.set_profile(kv, True)
     for _ in range(args.profile_steps):
         fwd.forward(nxt, pos, kv)
@@ -143,19 +176,100 @@ def child_profile(args):
     ctx.close()
 
 
-def rocprof_child(args, mode, tmp):
-    """Runs this script's child workload under rocprofv3; returns the rows of its CSV output."""
-    out = os.path.join(tmp, mode)
+def child_gemv(args):
+    """The C1 matrices under the traffic counters: for each type and shape, GEMV_COPIES distinct
+    copies regrouped by fllm_gemv_pack, one fllm_gemv_ex launch on each (tile layout), then the
+    calibration copy."""
+    import numpy as np
+
+    import dotnetfoundryllm_amd as F
+    from dotnetfoundryllm_amd import gemv_bench as G
+    from dotnetfoundryllm_amd._native import type_bytes
+
+    ctx = F.Context(0)
+    rng = np.random.default_rng(7)
+    for t, tname in G.TYPES:
+        p0, p1 = G.weight_range(t)
+        for rows, cols in G.SHAPES:
+            x = rng.standard_normal(cols).astype(np.float32)
+            xb, yb = F.DeviceBuffer(ctx, x.nbytes), F.DeviceBuffer(ctx, rows * 4)
+            xb.write(x)
+            tiles = []
+            for c in range(GEMV_COPIES):
+                raw = F.synth_tensor(t, 0x5EED01, 1000 * rows + c, rows * cols, 0, p0, p1)
+                b = F.DeviceBuffer(ctx, raw.nbytes)
+                b.write(raw)
+                tb = F.DeviceBuffer(ctx, raw.nbytes)
+                F.gemv_pack(ctx, t, b, rows, cols, tb)
+                b.close()
+                tiles.append(tb)
+            for tb in tiles:
+                F.gemv(ctx, t, tb, rows, cols, xb, yb, layout=F.LAYOUT_TILES)
+            ctx.sync()
+            for b in tiles + [xb, yb]:
+                b.close()
+    device_copy_calibration()
+    ctx.close()
+
+
+GEMV_COPIES = 3
+
+
+def gemv_report(args):
+    """BASELINE's second metric: the C1 GEMV sweep (Q4_K, Q8_0, Q6_K at 4096x4096, 14336x4096,
+    4096x14336; dotnetfoundryllm_amd.gemv_bench) as algorithmic GB/s and fraction of 8 TB/s, with each
+    tile-layout launch's HBM traffic from FETCH_SIZE + WRITE_SIZE (calibrated like the roofline's) when
+    rocprofv3 is present."""
+    from dotnetfoundryllm_amd import gemv_bench as G
+    rows = G.run(iters=100, out=log)
+    sweep = [{"type": tn, "rows": r, "cols": c, "layout": lay, "bytes": nb, "us_per_launch": round(us, 2),
+              "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)} for tn, r, c, lay, nb, n, us, gbs in rows]
+    if args.no_rocprof or not shutil.which("rocprofv3"):
+        return sweep
+    tmp = tempfile.mkdtemp(prefix="fllm_gemv_")
+    try:
+        traffic = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            order = pmc_dispatches(rocprof_child(args, counter, tmp, child="--child-gemv"), counter)
+            factor = copy_factor(order)
+            gemv = [v for n, v in order if "k_gemv" in n]
+            cases = [(tn, r, c) for _, tn in G.TYPES for r, c in G.SHAPES]
+            if len(gemv) != len(cases) * GEMV_COPIES:
+                raise RuntimeError(f"{counter}: {len(gemv)} GEMV dispatches, expected {len(cases) * GEMV_COPIES}")
+            for i, case in enumerate(cases):
+                vals = gemv[i * GEMV_COPIES:(i + 1) * GEMV_COPIES]
+                traffic[case] = traffic.get(case, 0.0) + sum(vals) / len(vals) * 1024.0 * factor
+        for e in sweep:
+            tr = traffic.get((e["type"], e["rows"], e["cols"]))
+            if e["layout"] == "tiles" and tr is not None:
+                e["traffic"] = int(tr)
+                e["traffic_ratio"] = round(tr / e["bytes"], 3)
+    except Exception as e:
+        log(f"gemv sweep: traffic counters failed ({e})")
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return sweep
+
+
+def child_args(args):
+    return ["--config", args.config, "--profile-steps", str(args.profile_steps), "--prompt", str(args.prompt),
+            "--warmup", str(args.warmup), "--steps", str(args.steps), "--host-steps", str(args.host_steps)]
+
+
+def rocprof_child(args, mode, tmp, child="--child-profile"):
+    """Runs a child workload of this script under rocprofv3 (mode "trace": kernel trace; otherwise
+    the space-separated counters of one --pmc pass); returns the rows of its CSV output."""
+    out = os.path.join(tmp, mode.replace(" ", "+"))
     cmd = ["rocprofv3"]
     if mode == "trace":
         cmd += ["--kernel-trace"]
     else:
-        cmd += ["--pmc", mode]
+        cmd += ["--pmc", *mode.split()]
     cmd += ["--output-format", "csv", "-d", out, "-o", "run", "--",
-            sys.executable, os.path.abspath(__file__), "--child-profile", "--config", args.config,
-            "--profile-steps", str(args.profile_steps)]
+            sys.executable, os.path.abspath(__file__), child, *child_args(args)]
     env = dict(os.environ, TMPDIR=tmp)
-    r = subprocess.run(cmd, cwd=tmp, env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+    log(f"  rocprofv3 {'--kernel-trace' if mode == 'trace' else '--pmc ' + mode} ({child})")
+    r = subprocess.run(cmd, cwd=tmp, env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=150)
     files = glob.glob(os.path.join(out, "**", "*kernel_trace.csv" if mode == "trace" else "*counter_collection.csv"),
                       recursive=True)
     if not files:
@@ -167,18 +281,57 @@ def kernel_key(row):
     return (row["Kernel_Name"].split("(")[0], row.get("Grid_Size", row.get("Grid_Size_X", "")))
 
 
+def pmc_dispatches(rows, counter):
+    """[(kernel name, value)] of one counter per dispatch, in dispatch (= launch) order."""
+    per = {}
+    for r in rows:
+        if r["Counter_Name"] != counter:
+            continue
+        d = int(r["Dispatch_Id"])
+        name = r["Kernel_Name"]
+        per[d] = (name, per.get(d, (name, 0.0))[1] + float(r["Counter_Value"]))
+    return [per[d] for d in sorted(per)]
+
+
+def copy_factor(order):
+    """Bytes per counted KiB from the calibration copy, which reads and writes COPY_BYTES."""
+    copy = [v for n, v in order if "copyBuffer" in n]
+    if not copy:
+        raise RuntimeError("missing calibration copy dispatch")
+    return COPY_BYTES / (max(copy) * 1024.0)
+
+
+# Read requests by size (TCC_EA0_RDREQ_{32B,64B,128B}) and the DRAM-side 32-byte read / write units: the
+# per-size picture behind FETCH_SIZE, whose gfx950 formula counts a request as 128 bytes only when
+# TCC_BUBBLE counts it (at most 4 TCC counters per pass)
+SIZE_PASSES = (("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum"),
+               ("TCC_BUBBLE_sum", "TCC_EA0_RDREQ_DRAM_32B_sum", "TCC_EA0_WRREQ_WRITE_DRAM_32B_sum"))
+
+
 def profiler_roofline(args, bytes_per_launch, dom_name, steps_launches):
     """Mean duration and HBM traffic of the dominant launch from rocprofv3 child runs. The dominant
     launch is identified by position: the profiled steps' launches in order are the HIP-event
     names, so the kernel (and grid) at the positions named dom_name is the dominant one."""
     tmp = tempfile.mkdtemp(prefix="fllm_roofline_")
+    n_prof = len(steps_launches)
+
+    def dominant(order, what):
+        # the dominant launch by position among the profiled launches, as for the durations (one
+        # kernel can serve several launches of a step with the same grid: e.g. o and gate/up)
+        fl = [(n, v) for n, v in order if "fllm::" in n and "k_set_params" not in n]
+        if len(fl) < n_prof:
+            raise RuntimeError(f"{what}: fewer dispatches than the profiled launches")
+        dom = [v for (n, v), nm in zip(fl[-n_prof:], steps_launches) if nm == dom_name]
+        if not dom:
+            raise RuntimeError(f"{what}: no dominant-kernel dispatches")
+        return sum(dom) / len(dom)
+
     try:
         trace = rocprof_child(args, "trace", tmp)
         trace.sort(key=lambda r: int(r["Start_Timestamp"]))
         # the profiled launches (one kernel each, names in order) are the child's last fllm kernels
         # (the step-parameter write at the start of each forward is not a profiled launch)
         mine = [r for r in trace if "fllm::" in r["Kernel_Name"] and "k_set_params" not in r["Kernel_Name"]]
-        n_prof = len(steps_launches)
         if n_prof == 0 or len(mine) < n_prof:
             raise RuntimeError("kernel trace shorter than the profiled launches")
         prof = mine[-n_prof:]
@@ -189,31 +342,24 @@ def profiler_roofline(args, bytes_per_launch, dom_name, steps_launches):
                "kernel_symbol": sorted(k[0] for k in keys)[0] if keys else None}
         traffic = 0.0
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            rows = rocprof_child(args, counter, tmp)
-            per = {}
-            for r in rows:
-                if r["Counter_Name"] != counter:
-                    continue
-                d = int(r["Dispatch_Id"])
-                name = r["Kernel_Name"]
-                per[d] = (name, per.get(d, (name, 0.0))[1] + float(r["Counter_Value"]))
-            order = [per[d] for d in sorted(per)]  # dispatch order = launch order
-            copy = [v for n, v in order if "copyBuffer" in n]
-            # the dominant launch by position among the profiled launches, as for the durations (one
-            # kernel can serve several launches of a step with the same grid: e.g. o and gate/up)
-            fl = [(n, v) for n, v in order if "fllm::" in n and "k_set_params" not in n]
-            if len(fl) < n_prof:
-                raise RuntimeError(f"{counter}: fewer dispatches than the profiled launches")
-            dom = [v for (n, v), nm in zip(fl[-n_prof:], steps_launches) if nm == dom_name]
-            if not copy or not dom:
-                raise RuntimeError(f"{counter}: missing copy or dominant-kernel dispatches")
-            # the copy reads and writes COPY_BYTES: counts per byte of that copy
-            factor = COPY_BYTES / (max(copy) * 1024.0)
-            kib = sum(dom) / len(dom)
+            order = pmc_dispatches(rocprof_child(args, counter, tmp), counter)
+            factor = copy_factor(order)
+            kib = dominant(order, counter)
             res[counter.lower() + "_kib_raw"] = round(kib, 1)
             res[counter.lower() + "_copy_factor"] = round(factor, 4)
             traffic += kib * 1024.0 * factor
         res["traffic"] = int(traffic)
+        try:
+            sizes = {}
+            for group in SIZE_PASSES:
+                rows = rocprof_child(args, " ".join(group), tmp)
+                for counter in group:
+                    sizes[counter] = round(dominant(pmc_dispatches(rows, counter), counter), 1)
+            res["read_requests_per_launch"] = sizes
+            res["dram_traffic_from_32b_units"] = int(32 * (sizes["TCC_EA0_RDREQ_DRAM_32B_sum"] +
+                                                          sizes["TCC_EA0_WRREQ_WRITE_DRAM_32B_sum"]))
+        except Exception as e:  # the cross-check is optional
+            log(f"roofline: request-size counters failed ({e})")
         return res
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
@@ -324,9 +470,14 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-rocprof", action="store_true", help="roofline from HIP events only (no profiler child runs)")
     ap.add_argument("--child-profile", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--child-gemv", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--no-gemv-sweep", action="store_true", help="skip the isolated GEMV sweep")
     args = ap.parse_args()
     if args.child_profile:
         child_profile(args)
+        return
+    if args.child_gemv:
+        child_gemv(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -348,7 +499,7 @@ def main():
     log(f"weights generated and uploaded in {time.time() - t:.1f} s")
     load_report = upload_report(F, ctx, load)
     log(f"upload: {load_report}")
-    max_seq = min(cfg["max_ctx"], args.prompt + args.warmup + args.steps + args.host_steps + args.profile_steps + 8)
+    max_seq = timed_capacity(args, cfg)
     kv = F.HipKvCache(model, max_seq)
     if args.no_graph:
         F.set_graph(kv, False)
@@ -441,9 +592,9 @@ def main():
         log("roofline: rocprofv3 child runs (kernel trace, FETCH_SIZE, WRITE_SIZE) ...")
         try:
             names = json.loads(subprocess.run([sys.executable, os.path.abspath(__file__), "--child-profile",
-                                               "--config", args.config, "--profile-steps", str(args.profile_steps)],
+                                               *child_args(args)],
                                               stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True,
-                                              timeout=300).stdout.strip().splitlines()[-1])["launch_names"]
+                                              timeout=240).stdout.strip().splitlines()[-1])["launch_names"]
             roofline.update(profiler_roofline(args, bytes_launch, dom["name"], names))
             roofline["event_avg_launch_us"] = round(avg_ms * 1e3, 2)
         except Exception as e:  # the profiler is optional: keep the event timing
@@ -451,6 +602,11 @@ def main():
     achieved = bytes_launch / (roofline["avg_launch_us"] * 1e-6) / 1e9
     roofline["achieved"] = round(achieved, 1)
     roofline["frac"] = round(achieved / HBM_PEAK_GBS, 4)
+
+    sweep = None
+    if not args.no_gemv_sweep:
+        log("isolated GEMV sweep (Q4_K, Q8_0, Q6_K) ...")
+        sweep = gemv_report(args)
 
     sampling = sampling_report(F, fwd, kv, cfg, args.seed)
     log(f"sampling per call (us): {sampling}")
@@ -490,6 +646,7 @@ def main():
         "profiled_step_ms": round(total_ms, 4),
         "sampling_us_per_call": sampling,
         "weight_upload": load_report,
+        "gemv_sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

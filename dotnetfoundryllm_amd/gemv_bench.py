@@ -26,13 +26,19 @@ TYPES = [(Q4_K, "Q4_K"), (Q8_0, "Q8_0"), (Q6_K, "Q6_K")]
 HBM_PEAK_GBS = 8000.0
 
 
-def run(iters=200, copies_bytes=1 << 30, seed=0x5EED01):
+def weight_range(t):
+    """Range of the blocks' f16 scales: Q8_0 d in [1e-3, 1e-2], K-quant d / dmin in [1e-3, 4e-3]."""
+    return Q8_RANGE if t == Q8_0 else KQ_RANGE
+
+
+def run(iters=200, copies_bytes=1 << 30, seed=0x5EED01, out=print):
+    """[(type name, rows, cols, layout name, bytes, copies, us per launch, GB/s)]; progress to out."""
     ctx = Context(0)
     rng = np.random.default_rng(seed)
     rows_out = []
     try:
         for t, tname in TYPES:
-            p0, p1 = Q8_RANGE if t == Q8_0 else KQ_RANGE
+            p0, p1 = weight_range(t)
             for rows, cols in SHAPES:
                 nb = type_bytes(t, rows * cols)
                 n_copies = max(2, -(-copies_bytes // nb))
@@ -54,8 +60,8 @@ def run(iters=200, copies_bytes=1 << 30, seed=0x5EED01):
                         us = gemv_time(ctx, t, ws, rows, cols, xb, yb, iters, layout)
                         gbs = nb / (us * 1e-6) / 1e9
                         rows_out.append((tname, rows, cols, name, nb, n_copies, us, gbs))
-                        print(f"{tname} {rows}x{cols} {name}: {nb / 1e6:.2f} MB x {n_copies} copies, {us:.2f} us, "
-                              f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)", flush=True)
+                        out(f"{tname} {rows}x{cols} {name}: {nb / 1e6:.2f} MB x {n_copies} copies, {us:.2f} us, "
+                            f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
                 finally:
                     for b in bufs + tiles + [xb, yb]:
                         b.close()
