@@ -440,6 +440,41 @@ def upload_report(F, ctx, load, probe_bytes=1 << 30):
             "direct_pageable_copy_GB_s": round(direct, 2), "finalize_s": round(load["finalize_s"], 3)}
 
 
+def gguf_load_report(F, ctx, cfg, model):
+    """GgufModelLoader's path at full size: the model's seeded tensors written as a GGUF file, its
+    page cache dropped, then fllmh_load_gguf (mapped file, large tensors through the pinned staging
+    pair, finalize) timed cold (disk reads and page faults included) and again warm (page faults of a
+    cached file); 8 greedy tokens from the loaded model against the in-memory one."""
+    from dotnetfoundryllm_amd.gguf import drop_page_cache, write_synthetic_gguf
+    path = os.path.join(tempfile.gettempdir(), f"fllm_bench_{os.getpid()}.gguf")
+    try:
+        t = time.perf_counter()
+        write_synthetic_gguf(path, cfg)
+        write_s = time.perf_counter() - t
+        size = os.path.getsize(path)
+        drop_page_cache(path)
+        out = {"file_bytes": size, "write_s": round(write_s, 2)}
+        prompt = F.synth_tokens(cfg["seed"], 9, cfg["vocab"], 16)
+        ref_kv = F.HipKvCache(model, 64)
+        ref = list(F.HipForwardPass(model).decode_greedy(int(prompt[0]), 0, 8, ref_kv))
+        ref_kv.close()
+        for mode in ("cold", "warm"):
+            t = time.perf_counter()
+            m, _ = F.GgufModelLoader.load(ctx, path)
+            s_ = time.perf_counter() - t
+            out[f"{mode}_s"] = round(s_, 3)
+            out[f"{mode}_GB_s"] = round(size / s_ / 1e9, 2)
+            kv = F.HipKvCache(m, 64)
+            toks = list(F.HipForwardPass(m).decode_greedy(int(prompt[0]), 0, 8, kv))
+            kv.close()
+            m.close()
+            out[f"{mode}_greedy_tokens_match"] = toks == ref
+        return out
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+
+
 def weights_text(cfg):
     """'Q4_K (q,k,o,gate,up) + Q6_K (v,down,output), seeded random blocks' from the config's types."""
     from dotnetfoundryllm_amd._native import TYPE_NAMES
@@ -472,6 +507,7 @@ def main():
     ap.add_argument("--child-profile", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--child-gemv", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-gemv-sweep", action="store_true", help="skip the isolated GEMV sweep")
+    ap.add_argument("--no-gguf-load", action="store_true", help="skip the GGUF file-to-device measurement")
     args = ap.parse_args()
     if args.child_profile:
         child_profile(args)
@@ -609,6 +645,15 @@ def main():
         sweep = gemv_report(args)
 
     sampling = sampling_report(F, fwd, kv, cfg, args.seed)
+
+    gguf_load = None
+    if not args.no_gguf_load:
+        log("GGUF file load (write, drop the page cache, fllmh_load_gguf cold and warm) ...")
+        try:
+            gguf_load = gguf_load_report(F, ctx, cfg, model)
+            log(f"GGUF load: {gguf_load}")
+        except Exception as e:
+            log(f"GGUF load failed: {e}")
     log(f"sampling per call (us): {sampling}")
 
     cpu = None
@@ -647,6 +692,7 @@ def main():
         "sampling_us_per_call": sampling,
         "weight_upload": load_report,
         "gemv_sweep": sweep,
+        "gguf_file_load": gguf_load,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

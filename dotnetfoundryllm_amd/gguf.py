@@ -6,6 +6,7 @@ Layout: magic "GGUF", u32 version, u64 tensor count, u64 metadata count, metadat
 first), u32 type, u64 offset relative to the data start), padding to `general.alignment`
 (32), tensor data. Strings are u64 length + UTF-8 bytes.
 """
+import os
 import struct
 
 import numpy as np
@@ -42,8 +43,14 @@ class GgufWriter:
     def add_array(self, key, etype, values):
         self.meta.append((key, ARR, (etype, list(values))))
 
-    def add_tensor(self, name, dims, ttype, data):
-        self.tensors.append((name, list(dims), ttype, np.ascontiguousarray(data).view(np.uint8).reshape(-1)))
+    def add_tensor(self, name, dims, ttype, data, nbytes=None):
+        """data: the tensor's bytes, or a callable returning them (then nbytes is required), so that
+        a large file is written one tensor at a time."""
+        if callable(data):
+            self.tensors.append((name, list(dims), ttype, int(nbytes), data))
+        else:
+            a = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+            self.tensors.append((name, list(dims), ttype, a.nbytes, lambda a=a: a))
 
     def write(self):
         out = bytearray()
@@ -58,11 +65,11 @@ class GgufWriter:
             else:
                 out += _val(vtype, value)
         offsets, off = [], 0
-        for name, dims, ttype, data in self.tensors:
+        for name, dims, ttype, nbytes, data in self.tensors:
             off = (off + self.alignment - 1) // self.alignment * self.alignment
             offsets.append(off)
-            off += data.nbytes
-        for (name, dims, ttype, data), o in zip(self.tensors, offsets):
+            off += nbytes
+        for (name, dims, ttype, nbytes, data), o in zip(self.tensors, offsets):
             out += _s(name) + struct.pack("<I", len(dims))
             for d in dims:
                 out += struct.pack("<Q", d)
@@ -72,11 +79,15 @@ class GgufWriter:
         with open(self.path, "wb") as f:
             f.write(out)
             pos = 0
-            for (name, dims, ttype, data), o in zip(self.tensors, offsets):
+            for (name, dims, ttype, nbytes, data), o in zip(self.tensors, offsets):
                 if o > pos:
                     f.write(b"\0" * (o - pos))
-                f.write(data.tobytes())
-                pos = o + data.nbytes
+                a = np.ascontiguousarray(data()).view(np.uint8).reshape(-1)
+                if a.nbytes != nbytes:
+                    raise ValueError(f"{name}: {a.nbytes} bytes, declared {nbytes}")
+                f.write(a.data)
+                pos = o + nbytes
+                del a
 
 
 def write_synthetic_gguf(path, cfg, n_vocab_tokens=None):
@@ -111,8 +122,20 @@ def write_synthetic_gguf(path, cfg, n_vocab_tokens=None):
     w.add("tokenizer.ggml.eos_token_id", U32, 2)
     for entry in tensor_plan(cfg):
         name, slot, layer, tt, rows, cols, dist, tid = entry
-        data = synth_bytes(cfg, entry)
+        n = rows * cols
+        nbytes = n * {N.F32: 4, N.F16: 2, N.BF16: 2}[tt] if tt in (N.F32, N.F16, N.BF16) else N.type_bytes(tt, n)
         dims = [cols] if rows == 1 else [cols, rows]
-        w.add_tensor(name, dims, tt, data)
+        w.add_tensor(name, dims, tt, lambda e=entry: synth_bytes(cfg, e), nbytes)
     w.write()
     return path
+
+
+def drop_page_cache(path):
+    """Writes the file's dirty pages out and asks the kernel to drop its cached pages, so the next
+    read of it comes from the disk (posix_fadvise DONTNEED on a file this process may read)."""
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        os.fsync(fd)
+        os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+    finally:
+        os.close(fd)

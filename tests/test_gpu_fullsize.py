@@ -126,3 +126,57 @@ def test_gemma2_long_context_window(ctx):
     finally:
         kv.close()
         m.close()
+
+
+def test_gguf_full_width_file_matches_oracle(ctx, tmp_path):
+    """GgufReader / GgufModelLoader at full width (GgufReader.cs:113-185, GgufFile.cs:76-97,
+    GgufModelLoader.cs:336-432): the Llama-3-8B shape at two layers written as a 2.8 GB GGUF file
+    (the reference maps files of 256 MB and more), its page cache dropped, loaded with
+    fllmh_load_gguf (mapped file, tensors of 32 MiB and more through the pinned staging pair),
+    then the logits of a 12-token prompt and 8 greedy tokens against the oracle fed the same
+    tensors. Prints the file-to-device rate with page faults and disk reads included."""
+    import time
+
+    from dotnetfoundryllm_amd.gguf import drop_page_cache, write_synthetic_gguf
+    cfg = dict(CONFIGS["llama3-8b-q4km"])
+    cfg["n_layers"] = 2
+    path = str(tmp_path / "llama3-8b-2l.gguf")
+    write_synthetic_gguf(path, cfg)
+    size = os.path.getsize(path)
+    assert size >= 256 << 20
+    drop_page_cache(path)
+    t = time.perf_counter()
+    m, info = F.GgufModelLoader.load(ctx, path)
+    cold = time.perf_counter() - t
+    say(f"GGUF file {size / 1e9:.2f} GB loaded from disk in {cold:.2f} s: {size / cold / 1e9:.2f} GB/s")
+    assert info.desc.n_layers == 2 and info.desc.vocab == cfg["vocab"] and info.desc.head_dim == 128
+    _, desc, tensors = synthetic("llama3-8b-q4km", n_layers=2)
+    O.lib.orc_set_threads(16)
+    orc = O.OracleModel(desc, tensors, 64)
+    del tensors
+    kv = F.HipKvCache(m, 64)
+    fwd = F.HipForwardPass(m)
+    try:
+        prompt = F.synth_tokens(cfg["seed"], 7, desc.vocab, 12)
+        worst = 0.0
+        for p, tok in enumerate(prompt):
+            fwd.forward(int(tok), p, kv)
+            assert orc.forward(int(tok), p) == 0
+            worst = max(worst, O.normwise_rel_err(fwd.logits, orc.logits()))
+        nxt_d = nxt_o = int(prompt[-1])
+        for step in range(8):
+            pos = prompt.size + step
+            fwd.forward(nxt_d, pos, kv)
+            assert orc.forward(nxt_o, pos) == 0
+            lg = orc.logits()
+            worst = max(worst, O.normwise_rel_err(fwd.logits, lg))
+            nxt_d, nxt_o = fwd.sample_greedy(), int(np.argmax(lg))
+            assert nxt_d == nxt_o, f"greedy token at step {step}"
+        say(f"logits worst normwise error {worst:.2e}")
+        assert worst <= TOL
+    finally:
+        O.lib.orc_set_threads(1)
+        orc.close()
+        kv.close()
+        m.close()
+        os.remove(path)
