@@ -366,22 +366,59 @@ def profiler_roofline(args, bytes_per_launch, dom_name, steps_launches):
 
 
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
+Q4_K_TYPE = 12
 
 
-def prefill_report(cfg, n, seconds):
-    """Arithmetic rate of the batched prefill (f32 matrix-core GEMMs): the projections' 2 flop per
-    weight per token plus the causal attention's 4 * heads * head_dim flop per (query, key) pair, over
-    the wall time of the whole prefill call (norms, element-wise steps and the last token's LM head
-    included, so the fraction is a lower bound for the GEMMs)."""
+def prefill_report(cfg, n, seconds, stages=None):
+    """Arithmetic rate of the batched prefill over the wall time of the whole prefill call (norms,
+    element-wise steps and the last token's LM head included, so every fraction is a lower bound).
+    `tflops`: the reference's own arithmetic, 2 flop per weight per token plus the causal attention's
+    4 * heads * head_dim flop per (query, key) pair. The projections run on the fp16 matrix cores:
+    a launch of Q4_K matrices only takes two fp16 products per weight (exact integer weights against
+    the activations' hi and lo halves) plus one min-term product per 256-element block (1/8 of a
+    product), any other launch three (hi/lo splits of both operands); `gemm` is those fp16 products'
+    rate against the fp16 peak. Attention runs on the f32 matrix cores, one product per flop."""
     H, L, F = cfg["hidden"], cfg["n_layers"], cfg["ffn"]
     hd = cfg["head_dim"]
     qdim, kvdim = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
+    ty = cfg["types"]
     weights = L * (qdim * H + 2 * kvdim * H + H * qdim + 3 * F * H)
     pairs = n * (n + 1) // 2
-    flops = 2.0 * n * weights + 4.0 * cfg["n_heads"] * hd * pairs * L
+    attn = 4.0 * cfg["n_heads"] * hd * pairs * L
+    flops = 2.0 * n * weights + attn
+    launches = [((qdim * H, ty["q"]), (kvdim * H, ty["k"]), (kvdim * H, ty["v"])), ((H * qdim, ty["o"]),),
+                ((F * H, ty["gate"]), (F * H, ty["up"])), ((H * F, ty["down"]),)]
+    fp16 = 0.0
+    for g in launches:
+        products = 2.125 if all(t == Q4_K_TYPE for _, t in g) else 3.0
+        fp16 += products * sum(w for w, _ in g)
+    fp16_tf = 2.0 * n * L * fp16 / seconds / 1e12
+    attn_tf = attn / seconds / 1e12
     tf = flops / seconds / 1e12
-    return {"tokens": n, "tok_s": round(n / seconds, 2), "tflops": round(tf, 2), "dtype": "f32",
-            "mfma_peak_tflops": FP32_MFMA_PEAK_TFLOPS, "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+    out = {"tokens": n, "tok_s": round(n / seconds, 2), "tflops": round(tf, 2),
+           "gemm": {"dtype": "fp16", "mfma_tflops": round(fp16_tf, 2), "mfma_peak_tflops": FP16_MFMA_PEAK_TFLOPS,
+                    "mfma_frac": round(fp16_tf / FP16_MFMA_PEAK_TFLOPS, 4)},
+           "attention": {"dtype": "f32", "mfma_tflops": round(attn_tf, 2), "mfma_peak_tflops": FP32_MFMA_PEAK_TFLOPS,
+                         "mfma_frac": round(attn_tf / FP32_MFMA_PEAK_TFLOPS, 4)}}
+    if stages:
+        # each stage's own device time (events around its launches in a second, profiled prefill)
+        gemm_of = {"pf_qkv": launches[0], "pf_o": launches[1], "pf_gate_up": launches[2], "pf_down": launches[3]}
+        table = {}
+        for name, st in sorted(stages.items(), key=lambda kv: -kv[1]["ms"]):
+            row = {"launches": st["launches"], "ms": round(st["ms"], 3)}
+            if name in gemm_of:
+                g = gemm_of[name]
+                products = 2.125 if all(t == Q4_K_TYPE for _, t in g) else 3.0
+                mf = 2.0 * n * L * products * sum(w for w, _ in g) / (st["ms"] * 1e-3) / 1e12
+                row.update(dtype="fp16", products=products, mfma_tflops=round(mf, 1),
+                           mfma_frac=round(mf / FP16_MFMA_PEAK_TFLOPS, 4))
+            elif name == "pf_attention":
+                mf = attn / (st["ms"] * 1e-3) / 1e12
+                row.update(dtype="f32", mfma_tflops=round(mf, 1), mfma_frac=round(mf / FP32_MFMA_PEAK_TFLOPS, 4))
+            table[name] = row
+        out["stages"] = table
+    return out
 
 
 def sampling_report(F, fwd, kv, cfg, seed, reps=50):
@@ -554,6 +591,14 @@ def main():
     prefill_s = time.perf_counter() - t
     pos = args.prompt - 1
     log(f"prefill {args.prompt - 1} tokens in {prefill_s:.2f} s")
+    # the same prefill once more with each stage's launches timed by events; the cache ends as the
+    # timed prefill left it
+    kv.clear()
+    F.set_profile(kv, True)
+    fwd.prefill(prompt[:-1], 0, kv)
+    F.set_profile(kv, False)
+    prefill_stages = {e["name"]: e for e in F.profile_entries(kv)}
+    F.profile_reset(kv)
 
     nxt = int(prompt[-1])
     sampled = args.temperature > 0.0
@@ -686,7 +731,7 @@ def main():
         "roofline": roofline,
         "decode_step_hbm_frac": round(tok_s * tok_bytes / (HBM_PEAK_GBS * 1e9), 4),
         "prefill_tok_s": round((args.prompt - 1) / prefill_s, 2),
-        "prefill": prefill_report(cfg, args.prompt - 1, prefill_s),
+        "prefill": prefill_report(cfg, args.prompt - 1, prefill_s, prefill_stages),
         "host_loop_tok_s": round(host_tok_s, 2) if host_tok_s else None,
         "profiled_step_ms": round(total_ms, 4),
         "sampling_us_per_call": sampling,

@@ -150,6 +150,7 @@ struct Tensor {
     int type = -1;
     int64_t rows = 0, cols = 0;
     uint64_t bytes = 0;
+    int wexp = 0;  // batched prefill: 2^-wexp brings the largest |w| into [2^14, 2^15) (pf_wexp)
     bool present() const { return ptr != nullptr; }
     WMat mat() const { return WMat{ptr, type, rows, cols}; }
 };
@@ -239,6 +240,8 @@ struct fllm_seq {
     float *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_gu = nullptr, *pf_tmp = nullptr;
     float* pf_part = nullptr;  // K-split partial products of the short GEMM launches
     size_t pf_part_cap = 0;
+    _Float16* pf_xh = nullptr;  // fp16 hi / lo planes of the current GEMM input
+    float* pf_xs = nullptr;     // their per-row scales
     int* pf_tok = nullptr;
 };
 
@@ -796,6 +799,27 @@ extern "C" int32_t fllm_model_finalize(fllm_model* m) {
     const Tensor* head[1] = {&m->output};
     if (!m->output_tied && tiles_launch_ok(head, 1, 0)) to_pack.push_back(&m->output);
     HIP_TRY(hipSetDevice(m->ctx->device));
+    {
+        // the largest |w| of every projection matrix, for the batched prefill's fp16 split (read in
+        // GGUF row layout, before the regrouping)
+        std::vector<Tensor*> mats;
+        for (Layer& L : m->layers) {
+            Tensor* ts[7] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+            for (Tensor* t : ts) mats.push_back(t);
+        }
+        unsigned* dmax = nullptr;
+        hipError_t e = hipMalloc(&dmax, sizeof(unsigned) * mats.size());
+        if (e == hipSuccess) e = hipMemsetAsync(dmax, 0, sizeof(unsigned) * mats.size(), m->ctx->stream);
+        for (size_t i = 0; i < mats.size() && e == hipSuccess; i++)
+            e = launch_pf_wmax(mats[i]->type, mats[i]->ptr, mats[i]->rows * mats[i]->cols, dmax + i, m->ctx->stream);
+        std::vector<unsigned> hmax(mats.size(), 0u);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(hmax.data(), dmax, sizeof(unsigned) * mats.size(), hipMemcpyDeviceToHost, m->ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
+        if (dmax) hipFree(dmax);
+        if (e != hipSuccess) return fail(FLLM_E_DEVICE, "weight range: %s", hipGetErrorString(e));
+        for (size_t i = 0; i < mats.size(); i++) mats[i]->wexp = pf_wexp(hmax[i]);
+    }
     for (Tensor* t : to_pack) {
         hipError_t e = pack_tiles(m, *t);
         if (e != hipSuccess) return fail(FLLM_E_DEVICE, "weight regrouping: %s", hipGetErrorString(e));
@@ -1572,6 +1596,10 @@ static hipError_t prefill_alloc(fllm_seq* s) {
     PF_ALLOC(s->pf_tok, C);
     const size_t part_cap = 3 * C * std::max(H, (size_t)(m.qdim + 2 * m.kvdim));
     PF_ALLOC(s->pf_part, part_cap);
+    // widest GEMM input: hidden (q/k/v, gate/up), q_dim (output projection) or ffn (down)
+    const size_t kmax = ((size_t)std::max(std::max(m.d.hidden, m.d.ffn), m.qdim) + 7) / 8 * 8;
+    PF_ALLOC(s->pf_xh, 2 * C * kmax + 2 * C * (kmax / 32 + 1));  // value planes, then group-sum planes
+    PF_ALLOC(s->pf_xs, C);
 #undef PF_ALLOC
     if (e == hipSuccess) {
         s->pf_cap = cap;
@@ -1593,9 +1621,15 @@ static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w,
     g.add = add ? 1 : 0;
     g.part = s->pf_part;
     g.part_cap = s->pf_part_cap;
+    // the input's fp16 hi / lo planes, once for all the launch's matrices
+    g.ldh = (g.K + 7) / 8 * 8;
+    g.xh = s->pf_xh;
+    g.xs = s->pf_xs;
+    STEP("pf_split", 4.0 * T * g.K + 4.0 * T * g.ldh, launch_pf_split(g.x, g.ldx, T, g.K, s->pf_xh, g.ldh, s->pf_xs, s->st));
     double bytes = 0.0;
     for (int i = 0; i < n; i++) {
-        // one launch per run of tile-interleaved matrices, or of GGUF-row matrices of one type
+        // one launch per run of tile-interleaved matrices, or of GGUF-row matrices of one type (a run
+        // of tile Q4_K matrices only takes their own fp16 form; a mixed run, the general one)
         const bool split = g.nseg > 0 && ((w[i]->layout == LAYOUT_TILES) != (g.seg[0].layout == LAYOUT_TILES) ||
                                           (w[i]->layout != LAYOUT_TILES && w[i]->type != g.seg[0].type));
         if (split) {
@@ -1605,7 +1639,7 @@ static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w,
         }
         PfSeg& sg = g.seg[g.nseg++];
         sg.w = w[i]->ptr; sg.type = w[i]->type; sg.layout = w[i]->layout; sg.N = (int)w[i]->rows;
-        sg.y = y[i]; sg.ldy = ldy;
+        sg.y = y[i]; sg.ldy = ldy; sg.wexp = w[i]->wexp;
         bytes += (double)w[i]->bytes + 8.0 * T * (double)(w[i]->rows + w[i]->cols);
     }
     STEP(name, bytes, launch_pf_gemm(g, s->m->ctx->n_cu, s->st));

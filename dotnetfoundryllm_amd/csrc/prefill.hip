@@ -6,14 +6,25 @@
 // once), and the element-wise steps of the layer run over all rows.
 //
 // GEMM numerics. Weights are dequantized exactly (the Dequantizer arithmetic, as the device
-// dequant kernels do) while they are staged into LDS, and multiplied with the f32 activations on the
-// matrix cores in f32 (v_mfma_f32_16x16x4f32): the products of the reference's F32 path, summed in
-// f32 in the matrix core's order.
+// dequant kernels do) while they are staged into LDS. Two matrix-core forms multiply them with the
+// f32 activations:
+//  - fp16 (launch_pf_gemm with xh): each token row of X scaled by a power of two so that its largest
+//    magnitude lies in [2^14, 2^15), each weight matrix likewise (pf_wexp), and every value split
+//    into hi = fp16(v) and lo = fp16(v - hi), 22 significant bits together. A product is
+//    hi_x hi_w + hi_x lo_w + lo_x hi_w (v_mfma_f32_16x16x32_f16, exact fp16 products summed in f32),
+//    within 2^-21 of the f32 product (the dropped lo_x lo_w and the two splits' roundings); the
+//    scales are undone exactly in the epilogue. Three fp16 products cost 3/16 of one f32 product
+//    on MI355X's matrix cores.
+//  - f32 (xh null): v_mfma_f32_16x16x4f32 on the f32 values, the products of the reference's F32
+//    path summed in f32 in the matrix core's order.
 #include "prefill.hpp"
 #include "deq.hpp"
 #include "gemv.hpp"
 
 #include <math.h>
+#include <string.h>
+
+#include <algorithm>
 
 namespace fllm {
 
@@ -60,10 +71,24 @@ template <> struct PfW<FLLM_TYPE_Q4_K> {
     }
     // byte idx of the 16-byte header
     __device__ static uint32_t hbyte(const uint4& h, int idx) {
-        const uint32_t w = idx < 8 ? (idx < 4 ? h.x : h.y) : (idx < 12 ? h.z : h.w);
+        // selects of values, not of lvalues: a select of the fields' addresses keeps the header in
+        // scratch memory
+        const uint32_t x = h.x, y = h.y, z = h.z, w4 = h.w;
+        const uint32_t w = idx < 8 ? (idx < 4 ? x : y) : (idx < 12 ? z : w4);
         return (w >> (8 * (idx & 3))) & 0xFFu;
     }
-    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+    // DecodeKScaleMin (Dequantizer.cs:506-521) on scale bytes 4..15 of the header
+    __device__ static void scale_min(const uint4& h, int g, int& sc, int& mn) {
+        if (g < 4) {
+            sc = (int)(hbyte(h, 4 + g) & 63u);
+            mn = (int)(hbyte(h, 8 + g) & 63u);
+        } else {
+            const uint32_t b = hbyte(h, 8 + g), lo = hbyte(h, g), hi = hbyte(h, 4 + g);
+            sc = (int)((b & 15u) | ((lo >> 6) << 4));
+            mn = (int)((b >> 4) | ((hi >> 6) << 4));
+        }
+    }
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v, float s = 1.0f) {
         const int g = (k0 >> 5) & 7;
         const float d = half_exact(w4.hdr.x & 0xFFFFu), dmin = half_exact(w4.hdr.x >> 16);
         // DecodeKScaleMin (Dequantizer.cs:506-521) on scale bytes 4..15 of the header
@@ -76,8 +101,9 @@ template <> struct PfW<FLLM_TYPE_Q4_K> {
             sc = (int)((b & 15u) | ((lo >> 6) << 4));
             mn = (int)((b >> 4) | ((hi >> 6) << 4));
         }
-        const float dg = d * (float)sc;
-        const float mg = dmin * (float)mn;
+        // a power-of-two scale s commutes with the roundings: (dg s) q - mg s = s (dg q - mg) exactly
+        const float dg = d * (float)sc * s;
+        const float mg = dmin * (float)mn * s;
         const uint32_t wd[4] = {w4.qs.x, w4.qs.y, w4.qs.z, w4.qs.w};
 #pragma unroll
         for (int i = 0; i < 32; i++) {
@@ -101,10 +127,10 @@ template <> struct PfW<FLLM_TYPE_Q6_K> {
         w4.s4 = *(const uint32_t*)(reg + 3072 + 4 * L);
         w4.d = *(const uint16_t*)(reg + 3328 + 2 * n);
     }
-    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v, float s = 1.0f) {
         const int g = (k0 >> 5) & 7;
         const uint32_t sc2 = g < 4 ? (w4.s4 & 0xFFFFu) : (w4.s4 >> 16);
-        const float d = half_exact(w4.d);
+        const float d = half_exact(w4.d) * s;
         const uint32_t l4[4] = {w4.ql.x, w4.ql.y, w4.ql.z, w4.ql.w}, h2[2] = {w4.qh.x, w4.qh.y};
 #pragma unroll
         for (int i = 0; i < 32; i++) {
@@ -131,9 +157,9 @@ template <> struct PfW<FLLM_TYPE_Q8_0> {
         w4.h1 = *(const uint4*)(base + 1024);
         w4.d = *(const uint32_t*)(reg + 4096 + 16 * n + 4 * q);
     }
-    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v, float s = 1.0f) {
         const int g = (k0 >> 5) & 7;
-        const float d = half_exact(g < 4 ? (w4.d & 0xFFFFu) : (w4.d >> 16));
+        const float d = half_exact(g < 4 ? (w4.d & 0xFFFFu) : (w4.d >> 16)) * s;
         const uint32_t hw[8] = {w4.h0.x, w4.h0.y, w4.h0.z, w4.h0.w, w4.h1.x, w4.h1.y, w4.h1.z, w4.h1.w};
 #pragma unroll
         for (int e = 0; e < 32; e++) {
@@ -154,7 +180,7 @@ template <> struct PfW<FLLM_TYPE_Q5_K> {
         w4.h = *(const uint32_t*)(reg + 2048 + 8 * L + (g < 4 ? 0 : 4));
         w4.hdr = *(const uint4*)(reg + 2560 + 16 * n);
     }
-    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v) {
+    __device__ static void deq(const Raw& w4, const uint8_t*, int, int, int, int k0, float* v, float s = 1.0f) {
         const int g = (k0 >> 5) & 7;
         const float d = half_exact(w4.hdr.x & 0xFFFFu), dmin = half_exact(w4.hdr.x >> 16);
         int sc, mn;
@@ -167,8 +193,9 @@ template <> struct PfW<FLLM_TYPE_Q5_K> {
             sc = (int)((b & 15u) | ((lo >> 6) << 4));
             mn = (int)((b >> 4) | ((hi >> 6) << 4));
         }
-        const float dg = d * (float)sc;
-        const float mg = dmin * (float)mn;
+        // a power-of-two scale s commutes with the roundings: (dg s) q - mg s = s (dg q - mg) exactly
+        const float dg = d * (float)sc * s;
+        const float mg = dmin * (float)mn * s;
         const uint32_t wd[4] = {w4.qs.x, w4.qs.y, w4.qs.z, w4.qs.w};
 #pragma unroll
         for (int e = 0; e < 32; e++) {
@@ -189,9 +216,9 @@ constexpr int PF_ROWS = 100;
 template <> struct PfW<-1> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int type, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int type, int K, int r, int k0, float* v, float s = 1.0f) {
         const int64_t e0 = (int64_t)r * K + k0;
-        for (int i = 0; i < 32; i++) v[i] = deq_elem(type, w, e0 + i);
+        for (int i = 0; i < 32; i++) v[i] = deq_elem(type, w, e0 + i) * s;
     }
 };
 
@@ -199,9 +226,9 @@ template <> struct PfW<-1> {
 template <> struct PfW<PF_ROWS + FLLM_TYPE_Q8_0> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const uint8_t* p = w + (((int64_t)r * K + k0) >> 5) * 34;
-        const float d = half_exact(deq_ld_u16(p));
+        const float d = half_exact(deq_ld_u16(p)) * s;
 #pragma unroll
         for (int i = 0; i < 32; i++) v[i] = (float)(int8_t)p[2 + i] * d;
     }
@@ -211,9 +238,9 @@ template <> struct PfW<PF_ROWS + FLLM_TYPE_Q8_0> {
 template <> struct PfW<PF_ROWS + FLLM_TYPE_Q4_0> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const uint8_t* p = w + (((int64_t)r * K + k0) >> 5) * 18;
-        const float d = half_exact(deq_ld_u16(p));
+        const float d = half_exact(deq_ld_u16(p)) * s;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const uint32_t b = p[2 + j];
@@ -227,15 +254,16 @@ template <> struct PfW<PF_ROWS + FLLM_TYPE_Q4_0> {
 template <> struct PfW<PF_ROWS + FLLM_TYPE_Q4_K> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const int64_t e0 = (int64_t)r * K + k0;
         const uint8_t* p = w + (e0 >> 8) * 144;
         const int g = (int)((e0 & 255) >> 5);
         const float d = half_exact(deq_ld_u16(p)), dmin = half_exact(deq_ld_u16(p + 2));
         int sc, mn;
         kscale_min(p + 4, g, sc, mn);
-        const float dg = d * (float)sc;
-        const float mg = dmin * (float)mn;
+        // a power-of-two scale s commutes with the roundings: (dg s) q - mg s = s (dg q - mg) exactly
+        const float dg = d * (float)sc * s;
+        const float mg = dmin * (float)mn * s;
         const uint8_t* qs = p + 16 + 16 * g;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
@@ -250,15 +278,16 @@ template <> struct PfW<PF_ROWS + FLLM_TYPE_Q4_K> {
 template <> struct PfW<PF_ROWS + FLLM_TYPE_Q5_K> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const int64_t e0 = (int64_t)r * K + k0;
         const uint8_t* p = w + (e0 >> 8) * 176;
         const int t0 = (int)(e0 & 255), g = t0 >> 5;
         const float d = half_exact(deq_ld_u16(p)), dmin = half_exact(deq_ld_u16(p + 2));
         int sc, mn;
         kscale_min(p + 4, g, sc, mn);
-        const float dg = d * (float)sc;
-        const float mg = dmin * (float)mn;
+        // a power-of-two scale s commutes with the roundings: (dg s) q - mg s = s (dg q - mg) exactly
+        const float dg = d * (float)sc * s;
+        const float mg = dmin * (float)mn * s;
         const uint32_t qh = deq_ld_u32(p + 16 + (t0 >> 3));  // bits of elements t0 .. t0 + 31
 #pragma unroll
         for (int j = 0; j < 16; j++) {
@@ -275,11 +304,11 @@ template <> struct PfW<PF_ROWS + FLLM_TYPE_Q5_K> {
 template <> struct PfW<PF_ROWS + FLLM_TYPE_Q6_K> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const int64_t e0 = (int64_t)r * K + k0;
         const uint8_t* p = w + (e0 >> 8) * 210;
         const int i0 = (int)(e0 & 255);
-        const float d = half_exact(deq_ld_u16(p + 208));
+        const float d = half_exact(deq_ld_u16(p + 208)) * s;
         const uint32_t qh = deq_ld_u32(p + 128 + (i0 >> 2));
         const uint32_t qh2 = deq_ld_u32(p + 128 + (i0 >> 2) + 4);
 #pragma unroll
@@ -300,28 +329,28 @@ template <> struct PfW<PF_ROWS + FLLM_TYPE_Q6_K> {
 template <> struct PfW<PF_ROWS + FLLM_TYPE_F32> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const uint8_t* p = w + ((int64_t)r * K + k0) * 4;
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = bits_f32(deq_ld_u32(p + 4 * i));
+        for (int i = 0; i < 32; i++) v[i] = bits_f32(deq_ld_u32(p + 4 * i)) * s;
     }
 };
 template <> struct PfW<PF_ROWS + FLLM_TYPE_F16> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const uint8_t* p = w + ((int64_t)r * K + k0) * 2;
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = half_exact(deq_ld_u16(p + 2 * i));
+        for (int i = 0; i < 32; i++) v[i] = half_exact(deq_ld_u16(p + 2 * i)) * s;
     }
 };
 template <> struct PfW<PF_ROWS + FLLM_TYPE_BF16> {
     struct Raw {};
     __device__ static void load(Raw&, const uint8_t*, int, int, int) {}
-    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v) {
+    __device__ static void deq(const Raw&, const uint8_t* __restrict__ w, int, int K, int r, int k0, float* v, float s = 1.0f) {
         const uint8_t* p = w + ((int64_t)r * K + k0) * 2;
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = bf16_exact(deq_ld_u16(p + 2 * i));
+        for (int i = 0; i < 32; i++) v[i] = bf16_exact(deq_ld_u16(p + 2 * i)) * s;
     }
 };
 
@@ -438,6 +467,516 @@ __device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, i
             }
 }
 
+// workgroup (x, y): column tile x of the launch's segments, token tile y
+__device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
+    int si = 0;
+    while (si + 1 < a.nseg && bx >= a.seg[si].tiles) {
+        bx -= a.seg[si].tiles;
+        si++;
+    }
+    return si;
+}
+
+// ---- fp16 form ----------------------------------------------------------------------------------
+// LDS rows of PF_BK halves plus 16 bytes; X and W as [plane][row][k] with plane 0 = hi, 1 = lo.
+constexpr int PF_LDH = PF_BK + 8;
+typedef _Float16 pf_h8 __attribute__((ext_vector_type(8)));
+
+template <int BM>
+static constexpr size_t pf_gemm_lds_h() {
+    return sizeof(_Float16) * 2 * (size_t)(BM + PF_BN) * PF_LDH;
+}
+
+// hi / lo halves of 8 scaled values, two at a time with the packed round-toward-zero conversion:
+// hi keeps 11 bits of each value, lo the remainder (exact in f32) to 11 bits
+typedef __fp16 pf_h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void pf_split8(const float* v, uint4& hi, uint4& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const pf_h2 hh = __builtin_amdgcn_cvt_pkrtz(v[2 * u], v[2 * u + 1]);
+        const pf_h2 ll = __builtin_amdgcn_cvt_pkrtz(v[2 * u] - (float)hh[0], v[2 * u + 1] - (float)hh[1]);
+        h[u] = __builtin_bit_cast(uint32_t, hh);
+        l[u] = __builtin_bit_cast(uint32_t, ll);
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// Same tile as pf_gemm_tile: BM tokens x 128 weight rows, 4 waves of (BM / 2) x 64, K steps of 64.
+// MFMA 16x16x32 f16: lane l supplies row (l & 15) of the A (tokens) and B (weight rows) tiles with
+// k = 8 (l >> 4) .. + 7 of a 32-wide slice, one 16-byte LDS read per operand and plane; D lane l holds
+// rows 4 (l >> 4) .. + 3 of column l & 15.
+template <int WT, int BM>
+__device__ __forceinline__ void pf_gemm_tile_h(const PfGemm& a, const PfSeg& sg, int n0, int t0, _Float16* sx,
+                                               _Float16* sw) {
+    constexpr int WM = BM / 2;   // tokens per wave
+    constexpr int TI = WM / 16;  // MFMA tiles along the tokens
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    pf_f32x4 acc[TI][4];
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // X: per K step BM rows x 64 halves x 2 planes = BM * 16 pieces of 8 halves; piece c = tid + 256 i
+    // is plane c / (8 BM), row (c % (8 BM)) / 8, halves 8 (c % 8) .. + 7. W: group wgrp of row wrow
+    constexpr int XP = BM * 16 / 256;
+    const size_t plane = (size_t)a.T * a.ldh;
+    const int wrow = tid & (PF_BN - 1), wgrp = tid / PF_BN, wr = n0 + wrow;
+    const bool wlive = wr < sg.N;
+    const float wsc = ldexpf(1.0f, -sg.wexp);
+    using Raw = typename PfW<WT>::Raw;
+    uint4 xr[XP];
+    Raw wraw;
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM), row = rem >> 3, t = t0 + row;
+            const int k = k0 + (rem & 7) * 8;
+            xr[i] = (t < a.T && k < a.K) ? *(const uint4*)(a.xh + pl * plane + (size_t)t * a.ldh + k)
+                                         : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (wlive && k0 + 32 * wgrp < a.K) PfW<WT>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
+    };
+    const int kb = (int)blockIdx.z * a.kpart, ke = kb + a.kpart < a.K ? kb + a.kpart : a.K;
+    fetch(kb);
+    for (int k0 = kb; k0 < ke; k0 += PF_BK) {
+        __syncthreads();  // the previous step's operands have been read
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
+            *(uint4*)(sx + ((size_t)pl * BM + (rem >> 3)) * PF_LDH + (rem & 7) * 8) = xr[i];
+        }
+        {
+            float v[32];
+            const int k = k0 + 32 * wgrp;
+            if (wlive && k < a.K) {
+                PfW<WT>::deq(wraw, sg.w, sg.type, a.K, wr, k, v, wsc);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; i++) v[i] = 0.0f;
+            }
+            _Float16* d0 = sw + (size_t)wrow * PF_LDH + 32 * wgrp;
+            _Float16* d1 = d0 + (size_t)PF_BN * PF_LDH;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint4 hi, lo;
+                pf_split8(v + 8 * i, hi, lo);
+                *(uint4*)(d0 + 8 * i) = hi;
+                *(uint4*)(d1 + 8 * i) = lo;
+            }
+        }
+        // the next step's global loads fly while this step multiplies
+        if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < PF_BK; kk += 32) {
+            const int ko = kk + 8 * (lane >> 4);
+            pf_h8 ah[TI], al[TI], bh[4], bl[4];
+#pragma unroll
+            for (int i = 0; i < TI; i++) {
+                const _Float16* p = sx + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDH + ko;
+                ah[i] = *(const pf_h8*)p;
+                al[i] = *(const pf_h8*)(p + (size_t)BM * PF_LDH);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const _Float16* p = sw + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDH + ko;
+                bh[j] = *(const pf_h8*)p;
+                bl[j] = *(const pf_h8*)(p + (size_t)PF_BN * PF_LDH);
+            }
+            // the three products go over all tiles in turn, so consecutive MFMAs write different
+            // accumulators
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    const float wun = ldexpf(1.0f, sg.wexp);
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = t0 + WM * wm + 16 * i + 4 * (lane >> 4) + e;
+            if (t >= a.T) continue;
+            const float f = a.xs[t] * wun;  // undoes both scales: exact
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int n = n0 + 64 * wn + 16 * j + (lane & 15);
+                if (n >= sg.N) continue;
+                const float r = acc[i][j][e] * f;
+                if (blockIdx.z == 0) {
+                    float* p = sg.y + (size_t)t * sg.ldy + n;
+                    *p = a.add ? *p + r : r;
+                } else {
+                    const size_t col = (size_t)(sg.y - a.seg[0].y);
+                    a.part[(size_t)(blockIdx.z - 1) * a.T * sg.ldy + (size_t)t * sg.ldy + col + n] = r;
+                }
+            }
+        }
+}
+
+// ---- fp16 form, Q4_K -------------------------------------------------------------------------
+// A Q4_K weight is dg q - mg with dg = d sc_g, mg = dmin m_g (Dequantizer.cs:251-294), so
+//   sum_i w_i x_i = d sum_(g in block) sum_(i in g) (sc_g q_i) x_i - sum_g (dmin m_g) X_g,
+// X_g the sum of group g's x. sc_g q_i <= 945 is an integer, exact in fp16: the weights need no split
+// and a product is two MFMAs (x hi and x lo against the same weights). Every 256-element block's sum
+// is scaled by its d in f32; the min term of a block is one more MFMA whose K slice packs, per row,
+// (v_g hi, v_g lo, v_g hi) for v_g = -dmin m_g against, per token, (X_g hi, X_g hi, X_g lo), the
+// three products of the two splits, added to the same accumulator. The group sums are stored times
+// 2^-6 (to stay in fp16's range) and v_g taken times 2^6, so their products are unchanged.
+constexpr int PF_LDV = 40;  // LDS row stride (halves) of a block's min-term slice
+
+template <int BM>
+static constexpr size_t pf_gemm_lds_k() {
+    return sizeof(_Float16) * ((size_t)(2 * BM + PF_BN) * PF_LDH + (size_t)(BM + PF_BN) * PF_LDV) + sizeof(float) * PF_BN;
+}
+
+typedef _Float16 pf_hv2 __attribute__((ext_vector_type(2)));
+// sc q_i for the 8 elements of one qs dword (bytes b = 0..3: element 2 b the low nibble, 2 b + 1 the
+// high one), as 4 dwords of fp16 pairs: 1024 + q by setting the fp16 pattern 0x6400 | q, minus 1024,
+// times sc, all exact
+__device__ __forceinline__ void pf_q4_pairs(uint32_t x, pf_hv2 sc2, uint32_t* out) {
+    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+    const pf_hv2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        // bytes: low nibble of byte b, 0, high nibble of byte b, 0
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+        const uint32_t p = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+        const pf_hv2 v = (__builtin_bit_cast(pf_hv2, p) - bias) * sc2;
+        out[b] = __builtin_bit_cast(uint32_t, v);
+    }
+}
+
+template <int BM>
+__device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& sg, int n0, int t0, _Float16* lds) {
+    constexpr int WM = BM / 2, TI = WM / 16;
+    _Float16* sx = lds;                                    // [2][BM][PF_LDH]
+    _Float16* sw = sx + (size_t)2 * BM * PF_LDH;           // [PF_BN][PF_LDH]
+    _Float16* sav = sw + (size_t)PF_BN * PF_LDH;           // [BM][PF_LDV]
+    _Float16* swv = sav + (size_t)BM * PF_LDV;             // [PF_BN][PF_LDV]
+    float* sd = (float*)(swv + (size_t)PF_BN * PF_LDV);    // [PF_BN]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    pf_f32x4 acc[TI][4], blk[TI][4];
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = blk[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    constexpr int XP = BM * 16 / 256;
+    const size_t plane = (size_t)a.T * a.ldh;
+    const int G = a.K / 32;
+    const _Float16* xg = a.xh + 2 * plane;  // group sums: hi plane, then lo plane
+    const size_t gplane = (size_t)a.T * G;
+    const int wrow = tid & (PF_BN - 1), wgrp = tid / PF_BN, wr = n0 + wrow;
+    const bool wlive = wr < sg.N;
+    // block-start extras: token row (tid >> 1) of the min-term slice, its hi (tid even) or lo group sums
+    const int vt = tid >> 1, vhl = tid & 1;
+    using Raw = typename PfW<FLLM_TYPE_Q4_K>::Raw;
+    uint4 xr[XP], xv = make_uint4(0u, 0u, 0u, 0u);
+    Raw wraw;
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM), row = rem >> 3, t = t0 + row;
+            const int k = k0 + (rem & 7) * 8;
+            xr[i] = (t < a.T && k < a.K) ? *(const uint4*)(a.xh + pl * plane + (size_t)t * a.ldh + k)
+                                         : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if ((k0 & 255) == 0 && vt < BM) {
+            const int t = t0 + vt;
+            xv = t < a.T ? *(const uint4*)(xg + vhl * gplane + (size_t)t * G + (k0 >> 5)) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (wlive) PfW<FLLM_TYPE_Q4_K>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
+    };
+    const int kb = (int)blockIdx.z * a.kpart, ke = kb + a.kpart < a.K ? kb + a.kpart : a.K;
+    fetch(kb);
+    for (int k0 = kb; k0 < ke; k0 += PF_BK) {
+        __syncthreads();  // the previous step's operands have been read
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
+            *(uint4*)(sx + ((size_t)pl * BM + (rem >> 3)) * PF_LDH + (rem & 7) * 8) = xr[i];
+        }
+        const int g = ((k0 >> 5) & 7) + wgrp;
+        {
+            uint32_t out[16];
+            if (wlive) {
+                int sc, mn;
+                PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, g, sc, mn);
+                const _Float16 sch = (_Float16)(float)sc;
+                const pf_hv2 sc2 = {sch, sch};
+                pf_q4_pairs(wraw.qs.x, sc2, out);
+                pf_q4_pairs(wraw.qs.y, sc2, out + 4);
+                pf_q4_pairs(wraw.qs.z, sc2, out + 8);
+                pf_q4_pairs(wraw.qs.w, sc2, out + 12);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) out[i] = 0u;
+            }
+            uint4* dst = (uint4*)(sw + (size_t)wrow * PF_LDH + 32 * wgrp);
+#pragma unroll
+            for (int i = 0; i < 4; i++) dst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+        }
+        if ((k0 & 255) == 0) {
+            // the block's d and min-term slice of this row (v_g = -dmin m_g, exact in f32, split)
+            if (wgrp == 0) {
+                const float d = wlive ? half_exact(wraw.hdr.x & 0xFFFFu) : 0.0f;
+                const float dmin = wlive ? half_exact(wraw.hdr.x >> 16) : 0.0f;
+                sd[wrow] = d;
+                uint32_t vh[4], vl[4];
+#pragma unroll
+                for (int gg = 0; gg < 8; gg += 2) {
+                    int sc0, mn0, sc1, mn1;
+                    PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, gg, sc0, mn0);
+                    PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, gg + 1, sc1, mn1);
+                    const float v0 = wlive ? -(dmin * (float)mn0) * 64.0f : 0.0f;
+                    const float v1 = wlive ? -(dmin * (float)mn1) * 64.0f : 0.0f;
+                    const pf_h2 h = __builtin_amdgcn_cvt_pkrtz(v0, v1);
+                    const pf_h2 l = __builtin_amdgcn_cvt_pkrtz(v0 - (float)h[0], v1 - (float)h[1]);
+                    vh[gg >> 1] = __builtin_bit_cast(uint32_t, h);
+                    vl[gg >> 1] = __builtin_bit_cast(uint32_t, l);
+                }
+                uint4* dv = (uint4*)(swv + (size_t)wrow * PF_LDV);
+                dv[0] = make_uint4(vh[0], vh[1], vh[2], vh[3]);
+                dv[1] = make_uint4(vl[0], vl[1], vl[2], vl[3]);
+                dv[2] = dv[0];
+                dv[3] = make_uint4(0u, 0u, 0u, 0u);
+            }
+            // tokens: (X hi, X hi, X lo, 0) against (v hi, v lo, v hi, 0)
+            if (vt < BM) {
+                uint4* av = (uint4*)(sav + (size_t)vt * PF_LDV);
+                if (vhl == 0) {
+                    av[0] = xv;
+                    av[1] = xv;
+                } else {
+                    av[2] = xv;
+                    av[3] = make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+        }
+        const bool block_end = (k0 & 255) == 192;
+        if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < PF_BK; kk += 32) {
+            const int ko = kk + 8 * (lane >> 4);
+            pf_h8 ah[TI], al[TI], bw[4];
+#pragma unroll
+            for (int i = 0; i < TI; i++) {
+                const _Float16* p = sx + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDH + ko;
+                ah[i] = *(const pf_h8*)p;
+                al[i] = *(const pf_h8*)(p + (size_t)BM * PF_LDH);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) bw[j] = *(const pf_h8*)(sw + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDH + ko);
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], blk[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], blk[i][j], 0, 0, 0);
+        }
+        if (block_end) {
+            // the block's d times its sum, and its min term
+            const int ko = 8 * (lane >> 4);
+            pf_h8 av[TI], bv[4];
+#pragma unroll
+            for (int i = 0; i < TI; i++) av[i] = *(const pf_h8*)(sav + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDV + ko);
+#pragma unroll
+            for (int j = 0; j < 4; j++) bv[j] = *(const pf_h8*)(swv + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDV + ko);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float d = sd[64 * wn + 16 * j + (lane & 15)];
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[i][j][e] += d * blk[i][j][e];
+                    blk[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = t0 + WM * wm + 16 * i + 4 * (lane >> 4) + e;
+            if (t >= a.T) continue;
+            const float f = a.xs[t];  // undoes the activations' scale: exact
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int n = n0 + 64 * wn + 16 * j + (lane & 15);
+                if (n >= sg.N) continue;
+                const float r = acc[i][j][e] * f;
+                if (blockIdx.z == 0) {
+                    float* p = sg.y + (size_t)t * sg.ldy + n;
+                    *p = a.add ? *p + r : r;
+                } else {
+                    const size_t col = (size_t)(sg.y - a.seg[0].y);
+                    a.part[(size_t)(blockIdx.z - 1) * a.T * sg.ldy + (size_t)t * sg.ldy + col + n] = r;
+                }
+            }
+        }
+}
+
+template <int BM>
+__global__ __launch_bounds__(256) void k_pf_gemm_tiles_h(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_ldh[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    const PfSeg& sg = a.seg[si];
+    _Float16* sw = pf_ldh + (size_t)2 * BM * PF_LDH;
+    if (sg.type == FLLM_TYPE_Q6_K)
+        pf_gemm_tile_h<FLLM_TYPE_Q6_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ldh, sw);
+    else if (sg.type == FLLM_TYPE_Q8_0)
+        pf_gemm_tile_h<FLLM_TYPE_Q8_0, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ldh, sw);
+    else if (sg.type == FLLM_TYPE_Q5_K)
+        pf_gemm_tile_h<FLLM_TYPE_Q5_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ldh, sw);
+    else
+        pf_gemm_tile_h<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ldh, sw);
+}
+
+// launches whose segments are all tile-interleaved Q4_K
+template <int BM>
+__global__ __launch_bounds__(256) void k_pf_gemm_q4k(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_ldk[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    pf_gemm_tile_q4k<BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_ldk);
+}
+
+template <int BM, int RT>
+__global__ __launch_bounds__(256) void k_pf_gemm_rows_h(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_ldh[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    pf_gemm_tile_h<RT, BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_ldh, pf_ldh + (size_t)2 * BM * PF_LDH);
+}
+
+// row t of X: the power of two bringing its largest magnitude into [2^14, 2^15), then the hi / lo
+// halves of the scaled values (K a multiple of 32, ldx and ldh multiples of 4), and the hi / lo halves
+// of every 32-element group's sum of the scaled values (planes of K / 32 per row after the two value
+// planes: hi at 2 T ldh + t K / 32, lo T K / 32 further)
+__global__ __launch_bounds__(256) void k_pf_split(const float* __restrict__ x, int ldx, int K, _Float16* __restrict__ xh,
+                                                  int ldh, size_t plane, float* __restrict__ xs, int T) {
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    const float4* xr = (const float4*)(x + (size_t)t * ldx);
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < K / 4; i += 256) {
+        const float4 v = xr[i];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    m = pf_wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (m > 0.0f && m <= 3.0e38f) {
+        int ex;
+        (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
+        e = 15 - ex;
+        e = e < -120 ? -120 : (e > 120 ? 120 : e);
+    }
+    const float sc = ldexpf(1.0f, e);
+    _Float16* h = xh + (size_t)t * ldh;
+    for (int i = threadIdx.x; i < K / 4; i += 256) {
+        const float4 v = xr[i];
+        const float c[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            hi[u] = (_Float16)c[u];
+            lo[u] = (_Float16)(c[u] - (float)hi[u]);
+        }
+        *(uint2*)(h + 4 * i) = *(const uint2*)hi;
+        *(uint2*)(h + plane + 4 * i) = *(const uint2*)lo;
+    }
+    // group sums: 8 lanes of 4 elements per 32-element group, summed in a fixed order
+    const int G = K / 32;
+    _Float16* gs = xh + 2 * plane + (size_t)t * G;
+    const size_t gplane = (size_t)T * G;
+    for (int g0 = 0; g0 < G; g0 += 32) {
+        const int g = g0 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
+        float v = 0.0f;
+        if (g < G) {
+            const float4 q = xr[g * 8 + sub];
+            v = ((q.x * sc + q.y * sc) + (q.z * sc + q.w * sc));
+        }
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        v += __shfl_xor(v, 4);
+        if (g < G && sub == 0) {
+            // times 2^-6 (exact): 32 values of magnitude below 2^15 sum below 2^20, past fp16's range
+            v *= 0.015625f;
+            const _Float16 hi = (_Float16)v;
+            gs[g] = hi;
+            gs[gplane + g] = (_Float16)(v - (float)hi);
+        }
+    }
+    if (threadIdx.x == 0) xs[t] = ldexpf(1.0f, -e);
+}
+
+hipError_t launch_pf_split(const float* x, int ldx, int T, int K, _Float16* xh, int ldh, float* xs, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    if (K % 32 != 0 || ldx % 4 != 0 || ldh % 8 != 0 || ldh < K) return hipErrorInvalidValue;
+    k_pf_split<<<T, 256, 0, st>>>(x, ldx, K, xh, ldh, (size_t)T * ldh, xs, T);
+    return hipGetLastError();
+}
+
+// largest |w| of a matrix (exact dequantization of every element), as float bits (non-negative floats
+// order like their bits)
+__global__ __launch_bounds__(256) void k_pf_wmax(int type, const uint8_t* __restrict__ w, int64_t n, unsigned* out) {
+    __shared__ float red[4];
+    float m = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float v = fabsf(deq_elem(type, w, i));
+        m = v > m ? v : m;  // a NaN weight is skipped
+    }
+    m = pf_wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        if (m > 0.0f) atomicMax(out, __float_as_uint(m));
+    }
+}
+
+hipError_t launch_pf_wmax(int type, const uint8_t* w, int64_t n, unsigned* out, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    k_pf_wmax<<<(unsigned)blocks, 256, 0, st>>>(type, w, n, out);
+    return hipGetLastError();
+}
+
+int pf_wexp(unsigned max_bits) {
+    float m;
+    memcpy(&m, &max_bits, 4);
+    if (!(m > 0.0f) || !(m <= 3.0e38f)) return 0;  // zero or not finite: no scaling
+    int ex;
+    (void)frexpf(m, &ex);
+    int e = ex - 15;  // m 2^-e in [2^14, 2^15)
+    return e < -120 ? -120 : (e > 120 ? 120 : e);
+}
+
 typedef void (*PfGemmKernel)(const PfGemm);
 
 // y[i] += part[0][i] + part[1][i] + ... (in that order) over n = T * ldy values
@@ -450,15 +989,6 @@ __global__ __launch_bounds__(256) void k_pf_split_add(float* __restrict__ y, con
     }
 }
 
-// workgroup (x, y): column tile x of the launch's segments, token tile y
-__device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
-    int si = 0;
-    while (si + 1 < a.nseg && bx >= a.seg[si].tiles) {
-        bx -= a.seg[si].tiles;
-        si++;
-    }
-    return si;
-}
 
 // tile-interleaved Q4_K / Q6_K segments
 template <int BM>
@@ -501,6 +1031,21 @@ static PfGemmKernel pf_rows_kernel(int type) {
     }
 }
 
+template <int BM>
+static PfGemmKernel pf_rows_kernel_h(int type) {
+    switch (type) {
+        case FLLM_TYPE_Q8_0: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_Q8_0>;
+        case FLLM_TYPE_Q4_0: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_Q4_0>;
+        case FLLM_TYPE_Q4_K: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_Q4_K>;
+        case FLLM_TYPE_Q5_K: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_Q5_K>;
+        case FLLM_TYPE_Q6_K: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_Q6_K>;
+        case FLLM_TYPE_F32: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_F32>;
+        case FLLM_TYPE_F16: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_F16>;
+        case FLLM_TYPE_BF16: return k_pf_gemm_rows_h<BM, PF_ROWS + FLLM_TYPE_BF16>;
+        default: return k_pf_gemm_rows_h<BM, -1>;
+    }
+}
+
 static hipError_t pf_lds_attr(const void* k, size_t bytes) {
     return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
@@ -526,9 +1071,24 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
     // 511 tokens: 896 tiles of 128 tokens ran 3% slower than 1792 of 64)
     const bool tall = col_tiles * ((a.T + 127) / 128) >= 4 * (int64_t)(n_cu > 0 ? n_cu : 256);
     PfGemmKernel k;
-    if (tiles) k = tall ? k_pf_gemm_tiles<128> : k_pf_gemm_tiles<64>;
-    else k = tall ? pf_rows_kernel<128>(a.seg[0].type) : pf_rows_kernel<64>(a.seg[0].type);
-    const size_t lds = tall ? pf_gemm_lds<128>() : pf_gemm_lds<64>();
+    size_t lds;
+    if (a.xh) {
+        if (a.ldh < a.K || a.ldh % 8 != 0 || a.xs == nullptr) return hipErrorInvalidValue;
+        bool all_q4k = tiles;
+        for (int i = 0; i < a.nseg; i++) all_q4k = all_q4k && a.seg[i].type == FLLM_TYPE_Q4_K;
+        if (all_q4k) {
+            k = tall ? k_pf_gemm_q4k<128> : k_pf_gemm_q4k<64>;
+            lds = tall ? pf_gemm_lds_k<128>() : pf_gemm_lds_k<64>();
+        } else {
+            if (tiles) k = tall ? k_pf_gemm_tiles_h<128> : k_pf_gemm_tiles_h<64>;
+            else k = tall ? pf_rows_kernel_h<128>(a.seg[0].type) : pf_rows_kernel_h<64>(a.seg[0].type);
+            lds = tall ? pf_gemm_lds_h<128>() : pf_gemm_lds_h<64>();
+        }
+    } else {
+        if (tiles) k = tall ? k_pf_gemm_tiles<128> : k_pf_gemm_tiles<64>;
+        else k = tall ? pf_rows_kernel<128>(a.seg[0].type) : pf_rows_kernel<64>(a.seg[0].type);
+        lds = tall ? pf_gemm_lds<128>() : pf_gemm_lds<64>();
+    }
     hipError_t e = pf_lds_attr((const void*)k, lds);
     if (e != hipSuccess) return e;
     const int bm = tall ? 128 : 64;
@@ -683,88 +1243,136 @@ hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w
 
 // ---- causal attention over the cache (ComputeAttention, LlamaForwardPass.cs:158-211 and the
 // Mistral / Qwen2 / Gemma2 variants) ----------------------------------------------------------------
-// Workgroup = (query head, block of 8 consecutive queries), one wave per query. Keys go in blocks
-// of 64 rows of the head's kv head, staged in LDS (K rows padded to HD + 1 floats so that lane j
-// reading row j is conflict-free). Per block a wave scores its 64 keys (lane = key), updates the
-// running max / sum (online softmax) and adds p_j v_j to its output slice (lane = dims d, d + 64, ..).
-constexpr int PF_AQ = 8, PF_AK = 64;
+// Workgroup = (query head, block of 64 consecutive queries), wave w = queries 16 w .. + 15. Keys go in
+// blocks of 64 rows of the head's kv head, staged in LDS (K and V rows padded to HD + 4 floats). Per
+// block a wave forms the transposed scores S^T = K Q^T on the f32 matrix cores
+// (v_mfma_f32_16x16x4f32: lane l holds keys 16 t + 4 (l >> 4) + e of query l & 15), updates the running
+// max / sum per query (online softmax), and adds O^T += V^T P^T with P^T straight from the score
+// registers: a step's four keys are the four keys one lane holds, so V's rows are taken in that order.
+// The order of the terms inside the dot products and sums is a permutation of the reference's; every
+// product and sum is f32.
+constexpr int PF_AQ = 64, PF_AK = 64;
 
 template <int HD>
 static constexpr size_t pf_attn_lds() {
-    return sizeof(float) * ((size_t)PF_AK * (HD + 1) + (size_t)PF_AK * HD + PF_AQ * PF_AK + PF_AQ * HD);
+    return sizeof(float) * 2 * (size_t)PF_AK * (HD + 4);
 }
 
 template <int HD>
-__global__ __launch_bounds__(512) void k_pf_attn(const PfAttn a) {
-    constexpr int DPL = HD / 64;  // output dims per lane
+__global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
+    constexpr int LD = HD + 4, NU = HD / 16, NT = HD / 16;
     extern __shared__ float pa_lds[];
-    float* sk = pa_lds;                  // [PF_AK][HD + 1]
-    float* sv = sk + PF_AK * (HD + 1);   // [PF_AK][HD]
-    float* sp = sv + PF_AK * HD;         // [PF_AQ][PF_AK]
-    float* sq = sp + PF_AQ * PF_AK;      // [PF_AQ][HD]
+    float* sk = pa_lds;             // [PF_AK][LD]
+    float* sv = sk + PF_AK * LD;    // [PF_AK][LD]
     const int h = blockIdx.x, qb = blockIdx.y * PF_AQ;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q16 = lane & 15, kq = lane >> 4;
     const int kvh = h / (a.nh / a.nkv);
-    const int t = qb + wave;
-    const bool live = t < a.T;
-    const int pos = a.pos0 + (live ? t : a.T - 1);
+    // this lane's query (the column it holds) and the wave's query range
+    const int tq = qb + 16 * wave + q16, w0 = qb + 16 * wave;
+    const bool qlive = tq < a.T, wlive = w0 < a.T;
+    const int pos = a.pos0 + (qlive ? tq : a.T - 1);
     const int ws = pos + 1 - a.window > 0 ? pos + 1 - a.window : 0;
-    for (int d = lane; d < HD; d += 64) sq[wave * HD + d] = live ? a.q[(size_t)t * a.ldq + h * HD + d] : 0.0f;
+    const int wpos_hi = a.pos0 + (w0 + 15 < a.T ? w0 + 15 : a.T - 1);
+    const int wws = a.pos0 + w0 + 1 - a.window > 0 ? a.pos0 + w0 + 1 - a.window : 0;
+    // Q^T operand: dims 16 u + 4 (l >> 4) .. + 3 of the lane's query, one per MFMA step
+    float4 qr[NU];
+#pragma unroll
+    for (int u = 0; u < NU; u++)
+        qr[u] = qlive ? *(const float4*)(a.q + (size_t)tq * a.ldq + (size_t)h * HD + 16 * u + 4 * kq)
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     // keys of the workgroup: from the first query's window start to the last live query
     const int tl = (qb + PF_AQ < a.T ? qb + PF_AQ : a.T) - 1;
     const int kend = a.pos0 + tl;
     const int kstart = a.pos0 + qb + 1 - a.window > 0 ? a.pos0 + qb + 1 - a.window : 0;
     const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
     float m = -INFINITY, l = 0.0f;
-    float acc[DPL];
+    // O^T tile d = 4 c + r (c = dt / 4, r = dt % 4) holds dims 64 c + 4 i + r, i = 0..15
+    pf_f32x4 o[NT];
 #pragma unroll
-    for (int e = 0; e < DPL; e++) acc[e] = 0.0f;
+    for (int i = 0; i < NT; i++) o[i] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int kb = kstart; kb <= kend; kb += PF_AK) {
-        __syncthreads();  // the previous block's rows have been read (and sq is written)
-        for (int c = threadIdx.x; c < PF_AK * (HD / 4); c += 512) {
+        __syncthreads();  // the previous block's rows have been read
+        for (int c = threadIdx.x; c < PF_AK * (HD / 4); c += 256) {
             const int j = c / (HD / 4), d4 = (c % (HD / 4)) * 4;
             const int key = kb + j < kend ? kb + j : kend;
             const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
-            const float4 kv = *(const float4*)(a.kc + off);
-            float* kr = sk + j * (HD + 1) + d4;
-            kr[0] = kv.x; kr[1] = kv.y; kr[2] = kv.z; kr[3] = kv.w;
-            *(float4*)(sv + j * HD + d4) = *(const float4*)(a.vc + off);
+            *(float4*)(sk + j * LD + d4) = *(const float4*)(a.kc + off);
+            *(float4*)(sv + j * LD + d4) = *(const float4*)(a.vc + off);
         }
         __syncthreads();
-        if (live && kb <= pos && kb + PF_AK - 1 >= ws) {  // the block meets [ws, pos]
-            const int key = kb + lane;
-            const bool valid = key >= ws && key <= pos;
-            float s = -INFINITY;
-            if (valid) {
-                float dot = 0.0f;
-                const float* qr = sq + wave * HD;
-                const float* kr = sk + lane * (HD + 1);
-#pragma unroll 8
-                for (int d = 0; d < HD; d++) dot = fmaf(qr[d], kr[d], dot);
-                s = dot * a.scale;
-                if (a.softcap > 0.0f) s = tanhf(s * inv_cap) * a.softcap;
-            }
-            const float m_new = fmaxf(m, pf_wave_max(s));
-            const float corr = expf(m - m_new);
-            const float p = valid ? expf(s - m_new) : 0.0f;
-            l = l * corr + pf_wave_sum(p);
-            sp[wave * PF_AK + lane] = p;
-            pf_wave_sync();
+        if (!wlive || kb > wpos_hi || kb + PF_AK - 1 < wws) continue;  // no key of the block for the wave
+        pf_f32x4 s[4];
 #pragma unroll
-            for (int e = 0; e < DPL; e++) acc[e] *= corr;
-            for (int j = 0; j < PF_AK; j++) {
-                const float pj = sp[wave * PF_AK + j];
+        for (int t = 0; t < 4; t++) s[t] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int e = 0; e < DPL; e++) acc[e] = fmaf(pj, sv[j * HD + lane + 64 * e], acc[e]);
+        for (int u = 0; u < NU; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const float4 kr = *(const float4*)(sk + (16 * t + q16) * LD + 16 * u + 4 * kq);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.x, qr[u].x, s[t], 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.y, qr[u].y, s[t], 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.z, qr[u].z, s[t], 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.w, qr[u].w, s[t], 0, 0, 0);
             }
-            pf_wave_sync();  // sp is rewritten for the next block
-            m = m_new;
-        }
+        // scores of keys kb + 16 t + 4 (l >> 4) + e for query l & 15
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int key = kb + 16 * t + 4 * kq + e;
+                float x = s[t][e] * a.scale;
+                if (a.softcap > 0.0f) x = tanhf(x * inv_cap) * a.softcap;
+                x = (qlive && key >= ws && key <= pos) ? x : -INFINITY;
+                s[t][e] = x;
+                bmax = fmaxf(bmax, x);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const float m_new = fmaxf(m, bmax);
+        const float corr = m_new == -INFINITY ? 1.0f : expf(m - m_new);
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float p = s[t][e] == -INFINITY ? 0.0f : expf(s[t][e] - m_new);
+                s[t][e] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l = l * corr + psum;
+        m = m_new;
+#pragma unroll
+        for (int i = 0; i < NT; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[i][e] *= corr;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float* vr = sv + (16 * t + 4 * kq + e) * LD + 4 * q16;
+#pragma unroll
+                for (int c = 0; c < HD / 64; c++) {
+                    const float4 vv = *(const float4*)(vr + 64 * c);
+                    o[4 * c + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, s[t][e], o[4 * c + 0], 0, 0, 0);
+                    o[4 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, s[t][e], o[4 * c + 1], 0, 0, 0);
+                    o[4 * c + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, s[t][e], o[4 * c + 2], 0, 0, 0);
+                    o[4 * c + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, s[t][e], o[4 * c + 3], 0, 0, 0);
+                }
+            }
     }
-    if (live) {
+    if (qlive) {
+        // lane l holds dims 64 c + 16 (l >> 4) + 4 e + r (tile 4 c + r, row 4 (l >> 4) + e) of its query
         const float inv = 1.0f / l;
+        float* orow = a.out + (size_t)tq * a.nh * HD + (size_t)h * HD + 16 * kq;
 #pragma unroll
-        for (int e = 0; e < DPL; e++) a.out[(size_t)t * a.nh * HD + h * HD + lane + 64 * e] = acc[e] * inv;
+        for (int c = 0; c < HD / 64; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                *(float4*)(orow + 64 * c + 4 * e) = make_float4(o[4 * c][e] * inv, o[4 * c + 1][e] * inv,
+                                                                o[4 * c + 2][e] * inv, o[4 * c + 3][e] * inv);
     }
 }
 
@@ -776,15 +1384,15 @@ hipError_t launch_pf_attn(const PfAttn& a, hipStream_t st) {
     switch (a.hd) {
         case 64:
             if ((e = pf_lds_attr((const void*)k_pf_attn<64>, pf_attn_lds<64>())) != hipSuccess) return e;
-            k_pf_attn<64><<<grid, 512, pf_attn_lds<64>(), st>>>(a);
+            k_pf_attn<64><<<grid, 256, pf_attn_lds<64>(), st>>>(a);
             break;
         case 128:
             if ((e = pf_lds_attr((const void*)k_pf_attn<128>, pf_attn_lds<128>())) != hipSuccess) return e;
-            k_pf_attn<128><<<grid, 512, pf_attn_lds<128>(), st>>>(a);
+            k_pf_attn<128><<<grid, 256, pf_attn_lds<128>(), st>>>(a);
             break;
         case 256:
             if ((e = pf_lds_attr((const void*)k_pf_attn<256>, pf_attn_lds<256>())) != hipSuccess) return e;
-            k_pf_attn<256><<<grid, 512, pf_attn_lds<256>(), st>>>(a);
+            k_pf_attn<256><<<grid, 256, pf_attn_lds<256>(), st>>>(a);
             break;
         default: return hipErrorInvalidValue;
     }

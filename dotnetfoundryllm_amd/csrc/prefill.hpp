@@ -17,6 +17,7 @@ struct PfSeg {
     float* y;   // [T][ldy], column 0 = weight row 0
     int ldy;
     int tiles;  // set by launch_pf_gemm: 128-row column tiles of the segment
+    int wexp;   // fp16 matrix cores: the weights enter scaled by 2^-wexp (launch_pf_wmax gives it)
 };
 struct PfGemm {
     const float* x;
@@ -33,8 +34,26 @@ struct PfGemm {
     float* part;
     size_t part_cap;
     int nsplit, kpart;
+    // fp16 matrix cores: X as written by launch_pf_split (two fp16 planes of row stride ldh, each
+    // token row scaled by a power of two) and xs[t], the factor that undoes that scale; the weights
+    // are split the same way in the kernel. Null xh: f32 matrix cores on x.
+    const _Float16* xh;
+    int ldh;
+    const float* xs;
 };
 hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st);
+// The fp16 operand of a GEMM input: each row t of X [T][K] (stride ldx) scaled by 2^e_t, so that its
+// largest magnitude lies in [2^14, 2^15), and written as hi = fp16(x 2^e_t) (plane 0) and
+// lo = fp16(x 2^e_t - hi) (plane 1, at xh + T * ldh), 22 significant bits together; xs[t] = 2^-e_t.
+// After the two planes: the hi and lo halves of each 32-element group's sum of the scaled values
+// (xh + 2 T ldh: T rows of K / 32, then the lo plane), for the Q4_K form's min term. xh holds
+// 2 T (ldh + K / 32) halves.
+hipError_t launch_pf_split(const float* x, int ldx, int T, int K, _Float16* xh, int ldh, float* xs, hipStream_t st);
+// *out = max(*out, bits of the largest |w| over the n elements of a weight matrix in GGUF row layout)
+// (out holds a non-negative float's bits; zero it first). pf_wexp turns it into the exponent that
+// brings the matrix's largest magnitude into [2^14, 2^15) for the fp16 split.
+hipError_t launch_pf_wmax(int type, const uint8_t* w, int64_t n, unsigned* out, hipStream_t st);
+int pf_wexp(unsigned max_bits);
 
 // X[t] = embedding row tokens[t] (exact dequantization of any supported type)
 hipError_t launch_pf_embed(const int* tokens, int T, const uint8_t* emb, int type, int H, float* x, hipStream_t st);
