@@ -702,114 +702,120 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
         }
         if (wlive) PfW<FLLM_TYPE_Q4_K>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
     };
+    // whole 256-element blocks (K and the split parts are multiples of 256): four K steps per block,
+    // the block's end straight-line after them, so the accumulators stay in place across steps
     const int kb = (int)blockIdx.z * a.kpart, ke = kb + a.kpart < a.K ? kb + a.kpart : a.K;
     fetch(kb);
-    for (int k0 = kb; k0 < ke; k0 += PF_BK) {
-        __syncthreads();  // the previous step's operands have been read
+    for (int kblk = kb; kblk < ke; kblk += 256) {
 #pragma unroll
-        for (int i = 0; i < XP; i++) {
-            const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
-            *(uint4*)(sx + ((size_t)pl * BM + (rem >> 3)) * PF_LDH + (rem & 7) * 8) = xr[i];
-        }
-        const int g = ((k0 >> 5) & 7) + wgrp;
-        {
-            uint32_t out[16];
-            if (wlive) {
-                int sc, mn;
-                PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, g, sc, mn);
-                const _Float16 sch = (_Float16)(float)sc;
-                const pf_hv2 sc2 = {sch, sch};
-                pf_q4_pairs(wraw.qs.x, sc2, out);
-                pf_q4_pairs(wraw.qs.y, sc2, out + 4);
-                pf_q4_pairs(wraw.qs.z, sc2, out + 8);
-                pf_q4_pairs(wraw.qs.w, sc2, out + 12);
-            } else {
+        for (int st = 0; st < 4; st++) {
+            const int k0 = kblk + st * PF_BK;
+            __syncthreads();  // the previous step's operands have been read
 #pragma unroll
-                for (int i = 0; i < 16; i++) out[i] = 0u;
+            for (int i = 0; i < XP; i++) {
+                const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
+                *(uint4*)(sx + ((size_t)pl * BM + (rem >> 3)) * PF_LDH + (rem & 7) * 8) = xr[i];
             }
-            uint4* dst = (uint4*)(sw + (size_t)wrow * PF_LDH + 32 * wgrp);
-#pragma unroll
-            for (int i = 0; i < 4; i++) dst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
-        }
-        if ((k0 & 255) == 0) {
-            // the block's d and min-term slice of this row (v_g = -dmin m_g, exact in f32, split)
-            if (wgrp == 0) {
-                const float d = wlive ? half_exact(wraw.hdr.x & 0xFFFFu) : 0.0f;
-                const float dmin = wlive ? half_exact(wraw.hdr.x >> 16) : 0.0f;
-                sd[wrow] = d;
-                uint32_t vh[4], vl[4];
-#pragma unroll
-                for (int gg = 0; gg < 8; gg += 2) {
-                    int sc0, mn0, sc1, mn1;
-                    PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, gg, sc0, mn0);
-                    PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, gg + 1, sc1, mn1);
-                    const float v0 = wlive ? -(dmin * (float)mn0) * 64.0f : 0.0f;
-                    const float v1 = wlive ? -(dmin * (float)mn1) * 64.0f : 0.0f;
-                    const pf_h2 h = __builtin_amdgcn_cvt_pkrtz(v0, v1);
-                    const pf_h2 l = __builtin_amdgcn_cvt_pkrtz(v0 - (float)h[0], v1 - (float)h[1]);
-                    vh[gg >> 1] = __builtin_bit_cast(uint32_t, h);
-                    vl[gg >> 1] = __builtin_bit_cast(uint32_t, l);
-                }
-                uint4* dv = (uint4*)(swv + (size_t)wrow * PF_LDV);
-                dv[0] = make_uint4(vh[0], vh[1], vh[2], vh[3]);
-                dv[1] = make_uint4(vl[0], vl[1], vl[2], vl[3]);
-                dv[2] = dv[0];
-                dv[3] = make_uint4(0u, 0u, 0u, 0u);
-            }
-            // tokens: (X hi, X hi, X lo, 0) against (v hi, v lo, v hi, 0)
-            if (vt < BM) {
-                uint4* av = (uint4*)(sav + (size_t)vt * PF_LDV);
-                if (vhl == 0) {
-                    av[0] = xv;
-                    av[1] = xv;
+            const int g = 2 * st + wgrp;
+            {
+                uint32_t out[16];
+                if (wlive) {
+                    int sc, mn;
+                    PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, g, sc, mn);
+                    const _Float16 sch = (_Float16)(float)sc;
+                    const pf_hv2 sc2 = {sch, sch};
+                    pf_q4_pairs(wraw.qs.x, sc2, out);
+                    pf_q4_pairs(wraw.qs.y, sc2, out + 4);
+                    pf_q4_pairs(wraw.qs.z, sc2, out + 8);
+                    pf_q4_pairs(wraw.qs.w, sc2, out + 12);
                 } else {
-                    av[2] = xv;
-                    av[3] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+                    for (int i = 0; i < 16; i++) out[i] = 0u;
+                }
+                uint4* dst = (uint4*)(sw + (size_t)wrow * PF_LDH + 32 * wgrp);
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+            }
+            if (st == 0) {
+                // the block's d and min-term slice of this row (v_g = -dmin m_g, exact in f32, split)
+                if (wgrp == 0) {
+                    const float d = wlive ? half_exact(wraw.hdr.x & 0xFFFFu) : 0.0f;
+                    const float dmin = wlive ? half_exact(wraw.hdr.x >> 16) : 0.0f;
+                    sd[wrow] = d;
+                    uint32_t vh[4], vl[4];
+#pragma unroll
+                    for (int gg = 0; gg < 8; gg += 2) {
+                        int sc0, mn0, sc1, mn1;
+                        PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, gg, sc0, mn0);
+                        PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, gg + 1, sc1, mn1);
+                        const float v0 = wlive ? -(dmin * (float)mn0) * 64.0f : 0.0f;
+                        const float v1 = wlive ? -(dmin * (float)mn1) * 64.0f : 0.0f;
+                        const pf_h2 h = __builtin_amdgcn_cvt_pkrtz(v0, v1);
+                        const pf_h2 l = __builtin_amdgcn_cvt_pkrtz(v0 - (float)h[0], v1 - (float)h[1]);
+                        vh[gg >> 1] = __builtin_bit_cast(uint32_t, h);
+                        vl[gg >> 1] = __builtin_bit_cast(uint32_t, l);
+                    }
+                    uint4* dv = (uint4*)(swv + (size_t)wrow * PF_LDV);
+                    dv[0] = make_uint4(vh[0], vh[1], vh[2], vh[3]);
+                    dv[1] = make_uint4(vl[0], vl[1], vl[2], vl[3]);
+                    dv[2] = dv[0];
+                    dv[3] = make_uint4(0u, 0u, 0u, 0u);
+                }
+                // tokens: (X hi, X hi, X lo, 0) against (v hi, v lo, v hi, 0)
+                if (vt < BM) {
+                    uint4* av = (uint4*)(sav + (size_t)vt * PF_LDV);
+                    if (vhl == 0) {
+                        av[0] = xv;
+                        av[1] = xv;
+                    } else {
+                        av[2] = xv;
+                        av[3] = make_uint4(0u, 0u, 0u, 0u);
+                    }
                 }
             }
-        }
-        const bool block_end = (k0 & 255) == 192;
-        if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
-        __syncthreads();
+            if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
+            __syncthreads();
 #pragma unroll
-        for (int kk = 0; kk < PF_BK; kk += 32) {
-            const int ko = kk + 8 * (lane >> 4);
-            pf_h8 ah[TI], al[TI], bw[4];
-#pragma unroll
-            for (int i = 0; i < TI; i++) {
-                const _Float16* p = sx + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDH + ko;
-                ah[i] = *(const pf_h8*)p;
-                al[i] = *(const pf_h8*)(p + (size_t)BM * PF_LDH);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) bw[j] = *(const pf_h8*)(sw + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDH + ko);
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], blk[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], blk[i][j], 0, 0, 0);
-        }
-        if (block_end) {
-            // the block's d times its sum, and its min term
-            const int ko = 8 * (lane >> 4);
-            pf_h8 av[TI], bv[4];
-#pragma unroll
-            for (int i = 0; i < TI; i++) av[i] = *(const pf_h8*)(sav + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDV + ko);
-#pragma unroll
-            for (int j = 0; j < 4; j++) bv[j] = *(const pf_h8*)(swv + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDV + ko);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float d = sd[64 * wn + 16 * j + (lane & 15)];
+            for (int kk = 0; kk < PF_BK; kk += 32) {
+                const int ko = kk + 8 * (lane >> 4);
+                pf_h8 ah[TI], al[TI], bw[4];
 #pragma unroll
                 for (int i = 0; i < TI; i++) {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) acc[i][j][e] += d * blk[i][j][e];
-                    blk[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+                    const _Float16* p = sx + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDH + ko;
+                    ah[i] = *(const pf_h8*)p;
+                    al[i] = *(const pf_h8*)(p + (size_t)BM * PF_LDH);
                 }
+#pragma unroll
+                for (int j = 0; j < 4; j++) bw[j] = *(const pf_h8*)(sw + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDH + ko);
+                // the block's first product starts its sum from zero
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            al[i], bw[j], (st == 0 && kk == 0) ? pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f} : blk[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], blk[i][j], 0, 0, 0);
+            }
+        }
+        // the block's d times its sum, and its min term (sd / sav / swv were written at the block's
+        // first step and are rewritten only after the next block's first barrier)
+        const int ko = 8 * (lane >> 4);
+        pf_h8 av[TI], bv[4];
+#pragma unroll
+        for (int i = 0; i < TI; i++) av[i] = *(const pf_h8*)(sav + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDV + ko);
+#pragma unroll
+        for (int j = 0; j < 4; j++) bv[j] = *(const pf_h8*)(swv + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDV + ko);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float d = sd[64 * wn + 16 * j + (lane & 15)];
+#pragma unroll
+            for (int i = 0; i < TI; i++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][j][e] = fmaf(d, blk[i][j][e], acc[i][j][e]);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
             }
         }
     }
