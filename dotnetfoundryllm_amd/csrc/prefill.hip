@@ -649,13 +649,14 @@ typedef _Float16 pf_hv2 __attribute__((ext_vector_type(2)));
 // times sc, all exact
 __device__ __forceinline__ void pf_q4_pairs(uint32_t x, pf_hv2 sc2, uint32_t* out) {
     const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
-    const pf_hv2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+    // (1024 + q) sc - 1024 sc in one fma: exact, the result sc q being an integer below 2048
+    const pf_hv2 nb = sc2 * pf_hv2{(_Float16)-1024.0f, (_Float16)-1024.0f};
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         // bytes: low nibble of byte b, 0, high nibble of byte b, 0
         const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
         const uint32_t p = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
-        const pf_hv2 v = (__builtin_bit_cast(pf_hv2, p) - bias) * sc2;
+        const pf_hv2 v = __builtin_elementwise_fma(__builtin_bit_cast(pf_hv2, p), sc2, nb);
         out[b] = __builtin_bit_cast(uint32_t, v);
     }
 }
@@ -688,13 +689,22 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
     using Raw = typename PfW<FLLM_TYPE_Q4_K>::Raw;
     uint4 xr[XP], xv = make_uint4(0u, 0u, 0u, 0u);
     Raw wraw;
+    // a tile of BM whole token rows (uniform over the workgroup) loads without the row test
+    const bool full = t0 + BM <= a.T;
     auto fetch = [&](int k0) {
+        if (full) {
 #pragma unroll
-        for (int i = 0; i < XP; i++) {
-            const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM), row = rem >> 3, t = t0 + row;
-            const int k = k0 + (rem & 7) * 8;
-            xr[i] = (t < a.T && k < a.K) ? *(const uint4*)(a.xh + pl * plane + (size_t)t * a.ldh + k)
-                                         : make_uint4(0u, 0u, 0u, 0u);
+            for (int i = 0; i < XP; i++) {
+                const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
+                xr[i] = *(const uint4*)(a.xh + pl * plane + (size_t)(t0 + (rem >> 3)) * a.ldh + k0 + (rem & 7) * 8);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < XP; i++) {
+                const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM), t = t0 + (rem >> 3);
+                xr[i] = t < a.T ? *(const uint4*)(a.xh + pl * plane + (size_t)t * a.ldh + k0 + (rem & 7) * 8)
+                                : make_uint4(0u, 0u, 0u, 0u);
+            }
         }
         if ((k0 & 255) == 0 && vt < BM) {
             const int t = t0 + vt;
