@@ -852,6 +852,209 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
         }
 }
 
+// ---- fp16 form, Q6_K --------------------------------------------------------------------------
+// A Q6_K weight is d (sc q) with q = v - 32 (v the 6-bit code) and sc the int8 scale of its 16
+// elements (Dequantizer.cs:378-417). I = sc q is an integer of magnitude at most 4096: hi = fp16(I)
+// (exact up to 2048, even integers above) and lo = I - hi (0 or +-1) hold it exactly. A block's sum
+// is x hi * I hi + x lo * I hi + x hi * I lo (the dropped x lo * I lo is below 2^-22 of a product),
+// accumulated apart and added times the block's d in f32 at its end. The weights need no matrix
+// scale: the epilogue only undoes the activations' power of two.
+template <int BM>
+static constexpr size_t pf_gemm_lds_q6() {
+    return sizeof(_Float16) * (size_t)(2 * BM + 2 * PF_BN) * PF_LDH + sizeof(float) * PF_BN;
+}
+
+// the 8 elements of ql dword x (element 2 b: low nibble of byte b, 2 b + 1: high nibble) with their
+// high bits (element j: bits 2 j, 2 j + 1 of h16), scale pair sc2: hi and lo halves of sc q as 4
+// fp16 pairs each. A pair's code v goes into fp16 1024 + v (nibble at bits 0-3, high bits at 4-5 of
+// each half, pattern 0x6400), minus 1056 gives q exactly.
+__device__ __forceinline__ void pf_q6_pairs(uint32_t x, uint32_t h16, pf_hv2 sc2, uint32_t* hi, uint32_t* lo) {
+    const uint32_t nl = x & 0x0F0F0F0Fu, nh = (x >> 4) & 0x0F0F0F0Fu;
+    // y >> 4 b: bits 0-1 the high bits of element 2 b, bits 16-17 those of element 2 b + 1
+    const uint32_t y = h16 | (h16 << 14);
+    const pf_hv2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+        const uint32_t t = (b == 0 ? (y << 4) : (y >> (4 * b - 4))) & 0x00300030u;
+        const uint32_t p = __builtin_amdgcn_perm(nh, nl, sel) | t | 0x64006400u;
+        const pf_hv2 q = __builtin_bit_cast(pf_hv2, p) + off;
+        const pf_hv2 vh = q * sc2;
+        const pf_hv2 vl = __builtin_elementwise_fma(q, sc2, -vh);
+        hi[b] = __builtin_bit_cast(uint32_t, vh);
+        lo[b] = __builtin_bit_cast(uint32_t, vl);
+    }
+}
+
+// Same tile and step structure as pf_gemm_tile_q4k (whole 256-element blocks, four K steps each);
+// the weights go into LDS as hi / lo planes.
+template <int BM>
+__device__ __forceinline__ void pf_gemm_tile_q6k(const PfGemm& a, const PfSeg& sg, int n0, int t0, _Float16* lds) {
+    constexpr int WM = BM / 2, TI = WM / 16;
+    _Float16* sx = lds;                                    // [2][BM][PF_LDH]
+    _Float16* sw = sx + (size_t)2 * BM * PF_LDH;           // [2][PF_BN][PF_LDH]
+    float* sd = (float*)(sw + (size_t)2 * PF_BN * PF_LDH);  // [PF_BN]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    pf_f32x4 acc[TI][4], blk[TI][4];
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = blk[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    constexpr int XP = BM * 16 / 256;
+    const size_t plane = (size_t)a.T * a.ldh;
+    const int wrow = tid & (PF_BN - 1), wgrp = tid / PF_BN, wr = n0 + wrow;
+    const bool wlive = wr < sg.N;
+    using Raw = typename PfW<FLLM_TYPE_Q6_K>::Raw;
+    uint4 xr[XP];
+    Raw wraw;
+    const bool full = t0 + BM <= a.T;
+    auto fetch = [&](int k0) {
+        if (full) {
+#pragma unroll
+            for (int i = 0; i < XP; i++) {
+                const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
+                xr[i] = *(const uint4*)(a.xh + pl * plane + (size_t)(t0 + (rem >> 3)) * a.ldh + k0 + (rem & 7) * 8);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < XP; i++) {
+                const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM), t = t0 + (rem >> 3);
+                xr[i] = t < a.T ? *(const uint4*)(a.xh + pl * plane + (size_t)t * a.ldh + k0 + (rem & 7) * 8)
+                                : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        if (wlive) PfW<FLLM_TYPE_Q6_K>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
+    };
+    const int kb = (int)blockIdx.z * a.kpart, ke = kb + a.kpart < a.K ? kb + a.kpart : a.K;
+    fetch(kb);
+    for (int kblk = kb; kblk < ke; kblk += 256) {
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int k0 = kblk + st * PF_BK;
+            __syncthreads();  // the previous step's operands have been read
+#pragma unroll
+            for (int i = 0; i < XP; i++) {
+                const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
+                *(uint4*)(sx + ((size_t)pl * BM + (rem >> 3)) * PF_LDH + (rem & 7) * 8) = xr[i];
+            }
+            const int g = 2 * st + wgrp;
+            {
+                uint32_t hv[16], lv[16];
+                if (wlive) {
+                    const uint32_t sc = g < 4 ? (wraw.s4 & 0xFFFFu) : (wraw.s4 >> 16);
+                    const pf_hv2 sa = {(_Float16)(float)(int)(int8_t)(sc & 0xFFu), (_Float16)(float)(int)(int8_t)(sc & 0xFFu)};
+                    const pf_hv2 sb = {(_Float16)(float)(int)(int8_t)(sc >> 8), (_Float16)(float)(int)(int8_t)(sc >> 8)};
+                    pf_q6_pairs(wraw.ql.x, wraw.qh.x & 0xFFFFu, sa, hv, lv);
+                    pf_q6_pairs(wraw.ql.y, wraw.qh.x >> 16, sa, hv + 4, lv + 4);
+                    pf_q6_pairs(wraw.ql.z, wraw.qh.y & 0xFFFFu, sb, hv + 8, lv + 8);
+                    pf_q6_pairs(wraw.ql.w, wraw.qh.y >> 16, sb, hv + 12, lv + 12);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; i++) hv[i] = lv[i] = 0u;
+                }
+                uint4* dh = (uint4*)(sw + (size_t)wrow * PF_LDH + 32 * wgrp);
+                uint4* dl = (uint4*)(sw + (size_t)(PF_BN + wrow) * PF_LDH + 32 * wgrp);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    dh[i] = make_uint4(hv[4 * i], hv[4 * i + 1], hv[4 * i + 2], hv[4 * i + 3]);
+                    dl[i] = make_uint4(lv[4 * i], lv[4 * i + 1], lv[4 * i + 2], lv[4 * i + 3]);
+                }
+            }
+            if (st == 0 && wgrp == 0) sd[wrow] = wlive ? half_exact(wraw.d & 0xFFFFu) : 0.0f;
+            if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < PF_BK; kk += 32) {
+                const int ko = kk + 8 * (lane >> 4);
+                pf_h8 ah[TI], al[TI], bh[4], bl[4];
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+                    const _Float16* p = sx + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDH + ko;
+                    ah[i] = *(const pf_h8*)p;
+                    al[i] = *(const pf_h8*)(p + (size_t)BM * PF_LDH);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const _Float16* p = sw + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDH + ko;
+                    bh[j] = *(const pf_h8*)p;
+                    bl[j] = *(const pf_h8*)(p + (size_t)PF_BN * PF_LDH);
+                }
+                // the block's first product starts its sum from zero
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            al[i], bh[j], (st == 0 && kk == 0) ? pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f} : blk[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], blk[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], blk[i][j], 0, 0, 0);
+            }
+        }
+        // the block's d times its sum (sd was written at the block's first step and is rewritten only
+        // after the next block's first barrier)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float d = sd[64 * wn + 16 * j + (lane & 15)];
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][j][e] = fmaf(d, blk[i][j][e], acc[i][j][e]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int t = t0 + WM * wm + 16 * i + 4 * (lane >> 4) + e;
+            if (t >= a.T) continue;
+            const float f = a.xs[t];  // undoes the activations' scale: exact
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int n = n0 + 64 * wn + 16 * j + (lane & 15);
+                if (n >= sg.N) continue;
+                const float r = acc[i][j][e] * f;
+                if (blockIdx.z == 0) {
+                    float* p = sg.y + (size_t)t * sg.ldy + n;
+                    *p = a.add ? *p + r : r;
+                } else {
+                    const size_t col = (size_t)(sg.y - a.seg[0].y);
+                    a.part[(size_t)(blockIdx.z - 1) * a.T * sg.ldy + (size_t)t * sg.ldy + col + n] = r;
+                }
+            }
+        }
+}
+
+// launches whose segments are all tile-interleaved Q6_K
+template <int BM>
+__global__ __launch_bounds__(256) void k_pf_gemm_q6k(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_ld6[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    pf_gemm_tile_q6k<BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_ld6);
+}
+
+// launches of tile-interleaved Q4_K and Q6_K segments (q, k in Q4_K, v in Q6_K): each workgroup
+// takes its segment's form
+template <int BM>
+__global__ __launch_bounds__(256) void k_pf_gemm_q46(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_ld46[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    const PfSeg& sg = a.seg[si];
+    if (sg.type == FLLM_TYPE_Q6_K)
+        pf_gemm_tile_q6k<BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ld46);
+    else
+        pf_gemm_tile_q4k<BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ld46);
+}
+
 template <int BM>
 __global__ __launch_bounds__(256) void k_pf_gemm_tiles_h(const PfGemm a) {
     extern __shared__ __attribute__((aligned(16))) _Float16 pf_ldh[];
@@ -1092,9 +1295,20 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         if (a.ldh < a.K || a.ldh % 8 != 0 || a.xs == nullptr) return hipErrorInvalidValue;
         bool all_q4k = tiles;
         for (int i = 0; i < a.nseg; i++) all_q4k = all_q4k && a.seg[i].type == FLLM_TYPE_Q4_K;
+        bool all_q6k = tiles, q46 = tiles;
+        for (int i = 0; i < a.nseg; i++) {
+            all_q6k = all_q6k && a.seg[i].type == FLLM_TYPE_Q6_K;
+            q46 = q46 && (a.seg[i].type == FLLM_TYPE_Q4_K || a.seg[i].type == FLLM_TYPE_Q6_K);
+        }
         if (all_q4k) {
             k = tall ? k_pf_gemm_q4k<128> : k_pf_gemm_q4k<64>;
             lds = tall ? pf_gemm_lds_k<128>() : pf_gemm_lds_k<64>();
+        } else if (all_q6k) {
+            k = tall ? k_pf_gemm_q6k<128> : k_pf_gemm_q6k<64>;
+            lds = tall ? pf_gemm_lds_q6<128>() : pf_gemm_lds_q6<64>();
+        } else if (q46) {
+            k = tall ? k_pf_gemm_q46<128> : k_pf_gemm_q46<64>;
+            lds = tall ? std::max(pf_gemm_lds_k<128>(), pf_gemm_lds_q6<128>()) : std::max(pf_gemm_lds_k<64>(), pf_gemm_lds_q6<64>());
         } else {
             if (tiles) k = tall ? k_pf_gemm_tiles_h<128> : k_pf_gemm_tiles_h<64>;
             else k = tall ? pf_rows_kernel_h<128>(a.seg[0].type) : pf_rows_kernel_h<64>(a.seg[0].type);
