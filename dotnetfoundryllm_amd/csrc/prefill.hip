@@ -1074,7 +1074,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tiles_h(const PfGemm a) {
 
 // launches whose segments are all tile-interleaved Q4_K
 template <int BM>
-__global__ __launch_bounds__(256) void k_pf_gemm_q4k(const PfGemm a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1))) void k_pf_gemm_q4k(const PfGemm a) {
     extern __shared__ __attribute__((aligned(16))) _Float16 pf_ldk[];
     int bx = blockIdx.x;
     const int si = pf_seg_of(a, bx);
