@@ -375,10 +375,11 @@ def prefill_report(cfg, n, seconds, stages=None):
     element-wise steps and the last token's LM head included, so every fraction is a lower bound).
     `tflops`: the reference's own arithmetic, 2 flop per weight per token plus the causal attention's
     4 * heads * head_dim flop per (query, key) pair. The projections run on the fp16 matrix cores:
-    a launch of Q4_K matrices only takes two fp16 products per weight (exact integer weights against
-    the activations' hi and lo halves) plus one min-term product per 256-element block (1/8 of a
-    product), any other launch three (hi/lo splits of both operands); `gemm` is those fp16 products'
-    rate against the fp16 peak. Attention runs on the f32 matrix cores, one product per flop."""
+    a Q4_K matrix takes two fp16 products per weight (exact integer weights against the activations'
+    hi and lo halves) plus one min-term product per 256-element block (1/8 of a product), any other
+    three (Q6_K: exact integer hi / lo weights; other types: hi / lo splits of both operands); `gemm`
+    is those fp16 products' rate against the fp16 peak. Attention runs on the f32 matrix cores, one
+    product per flop."""
     H, L, F = cfg["hidden"], cfg["n_layers"], cfg["ffn"]
     hd = cfg["head_dim"]
     qdim, kvdim = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
@@ -389,18 +390,15 @@ def prefill_report(cfg, n, seconds, stages=None):
     flops = 2.0 * n * weights + attn
     launches = [((qdim * H, ty["q"]), (kvdim * H, ty["k"]), (kvdim * H, ty["v"])), ((H * qdim, ty["o"]),),
                 ((F * H, ty["gate"]), (F * H, ty["up"])), ((H * F, ty["down"]),)]
-    fp16 = 0.0
-    for g in launches:
-        products = 2.125 if all(t == Q4_K_TYPE for _, t in g) else 3.0
-        fp16 += products * sum(w for w, _ in g)
+    def products(t):
+        return 2.125 if t == Q4_K_TYPE else 3.0
+
+    fp16 = sum(products(t) * w for g in launches for w, t in g)
     fp16_tf = 2.0 * n * L * fp16 / seconds / 1e12
-    attn_tf = attn / seconds / 1e12
     tf = flops / seconds / 1e12
     out = {"tokens": n, "tok_s": round(n / seconds, 2), "tflops": round(tf, 2),
            "gemm": {"dtype": "fp16", "mfma_tflops": round(fp16_tf, 2), "mfma_peak_tflops": FP16_MFMA_PEAK_TFLOPS,
-                    "mfma_frac": round(fp16_tf / FP16_MFMA_PEAK_TFLOPS, 4)},
-           "attention": {"dtype": "f32", "mfma_tflops": round(attn_tf, 2), "mfma_peak_tflops": FP32_MFMA_PEAK_TFLOPS,
-                         "mfma_frac": round(attn_tf / FP32_MFMA_PEAK_TFLOPS, 4)}}
+                    "mfma_frac": round(fp16_tf / FP16_MFMA_PEAK_TFLOPS, 4)}}
     if stages:
         # each stage's own device time (events around its launches in a second, profiled prefill)
         gemm_of = {"pf_qkv": launches[0], "pf_o": launches[1], "pf_gate_up": launches[2], "pf_down": launches[3]}
@@ -409,9 +407,9 @@ def prefill_report(cfg, n, seconds, stages=None):
             row = {"launches": st["launches"], "ms": round(st["ms"], 3)}
             if name in gemm_of:
                 g = gemm_of[name]
-                products = 2.125 if all(t == Q4_K_TYPE for _, t in g) else 3.0
-                mf = 2.0 * n * L * products * sum(w for w, _ in g) / (st["ms"] * 1e-3) / 1e12
-                row.update(dtype="fp16", products=products, mfma_tflops=round(mf, 1),
+                issued = sum(products(t) * w for w, t in g)
+                mf = 2.0 * n * L * issued / (st["ms"] * 1e-3) / 1e12
+                row.update(dtype="fp16", products=round(issued / sum(w for w, _ in g), 3), mfma_tflops=round(mf, 1),
                            mfma_frac=round(mf / FP16_MFMA_PEAK_TFLOPS, 4))
             elif name == "pf_attention":
                 mf = attn / (st["ms"] * 1e-3) / 1e12
