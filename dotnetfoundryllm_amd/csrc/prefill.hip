@@ -5,18 +5,16 @@
 // Y[t][n] = sum_k X[t][k] W[n][k] (LinearProjection, LlamaForwardPass.cs:237-260, for all rows at
 // once), and the element-wise steps of the layer run over all rows.
 //
-// GEMM numerics. Weights are dequantized exactly (the Dequantizer arithmetic, as the device
-// dequant kernels do) while they are staged into LDS. Two matrix-core forms multiply them with the
-// f32 activations:
-//  - fp16 (launch_pf_gemm with xh): each token row of X scaled by a power of two so that its largest
-//    magnitude lies in [2^14, 2^15), each weight matrix likewise (pf_wexp), and every value split
-//    into hi = fp16(v) and lo = fp16(v - hi), 22 significant bits together. A product is
-//    hi_x hi_w + hi_x lo_w + lo_x hi_w (v_mfma_f32_16x16x32_f16, exact fp16 products summed in f32),
-//    within 2^-21 of the f32 product (the dropped lo_x lo_w and the two splits' roundings); the
-//    scales are undone exactly in the epilogue. Three fp16 products cost 3/16 of one f32 product
-//    on MI355X's matrix cores.
-//  - f32 (xh null): v_mfma_f32_16x16x4f32 on the f32 values, the products of the reference's F32
-//    path summed in f32 in the matrix core's order.
+// GEMM numerics: fp16 matrix cores (v_mfma_f32_16x16x32_f16, exact fp16 products summed in f32) on
+// operands of 22 significant bits. launch_pf_split scales each token row of X by a power of two so
+// that its largest magnitude lies in [2^14, 2^15) and writes hi = fp16(x) and lo = fp16(x - hi); the
+// epilogues undo the scale exactly. The weights enter in one of three forms:
+//  - Q4_K (pf_gemm_tile_q4k): sc q, an integer below 2048, exact in fp16; two products per weight,
+//    each 256-element block's sum scaled by its d in f32 and its min term one more product;
+//  - Q6_K (pf_gemm_tile_q6k): sc q as exact hi / lo fp16 integers; three products, d per block;
+//  - the other types (pf_gemm_tile_h): dequantized exactly (the Dequantizer arithmetic), scaled by
+//    a per-matrix power of two (pf_wexp) and split hi / lo; hi_x hi_w + hi_x lo_w + lo_x hi_w,
+//    within 2^-21 of the f32 product.
 #include "prefill.hpp"
 #include "deq.hpp"
 #include "gemv.hpp"
@@ -356,116 +354,9 @@ template <> struct PfW<PF_ROWS + FLLM_TYPE_BF16> {
 
 // ---- GEMM ---------------------------------------------------------------------------------------
 // Workgroup tile: BM tokens (128 or 64) x 128 weight rows, 4 waves in a 2 x 2 arrangement, each
-// (BM / 2) x 64 (BM / 32 x 4 MFMA tiles of 16 x 16). Per K step of 64 the workgroup stages X
-// (copied) and W (dequantized, one 32-weight group per thread) into LDS as f32 rows. The K step is
-// 4 blocks of 16; within a block, MFMA slice s (K = 4) takes from lane l the k index 4 (l >> 4) + s,
-// so a lane reads its 4 slices' values as one 16-byte LDS load (the same permutation of k for A and
-// B leaves the sum unchanged). MFMA 16x16x4 f32: lane l holds A row (l & 15) and B column (l & 15);
-// D lane l holds rows 4 (l >> 4) .. + 3 of column l & 15.
+// (BM / 2) x 64 (BM / 32 x 4 MFMA tiles of 16 x 16). Per K step of 64 the workgroup stages X and the
+// decoded weights into LDS.
 constexpr int PF_BN = 128, PF_BK = 64;
-constexpr int PF_LDF = PF_BK + 4;  // LDS row stride in floats (16 bytes of padding per row)
-
-template <int BM>
-static constexpr size_t pf_gemm_lds() {
-    return sizeof(float) * (size_t)(BM + PF_BN) * PF_LDF;
-}
-
-// one 128-row column tile (rows n0.., tokens t0..) of segment sg
-template <int WT, int BM>
-__device__ __forceinline__ void pf_gemm_tile(const PfGemm& a, const PfSeg& sg, int n0, int t0, float* sx, float* sw) {
-    constexpr int WM = BM / 2;   // tokens per wave
-    constexpr int TI = WM / 16;  // MFMA tiles along the tokens
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    pf_f32x4 acc[TI][4];
-#pragma unroll
-    for (int i = 0; i < TI; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // this thread's share of a K step: X pieces c = tid + 256 i, and W group (row tid % 128, group
-    // tid / 128): neighbouring lanes store neighbouring rows (68-float stride, 4 banks apart), so
-    // the W tile goes into LDS without bank conflicts
-    constexpr int XP = BM * 16 / 256;
-    const int wrow = tid & (PF_BN - 1), wgrp = tid / PF_BN, wr = n0 + wrow;
-    const bool wlive = wr < sg.N;
-    using Raw = typename PfW<WT>::Raw;
-    float4 xr[XP];
-    Raw wraw;
-    auto fetch = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < XP; i++) {
-            const int c = tid + 256 * i, row = c >> 4, col = (c & 15) * 4, t = t0 + row, k = k0 + col;
-            xr[i] = (t < a.T && k < a.K) ? *(const float4*)(a.x + (size_t)t * a.ldx + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-        if (wlive && k0 + 32 * wgrp < a.K) PfW<WT>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
-    };
-    // this workgroup's part of K (the whole row unless the launch splits K)
-    const int kb = (int)blockIdx.z * a.kpart, ke = kb + a.kpart < a.K ? kb + a.kpart : a.K;
-    fetch(kb);
-    for (int k0 = kb; k0 < ke; k0 += PF_BK) {
-        __syncthreads();  // the previous step's operands have been read
-#pragma unroll
-        for (int i = 0; i < XP; i++) {
-            const int c = tid + 256 * i;
-            *(float4*)(sx + (c >> 4) * PF_LDF + (c & 15) * 4) = xr[i];
-        }
-        {
-            float v[32];
-            const int k = k0 + 32 * wgrp;
-            if (wlive && k < a.K) {
-                PfW<WT>::deq(wraw, sg.w, sg.type, a.K, wr, k, v);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 32; i++) v[i] = 0.0f;
-            }
-            float4* dst = (float4*)(sw + wrow * PF_LDF + 32 * wgrp);
-#pragma unroll
-            for (int i = 0; i < 8; i++) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-        }
-        // the next step's global loads fly while this step multiplies
-        if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < PF_BK; kk += 16) {
-            const int ko = kk + 4 * (lane >> 4);
-            float4 av[TI], bv[4];
-#pragma unroll
-            for (int i = 0; i < TI; i++) av[i] = *(const float4*)(sx + (WM * wm + 16 * i + (lane & 15)) * PF_LDF + ko);
-#pragma unroll
-            for (int j = 0; j < 4; j++) bv[j] = *(const float4*)(sw + (64 * wn + 16 * j + (lane & 15)) * PF_LDF + ko);
-#pragma unroll
-            for (int s = 0; s < 4; s++)
-#pragma unroll
-                for (int i = 0; i < TI; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const float as = s == 0 ? av[i].x : s == 1 ? av[i].y : s == 2 ? av[i].z : av[i].w;
-                        const float bs = s == 0 ? bv[j].x : s == 1 ? bv[j].y : s == 2 ? bv[j].z : bv[j].w;
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(as, bs, acc[i][j], 0, 0, 0);
-                    }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < TI; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int t = t0 + WM * wm + 16 * i + 4 * (lane >> 4) + e;
-                const int n = n0 + 64 * wn + 16 * j + (lane & 15);
-                if (t < a.T && n < sg.N) {
-                    if (blockIdx.z == 0) {
-                        float* p = sg.y + (size_t)t * sg.ldy + n;
-                        *p = a.add ? *p + acc[i][j][e] : acc[i][j][e];
-                    } else {
-                        // K part z > 0: its slice of the scratch, at y's place in the shared rows
-                        const size_t col = (size_t)(sg.y - a.seg[0].y);
-                        a.part[(size_t)(blockIdx.z - 1) * a.T * sg.ldy + (size_t)t * sg.ldy + col + n] = acc[i][j][e];
-                    }
-                }
-            }
-}
 
 // workgroup (x, y): column tile x of the launch's segments, token tile y
 __device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
@@ -1209,47 +1100,6 @@ __global__ __launch_bounds__(256) void k_pf_split_add(float* __restrict__ y, con
 }
 
 
-// tile-interleaved Q4_K / Q6_K segments
-template <int BM>
-__global__ __launch_bounds__(256) void k_pf_gemm_tiles(const PfGemm a) {
-    extern __shared__ __attribute__((aligned(16))) float pf_lds[];
-    int bx = blockIdx.x;
-    const int si = pf_seg_of(a, bx);
-    const PfSeg& sg = a.seg[si];
-    if (sg.type == FLLM_TYPE_Q6_K)
-        pf_gemm_tile<FLLM_TYPE_Q6_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
-    else if (sg.type == FLLM_TYPE_Q8_0)
-        pf_gemm_tile<FLLM_TYPE_Q8_0, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
-    else if (sg.type == FLLM_TYPE_Q5_K)
-        pf_gemm_tile<FLLM_TYPE_Q5_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
-    else
-        pf_gemm_tile<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
-}
-
-// GGUF-row segments, all of type RT - PF_ROWS (RT = -1: any type, element-wise)
-template <int BM, int RT>
-__global__ __launch_bounds__(256) void k_pf_gemm_rows(const PfGemm a) {
-    extern __shared__ __attribute__((aligned(16))) float pf_lds[];
-    int bx = blockIdx.x;
-    const int si = pf_seg_of(a, bx);
-    pf_gemm_tile<RT, BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_lds, pf_lds + BM * PF_LDF);
-}
-
-template <int BM>
-static PfGemmKernel pf_rows_kernel(int type) {
-    switch (type) {
-        case FLLM_TYPE_Q8_0: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q8_0>;
-        case FLLM_TYPE_Q4_0: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q4_0>;
-        case FLLM_TYPE_Q4_K: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q4_K>;
-        case FLLM_TYPE_Q5_K: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q5_K>;
-        case FLLM_TYPE_Q6_K: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_Q6_K>;
-        case FLLM_TYPE_F32: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_F32>;
-        case FLLM_TYPE_F16: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_F16>;
-        case FLLM_TYPE_BF16: return k_pf_gemm_rows<BM, PF_ROWS + FLLM_TYPE_BF16>;
-        default: return k_pf_gemm_rows<BM, -1>;
-    }
-}
-
 template <int BM>
 static PfGemmKernel pf_rows_kernel_h(int type) {
     switch (type) {
@@ -1315,9 +1165,7 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
             lds = tall ? pf_gemm_lds_h<128>() : pf_gemm_lds_h<64>();
         }
     } else {
-        if (tiles) k = tall ? k_pf_gemm_tiles<128> : k_pf_gemm_tiles<64>;
-        else k = tall ? pf_rows_kernel<128>(a.seg[0].type) : pf_rows_kernel<64>(a.seg[0].type);
-        lds = tall ? pf_gemm_lds<128>() : pf_gemm_lds<64>();
+        return hipErrorInvalidValue;  // the fp16 planes are required
     }
     hipError_t e = pf_lds_attr((const void*)k, lds);
     if (e != hipSuccess) return e;

@@ -1,15 +1,17 @@
 // prefill.hpp — launch interface of the batched prefill kernels (prefill.hip): the prompt's
-// tokens pass through each layer together, the projections as f32 matrix-core GEMMs.
+// tokens pass through each layer together, the projections as fp16 matrix-core GEMMs on 22-bit
+// operand splits.
 #pragma once
 
 #include "kernels.hpp"
 
 namespace fllm {
 
-// Y[t][n] (+)= sum_k X[t][k] W[n][k] for t < T, n < N, in f32 on the matrix cores, for up to three
-// matrices that share X (one launch: q, k, v or gate, up). X: f32 rows of stride ldx; each W in its
-// stored layout (LAYOUT_TILES Q4_K / Q6_K, or GGUF rows of any supported type), dequantized exactly
-// in the kernel; all segments of a launch are tile-interleaved or none is. K is a multiple of 32.
+// Y[t][n] (+)= sum_k X[t][k] W[n][k] for t < T, n < N on the fp16 matrix cores, for up to three
+// matrices that share X (one launch: q, k, v or gate, up). X: f32 rows of stride ldx, read by the
+// kernels as the fp16 planes launch_pf_split wrote (xh, required); each W in its stored layout
+// (LAYOUT_TILES Q4_K / Q5_K / Q6_K / Q8_0, or GGUF rows of any supported type), decoded exactly in
+// the kernel; all segments of a launch are tile-interleaved or none is. K is a multiple of 32.
 struct PfSeg {
     const uint8_t* w;
     int type, layout;
@@ -34,9 +36,8 @@ struct PfGemm {
     float* part;
     size_t part_cap;
     int nsplit, kpart;
-    // fp16 matrix cores: X as written by launch_pf_split (two fp16 planes of row stride ldh, each
-    // token row scaled by a power of two) and xs[t], the factor that undoes that scale; the weights
-    // are split the same way in the kernel. Null xh: f32 matrix cores on x.
+    // X as written by launch_pf_split (two fp16 planes of row stride ldh, each token row scaled by a
+    // power of two, then the group-sum planes) and xs[t], the factor that undoes that scale
     const _Float16* xh;
     int ldh;
     const float* xs;
