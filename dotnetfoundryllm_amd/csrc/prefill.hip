@@ -552,7 +552,28 @@ __device__ __forceinline__ void pf_q4_pairs(uint32_t x, pf_hv2 sc2, uint32_t* ou
     }
 }
 
-template <int BM>
+// Q5_K: the same for 5-bit codes (sc q <= 63 * 31 < 2048, still exact). The group's regrouped
+// high-bit dword h holds element 16 hf + 4 by + j at bit 8 by + 4 hf + j: the pair (2 b, 2 b + 1)
+// of qs dword u has its high bits at bits p, p + 1 of the half (u & 1) of h, p = 8 (b >> 1) +
+// 4 (u >> 1) + 2 (b & 1) < 15. With z = h16 | h16 << 15 for that 16-bit half, (z >> p) puts them at
+// bits 0 and 16.
+template <int U>
+__device__ __forceinline__ void pf_q5_pairs(uint32_t x, uint32_t z, pf_hv2 sc2, uint32_t* out) {
+    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+    const pf_hv2 nb = sc2 * pf_hv2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + b) << 16) | (uint32_t)b;
+        const int pos = 8 * (b >> 1) + 4 * (U >> 1) + 2 * (b & 1);
+        const uint32_t t = (pos >= 4 ? (z >> (pos - 4)) : (z << (4 - pos))) & 0x00100010u;
+        const uint32_t p = __builtin_amdgcn_perm(hi, lo, sel) | t | 0x64006400u;
+        const pf_hv2 v = __builtin_elementwise_fma(__builtin_bit_cast(pf_hv2, p), sc2, nb);
+        out[b] = __builtin_bit_cast(uint32_t, v);
+    }
+}
+
+// WT: FLLM_TYPE_Q4_K or FLLM_TYPE_Q5_K (same header, scales and block structure)
+template <int BM, int WT = FLLM_TYPE_Q4_K>
 __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& sg, int n0, int t0, _Float16* lds) {
     constexpr int WM = BM / 2, TI = WM / 16;
     _Float16* sx = lds;                                    // [2][BM][PF_LDH]
@@ -577,7 +598,7 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
     const bool wlive = wr < sg.N;
     // block-start extras: token row (tid >> 1) of the min-term slice, its hi (tid even) or lo group sums
     const int vt = tid >> 1, vhl = tid & 1;
-    using Raw = typename PfW<FLLM_TYPE_Q4_K>::Raw;
+    using Raw = typename PfW<WT>::Raw;
     uint4 xr[XP], xv = make_uint4(0u, 0u, 0u, 0u);
     Raw wraw;
     // a tile of BM whole token rows (uniform over the workgroup) loads without the row test
@@ -601,7 +622,7 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
             const int t = t0 + vt;
             xv = t < a.T ? *(const uint4*)(xg + vhl * gplane + (size_t)t * G + (k0 >> 5)) : make_uint4(0u, 0u, 0u, 0u);
         }
-        if (wlive) PfW<FLLM_TYPE_Q4_K>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
+        if (wlive) PfW<WT>::load(wraw, sg.w, a.K, wr, k0 + 32 * wgrp);
     };
     // whole 256-element blocks (K and the split parts are multiples of 256): four K steps per block,
     // the block's end straight-line after them, so the accumulators stay in place across steps
@@ -625,10 +646,19 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
                     PfW<FLLM_TYPE_Q4_K>::scale_min(wraw.hdr, g, sc, mn);
                     const _Float16 sch = (_Float16)(float)sc;
                     const pf_hv2 sc2 = {sch, sch};
-                    pf_q4_pairs(wraw.qs.x, sc2, out);
-                    pf_q4_pairs(wraw.qs.y, sc2, out + 4);
-                    pf_q4_pairs(wraw.qs.z, sc2, out + 8);
-                    pf_q4_pairs(wraw.qs.w, sc2, out + 12);
+                    if constexpr (WT == FLLM_TYPE_Q5_K) {
+                        const uint32_t h0 = wraw.h & 0xFFFFu, h1 = wraw.h >> 16;
+                        const uint32_t z0 = h0 | (h0 << 15), z1 = h1 | (h1 << 15);
+                        pf_q5_pairs<0>(wraw.qs.x, z0, sc2, out);
+                        pf_q5_pairs<1>(wraw.qs.y, z1, sc2, out + 4);
+                        pf_q5_pairs<2>(wraw.qs.z, z0, sc2, out + 8);
+                        pf_q5_pairs<3>(wraw.qs.w, z1, sc2, out + 12);
+                    } else {
+                        pf_q4_pairs(wraw.qs.x, sc2, out);
+                        pf_q4_pairs(wraw.qs.y, sc2, out + 4);
+                        pf_q4_pairs(wraw.qs.z, sc2, out + 8);
+                        pf_q4_pairs(wraw.qs.w, sc2, out + 12);
+                    }
                 } else {
 #pragma unroll
                     for (int i = 0; i < 16; i++) out[i] = 0u;
@@ -963,6 +993,15 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tiles_h(const PfGemm a) {
         pf_gemm_tile_h<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ldh, sw);
 }
 
+// launches whose segments are all tile-interleaved Q5_K
+template <int BM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1))) void k_pf_gemm_q5k(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_ld5[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    pf_gemm_tile_q4k<BM, FLLM_TYPE_Q5_K>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_ld5);
+}
+
 // launches whose segments are all tile-interleaved Q4_K
 template <int BM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1))) void k_pf_gemm_q4k(const PfGemm a) {
@@ -1145,13 +1184,17 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         if (a.ldh < a.K || a.ldh % 8 != 0 || a.xs == nullptr) return hipErrorInvalidValue;
         bool all_q4k = tiles;
         for (int i = 0; i < a.nseg; i++) all_q4k = all_q4k && a.seg[i].type == FLLM_TYPE_Q4_K;
-        bool all_q6k = tiles, q46 = tiles;
+        bool all_q6k = tiles, all_q5k = tiles, q46 = tiles;
         for (int i = 0; i < a.nseg; i++) {
             all_q6k = all_q6k && a.seg[i].type == FLLM_TYPE_Q6_K;
+            all_q5k = all_q5k && a.seg[i].type == FLLM_TYPE_Q5_K;
             q46 = q46 && (a.seg[i].type == FLLM_TYPE_Q4_K || a.seg[i].type == FLLM_TYPE_Q6_K);
         }
         if (all_q4k) {
             k = tall ? k_pf_gemm_q4k<128> : k_pf_gemm_q4k<64>;
+            lds = tall ? pf_gemm_lds_k<128>() : pf_gemm_lds_k<64>();
+        } else if (all_q5k) {
+            k = tall ? k_pf_gemm_q5k<128> : k_pf_gemm_q5k<64>;
             lds = tall ? pf_gemm_lds_k<128>() : pf_gemm_lds_k<64>();
         } else if (all_q6k) {
             k = tall ? k_pf_gemm_q6k<128> : k_pf_gemm_q6k<64>;
