@@ -372,6 +372,7 @@ __device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
 // LDS rows of PF_BK halves plus 16 bytes; X and W as [plane][row][k] with plane 0 = hi, 1 = lo.
 constexpr int PF_LDH = PF_BK + 8;
 typedef _Float16 pf_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pf_hv2 __attribute__((ext_vector_type(2)));
 
 template <int BM>
 static constexpr size_t pf_gemm_lds_h() {
@@ -440,7 +441,41 @@ __device__ __forceinline__ void pf_gemm_tile_h(const PfGemm& a, const PfSeg& sg,
             const int c = tid + 256 * i, pl = c / (8 * BM), rem = c % (8 * BM);
             *(uint4*)(sx + ((size_t)pl * BM + (rem >> 3)) * PF_LDH + (rem & 7) * 8) = xr[i];
         }
-        {
+        if constexpr (WT == FLLM_TYPE_Q8_0) {
+            // d' q with d' = d 2^-wexp (fp16) and q the int8 code: q exact in fp16 (its byte as
+            // 0x64 80 ^ byte = 1024 + 128 + q, minus 1152), hi = d' q rounded once, lo = d' q - hi from
+            // one fma, exact (d' q needs at most 18 significant bits). Element 16 hh + 4 by + j is
+            // byte by of dword j of half hh, so a pair (e, e + 1) takes byte by of dwords j and j + 1.
+            const int k = k0 + 32 * wgrp;
+            uint32_t hv[16], lv[16];
+            if (wlive && k < a.K) {
+                const int g = (k >> 5) & 7;
+                const _Float16 dh = (_Float16)(half_exact(g < 4 ? (wraw.d & 0xFFFFu) : (wraw.d >> 16)) * wsc);
+                const pf_hv2 d2 = {dh, dh}, off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+                const uint32_t wd[8] = {wraw.h0.x, wraw.h0.y, wraw.h0.z, wraw.h0.w, wraw.h1.x, wraw.h1.y, wraw.h1.z, wraw.h1.w};
+#pragma unroll
+                for (int pr = 0; pr < 16; pr++) {
+                    const int e = 2 * pr, hh = e >> 4, by = (e & 15) >> 2, j = e & 3;
+                    const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + by) << 16) | (uint32_t)by;
+                    const uint32_t p = __builtin_amdgcn_perm(wd[4 * hh + j + 1], wd[4 * hh + j], sel) ^ 0x64806480u;
+                    const pf_hv2 q = __builtin_bit_cast(pf_hv2, p) + off;
+                    const pf_hv2 vh = q * d2;
+                    const pf_hv2 vl = __builtin_elementwise_fma(q, d2, -vh);
+                    hv[pr] = __builtin_bit_cast(uint32_t, vh);
+                    lv[pr] = __builtin_bit_cast(uint32_t, vl);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) hv[i] = lv[i] = 0u;
+            }
+            _Float16* d0 = sw + (size_t)wrow * PF_LDH + 32 * wgrp;
+            _Float16* d1 = d0 + (size_t)PF_BN * PF_LDH;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                *(uint4*)(d0 + 8 * i) = make_uint4(hv[4 * i], hv[4 * i + 1], hv[4 * i + 2], hv[4 * i + 3]);
+                *(uint4*)(d1 + 8 * i) = make_uint4(lv[4 * i], lv[4 * i + 1], lv[4 * i + 2], lv[4 * i + 3]);
+            }
+        } else {
             float v[32];
             const int k = k0 + 32 * wgrp;
             if (wlive && k < a.K) {
@@ -534,7 +569,6 @@ static constexpr size_t pf_gemm_lds_k() {
     return sizeof(_Float16) * ((size_t)(2 * BM + PF_BN) * PF_LDH + (size_t)(BM + PF_BN) * PF_LDV) + sizeof(float) * PF_BN;
 }
 
-typedef _Float16 pf_hv2 __attribute__((ext_vector_type(2)));
 // sc q_i for the 8 elements of one qs dword (bytes b = 0..3: element 2 b the low nibble, 2 b + 1 the
 // high one), as 4 dwords of fp16 pairs: 1024 + q by setting the fp16 pattern 0x6400 | q, minus 1024,
 // times sc, all exact
