@@ -1445,14 +1445,52 @@ __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
     pf_f32x4 o[NT];
 #pragma unroll
     for (int i = 0; i < NT; i++) o[i] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // head dims up to 128: the next block's K / V rows are loaded into registers while this block
+    // multiplies (PF_AK * HD / 4 float4 pieces of each, NPC per thread); 256: staged block by block
+    constexpr bool PRE = HD <= 128;
+    constexpr int NPC = PF_AK * (HD / 4) / 256;
+    // (vectors rather than arrays of float4, which the compiler would keep in scratch memory)
+    typedef float pf_fv __attribute__((ext_vector_type(4 * (PRE ? NPC : 1))));
+    pf_fv pk, pv;
+    // piece c = thread + 256 i: key row c / (HD / 4), dims 4 (c % (HD / 4)) .. + 3
+    const int jrow = threadIdx.x / (HD / 4), d4 = (threadIdx.x % (HD / 4)) * 4;
+    if constexpr (PRE) {
+#pragma unroll
+        for (int i = 0; i < NPC; i++) {
+            const int j = jrow + i * (256 / (HD / 4)), key = kstart + j < kend ? kstart + j : kend;
+            const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
+            const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
+            pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
+            pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
+        }
+    }
     for (int kb = kstart; kb <= kend; kb += PF_AK) {
         __syncthreads();  // the previous block's rows have been read
-        for (int c = threadIdx.x; c < PF_AK * (HD / 4); c += 256) {
-            const int j = c / (HD / 4), d4 = (c % (HD / 4)) * 4;
-            const int key = kb + j < kend ? kb + j : kend;
-            const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
-            *(float4*)(sk + j * LD + d4) = *(const float4*)(a.kc + off);
-            *(float4*)(sv + j * LD + d4) = *(const float4*)(a.vc + off);
+        if constexpr (PRE) {
+#pragma unroll
+            for (int i = 0; i < NPC; i++) {
+                const int j = jrow + i * (256 / (HD / 4));
+                *(float4*)(sk + j * LD + d4) = make_float4(pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]);
+                *(float4*)(sv + j * LD + d4) = make_float4(pv[4 * i], pv[4 * i + 1], pv[4 * i + 2], pv[4 * i + 3]);
+            }
+            if (kb + PF_AK <= kend) {
+#pragma unroll
+                for (int i = 0; i < NPC; i++) {
+                    const int j = jrow + i * (256 / (HD / 4)), key = kb + PF_AK + j < kend ? kb + PF_AK + j : kend;
+                    const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
+                    const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
+                    pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
+                    pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
+                }
+            }
+        } else {
+            for (int c = threadIdx.x; c < PF_AK * (HD / 4); c += 256) {
+                const int j = c / (HD / 4), e4 = (c % (HD / 4)) * 4;
+                const int key = kb + j < kend ? kb + j : kend;
+                const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + e4;
+                *(float4*)(sk + j * LD + e4) = *(const float4*)(a.kc + off);
+                *(float4*)(sv + j * LD + e4) = *(const float4*)(a.vc + off);
+            }
         }
         __syncthreads();
         if (!wlive || kb > wpos_hi || kb + PF_AK - 1 < wws) continue;  // no key of the block for the wave
