@@ -1399,23 +1399,27 @@ hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w
 // ---- causal attention over the cache (ComputeAttention, LlamaForwardPass.cs:158-211 and the
 // Mistral / Qwen2 / Gemma2 variants) ----------------------------------------------------------------
 // Workgroup = (query head, block of 64 consecutive queries), wave w = queries 16 w .. + 15. Keys go in
-// blocks of 64 rows of the head's kv head, staged in LDS (K and V rows padded to HD + 4 floats). Per
+// blocks of 64 rows (32 for head_dim 256) of the head's kv head, staged in LDS (K and V rows padded to
+// HD + 4 floats); the next block's rows are loaded into registers while the current one multiplies. Per
 // block a wave forms the transposed scores S^T = K Q^T on the f32 matrix cores
 // (v_mfma_f32_16x16x4f32: lane l holds keys 16 t + 4 (l >> 4) + e of query l & 15), updates the running
 // max / sum per query (online softmax), and adds O^T += V^T P^T with P^T straight from the score
 // registers: a step's four keys are the four keys one lane holds, so V's rows are taken in that order.
 // The order of the terms inside the dot products and sums is a permutation of the reference's; every
 // product and sum is f32.
-constexpr int PF_AQ = 64, PF_AK = 64;
+constexpr int PF_AQ = 64;
+// key block: 64 positions (32 for head_dim 256, whose block-ahead registers would not fit)
+template <int HD> struct PfAk { static constexpr int v = HD <= 128 ? 64 : 32; };
 
 template <int HD>
 static constexpr size_t pf_attn_lds() {
-    return sizeof(float) * 2 * (size_t)PF_AK * (HD + 4);
+    return sizeof(float) * 2 * (size_t)PfAk<HD>::v * (HD + 4);
 }
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
     constexpr int LD = HD + 4, NU = HD / 16, NT = HD / 16;
+    constexpr int PF_AK = PfAk<HD>::v, KT = PF_AK / 16;  // key block and its 16-key MFMA tiles
     extern __shared__ float pa_lds[];
     float* sk = pa_lds;             // [PF_AK][LD]
     float* sv = sk + PF_AK * LD;    // [PF_AK][LD]
@@ -1445,62 +1449,49 @@ __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
     pf_f32x4 o[NT];
 #pragma unroll
     for (int i = 0; i < NT; i++) o[i] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // head dims up to 128: the next block's K / V rows are loaded into registers while this block
-    // multiplies (PF_AK * HD / 4 float4 pieces of each, NPC per thread); 256: staged block by block
-    constexpr bool PRE = HD <= 128;
+    // the next block's K / V rows are loaded into registers while this block multiplies
+    // (PF_AK * HD / 4 float4 pieces of each, NPC per thread; vectors rather than arrays of float4,
+    // which the compiler would keep in scratch memory)
     constexpr int NPC = PF_AK * (HD / 4) / 256;
-    // (vectors rather than arrays of float4, which the compiler would keep in scratch memory)
-    typedef float pf_fv __attribute__((ext_vector_type(4 * (PRE ? NPC : 1))));
+    typedef float pf_fv __attribute__((ext_vector_type(4 * NPC)));
     pf_fv pk, pv;
     // piece c = thread + 256 i: key row c / (HD / 4), dims 4 (c % (HD / 4)) .. + 3
     const int jrow = threadIdx.x / (HD / 4), d4 = (threadIdx.x % (HD / 4)) * 4;
-    if constexpr (PRE) {
 #pragma unroll
-        for (int i = 0; i < NPC; i++) {
-            const int j = jrow + i * (256 / (HD / 4)), key = kstart + j < kend ? kstart + j : kend;
-            const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
-            const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
-            pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
-            pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
-        }
+    for (int i = 0; i < NPC; i++) {
+        const int j = jrow + i * (256 / (HD / 4)), key = kstart + j < kend ? kstart + j : kend;
+        const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
+        const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
+        pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
+        pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
     }
     for (int kb = kstart; kb <= kend; kb += PF_AK) {
         __syncthreads();  // the previous block's rows have been read
-        if constexpr (PRE) {
+#pragma unroll
+        for (int i = 0; i < NPC; i++) {
+            const int j = jrow + i * (256 / (HD / 4));
+            *(float4*)(sk + j * LD + d4) = make_float4(pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]);
+            *(float4*)(sv + j * LD + d4) = make_float4(pv[4 * i], pv[4 * i + 1], pv[4 * i + 2], pv[4 * i + 3]);
+        }
+        if (kb + PF_AK <= kend) {
 #pragma unroll
             for (int i = 0; i < NPC; i++) {
-                const int j = jrow + i * (256 / (HD / 4));
-                *(float4*)(sk + j * LD + d4) = make_float4(pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]);
-                *(float4*)(sv + j * LD + d4) = make_float4(pv[4 * i], pv[4 * i + 1], pv[4 * i + 2], pv[4 * i + 3]);
-            }
-            if (kb + PF_AK <= kend) {
-#pragma unroll
-                for (int i = 0; i < NPC; i++) {
-                    const int j = jrow + i * (256 / (HD / 4)), key = kb + PF_AK + j < kend ? kb + PF_AK + j : kend;
-                    const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
-                    const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
-                    pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
-                    pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
-                }
-            }
-        } else {
-            for (int c = threadIdx.x; c < PF_AK * (HD / 4); c += 256) {
-                const int j = c / (HD / 4), e4 = (c % (HD / 4)) * 4;
-                const int key = kb + j < kend ? kb + j : kend;
-                const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + e4;
-                *(float4*)(sk + j * LD + e4) = *(const float4*)(a.kc + off);
-                *(float4*)(sv + j * LD + e4) = *(const float4*)(a.vc + off);
+                const int j = jrow + i * (256 / (HD / 4)), key = kb + PF_AK + j < kend ? kb + PF_AK + j : kend;
+                const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
+                const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
+                pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
+                pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
             }
         }
         __syncthreads();
         if (!wlive || kb > wpos_hi || kb + PF_AK - 1 < wws) continue;  // no key of the block for the wave
-        pf_f32x4 s[4];
+        pf_f32x4 s[KT];
 #pragma unroll
-        for (int t = 0; t < 4; t++) s[t] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < KT; t++) s[t] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int u = 0; u < NU; u++)
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
+            for (int t = 0; t < KT; t++) {
                 const float4 kr = *(const float4*)(sk + (16 * t + q16) * LD + 16 * u + 4 * kq);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.x, qr[u].x, s[t], 0, 0, 0);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.y, qr[u].y, s[t], 0, 0, 0);
@@ -1510,7 +1501,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
         // scores of keys kb + 16 t + 4 (l >> 4) + e for query l & 15
         float bmax = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < KT; t++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int key = kb + 16 * t + 4 * kq + e;
@@ -1526,7 +1517,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
         const float corr = m_new == -INFINITY ? 1.0f : expf(m - m_new);
         float psum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < KT; t++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float p = s[t][e] == -INFINITY ? 0.0f : expf(s[t][e] - m_new);
@@ -1542,7 +1533,7 @@ __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
 #pragma unroll
             for (int e = 0; e < 4; e++) o[i][e] *= corr;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < KT; t++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float* vr = sv + (16 * t + 4 * kq + e) * LD + 4 * q16;
