@@ -1141,6 +1141,21 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
     }
 }
 
+// The last N items of a workgroup (N < 2 RING, first item at a multiple of RING) as straight-line
+// code: the first N - RING refill, the rest do not. One instantiation per remainder keeps the
+// per-item refill choice a compile-time constant, as in the main loop (a runtime choice per item
+// keeps both variants' registers live).
+template <int T, int KC, bool IL, bool RAGGED, int N>
+__device__ __forceinline__ void mf_tail(const GemvArgs& a, const MfCtx& x, typename MfPick<T, IL>::Raw* ring, int i0,
+                                        float& y, uint32_t& offr, const uint8_t*& Wr, unsigned long long& best) {
+    constexpr int RING = MfRing<T, KC>::v;
+#pragma unroll
+    for (int r = 0; r < N; r++) {
+        if (r + RING < N) mf_item<T, KC, IL, true, RAGGED>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        else mf_item<T, KC, IL, false, RAGGED>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+    }
+}
+
 // TABIN: the input is an activation table (XIN_TAB); otherwise a vector, quantized here. The
 // workgroup is number wg of ng that share units [u0, u0 + nu) of the launch.
 // RAGGED: the row's NB chunks do not split evenly: the nw waves of KC chunks cover nw * KC >= NB,
@@ -1459,6 +1474,24 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
         for (int r = 0; r < U - RING; r++) mf_item<T, KC, IL, true, RAGGED>(a, x, ring, i0 + r, r, y, offr, Wr, best);
 #pragma unroll
         for (int r = U - RING; r < U; r++) mf_item<T, KC, IL, false, RAGGED>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+    } else if constexpr (KC == RING / 2) {
+        // U == RING items per iteration while the item RING ahead of each exists, then the last
+        // 0 .. U + RING - 1 items (a multiple of KC) as one straight-line tail
+        int i0 = 0;
+        for (; i0 + U + RING <= x.items; i0 += U) {
+            x.at = abase;
+            __asm__ volatile("" : "+v"(x.at));
+#pragma unroll
+            for (int r = 0; r < U; r++) mf_item<T, KC, IL, true, RAGGED>(a, x, ring, i0 + r, r, y, offr, Wr, best);
+        }
+        x.at = abase;
+        __asm__ volatile("" : "+v"(x.at));
+        switch (x.items - i0) {
+            case 2: mf_tail<T, KC, IL, RAGGED, 2>(a, x, ring, i0, y, offr, Wr, best); break;
+            case 4: mf_tail<T, KC, IL, RAGGED, 4>(a, x, ring, i0, y, offr, Wr, best); break;
+            case 6: mf_tail<T, KC, IL, RAGGED, 6>(a, x, ring, i0, y, offr, Wr, best); break;
+            default: break;
+        }
     } else {
         for (int i0 = 0; i0 < x.items; i0 += U) {
             x.at = abase;
@@ -1493,10 +1526,16 @@ __global__ __launch_bounds__(512) void k_gemv_mfma_mix(const GemvArgs a) {
                                                 (int)gridDim.x - a.mix_wg);
 }
 
-// waves per workgroup and chunks per wave (*kc) for rows of NB chunks: an even split over at most 8
-// waves of 1, 2, 4 or 8 chunks (4 preferred), else 8 chunks per wave over up to 10 waves with the
-// last one partly past the row (a ragged row, e.g. 74 chunks); 0: no split
+// waves per workgroup and chunks per wave (*kc) for rows of NB chunks: 10 or 14 chunks as 4 per
+// wave with the last wave partly past the row (a ragged row: 2 chunks per wave would leave one
+// workgroup of 5 or 7 waves per CU at its register count); else an even split over at most 8 waves
+// of 1, 2, 4 or 8 chunks (4 preferred), else 8 chunks per wave over up to 10 waves with the last one
+// partly past the row (e.g. 74 chunks); 0: no split
 static int mf_split(int NB, int* kc) {
+    if (NB == 10 || NB == 14) {
+        *kc = 4;
+        return (NB + 3) / 4;
+    }
     const int order[4] = {4, 8, 2, 1};
     for (int c : order)
         if (NB % c == 0 && NB / c <= 8) {
@@ -1525,10 +1564,10 @@ static bool mf_ragged(int NB) {
     return nw > 0 && nw * kc != NB;
 }
 
-// rows whose chunks do not split evenly over at most 8 waves: 8 chunks per wave, up to 10 waves
-template <int T, bool TABIN>
-__global__ __launch_bounds__(640) void k_gemv_mfma_r(const GemvArgs a) {
-    mfma_body<T, 8, TABIN, true, true>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
+// ragged rows (chunks that do not split evenly): KC chunks per wave, the last wave partly past the row
+template <int T, int KC, bool TABIN>
+__global__ __launch_bounds__(KC == 8 ? 640 : 512) void k_gemv_mfma_r(const GemvArgs a) {
+    mfma_body<T, KC, TABIN, true, true>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
 }
 
 typedef void (*MfKernel)(const GemvArgs);
@@ -1551,8 +1590,9 @@ static MfKernel mf_kernel_mix(int kc) {
     }
 }
 template <int T>
-static MfKernel mf_kernel_ragged(bool tab) {
-    return tab ? k_gemv_mfma_r<T, true> : k_gemv_mfma_r<T, false>;
+static MfKernel mf_kernel_ragged(bool tab, int kc) {
+    if (kc == 4) return tab ? k_gemv_mfma_r<T, 4, true> : k_gemv_mfma_r<T, 4, false>;
+    return tab ? k_gemv_mfma_r<T, 8, true> : k_gemv_mfma_r<T, 8, false>;
 }
 template <bool IL>
 static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
@@ -1560,10 +1600,10 @@ static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
     if constexpr (IL) {
         if (mf_ragged(a.G / 8)) {
             switch (a.seg[0].type) {
-                case FLLM_TYPE_Q4_K: return mf_kernel_ragged<FLLM_TYPE_Q4_K>(tab);
-                case FLLM_TYPE_Q6_K: return mf_kernel_ragged<FLLM_TYPE_Q6_K>(tab);
-                case FLLM_TYPE_Q8_0: return mf_kernel_ragged<FLLM_TYPE_Q8_0>(tab);
-                default: return mf_kernel_ragged<FLLM_TYPE_Q5_K>(tab);
+                case FLLM_TYPE_Q4_K: return mf_kernel_ragged<FLLM_TYPE_Q4_K>(tab, kc);
+                case FLLM_TYPE_Q6_K: return mf_kernel_ragged<FLLM_TYPE_Q6_K>(tab, kc);
+                case FLLM_TYPE_Q8_0: return mf_kernel_ragged<FLLM_TYPE_Q8_0>(tab, kc);
+                default: return mf_kernel_ragged<FLLM_TYPE_Q5_K>(tab, kc);
             }
         }
     }
@@ -1623,8 +1663,7 @@ bool gemv_fusable_cols(int64_t cols) { return cols % 32 == 0 && cols >= 32 && co
 static bool mfma_ok(const GemvArgs& a, int64_t cols) {
     const int NB = (int)(cols / 256);
     if (cols % 256 != 0 || mf_waves(NB) == 0) return false;
-    // ragged rows: tile-interleaved matrices of one type, no GLU
-    if (mf_ragged(NB) && a.glu) return false;
+    // ragged rows: tile-interleaved matrices of one type
     for (int i = 0; i < a.nseg; i++) {
         if (mf_ragged(NB) && (a.seg[i].layout != LAYOUT_TILES || a.seg[i].type != a.seg[0].type)) return false;
         const int t = a.seg[i].type;

@@ -103,10 +103,11 @@ def test_gemv_microbenchmark_shapes(ctx, t, shape):
 
 
 @pytest.mark.parametrize("t", [N.Q4_K, N.Q8_0, N.Q6_K, N.Q5_K])
-@pytest.mark.parametrize("shape", C1 + [(64, 18944), (16, 256)])
+@pytest.mark.parametrize("shape", C1 + [(64, 18944), (16, 256), (48, 3584), (32, 2560)])
 def test_gemv_tiles_layout(ctx, t, shape):
     """fllm_gemv_pack + fllm_gemv_ex(FLLM_LAYOUT_TILES) against the oracle's F32 dot (18944
-    columns: 74 chunks, the ragged wave split)."""
+    columns: 74 chunks, 8 per wave over 10 waves; 3584 and 2560 columns: 14 and 10 chunks, 4 per
+    wave with the last wave partly past the row)."""
     rows, cols = shape
     raw = synth(t, rows * cols, seed=5, tid=rows + 1)
     x = np.random.default_rng(5).standard_normal(cols).astype(np.float32)
