@@ -90,13 +90,32 @@ __device__ __forceinline__ void attn_pv(float4* acc, const float4& vr, int t, in
 
 // G = query heads per kv head. Rows of the chunk go in blocks of BLK = 4 rows per lane; the K and V
 // rows of the first two blocks are loaded together up front (row indices clamped to the chunk, so
-// every load is unconditional and all are in flight at once), later blocks in a loop.
+// every load is unconditional and all are in flight at once); later blocks (long chunks) stream
+// through a ring of two blocks loaded ahead of the one in use, K's during the first blocks' scores,
+// V's during the softmax.
 // K / V cache rows, read once per step: non-temporal, so that they do not displace the weights'
 // neighbours in L2 (activation tables, epilogue operands, code)
 typedef float kv_f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 kv_ld(const float* p) {
     const kv_f4 v = __builtin_nontemporal_load((const kv_f4*)p);
     return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// this lane's NP = 4 rows of the block at b0 (row indices clamped to the chunk) as one register
+// vector (a vector rather than an array of float4 keeps it out of scratch memory across the loops)
+typedef float kv_blk __attribute__((ext_vector_type(16)));
+template <int RPP>
+__device__ __forceinline__ kv_blk kv_ld_blk(const float* base, int b0, int r0, int len, int kvdim) {
+    kv_blk v;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const float4 t = kv_ld(base + (int64_t)min(b0 + r0 + u * RPP, len - 1) * kvdim);
+        v[4 * u] = t.x; v[4 * u + 1] = t.y; v[4 * u + 2] = t.z; v[4 * u + 3] = t.w;
+    }
+    return v;
+}
+__device__ __forceinline__ float4 kv_row(const kv_blk& v, int u) {
+    return make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]);
 }
 
 template <int HD, int G>
@@ -144,18 +163,40 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < NP; u++) vB[u] = kv_ld(vbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
 
+    static_assert(NP == 4, "kv_blk holds 4 rows");
+    // K of blocks 2 .. 2 + KR - 1 (then the next KR, ...). Past the chunk the rows clamp to its last
+    // one (re-read from cache; blocks wholly past it are not scored), so every load of the ring is
+    // unconditional and they complete in the order issued: a block waits only for its own loads.
+    constexpr int KR = 2;  // blocks in flight (4 measured slower for head_dim 256 at 6k positions)
+    kv_blk kn[KR];  // (read only when the ring was loaded: the loops run only when 2 BLK < len)
+    const bool ring = 2 * BLK < len;
+    if (ring) {
+#pragma unroll
+        for (int j = 0; j < KR; j++) kn[j] = kv_ld_blk<RPP>(kbase, (2 + j) * BLK, r0, len, a.kvdim);
+    }
+
     // ---- scores ---------------------------------------------------------------------------------
 #pragma unroll
     for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kA[u], r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
 #pragma unroll
     for (int u = 0; u < NP; u++)
         attn_scores<HD, G>(qv, kB[u], BLK + r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
-    for (int b0 = 2 * BLK; b0 < len; b0 += BLK) {
-        float4 kr[NP];
+    for (int b0 = 2 * BLK; b0 < len; b0 += KR * BLK) {
 #pragma unroll
-        for (int u = 0; u < NP; u++) kr[u] = kv_ld(kbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
+        for (int j = 0; j < KR; j++) {
+            if (b0 + j * BLK < len) {
 #pragma unroll
-        for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kr[u], b0 + r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
+                for (int u = 0; u < NP; u++)
+                    attn_scores<HD, G>(qv, kv_row(kn[j], u), b0 + j * BLK + r0 + u * RPP, len, dl, sc, ch, a.scale,
+                                       a.softcap, inv_cap);
+            }
+            kn[j] = kv_ld_blk<RPP>(kbase, b0 + (j + KR) * BLK, r0, len, a.kvdim);
+        }
+    }
+    kv_blk vn[KR];  // V of blocks 2 .. 2 + KR - 1, in flight during the softmax
+    if (ring) {
+#pragma unroll
+        for (int j = 0; j < KR; j++) vn[j] = kv_ld_blk<RPP>(vbase, (2 + j) * BLK, r0, len, a.kvdim);
     }
     __syncthreads();
 
@@ -183,12 +224,15 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     for (int u = 0; u < NP; u++) attn_pv<G>(acc, vA[u], r0 + u * RPP, len, sc, ch);
 #pragma unroll
     for (int u = 0; u < NP; u++) attn_pv<G>(acc, vB[u], BLK + r0 + u * RPP, len, sc, ch);
-    for (int b0 = 2 * BLK; b0 < len; b0 += BLK) {
-        float4 vr[NP];
+    for (int b0 = 2 * BLK; b0 < len; b0 += KR * BLK) {
 #pragma unroll
-        for (int u = 0; u < NP; u++) vr[u] = kv_ld(vbase + (int64_t)min(b0 + r0 + u * RPP, len - 1) * a.kvdim);
+        for (int j = 0; j < KR; j++) {
+            if (b0 + j * BLK < len) {
 #pragma unroll
-        for (int u = 0; u < NP; u++) attn_pv<G>(acc, vr[u], b0 + r0 + u * RPP, len, sc, ch);
+                for (int u = 0; u < NP; u++) attn_pv<G>(acc, kv_row(vn[j], u), b0 + j * BLK + r0 + u * RPP, len, sc, ch);
+            }
+            vn[j] = kv_ld_blk<RPP>(vbase, b0 + (j + KR) * BLK, r0, len, a.kvdim);
+        }
     }
     // every (wave, row slot) leaves its partial sums in LDS; 4 * RPL slots are then summed
 #pragma unroll
