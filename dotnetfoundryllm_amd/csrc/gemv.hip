@@ -761,6 +761,33 @@ __device__ __forceinline__ void atab_write(lds_tab* atab, int b, int g, const fl
     *st = make_float4(sc[0], sc[1], sm[0], sm[1]);
 }
 
+// One thread: the digit entries of half h of group g (0..7) of chunk b from its 16 values (the
+// arithmetic of atab_write for one half); returns the half's scale and sum.
+__device__ __forceinline__ void atab_write_half(lds_tab* atab, int b, int g, int h, const float* v, float& sc,
+                                                float& sm) {
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) { sum += v[i]; amax = fmaxf(amax, fabsf(v[i])); }
+    float inv;
+    half_scale(amax, sc, inv);
+    sm = sum;
+    uint32_t w[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        int b2, b1, b0;
+        digits3(quant_x(v[e], inv), b2, b1, b0);
+        const int j = e & 3, sh = 8 * (e >> 2);
+        w[0][j] |= (uint32_t)(b2 & 0xFF) << sh;
+        w[1][j] |= (uint32_t)(b1 & 0xFF) << sh;
+        w[2][j] |= (uint32_t)(b0 & 0xFF) << sh;
+    }
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+        u32x4 e4 = {w[d][0], w[d][1], w[d][2], w[d][3]};
+        atab[atab_index(b, 2 * (g >> 2) + h, g & 3, d)] = e4;
+    }
+}
+
 // Producer side of the table, for a consumer whose columns are this launch's rows: lanes 0..15 of
 // the calling wave hold v for rows row_base .. row_base + 15 (one half of a group; other lanes hold
 // 0) and sq, the square of the raw output for the consumer's RMSNorm. Writes the half's three
@@ -1293,6 +1320,73 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             float tot = 0.0f;
             for (int i = 0; i < x.nw; i++) tot += x.red[i];
             x.xs = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
+        }
+    } else if (a.xin == XIN_POST && 2 * a.G <= x.nw * 64) {
+        // Gemma-2 post-norm folded in (Gemma2ForwardPass.cs:90-96), two threads per 32-element
+        // group (one per 16-element half, the table's quantization unit): x2, x, post_w and the
+        // norm weight all load at once and stay in registers across the two reductions. The new
+        // residual is x + (x2 * rms(x2)) * (post_w + 1), the operation order of the separate
+        // post-norm kernel, then normalized as XIN_NORM.
+        const int g = (int)threadIdx.x >> 1, hh = (int)threadIdx.x & 1;
+        const bool live = g < a.G;
+        const int e0 = g * 32 + 16 * hh;
+        float t2[16], xv[16], pw[16], wv[16];
+        float ss = 0.0f;
+        if (live) {
+            const float4* ti = (const float4*)(a.x2 + e0);
+            const float4* xi = (const float4*)(a.x + e0);
+            const float4* pi = (const float4*)(a.post_w + e0);
+            const float4* wi = (const float4*)(a.norm_w + e0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 t = ti[i], u = xi[i], p4 = pi[i], w4 = wi[i];
+                t2[4 * i] = t.x; t2[4 * i + 1] = t.y; t2[4 * i + 2] = t.z; t2[4 * i + 3] = t.w;
+                xv[4 * i] = u.x; xv[4 * i + 1] = u.y; xv[4 * i + 2] = u.z; xv[4 * i + 3] = u.w;
+                pw[4 * i] = p4.x; pw[4 * i + 1] = p4.y; pw[4 * i + 2] = p4.z; pw[4 * i + 3] = p4.w;
+                wv[4 * i] = w4.x; wv[4 * i + 1] = w4.y; wv[4 * i + 2] = w4.z; wv[4 * i + 3] = w4.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) ss = fmaf(t2[i], t2[i], ss);
+        }
+        ss = wsum(ss);
+        if (x.lane == 0) x.red[x.wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < x.nw; i++) tot += x.red[i];
+        const float prms = 1.0f / sqrtf(tot / (float)(a.G * 32) + 1e-6f);
+        __syncthreads();  // x.red is reused below
+        float ssq = 0.0f;
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) xv[i] = xv[i] + (t2[i] * prms) * (pw[i] + 1.0f);
+#pragma unroll
+            for (int i = 0; i < 16; i++) ssq = fmaf(xv[i], xv[i], ssq);
+        }
+        ssq = wsum(ssq);
+        if (x.lane == 0) x.red[x.wave] = ssq;
+        __syncthreads();
+        tot = 0.0f;
+        for (int i = 0; i < x.nw; i++) tot += x.red[i];
+        const float scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
+        float hsc = 0.0f, hsm = 0.0f;
+        if (live) {
+            if (blockIdx.x == 0) {
+                float4* xo = (float4*)(a.x_out + e0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) xo[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float t = xv[i] * scale;
+                xv[i] = a.norm_kind ? t * (wv[i] + 1.0f) : t * wv[i];
+            }
+            atab_write_half(atab, g >> 3, g & 7, hh, xv, hsc, hsm);
+        }
+        // the group's stats {scale of half 0, of half 1, sum of half 0, of half 1} from the pair
+        const float osc = __shfl_xor(hsc, 1), osm = __shfl_xor(hsm, 1);
+        if (live && hh == 0) {
+            const f32x4 stv = {hsc, osc, hsm, osm};
+            x.stats[(g >> 3) * 8 + (g & 7)] = stv;
         }
     } else if (a.xin == XIN_POST && a.G <= x.nw * 64) {
         // Gemma-2 post-norm folded in (Gemma2ForwardPass.cs:90-96), one 32-element group per
