@@ -54,10 +54,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // dot of q with the K row slice kr for every head of the group, reduced over the row's lanes; the
-// row's last lane stores the scaled (and capped) score of row t
+// row's last lane stores the raw dot of row t (scale and softcap come in the softmax pass, one score
+// per lane, rather than here with one lane of the wave active)
 template <int HD, int G>
 __device__ __forceinline__ void attn_scores(const float4* qv, const float4& kr, int t, int len, int dl, float* sc,
-                                            int ch, float scale, float softcap, float inv_cap) {
+                                            int ch) {
     constexpr int LPR = HD / 4;
 #pragma unroll
     for (int h = 0; h < G; h++) {
@@ -66,11 +67,7 @@ __device__ __forceinline__ void attn_scores(const float4* qv, const float4& kr, 
         s = fmaf(qv[h].z, kr.z, s);
         s = fmaf(qv[h].w, kr.w, s);
         s = group_sum<LPR>(s);
-        if (dl == LPR - 1 && t < len) {
-            s = s * scale;
-            if (softcap > 0.0f) s = tanhf(s * inv_cap) * softcap;
-            sc[h * ch + t] = s;
-        }
+        if (dl == LPR - 1 && t < len) sc[h * ch + t] = s;
     }
 }
 
@@ -177,18 +174,17 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
 
     // ---- scores ---------------------------------------------------------------------------------
 #pragma unroll
-    for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kA[u], r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
+    for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kA[u], r0 + u * RPP, len, dl, sc, ch);
 #pragma unroll
     for (int u = 0; u < NP; u++)
-        attn_scores<HD, G>(qv, kB[u], BLK + r0 + u * RPP, len, dl, sc, ch, a.scale, a.softcap, inv_cap);
+        attn_scores<HD, G>(qv, kB[u], BLK + r0 + u * RPP, len, dl, sc, ch);
     for (int b0 = 2 * BLK; b0 < len; b0 += KR * BLK) {
 #pragma unroll
         for (int j = 0; j < KR; j++) {
             if (b0 + j * BLK < len) {
 #pragma unroll
                 for (int u = 0; u < NP; u++)
-                    attn_scores<HD, G>(qv, kv_row(kn[j], u), b0 + j * BLK + r0 + u * RPP, len, dl, sc, ch, a.scale,
-                                       a.softcap, inv_cap);
+                    attn_scores<HD, G>(qv, kv_row(kn[j], u), b0 + j * BLK + r0 + u * RPP, len, dl, sc, ch);
             }
             kn[j] = kv_ld_blk<RPP>(kbase, b0 + (j + KR) * BLK, r0, len, a.kvdim);
         }
@@ -200,10 +196,15 @@ __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- softmax pieces per head: max, exp(s - max), sum -----------------------------------
+    // ---- softmax pieces per head: scores (scale, softcap), max, exp(s - max), sum ------------
     for (int h = wave; h < G; h += 4) {
         float m = -INFINITY;
-        for (int t = lane; t < len; t += 64) m = fmaxf(m, sc[h * ch + t]);
+        for (int t = lane; t < len; t += 64) {
+            float v = sc[h * ch + t] * a.scale;
+            if (a.softcap > 0.0f) v = tanhf(v * inv_cap) * a.softcap;
+            sc[h * ch + t] = v;
+            m = fmaxf(m, v);
+        }
         m = wave_max(m);
         float l = 0.0f;
         for (int t = lane; t < len; t += 64) {
