@@ -334,70 +334,92 @@ __global__ __launch_bounds__(64) void k_attn_merge_fast(const AttnArgs a) {
     if (a.tab_out) merge_emit_table<HD>(a, h, lane, res);
 }
 
-// out[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M) over the chunks of head h. One wave per
-// head: lane k holds chunk k's (m, l) (chunks are at most 256), the weights go through LDS, and
-// every lane then sums its float4 slices of the chunk outputs with all loads of a pass in flight.
+// out[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M) over the chunks of head h, for more chunks
+// than the one-wave merge holds (up to 256). Four waves per head: thread t holds chunk t's (m, l);
+// the chunk outputs are read as NS = 4 * 64 / (HD / 4) streams (HD / 4 lanes per chunk slice), each
+// lane loading its stream's slices of NB chunks at once, beside the (m, l) and step reads, so the
+// launch waits about one memory round trip. The streams' sums are added in stream order in LDS.
 template <int HD>
-__global__ __launch_bounds__(64) void k_attn_merge(const AttnArgs a) {
-    __shared__ float wts[256];
-    __shared__ float s_inv;
-    const int h = blockIdx.x, lane = threadIdx.x;
-    const int nchunks = attn_range(a.params->pos, a.window, a.nc).nchunks;
-    const float* pml = a.part_ml + (int64_t)h * a.nc * 2;
-    float mk[4], lk[4];
-    float M = -INFINITY;
+__global__ __launch_bounds__(256) void k_attn_merge_wide(const AttnArgs a) {
+    constexpr int LPC = HD / 4;   // lanes per chunk slice
+    constexpr int S = 64 / LPC;   // chunk streams per wave
+    constexpr int NS = 4 * S;     // chunk streams per workgroup
+    constexpr int NB = 16;        // chunks per stream in flight
+    __shared__ float wts[ATTN_MAX_CHUNKS];
+    __shared__ float red[8];
+    __shared__ float4 ored[NS][LPC];
+    const int h = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int stream = wave * S + lane / LPC, d4 = lane % LPC;
+    const int nc = a.nc;
+    const float2 ml = *(const float2*)(a.part_ml + ((int64_t)h * nc + (t < nc ? t : nc - 1)) * 2);
+    const float* po = a.part_o + (int64_t)h * nc * HD + d4 * 4;
+    // unconditional loads (chunk indices clamped) so that all of them are in flight at once
+    float4 p[NB];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int k = lane + 64 * i;
-        mk[i] = k < nchunks ? pml[2 * k] : -INFINITY;
-        lk[i] = k < nchunks ? pml[2 * k + 1] : 0.0f;
-        M = fmaxf(M, mk[i]);
+    for (int u = 0; u < NB; u++) {
+        const int k = stream + u * NS;
+        p[u] = *(const float4*)(po + (int64_t)(k < nc ? k : nc - 1) * HD);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    float L = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int k = lane + 64 * i;
-        float w = k < nchunks ? expf(mk[i] - M) : 0.0f;
-        if (k < 256) wts[k] = w;
-        L = fmaf(lk[i], w, L);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
-    if (lane == 0) s_inv = 1.0f / L;
+    const int nchunks = attn_range(a.params->pos, a.window, nc).nchunks;
+    // slots from nchunks on hold no partial of this step (possibly never-written memory): skipped,
+    // not weighted by zero
+    const bool valid = t < nchunks;
+    float m = wave_max(valid ? ml.x : -INFINITY);
+    if (lane == 0) red[wave] = m;
     __syncthreads();
-    const float inv = s_inv;
-    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's output slice (HD / 4 <= 64 lanes)
-    for (int d4 = lane; d4 < HD / 4; d4 += 64) {
-        const float* po = a.part_o + (int64_t)h * a.nc * HD + d4 * 4;
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        int k = 0;
-        for (; k + 8 <= nchunks; k += 8) {
-            float4 p[8];
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float w = valid ? expf(ml.x - M) : 0.0f;
+    wts[t] = w;
+    const float lw = wave_sum(valid ? ml.y * w : 0.0f);
+    if (lane == 0) red[4 + wave] = lw;
+    __syncthreads();
+    const float L = (red[4] + red[5]) + (red[6] + red[7]);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int u = 0; u < 8; u++) p[u] = *(const float4*)(po + (int64_t)(k + u) * HD);
+    for (int u = 0; u < NB; u++) {
+        const int k = stream + u * NS;
+        if (k < nchunks) {
+            const float wk = wts[k];
+            o.x = fmaf(p[u].x, wk, o.x);
+            o.y = fmaf(p[u].y, wk, o.y);
+            o.z = fmaf(p[u].z, wk, o.z);
+            o.w = fmaf(p[u].w, wk, o.w);
+        }
+    }
+    for (int k0 = NB * NS; k0 < nchunks; k0 += NB * NS) {  // more chunks than one pass holds
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                float w = wts[k + u];
-                o.x = fmaf(p[u].x, w, o.x);
-                o.y = fmaf(p[u].y, w, o.y);
-                o.z = fmaf(p[u].z, w, o.z);
-                o.w = fmaf(p[u].w, w, o.w);
+        for (int u = 0; u < NB; u++) {
+            const int k = k0 + stream + u * NS;
+            p[u] = *(const float4*)(po + (int64_t)(k < nc ? k : nc - 1) * HD);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            const int k = k0 + stream + u * NS;
+            if (k < nchunks) {
+                const float wk = wts[k];
+                o.x = fmaf(p[u].x, wk, o.x);
+                o.y = fmaf(p[u].y, wk, o.y);
+                o.z = fmaf(p[u].z, wk, o.z);
+                o.w = fmaf(p[u].w, wk, o.w);
             }
         }
-        for (; k < nchunks; k++) {
-            float4 p = *(const float4*)(po + (int64_t)k * HD);
-            float w = wts[k];
-            o.x = fmaf(p.x, w, o.x);
-            o.y = fmaf(p.y, w, o.y);
-            o.z = fmaf(p.z, w, o.z);
-            o.w = fmaf(p.w, w, o.w);
-        }
-        res = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
-        *(float4*)(a.out + (int64_t)h * HD + d4 * 4) = res;
     }
-    if (a.tab_out) merge_emit_table<HD>(a, h, lane, res);
+    ored[stream][d4] = o;
+    __syncthreads();
+    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < LPC) {
+        float4 acc = ored[0][t];
+#pragma unroll
+        for (int sidx = 1; sidx < NS; sidx++) {
+            const float4 v = ored[sidx][t];
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+        const float inv = 1.0f / L;
+        res = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        *(float4*)(a.out + (int64_t)h * HD + t * 4) = res;
+    }
+    // (threads from 64 on take no part in the table but reach its barrier)
+    if (a.tab_out) merge_emit_table<HD>(a, h, t, res);
 }
 
 bool attn_fast_supported(int head_dim, int group, int max_seq) {
@@ -461,10 +483,11 @@ hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t st) {
         }
         return hipGetLastError();
     }
+    if (a.nc > ATTN_MAX_CHUNKS) return hipErrorInvalidValue;
     switch (a.hd) {
-        case 64: k_attn_merge<64><<<a.nh, 64, 0, st>>>(a); break;
-        case 128: k_attn_merge<128><<<a.nh, 64, 0, st>>>(a); break;
-        default: k_attn_merge<256><<<a.nh, 64, 0, st>>>(a); break;
+        case 64: k_attn_merge_wide<64><<<a.nh, 256, 0, st>>>(a); break;
+        case 128: k_attn_merge_wide<128><<<a.nh, 256, 0, st>>>(a); break;
+        default: k_attn_merge_wide<256><<<a.nh, 256, 0, st>>>(a); break;
     }
     return hipGetLastError();
 }
