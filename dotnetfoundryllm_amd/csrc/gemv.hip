@@ -1686,7 +1686,8 @@ static MfKernel mf_kernel_mix(int kc) {
 template <int T>
 static MfKernel mf_kernel_ragged(bool tab, int kc) {
     if (kc == 4) return tab ? k_gemv_mfma_r<T, 4, true> : k_gemv_mfma_r<T, 4, false>;
-    return tab ? k_gemv_mfma_r<T, 8, true> : k_gemv_mfma_r<T, 8, false>;
+    if (kc == 8) return tab ? k_gemv_mfma_r<T, 8, true> : k_gemv_mfma_r<T, 8, false>;
+    return nullptr;
 }
 template <bool IL>
 static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
@@ -1992,9 +1993,20 @@ hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, siz
         if (a.seg[i].layout == LAYOUT_TILES && !a.mfma) return hipErrorInvalidValue;
     if (a.xin == XIN_POST && (!a.mfma || a.x2 == nullptr || a.post_w == nullptr || a.x_out == nullptr || a.x_out == a.x))
         return hipErrorInvalidValue;
-    if (a.mfma)
-        mf_kernel(a, a.chunks_per_wave)<<<grid, block_threads, lds, st>>>(a);
-    else if (block_threads <= 512)
+    if (a.mfma) {
+        // the kernel's chunks per wave and wave count must be the plan's: a ragged row only as its
+        // split, an even one covered exactly by at most 8 waves
+        const int NB = a.G / 8, kc = a.chunks_per_wave;
+        int kc_split;
+        const int nw_split = mf_split(NB, &kc_split);
+        const bool ragged = mf_ragged(NB);
+        if (block_threads != 64 * a.nw || (kc != 1 && kc != 2 && kc != 4 && kc != 8) ||
+            (ragged ? (kc != kc_split || a.nw != nw_split) : (a.nw < 1 || a.nw > 8 || a.nw * kc != NB)))
+            return hipErrorInvalidValue;
+        const MfKernel k = mf_kernel(a, kc);
+        if (k == nullptr) return hipErrorInvalidValue;
+        k<<<grid, block_threads, lds, st>>>(a);
+    } else if (block_threads <= 512)
         k_gemv_fused<false><<<grid, block_threads, lds, st>>>(a);
     else
         k_gemv_fused<true><<<grid, block_threads, lds, st>>>(a);
