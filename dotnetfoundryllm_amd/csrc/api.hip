@@ -1609,10 +1609,21 @@ static hipError_t prefill_alloc(fllm_seq* s) {
     return e;
 }
 
+// A GEMM input computed inside the fp16 split: the RmsNorm of rows (NORM: x [T][K], weights w) or
+// the gated activation (ACT: gu [T][2 K]), never written as f32 rows.
+struct PfSrc {
+    enum { NORM = 1, ACT = 2 };
+    int kind;
+    const float* x;
+    const float* w;
+    float eps;
+    int fn;  // NORM: 1 GemmaRmsNorm; ACT: 1 GELU, 0 SiLU
+};
+
 // y_i (+)= X W_i^T over the chunk's rows for the matrices w[0..n) (one launch when their layouts
-// agree); X = pf_xn (row stride pf_ldx) or the given rows
+// agree); X = pf_xn (row stride pf_ldx), the given rows, or the rows src computes
 static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w, float* const* y, int n, int ldy, int T,
-                          bool add, const float* x = nullptr, int ldx = 0) {
+                          bool add, const float* x = nullptr, int ldx = 0, const PfSrc* src = nullptr) {
     PfGemm g{};
     g.x = x ? x : s->pf_xn;
     g.ldx = x ? ldx : s->pf_ldx;
@@ -1625,7 +1636,20 @@ static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w,
     g.ldh = (g.K + 7) / 8 * 8;
     g.xh = s->pf_xh;
     g.xs = s->pf_xs;
-    STEP("pf_split", 4.0 * T * g.K + 4.0 * T * g.ldh, launch_pf_split(g.x, g.ldx, T, g.K, s->pf_xh, g.ldh, s->pf_xs, s->st));
+    if (src && src->kind == PfSrc::NORM) {
+        g.x = src->x;
+        g.ldx = g.K;
+        STEP("pf_norm_split", 8.0 * T * g.K + 4.0 * T * g.ldh,
+             launch_pf_split_norm(src->x, T, g.K, src->w, src->eps, src->fn, s->pf_xh, g.ldh, s->pf_xs, s->st));
+    } else if (src && src->kind == PfSrc::ACT) {
+        g.x = src->x;
+        g.ldx = 2 * g.K;
+        STEP("pf_act_split", 8.0 * T * g.K + 4.0 * T * g.ldh,
+             launch_pf_split_act(src->x, T, g.K, src->fn, s->pf_xh, g.ldh, s->pf_xs, s->st));
+    } else {
+        STEP("pf_split", 4.0 * T * g.K + 4.0 * T * g.ldh,
+             launch_pf_split(g.x, g.ldx, T, g.K, s->pf_xh, g.ldh, s->pf_xs, s->st));
+    }
     double bytes = 0.0;
     for (int i = 0; i < n; i++) {
         // one launch per run of tile-interleaved matrices, or of GGUF-row matrices of one type (a run
@@ -1663,11 +1687,15 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         const Layer& L = m->layers[(size_t)l];
         float* kc = s->kc + (size_t)l * layer_kv;
         float* vc = s->vc + (size_t)l * layer_kv;
-        STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.attn_norm, eps, nk, s->pf_xn, ldx, s->st));
+        // the norms and the activation go into the split of the GEMM input (rows up to 20480)
+        const bool fuse_h = pf_split_src_ok(H), fuse_f = pf_split_src_ok(F);
+        if (!fuse_h) STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.attn_norm, eps, nk, s->pf_xn, ldx, s->st));
         {
             const Tensor* w[3] = {&L.q, &L.k, &L.v};
             float* y[3] = {s->pf_qkv, s->pf_qkv + qdim, s->pf_qkv + qdim + kvdim};
-            if ((e = pf_gemm(s, "pf_qkv", w, y, 3, ldq, T, false)) != hipSuccess) return e;
+            const PfSrc src{PfSrc::NORM, s->pf_x, L.attn_norm, eps, nk};
+            if ((e = pf_gemm(s, "pf_qkv", w, y, 3, ldq, T, false, nullptr, 0, fuse_h ? &src : nullptr)) != hipSuccess)
+                return e;
         }
         STEP("pf_qkv_post", 8.0 * T * ldq,
              launch_pf_qkv_post(s->pf_qkv, ldq, T, pos0, L.bq, L.bk, L.bv, s->rope, d.n_heads, d.n_kv_heads, d.head_dim,
@@ -1683,17 +1711,22 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
             if ((e = pf_gemm(s, "pf_o", w, y, 1, H, T, !gemma, s->pf_att, qdim)) != hipSuccess) return e;
             if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_attn, s->pf_x, s->st));
         }
-        STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.ffn_norm, eps, nk, s->pf_xn, ldx, s->st));
+        if (!fuse_h) STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.ffn_norm, eps, nk, s->pf_xn, ldx, s->st));
         {
             const Tensor* w[2] = {&L.gate, &L.up};
             float* y[2] = {s->pf_gu, s->pf_gu + F};
-            if ((e = pf_gemm(s, "pf_gate_up", w, y, 2, 2 * F, T, false)) != hipSuccess) return e;
+            const PfSrc src{PfSrc::NORM, s->pf_x, L.ffn_norm, eps, nk};
+            if ((e = pf_gemm(s, "pf_gate_up", w, y, 2, 2 * F, T, false, nullptr, 0, fuse_h ? &src : nullptr)) !=
+                hipSuccess)
+                return e;
         }
-        STEP("pf_act", 12.0 * T * F, launch_pf_act(s->pf_gu, T, F, gemma ? 1 : 0, s->pf_xn, ldx, s->st));
+        if (!fuse_f) STEP("pf_act", 12.0 * T * F, launch_pf_act(s->pf_gu, T, F, gemma ? 1 : 0, s->pf_xn, ldx, s->st));
         {
             const Tensor* w[1] = {&L.down};
             float* y[1] = {gemma ? s->pf_tmp : s->pf_x};
-            if ((e = pf_gemm(s, "pf_down", w, y, 1, H, T, !gemma)) != hipSuccess) return e;
+            const PfSrc src{PfSrc::ACT, s->pf_gu, nullptr, 0.0f, gemma ? 1 : 0};
+            if ((e = pf_gemm(s, "pf_down", w, y, 1, H, T, !gemma, nullptr, 0, fuse_f ? &src : nullptr)) != hipSuccess)
+                return e;
             if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_ffn, s->pf_x, s->st));
         }
     }

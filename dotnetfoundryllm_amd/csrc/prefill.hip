@@ -1124,6 +1124,134 @@ hipError_t launch_pf_split(const float* x, int ldx, int T, int K, _Float16* xh, 
     return hipGetLastError();
 }
 
+// The split of a row computed here rather than read: SRC 1, RmsNorm / GemmaRmsNorm (kind 1) of row
+// t of x (row stride ldx, weights w), k_pf_norm's arithmetic per element; SRC 2, act(gate) * up of row
+// t of gu (gate in columns [0, K), up in [K, 2 K) of a row of stride ldx), k_pf_act's. The row stays
+// in registers (NPT float4 per thread: element 4 i .. 4 i + 3 with i = thread + 256 j), so the
+// normalized or gated row is never written; the scale, planes and group sums are k_pf_split's.
+template <int NPT, int SRC>
+__global__ __launch_bounds__(256) void k_pf_split_src(const float* __restrict__ x, int ldx, int K,
+                                                      const float* __restrict__ w, float eps, int kind,
+                                                      _Float16* __restrict__ xh, int ldh, size_t plane,
+                                                      float* __restrict__ xs, int T) {
+    __shared__ float red[4];
+    const int t = blockIdx.x;
+    const float* xr = x + (size_t)t * ldx;
+    const int K4 = K / 4;
+    float4 v[NPT];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPT; j++) {
+        const int i = threadIdx.x + 256 * j;
+        float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < K4) {
+            if constexpr (SRC == 2) {
+                const float4 g = ((const float4*)xr)[i], u = ((const float4*)(xr + K))[i];
+                q = make_float4(act_fn(g.x, kind) * u.x, act_fn(g.y, kind) * u.y, act_fn(g.z, kind) * u.z,
+                                act_fn(g.w, kind) * u.w);
+            } else {
+                q = ((const float4*)xr)[i];
+                ss = fmaf(q.x, q.x, ss);
+                ss = fmaf(q.y, q.y, ss);
+                ss = fmaf(q.z, q.z, ss);
+                ss = fmaf(q.w, q.w, ss);
+            }
+        }
+        v[j] = q;
+    }
+    if constexpr (SRC == 1) {
+        const float tot = pf_block_sum(ss, red);
+        const float rms = 1.0f / sqrtf(tot / (float)K + eps);
+#pragma unroll
+        for (int j = 0; j < NPT; j++) {
+            const int i = threadIdx.x + 256 * j;
+            if (i < K4) {
+                const float4 w4 = ((const float4*)w)[i];
+                const float t0 = v[j].x * rms, t1 = v[j].y * rms, t2 = v[j].z * rms, t3 = v[j].w * rms;
+                v[j] = kind ? make_float4(t0 * (w4.x + 1.0f), t1 * (w4.y + 1.0f), t2 * (w4.z + 1.0f), t3 * (w4.w + 1.0f))
+                            : make_float4(t0 * w4.x, t1 * w4.y, t2 * w4.z, t3 * w4.w);
+            }
+        }
+        __syncthreads();  // red is reused below
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NPT; j++)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    m = pf_wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (m > 0.0f && m <= 3.0e38f) {
+        int ex;
+        (void)frexpf(m, &ex);  // m in [2^(ex-1), 2^ex)
+        e = 15 - ex;
+        e = e < -120 ? -120 : (e > 120 ? 120 : e);
+    }
+    const float sc = ldexpf(1.0f, e);
+    _Float16* h = xh + (size_t)t * ldh;
+    const int G = K / 32;
+    _Float16* gs = xh + 2 * plane + (size_t)t * G;
+    const size_t gplane = (size_t)T * G;
+#pragma unroll
+    for (int j = 0; j < NPT; j++) {
+        const int i = threadIdx.x + 256 * j;
+        const float c[4] = {v[j].x * sc, v[j].y * sc, v[j].z * sc, v[j].w * sc};
+        if (i < K4) {
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                hi[u] = (_Float16)c[u];
+                lo[u] = (_Float16)(c[u] - (float)hi[u]);
+            }
+            *(uint2*)(h + 4 * i) = *(const uint2*)hi;
+            *(uint2*)(h + plane + 4 * i) = *(const uint2*)lo;
+        }
+        // group i / 8: 8 lanes of 4 elements, summed in k_pf_split's order
+        float gv = i < K4 ? ((c[0] + c[1]) + (c[2] + c[3])) : 0.0f;
+        gv += __shfl_xor(gv, 1);
+        gv += __shfl_xor(gv, 2);
+        gv += __shfl_xor(gv, 4);
+        if (i < K4 && (i & 7) == 0) {
+            gv *= 0.015625f;  // times 2^-6 (exact), as k_pf_split
+            const _Float16 ghi = (_Float16)gv;
+            gs[i >> 3] = ghi;
+            gs[gplane + (i >> 3)] = (_Float16)(gv - (float)ghi);
+        }
+    }
+    if (threadIdx.x == 0) xs[t] = ldexpf(1.0f, -e);
+}
+
+template <int SRC>
+static hipError_t pf_split_src(const float* x, int ldx, int T, int K, const float* w, float eps, int kind,
+                               _Float16* xh, int ldh, float* xs, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    if (K % 32 != 0 || ldx % 4 != 0 || ldh % 8 != 0 || ldh < K) return hipErrorInvalidValue;
+    const int n4 = (K / 4 + 255) / 256;
+    const size_t plane = (size_t)T * ldh;
+    if (n4 <= 1) k_pf_split_src<1, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
+    else if (n4 <= 2) k_pf_split_src<2, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
+    else if (n4 <= 4) k_pf_split_src<4, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
+    else if (n4 <= 8) k_pf_split_src<8, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
+    else if (n4 <= 16) k_pf_split_src<16, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
+    else if (n4 <= 20) k_pf_split_src<20, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
+    else return hipErrorNotSupported;
+    return hipGetLastError();
+}
+
+bool pf_split_src_ok(int K) { return K % 32 == 0 && (K / 4 + 255) / 256 <= 20; }
+
+hipError_t launch_pf_split_norm(const float* x, int T, int K, const float* w, float eps, int kind, _Float16* xh,
+                                int ldh, float* xs, hipStream_t st) {
+    return pf_split_src<1>(x, K, T, K, w, eps, kind, xh, ldh, xs, st);
+}
+
+hipError_t launch_pf_split_act(const float* gu, int T, int ffn, int act, _Float16* xh, int ldh, float* xs,
+                               hipStream_t st) {
+    return pf_split_src<2>(gu, 2 * ffn, T, ffn, nullptr, 0.0f, act, xh, ldh, xs, st);
+}
+
 // largest |w| of a matrix (exact dequantization of every element), as float bits (non-negative floats
 // order like their bits)
 __global__ __launch_bounds__(256) void k_pf_wmax(int type, const uint8_t* __restrict__ w, int64_t n, unsigned* out) {

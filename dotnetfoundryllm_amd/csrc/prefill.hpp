@@ -50,6 +50,14 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st);
 // (xh + 2 T ldh: T rows of K / 32, then the lo plane), for the Q4_K form's min term. xh holds
 // 2 T (ldh + K / 32) halves.
 hipError_t launch_pf_split(const float* x, int ldx, int T, int K, _Float16* xh, int ldh, float* xs, hipStream_t st);
+// launch_pf_split of a row computed on the way, never written: RmsNorm / GemmaRmsNorm (kind 1) of
+// every row of x [T][K] (launch_pf_norm's arithmetic), or act(gate) * up of every row of gu [T][2 ffn]
+// (launch_pf_act's). For K up to 20480 (pf_split_src_ok); larger rows: hipErrorNotSupported.
+bool pf_split_src_ok(int K);
+hipError_t launch_pf_split_norm(const float* x, int T, int K, const float* w, float eps, int kind, _Float16* xh,
+                                int ldh, float* xs, hipStream_t st);
+hipError_t launch_pf_split_act(const float* gu, int T, int ffn, int act, _Float16* xh, int ldh, float* xs,
+                               hipStream_t st);
 // *out = max(*out, bits of the largest |w| over the n elements of a weight matrix in GGUF row layout)
 // (out holds a non-negative float's bits; zero it first). pf_wexp turns it into the exponent that
 // brings the matrix's largest magnitude into [2^14, 2^15) for the fp16 split.
