@@ -450,3 +450,51 @@ def test_long_context_windowed_attention(ctx):
         orc.close()
         kv.close()
         m.close()
+
+
+
+@pytest.mark.parametrize("arch", ["llama-hd128", "gemma2-hd256"])
+def test_long_context_many_chunks(ctx, arch):
+    """More than 32 position chunks per kv head (one or two KV heads at a 4096-position capacity: 128
+    chunk slots, 79 live over 2500 positions), so the four-wave merge runs: head_dim 128 in one pass
+    over its streams; head_dim 256 (Gemma-2 softcaps) in two on its full-range odd layer and one on
+    its even layer's 1500-position window (47 chunks). Logits, K/V and 8 greedy tokens against the
+    oracle."""
+    from dotnetfoundryllm_amd.configs import _cfg, _types
+    if arch == "llama-hd128":
+        cfg = _cfg("long-llama", N.ARCH_LLAMA, 1, 512, 4, 2, 512, 512, 4096, 10000.0,
+                   _types(*([N.Q4_K] * 7), N.Q6_K), norm_std=0.1, seed=22)
+    else:
+        cfg = _cfg("long-gemma2", N.ARCH_GEMMA2, 2, 512, 2, 1, 512, 512, 4096, 10000.0,
+                   _types(*([N.Q8_0] * 8)), head_dim=256, emb_type=N.BF16, window=1500, attn_softcap=50.0,
+                   final_softcap=30.0, norm_std=0.1, seed=23)
+    desc = desc_of(cfg)
+    tensors = {e[0]: (e, synth_bytes(cfg, e)) for e in tensor_plan(cfg)}
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors)
+    n = 2500
+    prompt = F.synth_tokens(cfg["seed"], 2, desc.vocab, n)
+    try:
+        fwd.prefill(prompt, 0, kv)
+        for pos, t in enumerate(prompt):
+            assert orc.forward(int(t), pos) == 0
+        assert O.normwise_rel_err(fwd.logits, orc.logits()) <= TOL
+        assert O.normwise_rel_err(kv.get_keys(0), orc.kv(0, 0)) <= TOL
+        assert O.normwise_rel_err(kv.get_values(0), orc.kv(0, 1)) <= TOL
+        toks = fwd.decode_greedy(int(prompt[-1]), n, 8, kv)
+        ref, pos = [], n
+        nxt = int(prompt[-1])
+        for _ in range(8):
+            assert orc.forward(nxt, pos) == 0
+            pos += 1
+            lg = orc.logits()
+            nxt = int(O.lib.orc_argmax(O.fp(lg), lg.size))
+            ref.append(nxt)
+        assert list(toks) == ref
+        assert O.normwise_rel_err(fwd.logits, lg) <= TOL
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
