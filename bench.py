@@ -177,9 +177,9 @@ def child_profile(args):
 
 
 def child_gemv(args):
-    """The C1 matrices under the traffic counters: for each type and shape, GEMV_COPIES distinct
-    copies regrouped by fllm_gemv_pack, one fllm_gemv_ex launch on each (tile layout), then the
-    calibration copy."""
+    """The isolated-GEMV sweep's matrices under the traffic counters: for each type and shape,
+    GEMV_COPIES distinct copies regrouped by fllm_gemv_pack, one fllm_gemv_ex launch on each (tile
+    layout), then the calibration copy."""
     import numpy as np
 
     import dotnetfoundryllm_amd as F
@@ -216,7 +216,7 @@ GEMV_COPIES = 3
 
 
 def gemv_report(args):
-    """BASELINE's second metric: the C1 GEMV sweep (Q4_K, Q8_0, Q6_K at 4096x4096, 14336x4096,
+    """The second headline metric: the isolated GEMV sweep (Q4_K, Q8_0, Q6_K at 4096x4096, 14336x4096,
     4096x14336; dotnetfoundryllm_amd.gemv_bench) as algorithmic GB/s and fraction of 8 TB/s, with each
     tile-layout launch's HBM traffic from FETCH_SIZE + WRITE_SIZE (calibrated like the roofline's) when
     rocprofv3 is present."""

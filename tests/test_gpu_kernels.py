@@ -89,11 +89,11 @@ def run_gemv(ctx, t, rows, cols, seed=3, x=None):
 
 
 # the microbenchmark shapes (rows x cols) and their types
-C1 = [(4096, 4096), (14336, 4096), (4096, 14336)]
+GEMV_SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336)]
 
 
 @pytest.mark.parametrize("t", [N.Q4_K, N.Q8_0, N.Q6_K])
-@pytest.mark.parametrize("shape", C1)
+@pytest.mark.parametrize("shape", GEMV_SHAPES)
 def test_gemv_microbenchmark_shapes(ctx, t, shape):
     y, ref = run_gemv(ctx, t, *shape)
     err = O.normwise_rel_err(y, ref)
@@ -103,7 +103,7 @@ def test_gemv_microbenchmark_shapes(ctx, t, shape):
 
 
 @pytest.mark.parametrize("t", [N.Q4_K, N.Q8_0, N.Q6_K, N.Q5_K])
-@pytest.mark.parametrize("shape", C1 + [(64, 18944), (16, 256), (48, 3584), (32, 2560)])
+@pytest.mark.parametrize("shape", GEMV_SHAPES + [(64, 18944), (16, 256), (48, 3584), (32, 2560)])
 def test_gemv_tiles_layout(ctx, t, shape):
     """fllm_gemv_pack + fllm_gemv_ex(FLLM_LAYOUT_TILES) against the oracle's F32 dot (18944
     columns: 74 chunks, 8 per wave over 10 waves; 3584 and 2560 columns: 14 and 10 chunks, 4 per
