@@ -58,6 +58,10 @@ CONFIGS = {
     "gemma2-9b-q8": _cfg("gemma2-9b-q8", N.ARCH_GEMMA2, 42, 3584, 16, 8, 14336, 256000, 8192, 10000.0,
                          _types(*([Q8_0] * 8)), head_dim=256, emb_type=BF16, window=4096, attn_softcap=50.0,
                          final_softcap=30.0, seed=0x5EED04),
+    # the same with the LM head tied to the BF16 token embedding (no output.weight in the file)
+    "gemma2-9b-q8-tied": _cfg("gemma2-9b-q8-tied", N.ARCH_GEMMA2, 42, 3584, 16, 8, 14336, 256000, 8192, 10000.0,
+                              _types(*([Q8_0] * 8)), head_dim=256, emb_type=BF16, window=4096, attn_softcap=50.0,
+                              final_softcap=30.0, tied=True, seed=0x5EED04),
     # ---- small shapes for parity tests (every architecture and tensor type) ----
     "test-llama": _cfg("test-llama", N.ARCH_LLAMA, 2, 256, 4, 2, 512, 512, 128, 10000.0,
                        _types(Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K, Q6_K), norm_std=0.1, seed=11),

@@ -1243,7 +1243,8 @@ static hipError_t head_generic(fllm_seq* s) {
     hipError_t e = gemv_step(s, m->output, s->xn, s->logits, nullptr);
     if (e != hipSuccess) return e;
     if (gemma && d.final_softcap > 0.0f) STEP("softcap", 8.0 * d.vocab, launch_softcap(s->logits, d.vocab, d.final_softcap, s->st));
-    STEP("argmax", 4.0 * d.vocab, launch_argmax(s->logits, d.vocab, s->params, s->tokens_out, s->max_seq, s->st));
+    STEP("argmax", 4.0 * d.vocab,
+         launch_argmax_seg(s->logits, d.vocab, s->head_keys, s->params, s->tokens_out, s->max_seq, s->st));
     return hipSuccess;
 }
 

@@ -484,6 +484,37 @@ hipError_t launch_argmax(const float* x, int64_t n, StepParams* p, int* tokens_o
     return hipGetLastError();
 }
 
+// Per 4096-entry segment of x: the key (order key << 32) | ~index of its first maximum (the LM head
+// epilogue's key format, so k_argmax_keys reduces them); 16 loads per thread in flight.
+__global__ __launch_bounds__(256) void k_argmax_seg(const float* __restrict__ x, int64_t n,
+                                                    unsigned long long* __restrict__ keys) {
+    const int64_t base = (int64_t)blockIdx.x * 4096;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int64_t i = base + threadIdx.x + 256 * j;
+        v[j] = i < n ? x[i] : 0.0f;
+    }
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int64_t i = base + threadIdx.x + 256 * j;
+        const unsigned long long k = ((unsigned long long)okey(v[j]) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+        if (i < n && k > best) best = k;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long ot = __shfl_xor(best, o);
+        best = ot > best ? ot : best;
+    }
+    __shared__ unsigned long long sk[4];
+    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) best = sk[w] > best ? sk[w] : best;
+        keys[blockIdx.x] = best;
+    }
+}
+
 // Reduce the LM head's per-workgroup keys ((order key << 32) | ~row) to the first index of the
 // maximum, then advance the step like k_argmax with tokens_out.
 __global__ __launch_bounds__(256) void k_argmax_keys(const unsigned long long* __restrict__ keys, int n, StepParams* p,
@@ -512,6 +543,15 @@ __global__ __launch_bounds__(256) void k_argmax_keys(const unsigned long long* _
 hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams* p, int* tokens_out, int tokens_cap,
                               hipStream_t st) {
     k_argmax_keys<<<1, 256, 0, st>>>(keys, n, p, tokens_out, tokens_cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_seg(const float* x, int64_t n, unsigned long long* keys, StepParams* p, int* tokens_out,
+                             int tokens_cap, hipStream_t st) {
+    if (n <= 0 || n > 0xFFFFFFFFll) return hipErrorInvalidValue;
+    const int nseg = (int)((n + 4095) / 4096);
+    k_argmax_seg<<<nseg, 256, 0, st>>>(x, n, keys);
+    k_argmax_keys<<<1, 256, 0, st>>>(keys, nseg, p, tokens_out, tokens_cap);
     return hipGetLastError();
 }
 
