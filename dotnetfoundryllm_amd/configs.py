@@ -91,6 +91,9 @@ CONFIGS = {
     # chunk of the row and 7 past it
     "test-ragged": _cfg("test-ragged", N.ARCH_LLAMA, 2, 256, 4, 2, 16640, 512, 64, 10000.0,
                         _types(Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K, Q6_K), norm_std=0.1, seed=18),
+    # FFN rows past the prefill's fused-split limit (20480) and past the matrix-core GEMV's splits
+    "test-wide-ffn": _cfg("test-wide-ffn", N.ARCH_LLAMA, 2, 256, 4, 2, 20992, 512, 64, 10000.0,
+                          _types(Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K, Q6_K), norm_std=0.1, seed=19),
 }
 
 

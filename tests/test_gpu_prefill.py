@@ -42,7 +42,7 @@ def _oracle_continue(orc, first, pos, n):
 
 
 SMALL = ["test-llama", "test-llama-straddle", "test-mistral", "test-qwen2", "test-gemma2", "test-gemma2-hd256",
-         "test-mixed", "test-ragged"]
+         "test-mixed", "test-ragged", "test-wide-ffn"]
 
 
 @pytest.mark.parametrize("name", SMALL)
