@@ -453,17 +453,21 @@ def test_long_context_windowed_attention(ctx):
 
 
 
-@pytest.mark.parametrize("arch", ["llama-hd128", "gemma2-hd256"])
+@pytest.mark.parametrize("arch", ["llama-hd128", "gemma2-hd256", "llama-g7"])
 def test_long_context_many_chunks(ctx, arch):
     """More than 32 position chunks per kv head (one or two KV heads at a 4096-position capacity: 128
     chunk slots, 79 live over 2500 positions), so the four-wave merge runs: head_dim 128 in one pass
     over its streams; head_dim 256 (Gemma-2 softcaps) in two on its full-range odd layer and one on
-    its even layer's 1500-position window (47 chunks). Logits, K/V and 8 greedy tokens against the
-    oracle."""
+    its even layer's 1500-position window (47 chunks); and 7 query heads per kv head.
+    Logits, K/V and 8 greedy tokens against the oracle."""
     from dotnetfoundryllm_amd.configs import _cfg, _types
     if arch == "llama-hd128":
         cfg = _cfg("long-llama", N.ARCH_LLAMA, 1, 512, 4, 2, 512, 512, 4096, 10000.0,
                    _types(*([N.Q4_K] * 7), N.Q6_K), norm_std=0.1, seed=22)
+    elif arch == "llama-g7":
+        # 7 query heads per kv head in one attention workgroup
+        cfg = _cfg("long-llama-g7", N.ARCH_LLAMA, 1, 1792, 14, 2, 512, 512, 4096, 10000.0,
+                   _types(*([N.Q4_K] * 7), N.Q6_K), norm_std=0.1, seed=24)
     else:
         cfg = _cfg("long-gemma2", N.ARCH_GEMMA2, 2, 512, 2, 1, 512, 512, 4096, 10000.0,
                    _types(*([N.Q8_0] * 8)), head_dim=256, emb_type=N.BF16, window=1500, attn_softcap=50.0,
