@@ -1243,8 +1243,10 @@ static hipError_t head_generic(fllm_seq* s) {
     hipError_t e = gemv_step(s, m->output, s->xn, s->logits, nullptr);
     if (e != hipSuccess) return e;
     if (gemma && d.final_softcap > 0.0f) STEP("softcap", 8.0 * d.vocab, launch_softcap(s->logits, d.vocab, d.final_softcap, s->st));
-    STEP("argmax", 4.0 * d.vocab,
-         launch_argmax_seg(s->logits, d.vocab, s->head_keys, s->params, s->tokens_out, s->max_seq, s->st));
+    // (one kernel per profiled step: the segment keys, then their reduction and the step advance)
+    STEP("argmax_segments", 4.0 * d.vocab, launch_argmax_seg(s->logits, d.vocab, s->head_keys, s->st));
+    STEP("argmax", 8.0 * argmax_segments(d.vocab),
+         launch_argmax_keys(s->head_keys, argmax_segments(d.vocab), s->params, s->tokens_out, s->max_seq, s->st));
     return hipSuccess;
 }
 

@@ -546,12 +546,11 @@ hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams*
     return hipGetLastError();
 }
 
-hipError_t launch_argmax_seg(const float* x, int64_t n, unsigned long long* keys, StepParams* p, int* tokens_out,
-                             int tokens_cap, hipStream_t st) {
+int argmax_segments(int64_t n) { return (int)((n + 4095) / 4096); }
+
+hipError_t launch_argmax_seg(const float* x, int64_t n, unsigned long long* keys, hipStream_t st) {
     if (n <= 0 || n > 0xFFFFFFFFll) return hipErrorInvalidValue;
-    const int nseg = (int)((n + 4095) / 4096);
-    k_argmax_seg<<<nseg, 256, 0, st>>>(x, n, keys);
-    k_argmax_keys<<<1, 256, 0, st>>>(keys, nseg, p, tokens_out, tokens_cap);
+    k_argmax_seg<<<argmax_segments(n), 256, 0, st>>>(x, n, keys);
     return hipGetLastError();
 }
 

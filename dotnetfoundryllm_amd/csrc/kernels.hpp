@@ -55,10 +55,10 @@ hipError_t launch_argmax(const float* x, int64_t n, StepParams* p, int* tokens_o
 // reduce per-workgroup argmax keys of the fused LM head; advances the step as launch_argmax
 hipError_t launch_argmax_keys(const unsigned long long* keys, int n, StepParams* p, int* tokens_out, int tokens_cap,
                               hipStream_t st);
-// argmax of x (n entries) over 4096-entry segments (keys: one slot per segment), then the step advance
-// of launch_argmax_keys (tokens_out required)
-hipError_t launch_argmax_seg(const float* x, int64_t n, unsigned long long* keys, StepParams* p, int* tokens_out,
-                             int tokens_cap, hipStream_t st);
+// the first maximum of each 4096-entry segment of x (n entries) as an argmax key (argmax_segments(n)
+// slots), for launch_argmax_keys
+int argmax_segments(int64_t n);
+hipError_t launch_argmax_seg(const float* x, int64_t n, unsigned long long* keys, hipStream_t st);
 // largest vocabulary of the one-workgroup samplers (launch_topk, launch_sample_nucleus)
 constexpr int SAMPLE_MAX_VOCAB = 262144;
 // Device scratch of the grid form of launch_topk: the sample's threshold key, per-segment counts
