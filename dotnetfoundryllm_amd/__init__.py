@@ -382,6 +382,11 @@ def set_debug(kv, enable):
     _check(N.dev.fllm_seq_set_debug(kv.h, 1 if enable else 0))
 
 
+def set_prefill_chunk(kv, tokens):
+    """Tokens per pass of the batched prefill (before the sequence's first batched prefill)."""
+    _check(N.dev.fllm_seq_set_prefill_chunk(kv.h, int(tokens)))
+
+
 def set_profile(kv, enable):
     _check(N.dev.fllm_seq_set_profile(kv.h, 1 if enable else 0))
 

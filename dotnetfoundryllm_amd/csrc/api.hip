@@ -235,8 +235,9 @@ struct fllm_seq {
     std::vector<std::string> agg_order;
     std::vector<std::string> launch_names;  // every profiled launch in order (bounded)
     std::vector<void*> allocs;
-    // batched prefill scratch for chunks of up to pf_cap tokens (allocated on first use)
-    int pf_cap = 0, pf_ldx = 0;
+    // batched prefill scratch for chunks of up to pf_cap = min(max_seq, pf_chunk) tokens (allocated
+    // on first use)
+    int pf_chunk = 4096, pf_cap = 0, pf_ldx = 0;
     float *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_gu = nullptr, *pf_tmp = nullptr;
     float* pf_part = nullptr;  // K-split partial products of the short GEMM launches
     size_t pf_part_cap = 0;
@@ -1091,6 +1092,16 @@ extern "C" int32_t fllm_seq_set_graph(fllm_seq* s, int32_t enable) {
     return FLLM_OK;
 }
 
+extern "C" int32_t fllm_seq_set_prefill_chunk(fllm_seq* s, int32_t tokens) {
+    NOT_NULL(s);
+    if (tokens < 1) return fail(FLLM_E_ARG_RANGE, "prefill chunk must be >= 1 token");
+    // the chunk buffers are sized on the first batched prefill and kept for the sequence's life
+    if (s->pf_cap > 0 && tokens != s->pf_chunk)
+        return fail(FLLM_E_INVALID_OP, "the prefill chunk is fixed once a batched prefill has run");
+    s->pf_chunk = tokens;
+    return FLLM_OK;
+}
+
 extern "C" int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable) {
     NOT_NULL(s);
     if (s->debug != (enable != 0)) s->graph_valid = false;
@@ -1570,7 +1581,6 @@ extern "C" int32_t fllm_decode_greedy(fllm_seq* s, int32_t token, int32_t positi
 }
 
 // ---- batched prefill ---------------------------------------------------------------------------
-static const int kPrefillChunk = 512;  // tokens per pass through the layers
 
 // the batched path covers the fast attention's head dims and 32-aligned projection widths
 static bool prefill_batched_ok(const fllm_seq* s) {
@@ -1583,7 +1593,7 @@ static bool prefill_batched_ok(const fllm_seq* s) {
 static hipError_t prefill_alloc(fllm_seq* s) {
     if (s->pf_cap > 0) return hipSuccess;
     const fllm_model& m = *s->m;
-    const int cap = s->max_seq < kPrefillChunk ? s->max_seq : kPrefillChunk;
+    const int cap = s->max_seq < s->pf_chunk ? s->max_seq : s->pf_chunk;
     size_t ldx = (size_t)std::max(m.d.hidden, m.d.ffn);
     ldx = (ldx + 3) / 4 * 4;
     const size_t H = (size_t)m.d.hidden, C = (size_t)cap;

@@ -173,6 +173,13 @@ FLLM_API int32_t fllm_seq_capacity(fllm_seq* s, int32_t* cap);        /* KvCache
 FLLM_API int32_t fllm_seq_get_model(fllm_seq* s, fllm_model** out);
 /* 1 = replay the decode step from a captured HIP graph (default), 0 = launch kernels one by one. */
 FLLM_API int32_t fllm_seq_set_graph(fllm_seq* s, int32_t enable);
+/* Tokens per pass of the batched prefill through the layers (default 4096, capped at the
+ * capacity): each pass's projections are GEMMs over that many rows and its attention a grid over
+ * them, so long prompts fill the GPU. A tuning knob with no counterpart in the reference (whose
+ * prefill is one Forward per token). Only before the sequence's first batched prefill, which sizes
+ * the chunk buffers: later calls with another value return FLLM_E_INVALID_OP; tokens < 1 returns
+ * FLLM_E_ARG_RANGE. */
+FLLM_API int32_t fllm_seq_set_prefill_chunk(fllm_seq* s, int32_t tokens);
 /* 1 = keep the residual stream after every layer for fllm_debug_hidden (parity hook). */
 FLLM_API int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable);
 
@@ -193,8 +200,8 @@ FLLM_API int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position);
 /* n consecutive Forward calls for tokens[0..n) at positions pos0.. (prefill loop,
  * LlamaLanguageModel.cs:133-137), with their results: the K/V rows of every position, the last
  * position's logits and greedy token. When pos0 is the cache's current length (a prompt) and debug
- * capture is off, the tokens go through each layer together in chunks of up to 512 (f32
- * matrix-core GEMMs over the chunk, causal attention over the cache); otherwise, and for n = 1,
+ * capture is off, the tokens go through each layer together in chunks (fllm_seq_set_prefill_chunk;
+ * fp16 matrix-core GEMMs over the chunk, causal attention over the cache); otherwise, and for n = 1,
  * it is n fllm_forward calls. Token ids and the cache capacity are checked before anything runs. */
 FLLM_API int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, int32_t pos0);
 /* The greedy part of LlamaLanguageModel.GenerateAsync's decode loop (LlamaLanguageModel.cs:162-293

@@ -11,10 +11,10 @@
   the oracle's gap at that step: a gap inside float32 accumulation noise is a tie, not a kernel
   fault, and the test says which it is.
 - Gemma-2 long context (test-gemma2-long: head_dim 256, 16/8 heads, softcaps 50/30, window 4096 on
-  the even layer, an 8192-position cache): a 6200-token prompt through fllm_prefill (13 chunks of
-  512), then 8 greedy steps; every step's logits within 1e-3, the tokens identical, and K/V rows of
-  both layers at positions on both sides of the window edge within 1e-3 (Gemma2ForwardPass.cs:86-87,
-  126-185).
+  the even layer, an 8192-position cache): a 6200-token prompt through fllm_prefill (in passes of
+  the default 4096 tokens, so 2 chunks, and of 512, so 13), then 8 greedy steps; every step's logits
+  within 1e-3, the tokens identical, and K/V rows of both layers at positions on both sides of the
+  window edge within 1e-3 (Gemma2ForwardPass.cs:86-87, 126-185).
 """
 import os
 import sys
@@ -92,7 +92,8 @@ def test_llama3_8b_full_depth_greedy(ctx):
         model.close()
 
 
-def test_gemma2_long_context_window(ctx):
+@pytest.mark.parametrize("chunk", [None, 512], ids=["chunk-default", "chunk-512"])
+def test_gemma2_long_context_window(ctx, chunk):
     g = np.load(os.path.join(HERE, "golden", "gemma2_long_window.npz"))
     cfg, desc, tensors = synthetic("test-gemma2-long")
     prompt = g["prompt"]
@@ -102,8 +103,10 @@ def test_gemma2_long_context_window(ctx):
     kv = F.HipKvCache(m, desc.max_ctx)
     fwd = F.HipForwardPass(m)
     try:
+        if chunk:
+            F.set_prefill_chunk(kv, chunk)
         n = prompt.size - 1
-        say(f"test-gemma2-long: prefill of {n} tokens")
+        say(f"test-gemma2-long: prefill of {n} tokens (chunk {chunk or 'default'})")
         fwd.prefill(prompt[:-1], 0, kv)
         assert kv.current_length == n
         nxt, toks, worst = int(prompt[-1]), [], 0.0

@@ -79,10 +79,48 @@ def test_batched_prefill_matches_oracle_and_stepwise(ctx, name):
         m.close()
 
 
-def test_batched_prefill_several_chunks(ctx):
+def test_prefill_chunk_contract(ctx):
+    """fllm_seq_set_prefill_chunk: tokens < 1 is out of range; a chunk of 24 tokens takes a 61-token
+    prompt in passes of 24, 24 and 13 (logits, K/V and the greedy token against the oracle); once a
+    batched prefill has sized the chunk buffers another value is an invalid operation, the same
+    value is accepted, and a reset keeps the chunk."""
+    cfg, desc, tensors = synthetic("test-llama")
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors)
+    prompt = F.synth_tokens(cfg["seed"], 5, desc.vocab, 61)
+    try:
+        for bad in (0, -5):
+            with pytest.raises(F.ArgumentOutOfRangeException):
+                F.set_prefill_chunk(kv, bad)
+        F.set_prefill_chunk(kv, 100)
+        F.set_prefill_chunk(kv, 24)  # another value before the first prefill
+        fwd.prefill(prompt, 0, kv)
+        _oracle_prefill(orc, prompt)
+        want = orc.logits()
+        assert O.normwise_rel_err(fwd.logits, want) <= TOL
+        for l in range(desc.n_layers):
+            assert O.normwise_rel_err(kv.get_keys(l), orc.kv(l, 0)) <= TOL
+            assert O.normwise_rel_err(kv.get_values(l), orc.kv(l, 1)) <= TOL
+        assert fwd.sample_greedy() == int(O.lib.orc_argmax(O.fp(want), want.size))
+        with pytest.raises(F.InvalidOperationException):
+            F.set_prefill_chunk(kv, 32)
+        F.set_prefill_chunk(kv, 24)
+        kv.clear()
+        fwd.prefill(prompt[:30], 0, kv)
+        assert kv.current_length == 30
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
+
+
+@pytest.mark.parametrize("chunk", [512, None], ids=["chunk-512", "chunk-default"])
+def test_batched_prefill_several_chunks(ctx, chunk):
     """1100 tokens go through the layers in chunks of 512, 512 and 76: every chunk attends to the
-    rows the earlier chunks stored. No window; K/V of the first, a middle and the last position
-    and the logits against the oracle."""
+    rows the earlier chunks stored (and, with the default chunk, in one pass). No window; K/V of the
+    first, a middle and the last position and the logits against the oracle."""
     from dotnetfoundryllm_amd.configs import _cfg, _types
     cfg = _cfg("chunks-llama", N.ARCH_LLAMA, 2, 256, 4, 2, 512, 512, 1200, 10000.0,
                _types(N.Q4_K, N.Q4_K, N.Q6_K, N.Q4_K, N.Q4_K, N.Q4_K, N.Q6_K, N.Q6_K), norm_std=0.1, seed=23)
@@ -94,6 +132,8 @@ def test_batched_prefill_several_chunks(ctx):
     orc = O.OracleModel(desc, tensors)
     prompt = F.synth_tokens(cfg["seed"], 3, desc.vocab, 1100)
     try:
+        if chunk:
+            F.set_prefill_chunk(kv, chunk)
         fwd.prefill(prompt, 0, kv)
         _oracle_prefill(orc, prompt)
         assert kv.current_length == 1100
@@ -114,13 +154,14 @@ def test_batched_prefill_several_chunks(ctx):
         m.close()
 
 
+@pytest.mark.parametrize("chunk", [512, None], ids=["chunk-512", "chunk-default"])
 @pytest.mark.parametrize("arch", [N.ARCH_MISTRAL, N.ARCH_GEMMA2])
-def test_batched_prefill_window_across_chunks(ctx, arch):
-    """A sliding window of 700 over a 1100-token prompt (chunks of 512, 512, 76): from position 700
-    on, the first keys a row may attend are in an earlier chunk, so the window start of the batched
-    attention is checked against keys other chunks stored (Mistral: every layer windowed; Gemma-2:
-    the even layer, with softcaps). Logits, K/V rows on both sides of the edge and the greedy tokens
-    after it against the oracle."""
+def test_batched_prefill_window_across_chunks(ctx, arch, chunk):
+    """A sliding window of 700 over a 1100-token prompt (chunks of 512, 512, 76, or one pass with the
+    default chunk): from position 700 on, the first keys a row may attend are in an earlier chunk, so
+    the window start of the batched attention is checked against keys other chunks stored (Mistral:
+    every layer windowed; Gemma-2: the even layer, with softcaps). Logits, K/V rows on both sides of
+    the edge and the greedy tokens after it against the oracle."""
     from dotnetfoundryllm_amd.configs import _cfg, _types
     if arch == N.ARCH_MISTRAL:
         cfg = _cfg("window-mistral", arch, 2, 256, 4, 2, 512, 512, 1200, 10000.0, _types(*([N.Q8_0] * 8)),
@@ -137,6 +178,8 @@ def test_batched_prefill_window_across_chunks(ctx, arch):
     orc = O.OracleModel(desc, tensors)
     prompt = F.synth_tokens(cfg["seed"], 3, desc.vocab, 1100)
     try:
+        if chunk:
+            F.set_prefill_chunk(kv, chunk)
         fwd.prefill(prompt, 0, kv)
         _oracle_prefill(orc, prompt)
         assert kv.current_length == 1100
