@@ -1526,9 +1526,10 @@ hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w
 
 // ---- causal attention over the cache (ComputeAttention, LlamaForwardPass.cs:158-211 and the
 // Mistral / Qwen2 / Gemma2 variants) ----------------------------------------------------------------
-// Workgroup = (query head, block of 64 consecutive queries), wave w = queries 16 w .. + 15. Keys go in
-// blocks of 64 rows (32 for head_dim 256) of the head's kv head, staged in LDS (K and V rows padded to
-// HD + 4 floats); the next block's rows are loaded into registers while the current one multiplies. Per
+// Workgroup = (query head, block of 64 consecutive queries, the last block first), wave w = queries
+// 16 w .. + 15. Keys go in blocks of 64 rows (32 for head_dim 256) of the head's kv head, staged in
+// LDS (K and V rows padded to HD + 4 floats); the next block's rows are loaded into registers while
+// the current one multiplies. Per
 // block a wave forms the transposed scores S^T = K Q^T on the f32 matrix cores
 // (v_mfma_f32_16x16x4f32: lane l holds keys 16 t + 4 (l >> 4) + e of query l & 15), updates the running
 // max / sum per query (online softmax), and adds O^T += V^T P^T with P^T straight from the score
@@ -1551,7 +1552,9 @@ __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
     extern __shared__ float pa_lds[];
     float* sk = pa_lds;             // [PF_AK][LD]
     float* sv = sk + PF_AK * LD;    // [PF_AK][LD]
-    const int h = blockIdx.x, qb = blockIdx.y * PF_AQ;
+    // query blocks from the last (the most keys under the causal mask) to the first, so that the
+    // longest workgroups are dispatched first and the short ones fill in behind them
+    const int h = blockIdx.x, qb = ((int)gridDim.y - 1 - (int)blockIdx.y) * PF_AQ;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q16 = lane & 15, kq = lane >> 4;
     const int kvh = h / (a.nh / a.nkv);
     // this lane's query (the column it holds) and the wave's query range
