@@ -442,39 +442,36 @@ __device__ __forceinline__ void pf_gemm_tile_h(const PfGemm& a, const PfSeg& sg,
             *(uint4*)(sx + ((size_t)pl * BM + (rem >> 3)) * PF_LDH + (rem & 7) * 8) = xr[i];
         }
         if constexpr (WT == FLLM_TYPE_Q8_0) {
-            // d' q with d' = d 2^-wexp (fp16) and q the int8 code: q exact in fp16 (its byte as
-            // 0x64 80 ^ byte = 1024 + 128 + q, minus 1152), hi = d' q rounded once, lo = d' q - hi from
-            // one fma, exact (d' q needs at most 18 significant bits). Element 16 hh + 4 by + j is
-            // byte by of dword j of half hh, so a pair (e, e + 1) takes byte by of dwords j and j + 1.
+            // exact-integer form: the int8 code q as an fp16 integer (its byte as 0x64 80 ^ byte =
+            // 1024 + 128 + q, minus 1152) in the weight plane, and the block's d' = d 2^-wexp (f32,
+            // exact) beside it; the products sum x hi q + x lo q per 32-element block and the block
+            // sum is added times d' in f32. Element 16 hh + 4 by + j is byte by of dword j of half hh,
+            // so a pair (e, e + 1) takes byte by of dwords j and j + 1.
             const int k = k0 + 32 * wgrp;
-            uint32_t hv[16], lv[16];
+            uint32_t qv[16];
+            float dq = 0.0f;
             if (wlive && k < a.K) {
                 const int g = (k >> 5) & 7;
-                const _Float16 dh = (_Float16)(half_exact(g < 4 ? (wraw.d & 0xFFFFu) : (wraw.d >> 16)) * wsc);
-                const pf_hv2 d2 = {dh, dh}, off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+                dq = half_exact(g < 4 ? (wraw.d & 0xFFFFu) : (wraw.d >> 16)) * wsc;
+                const pf_hv2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
                 const uint32_t wd[8] = {wraw.h0.x, wraw.h0.y, wraw.h0.z, wraw.h0.w, wraw.h1.x, wraw.h1.y, wraw.h1.z, wraw.h1.w};
 #pragma unroll
                 for (int pr = 0; pr < 16; pr++) {
                     const int e = 2 * pr, hh = e >> 4, by = (e & 15) >> 2, j = e & 3;
                     const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + by) << 16) | (uint32_t)by;
                     const uint32_t p = __builtin_amdgcn_perm(wd[4 * hh + j + 1], wd[4 * hh + j], sel) ^ 0x64806480u;
-                    const pf_hv2 q = __builtin_bit_cast(pf_hv2, p) + off;
-                    const pf_hv2 vh = q * d2;
-                    const pf_hv2 vl = __builtin_elementwise_fma(q, d2, -vh);
-                    hv[pr] = __builtin_bit_cast(uint32_t, vh);
-                    lv[pr] = __builtin_bit_cast(uint32_t, vl);
+                    qv[pr] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_hv2, p) + off);
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 16; i++) hv[i] = lv[i] = 0u;
+                for (int i = 0; i < 16; i++) qv[i] = 0u;
             }
             _Float16* d0 = sw + (size_t)wrow * PF_LDH + 32 * wgrp;
-            _Float16* d1 = d0 + (size_t)PF_BN * PF_LDH;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                *(uint4*)(d0 + 8 * i) = make_uint4(hv[4 * i], hv[4 * i + 1], hv[4 * i + 2], hv[4 * i + 3]);
-                *(uint4*)(d1 + 8 * i) = make_uint4(lv[4 * i], lv[4 * i + 1], lv[4 * i + 2], lv[4 * i + 3]);
-            }
+            for (int i = 0; i < 4; i++)
+                *(uint4*)(d0 + 8 * i) = make_uint4(qv[4 * i], qv[4 * i + 1], qv[4 * i + 2], qv[4 * i + 3]);
+            // the block scales in the second weight plane, which this form leaves free
+            ((float*)(sw + (size_t)PF_BN * PF_LDH))[wgrp * PF_BN + wrow] = dq;
         } else {
             float v[32];
             const int k = k0 + 32 * wgrp;
@@ -497,6 +494,44 @@ __device__ __forceinline__ void pf_gemm_tile_h(const PfGemm& a, const PfSeg& sg,
         // the next step's global loads fly while this step multiplies
         if (k0 + PF_BK < ke) fetch(k0 + PF_BK);
         __syncthreads();
+        if constexpr (WT == FLLM_TYPE_Q8_0) {
+            const float* sdq = (const float*)(sw + (size_t)PF_BN * PF_LDH);
+#pragma unroll
+            for (int kk = 0; kk < PF_BK; kk += 32) {
+                const int ko = kk + 8 * (lane >> 4);
+                pf_h8 ah[TI], al[TI], bq[4];
+                float dj[4];
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+                    const _Float16* p = sx + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDH + ko;
+                    ah[i] = *(const pf_h8*)p;
+                    al[i] = *(const pf_h8*)(p + (size_t)BM * PF_LDH);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int r = 64 * wn + 16 * j + (lane & 15);
+                    bq[j] = *(const pf_h8*)(sw + (size_t)r * PF_LDH + ko);
+                    dj[j] = sdq[(kk >> 5) * PF_BN + r];
+                }
+                // the block's sum (x lo q, then x hi q) over all tiles in turn, then its d' times it
+                pf_f32x4 bs[TI][4];
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        bs[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bq[j], pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) bs[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bq[j], bs[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[i][j][e] = fmaf(dj[j], bs[i][j][e], acc[i][j][e]);
+            }
+        } else {
 #pragma unroll
         for (int kk = 0; kk < PF_BK; kk += 32) {
             const int ko = kk + 8 * (lane >> 4);
@@ -527,6 +562,7 @@ __device__ __forceinline__ void pf_gemm_tile_h(const PfGemm& a, const PfSeg& sg,
             for (int i = 0; i < TI; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+        }
         }
     }
     const float wun = ldexpf(1.0f, sg.wexp);
