@@ -8,10 +8,12 @@
 // GEMM numerics: fp16 matrix cores (v_mfma_f32_16x16x32_f16, exact fp16 products summed in f32) on
 // operands of 22 significant bits. launch_pf_split scales each token row of X by a power of two so
 // that its largest magnitude lies in [2^14, 2^15) and writes hi = fp16(x) and lo = fp16(x - hi); the
-// epilogues undo the scale exactly. The weights enter in one of three forms:
+// epilogues undo the scale exactly. The weights enter in one of four forms:
 //  - Q4_K (pf_gemm_tile_q4k): sc q, an integer below 2048, exact in fp16; two products per weight,
 //    each 256-element block's sum scaled by its d in f32 and its min term one more product;
 //  - Q6_K (pf_gemm_tile_q6k): sc q as exact hi / lo fp16 integers; three products, d per block;
+//  - tile-interleaved Q8_0 (pf_gemm_tile_h): the int8 code q, exact in fp16; two products per
+//    weight, each 32-element block's sum scaled by its d in f32;
 //  - the other types (pf_gemm_tile_h): dequantized exactly (the Dequantizer arithmetic), scaled by
 //    a per-matrix power of two (pf_wexp) and split hi / lo; hi_x hi_w + hi_x lo_w + lo_x hi_w,
 //    within 2^-21 of the f32 product.
@@ -353,7 +355,7 @@ template <> struct PfW<PF_ROWS + FLLM_TYPE_BF16> {
 };
 
 // ---- GEMM ---------------------------------------------------------------------------------------
-// Workgroup tile: BM tokens (128 or 64) x 128 weight rows, 4 waves in a 2 x 2 arrangement, each
+// Workgroup tile: BM tokens (64 in every launch) x 128 weight rows, 4 waves in a 2 x 2 arrangement, each
 // (BM / 2) x 64 (BM / 32 x 4 MFMA tiles of 16 x 16). Per K step of 64 the workgroup stages X and the
 // decoded weights into LDS.
 constexpr int PF_BN = 128, PF_BK = 64;
@@ -1372,10 +1374,8 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         g.tiles = (g.N + PF_BN - 1) / PF_BN;
         col_tiles += g.tiles;
     }
-    // 128-token tiles only for grids of at least four of them per CU: the 64-token tiles fit three
-    // workgroups per CU (128-token ones two), and their finer grain wins below that (gate/up at
-    // 511 tokens: 896 tiles of 128 tokens ran 3% slower than 1792 of 64)
-    const bool tall = col_tiles * ((a.T + 127) / 128) >= 4 * (int64_t)(n_cu > 0 ? n_cu : 256);
+    // 64-token tiles at every length: two or three workgroups per CU against one for 128-token
+    // tiles (at 288-352 registers), which ran 15-25% slower even on 4096-token chunks
     PfGemmKernel k;
     size_t lds;
     if (a.xh) {
@@ -1389,32 +1389,32 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
             q46 = q46 && (a.seg[i].type == FLLM_TYPE_Q4_K || a.seg[i].type == FLLM_TYPE_Q6_K);
         }
         if (all_q4k) {
-            k = tall ? k_pf_gemm_q4k<128> : k_pf_gemm_q4k<64>;
-            lds = tall ? pf_gemm_lds_k<128>() : pf_gemm_lds_k<64>();
+            k = k_pf_gemm_q4k<64>;
+            lds = pf_gemm_lds_k<64>();
         } else if (all_q5k) {
-            k = tall ? k_pf_gemm_q5k<128> : k_pf_gemm_q5k<64>;
-            lds = tall ? pf_gemm_lds_k<128>() : pf_gemm_lds_k<64>();
+            k = k_pf_gemm_q5k<64>;
+            lds = pf_gemm_lds_k<64>();
         } else if (all_q6k) {
-            k = tall ? k_pf_gemm_q6k<128> : k_pf_gemm_q6k<64>;
-            lds = tall ? pf_gemm_lds_q6<128>() : pf_gemm_lds_q6<64>();
+            k = k_pf_gemm_q6k<64>;
+            lds = pf_gemm_lds_q6<64>();
         } else if (q46) {
-            k = tall ? k_pf_gemm_q46<128> : k_pf_gemm_q46<64>;
-            lds = tall ? std::max(pf_gemm_lds_k<128>(), pf_gemm_lds_q6<128>()) : std::max(pf_gemm_lds_k<64>(), pf_gemm_lds_q6<64>());
+            k = k_pf_gemm_q46<64>;
+            lds = std::max(pf_gemm_lds_k<64>(), pf_gemm_lds_q6<64>());
         } else {
-            if (tiles) k = tall ? k_pf_gemm_tiles_h<128> : k_pf_gemm_tiles_h<64>;
-            else k = tall ? pf_rows_kernel_h<128>(a.seg[0].type) : pf_rows_kernel_h<64>(a.seg[0].type);
-            lds = tall ? pf_gemm_lds_h<128>() : pf_gemm_lds_h<64>();
+            if (tiles) k = k_pf_gemm_tiles_h<64>;
+            else k = pf_rows_kernel_h<64>(a.seg[0].type);
+            lds = pf_gemm_lds_h<64>();
         }
     } else {
         return hipErrorInvalidValue;  // the fp16 planes are required
     }
     hipError_t e = pf_lds_attr((const void*)k, lds);
     if (e != hipSuccess) return e;
-    const int bm = tall ? 128 : 64;
+    constexpr int bm = 64;
     // a short grid splits K (parts of whole 512-element multiples) when the segments fill the rows
     // of one buffer side by side and the scratch holds the extra parts
     int nsplit = 1;
-    if (!tall && a.part != nullptr) {
+    if (a.part != nullptr) {
         const int64_t base = col_tiles * ((a.T + bm - 1) / bm), want = 2 * (int64_t)(n_cu > 0 ? n_cu : 256);
         bool side_by_side = true;
         int64_t off = 0;
