@@ -1574,7 +1574,13 @@ hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w
 // product and sum is f32.
 constexpr int PF_AQ = 64;
 // key block: 64 positions (32 for head_dim 256, whose block-ahead registers would not fit)
-template <int HD> struct PfAk { static constexpr int v = HD <= 128 ? 64 : 32; };
+template <int HD> struct PfAk {
+    static constexpr int v = HD <= 128 ? 64 : 32;
+    // the next block's rows prefetched into registers (one workgroup per CU); head_dim 256 instead
+    // loads each block when it is staged, at two workgroups per CU (at most 256 registers, LDS for
+    // two), the other workgroup's products covering the loads
+    static constexpr bool pre = HD <= 128;
+};
 
 template <int HD>
 static constexpr size_t pf_attn_lds() {
@@ -1582,7 +1588,7 @@ static constexpr size_t pf_attn_lds() {
 }
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::pre ? 1 : 2))) void k_pf_attn(const PfAttn a) {
     constexpr int LD = HD + 4, NU = HD / 16, NT = HD / 16;
     constexpr int PF_AK = PfAk<HD>::v, KT = PF_AK / 16;  // key block and its 16-key MFMA tiles
     extern __shared__ float pa_lds[];
@@ -1624,30 +1630,50 @@ __global__ __launch_bounds__(256) void k_pf_attn(const PfAttn a) {
     pf_fv pk, pv;
     // piece c = thread + 256 i: key row c / (HD / 4), dims 4 (c % (HD / 4)) .. + 3
     const int jrow = threadIdx.x / (HD / 4), d4 = (threadIdx.x % (HD / 4)) * 4;
+    if constexpr (PfAk<HD>::pre) {
 #pragma unroll
-    for (int i = 0; i < NPC; i++) {
-        const int j = jrow + i * (256 / (HD / 4)), key = kstart + j < kend ? kstart + j : kend;
-        const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
-        const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
-        pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
-        pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
+        for (int i = 0; i < NPC; i++) {
+            const int j = jrow + i * (256 / (HD / 4)), key = kstart + j < kend ? kstart + j : kend;
+            const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
+            const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
+            pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
+            pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
+        }
     }
     for (int kb = kstart; kb <= kend; kb += PF_AK) {
         __syncthreads();  // the previous block's rows have been read
-#pragma unroll
-        for (int i = 0; i < NPC; i++) {
-            const int j = jrow + i * (256 / (HD / 4));
-            *(float4*)(sk + j * LD + d4) = make_float4(pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]);
-            *(float4*)(sv + j * LD + d4) = make_float4(pv[4 * i], pv[4 * i + 1], pv[4 * i + 2], pv[4 * i + 3]);
-        }
-        if (kb + PF_AK <= kend) {
+        if constexpr (PfAk<HD>::pre) {
 #pragma unroll
             for (int i = 0; i < NPC; i++) {
-                const int j = jrow + i * (256 / (HD / 4)), key = kb + PF_AK + j < kend ? kb + PF_AK + j : kend;
+                const int j = jrow + i * (256 / (HD / 4));
+                *(float4*)(sk + j * LD + d4) = make_float4(pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]);
+                *(float4*)(sv + j * LD + d4) = make_float4(pv[4 * i], pv[4 * i + 1], pv[4 * i + 2], pv[4 * i + 3]);
+            }
+            if (kb + PF_AK <= kend) {
+#pragma unroll
+                for (int i = 0; i < NPC; i++) {
+                    const int j = jrow + i * (256 / (HD / 4)), key = kb + PF_AK + j < kend ? kb + PF_AK + j : kend;
+                    const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
+                    const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
+                    pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
+                    pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
+                }
+            }
+        } else {
+            // this block's rows, all loads issued before the stores
+            float4 k4[NPC], v4[NPC];
+#pragma unroll
+            for (int i = 0; i < NPC; i++) {
+                const int j = jrow + i * (256 / (HD / 4)), key = kb + j < kend ? kb + j : kend;
                 const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
-                const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
-                pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
-                pv[4 * i] = v4.x; pv[4 * i + 1] = v4.y; pv[4 * i + 2] = v4.z; pv[4 * i + 3] = v4.w;
+                k4[i] = *(const float4*)(a.kc + off);
+                v4[i] = *(const float4*)(a.vc + off);
+            }
+#pragma unroll
+            for (int i = 0; i < NPC; i++) {
+                const int j = jrow + i * (256 / (HD / 4));
+                *(float4*)(sk + j * LD + d4) = k4[i];
+                *(float4*)(sv + j * LD + d4) = v4[i];
             }
         }
         __syncthreads();
