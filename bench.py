@@ -367,7 +367,7 @@ def profiler_roofline(args, bytes_per_launch, dom_name, steps_launches):
 
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
-Q4_K_TYPE = 12
+Q8_0_TYPE, Q4_K_TYPE, Q5_K_TYPE = 8, 12, 13
 
 
 def prefill_report(cfg, n, seconds, stages=None):
@@ -375,23 +375,32 @@ def prefill_report(cfg, n, seconds, stages=None):
     element-wise steps and the last token's LM head included, so every fraction is a lower bound).
     `tflops`: the reference's own arithmetic, 2 flop per weight per token plus the causal attention's
     4 * heads * head_dim flop per (query, key) pair. The projections run on the fp16 matrix cores:
-    a Q4_K matrix takes two fp16 products per weight (exact integer weights against the activations'
-    hi and lo halves) plus one min-term product per 256-element block (1/8 of a product), any other
-    three (Q6_K: exact integer hi / lo weights; other types: hi / lo splits of both operands); `gemm`
-    is those fp16 products' rate against the fp16 peak. Attention runs on the f32 matrix cores, one
-    product per flop."""
+    a Q4_K or Q5_K matrix takes two fp16 products per weight (exact integer weights against the
+    activations' hi and lo halves) plus one min-term product per 256-element block (1/8 of a
+    product), a Q8_0 one two (its int8 codes against the hi and lo halves), any other three (Q6_K:
+    exact integer hi / lo weights; other types: hi / lo splits of both operands); `gemm` is those
+    fp16 products' rate against the fp16 peak. Attention runs on the f32 matrix cores, one product
+    per flop."""
     H, L, F = cfg["hidden"], cfg["n_layers"], cfg["ffn"]
     hd = cfg["head_dim"]
     qdim, kvdim = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
     ty = cfg["types"]
     weights = L * (qdim * H + 2 * kvdim * H + H * qdim + 3 * F * H)
+    # (query, key) pairs per layer: causal, and inside the sliding window on the layers that have one
+    # (every Mistral layer, Gemma-2's even layers)
     pairs = n * (n + 1) // 2
-    attn = 4.0 * cfg["n_heads"] * hd * pairs * L
+    win = cfg.get("window", 0)
+    if 0 < win < n:
+        pairs_w = win * (win + 1) // 2 + (n - win) * win
+        n_win = L if cfg["arch"] == 1 else (L + 1) // 2 if cfg["arch"] == 3 else 0
+    else:
+        pairs_w, n_win = pairs, 0
+    attn = 4.0 * cfg["n_heads"] * hd * (pairs * (L - n_win) + pairs_w * n_win)
     flops = 2.0 * n * weights + attn
     launches = [((qdim * H, ty["q"]), (kvdim * H, ty["k"]), (kvdim * H, ty["v"])), ((H * qdim, ty["o"]),),
                 ((F * H, ty["gate"]), (F * H, ty["up"])), ((H * F, ty["down"]),)]
     def products(t):
-        return 2.125 if t == Q4_K_TYPE else 3.0
+        return 2.125 if t in (Q4_K_TYPE, Q5_K_TYPE) else 2.0 if t == Q8_0_TYPE else 3.0
 
     fp16 = sum(products(t) * w for g in launches for w, t in g)
     fp16_tf = 2.0 * n * L * fp16 / seconds / 1e12
