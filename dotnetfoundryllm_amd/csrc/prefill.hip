@@ -1573,12 +1573,13 @@ hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w
 // The order of the terms inside the dot products and sums is a permutation of the reference's; every
 // product and sum is f32.
 constexpr int PF_AQ = 64;
-// key block: 64 positions (32 for head_dim 256, whose block-ahead registers would not fit)
+// key block: 64 positions, 32 for head_dim 256 (LDS for two workgroups per CU: 66.5 KB each)
 template <int HD> struct PfAk {
     static constexpr int v = HD <= 128 ? 64 : 32;
-    // the next block's rows prefetched into registers (one workgroup per CU); head_dim 256 instead
-    // loads each block when it is staged, at two workgroups per CU (at most 256 registers, LDS for
-    // two), the other workgroup's products covering the loads
+    // head_dim up to 128: the next block's rows are prefetched into registers while the current one
+    // multiplies (216 registers at 128). Head_dim 256 loads each block when it is staged instead:
+    // the prefetch took it to 300 registers and one workgroup per CU; without it two workgroups
+    // share a CU (at most 256 registers) and each one's products cover the other's loads
     static constexpr bool pre = HD <= 128;
 };
 
