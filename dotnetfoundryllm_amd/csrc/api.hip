@@ -216,6 +216,9 @@ struct fllm_seq {
     int topk_cap = 0;
     float* probs = nullptr;       // distribution left by the nucleus sampler (vocab floats)
     int* samp_token = nullptr;    // its drawn token
+    // pinned host block the samplers' results come back through (the count, the first kPinCand
+    // candidate ids and values; a drawn token), so each call is one DMA round trip
+    int32_t* pin = nullptr;
     int* pen_counts = nullptr;    // repetition-penalty counters (vocab ints, zero between calls)
     int* pen_ids = nullptr;       // the penalised ids of the last call (device copy)
     TopkScratch* topk_sc = nullptr;  // grid top-k: threshold, segment counts, candidates
@@ -870,6 +873,7 @@ static hipError_t seq_alloc(fllm_seq* s, T** p, size_t count) {
 }
 
 static void seq_free(fllm_seq* s) {
+    if (s->pin) hipHostFree(s->pin);
     if (s->gexec) hipGraphExecDestroy(s->gexec);
     if (s->graph) hipGraphDestroy(s->graph);
     for (void* p : s->allocs) hipFree(p);
@@ -1832,6 +1836,14 @@ extern "C" int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token) {
     return FLLM_OK;
 }
 
+static const int kPinCand = 256;  // candidates the pinned block holds
+
+// the sequence's pinned result block: [0] count or token, [16, 16 + kPinCand) ids, then kPinCand values
+static hipError_t seq_pin(fllm_seq* s) {
+    if (s->pin) return hipSuccess;
+    return hipHostMalloc((void**)&s->pin, sizeof(int32_t) * (16 + 2 * (size_t)kPinCand), hipHostMallocDefault);
+}
+
 extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int32_t* ids, float* vals, int32_t cap,
                                     int32_t* n_out) {
     NOT_NULL(s);
@@ -1847,16 +1859,35 @@ extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int3
     HIP_TRY(launch_topk(s->logits, V, inv_temp, k, dcap, s->topk_ids, s->topk_vals, s->topk_count, s->topk_sc, s->st));
     if (inv_temp != 1.0f) s->argmax_valid = false;
     // one round trip for the usual case: the count and the first candidates (as many as k, at
-    // least 64, at most cap) come back together; only more survivors than that need a second copy
+    // least 64, at most cap) come back together, through the pinned block when they fit in it;
+    // only more survivors than that need a second copy
     int cnt = 0;
     int first = k < 64 ? 64 : k;
     first = first < dcap ? first : dcap;
-    HIP_TRY(hipMemcpyAsync(&cnt, s->topk_count, sizeof(int), hipMemcpyDeviceToHost, s->st));
-    if (first > 0) {
-        HIP_TRY(hipMemcpyAsync(ids, s->topk_ids, sizeof(int) * (size_t)first, hipMemcpyDeviceToHost, s->st));
-        HIP_TRY(hipMemcpyAsync(vals, s->topk_vals, sizeof(float) * (size_t)first, hipMemcpyDeviceToHost, s->st));
+    const bool pinned = first <= kPinCand && seq_pin(s) == hipSuccess;
+    if (pinned) {
+        HIP_TRY(hipMemcpyAsync(s->pin, s->topk_count, sizeof(int), hipMemcpyDeviceToHost, s->st));
+        if (first > 0) {
+            HIP_TRY(hipMemcpyAsync(s->pin + 16, s->topk_ids, sizeof(int) * (size_t)first, hipMemcpyDeviceToHost, s->st));
+            HIP_TRY(hipMemcpyAsync(s->pin + 16 + kPinCand, s->topk_vals, sizeof(float) * (size_t)first,
+                                   hipMemcpyDeviceToHost, s->st));
+        }
+        HIP_TRY(hipStreamSynchronize(s->st));
+        cnt = s->pin[0];
+        // the caller receives at most the survivors (fewer than `first` when fewer survive)
+        const int got = cnt < first ? (cnt > 0 ? cnt : 0) : first;
+        if (got > 0) {
+            memcpy(ids, s->pin + 16, sizeof(int) * (size_t)got);
+            memcpy(vals, s->pin + 16 + kPinCand, sizeof(float) * (size_t)got);
+        }
+    } else {
+        HIP_TRY(hipMemcpyAsync(&cnt, s->topk_count, sizeof(int), hipMemcpyDeviceToHost, s->st));
+        if (first > 0) {
+            HIP_TRY(hipMemcpyAsync(ids, s->topk_ids, sizeof(int) * (size_t)first, hipMemcpyDeviceToHost, s->st));
+            HIP_TRY(hipMemcpyAsync(vals, s->topk_vals, sizeof(float) * (size_t)first, hipMemcpyDeviceToHost, s->st));
+        }
+        HIP_TRY(hipStreamSynchronize(s->st));
     }
-    HIP_TRY(hipStreamSynchronize(s->st));
     *n_out = cnt;
     if (cnt > cap) return fail(FLLM_E_ARG, "%d candidates survive top-%d, capacity %d", cnt, k, cap);
     if (cnt > first) {
@@ -1907,8 +1938,14 @@ extern "C" int32_t fllm_sample_nucleus(fllm_seq* s, float inv_temp, float top_p,
     HIP_TRY(launch_sample_nucleus(s->logits, V, inv_temp, top_p, u, s->probs, s->samp_token, s->nuc_sc, s->st));
     if (inv_temp != 1.0f) s->argmax_valid = false;
     int tok = 0;
-    HIP_TRY(hipMemcpyAsync(&tok, s->samp_token, sizeof(int), hipMemcpyDeviceToHost, s->st));
-    HIP_TRY(hipStreamSynchronize(s->st));
+    if (seq_pin(s) == hipSuccess) {
+        HIP_TRY(hipMemcpyAsync(s->pin, s->samp_token, sizeof(int), hipMemcpyDeviceToHost, s->st));
+        HIP_TRY(hipStreamSynchronize(s->st));
+        tok = s->pin[0];
+    } else {
+        HIP_TRY(hipMemcpyAsync(&tok, s->samp_token, sizeof(int), hipMemcpyDeviceToHost, s->st));
+        HIP_TRY(hipStreamSynchronize(s->st));
+    }
     *out_token = tok;
     return FLLM_OK;
 }
