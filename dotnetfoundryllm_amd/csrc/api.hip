@@ -4,6 +4,7 @@
 // entry points. No C++ exception crosses the ABI.
 #include <math.h>
 #include <stdarg.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -1822,6 +1823,14 @@ extern "C" int32_t fllm_logits_write(fllm_seq* s, const float* src, int64_t n) {
     return FLLM_OK;
 }
 
+static const int kPinCand = 256;  // candidates the pinned block holds
+
+// the sequence's pinned result block: [0] count or token, [16, 16 + kPinCand) ids, then kPinCand values
+static hipError_t seq_pin(fllm_seq* s) {
+    if (s->pin) return hipSuccess;
+    return hipHostMalloc((void**)&s->pin, sizeof(int32_t) * (16 + 2 * (size_t)kPinCand), hipHostMallocDefault);
+}
+
 extern "C" int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token) {
     NOT_NULL(s);
     NOT_NULL(out_token);
@@ -1829,19 +1838,18 @@ extern "C" int32_t fllm_sample_greedy(fllm_seq* s, int32_t* out_token) {
     // logits were changed on the host or by the top-k sampler
     if (!s->argmax_valid) HIP_TRY(launch_argmax(s->logits, s->m->d.vocab, s->params, nullptr, 0, s->st));
     s->argmax_valid = true;
+    if (seq_pin(s) == hipSuccess) {
+        HIP_TRY(hipMemcpyAsync(s->pin, (const uint8_t*)s->params + offsetof(StepParams, argmax), sizeof(int32_t),
+                               hipMemcpyDeviceToHost, s->st));
+        HIP_TRY(hipStreamSynchronize(s->st));
+        *out_token = s->pin[0];
+        return FLLM_OK;
+    }
     StepParams hp;
     HIP_TRY(hipMemcpyAsync(&hp, s->params, sizeof(hp), hipMemcpyDeviceToHost, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));
     *out_token = hp.argmax;
     return FLLM_OK;
-}
-
-static const int kPinCand = 256;  // candidates the pinned block holds
-
-// the sequence's pinned result block: [0] count or token, [16, 16 + kPinCand) ids, then kPinCand values
-static hipError_t seq_pin(fllm_seq* s) {
-    if (s->pin) return hipSuccess;
-    return hipHostMalloc((void**)&s->pin, sizeof(int32_t) * (16 + 2 * (size_t)kPinCand), hipHostMallocDefault);
 }
 
 extern "C" int32_t fllm_sample_topk(fllm_seq* s, float inv_temp, int32_t k, int32_t* ids, float* vals, int32_t cap,
