@@ -1427,6 +1427,14 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         while (side_by_side && nsplit < 4 && base * nsplit < want && a.K % (512 * nsplit) == 0 &&
                (size_t)(2 * nsplit - 1) * (size_t)a.T * (size_t)a.seg[0].ldy <= a.part_cap)
             nsplit *= 2;
+        // once more when the split grid ends in a partly filled wave of resident workgroups and
+        // shorter parts shorten the whole: waves x part length, w_next / 2 nsplit < w_now / nsplit
+        // (q/k/v at 511 tokens: 384 tiles in 2 parts are 1.5 waves of 512, in 4 parts 3)
+        if (side_by_side && nsplit > 1 && nsplit < 4 && a.K % (512 * nsplit) == 0 &&
+            (size_t)(2 * nsplit - 1) * (size_t)a.T * (size_t)a.seg[0].ldy <= a.part_cap) {
+            const int64_t w_now = (base * nsplit + want - 1) / want, w_next = (base * 2 * nsplit + want - 1) / want;
+            if (w_next < 2 * w_now) nsplit *= 2;
+        }
     }
     a.nsplit = nsplit;
     a.kpart = a.K / nsplit;
