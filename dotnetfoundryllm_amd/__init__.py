@@ -383,7 +383,7 @@ def set_debug(kv, enable):
 
 
 def set_prefill_chunk(kv, tokens):
-    """Tokens per pass of the batched prefill (before the sequence's first batched prefill)."""
+    """Tokens per pass of the batched prefill (for the sequence's later prefills)."""
     _check(N.dev.fllm_seq_set_prefill_chunk(kv.h, int(tokens)))
 
 

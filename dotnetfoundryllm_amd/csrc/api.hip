@@ -239,9 +239,10 @@ struct fllm_seq {
     std::vector<std::string> agg_order;
     std::vector<std::string> launch_names;  // every profiled launch in order (bounded)
     std::vector<void*> allocs;
-    // batched prefill scratch for chunks of up to pf_cap = min(max_seq, pf_chunk) tokens (allocated
-    // on first use)
+    // batched prefill: passes of up to pf_chunk tokens; scratch for pf_cap rows, sized by the
+    // prompts seen (a multiple of 256 up to min(max_seq, pf_chunk)) and grown when a longer one comes
     int pf_chunk = 4096, pf_cap = 0, pf_ldx = 0;
+    std::vector<void*> pf_allocs;
     float *pf_x = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_gu = nullptr, *pf_tmp = nullptr;
     float* pf_part = nullptr;  // K-split partial products of the short GEMM launches
     size_t pf_part_cap = 0;
@@ -875,6 +876,7 @@ static hipError_t seq_alloc(fllm_seq* s, T** p, size_t count) {
 
 static void seq_free(fllm_seq* s) {
     if (s->pin) hipHostFree(s->pin);
+    for (void* p : s->pf_allocs) hipFree(p);
     if (s->gexec) hipGraphExecDestroy(s->gexec);
     if (s->graph) hipGraphDestroy(s->graph);
     for (void* p : s->allocs) hipFree(p);
@@ -1100,10 +1102,7 @@ extern "C" int32_t fllm_seq_set_graph(fllm_seq* s, int32_t enable) {
 extern "C" int32_t fllm_seq_set_prefill_chunk(fllm_seq* s, int32_t tokens) {
     NOT_NULL(s);
     if (tokens < 1) return fail(FLLM_E_ARG_RANGE, "prefill chunk must be >= 1 token");
-    // the chunk buffers are sized on the first batched prefill and kept for the sequence's life
-    if (s->pf_cap > 0 && tokens != s->pf_chunk)
-        return fail(FLLM_E_INVALID_OP, "the prefill chunk is fixed once a batched prefill has run");
-    s->pf_chunk = tokens;
+    s->pf_chunk = tokens;  // later prefills; the scratch grows at the next one if it needs to
     return FLLM_OK;
 }
 
@@ -1595,16 +1594,50 @@ static bool prefill_batched_ok(const fllm_seq* s) {
            d.hidden % 32 == 0 && s->m->qdim % 32 == 0 && d.ffn % 32 == 0;
 }
 
-static hipError_t prefill_alloc(fllm_seq* s) {
-    if (s->pf_cap > 0) return hipSuccess;
+// tokens per pass of a prefill of n tokens: at most pf_chunk and the capacity
+static int prefill_pass(const fllm_seq* s) {
+    return s->max_seq < s->pf_chunk ? s->max_seq : s->pf_chunk;
+}
+
+static void prefill_release(fllm_seq* s) {
+    for (void* p : s->pf_allocs) hipFree(p);
+    s->pf_allocs.clear();
+    s->pf_x = s->pf_xn = s->pf_qkv = s->pf_att = s->pf_gu = s->pf_tmp = s->pf_part = nullptr;
+    s->pf_xh = nullptr;
+    s->pf_xs = nullptr;
+    s->pf_tok = nullptr;
+    s->pf_cap = 0;
+    s->pf_part_cap = 0;
+}
+
+// scratch for passes over n tokens: rows for min(pass, n rounded up to 256); kept and reused while
+// it holds enough (about 0.4 MB per row at 8B-model widths), replaced by a larger one otherwise
+static hipError_t prefill_alloc(fllm_seq* s, int n) {
+    const int pass = prefill_pass(s);
+    int want = (n + 255) / 256 * 256;
+    want = want < pass ? want : pass;
+    if (s->pf_cap >= want) return hipSuccess;
+    if (s->pf_cap > 0) {
+        hipError_t e = hipStreamSynchronize(s->st);  // nothing queued may still use the old rows
+        if (e != hipSuccess) return e;
+        prefill_release(s);
+    }
     const fllm_model& m = *s->m;
-    const int cap = s->max_seq < s->pf_chunk ? s->max_seq : s->pf_chunk;
+    const int cap = want;
     size_t ldx = (size_t)std::max(m.d.hidden, m.d.ffn);
     ldx = (ldx + 3) / 4 * 4;
     const size_t H = (size_t)m.d.hidden, C = (size_t)cap;
     hipError_t e = hipSuccess;
-#define PF_ALLOC(ptr, count) \
-    if (e == hipSuccess) e = seq_alloc(s, &(ptr), (count))
+    auto pf_alloc = [&](auto** ptr, size_t count) {
+        if (e != hipSuccess) return;
+        void* v = nullptr;
+        e = hipMalloc(&v, sizeof(**ptr) * (count ? count : 1));
+        if (e == hipSuccess) {
+            s->pf_allocs.push_back(v);
+            *ptr = (std::remove_reference_t<decltype(*ptr)>)v;
+        }
+    };
+#define PF_ALLOC(ptr, count) pf_alloc(&(ptr), (count))
     PF_ALLOC(s->pf_x, C * H);
     PF_ALLOC(s->pf_qkv, C * (size_t)(m.qdim + 2 * m.kvdim));
     PF_ALLOC(s->pf_att, C * (size_t)m.qdim);
@@ -1623,6 +1656,8 @@ static hipError_t prefill_alloc(fllm_seq* s) {
         s->pf_cap = cap;
         s->pf_ldx = (int)ldx;
         s->pf_part_cap = part_cap;
+    } else {
+        prefill_release(s);
     }
     return e;
 }
@@ -1776,11 +1811,13 @@ extern "C" int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, i
     if ((int64_t)s->cur_len + n > s->max_seq)
         return fail(FLLM_E_ARG_RANGE, "KV cache full (%d positions)", s->max_seq);
     HIP_TRY(hipSetDevice(s->m->ctx->device));
-    hipError_t e = prefill_alloc(s);
+    hipError_t e = prefill_alloc(s, n);
     if (e != hipSuccess) return fail(FLLM_E_OOM, "prefill scratch: %s", hipGetErrorString(e));
+    // tokens per pass: the chunk, within the rows the scratch holds
+    const int pass = std::min(prefill_pass(s), s->pf_cap);
     int done = 0;
     while (done < n) {
-        const int T = n - done < s->pf_cap ? n - done : s->pf_cap;
+        const int T = n - done < pass ? n - done : pass;
         e = hipMemcpyAsync(s->pf_tok, tokens + done, sizeof(int32_t) * (size_t)T, hipMemcpyHostToDevice, s->st);
         if (e == hipSuccess) e = prefill_chunk(s, T, pos0 + done);
         if (e == hipSuccess) e = prof_collect(s);
@@ -1791,7 +1828,7 @@ extern "C" int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, i
         s->cur_len = pos0 + done;
     }
     // the last token's logits and greedy token, with the step parameters of its Forward call
-    const int T_last = n - ((n - 1) / s->pf_cap) * s->pf_cap;
+    const int T_last = n - ((n - 1) / pass) * pass;
     e = hipMemcpyAsync(s->x, s->pf_x + (size_t)(T_last - 1) * d.hidden, sizeof(float) * (size_t)d.hidden,
                        hipMemcpyDeviceToDevice, s->st);
     if (e == hipSuccess) e = launch_set_params(s->params, tokens[n - 1], pos0 + n - 1, pos0 + n - 1, s->st);

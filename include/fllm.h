@@ -176,9 +176,9 @@ FLLM_API int32_t fllm_seq_set_graph(fllm_seq* s, int32_t enable);
 /* Tokens per pass of the batched prefill through the layers (default 4096, capped at the
  * capacity): each pass's projections are GEMMs over that many rows and its attention a grid over
  * them, so long prompts fill the GPU. A tuning knob with no counterpart in the reference (whose
- * prefill is one Forward per token). Only before the sequence's first batched prefill, which sizes
- * the chunk buffers: later calls with another value return FLLM_E_INVALID_OP; tokens < 1 returns
- * FLLM_E_ARG_RANGE. */
+ * prefill is one Forward per token). Applies to later prefills; the sequence's prefill scratch
+ * holds rows for the longest pass seen so far (the prompt rounded up to 256, at most one pass) and
+ * grows when a prefill needs more. tokens < 1 returns FLLM_E_ARG_RANGE. */
 FLLM_API int32_t fllm_seq_set_prefill_chunk(fllm_seq* s, int32_t tokens);
 /* 1 = keep the residual stream after every layer for fllm_debug_hidden (parity hook). */
 FLLM_API int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable);

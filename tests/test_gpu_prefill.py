@@ -81,9 +81,9 @@ def test_batched_prefill_matches_oracle_and_stepwise(ctx, name):
 
 def test_prefill_chunk_contract(ctx):
     """fllm_seq_set_prefill_chunk: tokens < 1 is out of range; a chunk of 24 tokens takes a 61-token
-    prompt in passes of 24, 24 and 13 (logits, K/V and the greedy token against the oracle); once a
-    batched prefill has sized the chunk buffers another value is an invalid operation, the same
-    value is accepted, and a reset keeps the chunk."""
+    prompt in passes of 24, 24 and 13 (logits, K/V and the greedy token against the oracle); after
+    it, a chunk of 40 makes the next prefill replace the 24-row scratch with a 40-row one, and a
+    30-token prompt in one pass stores the same K/V rows as the oracle's first 30 positions."""
     cfg, desc, tensors = synthetic("test-llama")
     m = device_model(ctx, desc, tensors)
     kv = F.HipKvCache(m)
@@ -104,12 +104,14 @@ def test_prefill_chunk_contract(ctx):
             assert O.normwise_rel_err(kv.get_keys(l), orc.kv(l, 0)) <= TOL
             assert O.normwise_rel_err(kv.get_values(l), orc.kv(l, 1)) <= TOL
         assert fwd.sample_greedy() == int(O.lib.orc_argmax(O.fp(want), want.size))
-        with pytest.raises(F.InvalidOperationException):
-            F.set_prefill_chunk(kv, 32)
-        F.set_prefill_chunk(kv, 24)
+        F.set_prefill_chunk(kv, 40)
         kv.clear()
         fwd.prefill(prompt[:30], 0, kv)
         assert kv.current_length == 30
+        kvdim = desc.n_kv_heads * desc.head_dim
+        for l in range(desc.n_layers):
+            for got, kind in ((kv.get_keys(l), 0), (kv.get_values(l), 1)):
+                assert O.normwise_rel_err(got, orc.kv(l, kind)[: 30 * kvdim]) <= TOL, (l, kind)
     finally:
         orc.close()
         kv.close()
