@@ -237,7 +237,8 @@ def test_topk_sample_select_and_fallback(big_vocab):
     """Top-k over the 32000 vocabulary: the sample-select path (a threshold from 2048 evenly spaced
     entries, then an exact select among the entries reaching it) and both of its fallbacks to the
     full radix select (too few entries reach the sample's threshold; too many, with all logits
-    equal) give the oracle's survivors, ties kept, in index order."""
+    equal) give the oracle's survivors, ties kept, in index order; k up to 256 returns through the
+    sequence's pinned result block, k = 300 through the caller's arrays."""
     desc, m, kv, fwd = big_vocab
     V = desc.vocab
     rng = np.random.default_rng(17)
@@ -253,6 +254,7 @@ def test_topk_sample_select_and_fallback(big_vocab):
     cases.append((np.full(V, 0.5, dtype=np.float32), 40))  # every entry ties
     lg = np.round(rng.standard_normal(V) * 2, 1).astype(np.float32)
     cases.append((lg, 256))
+    cases.append((lg, 300))  # more candidates than the pinned result block holds
     cases.append((lg, 1))
     for lg, k in cases:
         for inv in (1.0, 1.25):
