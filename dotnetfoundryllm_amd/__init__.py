@@ -303,6 +303,7 @@ class HipForwardPass:
 
     def __init__(self, model):
         self.model = model
+        self._kv = None
 
     def forward(self, token_id, position, kv):
         if kv is None:
@@ -330,6 +331,9 @@ class HipForwardPass:
 
     @property
     def logits(self):
+        # before the first Forward: zeros, as LlamaForwardPass's fresh _logits (LlamaForwardPass.cs:38)
+        if self._kv is None:
+            return np.zeros(self.model.desc.vocab, dtype=np.float32)
         out = np.empty(self.model.desc.vocab, dtype=np.float32)
         _check(N.dev.fllm_logits_copy(self._kv.h, _fptr(out), out.size))
         return out

@@ -85,6 +85,9 @@ static __device__ __align__(256) uint8_t scratch[kNoallocSrcRegion + kNoallocEle
 static const int kMaxDevices = 64;
 static uint8_t* g_scratch_dev[kMaxDevices];  // per device, set once with that device current
 static std::mutex g_scratch_mu;
+// held by fllm_dequantize_noalloc from its first copy to its stream sync, so calls from other
+// threads or contexts on the same device take the array one after the other
+static std::mutex g_scratch_use[kMaxDevices];
 
 // Resolves this device's scratch address once (the device is current).
 static hipError_t scratch_init(int device, uint8_t** out) {
@@ -344,7 +347,8 @@ extern "C" int32_t fllm_dequantize(fllm_ctx* ctx, int32_t type, const void* src,
 
 // fllm_dequantize without allocating: the source blocks and the floats go through this device's
 // scratch array (its address resolved at context creation), so nothing is allocated or freed.
-// Calls that overlap on one device (other threads or streams) share the array and race.
+// The call is synchronous and holds the device's lock on the array for its whole use, so calls
+// from several threads or contexts on one device are serialized rather than racing.
 extern "C" int32_t fllm_dequantize_noalloc(fllm_ctx* ctx, int32_t type, const void* src, uint64_t nbytes, float* dst,
                                            int64_t n) {
     NOT_NULL(ctx);
@@ -367,6 +371,7 @@ extern "C" int32_t fllm_dequantize_noalloc(fllm_ctx* ctx, int32_t type, const vo
         return fail(FLLM_E_DEVICE, "hipGetSymbolAddress(scratch) failed at context creation: %s",
                     hipGetErrorString(ctx->scratch_err));
     HIP_TRY(hipSetDevice(ctx->device));
+    std::lock_guard<std::mutex> use(g_scratch_use[ctx->device]);
     uint8_t* dsrc = ctx->scratch;
     float* ddst = (float*)(ctx->scratch + kNoallocSrcRegion);
     hipError_t e = hipMemcpyAsync(dsrc, src, nbytes, hipMemcpyHostToDevice, ctx->stream);
@@ -1526,8 +1531,13 @@ extern "C" int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position) {
     if (position > s->cur_len) {
         // The reference appends layer 0 at the current length, then attention slices positions
         // [0, position] of a cache that holds cur_len + 1 and throws (LlamaForwardPass.cs:186-188):
-        // the cache is left expecting layer 1. That state is kept here (the row of layer 0 holds
-        // zeros instead of the failed token's keys); nothing is launched.
+        // the cache is left expecting layer 1. That state is kept here, with layer 0's row at the
+        // slot cleared to zeros instead of the failed token's keys and values (the slot may hold a
+        // row of an earlier use of the cache, before a reset or an eviction).
+        const size_t row = (size_t)s->cur_len * s->m->kvdim;
+        const size_t nb = sizeof(float) * (size_t)s->m->kvdim;
+        HIP_TRY(hipMemsetAsync(s->kc + row, 0, nb, s->st));
+        HIP_TRY(hipMemsetAsync(s->vc + row, 0, nb, s->st));
         if (++s->next_layer == d.n_layers) {
             s->next_layer = 0;
             s->cur_len++;
@@ -1796,6 +1806,16 @@ extern "C" int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, i
     // The batched path runs when the positions continue the cache (the case of a prompt); with
     // debug capture, a single token, or positions that rewrite earlier slots it is n Forward calls.
     const bool batched = n >= 2 && pos0 == s->cur_len && !s->debug && prefill_batched_ok(s);
+    // The checks of n Forward calls, before anything runs, on both paths: a prompt with an invalid
+    // token or more positions than the cache has left is rejected with the cache unchanged (each
+    // Forward appends one position). The per-token fllm_forward keeps the reference's
+    // evict-then-throw at a full cache; a prompt does not start that way part-done.
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= d.vocab)
+            return fail(FLLM_E_ARG_RANGE, "Token id %d is outside the valid vocabulary range [0, %d].", tokens[i],
+                        d.vocab - 1);
+    if ((int64_t)s->cur_len + n > s->max_seq)
+        return fail(FLLM_E_ARG_RANGE, "KV cache full (%d positions)", s->max_seq);
     if (!batched) {
         for (int i = 0; i < n; i++) {
             int32_t rc = fllm_forward(s, tokens[i], pos0 + i);
@@ -1803,13 +1823,6 @@ extern "C" int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, i
         }
         return FLLM_OK;
     }
-    // the checks of n Forward calls, before anything runs
-    for (int i = 0; i < n; i++)
-        if (tokens[i] < 0 || tokens[i] >= d.vocab)
-            return fail(FLLM_E_ARG_RANGE, "Token id %d is outside the valid vocabulary range [0, %d].", tokens[i],
-                        d.vocab - 1);
-    if ((int64_t)s->cur_len + n > s->max_seq)
-        return fail(FLLM_E_ARG_RANGE, "KV cache full (%d positions)", s->max_seq);
     HIP_TRY(hipSetDevice(s->m->ctx->device));
     hipError_t e = prefill_alloc(s, n);
     if (e != hipSuccess) return fail(FLLM_E_OOM, "prefill scratch: %s", hipGetErrorString(e));

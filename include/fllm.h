@@ -155,7 +155,9 @@ FLLM_API int32_t fllm_model_finalize(fllm_model* m);
  * (LlamaForwardPass.cs:87, LlamaWeights.cs:138-139), as do upload, finalize and seq_create while
  * the handle is still valid. The device memory is released at once when no sequence of the model
  * is alive, otherwise when the last one is destroyed (sequences keep using the weights until
- * then, so destroy never frees memory a sequence still reads). Idempotent. */
+ * then, so destroy never frees memory a sequence still reads). Repeated calls are harmless while a
+ * sequence of the model is alive; once destroy has released the model (no sequence left) the
+ * handle is invalid and must not be passed again. */
 FLLM_API int32_t fllm_model_destroy(fllm_model* m);
 /* The description the model was created with. */
 FLLM_API int32_t fllm_model_get_desc(fllm_model* m, fllm_model_desc* out);
@@ -202,7 +204,10 @@ FLLM_API int32_t fllm_forward(fllm_seq* s, int32_t token, int32_t position);
  * position's logits and greedy token. When pos0 is the cache's current length (a prompt) and debug
  * capture is off, the tokens go through each layer together in chunks (fllm_seq_set_prefill_chunk;
  * fp16 matrix-core GEMMs over the chunk, causal attention over the cache); otherwise, and for n = 1,
- * it is n fllm_forward calls. Token ids and the cache capacity are checked before anything runs. */
+ * it is n fllm_forward calls. On both paths the token ids and the cache capacity are checked before
+ * anything runs: a prompt that would overflow the cache (current length + n > capacity) returns
+ * FLLM_E_ARG_RANGE with the cache unchanged (no eviction), unlike a lone fllm_forward at a full
+ * cache, which evicts the oldest half first as KvCache.Append does (KvCache.cs:82-85). */
 FLLM_API int32_t fllm_prefill(fllm_seq* s, const int32_t* tokens, int32_t n, int32_t pos0);
 /* The greedy part of LlamaLanguageModel.GenerateAsync's decode loop (LlamaLanguageModel.cs:162-293
  * with SamplerPipeline Temperature == 0, SamplerPipeline.cs:61-64, no EOS stop): n_steps Forward
@@ -292,8 +297,9 @@ FLLM_API int32_t fllm_dequantize(fllm_ctx* ctx, int32_t type, const void* src, u
  * floats are staged through a fixed scratch array in device memory that the library holds per
  * device for the life of the process (FLLM_NOALLOC_MAX_BYTES source bytes and FLLM_NOALLOC_MAX_ELEMS
  * floats); larger calls return FLLM_E_ARG. Same results and error contract as fllm_dequantize
- * otherwise. Every call on one device uses the same array: calls that overlap on one device (from
- * several threads or contexts) race. */
+ * otherwise. Every call on one device uses the same array; the call is synchronous and holds a
+ * per-device lock on it throughout, so calls from several threads or contexts on one device run
+ * one after the other. */
 #define FLLM_NOALLOC_MAX_BYTES (2u << 20)
 #define FLLM_NOALLOC_MAX_ELEMS (2u << 20)
 FLLM_API int32_t fllm_dequantize_noalloc(fllm_ctx* ctx, int32_t type, const void* src, uint64_t nbytes,

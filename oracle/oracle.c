@@ -15,8 +15,12 @@
  *    vendored and stays unpinned at the bit level (tolerance-pinned only).
  *  - norms, activations, softcap, softmax, RoPE: closed forms checked in tests; bit-level
  *    parity with TensorPrimitives' vectorised Exp/Tanh/Sigmoid is unpinned.
- *  - argmax / top-k / xoshiro256**: integer-exact; pinned by the reference's sampler tests
- *    and the published xoshiro256** / SplitMix64 algorithm.
+ *  - argmax / top-k: integer-exact; pinned by the reference's sampler tests.
+ *  - xoshiro256** (orc_xoshiro_*): integer-exact; pinned by published known answers that no
+ *    code here computes: SplitMix64 from seeds 1234567 (Rosetta Code) and 0 (Vigna's
+ *    splitmix64.c outputs) as the seeded state, and the xoshiro256** vector from the state
+ *    {1, 2, 3, 4} (rand_xoshiro's reference test; its first three values follow by hand);
+ *    NextFloat by its closed form on those outputs (tests/test_oracle_ops.py).
  *  - top-p (orc_apply_top_p): pinned by TopPSamplerTests.cs's cases and by the nucleus
  *    invariants (kept mass reaches p, dropping the smallest kept entry falls below it, every
  *    kept probability is at least every dropped one); the order among equal probabilities at

@@ -4,7 +4,8 @@
   then 64 greedy tokens identical to the oracle's (LlamaLanguageModel.cs:131-166,
   LlamaForwardPass.cs:82-130), twice: from a host loop of Forward + device argmax, where every step's
   eight largest oracle logits must match within 1e-3 of the largest logit and the first and last
-  steps' logits within normwise 1e-3; and from the device-side loop fllm_decode_greedy after a
+  steps' logits within normwise 1e-3 (asserted at 1e-5, near the measured 6e-7), every step's top-8
+  absolute error below a tenth of the oracle's top-1/top-2 gap; and from the device-side loop fllm_decode_greedy after a
   fresh prefill. The seeded random-init model of this shape settles on one token (its K-quant
   weights have a positive mean), with an oracle top-1/top-2 gap of at least 0.59 at |logit| about
   712 at every step, so the logit checks carry most of the weight. A divergence is reported with
@@ -29,7 +30,13 @@ from fixtures import synthetic, upload
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
-TOL = 1e-3
+TOL = 1e-3  # the parity bar on logits and hidden states (normwise relative)
+# Regression bars near what the device path measures (5-7e-7 on the Llama-3-8B shape at full
+# depth, 3-4e-6 on the Gemma-2 long-context model, 1.4e-5 on the two-layer file-loaded model):
+# far inside the parity bar, so a numerical regression shows before it reaches it.
+TIGHT_LLAMA = 1e-5
+TIGHT_GEMMA_LONG = 2e-5
+TIGHT_GGUF = 5e-5
 
 
 def say(msg):
@@ -62,7 +69,7 @@ def test_llama3_8b_full_depth_greedy(ctx):
     try:
         # 1. host loop: Forward + device argmax per step, the logits of every step checked
         fwd.prefill(prompt[:-1], 0, kv)
-        nxt, toks, worst_top = int(prompt[-1]), [], 0.0
+        nxt, toks, worst_top, worst_gap_frac = int(prompt[-1]), [], 0.0, 0.0
         for step in range(steps):
             fwd.forward(nxt, n + step, kv)
             lg = fwd.logits
@@ -72,12 +79,20 @@ def test_llama3_8b_full_depth_greedy(ctx):
                 err_last = O.normwise_rel_err(lg, g["logits_last"])
             # the oracle's eight largest logits: same values within the parity bar, same order
             ids = g["top_ids"][step]
-            worst_top = max(worst_top, float(np.max(np.abs(lg[ids] - g["top_val"][step]))) / float(np.max(np.abs(lg))))
+            top_abs = float(np.max(np.abs(lg[ids] - g["top_val"][step])))
+            worst_top = max(worst_top, top_abs / float(np.max(np.abs(lg))))
+            # the identity of the greedy token is more than luck only if the device's error on the
+            # leading logits is small against the oracle's top-1/top-2 gap at that step
+            gap_frac = top_abs / float(g["gap"][step])
+            worst_gap_frac = max(worst_gap_frac, gap_frac)
+            assert gap_frac < 0.1, (f"step {step}: top-8 absolute error {top_abs:.3g} is not below a tenth of the "
+                                    f"oracle's top-1/top-2 gap {float(g['gap'][step]):.3g}")
             nxt = fwd.sample_greedy()
             toks.append(nxt)
-        say(f"logits error: first step {err_first:.2e}, last step {err_last:.2e}, top-8 of every step {worst_top:.2e}")
+        say(f"logits error: first step {err_first:.2e}, last step {err_last:.2e}, top-8 of every step {worst_top:.2e}, "
+            f"top-8 absolute error at most {worst_gap_frac:.2e} of the step's top-1/top-2 gap")
         check_tokens(toks, "Forward loop")
-        assert err_first <= TOL and err_last <= TOL and worst_top <= TOL
+        assert err_first <= TIGHT_LLAMA and err_last <= TIGHT_LLAMA and worst_top <= TIGHT_LLAMA
         # 2. the device-side loop from a fresh prefill: the same tokens
         kv.clear()
         fwd.prefill(prompt[:-1], 0, kv)
@@ -85,7 +100,7 @@ def test_llama3_8b_full_depth_greedy(ctx):
         toks = [fwd.sample_greedy()]
         toks += [int(t) for t in fwd.decode_greedy(toks[0], n + 1, steps - 1, kv)]
         check_tokens(toks, "fllm_decode_greedy")
-        assert O.normwise_rel_err(fwd.logits, g["logits_last"]) <= TOL
+        assert O.normwise_rel_err(fwd.logits, g["logits_last"]) <= TIGHT_LLAMA
         say(f"{steps} greedy tokens identical on both paths; smallest oracle gap {float(g['gap'].min()):.3g}")
     finally:
         kv.close()
@@ -117,7 +132,7 @@ def test_gemma2_long_context_window(ctx, chunk):
             toks.append(nxt)
         say(f"decode logits worst error {worst:.2e}")
         assert toks == [int(t) for t in g["tokens"]]
-        assert worst <= TOL
+        assert worst <= TIGHT_GEMMA_LONG
         pos = g["kv_positions"]
         for l in range(desc.n_layers):
             K = kv.get_keys(l).reshape(kv.current_length, -1)[pos]
@@ -176,7 +191,7 @@ def test_gguf_full_width_file_matches_oracle(ctx, tmp_path):
             nxt_d, nxt_o = fwd.sample_greedy(), int(np.argmax(lg))
             assert nxt_d == nxt_o, f"greedy token at step {step}"
         say(f"logits worst normwise error {worst:.2e}")
-        assert worst <= TOL
+        assert worst <= TIGHT_GGUF
     finally:
         O.lib.orc_set_threads(1)
         orc.close()

@@ -307,6 +307,51 @@ def test_forward_eviction_matches_oracle(ctx):
         m.close()
 
 
+def test_failed_forward_clears_layer0_row_after_reset(model2):
+    """A Forward at a position past the cache fails after layer 0's append (the cache then expects
+    layer 1); the row it leaves at that slot reads as zeros, also when an earlier use of the cache
+    had written that slot before a reset."""
+    with F.HipKvCache(model2, 8) as cache:
+        fwd = F.HipForwardPass(model2)
+        for p in range(3):
+            fwd.forward(1 + p, p, cache)
+        assert np.any(cache.get_keys(0)[:4] != 0) and np.any(cache.get_values(0)[:4] != 0)
+        cache.clear()
+        with pytest.raises(F.ArgumentOutOfRangeException):
+            fwd.forward(5, 1, cache)
+        k, v = cache.get_keys(0), cache.get_values(0)
+        assert k.size == 4 and v.size == 4  # one effective row (kv_dim 4) in layer 0
+        assert np.all(k == 0) and np.all(v == 0)
+        assert cache.get_keys(1).size == 0
+
+
+@pytest.mark.parametrize("debug", [False, True], ids=["batched", "stepwise"])
+def test_prefill_overflow_leaves_cache_unchanged(ctx, debug):
+    """fllm_prefill checks the capacity before anything runs on both of its paths (the batched
+    prefill, and the per-token Forward calls that debug capture selects): a prompt longer than the
+    room left returns ArgumentOutOfRange with the length and the rows unchanged, no eviction."""
+    cfg, desc, tensors = synthetic("test-llama")
+    m = F.Model(ctx, desc)
+    upload(m, tensors)
+    try:
+        with F.HipKvCache(m, 16) as kv:
+            F.set_debug(kv, debug)
+            fwd = F.HipForwardPass(m)
+            toks = F.synth_tokens(3, 0, desc.vocab, 17)
+            fwd.prefill(toks[:10], 0, kv)
+            assert kv.current_length == 10
+            keys = [kv.get_keys(l).copy() for l in range(desc.n_layers)]
+            with pytest.raises(F.ArgumentOutOfRangeException):
+                fwd.prefill(toks[10:17], 10, kv)
+            assert kv.current_length == 10 and not kv.was_evicted
+            for l in range(desc.n_layers):
+                assert np.array_equal(kv.get_keys(l), keys[l])
+            fwd.prefill(toks[10:16], 10, kv)  # exactly the room left
+            assert kv.current_length == 16
+    finally:
+        m.close()
+
+
 def test_disposed_weights(ctx):
     """LlamaWeights.Dispose + ThrowIfDisposed (LlamaWeights.cs:93-107, 138-139): after the model is
     destroyed, Forward / prefill / decode on its sequences throw ObjectDisposedException before

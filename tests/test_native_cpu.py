@@ -87,6 +87,20 @@ def test_synth_deterministic_and_in_range():
     assert toks.min() >= 0 and toks.max() < 1000 and np.array_equal(toks, F.synth_tokens(5, 0, 1000, 500))
 
 
+def test_xoshiro_host_known_answers():
+    """The host XoshiroRandom against the published SplitMix64 and xoshiro256** vectors
+    (the same literals that pin the oracle)."""
+    from test_oracle_ops import SPLITMIX64_0, SPLITMIX64_1234567, XOSHIRO256SS_1234, next_float_of
+    for seed, want in ((1234567, SPLITMIX64_1234567), (0, SPLITMIX64_0)):
+        r = F.XoshiroRandom(seed)
+        assert [r.s.s0, r.s.s1, r.s.s2, r.s.s3] == want[:4]
+    s = N.Xoshiro(1, 2, 3, 4)
+    assert [N.host.fllmh_xoshiro_next(C.byref(s)) for _ in range(10)] == XOSHIRO256SS_1234
+    s = N.Xoshiro(1, 2, 3, 4)
+    assert [N.host.fllmh_xoshiro_next_float(C.byref(s)) for _ in range(10)] == \
+        [next_float_of(v) for v in XOSHIRO256SS_1234]
+
+
 def test_xoshiro_host_matches_oracle():
     for seed in (1, 42, 2 ** 63 + 5):
         a, b = F.XoshiroRandom(seed), O.Xoshiro(seed)

@@ -5,8 +5,8 @@ TopKSamplerTests.cs:45-71, SamplerPipelineTests.cs:24-70, TopPSamplerTests.cs,
 RepetitionPenaltySamplerTests.cs. Beyond those: closed forms
 (RoPE at position 0 is the identity and preserves pair norms; softcap(x) -> x for |x| << cap;
 GELU/SiLU fixed points), float64 brute force for Dot/LinearProjection, numpy's order
-statistic for the top-k threshold, and the published xoshiro256** algorithm (restated with
-Python integers) for the RNG.
+statistic for the top-k threshold, and published known answers of SplitMix64 and
+xoshiro256** for the RNG.
 """
 import math
 
@@ -136,47 +136,57 @@ def test_topk_threshold_matches_order_statistic():
         assert th == np.sort(x)[::-1][k - 1]
 
 
-def py_xoshiro(seed, count):
-    M = (1 << 64) - 1
-
-    def sm(x):
-        x = (x + 0x9E3779B97F4A7C15) & M
-        z = x
-        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
-        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
-        return x, z ^ (z >> 31)
-
-    s = []
-    x = seed
-    for _ in range(4):
-        x, v = sm(x)
-        s.append(v)
-
-    def rotl(v, k):
-        return ((v << k) | (v >> (64 - k))) & M
-
-    out = []
-    for _ in range(count):
-        r = (rotl((s[1] * 5) & M, 7) * 9) & M
-        t = (s[1] << 17) & M
-        s[2] ^= s[0]
-        s[3] ^= s[1]
-        s[1] ^= s[2]
-        s[0] ^= s[3]
-        s[2] ^= t
-        s[3] = rotl(s[3], 45)
-        out.append(r)
-    return out
+# Published known answers for the two generators XoshiroRandom combines
+# (XoshiroRandom.cs:9-44). None of them is computed by code in this repository.
+# SplitMix64 from seed 1234567: Rosetta Code, "Pseudo-random numbers/Splitmix64".
+SPLITMIX64_1234567 = [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                      4593380528125082431, 16408922859458223821]
+# SplitMix64 from seed 0 (the reference's default seed): the outputs listed with Vigna's
+# splitmix64.c and used by Java's SplittableRandom test suites.
+SPLITMIX64_0 = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+# xoshiro256** from the state {1, 2, 3, 4}: the reference vector of the rand_xoshiro crate's
+# Xoshiro256StarStar test. The first three follow by hand: rotl(2 * 5, 7) * 9 = 11520; the step
+# leaves s1 = 0, so the second is 0; then s1 = 262149 and rotl(262149 * 5, 7) * 9 = 1509978240.
+XOSHIRO256SS_1234 = [11520, 0, 1509978240, 1215971899390074240, 1216172134540287360,
+                     607988272756665600, 16172922978634559625, 8476171486693032832,
+                     10595114339597558777, 2904607092377533576]
 
 
-def test_xoshiro_published_algorithm():
-    for seed in (1, 7, 42, 123, 0xDEADBEEF):
+def next_float_of(u64):
+    """NextFloat's mapping (XoshiroRandom.cs:44) of a known 64-bit output, in exact arithmetic:
+    the top 53 bits times 2^-53 is a double without rounding, then one rounding to float."""
+    return np.float32(math.ldexp(u64 >> 11, -53))
+
+
+def test_xoshiro_seeding_is_splitmix64():
+    """XoshiroRandom(seed) holds the first four SplitMix64 outputs of the seed as s0..s3."""
+    for seed, want in ((1234567, SPLITMIX64_1234567), (0, SPLITMIX64_0)):
         r = O.Xoshiro(seed)
-        want = py_xoshiro(seed, 50)
-        assert [r.next() for _ in range(50)] == want
-        r = O.Xoshiro(seed)
-        for w in want[:20]:
-            assert r.next_float() == np.float32((w >> 11) * (1.0 / (1 << 53)))
+        assert [r.s.s0, r.s.s1, r.s.s2, r.s.s3] == want[:4]
+
+
+def test_xoshiro256ss_known_answers():
+    """The step from an injected state, against the published vector."""
+    import ctypes as C
+    s = O.OrcXoshiro(1, 2, 3, 4)
+    assert [O.lib.orc_xoshiro_next(C.byref(s)) for _ in range(10)] == XOSHIRO256SS_1234
+    s = O.OrcXoshiro(1, 2, 3, 4)
+    got = [O.lib.orc_xoshiro_next_float(C.byref(s)) for _ in range(10)]
+    assert got == [next_float_of(v) for v in XOSHIRO256SS_1234]
+    assert got[1] == 0.0 and got[0] == np.float32(5 * 2.0 ** -53)  # 11520 >> 11 = 5
+
+
+def test_xoshiro_next_float_range_and_rounding():
+    """NextFloat lies in [0, 1] (the float rounding of (2^53 - 1) 2^-53 is 1.0f, as in the
+    reference), is the float nearest the 53-bit fraction, and the extreme outputs map as the
+    closed form says."""
+    assert next_float_of(0) == 0.0
+    assert next_float_of((1 << 64) - 1) == np.float32(1.0)
+    assert next_float_of(1 << 11) == np.float32(2.0 ** -53)
+    r = O.Xoshiro(7)
+    for _ in range(2000):
+        f = r.next_float()
+        assert 0.0 <= f <= 1.0
 
 
 def test_sampler_pipeline_reference_cases():
