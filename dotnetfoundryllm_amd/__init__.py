@@ -391,6 +391,11 @@ def set_prefill_chunk(kv, tokens):
     _check(N.dev.fllm_seq_set_prefill_chunk(kv.h, int(tokens)))
 
 
+def set_fused_attention(kv, enable):
+    """q/k/v projection and attention of each decode layer in one launch (default on) or three."""
+    _check(N.dev.fllm_seq_set_fused_attention(kv.h, 1 if enable else 0))
+
+
 def set_profile(kv, enable):
     _check(N.dev.fllm_seq_set_profile(kv.h, 1 if enable else 0))
 

@@ -198,6 +198,11 @@ struct fllm_seq {
     int attn_nc = 1;              // chunks per kv head of the fast attention kernel
     size_t attn_lds = 0;
     bool attn_fast = false;
+    // q/k/v and the attention in one launch where a fused kernel exists (fllm_seq_set_fused_attention);
+    // attn_sync: its counters and error flag (zero between launches), attn_sync_used: it has run
+    bool attn_fuse = true;
+    bool attn_sync_used = false;
+    unsigned* attn_sync = nullptr;
     bool fused = false;           // layers run as fused GEMV launches
     bool head_fused = false;
     bool argmax_valid = false;    // params->argmax holds the argmax of the current logits
@@ -955,6 +960,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->nuc_sc, 1);
     ALLOC(s->hidden_dbg, (L + 1) * H);
     ALLOC(s->x2, H);
+    ALLOC(s->attn_sync, (size_t)attn_sync_words(d.n_kv_heads));
 #undef ALLOC
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_OOM, "sequence allocation: %s", hipGetErrorString(e)); }
     // RoPE table: theta = scaledPos * inv[i] (LlamaForwardPass.cs:137-147), cos/sin on the host.
@@ -972,6 +978,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, sizeof(float) * kvsz, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->pen_counts, 0, sizeof(int) * (size_t)d.vocab, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->nuc_sc, 0, sizeof(NucleusScratch), s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->attn_sync, 0, sizeof(unsigned) * (size_t)attn_sync_words(d.n_kv_heads), s->st);
     if (e == hipSuccess) e = hipStreamSynchronize(s->st);
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_DEVICE, "sequence init: %s", hipGetErrorString(e)); }
     m->n_seqs++;
@@ -1118,10 +1125,33 @@ extern "C" int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable) {
     return FLLM_OK;
 }
 
+extern "C" int32_t fllm_seq_set_fused_attention(fllm_seq* s, int32_t enable) {
+    NOT_NULL(s);
+    s->attn_fuse = enable != 0;
+    s->graph_valid = false;  // the next graph replay captures the launches again
+    return FLLM_OK;
+}
+
+// The fused q/k/v + attention launch's sticky error flag (an attention chunk whose wait ran past its
+// bound, which leaves that step's results undefined), read with the stream synchronized; a set flag
+// clears the counters and the flag and reports a device error.
+static int32_t attn_sync_check(fllm_seq* s) {
+    if (!s->attn_sync_used) return FLLM_OK;
+    unsigned v = 0;
+    HIP_TRY(hipMemcpyAsync(&v, s->attn_sync + attn_sync_err_word(s->m->d.n_kv_heads), sizeof(unsigned),
+                           hipMemcpyDeviceToHost, s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    if (v == 0u) return FLLM_OK;
+    HIP_TRY(hipMemsetAsync(s->attn_sync, 0, sizeof(unsigned) * (size_t)attn_sync_words(s->m->d.n_kv_heads), s->st));
+    HIP_TRY(hipStreamSynchronize(s->st));
+    return fail(FLLM_E_DEVICE, "decode attention: a chunk's wait for its q/k/v tiles ran past its bound; the step's "
+                               "results are undefined");
+}
+
 extern "C" int32_t fllm_seq_sync(fllm_seq* s) {
     NOT_NULL(s);
     HIP_TRY(hipStreamSynchronize(s->st));
-    return FLLM_OK;
+    return attn_sync_check(s);
 }
 
 // ---- profiling helpers ------------------------------------------------------------
@@ -1194,21 +1224,34 @@ static int layer_window(const fllm_model_desc& d, int l) {
     return 0x7FFFFFFF;
 }
 
+// arguments of the fast decode attention of layer l (tab: it also writes the output projection's table)
+static AttnArgs attn_args(const fllm_seq* s, int l, const float* kc, const float* vc, bool tab) {
+    const fllm_model_desc& d = s->m->d;
+    const bool gemma = d.arch == FLLM_ARCH_GEMMA2;
+    AttnArgs a{};
+    a.q = s->q; a.kc = kc; a.vc = vc;
+    a.nh = d.n_heads; a.nkv = d.n_kv_heads; a.hd = d.head_dim; a.kvdim = s->m->kvdim;
+    a.window = layer_window(d, l); a.scale = d.attn_scale; a.softcap = gemma ? d.attn_softcap : 0.0f;
+    a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml;
+    a.out = s->att; a.params = s->params;
+    a.tab_out = tab ? s->tab_att : nullptr;
+    a.kv_bytes = (uint32_t)((size_t)s->max_seq * (size_t)s->m->kvdim * sizeof(float));
+    return a;
+}
+
+// K and V rows attended (at most the whole cache) plus q and the output
+static double attn_bytes(const fllm_seq* s) {
+    return 8.0 * (double)s->m->kvdim * (double)s->max_seq + 8.0 * s->m->qdim;
+}
+
 static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const float* vc, bool tab) {
     const fllm_model_desc& d = s->m->d;
     bool gemma = d.arch == FLLM_ARCH_GEMMA2;
     int window = layer_window(d, l);
     float softcap = gemma ? d.attn_softcap : 0.0f;
-    // K and V rows attended (at most the whole cache) plus q and the output
-    double bytes = 8.0 * (double)s->m->kvdim * (double)s->max_seq + 8.0 * s->m->qdim;
+    const double bytes = attn_bytes(s);
     if (s->attn_fast) {
-        AttnArgs a{};
-        a.q = s->q; a.kc = kc; a.vc = vc;
-        a.nh = d.n_heads; a.nkv = d.n_kv_heads; a.hd = d.head_dim; a.kvdim = s->m->kvdim;
-        a.window = window; a.scale = d.attn_scale; a.softcap = softcap;
-        a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml;
-        a.out = s->att; a.params = s->params;
-        a.tab_out = tab ? s->tab_att : nullptr;
+        const AttnArgs a = attn_args(s, l, kc, vc, tab);
         STEP("attention", bytes, launch_attn_partial(a, s->attn_lds, s->st));
         const double merge_bytes = 4.0 * (double)d.n_heads * s->attn_nc * (d.head_dim + 2) + 4.0 * s->m->qdim;
         STEP("attention_merge", merge_bytes, launch_attn_merge(a, s->st));
@@ -1225,6 +1268,27 @@ static GemvSeg seg_of(const Tensor& t, int epi, float* out, const float* bias, c
     g.w = t.ptr; g.layout = t.layout; g.type = t.type; g.rows = (int)t.rows;
     g.epi = epi; g.out = out; g.bias = bias; g.resid = resid;
     return g;
+}
+
+// The q/k/v launch with the layer's attention in its grid, when a fused kernel covers this shape:
+// *done tells whether it was launched (otherwise the caller launches q/k/v and the attention).
+static hipError_t qkv_attention_step(fllm_seq* s, int l, GemvArgs& a, int64_t cols, double bytes, const float* kc,
+                                     const float* vc, bool tab, bool* done) {
+    *done = false;
+    if (!s->attn_fuse || !s->attn_fast || s->debug) return hipSuccess;
+    const int n_cu = s->m->ctx->n_cu > 0 ? s->m->ctx->n_cu : 256;
+    int threads;
+    size_t lds;
+    const int grid = gemv_plan(a, cols, n_cu, 0, &threads, &lds);
+    const AttnArgs at = attn_args(s, l, kc, vc, tab);
+    hipError_t e = launch_qkv_attention(a, grid, threads, lds, at, s->attn_lds, s->attn_sync, n_cu, s->st, true);
+    if (e == hipErrorNotSupported) return hipSuccess;
+    if (e != hipSuccess) return e;
+    STEP("qkv_attention", bytes + attn_bytes(s),
+         launch_qkv_attention(a, grid, threads, lds, at, s->attn_lds, s->attn_sync, n_cu, s->st, false));
+    s->attn_sync_used = true;
+    *done = true;
+    return hipSuccess;
 }
 
 static hipError_t fused_step(fllm_seq* s, const char* name, GemvArgs& a, int64_t cols, double bytes) {
@@ -1333,6 +1397,10 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
         const Tensor* dn_t[1] = {&L.down};
         const bool o_mf = mfma_launch(o_t, 1, 0, m->qdim), gu_mf = mfma_launch(gu_t, 2, 1, H);
         const bool dn_mf = mfma_launch(dn_t, 1, 0, d.ffn);
+        // the attention merge writes the output projection's activation table when that runs on
+        // the matrix cores
+        const bool atab = s->attn_fast && o_mf;
+        bool attn_done = false;
         {
             // q, k and v in one launch (the matrix-core variant takes Q4_K q/k with a Q6_K v)
             GemvArgs a{};
@@ -1348,13 +1416,14 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
             hipError_t e = fold_post(a, H);
             if (e != hipSuccess) return e;
-            e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
+            e = qkv_attention_step(s, l, a, H, bytes + 8.0 * H, kc, vc, atab, &attn_done);
             if (e != hipSuccess) return e;
+            if (!attn_done) {
+                e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
+                if (e != hipSuccess) return e;
+            }
         }
-        // the attention merge writes the output projection's activation table when that runs on
-        // the matrix cores
-        const bool atab = s->attn_fast && o_mf;
-        hipError_t e = attention_step(s, l, kc, vc, atab);
+        hipError_t e = attn_done ? hipSuccess : attention_step(s, l, kc, vc, atab);
         if (e != hipSuccess) return e;
         {
             GemvArgs a{};
@@ -1591,7 +1660,7 @@ extern "C" int32_t fllm_decode_greedy(fllm_seq* s, int32_t token, int32_t positi
     HIP_TRY(hipMemcpyAsync(out_tokens, s->tokens_out, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));
     s->argmax_valid = true;
-    return FLLM_OK;
+    return attn_sync_check(s);
 }
 
 // ---- batched prefill ---------------------------------------------------------------------------
@@ -1859,7 +1928,7 @@ extern "C" int32_t fllm_logits_copy(fllm_seq* s, float* dst, int64_t n) {
     if (n < V) return fail(FLLM_E_ARG, "destination must hold %d floats", V);
     HIP_TRY(hipMemcpyAsync(dst, s->logits, sizeof(float) * (size_t)V, hipMemcpyDeviceToHost, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));
-    return FLLM_OK;
+    return attn_sync_check(s);
 }
 
 extern "C" int32_t fllm_logits_write(fllm_seq* s, const float* src, int64_t n) {

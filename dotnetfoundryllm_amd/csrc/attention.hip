@@ -5,251 +5,23 @@
 // scores s_t = Dot(q, k_t) * scale over t in [window_start, position], optional tanh softcap,
 // Softmax, out = sum_t p_t v_t.
 //
-// Split-K ("flash decoding") layout. Workgroup (kv head, chunk) takes a contiguous chunk of
-// the attended range for the whole query group of that kv head, so each K/V row is read from
-// HBM once per group. Lanes split a K/V row into float4 slices (hd/4 lanes per row, 64/(hd/4)
-// rows per wave load, fully coalesced); q for the group stays in registers. Each workgroup
-// writes its unnormalised partial output with the chunk's max and sum; a second kernel merges
-// the chunks of every head. (Merging inside the first kernel would need a device-scope release
-// per workgroup, which on a multi-XCD part writes back each XCD's L2.)
+// Split-K ("flash decoding") layout, device code in attn_body.hpp: workgroup (kv head, chunk)
+// takes a contiguous chunk of the attended range for the whole query group of that kv head and
+// writes its unnormalised partial output with the chunk's max and sum; a second kernel merges the
+// chunks of every head. The q/k/v launch can also run both steps in its own grid
+// (launch_qkv_attention, gemv.hip).
 #include "attention.hpp"
 #include "actab.hpp"
+#include "attn_body.hpp"
 
 #include <math.h>
 
 namespace fllm {
 
-// Cross-lane reductions with DPP row operations (VALU, no LDS round trip). dpp<CTRL, ROWS>(old, v):
-// v moved by the DPP control CTRL in the rows of mask ROWS, old elsewhere.
-template <int CTRL, int ROWS = 0xF>
-__device__ __forceinline__ float dpp(float old, float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
-}
-enum { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_BCAST15 = 0x142,
-       DPP_BCAST31 = 0x143 };
-
-// sum over each group of N lanes (16, 32 or 64); the total is in the group's last lane
-template <int N>
-__device__ __forceinline__ float group_sum(float v) {
-    v += dpp<DPP_XOR1>(0.0f, v);
-    v += dpp<DPP_XOR2>(0.0f, v);
-    v += dpp<DPP_HALF_MIRROR>(0.0f, v);
-    v += dpp<DPP_MIRROR>(0.0f, v);  // every lane: its 16-lane row
-    if (N >= 32) v += dpp<DPP_BCAST15, 0xA>(0.0f, v);  // rows 1, 3: rows 0 + 1, 2 + 3
-    if (N >= 64) v += dpp<DPP_BCAST31, 0xC>(0.0f, v);  // rows 2, 3: adds rows 0 + 1 (row 3 = all)
-    return v;
-}
-// maximum over the wave, in every lane
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp<DPP_XOR1>(v, v));
-    v = fmaxf(v, dpp<DPP_XOR2>(v, v));
-    v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v, v));
-    v = fmaxf(v, dpp<DPP_MIRROR>(v, v));
-    v = fmaxf(v, dpp<DPP_BCAST15, 0xA>(v, v));
-    v = fmaxf(v, dpp<DPP_BCAST31, 0xC>(v, v));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum<64>(v)), 63));
-}
-
-// dot of q with the K row slice kr for every head of the group, reduced over the row's lanes; the
-// row's last lane stores the raw dot of row t (scale and softcap come in the softmax pass, one score
-// per lane, rather than here with one lane of the wave active)
-template <int HD, int G>
-__device__ __forceinline__ void attn_scores(const float4* qv, const float4& kr, int t, int len, int dl, float* sc,
-                                            int ch) {
-    constexpr int LPR = HD / 4;
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        float s = qv[h].x * kr.x;
-        s = fmaf(qv[h].y, kr.y, s);
-        s = fmaf(qv[h].z, kr.z, s);
-        s = fmaf(qv[h].w, kr.w, s);
-        s = group_sum<LPR>(s);
-        if (dl == LPR - 1 && t < len) sc[h * ch + t] = s;
-    }
-}
-
-// acc[h] += p_t v_t for the rows of the group's heads
-template <int G>
-__device__ __forceinline__ void attn_pv(float4* acc, const float4& vr, int t, int len, const float* sc, int ch) {
-    if (t >= len) return;
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float p = sc[h * ch + t];
-        acc[h].x = fmaf(p, vr.x, acc[h].x);
-        acc[h].y = fmaf(p, vr.y, acc[h].y);
-        acc[h].z = fmaf(p, vr.z, acc[h].z);
-        acc[h].w = fmaf(p, vr.w, acc[h].w);
-    }
-}
-
-// G = query heads per kv head. Rows of the chunk go in blocks of BLK = 4 rows per lane; the K and V
-// rows of the first two blocks are loaded together up front (row indices clamped to the chunk, so
-// every load is unconditional and all are in flight at once); later blocks (long chunks) stream
-// through a ring of two blocks loaded ahead of the one in use, K's during the first blocks' scores,
-// V's during the softmax.
-// K / V cache rows, read once per step: non-temporal, so that they do not displace the weights'
-// neighbours in L2 (activation tables, epilogue operands, code)
-typedef float kv_f4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ float4 kv_ld(const float* p) {
-    const kv_f4 v = __builtin_nontemporal_load((const kv_f4*)p);
-    return make_float4(v.x, v.y, v.z, v.w);
-}
-
-// this lane's NP = 4 rows of the block at b0 (row indices clamped to the chunk) as one register
-// vector (a vector rather than an array of float4 keeps it out of scratch memory across the loops)
-typedef float kv_blk __attribute__((ext_vector_type(16)));
-template <int RPP>
-__device__ __forceinline__ kv_blk kv_ld_blk(const float* base, int b0, int r0, int len, int kvdim) {
-    kv_blk v;
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const float4 t = kv_ld(base + (int64_t)min(b0 + r0 + u * RPP, len - 1) * kvdim);
-        v[4 * u] = t.x; v[4 * u + 1] = t.y; v[4 * u + 2] = t.z; v[4 * u + 3] = t.w;
-    }
-    return v;
-}
-__device__ __forceinline__ float4 kv_row(const kv_blk& v, int u) {
-    return make_float4(v[4 * u], v[4 * u + 1], v[4 * u + 2], v[4 * u + 3]);
-}
-
 template <int HD, int G>
 __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
-    constexpr int LPR = HD / 4;    // lanes per K/V row
-    constexpr int RPL = 64 / LPR;  // rows per wave load
-    constexpr int RPP = 4 * RPL;   // rows per load of the 4 waves
-    constexpr int NP = 4;          // rows per lane per block
-    constexpr int BLK = NP * RPP;  // rows per block
-    extern __shared__ float sh[];
-    const int kvh = blockIdx.x, c = blockIdx.y;
-    const int h0 = kvh * G;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int sub = lane / LPR, dl = lane % LPR;
-    const int r0 = wave * RPL + sub;  // this lane's rows in a block: r0 + u * RPP
-
-    // q slice of every head of the group (independent of the position)
-    float4 qv[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) qv[h] = *(const float4*)(a.q + (int64_t)(h0 + h) * HD + dl * 4);
-
-    const int seq = a.params->pos + 1;
-    const AttnRange rg = attn_range(a.params->pos, a.window, a.nc);
-    const int ws = rg.ws, ch = rg.ch, nchunks = rg.nchunks;
-    if (c >= nchunks) return;
-    const int t0 = ws + c * ch;
-    const int len = min(ch, seq - t0);
-
-    float* sc = sh;                                   // [G][ch] scores, then weights
-    float* red = sh + G * ch;                         // [4 waves * RPL row slots][G][HD] = 1024 G floats
-    float* ml = red + 4 * RPL * G * HD;               // [G][2]
-
-    const float* kbase = a.kc + (int64_t)t0 * a.kvdim + (int64_t)kvh * HD + dl * 4;
-    const float* vbase = a.vc + (int64_t)t0 * a.kvdim + (int64_t)kvh * HD + dl * 4;
-    const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
-
-    // ---- K and V rows of blocks 0 and 1 -------------------------------------------------------
-    float4 kA[NP], kB[NP], vA[NP], vB[NP];
-#pragma unroll
-    for (int u = 0; u < NP; u++) kA[u] = kv_ld(kbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
-#pragma unroll
-    for (int u = 0; u < NP; u++) kB[u] = kv_ld(kbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
-#pragma unroll
-    for (int u = 0; u < NP; u++) vA[u] = kv_ld(vbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
-#pragma unroll
-    for (int u = 0; u < NP; u++) vB[u] = kv_ld(vbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
-
-    static_assert(NP == 4, "kv_blk holds 4 rows");
-    // K of blocks 2 .. 2 + KR - 1 (then the next KR, ...). Past the chunk the rows clamp to its last
-    // one (re-read from cache; blocks wholly past it are not scored), so every load of the ring is
-    // unconditional and they complete in the order issued: a block waits only for its own loads.
-    constexpr int KR = 2;  // blocks in flight (4 measured slower for head_dim 256 at 6k positions)
-    kv_blk kn[KR];  // (read only when the ring was loaded: the loops run only when 2 BLK < len)
-    const bool ring = 2 * BLK < len;
-    if (ring) {
-#pragma unroll
-        for (int j = 0; j < KR; j++) kn[j] = kv_ld_blk<RPP>(kbase, (2 + j) * BLK, r0, len, a.kvdim);
-    }
-
-    // ---- scores ---------------------------------------------------------------------------------
-#pragma unroll
-    for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kA[u], r0 + u * RPP, len, dl, sc, ch);
-#pragma unroll
-    for (int u = 0; u < NP; u++)
-        attn_scores<HD, G>(qv, kB[u], BLK + r0 + u * RPP, len, dl, sc, ch);
-    for (int b0 = 2 * BLK; b0 < len; b0 += KR * BLK) {
-#pragma unroll
-        for (int j = 0; j < KR; j++) {
-            if (b0 + j * BLK < len) {
-#pragma unroll
-                for (int u = 0; u < NP; u++)
-                    attn_scores<HD, G>(qv, kv_row(kn[j], u), b0 + j * BLK + r0 + u * RPP, len, dl, sc, ch);
-            }
-            kn[j] = kv_ld_blk<RPP>(kbase, b0 + (j + KR) * BLK, r0, len, a.kvdim);
-        }
-    }
-    kv_blk vn[KR];  // V of blocks 2 .. 2 + KR - 1, in flight during the softmax
-    if (ring) {
-#pragma unroll
-        for (int j = 0; j < KR; j++) vn[j] = kv_ld_blk<RPP>(vbase, (2 + j) * BLK, r0, len, a.kvdim);
-    }
-    __syncthreads();
-
-    // ---- softmax pieces per head: scores (scale, softcap), max, exp(s - max), sum ------------
-    for (int h = wave; h < G; h += 4) {
-        float m = -INFINITY;
-        for (int t = lane; t < len; t += 64) {
-            float v = sc[h * ch + t] * a.scale;
-            if (a.softcap > 0.0f) v = tanhf(v * inv_cap) * a.softcap;
-            sc[h * ch + t] = v;
-            m = fmaxf(m, v);
-        }
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int t = lane; t < len; t += 64) {
-            float e = expf(sc[h * ch + t] - m);
-            sc[h * ch + t] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) { ml[2 * h] = m; ml[2 * h + 1] = l; }
-    }
-    __syncthreads();
-
-    // ---- weighted sum of V ------------------------------------------------------------------
-    float4 acc[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int u = 0; u < NP; u++) attn_pv<G>(acc, vA[u], r0 + u * RPP, len, sc, ch);
-#pragma unroll
-    for (int u = 0; u < NP; u++) attn_pv<G>(acc, vB[u], BLK + r0 + u * RPP, len, sc, ch);
-    for (int b0 = 2 * BLK; b0 < len; b0 += KR * BLK) {
-#pragma unroll
-        for (int j = 0; j < KR; j++) {
-            if (b0 + j * BLK < len) {
-#pragma unroll
-                for (int u = 0; u < NP; u++) attn_pv<G>(acc, kv_row(vn[j], u), b0 + j * BLK + r0 + u * RPP, len, sc, ch);
-            }
-            vn[j] = kv_ld_blk<RPP>(vbase, b0 + (j + KR) * BLK, r0, len, a.kvdim);
-        }
-    }
-    // every (wave, row slot) leaves its partial sums in LDS; 4 * RPL slots are then summed
-#pragma unroll
-    for (int h = 0; h < G; h++) *(float4*)(red + (((wave * RPL + sub) * G + h) * HD) + dl * 4) = acc[h];
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < G * HD; idx += blockDim.x) {
-        float o = 0.0f;
-#pragma unroll
-        for (int sl = 0; sl < 4 * RPL; sl++) o += red[sl * G * HD + idx];
-        int h = idx / HD, d = idx % HD;
-        a.part_o[((int64_t)(h0 + h) * a.nc + c) * HD + d] = o;
-    }
-    for (int h = threadIdx.x; h < G; h += blockDim.x) {
-        a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2] = ml[2 * h];
-        a.part_ml[((int64_t)(h0 + h) * a.nc + c) * 2 + 1] = ml[2 * h + 1];
-    }
+    extern __shared__ __attribute__((aligned(16))) float sh[];
+    attn_chunk<HD, G, false>(a, (int)blockIdx.x, (int)blockIdx.y, sh, AttnSync{nullptr, 0});
 }
 
 // The head's part of the activation table of out, for the output projection: lanes 4k .. 4k + 3

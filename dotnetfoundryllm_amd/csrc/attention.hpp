@@ -21,6 +21,7 @@ struct AttnArgs {
     float* out;            // [nh][hd]
     const StepParams* params;
     void* tab_out;         // optional: activation table of out (nh * hd elements, a multiple of 256)
+    uint32_t kv_bytes;     // bytes of this layer's K (and of its V) cache: capacity * kvdim * 4
 };
 
 // The attended positions [ws, pos] of a step split into nchunks chunks of ch positions (ch =
@@ -36,6 +37,18 @@ __host__ __device__ __forceinline__ AttnRange attn_range(int pos, int window, in
     ch = (ch + 31) / 32 * 32;
     return AttnRange{ws, ch, (alen + ch - 1) / ch};
 }
+
+// Counters of the q/k/v launch that runs the attention in its grid, one 128-byte line each: [kvh]
+// counts the q/k/v tiles of kv head kvh that are stored, [nkv + kvh] the attention chunks of kv head
+// kvh that are stored; the word after them is a sticky error flag (a wait that ran past its bound).
+constexpr int ATTN_SYNC_STRIDE = 32;
+__host__ __device__ __forceinline__ int attn_sync_words(int nkv) { return (2 * nkv + 1) * ATTN_SYNC_STRIDE; }
+__host__ __device__ __forceinline__ int attn_sync_err_word(int nkv) { return 2 * nkv * ATTN_SYNC_STRIDE; }
+
+struct AttnSync {
+    unsigned* cnt;  // attn_sync_words(nkv) words, zero between launches
+    int target;     // q/k/v tiles per kv head: (group + 2) * head_dim / 16
+};
 
 bool attn_fast_supported(int head_dim, int group, int max_seq);
 int attn_chunks(int n_kv, int max_seq, int n_cu);

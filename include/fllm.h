@@ -184,6 +184,13 @@ FLLM_API int32_t fllm_seq_set_graph(fllm_seq* s, int32_t enable);
 FLLM_API int32_t fllm_seq_set_prefill_chunk(fllm_seq* s, int32_t tokens);
 /* 1 = keep the residual stream after every layer for fllm_debug_hidden (parity hook). */
 FLLM_API int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable);
+/* 1 (default) = run each decode layer's q/k/v projection and its attention as one launch where a
+ * fused kernel covers the shape (the attention chunks of a kv head start on its K/V rows while the
+ * q/k/v tiles stream, then wait for them; the last chunk merges); 0 = three launches (q/k/v, the
+ * attention chunks, the merge). Same results either way. A tuning knob with no counterpart in the
+ * reference. fllm_decode_greedy, fllm_logits_copy and fllm_seq_sync report FLLM_E_DEVICE if a fused
+ * launch's wait ran past its bound (the counters are then cleared). */
+FLLM_API int32_t fllm_seq_set_fused_attention(fllm_seq* s, int32_t enable);
 
 /* IForwardPass.Forward(tokenId, position, kv): one decode step. Appends K/V at the current
  * length, attends over positions [window_start, position], leaves logits on the device.
