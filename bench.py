@@ -154,8 +154,8 @@ def child_profile(args):
     ctx = F.Context(0)
     model, _ = build_model(ctx, cfg)
     kv = F.HipKvCache(model, timed_capacity(args, cfg))
-    if args.no_fused_attention:
-        F.set_fused_attention(kv, False)
+    if args.attention_merge != "auto":
+        F.set_attention_merge(kv, args.attention_merge == "in")
     fwd = F.HipForwardPass(model)
     prompt = F.synth_tokens(cfg["seed"], 0, cfg["vocab"], args.prompt)
     fwd.prefill(prompt[:-1], 0, kv)
@@ -256,7 +256,7 @@ def gemv_report(args):
 def child_args(args):
     return ["--config", args.config, "--profile-steps", str(args.profile_steps), "--prompt", str(args.prompt),
             "--warmup", str(args.warmup), "--steps", str(args.steps), "--host-steps", str(args.host_steps)] + \
-        (["--no-fused-attention"] if args.no_fused_attention else [])
+        ["--attention-merge", args.attention_merge]
 
 
 def rocprof_child(args, mode, tmp, child="--child-profile"):
@@ -550,8 +550,9 @@ def main():
     ap.add_argument("--seed", type=int, default=0x5EED)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--no-fused-attention", action="store_true",
-                    help="q/k/v, the attention chunks and their merge as three launches per layer")
+    ap.add_argument("--attention-merge", choices=("auto", "in", "separate"), default="auto",
+                    help="merge the decode attention's chunks inside the attention launch or in a second launch "
+                         "(auto: the library's choice for the shape)")
     ap.add_argument("--no-rocprof", action="store_true", help="roofline from HIP events only (no profiler child runs)")
     ap.add_argument("--child-profile", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--child-gemv", action="store_true", help=argparse.SUPPRESS)
@@ -588,8 +589,8 @@ def main():
     kv = F.HipKvCache(model, max_seq)
     if args.no_graph:
         F.set_graph(kv, False)
-    if args.no_fused_attention:
-        F.set_fused_attention(kv, False)
+    if args.attention_merge != "auto":
+        F.set_attention_merge(kv, args.attention_merge == "in")
     fwd = F.HipForwardPass(model)
     prompt = F.synth_tokens(cfg["seed"], 0, cfg["vocab"], args.prompt)
 

@@ -391,9 +391,10 @@ def set_prefill_chunk(kv, tokens):
     _check(N.dev.fllm_seq_set_prefill_chunk(kv.h, int(tokens)))
 
 
-def set_fused_attention(kv, enable):
-    """q/k/v projection and attention of each decode layer in one launch (default on) or three."""
-    _check(N.dev.fllm_seq_set_fused_attention(kv.h, 1 if enable else 0))
+def set_attention_merge(kv, in_launch):
+    """Decode attention chunks merged inside the attention launch or by a second launch (the default
+    is chosen per shape: inside when a kv head has at most 4 query heads and 32 chunks)."""
+    _check(N.dev.fllm_seq_set_attention_merge(kv.h, 1 if in_launch else 0))
 
 
 def set_profile(kv, enable):

@@ -101,7 +101,7 @@ DEVICE_SIGS = {
     "fllm_seq_set_graph": (I32, [P, I32]),
     "fllm_seq_set_debug": (I32, [P, I32]),
     "fllm_seq_set_prefill_chunk": (I32, [P, I32]),
-    "fllm_seq_set_fused_attention": (I32, [P, I32]),
+    "fllm_seq_set_attention_merge": (I32, [P, I32]),
     "fllm_forward": (I32, [P, I32, I32]),
     "fllm_prefill": (I32, [P, PI32, I32, I32]),
     "fllm_decode_greedy": (I32, [P, I32, I32, I32, PI32]),

@@ -43,9 +43,6 @@ def _run(cmd, cwd):
 
 
 DEVICE_SRCS = ["csrc/kernels.hip", "csrc/gemv.hip", "csrc/attention.hip", "csrc/prefill.hip", "csrc/api.hip"]
-# gemv.hip: matrix-core results in VGPRs in every kernel (the q/k/v launch that also runs the
-# attention otherwise gets its accumulators in AGPRs, a read and a hazard wait after each product)
-FILE_FLAGS = {"csrc/gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def build_device_lib(verbose=False):
@@ -54,7 +51,7 @@ def build_device_lib(verbose=False):
 
     def compile_one(src):
         obj = os.path.join("_build", os.path.splitext(os.path.basename(src))[0] + ".o")
-        return obj, _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src, []), "-c", "-o", obj, src], PKG)
+        return obj, _run([HIPCC, *HIP_FLAGS, "-c", "-o", obj, src], PKG)
 
     with ThreadPoolExecutor(max_workers=min(len(DEVICE_SRCS), os.cpu_count() or 1)) as pool:
         results = list(pool.map(compile_one, DEVICE_SRCS))

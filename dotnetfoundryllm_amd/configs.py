@@ -92,7 +92,7 @@ CONFIGS = {
     "test-ragged": _cfg("test-ragged", N.ARCH_LLAMA, 2, 256, 4, 2, 16640, 512, 64, 10000.0,
                         _types(Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K, Q6_K), norm_std=0.1, seed=18),
     # the decode layers' q/k/v + attention shapes of the three full-size models at a small FFN and
-    # vocabulary (the one-launch q/k/v + attention kernels): Llama-3-8B (dim 4096, 32 / 8 heads x 128,
+    # vocabulary (the attention's head groups and widths at full size): Llama-3-8B (dim 4096, 32 / 8 heads x 128,
     # Q4_K q/k, Q6_K v), Qwen2-7B (dim 3584 = 14 chunks, 28 / 4 heads x 128, Q5_K, QKV bias),
     # Gemma-2-9B (dim 3584, 16 / 8 heads x 256, Q8_0, softcaps, window 64 on the even layers)
     "test-llama-qkva": _cfg("test-llama-qkva", N.ARCH_LLAMA, 3, 4096, 32, 8, 1024, 512, 320, 500000.0,

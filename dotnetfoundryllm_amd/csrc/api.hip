@@ -19,6 +19,7 @@
 #include "gemv.hpp"
 #include "kernels.hpp"
 #include "prefill.hpp"
+#include "staging.hpp"
 
 using namespace fllm;
 
@@ -54,15 +55,6 @@ extern "C" int32_t fllm_version(void) { return 100; }
 // =====================================================================================
 // objects
 // =====================================================================================
-// Pinned staging of large host-to-device uploads: the host copies chunk i into buffer i % 2 (with
-// several threads) while the DMA engine moves chunk i - 1, so a pageable source (a mapped GGUF
-// file) streams at the rate of the slower of the two instead of their sum.
-struct Staging {
-    static const size_t kChunk = 32u << 20;
-    uint8_t* buf[2] = {nullptr, nullptr};
-    hipEvent_t done[2] = {nullptr, nullptr};
-};
-
 struct fllm_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -99,44 +91,6 @@ static hipError_t scratch_init(int device, uint8_t** out) {
         g_scratch_dev[device] = (uint8_t*)ptr;
     }
     *out = g_scratch_dev[device];
-    return hipSuccess;
-}
-
-// Copies n bytes of host memory to the device through the context's pinned staging buffers
-// (allocated on first use); returns when the last chunk's copy has been enqueued and the source
-// may be reused.
-static hipError_t staged_upload(fllm_ctx* ctx, uint8_t* dst, const uint8_t* src, size_t n) {
-    Staging& S = ctx->stage;
-    for (int b = 0; b < 2; b++) {
-        if (!S.buf[b]) {
-            hipError_t e = hipHostMalloc((void**)&S.buf[b], Staging::kChunk, hipHostMallocDefault);
-            if (e != hipSuccess) { S.buf[b] = nullptr; return e; }
-        }
-        if (!S.done[b]) {
-            hipError_t e = hipEventCreateWithFlags(&S.done[b], hipEventDisableTiming);
-            if (e != hipSuccess) { S.done[b] = nullptr; return e; }
-        }
-    }
-    const unsigned nthr = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
-    size_t off = 0;
-    for (int i = 0; off < n; i++) {
-        const int b = i & 1;
-        const size_t len = std::min(Staging::kChunk, n - off);
-        hipError_t e = hipEventSynchronize(S.done[b]);  // the DMA from this buffer two chunks ago
-        if (e != hipSuccess) return e;
-        uint8_t* stage = S.buf[b];
-        const uint8_t* from = src + off;
-        const size_t part = (len + nthr - 1) / nthr;
-        std::vector<std::thread> pool;
-        for (unsigned t = 1; t < nthr && t * part < len; t++)
-            pool.emplace_back([=] { memcpy(stage + t * part, from + t * part, std::min(part, len - t * part)); });
-        memcpy(stage, from, std::min(part, len));
-        for (auto& th : pool) th.join();
-        e = hipMemcpyAsync(dst + off, stage, len, hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess) e = hipEventRecord(S.done[b], ctx->stream);
-        if (e != hipSuccess) return e;
-        off += len;
-    }
     return hipSuccess;
 }
 
@@ -198,11 +152,12 @@ struct fllm_seq {
     int attn_nc = 1;              // chunks per kv head of the fast attention kernel
     size_t attn_lds = 0;
     bool attn_fast = false;
-    // q/k/v and the attention in one launch where a fused kernel exists (fllm_seq_set_fused_attention);
-    // attn_sync: its counters and error flag (zero between launches), attn_sync_used: it has run
-    bool attn_fuse = true;
-    bool attn_sync_used = false;
-    unsigned* attn_sync = nullptr;
+    // the fast attention merges its chunks inside its own launch (fllm_seq_set_attention_merge;
+    // by default when one wave per query head of a group and one load pass per head suffice, i.e.
+    // at most 4 query heads per kv head and 32 chunks); attn_cnt: its per-kv-head counters (zero
+    // between launches)
+    bool attn_merge_in = false;
+    unsigned* attn_cnt = nullptr;
     bool fused = false;           // layers run as fused GEMV launches
     bool head_fused = false;
     bool argmax_valid = false;    // params->argmax holds the argmax of the current logits
@@ -290,10 +245,7 @@ extern "C" int32_t fllm_ctx_destroy(fllm_ctx* ctx) {
     if (!ctx) return FLLM_OK;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
-    for (int b = 0; b < 2; b++) {
-        if (ctx->stage.done[b]) hipEventDestroy(ctx->stage.done[b]);
-        if (ctx->stage.buf[b]) hipHostFree(ctx->stage.buf[b]);
-    }
+    staging_free(ctx->stage);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return FLLM_OK;
@@ -686,11 +638,15 @@ extern "C" int32_t fllm_model_upload(fllm_model* m, int32_t slot, int32_t layer,
     uint8_t* dev = nullptr;
     hipError_t e = hipMalloc(&dev, nbytes + kPad);
     if (e != hipSuccess) return fail(FLLM_E_OOM, "hipMalloc(%llu): %s", (unsigned long long)nbytes, hipGetErrorString(e));
-    // large tensors through the pinned staging ring, small ones as one pageable copy
-    if (nbytes >= Staging::kChunk) e = staged_upload(m->ctx, dev, (const uint8_t*)bytes, nbytes);
-    else e = hipMemcpyAsync(dev, bytes, nbytes, hipMemcpyHostToDevice, st);
+    // every tensor through the pinned staging pair: the host reads the caller's bytes (a mapped
+    // file, say), no device copy does
+    e = staged_upload(m->ctx->stage, st, dev, (const uint8_t*)bytes, nbytes);
     if (e == hipSuccess) e = hipMemsetAsync(dev + nbytes, 0, kPad, st);
-    if (e != hipSuccess) { hipFree(dev); return fail(FLLM_E_DEVICE, "upload: %s", hipGetErrorString(e)); }
+    if (e != hipSuccess) {
+        hipStreamSynchronize(st);  // copies already enqueued into dev
+        hipFree(dev);
+        return fail(FLLM_E_DEVICE, "upload: %s", hipGetErrorString(e));
+    }
     if (vec) {
         // norms and biases: dequantize once to F32 on the device
         float* f = nullptr;
@@ -911,6 +867,10 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     s->attn_fast = attn_fast_supported(d.head_dim, d.n_heads / d.n_kv_heads, s->max_seq);
     s->attn_nc = attn_chunks(d.n_kv_heads, s->max_seq, m->ctx->n_cu > 0 ? m->ctx->n_cu : 256);
     s->attn_lds = attn_lds_bytes(d.head_dim, d.n_heads / d.n_kv_heads, s->attn_nc, s->max_seq);
+    // (Llama-3-8B at 4 heads / 32 chunks: 1.572 -> 1.566 ms per step, Gemma-2-9B at 2 / 32 and
+    // 6144 positions 3.290 -> 3.257; Qwen2-7B at 7 / 64 and 2048 positions 1.719 -> 1.934: the
+    // merging workgroup's two passes over 64 chunks for 7 heads cost more than a second launch)
+    s->attn_merge_in = d.n_heads / d.n_kv_heads <= 4 && s->attn_nc <= 32;
     s->fused = s->attn_fast && gemv_fusable_cols(d.hidden) && gemv_fusable_cols(m->qdim) && gemv_fusable_cols(d.ffn);
     for (const Layer& Lr : m->layers) {
         const Tensor* ts[] = {&Lr.q, &Lr.k, &Lr.v, &Lr.o, &Lr.gate, &Lr.up, &Lr.down};
@@ -960,7 +920,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     ALLOC(s->nuc_sc, 1);
     ALLOC(s->hidden_dbg, (L + 1) * H);
     ALLOC(s->x2, H);
-    ALLOC(s->attn_sync, (size_t)attn_sync_words(d.n_kv_heads));
+    ALLOC(s->attn_cnt, (size_t)attn_cnt_words(d.n_kv_heads));
 #undef ALLOC
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_OOM, "sequence allocation: %s", hipGetErrorString(e)); }
     // RoPE table: theta = scaledPos * inv[i] (LlamaForwardPass.cs:137-147), cos/sin on the host.
@@ -978,7 +938,7 @@ extern "C" int32_t fllm_seq_create(fllm_model* m, int32_t max_seq, fllm_seq** ou
     if (e == hipSuccess) e = hipMemsetAsync(s->vc, 0, sizeof(float) * kvsz, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->pen_counts, 0, sizeof(int) * (size_t)d.vocab, s->st);
     if (e == hipSuccess) e = hipMemsetAsync(s->nuc_sc, 0, sizeof(NucleusScratch), s->st);
-    if (e == hipSuccess) e = hipMemsetAsync(s->attn_sync, 0, sizeof(unsigned) * (size_t)attn_sync_words(d.n_kv_heads), s->st);
+    if (e == hipSuccess) e = hipMemsetAsync(s->attn_cnt, 0, sizeof(unsigned) * (size_t)attn_cnt_words(d.n_kv_heads), s->st);
     if (e == hipSuccess) e = hipStreamSynchronize(s->st);
     if (e != hipSuccess) { seq_free(s); return fail(FLLM_E_DEVICE, "sequence init: %s", hipGetErrorString(e)); }
     m->n_seqs++;
@@ -1125,33 +1085,17 @@ extern "C" int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable) {
     return FLLM_OK;
 }
 
-extern "C" int32_t fllm_seq_set_fused_attention(fllm_seq* s, int32_t enable) {
+extern "C" int32_t fllm_seq_set_attention_merge(fllm_seq* s, int32_t in_launch) {
     NOT_NULL(s);
-    s->attn_fuse = enable != 0;
+    s->attn_merge_in = in_launch != 0;
     s->graph_valid = false;  // the next graph replay captures the launches again
     return FLLM_OK;
-}
-
-// The fused q/k/v + attention launch's sticky error flag (an attention chunk whose wait ran past its
-// bound, which leaves that step's results undefined), read with the stream synchronized; a set flag
-// clears the counters and the flag and reports a device error.
-static int32_t attn_sync_check(fllm_seq* s) {
-    if (!s->attn_sync_used) return FLLM_OK;
-    unsigned v = 0;
-    HIP_TRY(hipMemcpyAsync(&v, s->attn_sync + attn_sync_err_word(s->m->d.n_kv_heads), sizeof(unsigned),
-                           hipMemcpyDeviceToHost, s->st));
-    HIP_TRY(hipStreamSynchronize(s->st));
-    if (v == 0u) return FLLM_OK;
-    HIP_TRY(hipMemsetAsync(s->attn_sync, 0, sizeof(unsigned) * (size_t)attn_sync_words(s->m->d.n_kv_heads), s->st));
-    HIP_TRY(hipStreamSynchronize(s->st));
-    return fail(FLLM_E_DEVICE, "decode attention: a chunk's wait for its q/k/v tiles ran past its bound; the step's "
-                               "results are undefined");
 }
 
 extern "C" int32_t fllm_seq_sync(fllm_seq* s) {
     NOT_NULL(s);
     HIP_TRY(hipStreamSynchronize(s->st));
-    return attn_sync_check(s);
+    return FLLM_OK;
 }
 
 // ---- profiling helpers ------------------------------------------------------------
@@ -1235,7 +1179,6 @@ static AttnArgs attn_args(const fllm_seq* s, int l, const float* kc, const float
     a.nc = s->attn_nc; a.part_o = s->part_o; a.part_ml = s->part_ml;
     a.out = s->att; a.params = s->params;
     a.tab_out = tab ? s->tab_att : nullptr;
-    a.kv_bytes = (uint32_t)((size_t)s->max_seq * (size_t)s->m->kvdim * sizeof(float));
     return a;
 }
 
@@ -1252,9 +1195,13 @@ static hipError_t attention_step(fllm_seq* s, int l, const float* kc, const floa
     const double bytes = attn_bytes(s);
     if (s->attn_fast) {
         const AttnArgs a = attn_args(s, l, kc, vc, tab);
-        STEP("attention", bytes, launch_attn_partial(a, s->attn_lds, s->st));
         const double merge_bytes = 4.0 * (double)d.n_heads * s->attn_nc * (d.head_dim + 2) + 4.0 * s->m->qdim;
-        STEP("attention_merge", merge_bytes, launch_attn_merge(a, s->st));
+        if (s->attn_merge_in) {
+            STEP("attention", bytes + merge_bytes, launch_attn_merged(a, s->attn_lds, s->attn_cnt, s->st));
+        } else {
+            STEP("attention", bytes, launch_attn_partial(a, s->attn_lds, s->st));
+            STEP("attention_merge", merge_bytes, launch_attn_merge(a, s->st));
+        }
     } else {
         STEP("attention", bytes,
              launch_attention(s->q, kc, vc, d.n_heads, d.n_kv_heads, d.head_dim, window, d.attn_scale, softcap,
@@ -1268,27 +1215,6 @@ static GemvSeg seg_of(const Tensor& t, int epi, float* out, const float* bias, c
     g.w = t.ptr; g.layout = t.layout; g.type = t.type; g.rows = (int)t.rows;
     g.epi = epi; g.out = out; g.bias = bias; g.resid = resid;
     return g;
-}
-
-// The q/k/v launch with the layer's attention in its grid, when a fused kernel covers this shape:
-// *done tells whether it was launched (otherwise the caller launches q/k/v and the attention).
-static hipError_t qkv_attention_step(fllm_seq* s, int l, GemvArgs& a, int64_t cols, double bytes, const float* kc,
-                                     const float* vc, bool tab, bool* done) {
-    *done = false;
-    if (!s->attn_fuse || !s->attn_fast || s->debug) return hipSuccess;
-    const int n_cu = s->m->ctx->n_cu > 0 ? s->m->ctx->n_cu : 256;
-    int threads;
-    size_t lds;
-    const int grid = gemv_plan(a, cols, n_cu, 0, &threads, &lds);
-    const AttnArgs at = attn_args(s, l, kc, vc, tab);
-    hipError_t e = launch_qkv_attention(a, grid, threads, lds, at, s->attn_lds, s->attn_sync, n_cu, s->st, true);
-    if (e == hipErrorNotSupported) return hipSuccess;
-    if (e != hipSuccess) return e;
-    STEP("qkv_attention", bytes + attn_bytes(s),
-         launch_qkv_attention(a, grid, threads, lds, at, s->attn_lds, s->attn_sync, n_cu, s->st, false));
-    s->attn_sync_used = true;
-    *done = true;
-    return hipSuccess;
 }
 
 static hipError_t fused_step(fllm_seq* s, const char* name, GemvArgs& a, int64_t cols, double bytes) {
@@ -1397,10 +1323,6 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
         const Tensor* dn_t[1] = {&L.down};
         const bool o_mf = mfma_launch(o_t, 1, 0, m->qdim), gu_mf = mfma_launch(gu_t, 2, 1, H);
         const bool dn_mf = mfma_launch(dn_t, 1, 0, d.ffn);
-        // the attention merge writes the output projection's activation table when that runs on
-        // the matrix cores
-        const bool atab = s->attn_fast && o_mf;
-        bool attn_done = false;
         {
             // q, k and v in one launch (the matrix-core variant takes Q4_K q/k with a Q6_K v)
             GemvArgs a{};
@@ -1416,14 +1338,13 @@ static hipError_t enqueue_body_fused(fllm_seq* s) {
             a.rope = s->rope; a.hd = d.head_dim; a.kc = kc; a.vc = vc; a.kvdim = kvdim;
             hipError_t e = fold_post(a, H);
             if (e != hipSuccess) return e;
-            e = qkv_attention_step(s, l, a, H, bytes + 8.0 * H, kc, vc, atab, &attn_done);
+            e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
             if (e != hipSuccess) return e;
-            if (!attn_done) {
-                e = fused_step(s, "qkv_rope_kv", a, H, bytes + 8.0 * H);
-                if (e != hipSuccess) return e;
-            }
         }
-        hipError_t e = attn_done ? hipSuccess : attention_step(s, l, kc, vc, atab);
+        // the attention merge writes the output projection's activation table when that runs on
+        // the matrix cores
+        const bool atab = s->attn_fast && o_mf;
+        hipError_t e = attention_step(s, l, kc, vc, atab);
         if (e != hipSuccess) return e;
         {
             GemvArgs a{};
@@ -1660,7 +1581,7 @@ extern "C" int32_t fllm_decode_greedy(fllm_seq* s, int32_t token, int32_t positi
     HIP_TRY(hipMemcpyAsync(out_tokens, s->tokens_out, sizeof(int32_t) * (size_t)n_steps, hipMemcpyDeviceToHost, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));
     s->argmax_valid = true;
-    return attn_sync_check(s);
+    return FLLM_OK;
 }
 
 // ---- batched prefill ---------------------------------------------------------------------------
@@ -1928,7 +1849,7 @@ extern "C" int32_t fllm_logits_copy(fllm_seq* s, float* dst, int64_t n) {
     if (n < V) return fail(FLLM_E_ARG, "destination must hold %d floats", V);
     HIP_TRY(hipMemcpyAsync(dst, s->logits, sizeof(float) * (size_t)V, hipMemcpyDeviceToHost, s->st));
     HIP_TRY(hipStreamSynchronize(s->st));
-    return attn_sync_check(s);
+    return FLLM_OK;
 }
 
 extern "C" int32_t fllm_logits_write(fllm_seq* s, const float* src, int64_t n) {

@@ -20,8 +20,14 @@ namespace fllm {
 
 template <int HD, int G>
 __global__ __launch_bounds__(256) void k_attn_decode(const AttnArgs a) {
-    extern __shared__ __attribute__((aligned(16))) float sh[];
-    attn_chunk<HD, G, false>(a, (int)blockIdx.x, (int)blockIdx.y, sh, AttnSync{nullptr, 0});
+    extern __shared__ float sh[];
+    attn_chunk<HD, G, false>(a, (int)blockIdx.x, (int)blockIdx.y, sh);
+}
+
+// the same chunks, merged by the last chunk of each kv head to finish (attn_chunk_and_merge)
+template <int HD, int G>
+__global__ __launch_bounds__(256) void k_attn_decode_merged(const AttnArgs a, unsigned* cnt) {
+    attn_chunk_and_merge<HD, G>(a, cnt + blockIdx.x * ATTN_CNT_STRIDE, (int)blockIdx.x, (int)blockIdx.y);
 }
 
 // The head's part of the activation table of out, for the output projection: lanes 4k .. 4k + 3
@@ -261,6 +267,35 @@ hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t st) {
         case 64: k_attn_merge_wide<64><<<a.nh, 256, 0, st>>>(a); break;
         case 128: k_attn_merge_wide<128><<<a.nh, 256, 0, st>>>(a); break;
         default: k_attn_merge_wide<256><<<a.nh, 256, 0, st>>>(a); break;
+    }
+    return hipGetLastError();
+}
+
+template <int HD>
+static void attn_merged_g(const AttnArgs& a, dim3 grid, size_t lds, unsigned* cnt, hipStream_t st) {
+    switch (a.nh / a.nkv) {
+        case 1: k_attn_decode_merged<HD, 1><<<grid, 256, lds, st>>>(a, cnt); break;
+        case 2: k_attn_decode_merged<HD, 2><<<grid, 256, lds, st>>>(a, cnt); break;
+        case 3: k_attn_decode_merged<HD, 3><<<grid, 256, lds, st>>>(a, cnt); break;
+        case 4: k_attn_decode_merged<HD, 4><<<grid, 256, lds, st>>>(a, cnt); break;
+        case 5: k_attn_decode_merged<HD, 5><<<grid, 256, lds, st>>>(a, cnt); break;
+        case 6: k_attn_decode_merged<HD, 6><<<grid, 256, lds, st>>>(a, cnt); break;
+        case 7: k_attn_decode_merged<HD, 7><<<grid, 256, lds, st>>>(a, cnt); break;
+        default: k_attn_decode_merged<HD, 8><<<grid, 256, lds, st>>>(a, cnt); break;
+    }
+}
+
+hipError_t launch_attn_merged(const AttnArgs& a, size_t lds, unsigned* cnt, hipStream_t st) {
+    dim3 grid(a.nkv, a.nc);
+    const int g = a.nh / a.nkv;
+    if (g < 1 || g > ATTN_GROUP_MAX || g * a.nkv != a.nh || cnt == nullptr || a.nc > ATTN_MAX_CHUNKS)
+        return hipErrorInvalidValue;
+    // the merging chunk's staging of the output table: one wave's share per head of the group
+    const size_t need = lds > (size_t)4 * (a.hd / 16) * 48 ? lds : (size_t)4 * (a.hd / 16) * 48;
+    switch (a.hd) {
+        case 64: attn_merged_g<64>(a, grid, need, cnt, st); break;
+        case 128: attn_merged_g<128>(a, grid, need, cnt, st); break;
+        default: attn_merged_g<256>(a, grid, need, cnt, st); break;
     }
     return hipGetLastError();
 }

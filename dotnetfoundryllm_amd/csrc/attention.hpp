@@ -21,7 +21,6 @@ struct AttnArgs {
     float* out;            // [nh][hd]
     const StepParams* params;
     void* tab_out;         // optional: activation table of out (nh * hd elements, a multiple of 256)
-    uint32_t kv_bytes;     // bytes of this layer's K (and of its V) cache: capacity * kvdim * 4
 };
 
 // The attended positions [ws, pos] of a step split into nchunks chunks of ch positions (ch =
@@ -38,17 +37,10 @@ __host__ __device__ __forceinline__ AttnRange attn_range(int pos, int window, in
     return AttnRange{ws, ch, (alen + ch - 1) / ch};
 }
 
-// Counters of the q/k/v launch that runs the attention in its grid, one 128-byte line each: [kvh]
-// counts the q/k/v tiles of kv head kvh that are stored, [nkv + kvh] the attention chunks of kv head
-// kvh that are stored; the word after them is a sticky error flag (a wait that ran past its bound).
-constexpr int ATTN_SYNC_STRIDE = 32;
-__host__ __device__ __forceinline__ int attn_sync_words(int nkv) { return (2 * nkv + 1) * ATTN_SYNC_STRIDE; }
-__host__ __device__ __forceinline__ int attn_sync_err_word(int nkv) { return 2 * nkv * ATTN_SYNC_STRIDE; }
-
-struct AttnSync {
-    unsigned* cnt;  // attn_sync_words(nkv) words, zero between launches
-    int target;     // q/k/v tiles per kv head: (group + 2) * head_dim / 16
-};
+// Counters of the attention launch that merges its own chunks: one per kv head, on its own 128-byte
+// line (word kvh * ATTN_CNT_STRIDE), zero between launches (each launch's merging chunks clear them).
+constexpr int ATTN_CNT_STRIDE = 32;
+__host__ __device__ __forceinline__ int attn_cnt_words(int nkv) { return nkv * ATTN_CNT_STRIDE; }
 
 bool attn_fast_supported(int head_dim, int group, int max_seq);
 int attn_chunks(int n_kv, int max_seq, int n_cu);
@@ -56,6 +48,9 @@ size_t attn_lds_bytes(int head_dim, int group, int nc, int max_seq);
 // the two kernels of the decode attention: per-chunk partials, then the merge over chunks
 hipError_t launch_attn_partial(const AttnArgs& a, size_t lds, hipStream_t st);
 hipError_t launch_attn_merge(const AttnArgs& a, hipStream_t st);
+// the decode attention as one launch: the chunks' partials, and the last chunk of each kv head to
+// finish merges them (cnt: attn_cnt_words(nkv) counters, zero before the launch, zero after it)
+hipError_t launch_attn_merged(const AttnArgs& a, size_t lds, unsigned* cnt, hipStream_t st);
 hipError_t launch_attn_decode(const AttnArgs& a, size_t lds, hipStream_t st);
 
 }  // namespace fllm

@@ -1,7 +1,6 @@
 // attn_body.hpp — device code of the split-K decode attention (ComputeAttention,
 // LlamaForwardPass.cs:158-211; Mistral window MistralForwardPass.cs:121-175; Gemma2 scale, score
-// softcap and window Gemma2ForwardPass.cs:126-185), shared by the attention kernels (attention.hip)
-// and the q/k/v launch that runs the attention in the same grid (gemv.hip).
+// softcap and window Gemma2ForwardPass.cs:126-185) for the kernels of attention.hip.
 //
 // One workgroup of 256 threads takes a contiguous chunk of the attended range for the whole query
 // group of a kv head, so each K/V row is read from HBM once per group. Lanes split a K/V row into
@@ -9,13 +8,13 @@
 // stays in registers. Each workgroup writes its unnormalised partial output with the chunk's max
 // and sum; the merge combines the chunks of every head.
 //
-// In-launch handoff (FUSED): the workgroups that produce a value another workgroup of the same
-// launch reads write it with write-through stores (agent-scope relaxed atomics: global stores with
-// sc1), wait until those stores are acknowledged, then add to a counter with a relaxed agent-scope
-// atomic; the reader polls the counter (relaxed agent-scope loads) and reads the values with sc1
-// loads, which are served from memory rather than from a non-coherent L2 of another XCD. No L2
-// write-back or invalidate (release / acquire fences) is needed, which on a multi-XCD part cost
-// several microseconds per handoff.
+// In-launch merge (WT): the chunks write their partials with write-through stores (agent-scope
+// relaxed atomics: global stores with sc1), wait until those stores are acknowledged, then count
+// themselves on a per-kv-head counter with a relaxed agent-scope atomic; the chunk whose count
+// completes the kv head reads the others' partials with sc1 loads, which are served from memory
+// rather than from a non-coherent L2 of another XCD, and merges them. No L2 write-back or invalidate
+// (release / acquire fences) is needed: on this multi-XCD part those cost several microseconds per
+// handoff, against about one for the write-through path.
 #pragma once
 
 #include "attention.hpp"
@@ -84,23 +83,6 @@ __device__ __forceinline__ void st_wt_u(unsigned* p, unsigned v) {
 // every store this thread issued has been acknowledged (the write-through data is in memory)
 __device__ __forceinline__ void wt_complete() { __builtin_amdgcn_s_waitcnt(0); }
 
-constexpr int ATTN_SPIN_LIMIT = 1 << 16;  // polls of about 60 ns: milliseconds, far past any real wait
-
-// thread 0 polls counter c until it reaches target (bounded: past the bound the error flag is set and
-// the workgroup goes on); the workgroup then proceeds
-__device__ __forceinline__ void wait_count(unsigned* c, unsigned target, unsigned* err) {
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int i = 0;
-        for (; i < ATTN_SPIN_LIMIT; i++) {
-            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (i == ATTN_SPIN_LIMIT) st_wt_u(err, 1u);
-    }
-    __syncthreads();
-}
-
 // dot of q with the K row slice kr for every head of the group, reduced over the row's lanes; the
 // row's last lane stores the raw dot of row t (scale and softcap come in the softmax pass, one score
 // per lane, rather than here with one lane of the wave active)
@@ -151,28 +133,11 @@ __device__ __forceinline__ void kv_set(kv_blk& v, int u, const float4 t) {
     v[4 * u] = t.x; v[4 * u + 1] = t.y; v[4 * u + 2] = t.z; v[4 * u + 3] = t.w;
 }
 
-// The row this launch writes (FUSED): row fr of the chunk (-1: none in it) comes from memory with a
-// write-through load (cache: the K or V cache as a buffer, off0: byte offset of the chunk's row 0
-// slice of this lane); every other row with the non-temporal load.
-struct FreshRow {
-    int fr;
-    __amdgpu_buffer_rsrc_t kr, vr;
-    uint32_t off0, row_bytes;
-};
-
-template <int RPP, bool FUSED>
-__device__ __forceinline__ kv_blk kv_ld_blk(const float* base, int b0, int r0, int len, int kvdim, const FreshRow& f,
-                                            bool is_v) {
+template <int RPP>
+__device__ __forceinline__ kv_blk kv_ld_blk(const float* base, int b0, int r0, int len, int kvdim) {
     kv_blk v;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int t = b0 + r0 + u * RPP;
-        const int tc = min(t, len - 1);
-        float4 x;
-        if (FUSED && t == f.fr) x = ld_wt4(is_v ? f.vr : f.kr, f.off0 + (uint32_t)tc * f.row_bytes);
-        else x = kv_ld(base + (int64_t)tc * kvdim);
-        kv_set(v, u, x);
-    }
+    for (int u = 0; u < 4; u++) kv_set(v, u, kv_ld(base + (int64_t)min(b0 + r0 + u * RPP, len - 1) * kvdim));
     return v;
 }
 
@@ -180,13 +145,11 @@ __device__ __forceinline__ kv_blk kv_ld_blk(const float* base, int b0, int r0, i
 // rows of the first two blocks are loaded together up front (row indices clamped to the chunk, so
 // every load is unconditional and all are in flight at once); later blocks (long chunks) stream
 // through a ring of two blocks loaded ahead of the one in use, K's during the first blocks' scores,
-// V's during the softmax. FUSED: the K/V rows are loaded before the wait for this kv head's q/k/v
-// tiles (every row but the one this launch writes is already in memory), q and that row after it;
-// the partials go out with write-through stores. Returns false when the chunk is past the attended
+// V's during the softmax. WT: the partials go out with write-through stores (read by the merging
+// chunk of the same launch). Returns the step's chunk count, 0 when chunk c is past the attended
 // range (the whole workgroup returns together).
-template <int HD, int G, bool FUSED>
-__device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, const int c, float* sh,
-                                           const AttnSync& sy) {
+template <int HD, int G, bool WT>
+__device__ __forceinline__ int attn_chunk(const AttnArgs& a, const int kvh, const int c, float* sh) {
     constexpr int LPR = HD / 4;    // lanes per K/V row
     constexpr int RPL = 64 / LPR;  // rows per wave load
     constexpr int RPP = 4 * RPL;   // rows per load of the 4 waves
@@ -197,17 +160,15 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
     const int sub = lane / LPR, dl = lane % LPR;
     const int r0 = wave * RPL + sub;  // this lane's rows in a block: r0 + u * RPP
 
-    // q slice of every head of the group (independent of the position); FUSED: after the wait
+    // q slice of every head of the group (independent of the position)
     float4 qv[G];
-    if constexpr (!FUSED) {
 #pragma unroll
-        for (int h = 0; h < G; h++) qv[h] = *(const float4*)(a.q + (int64_t)(h0 + h) * HD + dl * 4);
-    }
+    for (int h = 0; h < G; h++) qv[h] = *(const float4*)(a.q + (int64_t)(h0 + h) * HD + dl * 4);
 
     const int seq = a.params->pos + 1;
     const AttnRange rg = attn_range(a.params->pos, a.window, a.nc);
     const int ws = rg.ws, ch = rg.ch, nchunks = rg.nchunks;
-    if (c >= nchunks) return false;
+    if (c >= nchunks) return 0;
     const int t0 = ws + c * ch;
     const int len = min(ch, seq - t0);
 
@@ -218,27 +179,21 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
     const float* kbase = a.kc + (int64_t)t0 * a.kvdim + (int64_t)kvh * HD + dl * 4;
     const float* vbase = a.vc + (int64_t)t0 * a.kvdim + (int64_t)kvh * HD + dl * 4;
     const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
-    FreshRow f;
-    f.fr = -1;
-    if constexpr (FUSED) {
-        const int fr = a.params->cur_len - t0;
-        f.fr = (fr >= 0 && fr < len) ? fr : -1;
-        f.kr = wt_rsrc(a.kc, a.kv_bytes);
-        f.vr = wt_rsrc(a.vc, a.kv_bytes);
-        f.row_bytes = (uint32_t)a.kvdim * 4u;
-        f.off0 = ((uint32_t)t0 * (uint32_t)a.kvdim + (uint32_t)(kvh * HD + dl * 4)) * 4u;
-    }
-
-    // ---- K and V rows of blocks 0 and 1 -------------------------------------------------------
+    // ---- K and V rows of blocks 0 and 1 (block 1 only when the chunk reaches it) ---------------
+    const bool blk1 = BLK < len;
     float4 kA[NP], kB[NP], vA[NP], vB[NP];
 #pragma unroll
     for (int u = 0; u < NP; u++) kA[u] = kv_ld(kbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
+    if (blk1) {
 #pragma unroll
-    for (int u = 0; u < NP; u++) kB[u] = kv_ld(kbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
+        for (int u = 0; u < NP; u++) kB[u] = kv_ld(kbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
+    }
 #pragma unroll
     for (int u = 0; u < NP; u++) vA[u] = kv_ld(vbase + (int64_t)min(r0 + u * RPP, len - 1) * a.kvdim);
+    if (blk1) {
 #pragma unroll
-    for (int u = 0; u < NP; u++) vB[u] = kv_ld(vbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
+        for (int u = 0; u < NP; u++) vB[u] = kv_ld(vbase + (int64_t)min(BLK + r0 + u * RPP, len - 1) * a.kvdim);
+    }
 
     static_assert(NP == 4, "kv_blk holds 4 rows");
     // K of blocks 2 .. 2 + KR - 1 (then the next KR, ...). Past the chunk the rows clamp to its last
@@ -249,47 +204,16 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
     const bool ring = 2 * BLK < len;
     if (ring) {
 #pragma unroll
-        for (int j = 0; j < KR; j++) kn[j] = kv_ld_blk<RPP, false>(kbase, (2 + j) * BLK, r0, len, a.kvdim, f, false);
-    }
-
-    if constexpr (FUSED) {
-        // this kv head's q/k/v tiles are stored: q, and the row this launch wrote where this lane
-        // holds it, come from memory
-        wait_count(sy.cnt + kvh * ATTN_SYNC_STRIDE, (unsigned)sy.target, sy.cnt + attn_sync_err_word(a.nkv));
-        const __amdgpu_buffer_rsrc_t qr = wt_rsrc(a.q, (uint32_t)(a.nh * HD * 4));
-#pragma unroll
-        for (int h = 0; h < G; h++) qv[h] = ld_wt4(qr, (uint32_t)(((h0 + h) * HD + dl * 4) * 4));
-        if (f.fr >= 0) {
-#pragma unroll
-            for (int u = 0; u < NP; u++) {
-                const int tA = r0 + u * RPP, tB = BLK + r0 + u * RPP;
-                if (tA == f.fr) {
-                    kA[u] = ld_wt4(f.kr, f.off0 + (uint32_t)tA * f.row_bytes);
-                    vA[u] = ld_wt4(f.vr, f.off0 + (uint32_t)tA * f.row_bytes);
-                }
-                if (tB == f.fr) {
-                    kB[u] = ld_wt4(f.kr, f.off0 + (uint32_t)tB * f.row_bytes);
-                    vB[u] = ld_wt4(f.vr, f.off0 + (uint32_t)tB * f.row_bytes);
-                }
-            }
-            if (ring) {
-#pragma unroll
-                for (int j = 0; j < KR; j++)
-#pragma unroll
-                    for (int u = 0; u < NP; u++) {
-                        const int t = (2 + j) * BLK + r0 + u * RPP;
-                        if (t == f.fr) kv_set(kn[j], u, ld_wt4(f.kr, f.off0 + (uint32_t)t * f.row_bytes));
-                    }
-            }
-        }
+        for (int j = 0; j < KR; j++) kn[j] = kv_ld_blk<RPP>(kbase, (2 + j) * BLK, r0, len, a.kvdim);
     }
 
     // ---- scores ---------------------------------------------------------------------------------
 #pragma unroll
     for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kA[u], r0 + u * RPP, len, dl, sc, ch);
+    if (blk1) {
 #pragma unroll
-    for (int u = 0; u < NP; u++)
-        attn_scores<HD, G>(qv, kB[u], BLK + r0 + u * RPP, len, dl, sc, ch);
+        for (int u = 0; u < NP; u++) attn_scores<HD, G>(qv, kB[u], BLK + r0 + u * RPP, len, dl, sc, ch);
+    }
     for (int b0 = 2 * BLK; b0 < len; b0 += KR * BLK) {
 #pragma unroll
         for (int j = 0; j < KR; j++) {
@@ -298,13 +222,13 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
                 for (int u = 0; u < NP; u++)
                     attn_scores<HD, G>(qv, kv_row(kn[j], u), b0 + j * BLK + r0 + u * RPP, len, dl, sc, ch);
             }
-            kn[j] = kv_ld_blk<RPP, FUSED>(kbase, b0 + (j + KR) * BLK, r0, len, a.kvdim, f, false);
+            kn[j] = kv_ld_blk<RPP>(kbase, b0 + (j + KR) * BLK, r0, len, a.kvdim);
         }
     }
     kv_blk vn[KR];  // V of blocks 2 .. 2 + KR - 1, in flight during the softmax
     if (ring) {
 #pragma unroll
-        for (int j = 0; j < KR; j++) vn[j] = kv_ld_blk<RPP, FUSED>(vbase, (2 + j) * BLK, r0, len, a.kvdim, f, true);
+        for (int j = 0; j < KR; j++) vn[j] = kv_ld_blk<RPP>(vbase, (2 + j) * BLK, r0, len, a.kvdim);
     }
     __syncthreads();
 
@@ -335,8 +259,10 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
     for (int h = 0; h < G; h++) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int u = 0; u < NP; u++) attn_pv<G>(acc, vA[u], r0 + u * RPP, len, sc, ch);
+    if (blk1) {
 #pragma unroll
-    for (int u = 0; u < NP; u++) attn_pv<G>(acc, vB[u], BLK + r0 + u * RPP, len, sc, ch);
+        for (int u = 0; u < NP; u++) attn_pv<G>(acc, vB[u], BLK + r0 + u * RPP, len, sc, ch);
+    }
     for (int b0 = 2 * BLK; b0 < len; b0 += KR * BLK) {
 #pragma unroll
         for (int j = 0; j < KR; j++) {
@@ -344,7 +270,7 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
 #pragma unroll
                 for (int u = 0; u < NP; u++) attn_pv<G>(acc, kv_row(vn[j], u), b0 + j * BLK + r0 + u * RPP, len, sc, ch);
             }
-            vn[j] = kv_ld_blk<RPP, FUSED>(vbase, b0 + (j + KR) * BLK, r0, len, a.kvdim, f, true);
+            vn[j] = kv_ld_blk<RPP>(vbase, b0 + (j + KR) * BLK, r0, len, a.kvdim);
         }
     }
     // every (wave, row slot) leaves its partial sums in LDS; 4 * RPL slots are then summed
@@ -357,12 +283,12 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
         for (int sl = 0; sl < 4 * RPL; sl++) o += red[sl * G * HD + idx];
         int h = idx / HD, d = idx % HD;
         float* po = a.part_o + ((int64_t)(h0 + h) * a.nc + c) * HD + d;
-        if constexpr (FUSED) st_wt(po, o);
+        if constexpr (WT) st_wt(po, o);
         else *po = o;
     }
     for (int h = threadIdx.x; h < G; h += blockDim.x) {
         float* pm = a.part_ml + ((int64_t)(h0 + h) * a.nc + c) * 2;
-        if constexpr (FUSED) {
+        if constexpr (WT) {
             st_wt(pm, ml[2 * h]);
             st_wt(pm + 1, ml[2 * h + 1]);
         } else {
@@ -370,7 +296,7 @@ __device__ __forceinline__ bool attn_chunk(const AttnArgs& a, const int kvh, con
             pm[1] = ml[2 * h + 1];
         }
     }
-    return true;
+    return nchunks;
 }
 
 // The head's part of the activation table of out, for the output projection, from one wave: lanes
@@ -424,7 +350,8 @@ __device__ __forceinline__ void merge_emit_table_wave(const AttnArgs& a, int h, 
 
 // out[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M) over the nchunks chunks of head h, by one
 // wave, reading the partials other workgroups of this launch wrote (write-through loads). Up to 256
-// chunks: (m, l) of chunks lane + 64 i in registers; the chunk outputs 32 at a time, all in flight.
+// chunks: (m, l) of chunks lane + 64 i in registers; the chunk outputs NCM at a time, the first NCM
+// loaded together with the (m, l) so that a merge of up to NCM chunks waits one memory round trip.
 // With at most 64 chunks the arithmetic is the one-wave merge's (k_attn_merge_fast): the same
 // weights and the same order of the sums.
 template <int HD>
@@ -432,11 +359,19 @@ __device__ __forceinline__ float4 merge_head_wave(const AttnArgs& a, int h, int 
     constexpr int NCM = 32;
     const __amdgpu_buffer_rsrc_t pr = wt_rsrc(a.part_o, (uint32_t)((size_t)a.nh * a.nc * HD * 4));
     const __amdgpu_buffer_rsrc_t mr = wt_rsrc(a.part_ml, (uint32_t)((size_t)a.nh * a.nc * 8));
+    const uint32_t lo = (uint32_t)(((h * a.nc) * HD + (lane < HD / 4 ? lane : 0) * 4) * 4);
+    // (only the slots of existing chunks are read: each load goes to memory, and one workgroup
+    // pulls the whole head group's partials)
+    float4 p[NCM];
+#pragma unroll
+    for (int k = 0; k < NCM; k++)
+        if (k < nchunks) p[k] = ld_wt4(pr, lo + (uint32_t)(k * HD * 4));
     float2 mlv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int k = lane + 64 * i;
-        mlv[i] = ld_wt2(mr, (uint32_t)(((h * a.nc) + (k < a.nc ? k : a.nc - 1)) * 8));
+        mlv[i] = make_float2(-INFINITY, 0.0f);
+        if (64 * i < nchunks) mlv[i] = ld_wt2(mr, (uint32_t)(((h * a.nc) + (k < nchunks ? k : nchunks - 1)) * 8));
     }
     float M = -INFINITY;
 #pragma unroll
@@ -451,14 +386,12 @@ __device__ __forceinline__ float4 merge_head_wave(const AttnArgs& a, int h, int 
         lw += valid ? mlv[i].y * w[i] : 0.0f;
     }
     const float L = wave_sum(lw);
-    const uint32_t lo = (uint32_t)(((h * a.nc) * HD + (lane < HD / 4 ? lane : 0) * 4) * 4);
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k0 = 0; k0 < nchunks; k0 += NCM) {
-        float4 p[NCM];
+        if (k0 > 0) {
 #pragma unroll
-        for (int k = 0; k < NCM; k++) {
-            const int kk = min(k0 + k, nchunks - 1);
-            p[k] = ld_wt4(pr, lo + (uint32_t)(kk * HD * 4));
+            for (int k = 0; k < NCM; k++)
+                if (k0 + k < nchunks) p[k] = ld_wt4(pr, lo + (uint32_t)((k0 + k) * HD * 4));
         }
 #pragma unroll
         for (int k = 0; k < NCM; k++) {
@@ -478,29 +411,24 @@ __device__ __forceinline__ float4 merge_head_wave(const AttnArgs& a, int h, int 
     return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
 }
 
-// Attention role of the fused q/k/v launch, workgroup wg of nkv * nc: the chunk's partials, then the
-// last chunk of a kv head to finish merges the head group's chunks (one wave per head), writes out
-// and the output projection's table, and clears the kv head's counters for the next launch.
+// The attention kernel with its own merge, workgroup (kv head kvh, chunk c): the chunk's partials
+// (write-through), then the chunk that completes the kv head's count merges the head group's chunks
+// (one wave per head), writes out and the output projection's table, and clears the counter for the
+// next launch. cnt: this kv head's counter, zero before the launch.
 template <int HD, int G>
-__device__ __forceinline__ void attn_fused_role(const AttnArgs& a, const AttnSync& sy, int wg) {
-    // (the dynamic LDS base stays 16-byte aligned: the q/k/v role of the same kernel reads it with
-    // 16-byte LDS accesses, which a 4-byte static variable in front of it would misalign)
+__device__ __forceinline__ void attn_chunk_and_merge(const AttnArgs& a, unsigned* cnt, int kvh, int c) {
     extern __shared__ __attribute__((aligned(16))) float sh_attn[];
     __shared__ __attribute__((aligned(16))) int s_last[4];
-    const int kvh = wg % a.nkv, c = wg / a.nkv;
-    if (!attn_chunk<HD, G, true>(a, kvh, c, sh_attn, sy)) return;
-    const int nchunks = attn_range(a.params->pos, a.window, a.nc).nchunks;
+    const int nchunks = attn_chunk<HD, G, true>(a, kvh, c, sh_attn);
+    if (nchunks == 0) return;
     wt_complete();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(sy.cnt + (a.nkv + kvh) * ATTN_SYNC_STRIDE, 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        s_last[0] = old == (unsigned)(nchunks - 1);
-    }
+    if (threadIdx.x == 0)
+        s_last[0] = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(nchunks - 1);
     __syncthreads();
     if (!s_last[0]) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    uint8_t* stg = (uint8_t*)sh_attn + wave * (HD / 16) * 48;
+    uint8_t* stg = (uint8_t*)sh_attn + wave * (HD / 16) * 48;  // (the chunk's LDS is free again)
     for (int hb = 0; hb < G; hb += 4) {
         const int hh = hb + wave;
         if (hh < G) {
@@ -510,10 +438,7 @@ __device__ __forceinline__ void attn_fused_role(const AttnArgs& a, const AttnSyn
             if (a.tab_out) merge_emit_table_wave<HD>(a, h, lane, res, stg);
         }
     }
-    if (threadIdx.x == 0) {
-        st_wt_u(sy.cnt + kvh * ATTN_SYNC_STRIDE, 0u);
-        st_wt_u(sy.cnt + (a.nkv + kvh) * ATTN_SYNC_STRIDE, 0u);
-    }
+    if (threadIdx.x == 0) st_wt_u(cnt, 0u);
 }
 
 }  // namespace fllm

@@ -27,7 +27,6 @@
 // of the group's largest magnitude), float32 resolution.
 #include "gemv.hpp"
 #include "actab.hpp"
-#include "attn_body.hpp"
 
 #include <math.h>
 
@@ -514,14 +513,13 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
             float2 cs = rp[(r % a.hd) >> 1];
             float y0 = x0 * cs.x - x1 * cs.y;
             float y1 = x0 * cs.y + x1 * cs.x;
-            float* dst = epi == EPI_Q ? sg.out + r : a.kc + (int64_t)slot * a.kvdim + r;
-            if (a.sig) {
-                // read by attention workgroups of this launch: write-through
-                st_wt(dst, y0);
-                st_wt(dst + 1, y1);
+            if (epi == EPI_Q) {
+                sg.out[r] = y0;
+                sg.out[r + 1] = y1;
             } else {
-                dst[0] = y0;
-                dst[1] = y1;
+                float* kc = a.kc + (int64_t)slot * a.kvdim;
+                kc[r] = y0;
+                kc[r + 1] = y1;
             }
         }
         return;
@@ -570,9 +568,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
             }
         } else if (epi == EPI_V) {
             if (sg.bias) y = y + sg.bias[r];
-            float* dst = a.vc + (int64_t)a.params->cur_len * a.kvdim + r;
-            if (a.sig) st_wt(dst, y);
-            else *dst = y;
+            a.vc[(int64_t)a.params->cur_len * a.kvdim + r] = y;
         } else {
             if (sg.bias) y = y + sg.bias[r];
             sg.out[r] = y;
@@ -586,7 +582,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, const EpiSeg sg, con
 template <int T, bool PREFETCH>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, int wg_in_seg) {
     constexpr int NR = GEMV_NR;
-    extern __shared__ __attribute__((aligned(16))) float lds[];
+    extern __shared__ float lds[];
     const int nslice = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int j = wave * a.S + lane;
@@ -1167,16 +1163,6 @@ __device__ __forceinline__ void mf_item(const GemvArgs& a, const MfCtx& x, typen
                             si == 0 ? a.seg[0].resid : si == 1 ? a.seg[1].resid : a.seg[2].resid,
                             x.pre_on && (ti >> x.ltpu) == 0, x.pre_r, x.pre_w};
             epilogue(a, es, x.part, x.red, x.nw, MF_TILE, x.T_slots, row0, x.wave, x.lane, best);
-            if (a.sig) {
-                // the tile's q / K / V stores are acknowledged, then it counts for its kv head
-                wt_complete();
-                __syncthreads();
-                if (threadIdx.x == 0) {
-                    const int head = row0 / a.hd;
-                    const int kvh = si == 0 ? head / a.sig_group : head;
-                    __hip_atomic_fetch_add(a.sig + kvh * ATTN_SYNC_STRIDE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
             __syncthreads();
         }
     }
@@ -1209,7 +1195,7 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
     constexpr int RING = MfRing<T, KC>::v;
     constexpr int U = KC > RING ? KC : RING;  // items per unrolled iteration
-    extern __shared__ __attribute__((aligned(16))) float lds[];
+    extern __shared__ float lds[];
     MfCtx x;
     x.nw = a.nw;  // blockDim.x / 64 (the kernel argument avoids reading the dispatch packet)
     x.wave = threadIdx.x >> 6;
@@ -1746,107 +1732,6 @@ __global__ __launch_bounds__(WIDE ? 1024 : 512) __attribute__((amdgpu_waves_per_
         case FLLM_TYPE_Q8_0: gemv_body<FLLM_TYPE_Q8_0, !WIDE>(a, sg, wg_in_seg); break;
         default: gemv_body<FLLM_TYPE_Q4_0, !WIDE>(a, sg, wg_in_seg); break;
     }
-}
-
-// ---- q/k/v and the decode attention in one grid ------------------------------------------
-struct QkvAttnArgs {
-    GemvArgs g;
-    AttnArgs at;
-    AttnSync sy;
-    int qkv_grid;  // workgroups [0, qkv_grid): q/k/v tiles; the rest attention chunks
-};
-
-// QV: the q/k/v kernel's weights (0: Q4_K q/k with Q6_K v, else the one type of all three); TABIN: the
-// input is an activation table (else a vector the prologue normalizes); tile-interleaved weights. Workgroups of the q/k/v part count each stored tile for
-// its kv head; the attention chunks load their K/V rows, wait for their kv head's count, and merge
-// (attn_fused_role). The q/k/v workgroups never wait, and come first in the grid (workgroups are
-// dispatched in order), so every wait ends.
-// (launched with 256 threads; the bound of the q/k/v kernels keeps their register split: with a
-// 256-thread bound the compiler moves the matrix-core accumulators to AGPRs, which costs a read and
-// its hazard wait after every product)
-template <int QV, int KC, bool TABIN, bool RAGGED, int HD, int G>
-__global__ __launch_bounds__(512) void k_qkv_attn(const QkvAttnArgs fa) {
-    const int b = (int)blockIdx.x;
-    if (b < fa.qkv_grid) {
-        const GemvArgs& a = fa.g;
-        if constexpr (QV == 0) {
-            if (b < a.mix_wg)
-                mfma_body<FLLM_TYPE_Q4_K, KC, TABIN, true>(a, 0, a.mix_unit, b, a.mix_wg);
-            else
-                mfma_body<FLLM_TYPE_Q6_K, KC, TABIN, true>(a, a.mix_unit, a.nunits - a.mix_unit, b - a.mix_wg,
-                                                          fa.qkv_grid - a.mix_wg);
-        } else {
-            mfma_body<QV, KC, TABIN, true, RAGGED>(a, 0, a.nunits, b, fa.qkv_grid);
-        }
-    } else {
-        attn_fused_role<HD, G>(fa.at, fa.sy, b - fa.qkv_grid);
-    }
-}
-
-typedef void (*QaKernel)(const QkvAttnArgs);
-// the fused kernels built: Llama-3 shapes (Q4_K q/k, Q6_K v, 4 chunks per wave, head_dim 128, 4 query
-// heads per kv head; table input: the layers after the first), Qwen2-7B (Q5_K, 14-chunk rows, 128, 7;
-// table input), Gemma-2-9B (Q8_0, 14-chunk rows, 256, 2; vector input, its post-norm folded in)
-static QaKernel qa_kernel(const GemvArgs& a, int hd, int group) {
-    const int NB = a.G / 8;
-    const bool ragged = mf_ragged(NB), tab = a.xin == XIN_TAB;
-    if (a.chunks_per_wave != 4 || a.nw != 4 || a.seg[0].layout != LAYOUT_TILES) return nullptr;
-    if (a.mix_wg > 0 && !ragged && tab && hd == 128 && group == 4) return k_qkv_attn<0, 4, true, false, 128, 4>;
-    if (a.mix_wg == 0 && ragged && tab && a.seg[0].type == FLLM_TYPE_Q5_K && hd == 128 && group == 7)
-        return k_qkv_attn<FLLM_TYPE_Q5_K, 4, true, true, 128, 7>;
-    if (a.mix_wg == 0 && ragged && !tab && a.seg[0].type == FLLM_TYPE_Q8_0 && hd == 256 && group == 2)
-        return k_qkv_attn<FLLM_TYPE_Q8_0, 4, false, true, 256, 2>;
-    return nullptr;
-}
-
-hipError_t launch_qkv_attention(const GemvArgs& a, int grid, int block_threads, size_t lds, const AttnArgs& at,
-                                size_t attn_lds, unsigned* sync, int n_cu, hipStream_t st, bool dry_run) {
-    if (!a.mfma || a.nseg != 3 || block_threads != 256 || sync == nullptr || at.nkv <= 0 || at.nh % at.nkv != 0 ||
-        at.hd % MF_TILE != 0 || at.nc < 1 || at.nc > ATTN_MAX_CHUNKS)
-        return hipErrorNotSupported;
-    // the q/k/v part's input, as launch_gemv_fused checks it
-    if (a.xin == XIN_TAB ? a.xtab == nullptr : a.x == nullptr) return hipErrorInvalidValue;
-    if (a.xin == XIN_POST && (a.x2 == nullptr || a.post_w == nullptr || a.x_out == nullptr || a.x_out == a.x))
-        return hipErrorInvalidValue;
-    const int group = at.nh / at.nkv;
-    const QaKernel k = qa_kernel(a, at.hd, group);
-    if (k == nullptr) return hipErrorNotSupported;
-    // q, k and v rows of a tile belong to one head; the tiles of a kv head are counted
-    if (a.seg[0].rows != at.nh * at.hd || a.seg[1].rows != at.nkv * at.hd || a.seg[2].rows != at.nkv * at.hd)
-        return hipErrorInvalidValue;
-    const size_t need = lds > attn_lds ? lds : attn_lds;
-    if (need > 160 * 1024) return hipErrorNotSupported;
-    // every workgroup of the launch resident at once (the chunks' waits end without that too, since
-    // the q/k/v workgroups come first and never wait, but then the chunks would only start late):
-    // with one weight type the q/k/v part takes the slots the chunks leave (its workgroups then walk
-    // several tiles each), with two it keeps the planned split
-    // (the kernel holds a few bytes of static LDS, so the dynamic limit is what the launch uses)
-    if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess) {
-        (void)hipGetLastError();
-        return hipErrorNotSupported;
-    }
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, 256, need) != hipSuccess || per_cu < 1) {
-        (void)hipGetLastError();
-        return hipErrorNotSupported;
-    }
-    const int slots = per_cu * n_cu, chunks = at.nkv * at.nc;
-    int qkv_grid = grid;
-    if (qkv_grid + chunks > slots) {
-        if (a.mix_wg > 0 || slots - chunks < n_cu) return hipErrorNotSupported;
-        qkv_grid = slots - chunks;
-    }
-    if (dry_run) return hipSuccess;
-    const int total = qkv_grid + chunks;
-    QkvAttnArgs fa;
-    fa.g = a;
-    fa.g.sig = sync;
-    fa.g.sig_group = group;
-    fa.at = at;
-    fa.sy = AttnSync{sync, (group + 2) * at.hd / MF_TILE};
-    fa.qkv_grid = qkv_grid;
-    k<<<total, 256, need, st>>>(fa);
-    return hipGetLastError();
 }
 
 // ---- host side ------------------------------------------------------------------------

@@ -75,11 +75,6 @@ struct GemvArgs {
     const float* x2;       // the output whose post-norm is added to x
     const float* post_w;   // the post-norm weight (1 + w)
     int chunks_per_wave;   // matrix-core variant: chunks per wave (nw * chunks_per_wave = chunks per row)
-    // q/k/v launch that runs the attention in the same grid: after a 16-row tile's epilogue, whose
-    // q / K / V stores are then write-through, the tile is counted for its kv head at
-    // sig[kv head * 32] (nullptr: no counting)
-    unsigned* sig;
-    int sig_group;         // query heads per kv head
 };
 
 bool gemv_fusable_type(int t);
@@ -98,16 +93,5 @@ bool gemv_tiles_shape_ok(int type, int64_t rows, int64_t cols);
 // regroup a GGUF-row matrix (src) into LAYOUT_TILES (dst, same byte count); a byte permutation
 hipError_t launch_pack_tiles(int type, const uint8_t* src, uint8_t* dst, int64_t rows, int64_t cols, hipStream_t st);
 hipError_t launch_gemv_fused(const GemvArgs& a, int grid, int block_threads, size_t lds, hipStream_t st);
-
-// The q/k/v launch (a planned by gemv_plan, input a table) and the decode attention of its step
-// (at: the attention's arguments, with at.tab_out for the output projection) in one grid: grid
-// workgroups of q/k/v tiles, then nkv * nc attention chunks that wait for their kv head's tiles,
-// the last chunk of each kv head merging them. sync: attn_sync_words(nkv) words, zero before the
-// first launch (every launch leaves them zero). Returns hipErrorNotSupported when this combination
-// of weight types, head size and group has no fused kernel (the caller then launches the three
-// kernels); *grid_out receives the launch's workgroups.
-struct AttnArgs;
-hipError_t launch_qkv_attention(const GemvArgs& a, int grid, int block_threads, size_t lds, const AttnArgs& at,
-                                size_t attn_lds, unsigned* sync, int n_cu, hipStream_t st, bool dry_run = false);
 
 }  // namespace fllm

@@ -270,7 +270,7 @@ struct Cursor {
     const uint8_t* p;
     uint64_t n, pos = 0;
     bool ok = true;
-    bool need(uint64_t k) { if (pos + k > n) { ok = false; return false; } return true; }
+    bool need(uint64_t k) { if (k > n - pos) { ok = false; return false; } return true; }  // pos <= n
     uint64_t rd(int bytes) {
         if (!need((uint64_t)bytes)) return 0;
         uint64_t v = 0;
@@ -351,13 +351,18 @@ static int32_t open_gguf(const char* path, GFile& g) {
             v.arr_len = cnt;
             for (uint64_t j = 0; j < cnt && c.ok; j++) {
                 GVal e;
-                if (!read_scalar(c, et, e)) return hfail(FLLM_E_MODEL_LOAD, "Failed to read GGUF file: bad array element type %u", et);
+                if (!read_scalar(c, et, e)) {
+                    if (!c.ok) break;
+                    return hfail(FLLM_E_MODEL_LOAD, "Failed to read GGUF file: bad array element type %u", et);
+                }
             }
         } else if (!read_scalar(c, t, v)) {
+            if (!c.ok) break;
             return hfail(FLLM_E_MODEL_LOAD, "Failed to read GGUF file: Unknown GGUF metadata value type: %u", t);
         }
         g.meta[key] = v;
     }
+    if (!c.ok) return hfail(FLLM_E_MODEL_LOAD, "Failed to read GGUF file: truncated metadata");
     for (uint64_t i = 0; i < n_tensors && c.ok; i++) {
         GTensor t;
         t.name = c.str();

@@ -184,13 +184,12 @@ FLLM_API int32_t fllm_seq_set_graph(fllm_seq* s, int32_t enable);
 FLLM_API int32_t fllm_seq_set_prefill_chunk(fllm_seq* s, int32_t tokens);
 /* 1 = keep the residual stream after every layer for fllm_debug_hidden (parity hook). */
 FLLM_API int32_t fllm_seq_set_debug(fllm_seq* s, int32_t enable);
-/* 1 (default) = run each decode layer's q/k/v projection and its attention as one launch where a
- * fused kernel covers the shape (the attention chunks of a kv head start on its K/V rows while the
- * q/k/v tiles stream, then wait for them; the last chunk merges); 0 = three launches (q/k/v, the
- * attention chunks, the merge). Same results either way. A tuning knob with no counterpart in the
- * reference. fllm_decode_greedy, fllm_logits_copy and fllm_seq_sync report FLLM_E_DEVICE if a fused
- * launch's wait ran past its bound (the counters are then cleared). */
-FLLM_API int32_t fllm_seq_set_fused_attention(fllm_seq* s, int32_t enable);
+/* 1 = the decode attention merges its position chunks inside its own launch (the last chunk of each
+ * kv head to finish merges them); 0 = a second launch merges them. The default is 1 when a kv head
+ * has at most 4 query heads and 32 chunks (Llama-3-8B, Gemma-2-9B), else 0 (Qwen2-7B's 7 heads).
+ * Results agree (bit for bit up to 32 chunks per kv head, to float32 rounding beyond). A tuning knob
+ * with no counterpart in the reference. */
+FLLM_API int32_t fllm_seq_set_attention_merge(fllm_seq* s, int32_t in_launch);
 
 /* IForwardPass.Forward(tokenId, position, kv): one decode step. Appends K/V at the current
  * length, attends over positions [window_start, position], leaves logits on the device.
