@@ -49,13 +49,14 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg_name, ctx_positions=384):
+def cpu_baseline(cfg_name, first, steps=20, head_tokens=10):
     """The oracle (reference-order restatement, F32 weights dequantized at load, one thread) on a
-    bounded sample of the same workload: one decoder layer of the model shape and 1/16 of the
-    LM-head rows, timed separately and scaled to a whole token."""
+    bounded sample of the same workload at the timed decode context: one decoder layer of the model
+    shape, its cache filled to position `first` (untimed, with the row-parallel threads, whose
+    results are bit-identical to one thread), then `steps` Forward calls at positions first..
+    timed on one thread and scaled by the layer count (the layers share one shape); and the whole
+    LM head (every row) timed on one thread over `head_tokens` calls."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import numpy as np
-
     import oracle_bind as O
     from dotnetfoundryllm_amd.configs import CONFIGS, desc_of, synth_bytes, tensor_plan
 
@@ -65,33 +66,36 @@ def cpu_baseline(cfg_name, ctx_positions=384):
     tensors = {e[0]: (e, synth_bytes(cfg, e)) for e in tensor_plan(cfg)}
     desc = desc_of(cfg)
     t0 = time.time()
-    m = O.OracleModel(desc, tensors, ctx_positions + 8)
+    m = O.OracleModel(desc, tensors, first + steps + 8)
     load_s = time.time() - t0
     del tensors
-    head_rows = desc.vocab // 16
+    fill_threads = max(1, min(16, len(os.sched_getaffinity(0))))
     try:
         m.limit(1, 0)
-        for p in range(2):
-            m.forward(11 + p, p)
+        O.lib.orc_set_threads(fill_threads)
+        t0 = time.time()
+        for p in range(first):
+            m.forward(11 + p % 1000, p)
+        fill_s = time.time() - t0
+        O.lib.orc_set_threads(1)
         t = time.perf_counter()
-        for p in range(2, 2 + ctx_positions):
-            m.forward(11 + p, p)
-        t_layer = (time.perf_counter() - t) / ctx_positions
-        m.reset()
-        m.limit(1, head_rows)
-        for p in range(2):
-            m.forward(11 + p, p)
+        for p in range(first, first + steps):
+            m.forward(11 + p % 1000, p)
+        t_layer = (time.perf_counter() - t) / steps
+        m.limit(0, desc.vocab)  # embedding row, final norm and every LM-head row
+        m.forward(7, 0)
         t = time.perf_counter()
-        for p in range(2, 2 + ctx_positions):
-            m.forward(11 + p, p)
-        t_mixed = (time.perf_counter() - t) / ctx_positions
+        for k in range(head_tokens):
+            m.forward(7 + k, 0)
+        t_head = (time.perf_counter() - t) / head_tokens
     finally:
+        O.lib.orc_set_threads(1)
         m.close()
-    t_head = max(t_mixed - t_layer, 0.0) * (desc.vocab / head_rows)
     t_token = full_layers * t_layer + t_head
     # the reference prefills with one Forward per prompt token (LlamaLanguageModel.cs:133-137): its
-    # prefill rate is the per-token rate over the prompt's positions (the sample's positions 2..386
-    # average 194, the 511-token prompt's 255; attention is under 2% of a token at these lengths)
+    # prefill rate is the per-token rate over the prompt's positions (0..510 for the 511-token
+    # prefill, against the decode positions sampled here; attention is a few percent of a token at
+    # these lengths)
     return {
         "value": round(1.0 / t_token, 4),
         "unit": "tok/s",
@@ -101,21 +105,31 @@ def cpu_baseline(cfg_name, ctx_positions=384):
         "cpu_model": host_cpu_model(),
         "nproc": os.cpu_count(),
         "affinity_cpus": len(os.sched_getaffinity(0)),
-        "sample": (f"oracle F32 forward (weights dequantized at load, reference operation order), one thread: "
-                   f"1 decoder layer x {full_layers} ({t_layer * 1e3:.1f} ms) + {head_rows}/{desc.vocab} LM-head "
-                   f"rows scaled x16 ({t_head * 1e3:.1f} ms), {ctx_positions} positions each; load {load_s:.1f} s. "
+        "sample": (f"oracle F32 forward (weights dequantized at load, reference operation order), one thread, at "
+                   f"the timed decode context: 1 decoder layer at positions {first}-{first + steps - 1} "
+                   f"({t_layer * 1e3:.1f} ms per position, x {full_layers} layers) + the whole LM head "
+                   f"({desc.vocab} rows, {t_head * 1e3:.1f} ms, {head_tokens} calls); the cache filled to "
+                   f"position {first} untimed on {fill_threads} threads ({fill_s:.1f} s); load {load_s:.1f} s. "
                    f"Prefill = the same per-token Forward, as the reference prefills"),
     }
 
 
 def host_cpu_model():
+    """/proc/cpuinfo's model name with its family / model / stepping, clock and cache lines."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break  # the first processor's block
+            k, _, v = line.partition(":")
+            fields[k.strip()] = v.strip()
     except OSError:
-        pass
-    return None
+        return None
+    name = fields.get("model name")
+    if not name:
+        return None
+    extra = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping", "cpu MHz", "cache size") if k in fields]
+    return f"{name} ({', '.join(extra)})" if extra else name
 
 
 COPY_BYTES = 256 << 20  # calibration copy of the traffic counters
@@ -719,7 +733,9 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, one thread, bounded sample) ...")
-        cpu = cpu_baseline(args.config)
+        # 20 positions centred on the timed range's mean position
+        t0, t1 = args.prompt - 1 + args.warmup, args.prompt - 2 + args.warmup + args.steps
+        cpu = cpu_baseline(args.config, first=max(0, (t0 + t1) // 2 - 10))
         log(f"cpu baseline: {cpu['value']} tok/s")
 
     out = {

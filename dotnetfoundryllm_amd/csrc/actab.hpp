@@ -36,6 +36,24 @@ __device__ __forceinline__ void half_scale(float amax, float& sc, float& inv) {
 
 __device__ __forceinline__ int quant_x(float v, float inv) { return (int)rintf(v * inv * 65536.0f); }
 
+// The digits of four quantized values packed one byte per value: byte k of the returned dwords
+// comes from x_k. With X = 65536 b2 + 256 b1 + b0 and every digit in [-128, 127] (quant_x gives
+// |X| <= 127 * 65536),
+// b1 = floor((X + 128) / 256) and b2 = floor((X + 32896) / 65536), so b0 is byte 0 of X, b1 byte 1
+// of X + 128 and b2 byte 2 of X + 32896 (the bytes digits3 would give, without its shifts and
+// masks). d2 / d1 / d0: the dwords of b2 / b1 / b0.
+__device__ __forceinline__ uint32_t byte_k_of4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t k) {
+    const uint32_t sel = 0x0c0c0000u | ((4u + k) << 8) | k;  // {a_k, b_k, 0, 0} (0x0c selects zero)
+    const uint32_t lo = __builtin_amdgcn_perm(b, a, sel), hi = __builtin_amdgcn_perm(d, c, sel);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);  // {lo_0, lo_1, hi_0, hi_1}
+}
+__device__ __forceinline__ void digits3_pack4(int x0, int x1, int x2, int x3, uint32_t& d2, uint32_t& d1,
+                                              uint32_t& d0) {
+    d2 = byte_k_of4((uint32_t)(x0 + 32896), (uint32_t)(x1 + 32896), (uint32_t)(x2 + 32896), (uint32_t)(x3 + 32896), 2);
+    d1 = byte_k_of4((uint32_t)(x0 + 128), (uint32_t)(x1 + 128), (uint32_t)(x2 + 128), (uint32_t)(x3 + 128), 1);
+    d0 = byte_k_of4((uint32_t)x0, (uint32_t)x1, (uint32_t)x2, (uint32_t)x3, 0);
+}
+
 // position of element e (0 .. n-1, n a multiple of 256) in the table: entry of digit 0 of its step
 // and quarter, its byte inside that entry, and its 32-element group's stats entry and half
 __device__ __forceinline__ void tab_pos(int e, int n, int& entry0, int& byte, int& stat, int& half) {

@@ -742,16 +742,12 @@ __device__ __forceinline__ void atab_write(lds_tab* atab, int b, int g, const fl
     const int q = g & 3, s0 = 2 * (g >> 2);
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        uint32_t w[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+        uint32_t w[3][4];
+        // dword j of each digit entry: bytes from elements j, 4 + j, 8 + j, 12 + j
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            int b2, b1, b0;
-            digits3(X[16 * h + e], b2, b1, b0);
-            const int j = e & 3, sh = 8 * (e >> 2);
-            w[0][j] |= (uint32_t)(b2 & 0xFF) << sh;
-            w[1][j] |= (uint32_t)(b1 & 0xFF) << sh;
-            w[2][j] |= (uint32_t)(b0 & 0xFF) << sh;
-        }
+        for (int j = 0; j < 4; j++)
+            digits3_pack4(X[16 * h + j], X[16 * h + 4 + j], X[16 * h + 8 + j], X[16 * h + 12 + j], w[0][j], w[1][j],
+                          w[2][j]);
 #pragma unroll
         for (int d = 0; d < 3; d++) {
             u32x4 e4 = {w[d][0], w[d][1], w[d][2], w[d][3]};
@@ -771,16 +767,12 @@ __device__ __forceinline__ void atab_write_half(lds_tab* atab, int b, int g, int
     float inv;
     half_scale(amax, sc, inv);
     sm = sum;
-    uint32_t w[3][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    int X[16];
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-        int b2, b1, b0;
-        digits3(quant_x(v[e], inv), b2, b1, b0);
-        const int j = e & 3, sh = 8 * (e >> 2);
-        w[0][j] |= (uint32_t)(b2 & 0xFF) << sh;
-        w[1][j] |= (uint32_t)(b1 & 0xFF) << sh;
-        w[2][j] |= (uint32_t)(b0 & 0xFF) << sh;
-    }
+    for (int e = 0; e < 16; e++) X[e] = quant_x(v[e], inv);
+    uint32_t w[3][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) digits3_pack4(X[j], X[4 + j], X[8 + j], X[12 + j], w[0][j], w[1][j], w[2][j]);
 #pragma unroll
     for (int d = 0; d < 3; d++) {
         u32x4 e4 = {w[d][0], w[d][1], w[d][2], w[d][3]};
@@ -802,19 +794,12 @@ __device__ __forceinline__ void tab_emit(const GemvArgs& a, float v, float sq, i
     }
     float sc, inv;
     half_scale(amax, sc, inv);
-    int b2, b1, b0;
-    digits3(quant_x(v, inv), b2, b1, b0);
+    const int X = quant_x(v, inv);
     const int h16 = row_base >> 4, g32 = h16 >> 1, half = h16 & 1, b = g32 >> 3, gg = g32 & 7;
     const int s = 2 * (gg >> 2) + half, q = gg & 3, j = lane & 3;
     // dword j of each digit entry: bytes from elements j, 4 + j, 8 + j, 12 + j
-    uint32_t w2 = 0u, w1 = 0u, w0 = 0u;
-#pragma unroll
-    for (int by = 0; by < 4; by++) {
-        const int src = j + 4 * by;
-        w2 |= (uint32_t)(__shfl(b2, src) & 0xFF) << (8 * by);
-        w1 |= (uint32_t)(__shfl(b1, src) & 0xFF) << (8 * by);
-        w0 |= (uint32_t)(__shfl(b0, src) & 0xFF) << (8 * by);
-    }
+    uint32_t w2, w1, w0;
+    digits3_pack4(__shfl(X, j), __shfl(X, j + 4), __shfl(X, j + 8), __shfl(X, j + 12), w2, w1, w0);
     uint32_t* tab = (uint32_t*)a.tab_out;
     if (lane < 4) {
         tab[4 * atab_index(b, s, q, 0) + j] = w2;
@@ -1183,13 +1168,21 @@ __device__ __forceinline__ void mf_tail(const GemvArgs& a, const MfCtx& x, typen
     }
 }
 
-// TABIN: the input is an activation table (XIN_TAB); otherwise a vector, quantized here. The
-// workgroup is number wg of ng that share units [u0, u0 + nu) of the launch.
+// Input kinds of the matrix-core body's instantiations. XK_TAB: an activation table (XIN_TAB).
+// XK_ANY: a vector quantized here, its kind chosen at run time (XIN_F32 / XIN_NORM /
+// XIN_EMBED_NORM / XIN_POST). XK_F32: a plain f32 vector (XIN_F32), each thread's 32-element group
+// loaded before the weight ring, so the table is ready when those loads return instead of behind
+// the ring's (a wave's loads return in order), and without the other kinds' registers.
+enum { XK_TAB = 0, XK_ANY = 1, XK_F32 = 2 };
+
+// XK: the input kind (above). The workgroup is number wg of ng that share units [u0, u0 + nu) of
+// the launch.
 // RAGGED: the row's NB chunks do not split evenly: the nw waves of KC chunks cover nw * KC >= NB,
 // and the last wave's chunks past the row have zero activations (their weight loads re-read the
 // row's last chunk), so they add nothing.
-template <int T, int KC, bool TABIN, bool IL, bool RAGGED = false>
+template <int T, int KC, int XK, bool IL, bool RAGGED = false>
 __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int wg, int ng) {
+    constexpr bool TABIN = XK == XK_TAB;
     using Raw = typename MfPick<T, IL>::Raw;
     constexpr int CB = mf_chunk_bytes(T);
     constexpr int LKC = KC == 1 ? 0 : KC == 2 ? 1 : KC == 4 ? 2 : 3;
@@ -1262,6 +1255,17 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
         for (int k = 0; k < TSL; k++)
             if (x.kb0 + min(x.lane + 64 * k, KC * 16 - 1) / 16 >= NB) tsq[k] = 0.0f;
     }
+    // XK_F32: this thread's group of the input (threads past the row's groups read its last group
+    // and write nothing)
+    float xg[XK == XK_F32 ? 32 : 1];
+    if constexpr (XK == XK_F32) {
+        const float4* xi = (const float4*)(a.x + min((int)threadIdx.x, a.G - 1) * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 t = xi[i];
+            xg[4 * i] = t.x; xg[4 * i + 1] = t.y; xg[4 * i + 2] = t.z; xg[4 * i + 3] = t.w;
+        }
+    }
     // the residual and the consumer's norm weight of the first tile's rows, when it is a residual
     // add: written by earlier launches, so they go out with the table rather than after the last
     // weights (where they would add a round trip to the epilogue)
@@ -1278,6 +1282,11 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
         x.pre_r = *rp;
         x.pre_w = *wp;
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // every wave's input loads are issued before any wave's weight ring: a CU serves a wave's
+    // loads in the order the waves issued them, so the table would otherwise wait behind the other
+    // waves' rings (a barrier without a memory fence: nothing waits for the loads here)
+    if constexpr (XK != XK_ANY) __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 
     Raw ring[RING];
@@ -1320,6 +1329,14 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             float tot = 0.0f;
             for (int i = 0; i < x.nw; i++) tot += x.red[i];
             x.xs = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
+        }
+    } else if constexpr (XK == XK_F32) {
+        const int g = (int)threadIdx.x;
+        if (g < a.G) {
+            float4 st;
+            atab_write(atab, g >> 3, g & 7, xg, &st);
+            f32x4 stv = {st.x, st.y, st.z, st.w};
+            x.stats[(g >> 3) * 8 + (g & 7)] = stv;
         }
     } else if (a.xin == XIN_POST && 2 * a.G <= x.nw * 64) {
         // Gemma-2 post-norm folded in (Gemma2ForwardPass.cs:90-96), two threads per 32-element
@@ -1604,20 +1621,20 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
 
 // one kernel per (weight type, chunks per wave, input kind, weight layout), each with its own
 // register allocation; every segment of such a launch has the same weight type and layout
-template <int T, int KC, bool TABIN, bool IL>
+template <int T, int KC, int XK, bool IL>
 __global__ __launch_bounds__(512) void k_gemv_mfma(const GemvArgs a) {
-    mfma_body<T, KC, TABIN, IL>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
+    mfma_body<T, KC, XK, IL>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // Two weight types in one launch (q and k in Q4_K, v in Q6_K): the first mix_wg workgroups take the
 // Q4_K units [0, mix_unit), the others the Q6_K units after them.
-template <int KC, bool TABIN, bool IL>
+template <int KC, int XK, bool IL>
 __global__ __launch_bounds__(512) void k_gemv_mfma_mix(const GemvArgs a) {
     if ((int)blockIdx.x < a.mix_wg)
-        mfma_body<FLLM_TYPE_Q4_K, KC, TABIN, IL>(a, 0, a.mix_unit, (int)blockIdx.x, a.mix_wg);
+        mfma_body<FLLM_TYPE_Q4_K, KC, XK, IL>(a, 0, a.mix_unit, (int)blockIdx.x, a.mix_wg);
     else
-        mfma_body<FLLM_TYPE_Q6_K, KC, TABIN, IL>(a, a.mix_unit, a.nunits - a.mix_unit, (int)blockIdx.x - a.mix_wg,
-                                                (int)gridDim.x - a.mix_wg);
+        mfma_body<FLLM_TYPE_Q6_K, KC, XK, IL>(a, a.mix_unit, a.nunits - a.mix_unit, (int)blockIdx.x - a.mix_wg,
+                                             (int)gridDim.x - a.mix_wg);
 }
 
 // waves per workgroup and chunks per wave (*kc) for rows of NB chunks: 10 or 14 chunks as 4 per
@@ -1659,34 +1676,41 @@ static bool mf_ragged(int NB) {
 }
 
 // ragged rows (chunks that do not split evenly): KC chunks per wave, the last wave partly past the row
-template <int T, int KC, bool TABIN>
+template <int T, int KC, int XK>
 __global__ __launch_bounds__(KC == 8 ? 640 : 512) void k_gemv_mfma_r(const GemvArgs a) {
-    mfma_body<T, KC, TABIN, true, true>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
+    mfma_body<T, KC, XK, true, true>(a, 0, a.nunits, (int)blockIdx.x, (int)gridDim.x);
 }
 
 typedef void (*MfKernel)(const GemvArgs);
-template <int T, bool TABIN, bool IL>
-static MfKernel mf_kernel_in(int kc) {
+template <int T, int XK, bool IL>
+static MfKernel mf_kernel_kc(int kc) {
     switch (kc) {
-        case 1: return k_gemv_mfma<T, 1, TABIN, IL>;
-        case 2: return k_gemv_mfma<T, 2, TABIN, IL>;
-        case 4: return k_gemv_mfma<T, 4, TABIN, IL>;
-        default: return k_gemv_mfma<T, 8, TABIN, IL>;
+        case 1: return k_gemv_mfma<T, 1, XK, IL>;
+        case 2: return k_gemv_mfma<T, 2, XK, IL>;
+        case 4: return k_gemv_mfma<T, 4, XK, IL>;
+        default: return k_gemv_mfma<T, 8, XK, IL>;
     }
+}
+// XK_F32 for a plain vector input (one weight type, rows that split evenly), else XK_TAB / XK_ANY
+template <int T, bool IL>
+static MfKernel mf_kernel_in(int xk, int kc) {
+    return xk == XK_TAB ? mf_kernel_kc<T, XK_TAB, IL>(kc) : xk == XK_F32 ? mf_kernel_kc<T, XK_F32, IL>(kc)
+                                                                         : mf_kernel_kc<T, XK_ANY, IL>(kc);
 }
 template <bool TABIN, bool IL>
 static MfKernel mf_kernel_mix(int kc) {
+    constexpr int XK = TABIN ? XK_TAB : XK_ANY;
     switch (kc) {
-        case 1: return k_gemv_mfma_mix<1, TABIN, IL>;
-        case 2: return k_gemv_mfma_mix<2, TABIN, IL>;
-        case 4: return k_gemv_mfma_mix<4, TABIN, IL>;
-        default: return k_gemv_mfma_mix<8, TABIN, IL>;
+        case 1: return k_gemv_mfma_mix<1, XK, IL>;
+        case 2: return k_gemv_mfma_mix<2, XK, IL>;
+        case 4: return k_gemv_mfma_mix<4, XK, IL>;
+        default: return k_gemv_mfma_mix<8, XK, IL>;
     }
 }
 template <int T>
 static MfKernel mf_kernel_ragged(bool tab, int kc) {
-    if (kc == 4) return tab ? k_gemv_mfma_r<T, 4, true> : k_gemv_mfma_r<T, 4, false>;
-    if (kc == 8) return tab ? k_gemv_mfma_r<T, 8, true> : k_gemv_mfma_r<T, 8, false>;
+    if (kc == 4) return tab ? k_gemv_mfma_r<T, 4, XK_TAB> : k_gemv_mfma_r<T, 4, XK_ANY>;
+    if (kc == 8) return tab ? k_gemv_mfma_r<T, 8, XK_TAB> : k_gemv_mfma_r<T, 8, XK_ANY>;
     return nullptr;
 }
 template <bool IL>
@@ -1703,15 +1727,13 @@ static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
         }
     }
     if (a.mix_wg > 0) return tab ? mf_kernel_mix<true, IL>(kc) : mf_kernel_mix<false, IL>(kc);
+    const int xk = tab ? XK_TAB : a.xin == XIN_F32 ? XK_F32 : XK_ANY;
     if constexpr (IL) {
-        if (a.seg[0].type == FLLM_TYPE_Q8_0)
-            return tab ? mf_kernel_in<FLLM_TYPE_Q8_0, true, true>(kc) : mf_kernel_in<FLLM_TYPE_Q8_0, false, true>(kc);
-        if (a.seg[0].type == FLLM_TYPE_Q5_K)
-            return tab ? mf_kernel_in<FLLM_TYPE_Q5_K, true, true>(kc) : mf_kernel_in<FLLM_TYPE_Q5_K, false, true>(kc);
+        if (a.seg[0].type == FLLM_TYPE_Q8_0) return mf_kernel_in<FLLM_TYPE_Q8_0, true>(xk, kc);
+        if (a.seg[0].type == FLLM_TYPE_Q5_K) return mf_kernel_in<FLLM_TYPE_Q5_K, true>(xk, kc);
     }
-    if (a.seg[0].type == FLLM_TYPE_Q6_K)
-        return tab ? mf_kernel_in<FLLM_TYPE_Q6_K, true, IL>(kc) : mf_kernel_in<FLLM_TYPE_Q6_K, false, IL>(kc);
-    return tab ? mf_kernel_in<FLLM_TYPE_Q4_K, true, IL>(kc) : mf_kernel_in<FLLM_TYPE_Q4_K, false, IL>(kc);
+    if (a.seg[0].type == FLLM_TYPE_Q6_K) return mf_kernel_in<FLLM_TYPE_Q6_K, IL>(xk, kc);
+    return mf_kernel_in<FLLM_TYPE_Q4_K, IL>(xk, kc);
 }
 // the kernel of a planned launch (a.mix_wg > 0: two weight types)
 static MfKernel mf_kernel(const GemvArgs& a, int kc) {

@@ -257,3 +257,23 @@ def test_repetition_penalty_reference_cases():
     # repeats apply again, zero takes the multiply branch, ids out of range are skipped
     lg = O.repetition_penalty(f32([8.0, 0.0, -1.0]), [0, 0, 0, 1, 2, 2, 3, -1], 2.0)
     assert lg.tolist() == [1.0, 0.0, -4.0]
+
+
+def test_activation_digit_bytes_match_the_digit_recurrence():
+    """The matrix-core GEMV's activation table stores each quantized value X = rint(v * 127 / amax *
+    65536) (so |X| <= 127 * 65536) as signed base-256 digits X = 65536 b2 + 256 b1 + b0, each in
+    [-128, 127]. The device packs them as byte 0 of X, byte 1 of X + 128 and byte 2 of X + 32896
+    (csrc/actab.hpp digits3_pack4); over every X of the range those bytes equal the digits of the
+    recurrence b0 = int8(X), b1 = int8((X - b0) / 256), b2 = ((X - b0) / 256 - b1) / 256, and the
+    digits rebuild X."""
+    lim = 127 * 65536
+    X = np.arange(-lim, lim + 1, dtype=np.int32)
+    b0 = ((X & 0xFF) ^ 0x80) - 0x80
+    x1 = (X - b0) >> 8
+    b1 = ((x1 & 0xFF) ^ 0x80) - 0x80
+    b2 = (x1 - b1) >> 8
+    assert np.array_equal(65536 * b2 + 256 * b1 + b0, X)
+    assert b2.min() >= -128 and b2.max() <= 127 and int(b2.max()) == 127
+    assert np.array_equal(X & 0xFF, b0 & 0xFF)
+    assert np.array_equal(((X + 128) >> 8) & 0xFF, b1 & 0xFF)
+    assert np.array_equal(((X + 32896) >> 16) & 0xFF, b2 & 0xFF)
