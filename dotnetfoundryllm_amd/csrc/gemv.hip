@@ -1168,12 +1168,87 @@ __device__ __forceinline__ void mf_tail(const GemvArgs& a, const MfCtx& x, typen
     }
 }
 
+// The Gemma-2 post-norm prologue with two threads per 32-element group (Gemma2ForwardPass.cs:90-96),
+// thread half hh of group g (live: g < G) holding its 16 values of x2, x, post_w and the norm weight:
+// the new residual is x + (x2 * rms(x2)) * (post_w + 1), the operation order of the separate
+// post-norm kernel, stored by workgroup 0, then normalized as XIN_NORM into the table.
+__device__ __forceinline__ void post_prologue_half(const GemvArgs& a, MfCtx& x, lds_tab* atab, int g, int hh,
+                                                   bool live, const float* t2, float* xv, const float* pw,
+                                                   const float* wv) {
+    float ss = 0.0f;
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) ss = fmaf(t2[i], t2[i], ss);
+    }
+    ss = wsum(ss);
+    if (x.lane == 0) x.red[x.wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < x.nw; i++) tot += x.red[i];
+    const float prms = 1.0f / sqrtf(tot / (float)(a.G * 32) + 1e-6f);
+    __syncthreads();  // x.red is reused below
+    float ssq = 0.0f;
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) xv[i] = xv[i] + (t2[i] * prms) * (pw[i] + 1.0f);
+#pragma unroll
+        for (int i = 0; i < 16; i++) ssq = fmaf(xv[i], xv[i], ssq);
+    }
+    ssq = wsum(ssq);
+    if (x.lane == 0) x.red[x.wave] = ssq;
+    __syncthreads();
+    tot = 0.0f;
+    for (int i = 0; i < x.nw; i++) tot += x.red[i];
+    const float scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
+    float hsc = 0.0f, hsm = 0.0f;
+    if (live) {
+        const int e0 = g * 32 + 16 * hh;
+        if (blockIdx.x == 0) {
+            float4* xo = (float4*)(a.x_out + e0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) xo[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float t = xv[i] * scale;
+            xv[i] = a.norm_kind ? t * (wv[i] + 1.0f) : t * wv[i];
+        }
+        atab_write_half(atab, g >> 3, g & 7, hh, xv, hsc, hsm);
+    }
+    // the group's stats {scale of half 0, of half 1, sum of half 0, of half 1} from the pair
+    const float osc = __shfl_xor(hsc, 1), osm = __shfl_xor(hsm, 1);
+    if (live && hh == 0) {
+        const f32x4 stv = {hsc, osc, hsm, osm};
+        x.stats[(g >> 3) * 8 + (g & 7)] = stv;
+    }
+}
+
+// the 16 values of half hh of group g of the post-norm's four vectors
+__device__ __forceinline__ void post_load_half(const GemvArgs& a, int g, int hh, float* t2, float* xv, float* pw,
+                                               float* wv) {
+    const int e0 = g * 32 + 16 * hh;
+    const float4* ti = (const float4*)(a.x2 + e0);
+    const float4* xi = (const float4*)(a.x + e0);
+    const float4* pi = (const float4*)(a.post_w + e0);
+    const float4* wi = (const float4*)(a.norm_w + e0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 t = ti[i], u = xi[i], p4 = pi[i], w4 = wi[i];
+        t2[4 * i] = t.x; t2[4 * i + 1] = t.y; t2[4 * i + 2] = t.z; t2[4 * i + 3] = t.w;
+        xv[4 * i] = u.x; xv[4 * i + 1] = u.y; xv[4 * i + 2] = u.z; xv[4 * i + 3] = u.w;
+        pw[4 * i] = p4.x; pw[4 * i + 1] = p4.y; pw[4 * i + 2] = p4.z; pw[4 * i + 3] = p4.w;
+        wv[4 * i] = w4.x; wv[4 * i + 1] = w4.y; wv[4 * i + 2] = w4.z; wv[4 * i + 3] = w4.w;
+    }
+}
+
 // Input kinds of the matrix-core body's instantiations. XK_TAB: an activation table (XIN_TAB).
 // XK_ANY: a vector quantized here, its kind chosen at run time (XIN_F32 / XIN_NORM /
 // XIN_EMBED_NORM / XIN_POST). XK_F32: a plain f32 vector (XIN_F32), each thread's 32-element group
 // loaded before the weight ring, so the table is ready when those loads return instead of behind
 // the ring's (a wave's loads return in order), and without the other kinds' registers.
-enum { XK_TAB = 0, XK_ANY = 1, XK_F32 = 2 };
+// XK_POST: a Gemma-2 post-norm folded in (XIN_POST) with two threads per 32-element group, its four
+// vectors loaded before the weight ring.
+enum { XK_TAB = 0, XK_ANY = 1, XK_F32 = 2, XK_POST = 3 };
 
 // XK: the input kind (above). The workgroup is number wg of ng that share units [u0, u0 + nu) of
 // the launch.
@@ -1266,6 +1341,12 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             xg[4 * i] = t.x; xg[4 * i + 1] = t.y; xg[4 * i + 2] = t.z; xg[4 * i + 3] = t.w;
         }
     }
+    // XK_POST: this thread's half group of the post-norm's vectors (threads past the row's groups
+    // read its last group and write nothing)
+    constexpr int PN = XK == XK_POST ? 16 : 1;
+    float p_t2[PN], p_xv[PN], p_pw[PN], p_wv[PN];
+    if constexpr (XK == XK_POST)
+        post_load_half(a, min((int)threadIdx.x >> 1, a.G - 1), (int)threadIdx.x & 1, p_t2, p_xv, p_pw, p_wv);
     // the residual and the consumer's norm weight of the first tile's rows, when it is a residual
     // add: written by earlier launches, so they go out with the table rather than after the last
     // weights (where they would add a round trip to the epilogue)
@@ -1338,73 +1419,18 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             f32x4 stv = {st.x, st.y, st.z, st.w};
             x.stats[(g >> 3) * 8 + (g & 7)] = stv;
         }
+    } else if constexpr (XK == XK_POST) {
+        const int g = (int)threadIdx.x >> 1;
+        post_prologue_half(a, x, atab, g, (int)threadIdx.x & 1, g < a.G, p_t2, p_xv, p_pw, p_wv);
     } else if (a.xin == XIN_POST && 2 * a.G <= x.nw * 64) {
-        // Gemma-2 post-norm folded in (Gemma2ForwardPass.cs:90-96), two threads per 32-element
-        // group (one per 16-element half, the table's quantization unit): x2, x, post_w and the
-        // norm weight all load at once and stay in registers across the two reductions. The new
-        // residual is x + (x2 * rms(x2)) * (post_w + 1), the operation order of the separate
-        // post-norm kernel, then normalized as XIN_NORM.
+        // two threads per 32-element group (one per 16-element half, the table's quantization
+        // unit): x2, x, post_w and the norm weight all load at once and stay in registers across
+        // the two reductions
         const int g = (int)threadIdx.x >> 1, hh = (int)threadIdx.x & 1;
         const bool live = g < a.G;
-        const int e0 = g * 32 + 16 * hh;
         float t2[16], xv[16], pw[16], wv[16];
-        float ss = 0.0f;
-        if (live) {
-            const float4* ti = (const float4*)(a.x2 + e0);
-            const float4* xi = (const float4*)(a.x + e0);
-            const float4* pi = (const float4*)(a.post_w + e0);
-            const float4* wi = (const float4*)(a.norm_w + e0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 t = ti[i], u = xi[i], p4 = pi[i], w4 = wi[i];
-                t2[4 * i] = t.x; t2[4 * i + 1] = t.y; t2[4 * i + 2] = t.z; t2[4 * i + 3] = t.w;
-                xv[4 * i] = u.x; xv[4 * i + 1] = u.y; xv[4 * i + 2] = u.z; xv[4 * i + 3] = u.w;
-                pw[4 * i] = p4.x; pw[4 * i + 1] = p4.y; pw[4 * i + 2] = p4.z; pw[4 * i + 3] = p4.w;
-                wv[4 * i] = w4.x; wv[4 * i + 1] = w4.y; wv[4 * i + 2] = w4.z; wv[4 * i + 3] = w4.w;
-            }
-#pragma unroll
-            for (int i = 0; i < 16; i++) ss = fmaf(t2[i], t2[i], ss);
-        }
-        ss = wsum(ss);
-        if (x.lane == 0) x.red[x.wave] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int i = 0; i < x.nw; i++) tot += x.red[i];
-        const float prms = 1.0f / sqrtf(tot / (float)(a.G * 32) + 1e-6f);
-        __syncthreads();  // x.red is reused below
-        float ssq = 0.0f;
-        if (live) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) xv[i] = xv[i] + (t2[i] * prms) * (pw[i] + 1.0f);
-#pragma unroll
-            for (int i = 0; i < 16; i++) ssq = fmaf(xv[i], xv[i], ssq);
-        }
-        ssq = wsum(ssq);
-        if (x.lane == 0) x.red[x.wave] = ssq;
-        __syncthreads();
-        tot = 0.0f;
-        for (int i = 0; i < x.nw; i++) tot += x.red[i];
-        const float scale = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);  // rms
-        float hsc = 0.0f, hsm = 0.0f;
-        if (live) {
-            if (blockIdx.x == 0) {
-                float4* xo = (float4*)(a.x_out + e0);
-#pragma unroll
-                for (int i = 0; i < 4; i++) xo[i] = make_float4(xv[4 * i], xv[4 * i + 1], xv[4 * i + 2], xv[4 * i + 3]);
-            }
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float t = xv[i] * scale;
-                xv[i] = a.norm_kind ? t * (wv[i] + 1.0f) : t * wv[i];
-            }
-            atab_write_half(atab, g >> 3, g & 7, hh, xv, hsc, hsm);
-        }
-        // the group's stats {scale of half 0, of half 1, sum of half 0, of half 1} from the pair
-        const float osc = __shfl_xor(hsc, 1), osm = __shfl_xor(hsm, 1);
-        if (live && hh == 0) {
-            const f32x4 stv = {hsc, osc, hsm, osm};
-            x.stats[(g >> 3) * 8 + (g & 7)] = stv;
-        }
+        if (live) post_load_half(a, g, hh, t2, xv, pw, wv);
+        post_prologue_half(a, x, atab, g, hh, live, t2, xv, pw, wv);
     } else if (a.xin == XIN_POST && a.G <= x.nw * 64) {
         // Gemma-2 post-norm folded in (Gemma2ForwardPass.cs:90-96), one 32-element group per
         // thread: x2 and x stay in registers across the two reductions, so every vector is read
@@ -1708,9 +1734,11 @@ static MfKernel mf_kernel_mix(int kc) {
     }
 }
 template <int T>
-static MfKernel mf_kernel_ragged(bool tab, int kc) {
-    if (kc == 4) return tab ? k_gemv_mfma_r<T, 4, XK_TAB> : k_gemv_mfma_r<T, 4, XK_ANY>;
-    if (kc == 8) return tab ? k_gemv_mfma_r<T, 8, XK_TAB> : k_gemv_mfma_r<T, 8, XK_ANY>;
+static MfKernel mf_kernel_ragged(int xk, int kc) {
+    if (kc == 4)
+        return xk == XK_TAB ? k_gemv_mfma_r<T, 4, XK_TAB> : xk == XK_POST ? k_gemv_mfma_r<T, 4, XK_POST> : k_gemv_mfma_r<T, 4, XK_ANY>;
+    if (kc == 8)
+        return xk == XK_TAB ? k_gemv_mfma_r<T, 8, XK_TAB> : xk == XK_POST ? k_gemv_mfma_r<T, 8, XK_POST> : k_gemv_mfma_r<T, 8, XK_ANY>;
     return nullptr;
 }
 template <bool IL>
@@ -1718,11 +1746,13 @@ static MfKernel mf_kernel_layout(const GemvArgs& a, int kc) {
     const bool tab = a.xin == XIN_TAB;
     if constexpr (IL) {
         if (mf_ragged(a.G / 8)) {
+            // the post-norm's two threads per group: 2 G <= the workgroup's threads
+            const int xk = tab ? XK_TAB : (a.xin == XIN_POST && 2 * a.G <= 64 * a.nw) ? XK_POST : XK_ANY;
             switch (a.seg[0].type) {
-                case FLLM_TYPE_Q4_K: return mf_kernel_ragged<FLLM_TYPE_Q4_K>(tab, kc);
-                case FLLM_TYPE_Q6_K: return mf_kernel_ragged<FLLM_TYPE_Q6_K>(tab, kc);
-                case FLLM_TYPE_Q8_0: return mf_kernel_ragged<FLLM_TYPE_Q8_0>(tab, kc);
-                default: return mf_kernel_ragged<FLLM_TYPE_Q5_K>(tab, kc);
+                case FLLM_TYPE_Q4_K: return mf_kernel_ragged<FLLM_TYPE_Q4_K>(xk, kc);
+                case FLLM_TYPE_Q6_K: return mf_kernel_ragged<FLLM_TYPE_Q6_K>(xk, kc);
+                case FLLM_TYPE_Q8_0: return mf_kernel_ragged<FLLM_TYPE_Q8_0>(xk, kc);
+                default: return mf_kernel_ragged<FLLM_TYPE_Q5_K>(xk, kc);
             }
         }
     }
