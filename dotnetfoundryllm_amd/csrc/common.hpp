@@ -80,6 +80,19 @@ __host__ __device__ inline void kscale_min(const uint8_t* p, int g, int& sc, int
     }
 }
 
+// Q4_K in the matrix-core tile layout: each 8-byte half of a group's 16 qs bytes is stored as its
+// bytes 0, 2, 4, 6, 1, 3, 5, 7 (so one dword holds the half's elements 4 by, 4 by + 1 and the other
+// 4 by + 2, 4 by + 3, by = 0 .. 3: the activation table's order). q4t_src_byte(j): the group byte
+// stored at position j; q4t_pos(b): the position of group byte b.
+__host__ __device__ __forceinline__ int q4t_src_byte(int j) {
+    const int p = j & 7;
+    return (j & 8) + (p < 4 ? 2 * p : 2 * (p - 4) + 1);
+}
+__host__ __device__ __forceinline__ int q4t_pos(int b) {
+    const int o = b & 7;
+    return (b & 8) + ((o & 1) ? 4 + (o >> 1) : (o >> 1));
+}
+
 // FFN activation: 0 = SiLU, x * Sigmoid(x) (TensorOperations.cs:57-87); 1 = GELU, tanh form
 // (TensorOperations.cs:110-117)
 __device__ __forceinline__ float act_fn(float g, int act) {

@@ -814,8 +814,10 @@ __device__ __forceinline__ void tab_emit(const GemvArgs& a, float v, float sq, i
     }
 }
 
+// D2 + D1 / 256 + D0 / 65536 of a lane's three digit sums (D.x = D2 .. D.z = D0, each at most
+// 64 * 128 * 128 in magnitude, so 256 D1 + D0 fits an int32): two conversions and one fma
 __device__ __forceinline__ float mf_total(const v4i& D) {
-    return fmaf((float)D.z, 1.52587890625e-05f, fmaf((float)D.y, 0.00390625f, (float)D.x));
+    return fmaf((float)(D.y * 256 + D.z), 1.52587890625e-05f, (float)D.x);
 }
 
 // ---- Q4_K (Dequantizer.cs:251-294): 16-byte-aligned 144-byte blocks ---------------------------
@@ -844,14 +846,24 @@ __device__ __forceinline__ v4i q4_frag(uint32_t w0, uint32_t w1) {
     return r;
 }
 
+// The tile layout (k_pack_tiles) stores each 8-byte half of a group's qs as bytes 0, 2, 4, 6, 1, 3,
+// 5, 7, so its two dwords are q4_frag's E and O already: the fragment is four masks.
+struct MfQ4KT : MfQ4K {};
+__device__ __forceinline__ v4i q4_frag_t(uint32_t E, uint32_t O) {
+    v4i r = {(int)(E & 0x0F0F0F0Fu), (int)((E >> 4) & 0x0F0F0F0Fu), (int)(O & 0x0F0F0F0Fu),
+             (int)((O >> 4) & 0x0F0F0F0Fu)};
+    return r;
+}
+
 // 4 MFMAs over groups q and q+4 and their block scales; this lane's part of row n.
-__device__ __forceinline__ float mf_compute(const MfQ4K& r, const v4i* A, const f32x4& sA, const f32x4& sB, int q,
-                                            int) {
+template <bool TILES>
+__device__ __forceinline__ float mf_compute_q4k(const MfQ4K& r, const v4i* A, const f32x4& sA, const f32x4& sB, int q) {
     const v4i z = {0, 0, 0, 0};
-    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], q4_frag(r.qa.x, r.qa.y), z, 0, 0, 0);
-    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], q4_frag(r.qa.z, r.qa.w), z, 0, 0, 0);
-    const v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], q4_frag(r.qb.x, r.qb.y), z, 0, 0, 0);
-    const v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], q4_frag(r.qb.z, r.qb.w), z, 0, 0, 0);
+    auto frag = [](uint32_t w0, uint32_t w1) { return TILES ? q4_frag_t(w0, w1) : q4_frag(w0, w1); };
+    const v4i D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], frag(r.qa.x, r.qa.y), z, 0, 0, 0);
+    const v4i D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], frag(r.qa.z, r.qa.w), z, 0, 0, 0);
+    const v4i D2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], frag(r.qb.x, r.qb.y), z, 0, 0, 0);
+    const v4i D3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], frag(r.qb.z, r.qb.w), z, 0, 0, 0);
     // DecodeKScaleMin (Dequantizer.cs:506-521) for groups q (< 4) and q + 4
     const int sh = 8 * q;
     const uint32_t a = (r.hdr.y >> sh) & 0xFF, b = (r.hdr.z >> sh) & 0xFF, c = (r.hdr.w >> sh) & 0xFF;
@@ -864,6 +876,15 @@ __device__ __forceinline__ float mf_compute(const MfQ4K& r, const v4i* A, const 
     const float tB = fmaf(sB.x, mf_total(D2), sB.y * mf_total(D3));
     const float y = fmaf(dgA, tA, -mgA * (sA.z + sA.w));
     return y + fmaf(dgB, tB, -mgB * (sB.z + sB.w));
+}
+
+__device__ __forceinline__ float mf_compute(const MfQ4K& r, const v4i* A, const f32x4& sA, const f32x4& sB, int q,
+                                            int) {
+    return mf_compute_q4k<false>(r, A, sA, sB, q);
+}
+__device__ __forceinline__ float mf_compute(const MfQ4KT& r, const v4i* A, const f32x4& sA, const f32x4& sB, int q,
+                                            int) {
+    return mf_compute_q4k<true>(r, A, sA, sB, q);
 }
 
 // ---- Q6_K (Dequantizer.cs:378-417): 210-byte blocks -------------------------------------------
@@ -960,7 +981,8 @@ __device__ __forceinline__ float mf_compute(const MfQ6KT& r, const v4i* A, const
 
 // register image of one chunk of one lane, per weight type and layout
 template <int T, bool IL> struct MfPick;
-template <bool IL> struct MfPick<FLLM_TYPE_Q4_K, IL> { using Raw = MfQ4K; };
+template <> struct MfPick<FLLM_TYPE_Q4_K, false> { using Raw = MfQ4K; };
+template <> struct MfPick<FLLM_TYPE_Q4_K, true> { using Raw = MfQ4KT; };
 template <> struct MfPick<FLLM_TYPE_Q6_K, false> { using Raw = MfQ6K; };
 template <> struct MfPick<FLLM_TYPE_Q6_K, true> { using Raw = MfQ6KT; };
 
@@ -2015,8 +2037,9 @@ __global__ void k_pack_tiles(int type, const uint8_t* __restrict__ src, uint8_t*
                 reg[3072 + 4 * L + 2] = b[200 + 2 * q];
                 reg[3072 + 4 * L + 3] = b[201 + 2 * q];
             } else {
-                for (int j = 0; j < 16; j++) reg[16 * L + j] = b[16 + 16 * q + j];
-                for (int j = 0; j < 16; j++) reg[1024 + 16 * L + j] = b[80 + 16 * q + j];
+                // Q4_K: each 8-byte half of a group's qs stored as its bytes 0, 2, 4, 6, 1, 3, 5, 7
+                for (int j = 0; j < 16; j++) reg[16 * L + j] = b[16 + 16 * q + q4t_src_byte(j)];
+                for (int j = 0; j < 16; j++) reg[1024 + 16 * L + j] = b[80 + 16 * q + q4t_src_byte(j)];
             }
         }
         if (type == FLLM_TYPE_Q6_K) {

@@ -107,7 +107,8 @@ template <> struct PfW<FLLM_TYPE_Q4_K> {
         const uint32_t wd[4] = {w4.qs.x, w4.qs.y, w4.qs.z, w4.qs.w};
 #pragma unroll
         for (int i = 0; i < 32; i++) {
-            const uint32_t byte = (wd[i >> 3] >> (8 * ((i >> 1) & 3))) & 0xFFu;
+            const int at = q4t_pos(i >> 1);  // the tile layout's position of group byte i / 2
+            const uint32_t byte = (wd[at >> 2] >> (8 * (at & 3))) & 0xFFu;
             const int q = (i & 1) ? (int)(byte >> 4) : (int)(byte & 15u);
             v[i] = dg * (float)q - mg;
         }
@@ -726,10 +727,19 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
                         pf_q5_pairs<2>(wraw.qs.z, z0, sc2, out + 8);
                         pf_q5_pairs<3>(wraw.qs.w, z1, sc2, out + 12);
                     } else {
-                        pf_q4_pairs(wraw.qs.x, sc2, out);
-                        pf_q4_pairs(wraw.qs.y, sc2, out + 4);
-                        pf_q4_pairs(wraw.qs.z, sc2, out + 8);
-                        pf_q4_pairs(wraw.qs.w, sc2, out + 12);
+                        // the tile layout's dwords of a half: its bytes 0, 2, 4, 6 and 1, 3, 5, 7
+                        // (element pairs 0, 2, 4, 6 and 1, 3, 5, 7 of the half)
+                        uint32_t ev[4], od[4];
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            pf_q4_pairs(hf ? wraw.qs.z : wraw.qs.x, sc2, ev);
+                            pf_q4_pairs(hf ? wraw.qs.w : wraw.qs.y, sc2, od);
+#pragma unroll
+                            for (int b = 0; b < 4; b++) {
+                                out[8 * hf + 2 * b] = ev[b];
+                                out[8 * hf + 2 * b + 1] = od[b];
+                            }
+                        }
                     }
                 } else {
 #pragma unroll
