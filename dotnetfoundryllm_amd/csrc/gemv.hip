@@ -1352,13 +1352,18 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
         for (int k = 0; k < TSL; k++)
             if (x.kb0 + min(x.lane + 64 * k, KC * 16 - 1) / 16 >= NB) tsq[k] = 0.0f;
     }
-    // XK_F32: this thread's group of the input (threads past the row's groups read its last group
-    // and write nothing)
-    float xg[XK == XK_F32 ? 32 : 1];
+    // XK_F32: with 8 or 4 chunks per wave a wave quantizes its own chunks' groups (one per lane, or
+    // a 16-element half per lane), so it needs no other wave's entries (XL: lanes per group); with
+    // fewer, thread t takes group t of the row (XL = 0). Threads past the groups read the row's last
+    // group and write nothing.
+    constexpr int XL = XK != XK_F32 ? 0 : KC == 8 ? 1 : KC == 4 ? 2 : 0;
+    constexpr int XN = XK != XK_F32 ? 1 : XL == 2 ? 16 : 32;
+    const int xgrp = XL == 1 ? x.kb0 * 8 + x.lane : XL == 2 ? x.kb0 * 8 + (x.lane >> 1) : (int)threadIdx.x;
+    float xg[XN];
     if constexpr (XK == XK_F32) {
-        const float4* xi = (const float4*)(a.x + min((int)threadIdx.x, a.G - 1) * 32);
+        const float4* xi = (const float4*)(a.x + min(xgrp, a.G - 1) * 32 + (XL == 2 ? 16 * (x.lane & 1) : 0));
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < XN / 4; i++) {
             const float4 t = xi[i];
             xg[4 * i] = t.x; xg[4 * i + 1] = t.y; xg[4 * i + 2] = t.z; xg[4 * i + 3] = t.w;
         }
@@ -1405,7 +1410,8 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- prologue: the activation table -------------------------------------------------------
-    for (int e = threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += x.nw * 64) {
+    // (a wave-local table: every wave writes the zero block itself, so no wave waits for another)
+    for (int e = XL ? x.lane : (int)threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += XL ? 64 : x.nw * 64) {
         const u32x4 z4 = {0u, 0u, 0u, 0u};
         zeros[e] = z4;
     }
@@ -1434,8 +1440,18 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             x.xs = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
         }
     } else if constexpr (XK == XK_F32) {
-        const int g = (int)threadIdx.x;
-        if (g < a.G) {
+        // (a wave's items read only its own chunks' entries)
+        const int g = xgrp;
+        if constexpr (XL == 2) {
+            float hsc = 0.0f, hsm = 0.0f;
+            atab_write_half(atab, g >> 3, g & 7, x.lane & 1, xg, hsc, hsm);
+            // the group's stats {scale of half 0, of half 1, sum of half 0, of half 1} from the pair
+            const float osc = __shfl_xor(hsc, 1), osm = __shfl_xor(hsm, 1);
+            if ((x.lane & 1) == 0) {
+                const f32x4 stv = {hsc, osc, hsm, osm};
+                x.stats[(g >> 3) * 8 + (g & 7)] = stv;
+            }
+        } else if (XL == 1 ? x.lane < 8 * KC : g < a.G) {
             float4 st;
             atab_write(atab, g >> 3, g & 7, xg, &st);
             f32x4 stv = {st.x, st.y, st.z, st.w};
@@ -1612,7 +1628,14 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             x.stats[(g >> 3) * 8 + (g & 7)] = stv;
         }
     }
-    __syncthreads();
+    if constexpr (XL != 0) {
+        // the wave's own entries, written by its own lanes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+        __syncthreads();
+    }
 
     // ---- items ----------------------------------------------------------------------------------
     unsigned long long best = 0ull;
