@@ -1411,7 +1411,8 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
 
     // ---- prologue: the activation table -------------------------------------------------------
     // (a wave-local table: every wave writes the zero block itself, so no wave waits for another)
-    for (int e = XL ? x.lane : (int)threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += XL ? 64 : x.nw * 64) {
+    constexpr bool WAVE_LOCAL = XL != 0 || TABIN;
+    for (int e = WAVE_LOCAL ? x.lane : (int)threadIdx.x; e < MF_ZERO_ENTRIES(KC); e += WAVE_LOCAL ? 64 : x.nw * 64) {
         const u32x4 z4 = {0u, 0u, 0u, 0u};
         zeros[e] = z4;
     }
@@ -1428,13 +1429,14 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
 #pragma unroll
         for (int k = 0; k < TDL; k++) atab[x.kb0 * 48 + min(x.lane + 64 * k, KC * 48 - 1)] = tdig[k];
         x.stats[x.kb0 * 8 + min(x.lane, KC * 8 - 1)] = *(const f32x4*)&tst;
-        float s2 = 0.0f;
-#pragma unroll
-        for (int k = 0; k < TSL; k++) s2 += (x.lane + 64 * k < KC * 16 && a.xssq) ? tsq[k] : 0.0f;
-        s2 = wsum(s2);
-        if (x.lane == 0) x.red[x.wave] = s2;
-        __syncthreads();
         if (a.xssq) {
+            // the RMSNorm factor needs every wave's share of the sum of squares
+            float s2 = 0.0f;
+#pragma unroll
+            for (int k = 0; k < TSL; k++) s2 += x.lane + 64 * k < KC * 16 ? tsq[k] : 0.0f;
+            s2 = wsum(s2);
+            if (x.lane == 0) x.red[x.wave] = s2;
+            __syncthreads();
             float tot = 0.0f;
             for (int i = 0; i < x.nw; i++) tot += x.red[i];
             x.xs = 1.0f / sqrtf(tot / (float)(a.G * 32) + a.eps);
@@ -1628,8 +1630,9 @@ __device__ __forceinline__ void mfma_body(const GemvArgs& a, int u0, int nu, int
             x.stats[(g >> 3) * 8 + (g & 7)] = stv;
         }
     }
-    if constexpr (XL != 0) {
-        // the wave's own entries, written by its own lanes
+    if constexpr (WAVE_LOCAL) {
+        // a wave's items read only its own chunks' entries, written by its own lanes (the table
+        // input's copy or the f32 input's quantization)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
