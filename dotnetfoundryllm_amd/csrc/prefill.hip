@@ -372,8 +372,12 @@ __device__ __forceinline__ int pf_seg_of(const PfGemm& a, int& bx) {
 }
 
 // ---- fp16 form ----------------------------------------------------------------------------------
-// LDS rows of PF_BK halves plus 16 bytes; X and W as [plane][row][k] with plane 0 = hi, 1 = lo.
-constexpr int PF_LDH = PF_BK + 8;
+// LDS rows of PF_BK halves plus 32 bytes; X and W as [plane][row][k] with plane 0 = hi, 1 = lo.
+// A 128-bit LDS read on gfx950 is served for lanes 0-31 and 32-63 apart, over 128 banks of 4 bytes:
+// an operand read (16 rows x two 16-byte columns per half-wave) is conflict-free when the row
+// stride is 40 dwords (the 16 rows' 32-byte spans tile the 128 banks); at 36 dwords, rows r and
+// r + 7 share banks and every such read took two passes.
+constexpr int PF_LDH = PF_BK + 16;
 typedef _Float16 pf_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 pf_hv2 __attribute__((ext_vector_type(2)));
 
@@ -601,7 +605,7 @@ __device__ __forceinline__ void pf_gemm_tile_h(const PfGemm& a, const PfSeg& sg,
 // (v_g hi, v_g lo, v_g hi) for v_g = -dmin m_g against, per token, (X_g hi, X_g hi, X_g lo), the
 // three products of the two splits, added to the same accumulator. The group sums are stored times
 // 2^-6 (to stay in fp16's range) and v_g taken times 2^6, so their products are unchanged.
-constexpr int PF_LDV = 40;  // LDS row stride (halves) of a block's min-term slice
+constexpr int PF_LDV = 48;  // LDS row stride (halves) of a block's min-term slice: 24 dwords, conflict-free
 
 template <int BM>
 static constexpr size_t pf_gemm_lds_k() {
