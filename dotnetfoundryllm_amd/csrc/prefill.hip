@@ -1586,7 +1586,7 @@ hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w
 // Mistral / Qwen2 / Gemma2 variants) ----------------------------------------------------------------
 // Workgroup = (query head, block of 64 consecutive queries, the last block first), wave w = queries
 // 16 w .. + 15. Keys go in blocks of 64 rows (32 for head_dim 256) of the head's kv head, staged in
-// LDS (K and V rows padded to HD + 4 floats); the next block's rows are loaded into registers while
+// LDS (K rows padded to HD + 8 floats, V rows to HD + 16); the next block's rows are loaded into registers while
 // the current one multiplies. Per
 // block a wave forms the transposed scores S^T = K Q^T on the f32 matrix cores
 // (v_mfma_f32_16x16x4f32: lane l holds keys 16 t + 4 (l >> 4) + e of query l & 15), updates the running
@@ -1605,18 +1605,25 @@ template <int HD> struct PfAk {
     static constexpr bool pre = HD <= 128;
 };
 
+// LDS row strides (floats) of the staged K and V rows. A half-wave reads K as 16 rows x two 16-byte
+// columns (conflict-free over gfx950's 128 banks when the stride is 8 mod 16 dwords: the rows'
+// 32-byte spans tile the banks) and V as two rows 4 apart x 64 dwords (conflict-free when 4 strides
+// are 64 mod 128 dwords); HD + 4 had every K and V read take two passes.
+template <int HD> struct PfAld {
+    static constexpr int k = HD + 8, v = HD + 16;
+};
 template <int HD>
 static constexpr size_t pf_attn_lds() {
-    return sizeof(float) * 2 * (size_t)PfAk<HD>::v * (HD + 4);
+    return sizeof(float) * (size_t)PfAk<HD>::v * (PfAld<HD>::k + PfAld<HD>::v);
 }
 
 template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::pre ? 1 : 2))) void k_pf_attn(const PfAttn a) {
-    constexpr int LD = HD + 4, NU = HD / 16, NT = HD / 16;
+    constexpr int LDK = PfAld<HD>::k, LDV = PfAld<HD>::v, NU = HD / 16, NT = HD / 16;
     constexpr int PF_AK = PfAk<HD>::v, KT = PF_AK / 16;  // key block and its 16-key MFMA tiles
     extern __shared__ float pa_lds[];
-    float* sk = pa_lds;             // [PF_AK][LD]
-    float* sv = sk + PF_AK * LD;    // [PF_AK][LD]
+    float* sk = pa_lds;             // [PF_AK][LDK]
+    float* sv = sk + PF_AK * LDK;   // [PF_AK][LDV]
     // query blocks from the last (the most keys under the causal mask) to the first, so that the
     // longest workgroups are dispatched first and the short ones fill in behind them
     const int h = blockIdx.x, qb = ((int)gridDim.y - 1 - (int)blockIdx.y) * PF_AQ;
@@ -1669,8 +1676,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
 #pragma unroll
             for (int i = 0; i < NPC; i++) {
                 const int j = jrow + i * (256 / (HD / 4));
-                *(float4*)(sk + j * LD + d4) = make_float4(pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]);
-                *(float4*)(sv + j * LD + d4) = make_float4(pv[4 * i], pv[4 * i + 1], pv[4 * i + 2], pv[4 * i + 3]);
+                *(float4*)(sk + j * LDK + d4) = make_float4(pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]);
+                *(float4*)(sv + j * LDV + d4) = make_float4(pv[4 * i], pv[4 * i + 1], pv[4 * i + 2], pv[4 * i + 3]);
             }
             if (kb + PF_AK <= kend) {
 #pragma unroll
@@ -1695,8 +1702,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
 #pragma unroll
             for (int i = 0; i < NPC; i++) {
                 const int j = jrow + i * (256 / (HD / 4));
-                *(float4*)(sk + j * LD + d4) = k4[i];
-                *(float4*)(sv + j * LD + d4) = v4[i];
+                *(float4*)(sk + j * LDK + d4) = k4[i];
+                *(float4*)(sv + j * LDV + d4) = v4[i];
             }
         }
         __syncthreads();
@@ -1708,7 +1715,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
         for (int u = 0; u < NU; u++)
 #pragma unroll
             for (int t = 0; t < KT; t++) {
-                const float4 kr = *(const float4*)(sk + (16 * t + q16) * LD + 16 * u + 4 * kq);
+                const float4 kr = *(const float4*)(sk + (16 * t + q16) * LDK + 16 * u + 4 * kq);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.x, qr[u].x, s[t], 0, 0, 0);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.y, qr[u].y, s[t], 0, 0, 0);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr.z, qr[u].z, s[t], 0, 0, 0);
@@ -1752,7 +1759,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
         for (int t = 0; t < KT; t++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float* vr = sv + (16 * t + 4 * kq + e) * LD + 4 * q16;
+                const float* vr = sv + (16 * t + 4 * kq + e) * LDV + 4 * q16;
 #pragma unroll
                 for (int c = 0; c < HD / 64; c++) {
                     const float4 vv = *(const float4*)(vr + 64 * c);
