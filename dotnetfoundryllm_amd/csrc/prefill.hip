@@ -1079,6 +1079,21 @@ __global__ __launch_bounds__(256) void k_pf_gemm_tiles_h(const PfGemm a) {
         pf_gemm_tile_h<FLLM_TYPE_Q4_K, BM>(a, sg, bx * PF_BN, blockIdx.y * BM, pf_ldh, sw);
 }
 
+// launches whose segments are all tile-interleaved Q8_0: the exact-integer Q8_0 form uses one weight
+// plane plus the block scales (pf_gemm_lds_q8 bytes instead of pf_gemm_lds_h), so three workgroups
+// share a CU
+template <int BM>
+static constexpr size_t pf_gemm_lds_q8() {
+    return sizeof(_Float16) * (size_t)(2 * BM + PF_BN) * PF_LDH + sizeof(float) * 2 * PF_BN;
+}
+template <int BM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_pf_gemm_q8t(const PfGemm a) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 pf_ld8[];
+    int bx = blockIdx.x;
+    const int si = pf_seg_of(a, bx);
+    pf_gemm_tile_h<FLLM_TYPE_Q8_0, BM>(a, a.seg[si], bx * PF_BN, blockIdx.y * BM, pf_ld8, pf_ld8 + (size_t)2 * BM * PF_LDH);
+}
+
 // launches whose segments are all tile-interleaved Q5_K
 template <int BM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1))) void k_pf_gemm_q5k(const PfGemm a) {
@@ -1396,8 +1411,9 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         if (a.ldh < a.K || a.ldh % 8 != 0 || a.xs == nullptr) return hipErrorInvalidValue;
         bool all_q4k = tiles;
         for (int i = 0; i < a.nseg; i++) all_q4k = all_q4k && a.seg[i].type == FLLM_TYPE_Q4_K;
-        bool all_q6k = tiles, all_q5k = tiles, q46 = tiles;
+        bool all_q6k = tiles, all_q5k = tiles, q46 = tiles, all_q8 = tiles;
         for (int i = 0; i < a.nseg; i++) {
+            all_q8 = all_q8 && a.seg[i].type == FLLM_TYPE_Q8_0;
             all_q6k = all_q6k && a.seg[i].type == FLLM_TYPE_Q6_K;
             all_q5k = all_q5k && a.seg[i].type == FLLM_TYPE_Q5_K;
             q46 = q46 && (a.seg[i].type == FLLM_TYPE_Q4_K || a.seg[i].type == FLLM_TYPE_Q6_K);
@@ -1411,6 +1427,9 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
         } else if (all_q6k) {
             k = k_pf_gemm_q6k<64>;
             lds = pf_gemm_lds_q6<64>();
+        } else if (all_q8) {
+            k = k_pf_gemm_q8t<64>;
+            lds = pf_gemm_lds_q8<64>();
         } else if (q46) {
             k = k_pf_gemm_q46<64>;
             lds = std::max(pf_gemm_lds_k<64>(), pf_gemm_lds_q6<64>());
