@@ -605,7 +605,9 @@ __device__ __forceinline__ void pf_gemm_tile_h(const PfGemm& a, const PfSeg& sg,
 // (v_g hi, v_g lo, v_g hi) for v_g = -dmin m_g against, per token, (X_g hi, X_g hi, X_g lo), the
 // three products of the two splits, added to the same accumulator. The group sums are stored times
 // 2^-6 (to stay in fp16's range) and v_g taken times 2^6, so their products are unchanged.
-constexpr int PF_LDV = 48;  // LDS row stride (halves) of a block's min-term slice: 24 dwords, conflict-free
+// LDS row stride (halves) of a block's min-term slice: its three used 16-byte chunks (the fourth
+// of the MFMA's K slice is zero and is not stored: the lanes that would read it take zeros)
+constexpr int PF_LDV = 24;
 
 template <int BM>
 static constexpr size_t pf_gemm_lds_k() {
@@ -776,7 +778,6 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
                     dv[0] = make_uint4(vh[0], vh[1], vh[2], vh[3]);
                     dv[1] = make_uint4(vl[0], vl[1], vl[2], vl[3]);
                     dv[2] = dv[0];
-                    dv[3] = make_uint4(0u, 0u, 0u, 0u);
                 }
                 // tokens: (X hi, X hi, X lo, 0) against (v hi, v lo, v hi, 0)
                 if (vt < BM) {
@@ -786,7 +787,6 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
                         av[1] = xv;
                     } else {
                         av[2] = xv;
-                        av[3] = make_uint4(0u, 0u, 0u, 0u);
                     }
                 }
             }
@@ -820,11 +820,15 @@ __device__ __forceinline__ void pf_gemm_tile_q4k(const PfGemm& a, const PfSeg& s
         // the block's d times its sum, and its min term (sd / sav / swv were written at the block's
         // first step and are rewritten only after the next block's first barrier)
         const int ko = 8 * (lane >> 4);
+        const bool kz = (lane >> 4) == 3;  // the slice's fourth chunk: zeros
+        const pf_h8 z8 = {};
         pf_h8 av[TI], bv[4];
 #pragma unroll
-        for (int i = 0; i < TI; i++) av[i] = *(const pf_h8*)(sav + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDV + ko);
+        for (int i = 0; i < TI; i++)
+            av[i] = kz ? z8 : *(const pf_h8*)(sav + (size_t)(WM * wm + 16 * i + (lane & 15)) * PF_LDV + (kz ? 0 : ko));
 #pragma unroll
-        for (int j = 0; j < 4; j++) bv[j] = *(const pf_h8*)(swv + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDV + ko);
+        for (int j = 0; j < 4; j++)
+            bv[j] = kz ? z8 : *(const pf_h8*)(swv + (size_t)(64 * wn + 16 * j + (lane & 15)) * PF_LDV + (kz ? 0 : ko));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const float d = sd[64 * wn + 16 * j + (lane & 15)];
@@ -1096,7 +1100,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
 
 // launches whose segments are all tile-interleaved Q5_K
 template <int BM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1))) void k_pf_gemm_q5k(const PfGemm a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 3 : 1))) void k_pf_gemm_q5k(const PfGemm a) {
     extern __shared__ __attribute__((aligned(16))) _Float16 pf_ld5[];
     int bx = blockIdx.x;
     const int si = pf_seg_of(a, bx);
@@ -1105,7 +1109,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 
 
 // launches whose segments are all tile-interleaved Q4_K
 template <int BM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 2 : 1))) void k_pf_gemm_q4k(const PfGemm a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 64 ? 3 : 1))) void k_pf_gemm_q4k(const PfGemm a) {
     extern __shared__ __attribute__((aligned(16))) _Float16 pf_ldk[];
     int bx = blockIdx.x;
     const int si = pf_seg_of(a, bx);
