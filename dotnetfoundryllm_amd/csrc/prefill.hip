@@ -1472,6 +1472,18 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
             const int64_t w_now = (base * nsplit + want - 1) / want, w_next = (base * 2 * nsplit + want - 1) / want;
             if (w_next < 2 * w_now) nsplit *= 2;
         }
+        // a grid of more tiles than resident workgroups whose last wave is short (Qwen2-7B's down
+        // and o at 2047 tokens: 896 tiles on 768 slots of the three-per-CU forms, two waves of
+        // one tile each) splits K in two when that packs the waves at least a quarter tighter:
+        // 1792 half tiles are three waves of half the length
+        int per_cu = 0;
+        if (side_by_side && nsplit == 1 && (a.K / 256) % 2 == 0 &&
+            (size_t)a.T * (size_t)a.seg[0].ldy <= a.part_cap &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, 256, lds) == hipSuccess && per_cu > 0) {
+            const int64_t slots = (int64_t)per_cu * (n_cu > 0 ? n_cu : 256);
+            const int64_t w1 = (base + slots - 1) / slots, w2 = (2 * base + slots - 1) / slots;
+            if (base > slots && 2 * w2 <= 3 * w1) nsplit = 2;
+        }
     }
     a.nsplit = nsplit;
     a.kpart = a.K / nsplit;
