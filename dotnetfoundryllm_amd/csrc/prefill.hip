@@ -25,6 +25,9 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 namespace fllm {
 
@@ -1391,6 +1394,19 @@ static hipError_t pf_lds_attr(const void* k, size_t bytes) {
     return hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
+// resident workgroups of 256 threads per CU for a GEMM kernel at its LDS size (asked once per kernel)
+static int pf_resident(PfGemmKernel k, size_t lds) {
+    static std::mutex mu;
+    static std::vector<std::pair<PfGemmKernel, int>> seen;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& e : seen)
+        if (e.first == k) return e.second;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, 256, lds) != hipSuccess) per_cu = 0;
+    seen.emplace_back(k, per_cu);
+    return per_cu;
+}
+
 hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
     if (a.T <= 0 || a.nseg <= 0) return hipSuccess;
     if (a.nseg > 3 || a.K <= 0 || a.K % 32 != 0 || a.ldx < a.K || a.ldx % 4 != 0) return hipErrorInvalidValue;
@@ -1448,11 +1464,17 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
     hipError_t e = pf_lds_attr((const void*)k, lds);
     if (e != hipSuccess) return e;
     constexpr int bm = 64;
-    // a short grid splits K (parts of whole 512-element multiples) when the segments fill the rows
-    // of one buffer side by side and the scratch holds the extra parts
-    int nsplit = 1;
-    if (a.part != nullptr) {
-        const int64_t base = col_tiles * ((a.T + bm - 1) / bm), want = 2 * (int64_t)(n_cu > 0 ? n_cu : 256);
+    // K split: a launch whose segments fill the rows of one buffer side by side may run its K in
+    // nsplit parts of whole 256-element blocks (part 0 into y, parts z > 0 into the scratch, then a
+    // reduction in order). The choice minimises waves of resident workgroups x blocks per part
+    // plus the reduction's bytes, in units of one block of one full wave: about 0.0118 us per
+    // resident workgroup slot (a 64 x 128 tile's fp16 products at the forms' measured rate), the
+    // reduction reading the parts and y and writing y at 4 TB/s. Llama-3-8B at 511 tokens: o 256
+    // tiles in 3 parts on 768 slots, down 256 in 2 on 512, q/k/v 384 in 4; Qwen2-7B at 2047 tokens:
+    // down 896 tiles in 4 on 768.
+    int nsplit = 1, nbk = 0;
+    if (a.part != nullptr && a.K % 256 == 0) {
+        const int64_t base = col_tiles * ((a.T + bm - 1) / bm);
         bool side_by_side = true;
         int64_t off = 0;
         for (int i = 0; i < a.nseg; i++) {
@@ -1461,32 +1483,32 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
             off += g.N;
         }
         side_by_side = side_by_side && off == a.seg[0].ldy;
-        while (side_by_side && nsplit < 4 && base * nsplit < want && a.K % (512 * nsplit) == 0 &&
-               (size_t)(2 * nsplit - 1) * (size_t)a.T * (size_t)a.seg[0].ldy <= a.part_cap)
-            nsplit *= 2;
-        // once more when the split grid ends in a partly filled wave of resident workgroups and
-        // shorter parts shorten the whole: waves x part length, w_next / 2 nsplit < w_now / nsplit
-        // (q/k/v at 511 tokens: 384 tiles in 2 parts are 1.5 waves of 512, in 4 parts 3)
-        if (side_by_side && nsplit > 1 && nsplit < 4 && a.K % (512 * nsplit) == 0 &&
-            (size_t)(2 * nsplit - 1) * (size_t)a.T * (size_t)a.seg[0].ldy <= a.part_cap) {
-            const int64_t w_now = (base * nsplit + want - 1) / want, w_next = (base * 2 * nsplit + want - 1) / want;
-            if (w_next < 2 * w_now) nsplit *= 2;
-        }
-        // a grid of more tiles than resident workgroups whose last wave is short (Qwen2-7B's down
-        // and o at 2047 tokens: 896 tiles on 768 slots of the three-per-CU forms, two waves of
-        // one tile each) splits K in two when that packs the waves at least a quarter tighter:
-        // 1792 half tiles are three waves of half the length
-        int per_cu = 0;
-        if (side_by_side && nsplit == 1 && (a.K / 256) % 2 == 0 &&
-            (size_t)a.T * (size_t)a.seg[0].ldy <= a.part_cap &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k, 256, lds) == hipSuccess && per_cu > 0) {
+        const int per_cu = side_by_side ? pf_resident(k, lds) : 0;
+        if (per_cu > 0) {
             const int64_t slots = (int64_t)per_cu * (n_cu > 0 ? n_cu : 256);
-            const int64_t w1 = (base + slots - 1) / slots, w2 = (2 * base + slots - 1) / slots;
-            if (base > slots && 2 * w2 <= 3 * w1) nsplit = 2;
+            const int nb = a.K / 256;
+            const double out_bytes = 4.0 * (double)a.T * (double)a.seg[0].ldy;
+            const double unit_us = 0.0118 * (double)slots;  // one block of one full wave
+            double best = 0.0;
+            // grids of three or more waves unsplit (there the last wave's share is small and the
+            // reduction's cost was not repaid: Gemma-2-9B's o at 4096 tokens ran 6% longer in 2 parts)
+            const int nmax = (base + slots - 1) / slots <= 2 ? 4 : 1;
+            for (int n = 1; n <= nmax && n <= nb; n++) {
+                if (n > 1 && (size_t)(n - 1) * (size_t)a.T * (size_t)a.seg[0].ldy > a.part_cap) break;
+                const int64_t waves = (base * n + slots - 1) / slots;
+                const int bpp = (nb + n - 1) / n;
+                if ((n - 1) * bpp >= nb) continue;  // every part holds at least one block
+                const double cost = (double)waves * bpp + (n > 1 ? (n + 1) * out_bytes / 4.0e6 / unit_us : 0.0);
+                if (n == 1 || cost < best) {
+                    best = cost;
+                    nsplit = n;
+                    nbk = bpp;
+                }
+            }
         }
     }
     a.nsplit = nsplit;
-    a.kpart = a.K / nsplit;
+    a.kpart = nsplit > 1 ? 256 * nbk : a.K;
     dim3 grid((unsigned)col_tiles, (unsigned)((a.T + bm - 1) / bm), (unsigned)nsplit);
     k<<<grid, 256, lds, st>>>(a);
     e = hipGetLastError();
