@@ -29,10 +29,11 @@ struct PfGemm {
     int add;  // 1: y += X W^T (residual add), 0: y = X W^T
     int nseg;
     PfSeg seg[3];
-    // optional scratch of part_cap floats: a launch whose grid leaves fewer than two workgroups per
-    // CU splits K over grid.z (nsplit parts of kpart, set by launch_pf_gemm) when its segments fill
-    // one buffer's rows side by side; part 0 writes y, part z > 0 its own [T][ldy] slice of part,
-    // and a reduction adds the slices into y in order
+    // optional scratch of part_cap floats: a launch whose grid is at most two waves of resident
+    // workgroups may split K over grid.z (nsplit parts of kpart whole 256-element blocks, the last
+    // one possibly shorter, set by launch_pf_gemm) when its segments fill one buffer's rows side by
+    // side; part 0 writes y, part z > 0 its own [T][ldy] slice of part, and a reduction adds the
+    // slices into y in order
     float* part;
     size_t part_cap;
     int nsplit, kpart;
