@@ -1757,6 +1757,7 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         at.q = s->pf_qkv; at.ldq = ldq; at.kc = kc; at.vc = vc; at.out = s->pf_att;
         at.T = T; at.pos0 = pos0; at.nh = d.n_heads; at.nkv = d.n_kv_heads; at.hd = d.head_dim; at.kvdim = kvdim;
         at.window = layer_window(d, l); at.scale = d.attn_scale; at.softcap = gemma ? d.attn_softcap : 0.0f;
+        at.part = s->pf_part; at.part_cap = s->pf_part_cap; at.n_cu = s->m->ctx->n_cu;
         STEP("pf_attention", 8.0 * (double)kvdim * (pos0 + T) + 8.0 * T * qdim, launch_pf_attn(at, s->st));
         {
             const Tensor* w[1] = {&L.o};

@@ -25,6 +25,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <utility>
 #include <vector>
@@ -1682,8 +1683,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
     float* sk = pa_lds;             // [PF_AK][LDK]
     float* sv = sk + PF_AK * LDK;   // [PF_AK][LDV]
     // query blocks from the last (the most keys under the causal mask) to the first, so that the
-    // longest workgroups are dispatched first and the short ones fill in behind them
-    const int h = blockIdx.x, qb = ((int)gridDim.y - 1 - (int)blockIdx.y) * PF_AQ;
+    // longest workgroups are dispatched first and the short ones fill in behind them. With a.split,
+    // rows 2 i and 2 i + 1 of the grid are the first and second half of the key blocks of query
+    // block nqb - 1 - i (every block but block 0, which stays whole in the last row): the halves
+    // leave their unnormalised sums, max and sum in a.part for k_pf_attn_merge.
+    const int nqb = (a.T + PF_AQ - 1) / PF_AQ;
+    int qbi = nqb - 1 - (int)blockIdx.y, half = -1;
+    if (a.split) {
+        const int y = (int)blockIdx.y;
+        qbi = y < 2 * (nqb - 1) ? nqb - 1 - (y >> 1) : 0;
+        half = y < 2 * (nqb - 1) ? (y & 1) : -1;
+    }
+    const int h = blockIdx.x, qb = qbi * PF_AQ;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q16 = lane & 15, kq = lane >> 4;
     const int kvh = h / (a.nh / a.nkv);
     // this lane's query (the column it holds) and the wave's query range
@@ -1701,8 +1712,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     // keys of the workgroup: from the first query's window start to the last live query
     const int tl = (qb + PF_AQ < a.T ? qb + PF_AQ : a.T) - 1;
-    const int kend = a.pos0 + tl;
-    const int kstart = a.pos0 + qb + 1 - a.window > 0 ? a.pos0 + qb + 1 - a.window : 0;
+    int kend = a.pos0 + tl;
+    int kstart = a.pos0 + qb + 1 - a.window > 0 ? a.pos0 + qb + 1 - a.window : 0;
+    if (half >= 0) {
+        // the first ceil(nk / 2) key blocks, or the rest (empty when the range is one block: the
+        // half then leaves max -inf and sum 0)
+        const int nk = (kend - kstart) / PF_AK + 1, kmid = kstart + ((nk + 1) / 2) * PF_AK;
+        if (half == 0) kend = kmid - 1 < kend ? kmid - 1 : kend;
+        else kstart = kmid;
+    }
+    const int kclamp = a.pos0 + tl;  // a valid cache row for the clamped loads of an empty half
     const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
     float m = -INFINITY, l = 0.0f;
     // O^T tile d = 4 c + r (c = dt / 4, r = dt % 4) holds dims 64 c + 4 i + r, i = 0..15
@@ -1720,7 +1739,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
     if constexpr (PfAk<HD>::pre) {
 #pragma unroll
         for (int i = 0; i < NPC; i++) {
-            const int j = jrow + i * (256 / (HD / 4)), key = kstart + j < kend ? kstart + j : kend;
+            const int j = jrow + i * (256 / (HD / 4)), key = kstart + j < kend ? kstart + j : (kend < kstart ? kclamp : kend);
             const size_t off = (size_t)key * a.kvdim + (size_t)kvh * HD + d4;
             const float4 k4 = *(const float4*)(a.kc + off), v4 = *(const float4*)(a.vc + off);
             pk[4 * i] = k4.x; pk[4 * i + 1] = k4.y; pk[4 * i + 2] = k4.z; pk[4 * i + 3] = k4.w;
@@ -1827,7 +1846,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
                 }
             }
     }
-    if (qlive) {
+    if (qlive && half >= 0) {
+        // the half's unnormalised sums (the layout below), then max and sum of the lane's query
+        const size_t row = ((size_t)(h * nqb + qbi) * 2 + half) * PF_AQ + (tq - qb);
+        float* orow = a.part + row * HD + 16 * kq;
+#pragma unroll
+        for (int c = 0; c < HD / 64; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                *(float4*)(orow + 64 * c + 4 * e) = make_float4(o[4 * c][e], o[4 * c + 1][e], o[4 * c + 2][e], o[4 * c + 3][e]);
+        if (kq == 0) {
+            float* ml = a.part + (size_t)a.nh * nqb * 2 * PF_AQ * HD + row * 2;
+            ml[0] = m;
+            ml[1] = l;
+        }
+    } else if (qlive) {
         // lane l holds dims 64 c + 16 (l >> 4) + 4 e + r (tile 4 c + r, row 4 (l >> 4) + e) of its query
         const float inv = 1.0f / l;
         float* orow = a.out + (size_t)tq * a.nh * HD + (size_t)h * HD + 16 * kq;
@@ -1840,27 +1873,67 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
     }
 }
 
+// The two halves of the split query blocks (1 .. nqb - 1) of head blockIdx.x, query block
+// blockIdx.y + 1: out = (o1 e^(m1 - M) + o2 e^(m2 - M)) / (l1 e^(m1 - M) + l2 e^(m2 - M)), M = max(m1, m2)
+template <int HD>
+__global__ __launch_bounds__(256) void k_pf_attn_merge(const PfAttn a) {
+    const int nqb = (a.T + PF_AQ - 1) / PF_AQ, h = blockIdx.x, qbi = blockIdx.y + 1, qb = qbi * PF_AQ;
+    const size_t r0 = ((size_t)(h * nqb + qbi) * 2) * PF_AQ;
+    const float* ml = a.part + (size_t)a.nh * nqb * 2 * PF_AQ * HD;
+    for (int idx = threadIdx.x; idx < PF_AQ * HD / 4; idx += 256) {
+        const int ql = idx / (HD / 4), d4 = (idx % (HD / 4)) * 4, tq = qb + ql;
+        if (tq >= a.T) continue;
+        const size_t ra = r0 + ql, rb = r0 + PF_AQ + ql;
+        const float m1 = ml[2 * ra], l1 = ml[2 * ra + 1], m2 = ml[2 * rb], l2 = ml[2 * rb + 1];
+        const float M = fmaxf(m1, m2);
+        const float w1 = m1 == -INFINITY ? 0.0f : expf(m1 - M), w2 = m2 == -INFINITY ? 0.0f : expf(m2 - M);
+        const float inv = 1.0f / (l1 * w1 + l2 * w2);
+        const float4 oa = *(const float4*)(a.part + ra * HD + d4), ob = *(const float4*)(a.part + rb * HD + d4);
+        *(float4*)(a.out + (size_t)tq * a.nh * HD + (size_t)h * HD + d4) =
+            make_float4((oa.x * w1 + ob.x * w2) * inv, (oa.y * w1 + ob.y * w2) * inv, (oa.z * w1 + ob.z * w2) * inv,
+                        (oa.w * w1 + ob.w * w2) * inv);
+    }
+}
+
+template <int HD>
+static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
+    hipError_t e = pf_lds_attr((const void*)k_pf_attn<HD>, pf_attn_lds<HD>());
+    if (e != hipSuccess) return e;
+    const int nqb = (a.T + PF_AQ - 1) / PF_AQ;
+    // split the key ranges of query blocks 1 .. nqb - 1 in two when every half and block 0 then run
+    // at once on the resident slots and the scratch holds the halves (Llama-3-8B at 511 tokens:
+    // 32 heads x 15 rows on 512 slots; the longest workgroup had 8 key blocks against 4.5 on average)
+    a.split = 0;
+    if (a.part != nullptr && nqb >= 2) {
+        static std::atomic<int> resident{-1};  // resident workgroups per CU (asked once)
+        int per_cu = resident.load(std::memory_order_relaxed);
+        if (per_cu < 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_pf_attn<HD>, 256, pf_attn_lds<HD>()) !=
+                hipSuccess)
+                per_cu = 0;
+            resident.store(per_cu, std::memory_order_relaxed);
+        }
+        const int64_t items = (int64_t)a.nh * (2 * (nqb - 1) + 1);
+        const size_t need = (size_t)a.nh * nqb * 2 * PF_AQ * (HD + 2);
+        if (per_cu > 0 && items <= (int64_t)per_cu * (a.n_cu > 0 ? a.n_cu : 256) && need <= a.part_cap) a.split = 1;
+    }
+    dim3 grid((unsigned)a.nh, (unsigned)(a.split ? 2 * (nqb - 1) + 1 : nqb));
+    k_pf_attn<HD><<<grid, 256, pf_attn_lds<HD>(), st>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess || !a.split) return e;
+    k_pf_attn_merge<HD><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1)), 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
 hipError_t launch_pf_attn(const PfAttn& a, hipStream_t st) {
     if (a.T <= 0) return hipSuccess;
     if (a.nkv <= 0 || a.nh % a.nkv != 0 || a.kvdim != a.nkv * a.hd) return hipErrorInvalidValue;
-    dim3 grid((unsigned)a.nh, (unsigned)((a.T + PF_AQ - 1) / PF_AQ));
-    hipError_t e;
     switch (a.hd) {
-        case 64:
-            if ((e = pf_lds_attr((const void*)k_pf_attn<64>, pf_attn_lds<64>())) != hipSuccess) return e;
-            k_pf_attn<64><<<grid, 256, pf_attn_lds<64>(), st>>>(a);
-            break;
-        case 128:
-            if ((e = pf_lds_attr((const void*)k_pf_attn<128>, pf_attn_lds<128>())) != hipSuccess) return e;
-            k_pf_attn<128><<<grid, 256, pf_attn_lds<128>(), st>>>(a);
-            break;
-        case 256:
-            if ((e = pf_lds_attr((const void*)k_pf_attn<256>, pf_attn_lds<256>())) != hipSuccess) return e;
-            k_pf_attn<256><<<grid, 256, pf_attn_lds<256>(), st>>>(a);
-            break;
+        case 64: return pf_attn_run<64>(a, st);
+        case 128: return pf_attn_run<128>(a, st);
+        case 256: return pf_attn_run<256>(a, st);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace fllm

@@ -91,6 +91,12 @@ struct PfAttn {
     int nh, nkv, hd, kvdim;
     int window;      // attend to the last `window` positions (INT32_MAX = all)
     float scale, softcap;
+    // optional scratch of part_cap floats for the halves of split key ranges (launch_pf_attn splits
+    // the longer query blocks when all halves then fit the resident workgroup slots of n_cu CUs)
+    float* part;
+    size_t part_cap;
+    int n_cu;
+    int split;  // set by launch_pf_attn
 };
 hipError_t launch_pf_attn(const PfAttn& a, hipStream_t st);
 
