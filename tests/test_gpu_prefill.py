@@ -79,6 +79,39 @@ def test_batched_prefill_matches_oracle_and_stepwise(ctx, name):
         m.close()
 
 
+@pytest.mark.parametrize("name", ["test-llama", "test-qwen2", "test-gemma2-hd256", "test-mistral"])
+def test_batched_prefill_split_attention(ctx, name):
+    """A prompt of several query blocks with a partial last one (200 tokens: blocks of 64, 64, 64,
+    8) into a 256-position cache: the prefill attention runs every block but the first as two
+    halves of its key range plus a merge when all halves fit the resident workgroups, as here.
+    Head dim 64 (Llama; Qwen2 with its q/k/v bias; Mistral with its window) and 256 (Gemma-2:
+    softcaps, window on the even layer). Logits and every K/V row against the oracle, then greedy
+    decode."""
+    cfg, desc, tensors = synthetic(name)
+    cap, n = 256, 200
+    m = device_model(ctx, desc, tensors)
+    kv = F.HipKvCache(m, cap)
+    fwd = F.HipForwardPass(m)
+    orc = O.OracleModel(desc, tensors, cap)
+    prompt = F.synth_tokens(cfg["seed"], 7, desc.vocab, n)
+    try:
+        fwd.prefill(prompt, 0, kv)
+        _oracle_prefill(orc, prompt)
+        want = orc.logits()
+        err = O.normwise_rel_err(fwd.logits, want)
+        print(f"{name}: {n} tokens, logits normwise rel err {err:.2e}")
+        assert err <= TOL
+        for l in range(desc.n_layers):
+            assert O.normwise_rel_err(kv.get_keys(l), orc.kv(l, 0)) <= TOL, l
+            assert O.normwise_rel_err(kv.get_values(l), orc.kv(l, 1)) <= TOL, l
+        toks = fwd.decode_greedy(int(prompt[-1]), n, 4, kv)
+        assert list(toks) == _oracle_continue(orc, prompt[-1], n, 4)
+    finally:
+        orc.close()
+        kv.close()
+        m.close()
+
+
 def test_prefill_chunk_contract(ctx):
     """fllm_seq_set_prefill_chunk: tokens < 1 is out of range; a chunk of 24 tokens takes a 61-token
     prompt in passes of 24, 24 and 13 (logits, K/V and the greedy token against the oracle); after
