@@ -1667,16 +1667,20 @@ static hipError_t prefill_alloc(fllm_seq* s, int n) {
 struct PfSrc {
     enum { NORM = 1, ACT = 2 };
     int kind;
-    const float* x;
+    float* x;
     const float* w;
     float eps;
-    int fn;  // NORM: 1 GemmaRmsNorm; ACT: 1 GELU, 0 SiLU
+    int fn;       // NORM: 1 GemmaRmsNorm; ACT: 1 GELU, 0 SiLU
+    int nsp = 0;  // NORM: K-split slices of x left in pf_part by the previous GEMM, added into x first
 };
 
 // y_i (+)= X W_i^T over the chunk's rows for the matrices w[0..n) (one launch when their layouts
-// agree); X = pf_xn (row stride pf_ldx), the given rows, or the rows src computes
+// agree); X = pf_xn (row stride pf_ldx), the given rows, or the rows src computes. With pending and
+// one launch for all the matrices, that launch leaves its K-split slices (laid out from y[0]) in
+// pf_part for the next kernel (launch_pf_gemm's pending); with several launches, *pending is 0.
 static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w, float* const* y, int n, int ldy, int T,
-                          bool add, const float* x = nullptr, int ldx = 0, const PfSrc* src = nullptr) {
+                          bool add, const float* x = nullptr, int ldx = 0, const PfSrc* src = nullptr,
+                          int* pending = nullptr) {
     PfGemm g{};
     g.x = x ? x : s->pf_xn;
     g.ldx = x ? ldx : s->pf_ldx;
@@ -1692,8 +1696,9 @@ static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w,
     if (src && src->kind == PfSrc::NORM) {
         g.x = src->x;
         g.ldx = g.K;
-        STEP("pf_norm_split", 8.0 * T * g.K + 4.0 * T * g.ldh,
-             launch_pf_split_norm(src->x, T, g.K, src->w, src->eps, src->fn, s->pf_xh, g.ldh, s->pf_xs, s->st));
+        STEP("pf_norm_split", (8.0 + 4.0 * src->nsp + (src->nsp > 0 ? 4.0 : 0.0)) * T * g.K + 4.0 * T * g.ldh,
+             launch_pf_split_norm(src->x, T, g.K, src->w, src->eps, src->fn, s->pf_xh, g.ldh, s->pf_xs, s->st,
+                                  s->pf_part, src->nsp));
     } else if (src && src->kind == PfSrc::ACT) {
         g.x = src->x;
         g.ldx = 2 * g.K;
@@ -1713,13 +1718,15 @@ static hipError_t pf_gemm(fllm_seq* s, const char* name, const Tensor* const* w,
             STEP(name, bytes, launch_pf_gemm(g, s->m->ctx->n_cu, s->st));
             g.nseg = 0;
             bytes = 0.0;
+            if (pending) *pending = 0;
+            pending = nullptr;
         }
         PfSeg& sg = g.seg[g.nseg++];
         sg.w = w[i]->ptr; sg.type = w[i]->type; sg.layout = w[i]->layout; sg.N = (int)w[i]->rows;
         sg.y = y[i]; sg.ldy = ldy; sg.wexp = w[i]->wexp;
         bytes += (double)w[i]->bytes + 8.0 * T * (double)(w[i]->rows + w[i]->cols);
     }
-    STEP(name, bytes, launch_pf_gemm(g, s->m->ctx->n_cu, s->st));
+    STEP(name, bytes, launch_pf_gemm(g, s->m->ctx->n_cu, s->st, pending));
     return hipSuccess;
 }
 
@@ -1735,6 +1742,9 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
     const int ldq = qdim + 2 * kvdim;
     const size_t layer_kv = (size_t)s->max_seq * kvdim;
     hipError_t e;
+    // K-split slices of the residual stream pf_x left in pf_part by the o or down GEMM, added by the
+    // next norm split (Llama-form layers whose norms go into the split)
+    int pend_x = 0;
     STEP("pf_embed", 4.0 * T * H, launch_pf_embed(s->pf_tok, T, m->tok_embd.ptr, m->tok_embd.type, H, s->pf_x, s->st));
     for (int l = 0; l < d.n_layers; l++) {
         const Layer& L = m->layers[(size_t)l];
@@ -1742,17 +1752,21 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         float* vc = s->vc + (size_t)l * layer_kv;
         // the norms and the activation go into the split of the GEMM input (rows up to 20480)
         const bool fuse_h = pf_split_src_ok(H), fuse_f = pf_split_src_ok(F);
+        const bool defer_x = fuse_h && !gemma;
         if (!fuse_h) STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.attn_norm, eps, nk, s->pf_xn, ldx, s->st));
+        int pend_qkv = 0;
         {
             const Tensor* w[3] = {&L.q, &L.k, &L.v};
             float* y[3] = {s->pf_qkv, s->pf_qkv + qdim, s->pf_qkv + qdim + kvdim};
-            const PfSrc src{PfSrc::NORM, s->pf_x, L.attn_norm, eps, nk};
-            if ((e = pf_gemm(s, "pf_qkv", w, y, 3, ldq, T, false, nullptr, 0, fuse_h ? &src : nullptr)) != hipSuccess)
+            const PfSrc src{PfSrc::NORM, s->pf_x, L.attn_norm, eps, nk, pend_x};
+            pend_x = 0;
+            if ((e = pf_gemm(s, "pf_qkv", w, y, 3, ldq, T, false, nullptr, 0, fuse_h ? &src : nullptr, &pend_qkv)) !=
+                hipSuccess)
                 return e;
         }
-        STEP("pf_qkv_post", 8.0 * T * ldq,
+        STEP("pf_qkv_post", (8.0 + 4.0 * pend_qkv) * T * ldq,
              launch_pf_qkv_post(s->pf_qkv, ldq, T, pos0, L.bq, L.bk, L.bv, s->rope, d.n_heads, d.n_kv_heads, d.head_dim,
-                                kc, vc, s->st));
+                                kc, vc, s->st, s->pf_part, pend_qkv));
         PfAttn at{};
         at.q = s->pf_qkv; at.ldq = ldq; at.kc = kc; at.vc = vc; at.out = s->pf_att;
         at.T = T; at.pos0 = pos0; at.nh = d.n_heads; at.nkv = d.n_kv_heads; at.hd = d.head_dim; at.kvdim = kvdim;
@@ -1762,14 +1776,17 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         {
             const Tensor* w[1] = {&L.o};
             float* y[1] = {gemma ? s->pf_tmp : s->pf_x};
-            if ((e = pf_gemm(s, "pf_o", w, y, 1, H, T, !gemma, s->pf_att, qdim)) != hipSuccess) return e;
+            if ((e = pf_gemm(s, "pf_o", w, y, 1, H, T, !gemma, s->pf_att, qdim, nullptr, defer_x ? &pend_x : nullptr)) !=
+                hipSuccess)
+                return e;
             if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_attn, s->pf_x, s->st));
         }
         if (!fuse_h) STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.ffn_norm, eps, nk, s->pf_xn, ldx, s->st));
         {
             const Tensor* w[2] = {&L.gate, &L.up};
             float* y[2] = {s->pf_gu, s->pf_gu + F};
-            const PfSrc src{PfSrc::NORM, s->pf_x, L.ffn_norm, eps, nk};
+            const PfSrc src{PfSrc::NORM, s->pf_x, L.ffn_norm, eps, nk, pend_x};
+            pend_x = 0;
             if ((e = pf_gemm(s, "pf_gate_up", w, y, 2, 2 * F, T, false, nullptr, 0, fuse_h ? &src : nullptr)) !=
                 hipSuccess)
                 return e;
@@ -1779,7 +1796,9 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
             const Tensor* w[1] = {&L.down};
             float* y[1] = {gemma ? s->pf_tmp : s->pf_x};
             const PfSrc src{PfSrc::ACT, s->pf_gu, nullptr, 0.0f, gemma ? 1 : 0};
-            if ((e = pf_gemm(s, "pf_down", w, y, 1, H, T, !gemma, nullptr, 0, fuse_f ? &src : nullptr)) != hipSuccess)
+            // the last layer's sum is complete when the chunk ends
+            if ((e = pf_gemm(s, "pf_down", w, y, 1, H, T, !gemma, nullptr, 0, fuse_f ? &src : nullptr,
+                             defer_x && l + 1 < d.n_layers ? &pend_x : nullptr)) != hipSuccess)
                 return e;
             if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_ffn, s->pf_x, s->st));
         }

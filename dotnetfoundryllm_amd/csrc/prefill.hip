@@ -1204,14 +1204,17 @@ hipError_t launch_pf_split(const float* x, int ldx, int T, int K, _Float16* xh, 
 // t of gu (gate in columns [0, K), up in [K, 2 K) of a row of stride ldx), k_pf_act's. The row stays
 // in registers (NPT float4 per thread: element 4 i .. 4 i + 3 with i = thread + 256 j), so the
 // normalized or gated row is never written; the scale, planes and group sums are k_pf_split's.
+// SRC 1 with nsp > 0: the row is x[t] + part[0][t] + ... + part[nsp - 1][t] (slices of pn floats,
+// row stride ldx), k_pf_split_add's sum, written back to x before the norm.
 template <int NPT, int SRC>
-__global__ __launch_bounds__(256) void k_pf_split_src(const float* __restrict__ x, int ldx, int K,
+__global__ __launch_bounds__(256) void k_pf_split_src(float* __restrict__ x, int ldx, int K,
                                                       const float* __restrict__ w, float eps, int kind,
                                                       _Float16* __restrict__ xh, int ldh, size_t plane,
-                                                      float* __restrict__ xs, int T) {
+                                                      float* __restrict__ xs, int T, const float* __restrict__ part,
+                                                      int nsp, size_t pn) {
     __shared__ float red[4];
     const int t = blockIdx.x;
-    const float* xr = x + (size_t)t * ldx;
+    float* xr = x + (size_t)t * ldx;
     const int K4 = K / 4;
     float4 v[NPT];
     float ss = 0.0f;
@@ -1226,6 +1229,16 @@ __global__ __launch_bounds__(256) void k_pf_split_src(const float* __restrict__ 
                                 act_fn(g.w, kind) * u.w);
             } else {
                 q = ((const float4*)xr)[i];
+                if (nsp > 0) {
+                    for (int z = 0; z < nsp; z++) {
+                        const float4 p = ((const float4*)(part + (size_t)z * pn + (size_t)t * ldx))[i];
+                        q.x += p.x;
+                        q.y += p.y;
+                        q.z += p.z;
+                        q.w += p.w;
+                    }
+                    ((float4*)xr)[i] = q;
+                }
                 ss = fmaf(q.x, q.x, ss);
                 ss = fmaf(q.y, q.y, ss);
                 ss = fmaf(q.z, q.z, ss);
@@ -1299,32 +1312,35 @@ __global__ __launch_bounds__(256) void k_pf_split_src(const float* __restrict__ 
 }
 
 template <int SRC>
-static hipError_t pf_split_src(const float* x, int ldx, int T, int K, const float* w, float eps, int kind,
-                               _Float16* xh, int ldh, float* xs, hipStream_t st) {
+static hipError_t pf_split_src(float* x, int ldx, int T, int K, const float* w, float eps, int kind,
+                               _Float16* xh, int ldh, float* xs, hipStream_t st, const float* part = nullptr,
+                               int nsp = 0) {
     if (T <= 0) return hipSuccess;
     if (K % 32 != 0 || ldx % 4 != 0 || ldh % 8 != 0 || ldh < K) return hipErrorInvalidValue;
+    if (nsp < 0 || (nsp > 0 && (SRC != 1 || part == nullptr || (uintptr_t)part % 16 != 0))) return hipErrorInvalidValue;
     const int n4 = (K / 4 + 255) / 256;
-    const size_t plane = (size_t)T * ldh;
-    if (n4 <= 1) k_pf_split_src<1, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
-    else if (n4 <= 2) k_pf_split_src<2, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
-    else if (n4 <= 4) k_pf_split_src<4, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
-    else if (n4 <= 8) k_pf_split_src<8, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
-    else if (n4 <= 16) k_pf_split_src<16, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
-    else if (n4 <= 20) k_pf_split_src<20, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T);
+    const size_t plane = (size_t)T * ldh, pn = (size_t)T * ldx;
+    if (n4 <= 1) k_pf_split_src<1, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T, part, nsp, pn);
+    else if (n4 <= 2) k_pf_split_src<2, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T, part, nsp, pn);
+    else if (n4 <= 4) k_pf_split_src<4, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T, part, nsp, pn);
+    else if (n4 <= 8) k_pf_split_src<8, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T, part, nsp, pn);
+    else if (n4 <= 16) k_pf_split_src<16, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T, part, nsp, pn);
+    else if (n4 <= 20) k_pf_split_src<20, SRC><<<T, 256, 0, st>>>(x, ldx, K, w, eps, kind, xh, ldh, plane, xs, T, part, nsp, pn);
     else return hipErrorNotSupported;
     return hipGetLastError();
 }
 
 bool pf_split_src_ok(int K) { return K % 32 == 0 && (K / 4 + 255) / 256 <= 20; }
 
-hipError_t launch_pf_split_norm(const float* x, int T, int K, const float* w, float eps, int kind, _Float16* xh,
-                                int ldh, float* xs, hipStream_t st) {
-    return pf_split_src<1>(x, K, T, K, w, eps, kind, xh, ldh, xs, st);
+hipError_t launch_pf_split_norm(float* x, int T, int K, const float* w, float eps, int kind, _Float16* xh,
+                                int ldh, float* xs, hipStream_t st, const float* part, int nsp) {
+    return pf_split_src<1>(x, K, T, K, w, eps, kind, xh, ldh, xs, st, part, nsp);
 }
 
 hipError_t launch_pf_split_act(const float* gu, int T, int ffn, int act, _Float16* xh, int ldh, float* xs,
                                hipStream_t st) {
-    return pf_split_src<2>(gu, 2 * ffn, T, ffn, nullptr, 0.0f, act, xh, ldh, xs, st);
+    // the gated form only reads gu
+    return pf_split_src<2>(const_cast<float*>(gu), 2 * ffn, T, ffn, nullptr, 0.0f, act, xh, ldh, xs, st);
 }
 
 // largest |w| of a matrix (exact dequantization of every element), as float bits (non-negative floats
@@ -1368,7 +1384,21 @@ typedef void (*PfGemmKernel)(const PfGemm);
 // y[i] += part[0][i] + part[1][i] + ... (in that order) over n = T * ldy values
 __global__ __launch_bounds__(256) void k_pf_split_add(float* __restrict__ y, const float* __restrict__ part, int nsp,
                                                       int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    // four floats per thread and step where n and the pointers allow (the parts are added in order
+    // either way)
+    const int64_t n4 = n % 4 == 0 && ((uintptr_t)y | (uintptr_t)part) % 16 == 0 ? n / 4 : 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+        float4 v = ((const float4*)y)[i];
+        for (int z = 0; z < nsp; z++) {
+            const float4 w = ((const float4*)(part + (int64_t)z * n))[i];
+            v.x += w.x;
+            v.y += w.y;
+            v.z += w.z;
+            v.w += w.w;
+        }
+        ((float4*)y)[i] = v;
+    }
+    for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
         float v = y[i];
         for (int z = 0; z < nsp; z++) v += part[(int64_t)z * n + i];
         y[i] = v;
@@ -1408,7 +1438,8 @@ static int pf_resident(PfGemmKernel k, size_t lds) {
     return per_cu;
 }
 
-hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
+hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st, int* pending) {
+    if (pending) *pending = 0;
     if (a.T <= 0 || a.nseg <= 0) return hipSuccess;
     if (a.nseg > 3 || a.K <= 0 || a.K % 32 != 0 || a.ldx < a.K || a.ldx % 4 != 0) return hipErrorInvalidValue;
     const bool tiles = a.seg[0].layout == LAYOUT_TILES;
@@ -1514,10 +1545,18 @@ hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st) {
     k<<<grid, 256, lds, st>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess || nsplit == 1) return e;
-    const int64_t n = (int64_t)a.T * a.seg[0].ldy;
+    if (pending) {
+        *pending = nsplit - 1;
+        return hipSuccess;
+    }
+    return launch_pf_split_add(a.seg[0].y, a.part, nsplit - 1, (int64_t)a.T * a.seg[0].ldy, st);
+}
+
+hipError_t launch_pf_split_add(float* y, const float* part, int nsp, int64_t n, hipStream_t st) {
+    if (nsp <= 0 || n <= 0) return hipSuccess;
     int blocks = (int)((n + 255) / 256);
     if (blocks > 2048) blocks = 2048;
-    k_pf_split_add<<<blocks, 256, 0, st>>>(a.seg[0].y, a.part, nsplit - 1, n);
+    k_pf_split_add<<<blocks, 256, 0, st>>>(y, part, nsp, n);
     return hipGetLastError();
 }
 
@@ -1576,21 +1615,29 @@ hipError_t launch_pf_act(const float* gu, int T, int ffn, int act, float* h, int
 
 // Qwen2 bias (Qwen2ForwardPass.cs:83-85), RoPE on interleaved pairs (TensorOperations.cs:250-260)
 // at position pos0 + t, KvCache.Append into slot pos0 + t (KvCache.cs:86-89)
+// (nsp pending K-split slices of part, pn floats apart, added to each value first: k_pf_split_add's sum)
 __global__ __launch_bounds__(256) void k_pf_qkv_post(float* __restrict__ qkv, int ldq, int pos0,
                                                      const float* __restrict__ bq, const float* __restrict__ bk,
                                                      const float* __restrict__ bv, const float2* __restrict__ rope,
                                                      int nh, int nkv, int hd, float* __restrict__ kc,
-                                                     float* __restrict__ vc) {
+                                                     float* __restrict__ vc, const float* __restrict__ part, int nsp,
+                                                     size_t pn) {
     const int t = blockIdx.x, pos = pos0 + t, half = hd >> 1, qdim = nh * hd, kvdim = nkv * hd;
     float* row = qkv + (size_t)t * ldq;
+    const float* prow = part + (size_t)t * ldq;
+    auto val = [&](int c) {
+        float v = row[c];
+        for (int z = 0; z < nsp; z++) v += prow[(size_t)z * pn + c];
+        return v;
+    };
     const float2* rp = rope + (size_t)pos * half;
     const int npairs = (nh + nkv) * half;
     for (int idx = threadIdx.x; idx < npairs; idx += 256) {
         const bool isq = idx < nh * half;
         const int li = isq ? idx : idx - nh * half;
         const int head = li / half, i = li % half, o = head * hd + 2 * i;
-        const float* src = row + (isq ? 0 : qdim);
-        float x0 = src[o], x1 = src[o + 1];
+        const int c = (isq ? 0 : qdim) + o;
+        float x0 = val(c), x1 = val(c + 1);
         const float* b = isq ? bq : bk;
         if (b) { x0 = x0 + b[o]; x1 = x1 + b[o + 1]; }
         const float2 cs = rp[i];
@@ -1605,16 +1652,19 @@ __global__ __launch_bounds__(256) void k_pf_qkv_post(float* __restrict__ qkv, in
         }
     }
     for (int i = threadIdx.x; i < kvdim; i += 256) {
-        float v = row[qdim + kvdim + i];
+        float v = val(qdim + kvdim + i);
         if (bv) v = v + bv[i];
         vc[(size_t)pos * kvdim + i] = v;
     }
 }
 
 hipError_t launch_pf_qkv_post(float* qkv, int ldq, int T, int pos0, const float* bq, const float* bk, const float* bv,
-                              const float2* rope, int nh, int nkv, int hd, float* kc, float* vc, hipStream_t st) {
+                              const float2* rope, int nh, int nkv, int hd, float* kc, float* vc, hipStream_t st,
+                              const float* part, int nsp) {
     if (T <= 0) return hipSuccess;
-    k_pf_qkv_post<<<T, 256, 0, st>>>(qkv, ldq, pos0, bq, bk, bv, rope, nh, nkv, hd, kc, vc);
+    if (nsp < 0 || (nsp > 0 && part == nullptr)) return hipErrorInvalidValue;
+    k_pf_qkv_post<<<T, 256, 0, st>>>(qkv, ldq, pos0, bq, bk, bv, rope, nh, nkv, hd, kc, vc, nsp > 0 ? part : qkv, nsp,
+                                     (size_t)T * ldq);
     return hipGetLastError();
 }
 

@@ -33,7 +33,7 @@ struct PfGemm {
     // workgroups may split K over grid.z (nsplit parts of kpart whole 256-element blocks, the last
     // one possibly shorter, set by launch_pf_gemm) when its segments fill one buffer's rows side by
     // side; part 0 writes y, part z > 0 its own [T][ldy] slice of part, and a reduction adds the
-    // slices into y in order
+    // slices into y in order (or the caller's next kernel does: see launch_pf_gemm's pending)
     float* part;
     size_t part_cap;
     int nsplit, kpart;
@@ -43,7 +43,12 @@ struct PfGemm {
     int ldh;
     const float* xs;
 };
-hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st);
+// With pending non-null, a K-split launch leaves its parts z > 0 in a.part and sets *pending to their
+// number (0 when unsplit) instead of adding them: the next kernel that reads y adds them first, in
+// order (launch_pf_split_norm, launch_pf_qkv_post), or launch_pf_split_add does.
+hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st, int* pending = nullptr);
+// y[i] += part[0][i] + ... + part[nsp - 1][i] (in that order), slices of n floats
+hipError_t launch_pf_split_add(float* y, const float* part, int nsp, int64_t n, hipStream_t st);
 // The fp16 operand of a GEMM input: each row t of X [T][K] (stride ldx) scaled by 2^e_t, so that its
 // largest magnitude lies in [2^14, 2^15), and written as hi = fp16(x 2^e_t) (plane 0) and
 // lo = fp16(x 2^e_t - hi) (plane 1, at xh + T * ldh), 22 significant bits together; xs[t] = 2^-e_t.
@@ -54,9 +59,10 @@ hipError_t launch_pf_split(const float* x, int ldx, int T, int K, _Float16* xh, 
 // launch_pf_split of a row computed on the way, never written: RmsNorm / GemmaRmsNorm (kind 1) of
 // every row of x [T][K] (launch_pf_norm's arithmetic), or act(gate) * up of every row of gu [T][2 ffn]
 // (launch_pf_act's). For K up to 20480 (pf_split_src_ok); larger rows: hipErrorNotSupported.
+// The norm form first adds nsp pending K-split slices of part ([T][K] each) into x, written back.
 bool pf_split_src_ok(int K);
-hipError_t launch_pf_split_norm(const float* x, int T, int K, const float* w, float eps, int kind, _Float16* xh,
-                                int ldh, float* xs, hipStream_t st);
+hipError_t launch_pf_split_norm(float* x, int T, int K, const float* w, float eps, int kind, _Float16* xh,
+                                int ldh, float* xs, hipStream_t st, const float* part = nullptr, int nsp = 0);
 hipError_t launch_pf_split_act(const float* gu, int T, int ffn, int act, _Float16* xh, int ldh, float* xs,
                                hipStream_t st);
 // *out = max(*out, bits of the largest |w| over the n elements of a weight matrix in GGUF row layout)
@@ -73,9 +79,11 @@ hipError_t launch_pf_norm(const float* x, int T, int n, const float* w, float ep
 // h = act(gate) * up per row of gu [T][2 ffn] (gate columns, then up columns), row stride ldx
 hipError_t launch_pf_act(const float* gu, int T, int ffn, int act, float* h, int ldx, hipStream_t st);
 // rows of qkv [T][ldq] = (q | k | v): bias, RoPE at position pos0 + t on q and k, q written back,
-// k and v stored in cache slot pos0 + t of this layer's K / V cache
+// k and v stored in cache slot pos0 + t of this layer's K / V cache; nsp pending K-split slices of
+// part ([T][ldq] each) are added to every value first, in order
 hipError_t launch_pf_qkv_post(float* qkv, int ldq, int T, int pos0, const float* bq, const float* bk, const float* bv,
-                              const float2* rope, int nh, int nkv, int hd, float* kc, float* vc, hipStream_t st);
+                              const float2* rope, int nh, int nkv, int hd, float* kc, float* vc, hipStream_t st,
+                              const float* part = nullptr, int nsp = 0);
 // x[t] += GemmaRmsNorm(tmp[t], w) for every row
 hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w, float* x, hipStream_t st);
 
