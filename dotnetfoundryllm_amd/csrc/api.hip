@@ -211,6 +211,9 @@ struct fllm_seq {
     size_t pf_part_cap = 0;
     _Float16* pf_xh = nullptr;  // fp16 hi / lo planes of the current GEMM input
     float* pf_xs = nullptr;     // their per-row scales
+    _Float16* pf_kvh = nullptr;  // head_dim 256: fp16 planes of a layer's cached K / V (every position)
+    int* pf_kvs = nullptr;
+    int pf_kvblk = 0;
     int* pf_tok = nullptr;
 };
 
@@ -1605,6 +1608,9 @@ static void prefill_release(fllm_seq* s) {
     s->pf_x = s->pf_xn = s->pf_qkv = s->pf_att = s->pf_gu = s->pf_tmp = s->pf_part = nullptr;
     s->pf_xh = nullptr;
     s->pf_xs = nullptr;
+    s->pf_kvh = nullptr;
+    s->pf_kvs = nullptr;
+    s->pf_kvblk = 0;
     s->pf_tok = nullptr;
     s->pf_cap = 0;
     s->pf_part_cap = 0;
@@ -1651,11 +1657,18 @@ static hipError_t prefill_alloc(fllm_seq* s, int n) {
     const size_t kmax = ((size_t)std::max(std::max(m.d.hidden, m.d.ffn), m.qdim) + 7) / 8 * 8;
     PF_ALLOC(s->pf_xh, 2 * C * kmax + 2 * C * (kmax / 32 + 1));  // value planes, then group-sum planes
     PF_ALLOC(s->pf_xs, C);
+    const size_t kvh = pf_kv_planes_halves(m.d.head_dim, m.d.n_kv_heads, s->max_seq);
+    const int kvblk = (s->max_seq + 31) / 32;
+    if (kvh > 0) {
+        PF_ALLOC(s->pf_kvh, kvh);
+        PF_ALLOC(s->pf_kvs, 2 * (size_t)m.d.n_kv_heads * kvblk);
+    }
 #undef PF_ALLOC
     if (e == hipSuccess) {
         s->pf_cap = cap;
         s->pf_ldx = (int)ldx;
         s->pf_part_cap = part_cap;
+        s->pf_kvblk = kvh > 0 ? kvblk : 0;
     } else {
         prefill_release(s);
     }
@@ -1772,6 +1785,7 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         at.T = T; at.pos0 = pos0; at.nh = d.n_heads; at.nkv = d.n_kv_heads; at.hd = d.head_dim; at.kvdim = kvdim;
         at.window = layer_window(d, l); at.scale = d.attn_scale; at.softcap = gemma ? d.attn_softcap : 0.0f;
         at.part = s->pf_part; at.part_cap = s->pf_part_cap; at.n_cu = s->m->ctx->n_cu;
+        at.kvh = s->pf_kvh; at.kvs = s->pf_kvs; at.nblk = s->pf_kvblk;
         STEP("pf_attention", 8.0 * (double)kvdim * (pos0 + T) + 8.0 * T * qdim, launch_pf_attn(at, s->st));
         {
             const Tensor* w[1] = {&L.o};

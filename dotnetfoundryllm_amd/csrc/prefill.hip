@@ -1945,10 +1945,315 @@ __global__ __launch_bounds__(256) void k_pf_attn_merge(const PfAttn a) {
     }
 }
 
+// ---- head_dim 256: attention on the fp16 matrix cores ---------------------------------------------
+// The f32 products above bound the head_dim 256 kernel (v_mfma_f32_16x16x4f32 has 1/16 of the fp16
+// rate). Here a pass first splits the layer's cached K and V rows into fp16 hi / lo planes, per KV
+// head and block of PF_HK positions, each block scaled by its own power of two (its largest
+// magnitude into [2^14, 2^15), as the GEMM inputs: 22 significant bits with the lo plane), and
+// k_pf_attn_h forms S^T = K Q^T and O^T += V^T P^T with three v_mfma_f32_16x16x32_f16 products per
+// tile (hi hi, lo hi, hi lo; the dropped lo lo term is below 2^-22 of a product). Q is split per
+// query row in the kernel and P as p 2^14. Every sum is f32; exp, max, softcap and masks as above.
+// A block's planes are the LDS image the kernel stages, so staging is one contiguous copy:
+//   K hi [PF_HK keys][HD], K lo, V^T hi [HD][PF_HK], V^T lo, rows of 16-byte chunks (8 halves);
+//   K row r keeps chunk c at c ^ 2 (r & 15) and V^T row d keeps chunk c at c ^ 2 ((d >> 3) & 1), so
+//   the operand reads of a half-wave (16 rows x two chunks) cover gfx950's 128 banks once;
+//   V^T row d lists keys in MFMA k order: position 8 g + 4 t + e holds key 16 t + 4 g + e, the order
+//   in which lane (g = l >> 4) holds P^T in its score registers (keys 16 t + 4 g + e, t = 0, 1).
+// kvs holds each block's two exponents (K, V).
+constexpr int PF_HK = 32;
+template <int HD> constexpr int pf_kvh_block() { return 4 * PF_HK * HD; }  // halves per (head, block)
+
+// exponent e with m 2^e in [2^14, 2^15) (0 for m = 0 or non-finite), clamped to [-60, 60]
+__device__ __forceinline__ int pf_exp15(float m) {
+    int e = 0;
+    if (m > 0.0f && m <= 3.0e38f) {
+        int ex;
+        (void)frexpf(m, &ex);
+        e = 15 - ex;
+        e = e < -60 ? -60 : (e > 60 ? 60 : e);
+    }
+    return e;
+}
+
+// grid (blocks of the keys [0, nkeys), KV heads), 256 threads: block b of head h into its planes
+// (keys from nkeys on as zeros)
+template <int HD>
+__global__ __launch_bounds__(256) void k_pf_kv_split(const float* __restrict__ kc, const float* __restrict__ vc,
+                                                     int kvdim, int nkeys, int nblk, _Float16* __restrict__ kvh,
+                                                     int* __restrict__ kvs) {
+    static_assert(HD == 256, "one thread per V^T row");
+    __shared__ float sv[PF_HK * HD];
+    __shared__ float red[8];
+    const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    constexpr int NF = PF_HK * HD / 4 / 256;  // float4 pieces of K per thread
+    float4 kr[NF];
+    float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NF; i++) {
+        const int f = tid + 256 * i, r = f / (HD / 4), c4 = f % (HD / 4), key = b * PF_HK + r;
+        float4 k4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v4 = k4;
+        if (key < nkeys) {
+            const size_t off = (size_t)key * kvdim + (size_t)h * HD + 4 * c4;
+            k4 = *(const float4*)(kc + off);
+            v4 = *(const float4*)(vc + off);
+        }
+        kr[i] = k4;
+        mk = fmaxf(mk, fmaxf(fmaxf(fabsf(k4.x), fabsf(k4.y)), fmaxf(fabsf(k4.z), fabsf(k4.w))));
+        mv = fmaxf(mv, fmaxf(fmaxf(fabsf(v4.x), fabsf(v4.y)), fmaxf(fabsf(v4.z), fabsf(v4.w))));
+        *(float4*)(sv + r * HD + 4 * c4) = v4;
+    }
+    mk = pf_wave_max(mk);
+    mv = pf_wave_max(mv);
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = mk;
+        red[4 + (tid >> 6)] = mv;
+    }
+    __syncthreads();  // the maxima and the V rows in sv
+    mk = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mv = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+    const int ek = pf_exp15(mk), ev = pf_exp15(mv);
+    const float fk = ldexpf(1.0f, ek), fv = ldexpf(1.0f, ev);
+    _Float16* blk = kvh + ((size_t)h * nblk + b) * pf_kvh_block<HD>();
+#pragma unroll
+    for (int i = 0; i < NF; i++) {
+        const int f = tid + 256 * i, r = f / (HD / 4), c4 = f % (HD / 4);
+        const int off = r * HD + (((c4 >> 1) ^ (2 * (r & 15))) << 3) + 4 * (c4 & 1);
+        const float c[4] = {kr[i].x * fk, kr[i].y * fk, kr[i].z * fk, kr[i].w * fk};
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            hi[u] = (_Float16)c[u];
+            lo[u] = (_Float16)(c[u] - (float)hi[u]);
+        }
+        *(uint2*)(blk + off) = *(const uint2*)hi;
+        *(uint2*)(blk + PF_HK * HD + off) = *(const uint2*)lo;
+    }
+    const int d = tid;
+    _Float16* vh = blk + 2 * PF_HK * HD + d * PF_HK;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        _Float16 hi[8], lo[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x = sv[(16 * t + 4 * g + e) * HD + d] * fv;
+                hi[4 * t + e] = (_Float16)x;
+                lo[4 * t + e] = (_Float16)(x - (float)hi[4 * t + e]);
+            }
+        const int gs = g ^ (2 * ((d >> 3) & 1));
+        *(uint4*)(vh + 8 * gs) = *(const uint4*)hi;
+        *(uint4*)(vh + HD * PF_HK + 8 * gs) = *(const uint4*)lo;
+    }
+    if (tid == 0) {
+        kvs[2 * ((size_t)h * nblk + b)] = ek;
+        kvs[2 * ((size_t)h * nblk + b) + 1] = ev;
+    }
+}
+
+// k_pf_attn's workgroups, query blocks and halves over the planes of k_pf_kv_split; key blocks of
+// PF_HK aligned positions. O^T accumulates in units of 2^-E, E = 14 + the V exponent of the last
+// block added (a block of another exponent rescales it by the power of two with the max correction).
+template <int HD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_attn_h(const PfAttn a) {
+    static_assert(HD == 256, "chunk swizzles for 32 chunks per K row");
+    constexpr int NS = HD / 32, NT = HD / 16, BLK = pf_kvh_block<HD>();
+    extern __shared__ uint4 ph_lds[];
+    const _Float16* skh = (const _Float16*)ph_lds;
+    const _Float16* skl = skh + PF_HK * HD;
+    const _Float16* svh = skl + PF_HK * HD;
+    const _Float16* svl = svh + HD * PF_HK;
+    const int nqb = (a.T + PF_AQ - 1) / PF_AQ;
+    int qbi = nqb - 1 - (int)blockIdx.y, half = -1;
+    if (a.split) {
+        const int y = (int)blockIdx.y;
+        qbi = y < 2 * (nqb - 1) ? nqb - 1 - (y >> 1) : 0;
+        half = y < 2 * (nqb - 1) ? (y & 1) : -1;
+    }
+    const int h = blockIdx.x, qb = qbi * PF_AQ;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q16 = lane & 15, kq = lane >> 4;
+    const int kvh = h / (a.nh / a.nkv);
+    const int tq = qb + 16 * wave + q16, w0 = qb + 16 * wave;
+    const bool qlive = tq < a.T, wlive = w0 < a.T;
+    const int pos = a.pos0 + (qlive ? tq : a.T - 1);
+    const int ws = pos + 1 - a.window > 0 ? pos + 1 - a.window : 0;
+    const int wpos_hi = a.pos0 + (w0 + 15 < a.T ? w0 + 15 : a.T - 1);
+    const int wws = a.pos0 + w0 + 1 - a.window > 0 ? a.pos0 + w0 + 1 - a.window : 0;
+    // Q^T operand of step s: dims 32 s + 8 (l >> 4) .. + 7 of the lane's query, scaled by 2^eq
+    pf_h8 qh[NS], ql[NS];
+    int eq;
+    {
+        float4 qv[2 * NS];
+        float qm = 0.0f;
+#pragma unroll
+        for (int st = 0; st < NS; st++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                qv[2 * st + u] = qlive ? *(const float4*)(a.q + (size_t)tq * a.ldq + (size_t)h * HD + 32 * st + 8 * kq + 4 * u)
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const float4 x = qv[2 * st + u];
+                qm = fmaxf(qm, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+            }
+        qm = fmaxf(qm, __shfl_xor(qm, 16));
+        qm = fmaxf(qm, __shfl_xor(qm, 32));
+        eq = pf_exp15(qm);
+        const float fq = ldexpf(1.0f, eq);
+#pragma unroll
+        for (int st = 0; st < NS; st++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float4 x = qv[2 * st + u];
+                const float c[4] = {x.x * fq, x.y * fq, x.z * fq, x.w * fq};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const _Float16 hi = (_Float16)c[e];
+                    qh[st][4 * u + e] = hi;
+                    ql[st][4 * u + e] = (_Float16)(c[e] - (float)hi);
+                }
+            }
+    }
+    const int tl = (qb + PF_AQ < a.T ? qb + PF_AQ : a.T) - 1;
+    const int kend = a.pos0 + tl;
+    const int kfirst = a.pos0 + qb + 1 - a.window > 0 ? a.pos0 + qb + 1 - a.window : 0;
+    int b0 = kfirst / PF_HK, b1 = kend / PF_HK;  // key blocks b0 .. b1
+    if (half >= 0) {
+        // the first ceil(n / 2) blocks, or the rest (none when the range is one block: the half then
+        // leaves max -inf and sum 0)
+        const int bm = b0 + (b1 - b0 + 2) / 2;
+        if (half == 0) b1 = bm - 1;
+        else b0 = bm;
+    }
+    const float inv_cap = a.softcap > 0.0f ? 1.0f / a.softcap : 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    int E = 0;
+    pf_f32x4 o[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) o[i] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint4* hsrc = (const uint4*)(a.kvh + (size_t)kvh * a.nblk * BLK);
+    const int* hexp = a.kvs + 2 * (size_t)kvh * a.nblk;
+    for (int b = b0; b <= b1; b++) {
+        const int kb = b * PF_HK;
+        __syncthreads();  // the previous block's planes have been read
+        {
+            const uint4* src = hsrc + (size_t)b * (BLK / 8);
+#pragma unroll
+            for (int r = 0; r < BLK / 8 / 256; r += 8) {
+                uint4 v[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = src[threadIdx.x + 256 * (r + i)];
+#pragma unroll
+                for (int i = 0; i < 8; i++) ph_lds[threadIdx.x + 256 * (r + i)] = v[i];
+            }
+        }
+        __syncthreads();
+        if (!wlive || kb > wpos_hi || kb + PF_HK - 1 < wws) continue;  // no key of the block for the wave
+        const int ek = hexp[2 * b], ev = hexp[2 * b + 1];
+        pf_f32x4 s[2];
+        s[0] = s[1] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < NS; st++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int off = (16 * t + q16) * HD + (((4 * st + kq) ^ (2 * q16)) << 3);
+                const pf_h8 kh = *(const pf_h8*)(skh + off), kl = *(const pf_h8*)(skl + off);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[st], s[t], 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[st], s[t], 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[st], s[t], 0, 0, 0);
+            }
+        // scores of keys kb + 16 t + 4 (l >> 4) + e for query l & 15
+        const float sc = ldexpf(a.scale, -(eq + ek));
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int key = kb + 16 * t + 4 * kq + e;
+                float x = s[t][e] * sc;
+                if (a.softcap > 0.0f) x = tanhf(x * inv_cap) * a.softcap;
+                x = (qlive && key >= ws && key <= pos) ? x : -INFINITY;
+                s[t][e] = x;
+                bmax = fmaxf(bmax, x);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const float m_new = fmaxf(m, bmax);
+        const float corr = m_new == -INFINITY ? 1.0f : expf(m - m_new);
+        float psum = 0.0f;
+        pf_h8 ph, pl;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float p = s[t][e] == -INFINITY ? 0.0f : expf(s[t][e] - m_new);
+                psum += p;
+                const float x = p * 16384.0f;
+                const _Float16 hi = (_Float16)x;
+                ph[4 * t + e] = hi;
+                pl[4 * t + e] = (_Float16)(x - (float)hi);
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l = l * corr + psum;
+        m = m_new;
+        // the sums so far into this block's units 2^-(14 + ev), with the max correction
+        const int Eb = 14 + ev;
+        const float f = ldexpf(corr, Eb - E);
+        E = Eb;
+#pragma unroll
+        for (int i = 0; i < NT; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[i][e] *= f;
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int off = (16 * j + q16) * PF_HK + ((kq ^ ((q16 >> 2) & 2)) << 3);
+            const pf_h8 vh = *(const pf_h8*)(svh + off), vl = *(const pf_h8*)(svl + off);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, o[j], 0, 0, 0);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, o[j], 0, 0, 0);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, o[j], 0, 0, 0);
+        }
+    }
+    // lane l holds dims 16 j + 4 (l >> 4) + e of its query, in units of 2^-E
+    const float un = ldexpf(1.0f, -E);
+    if (qlive && half >= 0) {
+        const size_t row = ((size_t)(h * nqb + qbi) * 2 + half) * PF_AQ + (tq - qb);
+        float* orow = a.part + row * HD + 4 * kq;
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+            *(float4*)(orow + 16 * j) = make_float4(o[j][0] * un, o[j][1] * un, o[j][2] * un, o[j][3] * un);
+        if (kq == 0) {
+            float* ml = a.part + (size_t)a.nh * nqb * 2 * PF_AQ * HD + row * 2;
+            ml[0] = m;
+            ml[1] = l;
+        }
+    } else if (qlive) {
+        const float inv = un / l;
+        float* orow = a.out + (size_t)tq * a.nh * HD + (size_t)h * HD + 4 * kq;
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+            *(float4*)(orow + 16 * j) = make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv);
+    }
+}
+
+size_t pf_kv_planes_halves(int hd, int nkv, int max_seq) {
+    if (hd != 256) return 0;
+    return (size_t)nkv * (size_t)((max_seq + PF_HK - 1) / PF_HK) * pf_kvh_block<256>();
+}
+
 template <int HD>
 static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
-    hipError_t e = pf_lds_attr((const void*)k_pf_attn<HD>, pf_attn_lds<HD>());
+    // head_dim 256: the planes of keys [0, pos0 + T), then the fp16 kernel
+    constexpr bool planes = HD == 256;
+    const void* kfn = planes ? (const void*)k_pf_attn_h<256> : (const void*)k_pf_attn<HD>;
+    const size_t lds = planes ? sizeof(_Float16) * (size_t)pf_kvh_block<256>() : pf_attn_lds<HD>();
+    hipError_t e = pf_lds_attr(kfn, lds);
     if (e != hipSuccess) return e;
+    if constexpr (planes) {
+        const int nkeys = a.pos0 + a.T, nb = (nkeys + PF_HK - 1) / PF_HK;
+        if (a.kvh == nullptr || a.kvs == nullptr || nb > a.nblk) return hipErrorInvalidValue;
+        k_pf_kv_split<256><<<dim3((unsigned)nb, (unsigned)a.nkv), 256, 0, st>>>(a.kc, a.vc, a.kvdim, nkeys, a.nblk, a.kvh,
+                                                                                 a.kvs);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     const int nqb = (a.T + PF_AQ - 1) / PF_AQ;
     // split the key ranges of query blocks 1 .. nqb - 1 in two when every half and block 0 then run
     // at once on the resident slots and the scratch holds the halves (Llama-3-8B at 511 tokens:
@@ -1958,8 +2263,7 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
         static std::atomic<int> resident{-1};  // resident workgroups per CU (asked once)
         int per_cu = resident.load(std::memory_order_relaxed);
         if (per_cu < 0) {
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_pf_attn<HD>, 256, pf_attn_lds<HD>()) !=
-                hipSuccess)
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 256, lds) != hipSuccess)
                 per_cu = 0;
             resident.store(per_cu, std::memory_order_relaxed);
         }
@@ -1968,7 +2272,8 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
         if (per_cu > 0 && items <= (int64_t)per_cu * (a.n_cu > 0 ? a.n_cu : 256) && need <= a.part_cap) a.split = 1;
     }
     dim3 grid((unsigned)a.nh, (unsigned)(a.split ? 2 * (nqb - 1) + 1 : nqb));
-    k_pf_attn<HD><<<grid, 256, pf_attn_lds<HD>(), st>>>(a);
+    if constexpr (planes) k_pf_attn_h<256><<<grid, 256, lds, st>>>(a);
+    else k_pf_attn<HD><<<grid, 256, lds, st>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess || !a.split) return e;
     k_pf_attn_merge<HD><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1)), 256, 0, st>>>(a);

@@ -105,7 +105,15 @@ struct PfAttn {
     size_t part_cap;
     int n_cu;
     int split;  // set by launch_pf_attn
+    // head_dim 256 (required there): the fp16 planes of the cached K / V, nblk blocks of 32
+    // positions per KV head (pf_kv_planes_halves halves), and their exponents (2 ints per block)
+    _Float16* kvh;
+    int* kvs;
+    int nblk;
 };
+// halves of the K / V planes launch_pf_attn needs for head_dim hd over nkv heads and max_seq positions
+// (0 when it needs none)
+size_t pf_kv_planes_halves(int hd, int nkv, int max_seq);
 hipError_t launch_pf_attn(const PfAttn& a, hipStream_t st);
 
 }  // namespace fllm
