@@ -1955,13 +1955,20 @@ __global__ __launch_bounds__(256) void k_pf_attn_merge(const PfAttn a) {
 // query row in the kernel and P as p 2^14. Every sum is f32; exp, max, softcap and masks as above.
 // A block's planes are the LDS image the kernel stages, so staging is one contiguous copy:
 //   K hi [PF_HK keys][HD], K lo, V^T hi [HD][PF_HK], V^T lo, rows of 16-byte chunks (8 halves);
-//   K row r keeps chunk c at c ^ 2 (r & 15) and V^T row d keeps chunk c at c ^ 2 ((d >> 3) & 1), so
-//   the operand reads of a half-wave (16 rows x two chunks) cover gfx950's 128 banks once;
+//   K row r keeps chunk c at c ^ 2 (r & 15) (head_dim 256: 32 chunks, a row spans the 128 banks) or
+//   c ^ 2 ((r >> 1) & 7) (head_dim 128: two rows span them), V^T row d keeps chunk c at
+//   c ^ 2 ((d >> 3) & 1), so the operand reads of a half-wave (16 rows x two chunks) cover gfx950's
+//   128 banks once;
 //   V^T row d lists keys in MFMA k order: position 8 g + 4 t + e holds key 16 t + 4 g + e, the order
 //   in which lane (g = l >> 4) holds P^T in its score registers (keys 16 t + 4 g + e, t = 0, 1).
 // kvs holds each block's two exponents (K, V).
 constexpr int PF_HK = 32;
 template <int HD> constexpr int pf_kvh_block() { return 4 * PF_HK * HD; }  // halves per (head, block)
+// chunk c of K row r in its plane
+template <int HD> __device__ __forceinline__ int pf_kchunk(int c, int r) {
+    static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
+    return HD == 256 ? c ^ (2 * (r & 15)) : c ^ (2 * ((r >> 1) & 7));
+}
 
 // exponent e with m 2^e in [2^14, 2^15) (0 for m = 0 or non-finite), clamped to [-60, 60]
 __device__ __forceinline__ int pf_exp15(float m) {
@@ -1981,7 +1988,7 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_pf_kv_split(const float* __restrict__ kc, const float* __restrict__ vc,
                                                      int kvdim, int nkeys, int nblk, _Float16* __restrict__ kvh,
                                                      int* __restrict__ kvs) {
-    static_assert(HD == 256, "one thread per V^T row");
+    static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
     __shared__ float sv[PF_HK * HD];
     __shared__ float red[8];
     const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
@@ -2017,7 +2024,7 @@ __global__ __launch_bounds__(256) void k_pf_kv_split(const float* __restrict__ k
 #pragma unroll
     for (int i = 0; i < NF; i++) {
         const int f = tid + 256 * i, r = f / (HD / 4), c4 = f % (HD / 4);
-        const int off = r * HD + (((c4 >> 1) ^ (2 * (r & 15))) << 3) + 4 * (c4 & 1);
+        const int off = r * HD + (pf_kchunk<HD>(c4 >> 1, r) << 3) + 4 * (c4 & 1);
         const float c[4] = {kr[i].x * fk, kr[i].y * fk, kr[i].z * fk, kr[i].w * fk};
         _Float16 hi[4], lo[4];
 #pragma unroll
@@ -2028,10 +2035,12 @@ __global__ __launch_bounds__(256) void k_pf_kv_split(const float* __restrict__ k
         *(uint2*)(blk + off) = *(const uint2*)hi;
         *(uint2*)(blk + PF_HK * HD + off) = *(const uint2*)lo;
     }
-    const int d = tid;
+    // V^T row d: 256 / HD threads per row, each its share of the four chunks
+    constexpr int TPR = 256 / HD, GPT = 4 / TPR;
+    const int d = tid % HD, g0 = (tid / HD) * GPT;
     _Float16* vh = blk + 2 * PF_HK * HD + d * PF_HK;
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
+    for (int g = g0; g < g0 + GPT; g++) {
         _Float16 hi[8], lo[8];
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -2055,8 +2064,8 @@ __global__ __launch_bounds__(256) void k_pf_kv_split(const float* __restrict__ k
 // PF_HK aligned positions. O^T accumulates in units of 2^-E, E = 14 + the V exponent of the last
 // block added (a block of another exponent rescales it by the power of two with the max correction).
 template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_pf_attn_h(const PfAttn a) {
-    static_assert(HD == 256, "chunk swizzles for 32 chunks per K row");
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 256 ? 2 : 3))) void k_pf_attn_h(const PfAttn a) {
+    static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
     constexpr int NS = HD / 32, NT = HD / 16, BLK = pf_kvh_block<HD>();
     extern __shared__ uint4 ph_lds[];
     const _Float16* skh = (const _Float16*)ph_lds;
@@ -2154,7 +2163,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         for (int st = 0; st < NS; st++)
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                const int off = (16 * t + q16) * HD + (((4 * st + kq) ^ (2 * q16)) << 3);
+                const int off = (16 * t + q16) * HD + (pf_kchunk<HD>(4 * st + kq, 16 * t + q16) << 3);
                 const pf_h8 kh = *(const pf_h8*)(skh + off), kl = *(const pf_h8*)(skl + off);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[st], s[t], 0, 0, 0);
                 s[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[st], s[t], 0, 0, 0);
@@ -2235,23 +2244,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 size_t pf_kv_planes_halves(int hd, int nkv, int max_seq) {
-    if (hd != 256) return 0;
-    return (size_t)nkv * (size_t)((max_seq + PF_HK - 1) / PF_HK) * pf_kvh_block<256>();
+    if (hd != 128 && hd != 256) return 0;
+    return (size_t)nkv * (size_t)((max_seq + PF_HK - 1) / PF_HK) * 4 * PF_HK * (size_t)hd;
 }
 
 template <int HD>
 static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
-    // head_dim 256: the planes of keys [0, pos0 + T), then the fp16 kernel
-    constexpr bool planes = HD == 256;
-    const void* kfn = planes ? (const void*)k_pf_attn_h<256> : (const void*)k_pf_attn<HD>;
-    const size_t lds = planes ? sizeof(_Float16) * (size_t)pf_kvh_block<256>() : pf_attn_lds<HD>();
+    // head_dim 256, and 128 over at least 1024 keys: the planes of keys [0, pos0 + T), then the fp16
+    // kernel (Qwen2-7B over 2047 tokens: attention 10.2 -> 7.0 ms; over 511 keys the split pass cost
+    // more than the products saved: Llama-3-8B's 1.49 -> 1.55 ms)
+    constexpr int PH = HD == 128 || HD == 256 ? HD : 256;  // the fp16 kernel's instance
+    const bool planes = HD == 256 || (HD == 128 && a.pos0 + a.T >= 1024);
+    const void* kfn = planes ? (const void*)k_pf_attn_h<PH> : (const void*)k_pf_attn<HD>;
+    const size_t lds = planes ? sizeof(_Float16) * (size_t)pf_kvh_block<PH>() : pf_attn_lds<HD>();
     hipError_t e = pf_lds_attr(kfn, lds);
     if (e != hipSuccess) return e;
-    if constexpr (planes) {
+    if (planes) {
         const int nkeys = a.pos0 + a.T, nb = (nkeys + PF_HK - 1) / PF_HK;
         if (a.kvh == nullptr || a.kvs == nullptr || nb > a.nblk) return hipErrorInvalidValue;
-        k_pf_kv_split<256><<<dim3((unsigned)nb, (unsigned)a.nkv), 256, 0, st>>>(a.kc, a.vc, a.kvdim, nkeys, a.nblk, a.kvh,
-                                                                                 a.kvs);
+        k_pf_kv_split<PH><<<dim3((unsigned)nb, (unsigned)a.nkv), 256, 0, st>>>(a.kc, a.vc, a.kvdim, nkeys, a.nblk, a.kvh,
+                                                                                a.kvs);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     const int nqb = (a.T + PF_AQ - 1) / PF_AQ;
@@ -2260,19 +2272,20 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
     // 32 heads x 15 rows on 512 slots; the longest workgroup had 8 key blocks against 4.5 on average)
     a.split = 0;
     if (a.part != nullptr && nqb >= 2) {
-        static std::atomic<int> resident{-1};  // resident workgroups per CU (asked once)
-        int per_cu = resident.load(std::memory_order_relaxed);
+        // resident workgroups per CU of the f32 and the fp16 kernel (each asked once)
+        static std::atomic<int> resident[2] = {{-1}, {-1}};
+        int per_cu = resident[planes].load(std::memory_order_relaxed);
         if (per_cu < 0) {
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 256, lds) != hipSuccess)
                 per_cu = 0;
-            resident.store(per_cu, std::memory_order_relaxed);
+            resident[planes].store(per_cu, std::memory_order_relaxed);
         }
         const int64_t items = (int64_t)a.nh * (2 * (nqb - 1) + 1);
         const size_t need = (size_t)a.nh * nqb * 2 * PF_AQ * (HD + 2);
         if (per_cu > 0 && items <= (int64_t)per_cu * (a.n_cu > 0 ? a.n_cu : 256) && need <= a.part_cap) a.split = 1;
     }
     dim3 grid((unsigned)a.nh, (unsigned)(a.split ? 2 * (nqb - 1) + 1 : nqb));
-    if constexpr (planes) k_pf_attn_h<256><<<grid, 256, lds, st>>>(a);
+    if (planes) k_pf_attn_h<PH><<<grid, 256, lds, st>>>(a);
     else k_pf_attn<HD><<<grid, 256, lds, st>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess || !a.split) return e;

@@ -79,16 +79,18 @@ def test_batched_prefill_matches_oracle_and_stepwise(ctx, name):
         m.close()
 
 
-@pytest.mark.parametrize("name", ["test-llama", "test-qwen2", "test-gemma2-hd256", "test-mistral"])
-def test_batched_prefill_split_attention(ctx, name):
+@pytest.mark.parametrize("name,cap,n", [("test-llama", 256, 200), ("test-qwen2", 256, 200), ("test-gemma2", 256, 200),
+                                        ("test-gemma2", 1280, 1100), ("test-gemma2-hd256", 256, 200),
+                                        ("test-mistral", 256, 200)])
+def test_batched_prefill_split_attention(ctx, name, cap, n):
     """A prompt of several query blocks with a partial last one (200 tokens: blocks of 64, 64, 64,
-    8) into a 256-position cache: the prefill attention runs every block but the first as two
-    halves of its key range plus a merge when all halves fit the resident workgroups, as here.
-    Head dim 64 (Llama; Qwen2 with its q/k/v bias; Mistral with its window) and 256 (Gemma-2:
-    softcaps, window on the even layer). Logits and every K/V row against the oracle, then greedy
-    decode."""
+    8; 1100: 17 blocks and 12) into a 256- (1280-) position cache: the prefill attention runs every
+    block but the first as two halves of its key range plus a merge when all halves fit the
+    resident workgroups, as here. Head dim 64 (Llama; Qwen2 with its q/k/v bias; Mistral with its
+    window), 128 (Gemma-2: softcaps, window on the even layer) on the f32 kernel, and 128 over 1100
+    keys and 256 on the fp16 kernel over the K / V planes. Logits and every K/V row against the
+    oracle, then greedy decode."""
     cfg, desc, tensors = synthetic(name)
-    cap, n = 256, 200
     m = device_model(ctx, desc, tensors)
     kv = F.HipKvCache(m, cap)
     fwd = F.HipForwardPass(m)
