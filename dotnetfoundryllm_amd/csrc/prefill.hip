@@ -1925,15 +1925,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
 
 // The two halves of the split query blocks (1 .. nqb - 1) of head blockIdx.x, query block
 // blockIdx.y + 1: out = (o1 e^(m1 - M) + o2 e^(m2 - M)) / (l1 e^(m1 - M) + l2 e^(m2 - M)), M = max(m1, m2)
-template <int HD>
+template <int HD, int QB>
 __global__ __launch_bounds__(256) void k_pf_attn_merge(const PfAttn a) {
-    const int nqb = (a.T + PF_AQ - 1) / PF_AQ, h = blockIdx.x, qbi = blockIdx.y + 1, qb = qbi * PF_AQ;
-    const size_t r0 = ((size_t)(h * nqb + qbi) * 2) * PF_AQ;
-    const float* ml = a.part + (size_t)a.nh * nqb * 2 * PF_AQ * HD;
-    for (int idx = threadIdx.x; idx < PF_AQ * HD / 4; idx += 256) {
+    const int nqb = (a.T + QB - 1) / QB, h = blockIdx.x, qbi = blockIdx.y + 1, qb = qbi * QB;
+    const size_t r0 = ((size_t)(h * nqb + qbi) * 2) * QB;
+    const float* ml = a.part + (size_t)a.nh * nqb * 2 * QB * HD;
+    for (int idx = threadIdx.x; idx < QB * HD / 4; idx += 256) {
         const int ql = idx / (HD / 4), d4 = (idx % (HD / 4)) * 4, tq = qb + ql;
         if (tq >= a.T) continue;
-        const size_t ra = r0 + ql, rb = r0 + PF_AQ + ql;
+        const size_t ra = r0 + ql, rb = r0 + QB + ql;
         const float m1 = ml[2 * ra], l1 = ml[2 * ra + 1], m2 = ml[2 * rb], l2 = ml[2 * rb + 1];
         const float M = fmaxf(m1, m2);
         const float w1 = m1 == -INFINITY ? 0.0f : expf(m1 - M), w2 = m2 == -INFINITY ? 0.0f : expf(m2 - M);
@@ -2060,26 +2060,33 @@ __global__ __launch_bounds__(256) void k_pf_kv_split(const float* __restrict__ k
     }
 }
 
-// k_pf_attn's workgroups, query blocks and halves over the planes of k_pf_kv_split; key blocks of
-// PF_HK aligned positions. O^T accumulates in units of 2^-E, E = 14 + the V exponent of the last
-// block added (a block of another exponent rescales it by the power of two with the max correction).
+// k_pf_attn's grid of (head, query block) rows, halves included, over the planes of k_pf_kv_split;
+// NW waves of 16 queries share each staged key block of PF_HK aligned positions. Head_dim 256: eight
+// waves (one workgroup per CU), the planes brought in by direct global -> LDS loads into two
+// buffers, the next block's while the current one multiplies (Gemma-2-9B over 6143 tokens:
+// attention 59.5-60.1 -> 55.3-56.5 ms against four waves staging through registers); head_dim 128:
+// four waves staging each block through registers into one buffer (the eight-wave form's shorter
+// attention, 7.0 -> 5.0 ms for Qwen2-7B over 2047 tokens, came with GEMMs 2 ms longer in the same
+// prefill, 25.0k -> 24.4k tok/s). O^T accumulates in units of 2^-E, E = 14 + the V exponent of the
+// last block added (a block of another exponent rescales it by the power of two with the max
+// correction).
+template <int HD> struct PfHq {
+    static constexpr int nw = HD == 256 ? 8 : 4, q = 16 * nw, threads = 64 * nw, bufs = HD == 256 ? 2 : 1;
+};
 template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 256 ? 2 : 3))) void k_pf_attn_h(const PfAttn a) {
+__global__ __launch_bounds__(PfHq<HD>::threads) __attribute__((amdgpu_waves_per_eu(HD == 256 ? 2 : 3))) void k_pf_attn_h(const PfAttn a) {
     static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
     constexpr int NS = HD / 32, NT = HD / 16, BLK = pf_kvh_block<HD>();
-    extern __shared__ uint4 ph_lds[];
-    const _Float16* skh = (const _Float16*)ph_lds;
-    const _Float16* skl = skh + PF_HK * HD;
-    const _Float16* svh = skl + PF_HK * HD;
-    const _Float16* svl = svh + HD * PF_HK;
-    const int nqb = (a.T + PF_AQ - 1) / PF_AQ;
+    constexpr int QB = PfHq<HD>::q, NTH = PfHq<HD>::threads, NPU = BLK / 8 / NTH;
+    extern __shared__ uint4 ph_lds[];  // PfHq<HD>::bufs buffers of BLK halves
+    const int nqb = (a.T + QB - 1) / QB;
     int qbi = nqb - 1 - (int)blockIdx.y, half = -1;
     if (a.split) {
         const int y = (int)blockIdx.y;
         qbi = y < 2 * (nqb - 1) ? nqb - 1 - (y >> 1) : 0;
         half = y < 2 * (nqb - 1) ? (y & 1) : -1;
     }
-    const int h = blockIdx.x, qb = qbi * PF_AQ;
+    const int h = blockIdx.x, qb = qbi * QB;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q16 = lane & 15, kq = lane >> 4;
     const int kvh = h / (a.nh / a.nkv);
     const int tq = qb + 16 * wave + q16, w0 = qb + 16 * wave;
@@ -2121,7 +2128,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 256 ?
                 }
             }
     }
-    const int tl = (qb + PF_AQ < a.T ? qb + PF_AQ : a.T) - 1;
+    const int tl = (qb + QB < a.T ? qb + QB : a.T) - 1;
     const int kend = a.pos0 + tl;
     const int kfirst = a.pos0 + qb + 1 - a.window > 0 ? a.pos0 + qb + 1 - a.window : 0;
     int b0 = kfirst / PF_HK, b1 = kend / PF_HK;  // key blocks b0 .. b1
@@ -2140,22 +2147,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 256 ?
     for (int i = 0; i < NT; i++) o[i] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint4* hsrc = (const uint4*)(a.kvh + (size_t)kvh * a.nblk * BLK);
     const int* hexp = a.kvs + 2 * (size_t)kvh * a.nblk;
+    // (eight waves) block b's planes into buffer u: 16 bytes per lane, lane l of a wave at the wave's
+    // base + 16 l, which is the planes' own order
+    auto stage = [&](int b, int u) {
+        const uint4* src = hsrc + (size_t)b * (BLK / 8) + threadIdx.x;
+        uint4* dst = ph_lds + u * (BLK / 8) + 64 * wave;
+#pragma unroll
+        for (int i = 0; i < NPU; i++)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + NTH * i),
+                                             (__attribute__((address_space(3))) void*)(dst + NTH * i), 16, 0, 0);
+    };
+    if constexpr (PfHq<HD>::bufs == 2) {
+        if (b0 <= b1) stage(b0, 0);
+    }
     for (int b = b0; b <= b1; b++) {
-        const int kb = b * PF_HK;
-        __syncthreads();  // the previous block's planes have been read
-        {
+        const int kb = b * PF_HK, u = PfHq<HD>::bufs == 2 ? (b - b0) & 1 : 0;
+        if constexpr (PfHq<HD>::bufs == 2) {
+            // this thread's loads of block b have landed; after the barrier every thread's have, and
+            // every wave has left block b - 1, whose buffer the next block's loads then overwrite
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (b < b1) stage(b + 1, u ^ 1);
+        } else {
+            __syncthreads();  // the previous block's planes have been read
             const uint4* src = hsrc + (size_t)b * (BLK / 8);
 #pragma unroll
-            for (int r = 0; r < BLK / 8 / 256; r += 8) {
+            for (int r = 0; r < NPU; r += 8) {
                 uint4 v[8];
 #pragma unroll
-                for (int i = 0; i < 8; i++) v[i] = src[threadIdx.x + 256 * (r + i)];
+                for (int i = 0; i < 8; i++) v[i] = src[threadIdx.x + NTH * (r + i)];
 #pragma unroll
-                for (int i = 0; i < 8; i++) ph_lds[threadIdx.x + 256 * (r + i)] = v[i];
+                for (int i = 0; i < 8; i++) ph_lds[threadIdx.x + NTH * (r + i)] = v[i];
             }
+            __syncthreads();
         }
-        __syncthreads();
         if (!wlive || kb > wpos_hi || kb + PF_HK - 1 < wws) continue;  // no key of the block for the wave
+        const _Float16* skh = (const _Float16*)(ph_lds + u * (BLK / 8));
+        const _Float16* skl = skh + PF_HK * HD;
+        const _Float16* svh = skl + PF_HK * HD;
+        const _Float16* svl = svh + HD * PF_HK;
         const int ek = hexp[2 * b], ev = hexp[2 * b + 1];
         pf_f32x4 s[2];
         s[0] = s[1] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -2224,13 +2254,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 256 ?
     // lane l holds dims 16 j + 4 (l >> 4) + e of its query, in units of 2^-E
     const float un = ldexpf(1.0f, -E);
     if (qlive && half >= 0) {
-        const size_t row = ((size_t)(h * nqb + qbi) * 2 + half) * PF_AQ + (tq - qb);
+        const size_t row = ((size_t)(h * nqb + qbi) * 2 + half) * QB + (tq - qb);
         float* orow = a.part + row * HD + 4 * kq;
 #pragma unroll
         for (int j = 0; j < NT; j++)
             *(float4*)(orow + 16 * j) = make_float4(o[j][0] * un, o[j][1] * un, o[j][2] * un, o[j][3] * un);
         if (kq == 0) {
-            float* ml = a.part + (size_t)a.nh * nqb * 2 * PF_AQ * HD + row * 2;
+            float* ml = a.part + (size_t)a.nh * nqb * 2 * QB * HD + row * 2;
             ml[0] = m;
             ml[1] = l;
         }
@@ -2256,7 +2286,8 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
     constexpr int PH = HD == 128 || HD == 256 ? HD : 256;  // the fp16 kernel's instance
     const bool planes = HD == 256 || (HD == 128 && a.pos0 + a.T >= 1024);
     const void* kfn = planes ? (const void*)k_pf_attn_h<PH> : (const void*)k_pf_attn<HD>;
-    const size_t lds = planes ? sizeof(_Float16) * (size_t)pf_kvh_block<PH>() : pf_attn_lds<HD>();
+    const size_t lds = planes ? PfHq<PH>::bufs * sizeof(_Float16) * (size_t)pf_kvh_block<PH>() : pf_attn_lds<HD>();
+    const int qblk = planes ? PfHq<PH>::q : PF_AQ, nthr = planes ? PfHq<PH>::threads : 256;
     hipError_t e = pf_lds_attr(kfn, lds);
     if (e != hipSuccess) return e;
     if (planes) {
@@ -2266,7 +2297,7 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
                                                                                 a.kvs);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    const int nqb = (a.T + PF_AQ - 1) / PF_AQ;
+    const int nqb = (a.T + qblk - 1) / qblk;
     // split the key ranges of query blocks 1 .. nqb - 1 in two when every half and block 0 then run
     // at once on the resident slots and the scratch holds the halves (Llama-3-8B at 511 tokens:
     // 32 heads x 15 rows on 512 slots; the longest workgroup had 8 key blocks against 4.5 on average)
@@ -2276,20 +2307,21 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
         static std::atomic<int> resident[2] = {{-1}, {-1}};
         int per_cu = resident[planes].load(std::memory_order_relaxed);
         if (per_cu < 0) {
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, 256, lds) != hipSuccess)
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kfn, nthr, lds) != hipSuccess)
                 per_cu = 0;
             resident[planes].store(per_cu, std::memory_order_relaxed);
         }
         const int64_t items = (int64_t)a.nh * (2 * (nqb - 1) + 1);
-        const size_t need = (size_t)a.nh * nqb * 2 * PF_AQ * (HD + 2);
+        const size_t need = (size_t)a.nh * nqb * 2 * qblk * (HD + 2);
         if (per_cu > 0 && items <= (int64_t)per_cu * (a.n_cu > 0 ? a.n_cu : 256) && need <= a.part_cap) a.split = 1;
     }
     dim3 grid((unsigned)a.nh, (unsigned)(a.split ? 2 * (nqb - 1) + 1 : nqb));
-    if (planes) k_pf_attn_h<PH><<<grid, 256, lds, st>>>(a);
+    if (planes) k_pf_attn_h<PH><<<grid, nthr, lds, st>>>(a);
     else k_pf_attn<HD><<<grid, 256, lds, st>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess || !a.split) return e;
-    k_pf_attn_merge<HD><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1)), 256, 0, st>>>(a);
+    if (planes) k_pf_attn_merge<HD, PfHq<PH>::q><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1)), 256, 0, st>>>(a);
+    else k_pf_attn_merge<HD, PF_AQ><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1)), 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
