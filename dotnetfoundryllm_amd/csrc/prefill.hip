@@ -2061,24 +2061,22 @@ __global__ __launch_bounds__(256) void k_pf_kv_split(const float* __restrict__ k
 }
 
 // k_pf_attn's grid of (head, query block) rows, halves included, over the planes of k_pf_kv_split;
-// NW waves of 16 queries share each staged key block of PF_HK aligned positions. Head_dim 256: eight
-// waves (one workgroup per CU), the planes brought in by direct global -> LDS loads into two
-// buffers, the next block's while the current one multiplies (Gemma-2-9B over 6143 tokens:
-// attention 59.5-60.1 -> 55.3-56.5 ms against four waves staging through registers); head_dim 128:
-// four waves staging each block through registers into one buffer (the eight-wave form's shorter
-// attention, 7.0 -> 5.0 ms for Qwen2-7B over 2047 tokens, came with GEMMs 2 ms longer in the same
-// prefill, 25.0k -> 24.4k tok/s). O^T accumulates in units of 2^-E, E = 14 + the V exponent of the
-// last block added (a block of another exponent rescales it by the power of two with the max
-// correction).
+// eight waves of 16 queries share each staged key block of PF_HK aligned positions, brought in by
+// direct global -> LDS loads into two buffers, the next block's while the current one multiplies
+// (against four waves staging each block through registers into one buffer: Gemma-2-9B over 6143
+// tokens attention 59.5-60.1 -> 55.3-56.5 ms, one workgroup per CU; Qwen2-7B over 2047 tokens
+// 7.0 -> 5.0 ms, two per CU). O^T accumulates in units of 2^-E, E = 14 + the V exponent of the last
+// block added (a block of another exponent rescales it by the power of two with the max correction).
 template <int HD> struct PfHq {
-    static constexpr int nw = HD == 256 ? 8 : 4, q = 16 * nw, threads = 64 * nw, bufs = HD == 256 ? 2 : 1;
+    static constexpr int nw = 8, q = 16 * nw, threads = 64 * nw;  // waves, queries, threads
 };
 template <int HD>
-__global__ __launch_bounds__(PfHq<HD>::threads) __attribute__((amdgpu_waves_per_eu(HD == 256 ? 2 : 3))) void k_pf_attn_h(const PfAttn a) {
+__global__ __launch_bounds__(PfHq<HD>::threads) __attribute__((amdgpu_waves_per_eu(HD == 256 ? 2 : 4))) void k_pf_attn_h(const PfAttn a) {
     static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
     constexpr int NS = HD / 32, NT = HD / 16, BLK = pf_kvh_block<HD>();
     constexpr int QB = PfHq<HD>::q, NTH = PfHq<HD>::threads, NPU = BLK / 8 / NTH;
-    extern __shared__ uint4 ph_lds[];  // PfHq<HD>::bufs buffers of BLK halves
+    static_assert(BLK / 8 % NTH == 0, "whole 16-byte pieces per thread");
+    extern __shared__ uint4 ph_lds[];  // two buffers of BLK halves
     const int nqb = (a.T + QB - 1) / QB;
     int qbi = nqb - 1 - (int)blockIdx.y, half = -1;
     if (a.split) {
@@ -2147,8 +2145,8 @@ __global__ __launch_bounds__(PfHq<HD>::threads) __attribute__((amdgpu_waves_per_
     for (int i = 0; i < NT; i++) o[i] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint4* hsrc = (const uint4*)(a.kvh + (size_t)kvh * a.nblk * BLK);
     const int* hexp = a.kvs + 2 * (size_t)kvh * a.nblk;
-    // (eight waves) block b's planes into buffer u: 16 bytes per lane, lane l of a wave at the wave's
-    // base + 16 l, which is the planes' own order
+    // block b's planes into buffer u: 16 bytes per lane, lane l of a wave at the wave's base + 16 l,
+    // which is the planes' own order
     auto stage = [&](int b, int u) {
         const uint4* src = hsrc + (size_t)b * (BLK / 8) + threadIdx.x;
         uint4* dst = ph_lds + u * (BLK / 8) + 64 * wave;
@@ -2157,30 +2155,14 @@ __global__ __launch_bounds__(PfHq<HD>::threads) __attribute__((amdgpu_waves_per_
             __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + NTH * i),
                                              (__attribute__((address_space(3))) void*)(dst + NTH * i), 16, 0, 0);
     };
-    if constexpr (PfHq<HD>::bufs == 2) {
-        if (b0 <= b1) stage(b0, 0);
-    }
+    if (b0 <= b1) stage(b0, 0);
     for (int b = b0; b <= b1; b++) {
-        const int kb = b * PF_HK, u = PfHq<HD>::bufs == 2 ? (b - b0) & 1 : 0;
-        if constexpr (PfHq<HD>::bufs == 2) {
-            // this thread's loads of block b have landed; after the barrier every thread's have, and
-            // every wave has left block b - 1, whose buffer the next block's loads then overwrite
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (b < b1) stage(b + 1, u ^ 1);
-        } else {
-            __syncthreads();  // the previous block's planes have been read
-            const uint4* src = hsrc + (size_t)b * (BLK / 8);
-#pragma unroll
-            for (int r = 0; r < NPU; r += 8) {
-                uint4 v[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) v[i] = src[threadIdx.x + NTH * (r + i)];
-#pragma unroll
-                for (int i = 0; i < 8; i++) ph_lds[threadIdx.x + NTH * (r + i)] = v[i];
-            }
-            __syncthreads();
-        }
+        const int kb = b * PF_HK, u = (b - b0) & 1;
+        // this thread's loads of block b have landed; after the barrier every thread's have, and
+        // every wave has left block b - 1, whose buffer the next block's loads then overwrite
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (b < b1) stage(b + 1, u ^ 1);
         if (!wlive || kb > wpos_hi || kb + PF_HK - 1 < wws) continue;  // no key of the block for the wave
         const _Float16* skh = (const _Float16*)(ph_lds + u * (BLK / 8));
         const _Float16* skl = skh + PF_HK * HD;
@@ -2286,7 +2268,7 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
     constexpr int PH = HD == 128 || HD == 256 ? HD : 256;  // the fp16 kernel's instance
     const bool planes = HD == 256 || (HD == 128 && a.pos0 + a.T >= 1024);
     const void* kfn = planes ? (const void*)k_pf_attn_h<PH> : (const void*)k_pf_attn<HD>;
-    const size_t lds = planes ? PfHq<PH>::bufs * sizeof(_Float16) * (size_t)pf_kvh_block<PH>() : pf_attn_lds<HD>();
+    const size_t lds = planes ? 2 * sizeof(_Float16) * (size_t)pf_kvh_block<PH>() : pf_attn_lds<HD>();
     const int qblk = planes ? PfHq<PH>::q : PF_AQ, nthr = planes ? PfHq<PH>::threads : 256;
     hipError_t e = pf_lds_attr(kfn, lds);
     if (e != hipSuccess) return e;
