@@ -2262,11 +2262,11 @@ size_t pf_kv_planes_halves(int hd, int nkv, int max_seq) {
 
 template <int HD>
 static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
-    // head_dim 256, and 128 over at least 1024 keys: the planes of keys [0, pos0 + T), then the fp16
-    // kernel (Qwen2-7B over 2047 tokens: attention 10.2 -> 7.0 ms; over 511 keys the split pass cost
-    // more than the products saved: Llama-3-8B's 1.49 -> 1.55 ms)
+    // head_dim 128 and 256: the planes of keys [0, pos0 + T), then the fp16 kernel (attention over
+    // 2047 tokens of Qwen2-7B 10.2 -> 5.0 ms, over 511 of Llama-3-8B 1.48 -> 1.35 ms); head_dim 64:
+    // the f32 kernel
     constexpr int PH = HD == 128 || HD == 256 ? HD : 256;  // the fp16 kernel's instance
-    const bool planes = HD == 256 || (HD == 128 && a.pos0 + a.T >= 1024);
+    constexpr bool planes = HD == 128 || HD == 256;
     const void* kfn = planes ? (const void*)k_pf_attn_h<PH> : (const void*)k_pf_attn<HD>;
     const size_t lds = planes ? 2 * sizeof(_Float16) * (size_t)pf_kvh_block<PH>() : pf_attn_lds<HD>();
     const int qblk = planes ? PfHq<PH>::q : PF_AQ, nthr = planes ? PfHq<PH>::threads : 256;

@@ -87,8 +87,8 @@ def test_batched_prefill_split_attention(ctx, name, cap, n):
     8; 1100: 17 blocks and 12) into a 256- (1280-) position cache: the prefill attention runs every
     block but the first as two halves of its key range plus a merge when all halves fit the
     resident workgroups, as here. Head dim 64 (Llama; Qwen2 with its q/k/v bias; Mistral with its
-    window), 128 (Gemma-2: softcaps, window on the even layer) on the f32 kernel, and 128 over 1100
-    keys and 256 on the fp16 kernel over the K / V planes. Logits and every K/V row against the
+    window) on the f32 kernel, 128 (Gemma-2: softcaps, window on the even layer; also over 1100
+    keys) and 256 on the fp16 kernel over the K / V planes. Logits and every K/V row against the
     oracle, then greedy decode."""
     cfg, desc, tensors = synthetic(name)
     m = device_model(ctx, desc, tensors)
