@@ -397,9 +397,8 @@ def prefill_report(cfg, n, seconds, stages=None):
     product), a Q8_0 one two (its int8 codes against the hi and lo halves), any other three (Q6_K:
     exact integer hi / lo weights; other types: hi / lo splits of both operands); `gemm` is those
     fp16 products' rate against the fp16 peak. Attention runs on the f32 matrix cores, one product
-    per flop, except at head_dim 256, and at 128 over at least 1024 tokens, where it takes three fp16
-    products per flop (hi / lo splits of both operands, the lo lo product dropped) against the fp16
-    peak."""
+    per flop, except at head_dim 128 and 256, where it takes three fp16 products per flop (hi / lo
+    splits of both operands, the lo lo product dropped) against the fp16 peak."""
     H, L, F = cfg["hidden"], cfg["n_layers"], cfg["ffn"]
     hd = cfg["head_dim"]
     qdim, kvdim = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd
@@ -439,7 +438,7 @@ def prefill_report(cfg, n, seconds, stages=None):
                 mf = 2.0 * n * L * issued / (st["ms"] * 1e-3) / 1e12
                 row.update(dtype="fp16", products=round(issued / sum(w for w, _ in g), 3), mfma_tflops=round(mf, 1),
                            mfma_frac=round(mf / FP16_MFMA_PEAK_TFLOPS, 4))
-            elif name == "pf_attention" and (hd == 256 or (hd == 128 and n >= 1024)):
+            elif name == "pf_attention" and hd in (128, 256):
                 mf = 3.0 * attn / (st["ms"] * 1e-3) / 1e12
                 row.update(dtype="fp16", products=3.0, mfma_tflops=round(mf, 1),
                            mfma_frac=round(mf / FP16_MFMA_PEAK_TFLOPS, 4))
