@@ -1924,13 +1924,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PfAk<HD>::p
 }
 
 // The two halves of the split query blocks (1 .. nqb - 1) of head blockIdx.x, query block
-// blockIdx.y + 1: out = (o1 e^(m1 - M) + o2 e^(m2 - M)) / (l1 e^(m1 - M) + l2 e^(m2 - M)), M = max(m1, m2)
+// blockIdx.y + 1 (its rows spread over gridDim.z workgroups):
+// out = (o1 e^(m1 - M) + o2 e^(m2 - M)) / (l1 e^(m1 - M) + l2 e^(m2 - M)), M = max(m1, m2)
 template <int HD, int QB>
 __global__ __launch_bounds__(256) void k_pf_attn_merge(const PfAttn a) {
     const int nqb = (a.T + QB - 1) / QB, h = blockIdx.x, qbi = blockIdx.y + 1, qb = qbi * QB;
     const size_t r0 = ((size_t)(h * nqb + qbi) * 2) * QB;
     const float* ml = a.part + (size_t)a.nh * nqb * 2 * QB * HD;
-    for (int idx = threadIdx.x; idx < QB * HD / 4; idx += 256) {
+    for (int idx = threadIdx.x + 256 * (int)blockIdx.z; idx < QB * HD / 4; idx += 256 * (int)gridDim.z) {
         const int ql = idx / (HD / 4), d4 = (idx % (HD / 4)) * 4, tq = qb + ql;
         if (tq >= a.T) continue;
         const size_t ra = r0 + ql, rb = r0 + QB + ql;
@@ -2302,8 +2303,9 @@ static hipError_t pf_attn_run(PfAttn a, hipStream_t st) {
     else k_pf_attn<HD><<<grid, 256, lds, st>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess || !a.split) return e;
-    if (planes) k_pf_attn_merge<HD, PfHq<PH>::q><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1)), 256, 0, st>>>(a);
-    else k_pf_attn_merge<HD, PF_AQ><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1)), 256, 0, st>>>(a);
+    // a block's rows over 4 workgroups (32 heads x 3 split blocks of 128 queries alone took 9.3 us)
+    if (planes) k_pf_attn_merge<HD, PfHq<PH>::q><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1), 4), 256, 0, st>>>(a);
+    else k_pf_attn_merge<HD, PF_AQ><<<dim3((unsigned)a.nh, (unsigned)(nqb - 1), 2), 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
