@@ -1625,9 +1625,14 @@ __global__ __launch_bounds__(256) void k_pf_qkv_post(float* __restrict__ qkv, in
     const int t = blockIdx.x, pos = pos0 + t, half = hd >> 1, qdim = nh * hd, kvdim = nkv * hd;
     float* row = qkv + (size_t)t * ldq;
     const float* prow = part + (size_t)t * ldq;
-    auto val = [&](int c) {
-        float v = row[c];
-        for (int z = 0; z < nsp; z++) v += prow[(size_t)z * pn + c];
+    // values c, c + 1 (c even; every row, slice and cache row starts at an even offset)
+    auto val2 = [&](int c) {
+        float2 v = *(const float2*)(row + c);
+        for (int z = 0; z < nsp; z++) {
+            const float2 p = *(const float2*)(prow + (size_t)z * pn + c);
+            v.x += p.x;
+            v.y += p.y;
+        }
         return v;
     };
     const float2* rp = rope + (size_t)pos * half;
@@ -1636,25 +1641,27 @@ __global__ __launch_bounds__(256) void k_pf_qkv_post(float* __restrict__ qkv, in
         const bool isq = idx < nh * half;
         const int li = isq ? idx : idx - nh * half;
         const int head = li / half, i = li % half, o = head * hd + 2 * i;
-        const int c = (isq ? 0 : qdim) + o;
-        float x0 = val(c), x1 = val(c + 1);
+        const float2 xv = val2((isq ? 0 : qdim) + o);
+        float x0 = xv.x, x1 = xv.y;
         const float* b = isq ? bq : bk;
-        if (b) { x0 = x0 + b[o]; x1 = x1 + b[o + 1]; }
-        const float2 cs = rp[i];
-        const float y0 = x0 * cs.x - x1 * cs.y;
-        const float y1 = x0 * cs.y + x1 * cs.x;
-        if (isq) {
-            row[o] = y0;
-            row[o + 1] = y1;
-        } else {
-            kc[(size_t)pos * kvdim + o] = y0;
-            kc[(size_t)pos * kvdim + o + 1] = y1;
+        if (b) {
+            const float2 bb = *(const float2*)(b + o);
+            x0 = x0 + bb.x;
+            x1 = x1 + bb.y;
         }
+        const float2 cs = rp[i];
+        const float2 y = make_float2(x0 * cs.x - x1 * cs.y, x0 * cs.y + x1 * cs.x);
+        if (isq) *(float2*)(row + o) = y;
+        else *(float2*)(kc + (size_t)pos * kvdim + o) = y;
     }
-    for (int i = threadIdx.x; i < kvdim; i += 256) {
-        float v = val(qdim + kvdim + i);
-        if (bv) v = v + bv[i];
-        vc[(size_t)pos * kvdim + i] = v;
+    for (int i = 2 * threadIdx.x; i < kvdim; i += 512) {
+        float2 v = val2(qdim + kvdim + i);
+        if (bv) {
+            const float2 bb = *(const float2*)(bv + i);
+            v.x = v.x + bb.x;
+            v.y = v.y + bb.y;
+        }
+        *(float2*)(vc + (size_t)pos * kvdim + i) = v;
     }
 }
 
@@ -1663,6 +1670,7 @@ hipError_t launch_pf_qkv_post(float* qkv, int ldq, int T, int pos0, const float*
                               const float* part, int nsp) {
     if (T <= 0) return hipSuccess;
     if (nsp < 0 || (nsp > 0 && part == nullptr)) return hipErrorInvalidValue;
+    if (ldq % 2 != 0 || hd % 2 != 0) return hipErrorInvalidValue;  // pairs of floats at even offsets
     k_pf_qkv_post<<<T, 256, 0, st>>>(qkv, ldq, pos0, bq, bk, bv, rope, nh, nkv, hd, kc, vc, nsp > 0 ? part : qkv, nsp,
                                      (size_t)T * ldq);
     return hipGetLastError();
