@@ -1790,10 +1790,14 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
         {
             const Tensor* w[1] = {&L.o};
             float* y[1] = {gemma ? s->pf_tmp : s->pf_x};
-            if ((e = pf_gemm(s, "pf_o", w, y, 1, H, T, !gemma, s->pf_att, qdim, nullptr, defer_x ? &pend_x : nullptr)) !=
-                hipSuccess)
+            // Gemma-2: the slices of tmp go into the post-norm
+            int pend_t = 0;
+            if ((e = pf_gemm(s, "pf_o", w, y, 1, H, T, !gemma, s->pf_att, qdim, nullptr,
+                             defer_x ? &pend_x : (gemma ? &pend_t : nullptr))) != hipSuccess)
                 return e;
-            if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_attn, s->pf_x, s->st));
+            if (gemma)
+                STEP("pf_postnorm", (12.0 + 4.0 * pend_t + (pend_t > 0 ? 4.0 : 0.0)) * T * H,
+                     launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_attn, s->pf_x, s->st, s->pf_part, pend_t));
         }
         if (!fuse_h) STEP("pf_norm", 8.0 * T * H, launch_pf_norm(s->pf_x, T, H, L.ffn_norm, eps, nk, s->pf_xn, ldx, s->st));
         {
@@ -1810,11 +1814,14 @@ static hipError_t prefill_chunk(fllm_seq* s, int T, int pos0) {
             const Tensor* w[1] = {&L.down};
             float* y[1] = {gemma ? s->pf_tmp : s->pf_x};
             const PfSrc src{PfSrc::ACT, s->pf_gu, nullptr, 0.0f, gemma ? 1 : 0};
-            // the last layer's sum is complete when the chunk ends
+            // the last layer's sum is complete when the chunk ends; Gemma-2's goes into the post-norm
+            int pend_t = 0;
             if ((e = pf_gemm(s, "pf_down", w, y, 1, H, T, !gemma, nullptr, 0, fuse_f ? &src : nullptr,
-                             defer_x && l + 1 < d.n_layers ? &pend_x : nullptr)) != hipSuccess)
+                             defer_x && l + 1 < d.n_layers ? &pend_x : (gemma ? &pend_t : nullptr))) != hipSuccess)
                 return e;
-            if (gemma) STEP("pf_postnorm", 12.0 * T * H, launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_ffn, s->pf_x, s->st));
+            if (gemma)
+                STEP("pf_postnorm", (12.0 + 4.0 * pend_t + (pend_t > 0 ? 4.0 : 0.0)) * T * H,
+                     launch_pf_postnorm_add(s->pf_tmp, T, H, L.post_ffn, s->pf_x, s->st, s->pf_part, pend_t));
         }
     }
     return hipSuccess;

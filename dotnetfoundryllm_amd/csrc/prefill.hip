@@ -1677,24 +1677,51 @@ hipError_t launch_pf_qkv_post(float* qkv, int ldq, int T, int pos0, const float*
 }
 
 // Gemma2 post-norm: x += GemmaRmsNorm(tmp, w), eps 1e-6 (Gemma2ForwardPass.cs:90-96)
-__global__ __launch_bounds__(256) void k_pf_postnorm_add(const float* __restrict__ tmp, int n, const float* __restrict__ w,
-                                                         float* __restrict__ x) {
+// (n a multiple of 4: float4 pieces; nsp pending K-split slices of part, pn floats apart, added to
+// tmp's row first and written back, k_pf_split_add's sum)
+__global__ __launch_bounds__(256) void k_pf_postnorm_add(float* __restrict__ tmp, int n, const float* __restrict__ w,
+                                                         float* __restrict__ x, const float* __restrict__ part, int nsp,
+                                                         size_t pn) {
     __shared__ float red[4];
-    const int t = blockIdx.x;
-    const float* tr = tmp + (size_t)t * n;
+    const int t = blockIdx.x, n4 = n / 4;
+    float4* tr = (float4*)(tmp + (size_t)t * n);
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(tr[i], tr[i], ss);
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        float4 v = tr[i];
+        if (nsp > 0) {
+            for (int z = 0; z < nsp; z++) {
+                const float4 p = ((const float4*)(part + (size_t)z * pn + (size_t)t * n))[i];
+                v.x += p.x;
+                v.y += p.y;
+                v.z += p.z;
+                v.w += p.w;
+            }
+            tr[i] = v;  // read back below by this same thread
+        }
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
     const float tot = pf_block_sum(ss, red);
     const float rms = 1.0f / sqrtf(tot / (float)n + 1e-6f);
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float o = (tr[i] * rms) * (w[i] + 1.0f);
-        x[(size_t)t * n + i] = x[(size_t)t * n + i] + o;
+    float4* xr = (float4*)(x + (size_t)t * n);
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const float4 v = tr[i], w4 = ((const float4*)w)[i];
+        float4 o = xr[i];
+        o.x = o.x + (v.x * rms) * (w4.x + 1.0f);
+        o.y = o.y + (v.y * rms) * (w4.y + 1.0f);
+        o.z = o.z + (v.z * rms) * (w4.z + 1.0f);
+        o.w = o.w + (v.w * rms) * (w4.w + 1.0f);
+        xr[i] = o;
     }
 }
 
-hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w, float* x, hipStream_t st) {
+hipError_t launch_pf_postnorm_add(float* tmp, int T, int n, const float* w, float* x, hipStream_t st,
+                                  const float* part, int nsp) {
     if (T <= 0) return hipSuccess;
-    k_pf_postnorm_add<<<T, 256, 0, st>>>(tmp, n, w, x);
+    if (n % 4 != 0 || nsp < 0 || (nsp > 0 && part == nullptr)) return hipErrorInvalidValue;
+    k_pf_postnorm_add<<<T, 256, 0, st>>>(tmp, n, w, x, nsp > 0 ? part : tmp, nsp, (size_t)T * n);
     return hipGetLastError();
 }
 

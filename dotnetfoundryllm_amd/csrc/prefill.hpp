@@ -84,8 +84,10 @@ hipError_t launch_pf_act(const float* gu, int T, int ffn, int act, float* h, int
 hipError_t launch_pf_qkv_post(float* qkv, int ldq, int T, int pos0, const float* bq, const float* bk, const float* bv,
                               const float2* rope, int nh, int nkv, int hd, float* kc, float* vc, hipStream_t st,
                               const float* part = nullptr, int nsp = 0);
-// x[t] += GemmaRmsNorm(tmp[t], w) for every row
-hipError_t launch_pf_postnorm_add(const float* tmp, int T, int n, const float* w, float* x, hipStream_t st);
+// x[t] += GemmaRmsNorm(tmp[t], w) for every row (n a multiple of 4); nsp pending K-split slices of
+// part ([T][n] each) are added to tmp first, in order
+hipError_t launch_pf_postnorm_add(float* tmp, int T, int n, const float* w, float* x, hipStream_t st,
+                                  const float* part = nullptr, int nsp = 0);
 
 // Causal attention of T query rows (positions pos0 + t) over this layer's cache, which already
 // holds the T new rows: out[t][h*hd + d].
