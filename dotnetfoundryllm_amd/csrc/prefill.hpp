@@ -45,7 +45,7 @@ struct PfGemm {
 };
 // With pending non-null, a K-split launch leaves its parts z > 0 in a.part and sets *pending to their
 // number (0 when unsplit) instead of adding them: the next kernel that reads y adds them first, in
-// order (launch_pf_split_norm, launch_pf_qkv_post), or launch_pf_split_add does.
+// order (launch_pf_split_norm, launch_pf_qkv_post, launch_pf_postnorm_add), or launch_pf_split_add does.
 hipError_t launch_pf_gemm(PfGemm a, int n_cu, hipStream_t st, int* pending = nullptr);
 // y[i] += part[0][i] + ... + part[nsp - 1][i] (in that order), slices of n floats
 hipError_t launch_pf_split_add(float* y, const float* part, int nsp, int64_t n, hipStream_t st);
